@@ -1,0 +1,175 @@
+/* nimbleml_hip.h — C-ABI of the MI355X (gfx950) GPT token-loop library.
+ *
+ * The drop-in boundary for NimbleML's GPT path (prefill → decode, compute_loss).
+ * Conventions follow the reference extension's device-pointer API
+ * (native/src/module.cpp:229-285): the caller owns every input/output buffer and
+ * passes plain device pointers and sizes; launches are asynchronous on the
+ * library stream; failures are reported instead of thrown — every function
+ * returns 0 on success or -1, and nml_last_error() gives the message (the
+ * reference raises RuntimeError with the CUDA message, sdpa_cuda.cu:10-14).
+ *
+ * dtype arguments: 0 = float32, 1 = float16 (NIMBLEML_DTYPE, np_backend.py:157-176).
+ * Token ids and labels are int64 (Tensor.from_int64, utils/tensor.py:194-214).
+ */
+#ifndef NIMBLEML_HIP_H
+#define NIMBLEML_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---------------------------------------------------------------- runtime ---- */
+
+/* Capability probes; replace `with_cuda` (module.cpp:13-17) and
+ * `flash_sdpa_available()` (module.cpp:221-227). */
+int nml_with_hip(void);
+int nml_hip_available(int* device_count);
+const char* nml_last_error(void);
+
+/* Select the device and create the library stream (default priority). */
+int nml_init(int device);
+int nml_get_stream(void** stream);
+int nml_set_stream(void* stream);
+int nml_device_info(char* name, size_t name_len, int* cu_count, size_t* total_mem);
+
+/* Device memory. Replace CuPy's allocator for this path (np_backend.py:82-90). */
+int nml_malloc(size_t bytes, void** ptr);
+int nml_free(void* ptr);
+int nml_memcpy_h2d(void* dst, const void* src, size_t bytes); /* returns when done */
+int nml_memcpy_d2h(void* dst, const void* src, size_t bytes); /* returns when done */
+int nml_memcpy_d2d(void* dst, const void* src, size_t bytes); /* async */
+int nml_memset(void* dst, int value, size_t bytes);            /* async */
+int nml_synchronize(void); /* replaces sync_device(), np_backend.py:118-126 */
+
+/* Events on the library stream (timing). */
+int nml_event_create(void** ev);
+int nml_event_record(void* ev);
+int nml_event_elapsed_ms(void* start, void* end, float* ms);
+int nml_event_destroy(void* ev);
+
+/* ------------------------------------------------------------ single ops ---- */
+
+/* RMSNorm forward; same arguments as rmsnorm_forward_device (module.cpp:259-270,
+ * kernel sdpa_cuda.cu:135-165) plus dtype. ms/rms (float32, rows) may be NULL.
+ * Semantics: kernels/fused_rmsnorm.py:360-369 (fp16 branch :360-365). */
+int nml_rmsnorm_forward_device(const void* x, const void* gamma, void* out, float* ms,
+                               float* rms, size_t rows, size_t dim, float eps, int dtype);
+
+/* tanh-GELU forward; replaces gelu_forward (module.cpp:19-31, native/src/gelu.cpp:12-21)
+ * and the fp16 NumPy branch (kernels/fused_gelu.py:114-116). tanh_u may be NULL. */
+int nml_gelu_forward_device(const void* x, void* out, float* tanh_u, size_t n, int dtype);
+
+/* x[b,s] = weights[ids[b,s]] + pos_weights[pos_offsets[b] + s] (pos_offsets NULL → 0).
+ * Replaces embedding_lookup + forward_prefix (kernels/embedding_scatter.py:25-36,
+ * layers/embedding.py:72-118, models/gpt.py:85-86). Out-of-range ids or positions
+ * write zeros and set bit 0 of *err (err may be NULL). */
+int nml_embedding_gather_device(const void* weights, const void* pos_weights, const int64_t* ids,
+                                void* out, size_t batch, size_t seq, size_t dim, size_t vocab,
+                                size_t max_pos, const int32_t* pos_offsets, int* err, int dtype);
+
+/* out = epi(x · w_tᵀ): x (rows, in_f) at row stride ld_x, w_t (out_f, in_f) — the
+ * reference's Dense weight (in, out) (layers/dense.py:16-25) transposed.
+ * epilogue: 0 none, 1 +bias, 2 +bias then GELU, 3 resid + (x·wᵀ + bias).
+ * Replaces the `x @ W + b` GEMMs of neural_network/_fused_arrays.py:25-30,69-71,
+ * 200-205 and the tied head `h @ Eᵀ` (models/gpt.py:150-153, with w_t = E). */
+int nml_linear_device(const void* x, size_t ld_x, const void* w_t, const void* bias,
+                      const void* resid, void* out, size_t rows, size_t in_f, size_t out_f,
+                      int epilogue, int dtype);
+
+/* Causal attention; same arguments as flash_sdpa_forward_device (module.cpp:231-242)
+ * except that m/l are not produced and `scale` is the reference's divisor sqrt(dk)
+ * (attention.py:135, fused_sdpa.py:71-78). q, k, v: (bh, seq, dk); out: (bh, seq, dk). */
+int nml_flash_sdpa_forward_device(const void* q, const void* k, const void* v, void* out,
+                                  size_t bh, size_t seq, size_t dk, float scale, int dtype);
+
+/* Mean tied-head cross-entropy (kernels/fused_tied_crossentropy.py:8-24 →
+ * fused_crossentropy.py:14-30) without materialising all (rows, vocab) logits at once.
+ * has_ignore: drop rows with label == ignore_index (losses/_ce_prepare.py:46-69).
+ * *loss receives the mean as float64 (returns after the device finishes). */
+int nml_tied_ce_forward_device(const void* hidden, const void* weights, const int64_t* labels,
+                               size_t rows, size_t dim, size_t vocab, int64_t ignore_index,
+                               int has_ignore, double* loss, int dtype);
+
+/* Next-token choice per row of (batch, vocab) logits (models/generate.py:23-59):
+ * temperature ≤ 0 → argmax; else temperature, top_k (≤0 off), top_p (outside (0,1) off)
+ * with u[b] replacing RandomState.choice's draw. repetition_penalty uses
+ * history[b, 0:hist_len[b]] (history/hist_len may be NULL when the penalty is 1). */
+int nml_sample_device(const void* logits, size_t batch, size_t vocab, float temperature,
+                      int top_k, float top_p, float repetition_penalty, const double* u,
+                      const int64_t* history, size_t history_stride, const int32_t* hist_len,
+                      int64_t* out_ids, int dtype);
+
+/* ------------------------------------------------------------ GPT model ---- */
+
+/* Parameter kinds for nml_model_set_param. Host data must already be in device
+ * layout and dtype: Dense weights transposed to (out, in); Q/K/V stacked. */
+enum nml_param_kind {
+  NML_P_TOKEN_EMB = 0, /* (vocab, d)        token_emb.weights            */
+  NML_P_POS_EMB = 1,   /* (max_seq, d)      pos_emb.weights              */
+  NML_P_LN_F = 2,      /* (d)               ln.gamma                     */
+  NML_P_LN1 = 10,      /* (d)               blocks.layers.i.ln1.gamma    */
+  NML_P_WQKV = 11,     /* (3d, d)           [W_q | W_k | W_v]ᵀ           */
+  NML_P_BQKV = 12,     /* (3d)              [b_q | b_k | b_v]            */
+  NML_P_WO = 13,       /* (d, d)            W_oᵀ                         */
+  NML_P_BO = 14,       /* (d)                                            */
+  NML_P_LN2 = 15,      /* (d)               ln2.gamma                    */
+  NML_P_W1 = 16,       /* (d_ff, d)         ffn.dense1.weightsᵀ          */
+  NML_P_B1 = 17,       /* (d_ff)                                         */
+  NML_P_W2 = 18,       /* (d, d_ff)         ffn.dense2.weightsᵀ          */
+  NML_P_B2 = 19        /* (d)                                            */
+};
+
+typedef struct nml_model nml_model;
+typedef struct nml_cache nml_cache;
+
+/* A GPT of the reference's architecture (models/gpt.py:11-71, fused_blocks=True,
+ * absolute learned positions): device-resident parameters in one allocation. */
+int nml_model_create(int vocab, int d_model, int num_heads, int num_layers, int max_seq_len,
+                     int d_ff, int dtype, nml_model** out);
+int nml_model_destroy(nml_model* m);
+int nml_model_set_param(nml_model* m, int kind, int layer, const void* host, size_t bytes);
+/* Device pointer of a parameter (for tests). */
+int nml_model_param_ptr(nml_model* m, int kind, int layer, void** ptr);
+
+/* GPT.forward (models/gpt.py:92-121): logits (batch, seq, vocab); last_only → (batch, vocab)
+ * for the last position. ids: device int64 (batch, seq). */
+int nml_model_forward(nml_model* m, const int64_t* ids, size_t batch, size_t seq, void* logits,
+                      int last_only);
+
+/* GPT.compute_loss (models/gpt.py:123-137): mean tied-head CE over batch·seq rows,
+ * labels device int64. Returns after the device finishes; *loss is float64. */
+int nml_model_loss(nml_model* m, const int64_t* ids, const int64_t* labels, size_t batch,
+                   size_t seq, int64_t ignore_index, int has_ignore, double* loss);
+
+/* KV cache for batch rows: K and V per layer, (batch, heads, max_seq, head_dim) each.
+ * The seam generate() probes for (models/generate.py:93-100). */
+int nml_cache_create(nml_model* m, size_t batch, nml_cache** out);
+int nml_cache_destroy(nml_cache* c);
+int nml_cache_length(nml_cache* c, size_t* len);
+/* Append seq tokens (same count per row) and return their logits (batch, seq, vocab),
+ * or (batch, vocab) for the last position when last_only. */
+int nml_model_forward_cached(nml_model* m, nml_cache* c, const int64_t* ids, size_t batch,
+                             size_t seq, void* logits, int last_only);
+
+/* Whole generate() (models/generate.py:62-119) on device, no host sync per token:
+ * prompts (batch, prompt_stride) device int64, row b valid for prompt_len[b] (host array;
+ * rows may differ — ragged batch); tokens_out (batch, out_stride) device int64 receives
+ * prompt + max_new tokens per row. u: device float64 (max_new, batch) uniforms when
+ * temperature > 0. use_graph: replay each decode step from one captured HIP graph. */
+int nml_model_generate(nml_model* m, const int64_t* prompts, size_t prompt_stride,
+                       const int32_t* prompt_len, size_t batch, size_t max_new,
+                       float temperature, int top_k, float top_p, float repetition_penalty,
+                       const double* u, int64_t* tokens_out, size_t out_stride, int use_graph);
+
+/* Timing helper for the benchmark: average device time of one decode step
+ * (embedding … sampling) over `steps` steps of the last generate() call shape. */
+int nml_model_last_decode_ms(nml_model* m, float* ms_per_step);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* NIMBLEML_HIP_H */

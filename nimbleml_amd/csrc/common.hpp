@@ -1,0 +1,142 @@
+// Shared definitions for the gfx950 (CDNA4) kernels and the C-ABI.
+//
+// Every C-ABI entry point returns 0 on success and -1 on failure; the failure
+// text is kept per thread and read with nml_last_error(). Launches go to the
+// library stream (nml_get_stream / nml_set_stream), asynchronously.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstddef>
+#include <cstdint>
+
+namespace nml {
+
+typedef _Float16 half_t;
+typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef _Float16 half4 __attribute__((ext_vector_type(4)));
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+typedef float floatx16 __attribute__((ext_vector_type(16)));
+
+enum DType : int { F32 = 0, F16 = 1 };
+
+inline size_t dtype_size(int dt) { return dt == F16 ? 2 : 4; }
+
+// Per-thread error text (host side).
+void set_error(const char* fmt, ...) __attribute__((format(printf, 1, 2)));
+hipStream_t stream();
+
+constexpr int kWave = 64;
+
+// ----------------------------------------------------------------- device math
+// Rounding helpers: round a float to the storage type T and back. For
+// T = half this reproduces one NumPy fp16 op (float compute, one rounding).
+template <typename T>
+__device__ __forceinline__ float rnd(float x) {
+  return static_cast<float>(static_cast<T>(x));
+}
+
+template <typename T>
+__device__ __forceinline__ float ld(const T* p) {
+  return static_cast<float>(*p);
+}
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+  return v;
+}
+
+__device__ __forceinline__ double wave_sum_d(double v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+
+// Block-wide sum for blockDim.x a multiple of 64 (≤ 1024); `red` holds 16 floats.
+__device__ __forceinline__ float block_sum(float v, float* red) {
+  v = wave_sum(v);
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, nw = blockDim.x >> 6;
+  __syncthreads();
+  if (lane == 0) red[w] = v;
+  __syncthreads();
+  float t = 0.f;
+  for (int i = 0; i < nw; ++i) t += red[i];
+  return t;
+}
+
+// GELU, tanh form: 0.5·x·(1 + tanh(√(2/π)·(x + 0.044715·x³))).
+// fp32: the operation order of the reference's native kernel
+// (native/src/gelu.cpp:15-19). fp16: the reference evaluates the same formula
+// as NumPy fp16 ufuncs (kernels/fused_gelu.py:114-116), Python constants taken
+// as fp16, left to right, one rounding per op — reproduced op by op here.
+__device__ __forceinline__ float gelu_f32(float x) {
+#pragma clang fp contract(off)
+  const float x3 = x * x * x;
+  const float tu = tanhf(0.7978845608028654f * (x + 0.044715f * x3));
+  return 0.5f * x * (1.0f + tu);
+}
+
+__device__ __forceinline__ float gelu_f16(float x) {
+#pragma clang fp contract(off)
+  const float k = static_cast<float>(static_cast<half_t>(0.7978845608028654f));
+  const float c = static_cast<float>(static_cast<half_t>(0.044715f));
+  float t = rnd<half_t>(c * x);
+  t = rnd<half_t>(t * x);
+  t = rnd<half_t>(t * x);
+  t = rnd<half_t>(x + t);
+  t = rnd<half_t>(k * t);
+  const float tu = rnd<half_t>(tanhf(t));
+  const float a = rnd<half_t>(0.5f * x);
+  const float b = rnd<half_t>(1.0f + tu);
+  return rnd<half_t>(a * b);
+}
+
+template <typename T>
+__device__ __forceinline__ float gelu_t(float x);
+template <>
+__device__ __forceinline__ float gelu_t<float>(float x) { return gelu_f32(x); }
+template <>
+__device__ __forceinline__ float gelu_t<half_t>(float x) { return gelu_f16(x); }
+
+}  // namespace nml
+
+#define NML_HIP(call)                                                              \
+  do {                                                                             \
+    hipError_t e_ = (call);                                                        \
+    if (e_ != hipSuccess) {                                                        \
+      nml::set_error("%s failed: %s (%s:%d)", #call, hipGetErrorString(e_),         \
+                     __FILE__, __LINE__);                                          \
+      return -1;                                                                   \
+    }                                                                              \
+  } while (0)
+
+#define NML_REQUIRE(cond, ...)                                                     \
+  do {                                                                             \
+    if (!(cond)) {                                                                 \
+      nml::set_error(__VA_ARGS__);                                                 \
+      return -1;                                                                   \
+    }                                                                              \
+  } while (0)
+
+// Check the launch that was just issued.
+#define NML_LAUNCHED()                                                             \
+  do {                                                                             \
+    hipError_t e_ = hipGetLastError();                                             \
+    if (e_ != hipSuccess) {                                                        \
+      nml::set_error("kernel launch failed: %s (%s:%d)", hipGetErrorString(e_),     \
+                     __FILE__, __LINE__);                                          \
+      return -1;                                                                   \
+    }                                                                              \
+  } while (0)
+
+#define NML_TRY(expr)                                                              \
+  do {                                                                             \
+    if ((expr) != 0) return -1;                                                    \
+  } while (0)

@@ -1,0 +1,120 @@
+// Internal launch interface between the kernel files and the model driver.
+// All launches are asynchronous on the library stream; each returns 0 or -1
+// (with the message set through nml::set_error).
+#pragma once
+
+#include "common.hpp"
+
+namespace nml {
+
+// Epilogues of the projection kernels (x · Wᵀ, fp32 accumulation). "T(v)"
+// rounds to the storage type, reproducing the reference's separate NumPy ops
+// (`x @ w`, then `+ b`, then GELU / residual add: neural_network/_fused_arrays.py
+// :25-30, :69-71, :200-205, :262, :270).
+enum Epilogue : int {
+  EPI_NONE = 0,        // out = T(acc)
+  EPI_BIAS = 1,        // out = T(T(acc) + b)
+  EPI_BIAS_GELU = 2,   // out = gelu_T(T(T(acc) + b))
+  EPI_BIAS_RESID = 3,  // out = T(r + T(T(acc) + b))
+  EPI_QKV = 4,         // T(T(acc) + b) scattered to head-major Q and the K/V cache
+};
+
+// Destination of the QKV epilogue. Output row r = b·S + s of the projection is
+// token s of sequence b, at absolute position pos(b) + s where pos(b) is
+// pos_base[b] (device) or 0 when pos_base is null. Column n selects
+// q/k/v = n / d, head h = (n % d) / dk, lane j = n % dk.
+//   q  : [(b·H + h)·S + s]·dk + j                       (head-major, per call)
+//   k,v: b·kv_stride_b + h·kv_stride_h + pos·dk + j     (cache layout)
+struct QKVDst {
+  void* q;
+  void* k;
+  void* v;
+  const int32_t* pos_base;
+  long long kv_stride_b;
+  long long kv_stride_h;
+  int S, H, dk, d;
+};
+
+struct LinearArgs {
+  const void* x;     // (M, K) rows at stride lda
+  long long lda;
+  const void* w;     // (N, K) row-major: the reference's (in, out) weight transposed
+  const void* bias;  // (N) or null for EPI_NONE
+  const void* resid; // (M, N) for EPI_BIAS_RESID (may alias out)
+  void* out;         // (M, N) row-major, ldc = N
+  int M, N, K;
+  int epi;
+  QKVDst qkv;
+};
+
+int launch_linear(int dt, const LinearArgs& a, hipStream_t st);
+
+int launch_embed(int dt, const int64_t* ids, const void* emb, const void* pos,
+                 const int32_t* pos_base, void* out, int B, int S, int d, int V, int P,
+                 int* err, hipStream_t st);
+// Decode: row b embeds tokens[b·tok_stride + pos[b]] at position pos[b].
+int launch_embed_decode(int dt, const int64_t* tokens, long long tok_stride, const int32_t* pos,
+                        const void* emb, const void* posw, void* out, int B, int d, int V, int P,
+                        int* err, hipStream_t st);
+
+int launch_rmsnorm(int dt, const void* x, const void* g, void* out, float* ms, float* rms,
+                   int rows, int d, float eps, hipStream_t st);
+int launch_gelu(int dt, const void* x, void* out, float* tanh_u, size_t n, hipStream_t st);
+
+// Causal attention for S new queries per sequence. q is head-major
+// (B, H, S, dk); keys/values at positions [0, pos(b) + S) are read from
+// k/v at b·kv_stride_b + h·kv_stride_h + p·dk; query s sits at pos(b) + s and sees
+// keys p ≤ pos(b) + s. Output is merged-head (B·S, H·dk).
+struct AttnArgs {
+  const void* q;
+  const void* k;
+  const void* v;
+  void* out;
+  const int32_t* pos_base;  // null → 0
+  long long kv_stride_b, kv_stride_h;
+  int B, H, S, dk;
+  float scale;  // the reference's sqrt(dk) divisor (attention.py:135)
+};
+int launch_attention_prefill(int dt, const AttnArgs& a, hipStream_t st);
+
+// One new query per sequence at position pos[b] (keys 0..pos[b]). `part` is a
+// float workspace of B·H·max_chunks·(dk + 2); `max_len` bounds pos[b] + 1.
+int launch_attention_decode(int dt, const AttnArgs& a, const int32_t* pos, int max_len,
+                            float* part, hipStream_t st);
+size_t attention_decode_workspace(int B, int H, int dk, int max_len);
+
+// Row-wise cross-entropy over (rows, V) logits of storage type T. Writes the
+// per-row loss (rows) and a validity flag (0 for ignore_index rows).
+int launch_ce_rows(int dt, const void* logits, int rows, int V, const int64_t* labels,
+                   long long ignore_index, int has_ignore, float* row_loss, int* row_valid,
+                   int* err, hipStream_t st);
+// Sum of valid row losses / count → out[0] (double); 0 when no row is valid.
+int launch_ce_reduce(const float* row_loss, const int* row_valid, int rows, double* sum_count,
+                     int accumulate, hipStream_t st);
+int launch_ce_finalize(const double* sum_count, double* loss, hipStream_t st);
+
+// Next-token selection over (B, V) logits, models/generate.py:23-59 semantics.
+struct SampleArgs {
+  const void* logits;       // (B, V) storage type
+  long long logits_stride;  // elements between rows
+  int B, V;
+  float temperature;        // ≤ 0 → greedy argmax
+  int top_k;                // ≤ 0 → off
+  float top_p;              // outside (0,1) → off
+  float rep_penalty;        // 1 → off
+  const double* uniforms;   // uniforms[step·B + b]; step = pos[b] + 1 − plen[b]
+  int64_t* tokens;          // (B, tok_stride) token history of each row
+  long long tok_stride;
+  // Generation mode (pos non-null): the history is tokens[b][0..pos[b]]; the choice
+  // is written to tokens[b][pos[b] + 1], pos[b] advances by one, and the uniform is
+  // uniforms[(pos[b] + 1 − plen[b])·B + b].
+  int32_t* pos;
+  const int32_t* plen;
+  // Standalone mode (pos null): history tokens[b][0..hist_len[b]) (null → empty),
+  // uniform uniforms[b], nothing but out_ids is written.
+  const int32_t* hist_len;
+  int64_t* out_ids;         // optional (B) copy of the chosen ids
+};
+int launch_sample(int dt, const SampleArgs& a, hipStream_t st);
+
+}  // namespace nml

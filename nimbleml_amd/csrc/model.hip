@@ -1,0 +1,788 @@
+// GPT driver: device-resident parameters, the forward pass, compute_loss, the KV
+// cache and the whole generate() loop (models/gpt.py, models/generate.py,
+// neural_network/_fused_arrays.py:251-284 for the block).
+//
+// Per block, with x the residual stream (T) updated in place:
+//   xn = RMSNorm₁(x);  [q | k | v] = xn·W_qkvᵀ + b   (q head-major; k, v into the cache)
+//   a  = causal attention(q, K[0..pos], V[0..pos])  (merged heads)
+//   x  = x + (a·W_oᵀ + b_o);  xn = RMSNorm₂(x)
+//   h  = GELU(xn·W₁ᵀ + b₁);   x = x + (h·W₂ᵀ + b₂)
+// then xn = RMSNorm_f(x) and logits = xn·Eᵀ (tied head).
+#include <cstring>
+#include <vector>
+
+#include "kernels.hpp"
+#include "nimbleml_hip.h"
+
+using namespace nml;
+
+namespace {
+
+constexpr float kEps = 1e-5f;  // RMSNorm epsilon (layers/rms_norm.py:16)
+
+struct Layer {
+  void *ln1, *wqkv, *bqkv, *wo, *bo, *ln2, *w1, *b1, *w2, *b2;
+};
+
+struct Buf {
+  void* p = nullptr;
+  size_t bytes = 0;
+  int ensure(size_t want) {
+    if (want <= bytes) return 0;
+    if (p) {
+      NML_HIP(hipStreamSynchronize(nml::stream()));
+      NML_HIP(hipFree(p));
+      p = nullptr;
+      bytes = 0;
+    }
+    NML_HIP(hipMalloc(&p, want));
+    bytes = want;
+    return 0;
+  }
+  void release() {
+    if (p) (void)hipFree(p);
+    p = nullptr;
+    bytes = 0;
+  }
+};
+
+inline size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
+
+}  // namespace
+
+struct nml_model {
+  int V, d, H, L, P, F, dt, dk;
+  size_t es;
+  void* arena = nullptr;
+  size_t arena_bytes = 0;
+  void *emb = nullptr, *pos = nullptr, *lnf = nullptr;
+  std::vector<Layer> layers;
+  Buf ws;         // activations
+  Buf kvs;        // K/V scratch for forward() without a cache
+  Buf logits_ws;  // logits chunk for compute_loss / generate
+  Buf small;      // device counters, positions, loss accumulators
+  // decode timing of the last generate()
+  float last_decode_ms = 0.f;
+  int last_decode_steps = 0;
+};
+
+struct nml_cache {
+  nml_model* m;
+  int B;
+  void* k = nullptr;  // L × B × H × P × dk
+  void* v = nullptr;
+  int32_t* len_dev = nullptr;  // B
+  std::vector<int32_t> len;    // host mirror
+};
+
+namespace {
+
+size_t param_elems(const nml_model* m, int kind) {
+  const size_t d = m->d, F = m->F;
+  switch (kind) {
+    case NML_P_TOKEN_EMB: return (size_t)m->V * d;
+    case NML_P_POS_EMB: return (size_t)m->P * d;
+    case NML_P_LN_F:
+    case NML_P_LN1:
+    case NML_P_LN2:
+    case NML_P_BO:
+    case NML_P_B2: return d;
+    case NML_P_WQKV: return 3 * d * d;
+    case NML_P_BQKV: return 3 * d;
+    case NML_P_WO: return d * d;
+    case NML_P_W1: return F * d;
+    case NML_P_B1: return F;
+    case NML_P_W2: return d * F;
+  }
+  return 0;
+}
+
+void** param_slot(nml_model* m, int kind, int layer) {
+  switch (kind) {
+    case NML_P_TOKEN_EMB: return &m->emb;
+    case NML_P_POS_EMB: return &m->pos;
+    case NML_P_LN_F: return &m->lnf;
+  }
+  if (layer < 0 || layer >= m->L) return nullptr;
+  Layer& l = m->layers[layer];
+  switch (kind) {
+    case NML_P_LN1: return &l.ln1;
+    case NML_P_WQKV: return &l.wqkv;
+    case NML_P_BQKV: return &l.bqkv;
+    case NML_P_WO: return &l.wo;
+    case NML_P_BO: return &l.bo;
+    case NML_P_LN2: return &l.ln2;
+    case NML_P_W1: return &l.w1;
+    case NML_P_B1: return &l.b1;
+    case NML_P_W2: return &l.w2;
+    case NML_P_B2: return &l.b2;
+  }
+  return nullptr;
+}
+
+const int kLayerKinds[] = {NML_P_LN1, NML_P_WQKV, NML_P_BQKV, NML_P_WO, NML_P_BO,
+                           NML_P_LN2, NML_P_W1,   NML_P_B1,   NML_P_W2, NML_P_B2};
+
+// Activation workspace for R rows (B·S) of one forward.
+struct Acts {
+  void* x;   // (R, d) residual stream
+  void* xn;  // (R, d) normalised
+  void* q;   // (R, d) head-major queries
+  void* att; // (R, d) merged attention output
+  void* h;   // (R, F) FFN hidden
+  float* part;  // decode partials
+};
+
+int acts_for(nml_model* m, int R, int Bdec, Acts* a) {
+  const size_t rd = align256((size_t)R * m->d * m->es);
+  const size_t rf = align256((size_t)R * m->F * m->es);
+  const size_t part = Bdec ? align256(attention_decode_workspace(Bdec, m->H, m->dk, m->P)) : 0;
+  NML_TRY(m->ws.ensure(4 * rd + rf + part));
+  char* b = static_cast<char*>(m->ws.p);
+  a->x = b;
+  a->xn = b + rd;
+  a->q = b + 2 * rd;
+  a->att = b + 3 * rd;
+  a->h = b + 4 * rd;
+  a->part = part ? reinterpret_cast<float*>(b + 4 * rd + rf) : nullptr;
+  return 0;
+}
+
+// Small device scratch: [0] int err, then B int32 positions etc.
+struct Small {
+  int* err;
+  double* acc;   // 3 doubles
+  int32_t* pos;  // up to 4096 rows
+  int32_t* plen;
+  int32_t* zeros;
+};
+
+int small_for(nml_model* m, int B, Small* s) {
+  const size_t need = 256 + 256 + 3 * align256((size_t)B * 4 + 4);
+  NML_TRY(m->small.ensure(need < 4096 ? 4096 : need));
+  char* b = static_cast<char*>(m->small.p);
+  s->err = reinterpret_cast<int*>(b);
+  s->acc = reinterpret_cast<double*>(b + 256);
+  const size_t bb = align256((size_t)B * 4 + 4);
+  s->pos = reinterpret_cast<int32_t*>(b + 512);
+  s->plen = reinterpret_cast<int32_t*>(b + 512 + bb);
+  s->zeros = reinterpret_cast<int32_t*>(b + 512 + 2 * bb);
+  return 0;
+}
+
+// Where a layer's K/V go: base pointers and strides.
+struct KVView {
+  void* k;
+  void* v;
+  long long sb, sh;
+};
+
+// The transformer trunk over R = B·S rows already embedded in acts.x. Leaves the
+// final-normed hidden states in acts.xn. pos_base (device, B) gives each row's
+// first position (null → 0); kv(l) gives layer l's K/V destination.
+template <typename KVF>
+int trunk(nml_model* m, const Acts& a, int B, int S, const int32_t* pos_base, KVF kv,
+          hipStream_t st) {
+  const int R = B * S, d = m->d;
+  for (int l = 0; l < m->L; ++l) {
+    const Layer& w = m->layers[l];
+    const KVView c = kv(l);
+    NML_TRY(launch_rmsnorm(m->dt, a.x, w.ln1, a.xn, nullptr, nullptr, R, d, kEps, st));
+    LinearArgs qkv{};
+    qkv.x = a.xn;
+    qkv.lda = d;
+    qkv.w = w.wqkv;
+    qkv.bias = w.bqkv;
+    qkv.M = R;
+    qkv.N = 3 * d;
+    qkv.K = d;
+    qkv.epi = EPI_QKV;
+    qkv.qkv = QKVDst{a.q, c.k, c.v, pos_base, c.sb, c.sh, S, m->H, m->dk, d};
+    NML_TRY(launch_linear(m->dt, qkv, st));
+    AttnArgs at{};
+    at.q = a.q;
+    at.k = c.k;
+    at.v = c.v;
+    at.out = a.att;
+    at.pos_base = pos_base;
+    at.kv_stride_b = c.sb;
+    at.kv_stride_h = c.sh;
+    at.B = B;
+    at.H = m->H;
+    at.S = S;
+    at.dk = m->dk;
+    at.scale = sqrtf((float)m->dk);
+    NML_TRY(launch_attention_prefill(m->dt, at, st));
+    LinearArgs wo{};
+    wo.x = a.att;
+    wo.lda = d;
+    wo.w = w.wo;
+    wo.bias = w.bo;
+    wo.resid = a.x;
+    wo.out = a.x;
+    wo.M = R;
+    wo.N = d;
+    wo.K = d;
+    wo.epi = EPI_BIAS_RESID;
+    NML_TRY(launch_linear(m->dt, wo, st));
+    NML_TRY(launch_rmsnorm(m->dt, a.x, w.ln2, a.xn, nullptr, nullptr, R, d, kEps, st));
+    LinearArgs f1{};
+    f1.x = a.xn;
+    f1.lda = d;
+    f1.w = w.w1;
+    f1.bias = w.b1;
+    f1.out = a.h;
+    f1.M = R;
+    f1.N = m->F;
+    f1.K = d;
+    f1.epi = EPI_BIAS_GELU;
+    NML_TRY(launch_linear(m->dt, f1, st));
+    LinearArgs f2{};
+    f2.x = a.h;
+    f2.lda = m->F;
+    f2.w = w.w2;
+    f2.bias = w.b2;
+    f2.resid = a.x;
+    f2.out = a.x;
+    f2.M = R;
+    f2.N = d;
+    f2.K = m->F;
+    f2.epi = EPI_BIAS_RESID;
+    NML_TRY(launch_linear(m->dt, f2, st));
+  }
+  NML_TRY(launch_rmsnorm(m->dt, a.x, m->lnf, a.xn, nullptr, nullptr, R, d, kEps, st));
+  return 0;
+}
+
+// logits = xn · Eᵀ for all rows, or only the last position of each sequence.
+int head(nml_model* m, const Acts& a, int B, int S, void* logits, int last_only, hipStream_t st) {
+  LinearArgs lm{};
+  lm.w = m->emb;
+  lm.out = logits;
+  lm.N = m->V;
+  lm.K = m->d;
+  lm.epi = EPI_NONE;
+  if (last_only) {
+    lm.x = static_cast<const char*>(a.xn) + (size_t)(S - 1) * m->d * m->es;
+    lm.lda = (long long)S * m->d;
+    lm.M = B;
+  } else {
+    lm.x = a.xn;
+    lm.lda = m->d;
+    lm.M = B * S;
+  }
+  return launch_linear(m->dt, lm, st);
+}
+
+int check_ready(nml_model* m) {
+  NML_REQUIRE(m != nullptr, "model is null");
+  NML_REQUIRE(m->emb && m->pos && m->lnf, "model parameters not uploaded");
+  return 0;
+}
+
+// One decode step for B rows of a cache: feeds tokens[b][pos[b]] at position
+// pos[b], leaves logits (B, V) in `logits`.
+int decode_step(nml_model* m, nml_cache* c, const Acts& a, const int64_t* tokens,
+                long long tok_stride, int32_t* pos, int* err, void* logits, hipStream_t st) {
+  const int B = c->B, d = m->d;
+  NML_TRY(launch_embed_decode(m->dt, tokens, tok_stride, pos, m->emb, m->pos, a.x, B, d, m->V,
+                              m->P, err, st));
+  const size_t layer_kv = (size_t)B * m->H * m->P * m->dk * m->es;
+  for (int l = 0; l < m->L; ++l) {
+    const Layer& w = m->layers[l];
+    void* kl = static_cast<char*>(c->k) + l * layer_kv;
+    void* vl = static_cast<char*>(c->v) + l * layer_kv;
+    const long long sb = (long long)m->H * m->P * m->dk, sh = (long long)m->P * m->dk;
+    NML_TRY(launch_rmsnorm(m->dt, a.x, w.ln1, a.xn, nullptr, nullptr, B, d, kEps, st));
+    LinearArgs qkv{};
+    qkv.x = a.xn;
+    qkv.lda = d;
+    qkv.w = w.wqkv;
+    qkv.bias = w.bqkv;
+    qkv.M = B;
+    qkv.N = 3 * d;
+    qkv.K = d;
+    qkv.epi = EPI_QKV;
+    qkv.qkv = QKVDst{a.q, kl, vl, pos, sb, sh, 1, m->H, m->dk, d};
+    NML_TRY(launch_linear(m->dt, qkv, st));
+    AttnArgs at{};
+    at.q = a.q;
+    at.k = kl;
+    at.v = vl;
+    at.out = a.att;
+    at.pos_base = pos;
+    at.kv_stride_b = sb;
+    at.kv_stride_h = sh;
+    at.B = B;
+    at.H = m->H;
+    at.S = 1;
+    at.dk = m->dk;
+    at.scale = sqrtf((float)m->dk);
+    NML_TRY(launch_attention_decode(m->dt, at, pos, m->P, a.part, st));
+    LinearArgs wo{};
+    wo.x = a.att;
+    wo.lda = d;
+    wo.w = w.wo;
+    wo.bias = w.bo;
+    wo.resid = a.x;
+    wo.out = a.x;
+    wo.M = B;
+    wo.N = d;
+    wo.K = d;
+    wo.epi = EPI_BIAS_RESID;
+    NML_TRY(launch_linear(m->dt, wo, st));
+    NML_TRY(launch_rmsnorm(m->dt, a.x, w.ln2, a.xn, nullptr, nullptr, B, d, kEps, st));
+    LinearArgs f1{};
+    f1.x = a.xn;
+    f1.lda = d;
+    f1.w = w.w1;
+    f1.bias = w.b1;
+    f1.out = a.h;
+    f1.M = B;
+    f1.N = m->F;
+    f1.K = d;
+    f1.epi = EPI_BIAS_GELU;
+    NML_TRY(launch_linear(m->dt, f1, st));
+    LinearArgs f2{};
+    f2.x = a.h;
+    f2.lda = m->F;
+    f2.w = w.w2;
+    f2.bias = w.b2;
+    f2.resid = a.x;
+    f2.out = a.x;
+    f2.M = B;
+    f2.N = d;
+    f2.K = m->F;
+    f2.epi = EPI_BIAS_RESID;
+    NML_TRY(launch_linear(m->dt, f2, st));
+  }
+  NML_TRY(launch_rmsnorm(m->dt, a.x, m->lnf, a.xn, nullptr, nullptr, B, d, kEps, st));
+  LinearArgs lm{};
+  lm.x = a.xn;
+  lm.lda = d;
+  lm.w = m->emb;
+  lm.out = logits;
+  lm.M = B;
+  lm.N = m->V;
+  lm.K = d;
+  lm.epi = EPI_NONE;
+  return launch_linear(m->dt, lm, st);
+}
+
+__global__ void add_scalar_kernel(int32_t* p, int n, int v) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) p[i] += v;
+}
+
+__global__ void copy_rows_kernel(const int64_t* __restrict__ src, long long sstride,
+                                 int64_t* __restrict__ dst, long long dstride,
+                                 const int32_t* __restrict__ lens) {
+  const int b = blockIdx.x;
+  const int n = lens[b];
+  for (int i = threadIdx.x; i < n; i += blockDim.x) dst[b * dstride + i] = src[b * sstride + i];
+}
+
+}  // namespace
+
+extern "C" {
+
+int nml_model_create(int vocab, int d_model, int num_heads, int num_layers, int max_seq_len,
+                     int d_ff, int dtype, nml_model** out) {
+  *out = nullptr;
+  NML_REQUIRE(dtype == F32 || dtype == F16, "dtype must be 0 or 1");
+  NML_REQUIRE(vocab > 0 && d_model > 0 && num_heads > 0 && num_layers > 0 && max_seq_len > 0 &&
+                  d_ff > 0,
+              "model dimensions must be positive");
+  NML_REQUIRE(d_model % num_heads == 0, "d_model (%d) must be divisible by num_heads (%d).",
+              d_model, num_heads);
+  const int vec = dtype == F16 ? 8 : 4;
+  NML_REQUIRE(d_model % vec == 0 && d_ff % vec == 0,
+              "d_model and d_ff must be multiples of %d for 16-byte loads", vec);
+  nml_model* m = new nml_model();
+  m->V = vocab;
+  m->d = d_model;
+  m->H = num_heads;
+  m->L = num_layers;
+  m->P = max_seq_len;
+  m->F = d_ff;
+  m->dt = dtype;
+  m->dk = d_model / num_heads;
+  m->es = dtype_size(dtype);
+  m->layers.resize(num_layers);
+  size_t total = align256(param_elems(m, NML_P_TOKEN_EMB) * m->es) +
+                 align256(param_elems(m, NML_P_POS_EMB) * m->es) +
+                 align256(param_elems(m, NML_P_LN_F) * m->es);
+  for (int k : kLayerKinds) total += (size_t)num_layers * align256(param_elems(m, k) * m->es);
+  hipError_t e = hipMalloc(&m->arena, total);
+  if (e != hipSuccess) {
+    set_error("model: hipMalloc(%zu) failed: %s", total, hipGetErrorString(e));
+    delete m;
+    return -1;
+  }
+  m->arena_bytes = total;
+  char* p = static_cast<char*>(m->arena);
+  auto take = [&](int kind, int layer) {
+    void** slot = param_slot(m, kind, layer);
+    *slot = p;
+    p += align256(param_elems(m, kind) * m->es);
+  };
+  take(NML_P_TOKEN_EMB, 0);
+  take(NML_P_POS_EMB, 0);
+  take(NML_P_LN_F, 0);
+  for (int l = 0; l < num_layers; ++l)
+    for (int k : kLayerKinds) take(k, l);
+  *out = m;
+  return 0;
+}
+
+int nml_model_destroy(nml_model* m) {
+  if (!m) return 0;
+  (void)hipStreamSynchronize(nml::stream());
+  m->ws.release();
+  m->kvs.release();
+  m->logits_ws.release();
+  m->small.release();
+  if (m->arena) (void)hipFree(m->arena);
+  delete m;
+  return 0;
+}
+
+int nml_model_set_param(nml_model* m, int kind, int layer, const void* host, size_t bytes) {
+  NML_REQUIRE(m != nullptr, "model is null");
+  void** slot = param_slot(m, kind, layer);
+  NML_REQUIRE(slot != nullptr, "unknown parameter kind %d / layer %d", kind, layer);
+  const size_t want = param_elems(m, kind) * m->es;
+  NML_REQUIRE(bytes == want, "parameter kind %d: expected %zu bytes, got %zu", kind, want, bytes);
+  NML_HIP(hipMemcpyAsync(*slot, host, bytes, hipMemcpyHostToDevice, nml::stream()));
+  NML_HIP(hipStreamSynchronize(nml::stream()));
+  return 0;
+}
+
+int nml_model_param_ptr(nml_model* m, int kind, int layer, void** ptr) {
+  NML_REQUIRE(m != nullptr, "model is null");
+  void** slot = param_slot(m, kind, layer);
+  NML_REQUIRE(slot != nullptr, "unknown parameter kind %d / layer %d", kind, layer);
+  *ptr = *slot;
+  return 0;
+}
+
+int nml_model_forward(nml_model* m, const int64_t* ids, size_t batch, size_t seq, void* logits,
+                      int last_only) {
+  NML_TRY(check_ready(m));
+  NML_REQUIRE(seq <= (size_t)m->P, "Sequence length %zu exceeds maximum sequence length %d", seq,
+              m->P);
+  if (batch == 0 || seq == 0) return 0;
+  const int B = (int)batch, S = (int)seq;
+  hipStream_t st = nml::stream();
+  Acts a;
+  NML_TRY(acts_for(m, B * S, 0, &a));
+  const size_t kvb = align256((size_t)B * S * m->d * m->es);
+  NML_TRY(m->kvs.ensure(2 * kvb));
+  void* kbuf = m->kvs.p;
+  void* vbuf = static_cast<char*>(m->kvs.p) + kvb;
+  NML_TRY(launch_embed(m->dt, ids, m->emb, m->pos, nullptr, a.x, B, S, m->d, m->V, m->P, nullptr,
+                       st));
+  const long long sb = (long long)m->H * S * m->dk, sh = (long long)S * m->dk;
+  NML_TRY(trunk(m, a, B, S, nullptr, [&](int) { return KVView{kbuf, vbuf, sb, sh}; }, st));
+  return head(m, a, B, S, logits, last_only, st);
+}
+
+int nml_model_loss(nml_model* m, const int64_t* ids, const int64_t* labels, size_t batch,
+                   size_t seq, int64_t ignore_index, int has_ignore, double* loss) {
+  NML_TRY(check_ready(m));
+  NML_REQUIRE(seq <= (size_t)m->P, "Sequence length %zu exceeds maximum sequence length %d", seq,
+              m->P);
+  const int B = (int)batch, S = (int)seq, R = B * S;
+  if (R == 0) {
+    *loss = 0.0;
+    return 0;
+  }
+  hipStream_t st = nml::stream();
+  Acts a;
+  NML_TRY(acts_for(m, R, 0, &a));
+  const size_t kvb = align256((size_t)R * m->d * m->es);
+  NML_TRY(m->kvs.ensure(2 * kvb));
+  void* kbuf = m->kvs.p;
+  void* vbuf = static_cast<char*>(m->kvs.p) + kvb;
+  Small sm;
+  NML_TRY(small_for(m, 1, &sm));
+  NML_HIP(hipMemsetAsync(sm.err, 0, sizeof(int), st));
+  NML_TRY(launch_embed(m->dt, ids, m->emb, m->pos, nullptr, a.x, B, S, m->d, m->V, m->P, sm.err,
+                       st));
+  const long long sb = (long long)m->H * S * m->dk, sh = (long long)S * m->dk;
+  NML_TRY(trunk(m, a, B, S, nullptr, [&](int) { return KVView{kbuf, vbuf, sb, sh}; }, st));
+  // Logits in row chunks of ≤ 512 MiB, never all (R, V) at once.
+  size_t chunk = R;
+  while (chunk > 1 && chunk * m->V * m->es > ((size_t)512 << 20)) chunk = (chunk + 1) / 2;
+  const size_t lb = align256(chunk * m->V * m->es);
+  const size_t rb = align256((size_t)R * 4);
+  NML_TRY(m->logits_ws.ensure(lb + 2 * rb));
+  void* lg = m->logits_ws.p;
+  float* row_loss = reinterpret_cast<float*>(static_cast<char*>(m->logits_ws.p) + lb);
+  int* row_valid = reinterpret_cast<int*>(static_cast<char*>(m->logits_ws.p) + lb + rb);
+  for (size_t r0 = 0; r0 < (size_t)R; r0 += chunk) {
+    const int n = (int)(((size_t)R - r0 < chunk) ? (size_t)R - r0 : chunk);
+    LinearArgs lm{};
+    lm.x = static_cast<const char*>(a.xn) + r0 * m->d * m->es;
+    lm.lda = m->d;
+    lm.w = m->emb;
+    lm.out = lg;
+    lm.M = n;
+    lm.N = m->V;
+    lm.K = m->d;
+    lm.epi = EPI_NONE;
+    NML_TRY(launch_linear(m->dt, lm, st));
+    NML_TRY(launch_ce_rows(m->dt, lg, n, m->V, labels + r0, ignore_index, has_ignore, row_loss,
+                           row_valid, sm.err, st));
+    NML_TRY(launch_ce_reduce(row_loss, row_valid, n, sm.acc, r0 > 0, st));
+  }
+  NML_TRY(launch_ce_finalize(sm.acc, sm.acc + 2, st));
+  double host[3];
+  int herr = 0;
+  NML_HIP(hipMemcpyAsync(host, sm.acc, sizeof(host), hipMemcpyDeviceToHost, st));
+  NML_HIP(hipMemcpyAsync(&herr, sm.err, sizeof(int), hipMemcpyDeviceToHost, st));
+  NML_HIP(hipStreamSynchronize(st));
+  NML_REQUIRE((herr & 1) == 0, "Token ID out of range [0, %d)", m->V);
+  NML_REQUIRE((herr & 2) == 0, "label out of range [0, %d)", m->V);
+  *loss = host[2];
+  return 0;
+}
+
+int nml_cache_create(nml_model* m, size_t batch, nml_cache** out) {
+  *out = nullptr;
+  NML_TRY(check_ready(m));
+  NML_REQUIRE(batch > 0 && batch <= 4096, "cache batch %zu out of range", batch);
+  nml_cache* c = new nml_cache();
+  c->m = m;
+  c->B = (int)batch;
+  const size_t bytes = (size_t)m->L * batch * m->H * m->P * m->dk * m->es;
+  hipError_t e1 = hipMalloc(&c->k, bytes);
+  hipError_t e2 = e1 == hipSuccess ? hipMalloc(&c->v, bytes) : e1;
+  hipError_t e3 = e2 == hipSuccess ? hipMalloc(&c->len_dev, align256(batch * 4)) : e2;
+  if (e3 != hipSuccess) {
+    set_error("cache: allocation of 2 × %zu bytes failed: %s", bytes, hipGetErrorString(e3));
+    if (c->k) (void)hipFree(c->k);
+    if (c->v) (void)hipFree(c->v);
+    delete c;
+    return -1;
+  }
+  c->len.assign(batch, 0);
+  NML_HIP(hipMemsetAsync(c->len_dev, 0, batch * 4, nml::stream()));
+  *out = c;
+  return 0;
+}
+
+int nml_cache_destroy(nml_cache* c) {
+  if (!c) return 0;
+  (void)hipStreamSynchronize(nml::stream());
+  if (c->k) (void)hipFree(c->k);
+  if (c->v) (void)hipFree(c->v);
+  if (c->len_dev) (void)hipFree(c->len_dev);
+  delete c;
+  return 0;
+}
+
+int nml_cache_length(nml_cache* c, size_t* len) {
+  NML_REQUIRE(c != nullptr, "cache is null");
+  *len = c->len.empty() ? 0 : (size_t)c->len[0];
+  return 0;
+}
+
+int nml_model_forward_cached(nml_model* m, nml_cache* c, const int64_t* ids, size_t batch,
+                             size_t seq, void* logits, int last_only) {
+  NML_TRY(check_ready(m));
+  NML_REQUIRE(c != nullptr && c->m == m, "cache does not belong to this model");
+  NML_REQUIRE((int)batch == c->B, "batch %zu does not match the cache batch %d", batch, c->B);
+  const int B = (int)batch, S = (int)seq;
+  if (S == 0) return 0;
+  const int start = c->len[0];
+  NML_REQUIRE((size_t)start + seq <= (size_t)m->P,
+              "Sequence length %zu exceeds maximum sequence length %d", start + seq, m->P);
+  hipStream_t st = nml::stream();
+  Acts a;
+  NML_TRY(acts_for(m, B * S, 0, &a));
+  NML_TRY(launch_embed(m->dt, ids, m->emb, m->pos, c->len_dev, a.x, B, S, m->d, m->V, m->P,
+                       nullptr, st));
+  const size_t layer_kv = (size_t)B * m->H * m->P * m->dk * m->es;
+  const long long sb = (long long)m->H * m->P * m->dk, sh = (long long)m->P * m->dk;
+  NML_TRY(trunk(m, a, B, S, c->len_dev,
+                [&](int l) {
+                  return KVView{static_cast<char*>(c->k) + l * layer_kv,
+                                static_cast<char*>(c->v) + l * layer_kv, sb, sh};
+                },
+                st));
+  NML_TRY(head(m, a, B, S, logits, last_only, st));
+  add_scalar_kernel<<<(B + 255) / 256, 256, 0, st>>>(c->len_dev, B, S);
+  NML_LAUNCHED();
+  for (auto& v : c->len) v += S;
+  return 0;
+}
+
+int nml_model_generate(nml_model* m, const int64_t* prompts, size_t prompt_stride,
+                       const int32_t* prompt_len, size_t batch, size_t max_new,
+                       float temperature, int top_k, float top_p, float repetition_penalty,
+                       const double* u, int64_t* tokens_out, size_t out_stride, int use_graph) {
+  NML_TRY(check_ready(m));
+  const int B = (int)batch;
+  if (B == 0 || max_new == 0) return 0;
+  int maxp = 0;
+  bool same = true;
+  for (int b = 0; b < B; ++b) {
+    NML_REQUIRE(prompt_len[b] > 0, "prompt %d is empty", b);
+    NML_REQUIRE((size_t)prompt_len[b] <= prompt_stride, "prompt %d longer than its stride", b);
+    maxp = prompt_len[b] > maxp ? prompt_len[b] : maxp;
+    same = same && prompt_len[b] == prompt_len[0];
+    // The reference re-forwards the whole sequence before each new token; its last
+    // forward covers prompt_len + max_new − 1 tokens (models/gpt.py:82-83).
+    NML_REQUIRE((size_t)prompt_len[b] + max_new - 1 <= (size_t)m->P,
+                "Sequence length %zu exceeds maximum sequence length %d",
+                (size_t)prompt_len[b] + max_new - 1, m->P);
+  }
+  NML_REQUIRE(out_stride >= (size_t)maxp + max_new, "tokens_out stride too small");
+  NML_REQUIRE(temperature <= 0.f || u != nullptr, "uniforms required for sampling");
+  hipStream_t st = nml::stream();
+
+  nml_cache* c = nullptr;
+  NML_TRY(nml_cache_create(m, batch, &c));
+  struct Guard {
+    nml_cache* c;
+    ~Guard() { nml_cache_destroy(c); }
+  } guard{c};
+
+  Small sm;
+  NML_TRY(small_for(m, B, &sm));
+  std::vector<int32_t> plen(prompt_len, prompt_len + B);
+  NML_HIP(hipMemcpyAsync(sm.plen, plen.data(), B * 4, hipMemcpyHostToDevice, st));
+  NML_HIP(hipMemsetAsync(sm.err, 0, sizeof(int), st));
+  copy_rows_kernel<<<B, 256, 0, st>>>(prompts, (long long)prompt_stride, tokens_out,
+                                      (long long)out_stride, sm.plen);
+  NML_LAUNCHED();
+
+  // Logits for the batch (B, V).
+  const size_t lb = align256((size_t)B * m->V * m->es);
+  NML_TRY(m->logits_ws.ensure(lb));
+  void* logits = m->logits_ws.p;
+
+  // Prefill: one batched pass when all prompts have the same length, else per row.
+  const size_t layer_kv = (size_t)B * m->H * m->P * m->dk * m->es;
+  const long long sb = (long long)m->H * m->P * m->dk, sh = (long long)m->P * m->dk;
+  NML_HIP(hipMemsetAsync(sm.zeros, 0, B * 4, st));
+  if (same) {
+    const int S = plen[0];
+    Acts a;
+    NML_TRY(acts_for(m, B * S, B, &a));
+    if ((int)prompt_stride != S) {
+      for (int b = 0; b < B; ++b)
+        NML_TRY(launch_embed(m->dt, prompts + (size_t)b * prompt_stride, m->emb, m->pos, nullptr,
+                             static_cast<char*>(a.x) + (size_t)b * S * m->d * m->es, 1, S, m->d,
+                             m->V, m->P, sm.err, st));
+    } else {
+      NML_TRY(launch_embed(m->dt, prompts, m->emb, m->pos, nullptr, a.x, B, S, m->d, m->V, m->P,
+                           sm.err, st));
+    }
+    NML_TRY(trunk(m, a, B, S, sm.zeros,
+                  [&](int l) {
+                    return KVView{static_cast<char*>(c->k) + l * layer_kv,
+                                  static_cast<char*>(c->v) + l * layer_kv, sb, sh};
+                  },
+                  st));
+    NML_TRY(head(m, a, B, S, logits, 1, st));
+  } else {
+    for (int b = 0; b < B; ++b) {
+      const int S = plen[b];
+      Acts a;
+      NML_TRY(acts_for(m, S, B, &a));
+      NML_TRY(launch_embed(m->dt, prompts + (size_t)b * prompt_stride, m->emb, m->pos, nullptr,
+                           a.x, 1, S, m->d, m->V, m->P, sm.err, st));
+      NML_TRY(trunk(m, a, 1, S, sm.zeros,
+                    [&](int l) {
+                      return KVView{static_cast<char*>(c->k) + l * layer_kv + b * sb * m->es,
+                                    static_cast<char*>(c->v) + l * layer_kv + b * sb * m->es, sb,
+                                    sh};
+                    },
+                    st));
+      NML_TRY(head(m, a, 1, S, static_cast<char*>(logits) + (size_t)b * m->V * m->es, 1, st));
+    }
+  }
+  // pos[b] = prompt_len[b] − 1, then the first choice advances it to prompt_len[b].
+  std::vector<int32_t> pos0(B);
+  for (int b = 0; b < B; ++b) pos0[b] = plen[b] - 1;
+  NML_HIP(hipMemcpyAsync(sm.pos, pos0.data(), B * 4, hipMemcpyHostToDevice, st));
+
+  SampleArgs sa{};
+  sa.logits = logits;
+  sa.logits_stride = m->V;
+  sa.B = B;
+  sa.V = m->V;
+  sa.temperature = temperature;
+  sa.top_k = top_k;
+  sa.top_p = top_p;
+  sa.rep_penalty = repetition_penalty;
+  sa.uniforms = u;
+  sa.tokens = tokens_out;
+  sa.tok_stride = (long long)out_stride;
+  sa.pos = sm.pos;
+  sa.plen = sm.plen;
+  NML_TRY(launch_sample(m->dt, sa, st));
+
+  Acts a;
+  NML_TRY(acts_for(m, B, B, &a));
+  hipEvent_t e0 = nullptr, e1 = nullptr;
+  NML_HIP(hipEventCreate(&e0));
+  NML_HIP(hipEventCreate(&e1));
+  const int steps = (int)max_new - 1;
+  int rc = 0;
+  if (steps > 0) {
+    if (use_graph) {
+      hipGraph_t graph = nullptr;
+      hipGraphExec_t exec = nullptr;
+      NML_HIP(hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal));
+      int r1 = decode_step(m, c, a, tokens_out, (long long)out_stride, sm.pos, sm.err, logits, st);
+      int r2 = r1 == 0 ? launch_sample(m->dt, sa, st) : -1;
+      hipError_t ec = hipStreamEndCapture(st, &graph);
+      if (r1 != 0 || r2 != 0) {
+        if (graph) (void)hipGraphDestroy(graph);
+        return -1;
+      }
+      NML_HIP(ec);
+      NML_HIP(hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0));
+      NML_HIP(hipEventRecord(e0, st));
+      for (int t = 0; t < steps && rc == 0; ++t)
+        if (hipGraphLaunch(exec, st) != hipSuccess) rc = -1;
+      NML_HIP(hipEventRecord(e1, st));
+      (void)hipStreamSynchronize(st);
+      (void)hipGraphExecDestroy(exec);
+      (void)hipGraphDestroy(graph);
+      NML_REQUIRE(rc == 0, "hipGraphLaunch failed");
+    } else {
+      NML_HIP(hipEventRecord(e0, st));
+      for (int t = 0; t < steps; ++t) {
+        NML_TRY(decode_step(m, c, a, tokens_out, (long long)out_stride, sm.pos, sm.err, logits, st));
+        NML_TRY(launch_sample(m->dt, sa, st));
+      }
+      NML_HIP(hipEventRecord(e1, st));
+    }
+  } else {
+    NML_HIP(hipEventRecord(e0, st));
+    NML_HIP(hipEventRecord(e1, st));
+  }
+  int herr = 0;
+  NML_HIP(hipMemcpyAsync(&herr, sm.err, sizeof(int), hipMemcpyDeviceToHost, st));
+  NML_HIP(hipStreamSynchronize(st));
+  float ms = 0.f;
+  NML_HIP(hipEventElapsedTime(&ms, e0, e1));
+  (void)hipEventDestroy(e0);
+  (void)hipEventDestroy(e1);
+  m->last_decode_ms = ms;
+  m->last_decode_steps = steps;
+  NML_REQUIRE(herr == 0, "Token ID out of range [0, %d)", m->V);
+  return 0;
+}
+
+int nml_model_last_decode_ms(nml_model* m, float* ms_per_step) {
+  NML_REQUIRE(m != nullptr, "model is null");
+  *ms_per_step = m->last_decode_steps > 0 ? m->last_decode_ms / m->last_decode_steps : 0.f;
+  return 0;
+}
+
+}  // extern "C"

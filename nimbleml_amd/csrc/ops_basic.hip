@@ -1,0 +1,176 @@
+// Row-wise and elementwise kernels: embedding gather + position add, RMSNorm,
+// tanh-GELU. All are HBM-bound; one workgroup (256 lanes, 4 waves) per row.
+#include "kernels.hpp"
+
+namespace nml {
+
+namespace {
+
+// x = E[ids] + P[pos]  (models/gpt.py:85-86; gather kernels/embedding_scatter.py:25-36,
+// position prefix layers/embedding.py:72-118). fp16 + fp16 computed in fp32 and rounded
+// once is the correctly rounded fp16 sum, i.e. NumPy's fp16 add: bit-exact.
+template <typename T>
+__global__ __launch_bounds__(256) void embed_kernel(const int64_t* __restrict__ ids,
+                                                    const T* __restrict__ emb,
+                                                    const T* __restrict__ posw,
+                                                    const int32_t* __restrict__ pos_base,
+                                                    T* __restrict__ out, int S, int d, int V,
+                                                    int P, int* __restrict__ err) {
+  const int row = blockIdx.x;
+  const int b = row / S, s = row - b * S;
+  const int64_t id = ids[row];
+  const int p = (pos_base ? pos_base[b] : 0) + s;
+  T* o = out + static_cast<size_t>(row) * d;
+  if (id < 0 || id >= V || p < 0 || p >= P) {
+    if (threadIdx.x == 0 && err) atomicOr(err, 1);
+    for (int j = threadIdx.x; j < d; j += blockDim.x) o[j] = static_cast<T>(0.f);
+    return;
+  }
+  const T* e = emb + static_cast<size_t>(id) * d;
+  const T* q = posw + static_cast<size_t>(p) * d;
+  for (int j = threadIdx.x; j < d; j += blockDim.x)
+    o[j] = static_cast<T>(static_cast<float>(e[j]) + static_cast<float>(q[j]));
+}
+
+template <typename T>
+__global__ __launch_bounds__(256) void embed_decode_kernel(
+    const int64_t* __restrict__ tokens, long long tok_stride, const int32_t* __restrict__ pos,
+    const T* __restrict__ emb, const T* __restrict__ posw, T* __restrict__ out, int d, int V,
+    int P, int* __restrict__ err) {
+  const int b = blockIdx.x;
+  const int p = pos[b];
+  const int64_t id = (p >= 0) ? tokens[b * tok_stride + p] : -1;
+  T* o = out + static_cast<size_t>(b) * d;
+  if (id < 0 || id >= V || p < 0 || p >= P) {
+    if (threadIdx.x == 0 && err) atomicOr(err, 1);
+    for (int j = threadIdx.x; j < d; j += blockDim.x) o[j] = static_cast<T>(0.f);
+    return;
+  }
+  const T* e = emb + static_cast<size_t>(id) * d;
+  const T* q = posw + static_cast<size_t>(p) * d;
+  for (int j = threadIdx.x; j < d; j += blockDim.x)
+    o[j] = static_cast<T>(static_cast<float>(e[j]) + static_cast<float>(q[j]));
+}
+
+// RMSNorm (kernels/fused_rmsnorm.py:360-369).
+//   fp32: ms = mean(x²); rms = sqrt(ms + eps); y = (x / rms) · γ
+//   fp16: x² rounded to fp16, mean accumulated in fp32; inv = fp16(1 / rms);
+//         y = fp16(fp16(x · inv) · γ)
+template <typename T>
+__global__ __launch_bounds__(256) void rmsnorm_kernel(const T* __restrict__ x,
+                                                      const T* __restrict__ g,
+                                                      T* __restrict__ out, float* __restrict__ ms,
+                                                      float* __restrict__ rmsv, int d, float eps) {
+#pragma clang fp contract(off)
+  __shared__ float red[16];
+  const int row = blockIdx.x;
+  const T* xr = x + static_cast<size_t>(row) * d;
+  T* o = out + static_cast<size_t>(row) * d;
+  float acc = 0.f;
+  for (int j = threadIdx.x; j < d; j += blockDim.x) {
+    const float v = static_cast<float>(xr[j]);
+    acc += rnd<T>(v * v);
+  }
+  const float m = block_sum(acc, red) / static_cast<float>(d);
+  const float r = sqrtf(m + eps);
+  if (threadIdx.x == 0) {
+    if (ms) ms[row] = m;
+    if (rmsv) rmsv[row] = r;
+  }
+  if constexpr (sizeof(T) == 2) {
+    const float inv = rnd<T>(1.0f / r);
+    for (int j = threadIdx.x; j < d; j += blockDim.x) {
+      const float v = rnd<T>(static_cast<float>(xr[j]) * inv);
+      o[j] = static_cast<T>(v * static_cast<float>(g[j]));
+    }
+  } else {
+    for (int j = threadIdx.x; j < d; j += blockDim.x)
+      o[j] = static_cast<T>((static_cast<float>(xr[j]) / r) * static_cast<float>(g[j]));
+  }
+}
+
+// GELU with the reference's (out, tanh_u) outputs (native/src/gelu.cpp:12-21).
+template <typename T>
+__global__ __launch_bounds__(256) void gelu_kernel(const T* __restrict__ x, T* __restrict__ out,
+                                                   float* __restrict__ tanh_u, size_t n) {
+#pragma clang fp contract(off)
+  for (size_t i = blockIdx.x * static_cast<size_t>(blockDim.x) + threadIdx.x; i < n;
+       i += static_cast<size_t>(gridDim.x) * blockDim.x) {
+    const float v = static_cast<float>(x[i]);
+    out[i] = static_cast<T>(gelu_t<T>(v));
+    if (tanh_u) {
+      if constexpr (sizeof(T) == 2) {
+        const float k = static_cast<float>(static_cast<half_t>(0.7978845608028654f));
+        const float c = static_cast<float>(static_cast<half_t>(0.044715f));
+        float t = rnd<T>(c * v);
+        t = rnd<T>(t * v);
+        t = rnd<T>(t * v);
+        t = rnd<T>(v + t);
+        t = rnd<T>(k * t);
+        tanh_u[i] = rnd<T>(tanhf(t));
+      } else {
+        const float x3 = v * v * v;
+        tanh_u[i] = tanhf(0.7978845608028654f * (v + 0.044715f * x3));
+      }
+    }
+  }
+}
+
+}  // namespace
+
+int launch_embed(int dt, const int64_t* ids, const void* emb, const void* pos,
+                 const int32_t* pos_base, void* out, int B, int S, int d, int V, int P, int* err,
+                 hipStream_t st) {
+  if (B * S == 0) return 0;
+  dim3 grid(B * S), block(256);
+  if (dt == F16)
+    embed_kernel<half_t><<<grid, block, 0, st>>>(ids, (const half_t*)emb, (const half_t*)pos,
+                                                 pos_base, (half_t*)out, S, d, V, P, err);
+  else
+    embed_kernel<float><<<grid, block, 0, st>>>(ids, (const float*)emb, (const float*)pos,
+                                                pos_base, (float*)out, S, d, V, P, err);
+  NML_LAUNCHED();
+  return 0;
+}
+
+int launch_embed_decode(int dt, const int64_t* tokens, long long tok_stride, const int32_t* pos,
+                        const void* emb, const void* posw, void* out, int B, int d, int V, int P,
+                        int* err, hipStream_t st) {
+  if (B == 0) return 0;
+  if (dt == F16)
+    embed_decode_kernel<half_t><<<B, 256, 0, st>>>(tokens, tok_stride, pos, (const half_t*)emb,
+                                                   (const half_t*)posw, (half_t*)out, d, V, P,
+                                                   err);
+  else
+    embed_decode_kernel<float><<<B, 256, 0, st>>>(tokens, tok_stride, pos, (const float*)emb,
+                                                  (const float*)posw, (float*)out, d, V, P, err);
+  NML_LAUNCHED();
+  return 0;
+}
+
+int launch_rmsnorm(int dt, const void* x, const void* g, void* out, float* ms, float* rms,
+                   int rows, int d, float eps, hipStream_t st) {
+  if (rows == 0) return 0;
+  if (dt == F16)
+    rmsnorm_kernel<half_t><<<rows, 256, 0, st>>>((const half_t*)x, (const half_t*)g,
+                                                 (half_t*)out, ms, rms, d, eps);
+  else
+    rmsnorm_kernel<float><<<rows, 256, 0, st>>>((const float*)x, (const float*)g, (float*)out,
+                                                ms, rms, d, eps);
+  NML_LAUNCHED();
+  return 0;
+}
+
+int launch_gelu(int dt, const void* x, void* out, float* tanh_u, size_t n, hipStream_t st) {
+  if (n == 0) return 0;
+  size_t blocks = (n + 255) / 256;
+  if (blocks > 65536) blocks = 65536;
+  if (dt == F16)
+    gelu_kernel<half_t><<<blocks, 256, 0, st>>>((const half_t*)x, (half_t*)out, tanh_u, n);
+  else
+    gelu_kernel<float><<<blocks, 256, 0, st>>>((const float*)x, (float*)out, tanh_u, n);
+  NML_LAUNCHED();
+  return 0;
+}
+
+}  // namespace nml

@@ -1,0 +1,421 @@
+// Next-token selection on device, one 1024-lane workgroup per sequence, following
+// _sample_logits (models/generate.py:23-59) step by step:
+//   x = float32(logits); repetition penalty on tokens already in the row
+//   (generate.py:9-20: x<0 → x·p, else x/p, once per distinct token);
+//   T ≤ 0 → argmax (first index on ties);
+//   x /= T; top-k keeps x ≥ (k-th largest x) (ties kept, :43-46), others → −1e9;
+//   p = exp(x − max) / Σ;
+//   no top-p: the token is the first index i (index order) whose float64
+//   cumulative p, divided by the total, exceeds u — what RandomState.choice does
+//   with its uniform draw u (float64 cumsum, cdf/cdf[-1], searchsorted 'right');
+//   top-p (:49-58): walk p in descending order, keep the prefix whose running sum
+//   stays ≤ top_p (at least one), renormalise, and pick the first position of
+//   that descending order whose float64 running sum / total exceeds u.
+// No sort is formed: every "k-th largest" and "first descending position whose
+// running mass exceeds a target" is found by a 4-pass, 8-bit radix select over
+// the order-preserving integer image of x, with per-bin counts and masses. Ties
+// in the descending order are taken in ascending index order.
+#include "kernels.hpp"
+
+namespace nml {
+
+namespace {
+
+constexpr int kThreads = 1024;
+constexpr int kWaves = kThreads / 64;
+constexpr int kBitmapWords = 2048;  // repetition-penalty membership, V ≤ 65536
+
+__device__ __forceinline__ uint32_t fkey(float f) {
+  const uint32_t u = __float_as_uint(f);
+  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+
+struct Shared {
+  int hist_cnt[256];
+  double hist_mass[256];
+  uint32_t bitmap[kBitmapWords];
+  float redf[kWaves];
+  int redi[kWaves];
+  double redd[kWaves];
+  uint32_t sel_prefix;
+  int sel_k;
+  double sel_cum;
+  int sel_bin_cnt;
+  double sel_bin_mass;
+  int found_index;
+};
+
+__device__ float block_max_f(float v, Shared& sh) {
+  v = wave_max(v);
+  __syncthreads();
+  if ((threadIdx.x & 63) == 0) sh.redf[threadIdx.x >> 6] = v;
+  __syncthreads();
+  float t = sh.redf[0];
+  for (int i = 1; i < kWaves; ++i) t = fmaxf(t, sh.redf[i]);
+  return t;
+}
+
+__device__ float block_sum_f(float v, Shared& sh) {
+  v = wave_sum(v);
+  __syncthreads();
+  if ((threadIdx.x & 63) == 0) sh.redf[threadIdx.x >> 6] = v;
+  __syncthreads();
+  float t = 0.f;
+  for (int i = 0; i < kWaves; ++i) t += sh.redf[i];
+  return t;
+}
+
+// Exclusive prefix over threads (thread order) of a double; also returns the total.
+__device__ double block_excl_scan_d(double v, double* total, Shared& sh) {
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  double inc = v;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const double t = __shfl_up(inc, o, 64);
+    if (lane >= o) inc += t;
+  }
+  __syncthreads();
+  if (lane == 63) sh.redd[w] = inc;
+  __syncthreads();
+  double before = 0.0, tot = 0.0;
+  for (int i = 0; i < kWaves; ++i) {
+    if (i < w) before += sh.redd[i];
+    tot += sh.redd[i];
+  }
+  *total = tot;
+  return before + inc - v;
+}
+
+__device__ int block_excl_scan_i(int v, int* total, Shared& sh) {
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  int inc = v;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const int t = __shfl_up(inc, o, 64);
+    if (lane >= o) inc += t;
+  }
+  __syncthreads();
+  if (lane == 63) sh.redi[w] = inc;
+  __syncthreads();
+  int before = 0, tot = 0;
+  for (int i = 0; i < kWaves; ++i) {
+    if (i < w) before += sh.redi[i];
+    tot += sh.redi[i];
+  }
+  *total = tot;
+  return before + inc - v;
+}
+
+template <typename T>
+struct Row {
+  const T* lg;
+  int V;
+  float pen;
+  float inv_t;       // unused when greedy
+  float temperature;
+  bool use_pen;
+  const uint32_t* bitmap;
+
+  // Penalised float32 logit (generate.py:34-37 then :9-20).
+  __device__ float base(int i) const {
+    float x = static_cast<float>(lg[i]);
+    if (use_pen && ((bitmap[i >> 5] >> (i & 31)) & 1u)) x = x < 0.f ? x * pen : x / pen;
+    return x;
+  }
+  // After temperature (generate.py:42): float32 division by float32(T).
+  __device__ float scaled(int i) const { return base(i) / temperature; }
+};
+
+// k-th largest key among keys of x over all i (k ≥ 1).
+template <typename F>
+__device__ uint32_t select_kth_key(int V, int k, F key_of, Shared& sh) {
+  uint32_t prefix = 0, mask = 0;
+  if (threadIdx.x == 0) sh.sel_k = k;
+  for (int shift = 24; shift >= 0; shift -= 8) {
+    for (int i = threadIdx.x; i < 256; i += kThreads) sh.hist_cnt[i] = 0;
+    __syncthreads();
+    for (int i = threadIdx.x; i < V; i += kThreads) {
+      const uint32_t key = key_of(i);
+      if ((key & mask) == prefix) atomicAdd(&sh.hist_cnt[(key >> shift) & 255u], 1);
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+      int cum = 0, kk = sh.sel_k, chosen = 0;
+      for (int bin = 255; bin >= 0; --bin) {
+        if (cum + sh.hist_cnt[bin] >= kk) {
+          chosen = bin;
+          break;
+        }
+        cum += sh.hist_cnt[bin];
+      }
+      sh.sel_k = kk - cum;
+      sh.sel_prefix = prefix | (static_cast<uint32_t>(chosen) << shift);
+    }
+    __syncthreads();
+    prefix = sh.sel_prefix;
+    mask |= 255u << shift;
+  }
+  return prefix;
+}
+
+// First position of the descending order (key desc, index asc) over the elements
+// with in_set(i) whose inclusive running mass (weights w) exceeds `target`.
+// Returns the key τ, the 1-based tie rank j among in-set elements with key τ,
+// and the mass before the τ group.
+template <typename FK, typename FW, typename FS>
+__device__ void select_by_mass(int V, double target, FK key_of, FW weight, FS in_set,
+                               uint32_t* tau, int* rank, Shared& sh) {
+  uint32_t prefix = 0, mask = 0;
+  if (threadIdx.x == 0) sh.sel_cum = 0.0;
+  for (int shift = 24; shift >= 0; shift -= 8) {
+    for (int i = threadIdx.x; i < 256; i += kThreads) {
+      sh.hist_cnt[i] = 0;
+      sh.hist_mass[i] = 0.0;
+    }
+    __syncthreads();
+    for (int i = threadIdx.x; i < V; i += kThreads) {
+      if (!in_set(i)) continue;
+      const uint32_t key = key_of(i);
+      if ((key & mask) == prefix) {
+        const uint32_t bin = (key >> shift) & 255u;
+        atomicAdd(&sh.hist_cnt[bin], 1);
+        atomicAdd(&sh.hist_mass[bin], static_cast<double>(weight(i)));
+      }
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+      double cum = sh.sel_cum;
+      int chosen = -1, last_nonempty = -1;
+      double cum_at_last = cum;
+      for (int bin = 255; bin >= 0; --bin) {
+        if (sh.hist_cnt[bin] == 0) continue;
+        if (cum + sh.hist_mass[bin] > target) {
+          chosen = bin;
+          break;
+        }
+        last_nonempty = bin;
+        cum_at_last = cum;
+        cum += sh.hist_mass[bin];
+      }
+      if (chosen < 0) {  // rounding left the target at the very end: take the last element
+        chosen = last_nonempty < 0 ? 0 : last_nonempty;
+        cum = cum_at_last;
+      }
+      sh.sel_cum = cum;
+      sh.sel_bin_cnt = sh.hist_cnt[chosen];
+      sh.sel_bin_mass = sh.hist_mass[chosen];
+      sh.sel_prefix = prefix | (static_cast<uint32_t>(chosen) << shift);
+    }
+    __syncthreads();
+    prefix = sh.sel_prefix;
+    mask |= 255u << shift;
+  }
+  const int cnt = sh.sel_bin_cnt;
+  int j = 1;
+  if (cnt > 1) {
+    const double w = sh.sel_bin_mass / cnt;
+    const double jj = w > 0.0 ? floor((target - sh.sel_cum) / w) + 1.0 : 1.0;
+    j = jj < 1.0 ? 1 : (jj > cnt ? cnt : static_cast<int>(jj));
+  }
+  *tau = prefix;
+  *rank = j;
+}
+
+// Index of the j-th (1-based, index order) element with pred(i); -1 if none.
+template <typename FP>
+__device__ int find_nth(int V, int j, FP pred, Shared& sh) {
+  const int seg = (V + kThreads - 1) / kThreads;
+  const int lo = threadIdx.x * seg, hi = min(V, lo + seg);
+  int c = 0;
+  for (int i = lo; i < hi; ++i) c += pred(i) ? 1 : 0;
+  int total = 0;
+  const int before = block_excl_scan_i(c, &total, sh);
+  if (threadIdx.x == 0) sh.found_index = -1;
+  __syncthreads();
+  if (j <= total && before < j && before + c >= j) {
+    int k = before;
+    for (int i = lo; i < hi; ++i) {
+      if (pred(i) && ++k == j) {
+        sh.found_index = i;
+        break;
+      }
+    }
+  }
+  __syncthreads();
+  return sh.found_index;
+}
+
+template <typename T>
+__global__ __launch_bounds__(kThreads) void sample_kernel(SampleArgs a) {
+  __shared__ Shared sh;
+  const int b = blockIdx.x;
+  const int V = a.V;
+  const bool gen = a.pos != nullptr;
+  const int p_cur = gen ? a.pos[b] : (a.hist_len ? a.hist_len[b] - 1 : -1);
+  Row<T> row;
+  row.lg = static_cast<const T*>(a.logits) + b * a.logits_stride;
+  row.V = V;
+  row.pen = a.rep_penalty;
+  row.temperature = a.temperature;
+  row.use_pen = a.rep_penalty != 1.0f && a.tokens != nullptr;
+  row.bitmap = sh.bitmap;
+
+  if (row.use_pen) {
+    for (int i = threadIdx.x; i < kBitmapWords; i += kThreads) sh.bitmap[i] = 0u;
+    __syncthreads();
+    const int64_t* hist = a.tokens + b * a.tok_stride;
+    for (int i = threadIdx.x; i <= p_cur; i += kThreads) {
+      const int64_t t = hist[i];
+      if (t >= 0 && t < V) atomicOr(&sh.bitmap[t >> 5], 1u << (t & 31));
+    }
+    __syncthreads();
+  }
+
+  int chosen = 0;
+  if (a.temperature <= 0.f) {
+    // argmax, first index among equal maxima
+    float best = -INFINITY;
+    int bi = 0x7fffffff;
+    for (int i = threadIdx.x; i < V; i += kThreads) {
+      const float x = row.base(i);
+      if (x > best || (x == best && i < bi)) {
+        best = x;
+        bi = i;
+      }
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+      const float ob = __shfl_xor(best, o, 64);
+      const int oi = __shfl_xor(bi, o, 64);
+      if (ob > best || (ob == best && oi < bi)) {
+        best = ob;
+        bi = oi;
+      }
+    }
+    __syncthreads();
+    if ((threadIdx.x & 63) == 0) {
+      sh.redf[threadIdx.x >> 6] = best;
+      sh.redi[threadIdx.x >> 6] = bi;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+      float bb = sh.redf[0];
+      int ii = sh.redi[0];
+      for (int w = 1; w < kWaves; ++w) {
+        if (sh.redf[w] > bb || (sh.redf[w] == bb && sh.redi[w] < ii)) {
+          bb = sh.redf[w];
+          ii = sh.redi[w];
+        }
+      }
+      sh.found_index = ii;
+    }
+    __syncthreads();
+    chosen = sh.found_index;
+  } else {
+    const long long ui = gen ? static_cast<long long>(p_cur + 1 - a.plen[b]) * a.B + b : b;
+    const double u = a.uniforms[ui];
+    // top-k threshold on the temperature-scaled logits
+    bool use_k = a.top_k > 0;
+    float thresh = -INFINITY;
+    if (use_k) {
+      const int k = a.top_k < V ? a.top_k : V;
+      const uint32_t tk = select_kth_key(V, k, [&](int i) { return fkey(row.scaled(i)); }, sh);
+      const uint32_t bits = (tk & 0x80000000u) ? (tk & 0x7fffffffu) : ~tk;
+      thresh = __uint_as_float(bits);
+    }
+    auto xm = [&](int i) {
+      const float x = row.scaled(i);
+      return (use_k && x < thresh) ? -1e9f : x;
+    };
+    float mx = -INFINITY;
+    for (int i = threadIdx.x; i < V; i += kThreads) mx = fmaxf(mx, xm(i));
+    mx = block_max_f(mx, sh);
+    float se = 0.f;
+    for (int i = threadIdx.x; i < V; i += kThreads) se += expf(xm(i) - mx);
+    se = block_sum_f(se, sh);
+    auto prob = [&](int i) { return expf(xm(i) - mx) / se; };
+    auto keyp = [&](int i) { return fkey(prob(i)); };
+
+    if (a.top_p > 0.f && a.top_p < 1.f) {
+      // Cut: first descending position whose running mass exceeds top_p.
+      uint32_t tau1;
+      int j1;
+      select_by_mass(V, static_cast<double>(a.top_p), keyp, prob, [](int) { return true; }, &tau1,
+                     &j1, sh);
+      // Index of that element; kept = key > τ1, or key == τ1 and index < cut index.
+      const int cut = find_nth(V, j1, [&](int i) { return keyp(i) == tau1; }, sh);
+      // Empty prefix (the crossing element is the top one) keeps that element alone.
+      int above = 0;
+      for (int i = threadIdx.x; i < V; i += kThreads) above += keyp(i) > tau1 ? 1 : 0;
+      {
+        int tot = 0;
+        block_excl_scan_i(above, &tot, sh);
+        above = tot;
+      }
+      const bool single = (above == 0 && j1 == 1);
+      auto kept = [&](int i) {
+        const uint32_t k = keyp(i);
+        if (single) return i == cut;
+        return k > tau1 || (k == tau1 && i < cut);
+      };
+      float ks = 0.f;
+      for (int i = threadIdx.x; i < V; i += kThreads) ks += kept(i) ? prob(i) : 0.f;
+      ks = block_sum_f(ks, sh);
+      auto q = [&](int i) { return prob(i) / ks; };
+      double tq = 0.0;
+      for (int i = threadIdx.x; i < V; i += kThreads) tq += kept(i) ? static_cast<double>(q(i)) : 0.0;
+      double total = 0.0;
+      block_excl_scan_d(tq, &total, sh);
+      uint32_t tau2;
+      int j2;
+      select_by_mass(V, u * total, [&](int i) { return fkey(q(i)); }, q, kept, &tau2, &j2, sh);
+      chosen = find_nth(V, j2, [&](int i) { return kept(i) && fkey(q(i)) == tau2; }, sh);
+    } else {
+      // Index-order float64 CDF; first i with cdf[i] / cdf[-1] > u.
+      const int seg = (V + kThreads - 1) / kThreads;
+      const int lo = threadIdx.x * seg, hi = min(V, lo + seg);
+      double part = 0.0;
+      for (int i = lo; i < hi; ++i) part += static_cast<double>(prob(i));
+      double total = 0.0;
+      double run = block_excl_scan_d(part, &total, sh);
+      if (threadIdx.x == 0) sh.found_index = 0x7fffffff;
+      __syncthreads();
+      for (int i = lo; i < hi; ++i) {
+        run += static_cast<double>(prob(i));
+        if (run / total > u) {
+          atomicMin(&sh.found_index, i);
+          break;
+        }
+      }
+      __syncthreads();
+      chosen = sh.found_index == 0x7fffffff ? V - 1 : sh.found_index;
+    }
+  }
+
+  if (threadIdx.x == 0) {
+    if (gen) {
+      a.tokens[b * a.tok_stride + p_cur + 1] = chosen;
+      a.pos[b] = p_cur + 1;
+    }
+    if (a.out_ids) a.out_ids[b] = chosen;
+  }
+}
+
+}  // namespace
+
+int launch_sample(int dt, const SampleArgs& a, hipStream_t st) {
+  if (a.B == 0) return 0;
+  NML_REQUIRE(a.temperature <= 0.f || a.uniforms != nullptr, "sample: uniforms required when T > 0");
+  NML_REQUIRE(a.pos == nullptr || (a.tokens != nullptr && a.plen != nullptr),
+              "sample: generation mode needs the token history and prompt lengths");
+  NML_REQUIRE(a.rep_penalty == 1.0f || a.V <= kBitmapWords * 32,
+              "sample: repetition penalty supports vocab ≤ %d", kBitmapWords * 32);
+  if (dt == F16)
+    sample_kernel<half_t><<<a.B, kThreads, 0, st>>>(a);
+  else
+    sample_kernel<float><<<a.B, kThreads, 0, st>>>(a);
+  NML_LAUNCHED();
+  return 0;
+}
+
+}  // namespace nml

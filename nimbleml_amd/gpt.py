@@ -1,0 +1,291 @@
+"""GPT on the MI355X: the reference's model API over a device-resident driver.
+
+``GPT`` keeps NimbleML's constructor, module tree and parameter names
+(NimbleML/models/gpt.py:11-71) so checkpoints and user code carry over; its
+forward, ``compute_loss``, ``forward_with_cache`` and ``generate`` run on the GPU
+through the C-ABI (include/nimbleml_hip.h). Parameters live on the host as the
+reference's Tensors and are uploaded once — transposed to (out, in) and with
+Q/K/V stacked — into one device allocation, re-uploaded after ``load``.
+"""
+from __future__ import annotations
+
+import ctypes as C
+
+import numpy as np
+
+from nimbleml_amd import _native as N
+from nimbleml_amd import np_backend
+from nimbleml_amd.layers import (Embedding, FusedGPTTrunk, FusedTransformerBlock, Module,
+                                 RMSNorm, Sequential)
+from nimbleml_amd.tensor import Tensor
+
+
+def _ids_array(input_ids) -> np.ndarray:
+    if isinstance(input_ids, Tensor):
+        return np.asarray(input_ids.data, dtype=np.int64).reshape(input_ids.shape)
+    return np.asarray(input_ids, dtype=np.int64)
+
+
+class KVCache:
+    """Per-layer K/V cache on the device (the ``cache`` of ``forward_with_cache``)."""
+
+    def __init__(self, model: "GPT", batch: int):
+        self.model = model
+        self.batch = int(batch)
+        h = C.c_void_p()
+        self._model_handle = model._device_model()
+        N.check(N.lib.nml_cache_create(self._model_handle, self.batch, C.byref(h)))
+        self._h = h
+        self._owner = model._dev  # keeps the device model alive while the cache exists
+
+    @property
+    def length(self) -> int:
+        n = C.c_size_t()
+        N.check(N.lib.nml_cache_length(self._h, C.byref(n)))
+        return int(n.value)
+
+    def __del__(self):
+        try:
+            if self._h:
+                N.lib.nml_cache_destroy(self._h)
+                self._h = None
+        except Exception:
+            pass
+
+
+class GPT(Module):
+    """Minimal GPT-style autoregressive language model (models/gpt.py:11-211)."""
+
+    def __init__(self, vocab_size, d_model, num_heads, num_layers, max_seq_len, ff_mult=4, *,
+                 fused_blocks: bool = True, fused_trunk: bool = False,
+                 gradient_checkpointing: bool = False, use_rope: bool = False):
+        if d_model % num_heads != 0:
+            raise ValueError(f"d_model ({d_model}) must be divisible by num_heads ({num_heads}).")
+        if fused_trunk and not fused_blocks:
+            raise ValueError("fused_trunk requires fused_blocks=True.")
+        if not fused_blocks:
+            raise ValueError("nimbleml_amd implements the fused_blocks=True path of GPT.")
+        if use_rope:
+            raise NotImplementedError("use_rope is not part of this HIP path yet.")
+        self.vocab_size = vocab_size
+        self.d_model = d_model
+        self.num_heads = num_heads
+        self.num_layers = num_layers
+        self.max_seq_len = max_seq_len
+        self.ff_mult = ff_mult
+        self.fused_blocks = fused_blocks
+        self.fused_trunk = fused_trunk
+        self.gradient_checkpointing = bool(gradient_checkpointing)
+        self.use_rope = False
+        self.token_emb = Embedding(vocab_size, d_model)
+        self.pos_emb = Embedding(max_seq_len, d_model)
+        block_modules = [FusedTransformerBlock(d_model, num_heads, ff_mult,
+                                               gradient_checkpointing=gradient_checkpointing)
+                         for _ in range(num_layers)]
+        self.ln = RMSNorm(d_model)
+        self.blocks = (FusedGPTTrunk(block_modules, self.ln) if fused_trunk
+                       else Sequential(*block_modules))
+        self._dtype = np.dtype(np_backend.dtype)
+        self._dev = None
+
+    # ------------------------------------------------------------------ params
+    @property
+    def _block_list(self):
+        return self.blocks.blocks if self.fused_trunk else self.blocks.layers
+
+    def parameters(self):
+        params = []
+        for layer in (self.token_emb, self.blocks):
+            params.extend(layer.parameters())
+        params.extend(self.pos_emb.parameters())
+        if not self.fused_trunk:
+            params.extend(self.ln.parameters())
+        return params
+
+    def _invalidate_device(self):
+        self._dev = None  # re-upload on next use (the old handle is freed by __del__ below)
+
+    def _device_arrays(self):
+        """(kind, layer, host array in device layout) for every device parameter."""
+        dt = self._dtype
+
+        def a(t, shape=None):
+            return np.ascontiguousarray(np.asarray(t.data, dtype=dt).reshape(shape or t.shape))
+
+        out = [(N.P_TOKEN_EMB, 0, a(self.token_emb.weights)),
+               (N.P_POS_EMB, 0, a(self.pos_emb.weights)),
+               (N.P_LN_F, 0, a(self.ln.gamma))]
+        for i, blk in enumerate(self._block_list):
+            m = blk.mha
+            wqkv = np.concatenate([a(m.W_q.weights), a(m.W_k.weights), a(m.W_v.weights)], axis=1)
+            bqkv = np.concatenate([a(m.W_q.biases), a(m.W_k.biases), a(m.W_v.biases)])
+            out += [(N.P_LN1, i, a(blk.ln1.gamma)),
+                    (N.P_WQKV, i, np.ascontiguousarray(wqkv.T)),
+                    (N.P_BQKV, i, bqkv),
+                    (N.P_WO, i, np.ascontiguousarray(a(m.W_o.weights).T)),
+                    (N.P_BO, i, a(m.W_o.biases)),
+                    (N.P_LN2, i, a(blk.ln2.gamma)),
+                    (N.P_W1, i, np.ascontiguousarray(a(blk.ffn.dense1.weights).T)),
+                    (N.P_B1, i, a(blk.ffn.dense1.biases)),
+                    (N.P_W2, i, np.ascontiguousarray(a(blk.ffn.dense2.weights).T)),
+                    (N.P_B2, i, a(blk.ffn.dense2.biases))]
+        return out
+
+    def _device_model(self):
+        if self._dev is not None:
+            return self._dev.handle
+        N.ensure_init()
+        for blk in self._block_list:
+            for dense in (blk.mha.W_q, blk.mha.W_k, blk.mha.W_v, blk.mha.W_o,
+                          blk.ffn.dense1, blk.ffn.dense2):
+                if dense.biases is None:
+                    raise ValueError("the HIP path expects Dense layers with biases")
+        self._dev = _DeviceModel(self)
+        return self._dev.handle
+
+    def to_device(self):
+        """Upload (again) the current host parameters."""
+        self._dev = None
+        self._device_model()
+        return self
+
+    # ----------------------------------------------------------------- inputs
+    def _check_ids(self, ids: np.ndarray):
+        if ids.ndim != 2:
+            raise ValueError(f"input_ids must be 2D (batch, seq), got shape {ids.shape}.")
+        if ids.shape[1] > self.max_seq_len:
+            raise ValueError(f"Sequence length {ids.shape[1]} exceeds maximum sequence length "
+                             f"{self.max_seq_len}")
+        if ids.size and (int(ids.min()) < 0 or int(ids.max()) >= self.vocab_size):
+            raise ValueError(f"Token ID out of range [0, {self.vocab_size})")
+
+    def _logits_array(self, shape):
+        return N.DeviceArray(shape, self._dtype)
+
+    # ---------------------------------------------------------------- forward
+    def forward(self, input_ids):
+        """All-position logits (batch, seq, vocab) on the device (models/gpt.py:92-121)."""
+        ids = _ids_array(input_ids)
+        self._check_ids(ids)
+        h = self._device_model()
+        b, s = ids.shape
+        out = self._logits_array((b, s, self.vocab_size))
+        dids = N.DeviceArray.from_host(ids)
+        N.check(N.lib.nml_model_forward(h, dids.ptr, b, s, out.ptr, 0))
+        return Tensor(out, (b, s, self.vocab_size))
+
+    def forward_last(self, input_ids):
+        """Logits of the last position only, (batch, vocab)."""
+        ids = _ids_array(input_ids)
+        self._check_ids(ids)
+        h = self._device_model()
+        b, s = ids.shape
+        out = self._logits_array((b, self.vocab_size))
+        dids = N.DeviceArray.from_host(ids)
+        N.check(N.lib.nml_model_forward(h, dids.ptr, b, s, out.ptr, 1))
+        return Tensor(out, (b, self.vocab_size))
+
+    def forward_with_cache(self, input_ids, cache=None):
+        """Append ``input_ids`` (batch, s) to the KV cache and return their logits
+        (batch, s, vocab) — the hook models/generate.py:93-100 looks for."""
+        ids = _ids_array(input_ids)
+        if ids.ndim != 2:
+            raise ValueError(f"input_ids must be 2D (batch, seq), got shape {ids.shape}.")
+        if ids.size and (int(ids.min()) < 0 or int(ids.max()) >= self.vocab_size):
+            raise ValueError(f"Token ID out of range [0, {self.vocab_size})")
+        h = self._device_model()
+        b, s = ids.shape
+        if cache is None:
+            cache = KVCache(self, b)
+        if cache.model is not self or cache.batch != b:
+            raise ValueError("cache was created for another model or batch size")
+        if cache._model_handle is not h:
+            raise ValueError("parameters were reloaded since this cache was created; start a "
+                             "new cache")
+        if cache.length + s > self.max_seq_len:
+            raise ValueError(f"Sequence length {cache.length + s} exceeds maximum sequence "
+                             f"length {self.max_seq_len}")
+        out = self._logits_array((b, s, self.vocab_size))
+        dids = N.DeviceArray.from_host(ids)
+        N.check(N.lib.nml_model_forward_cached(h, cache._h, dids.ptr, b, s, out.ptr, 0))
+        return Tensor(out, (b, s, self.vocab_size)), cache
+
+    def compute_loss(self, input_ids, labels, ignore_index=None):
+        """Mean tied-head cross-entropy (models/gpt.py:123-137); logits are formed in
+        row chunks on the device and never all at once."""
+        ids = _ids_array(input_ids)
+        self._check_ids(ids)
+        b, s = ids.shape
+        lab = np_backend.as_label_indices(labels, batch_size=b * s)
+        h = self._device_model()
+        dids = N.DeviceArray.from_host(ids)
+        dlab = N.DeviceArray.from_host(lab)
+        loss = C.c_double()
+        has_ign = ignore_index is not None
+        N.check(N.lib.nml_model_loss(h, dids.ptr, dlab.ptr, b, s,
+                                     int(ignore_index) if has_ign else 0, int(has_ign),
+                                     C.byref(loss)))
+        # The reference wraps the loss in a compute-dtype Tensor (losses/cross_entropy.py:158-164).
+        out = Tensor([0.0], ())
+        out.data = np.asarray([loss.value], dtype=self._dtype)
+        return out
+
+    @classmethod
+    def from_arrays(cls, arrays, vocab_size, d_model, num_heads, num_layers, max_seq_len,
+                    ff_mult=4, dtype=None, **kwargs):
+        """Build a model directly from ``{name: array}`` (reference checkpoint names)
+        without drawing random initial weights first."""
+        from nimbleml_amd import layers
+        from nimbleml_amd.saveload import load_arrays
+
+        old = np_backend.dtype
+        if dtype is not None:
+            np_backend.set_dtype(np.dtype(dtype).name)
+        try:
+            with layers.skip_init():
+                m = cls(vocab_size, d_model, num_heads, num_layers, max_seq_len, ff_mult, **kwargs)
+        finally:
+            np_backend.set_dtype(np.dtype(old).name)
+        return load_arrays(m, arrays)
+
+    def generate(self, input_ids, **kwargs):
+        """Autoregressive generation (see ``nimbleml_amd.generate.generate``)."""
+        from nimbleml_amd.generate import generate as _generate
+
+        return _generate(self, input_ids, **kwargs)
+
+    def last_decode_ms(self) -> float:
+        """Average device time of one decode step in the last generate() call."""
+        ms = C.c_float()
+        N.check(N.lib.nml_model_last_decode_ms(self._device_model(), C.byref(ms)))
+        return float(ms.value)
+
+    def __del__(self):
+        self._dev = None
+
+
+class _DeviceModel:
+    """Owns the C model handle."""
+
+    def __init__(self, model: GPT):
+        h = C.c_void_p()
+        N.check(N.lib.nml_model_create(model.vocab_size, model.d_model, model.num_heads,
+                                       model.num_layers, model.max_seq_len,
+                                       model.ff_mult * model.d_model,
+                                       N.np_dtype_code(model._dtype), C.byref(h)))
+        self.handle = h
+        try:
+            for kind, layer, arr in model._device_arrays():
+                N.check(N.lib.nml_model_set_param(h, kind, layer, arr.ctypes.data, arr.nbytes))
+        except Exception:
+            N.lib.nml_model_destroy(h)
+            self.handle = None
+            raise
+
+    def __del__(self):
+        try:
+            if self.handle:
+                N.lib.nml_model_destroy(self.handle)
+                self.handle = None
+        except Exception:
+            pass

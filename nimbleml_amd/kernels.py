@@ -1,0 +1,158 @@
+"""Array-level device ops under the reference kernel names (NimbleML/kernels/).
+
+Each takes host arrays or ``DeviceArray``s in the compute dtype and returns
+``DeviceArray`` results computed by the HIP kernels:
+  fused_rmsnorm_forward       kernels/fused_rmsnorm.py:130-162
+  fused_gelu_forward          kernels/fused_gelu.py:57-83
+  fused_sdpa_forward          kernels/fused_sdpa.py:256-289 (causal mask only)
+  embedding_lookup            kernels/embedding_scatter.py:25-36
+  fused_tied_crossentropy_forward  kernels/fused_tied_crossentropy.py:8-24 (loss only)
+  linear                      the `x @ W + b` of neural_network/_fused_arrays.py:25-30
+  sample_tokens               models/generate.py:23-59 on a (batch, vocab) logits block
+"""
+from __future__ import annotations
+
+import ctypes as C
+
+import numpy as np
+
+from nimbleml_amd import _native as N
+from nimbleml_amd import np_backend
+
+EPI_NONE, EPI_BIAS, EPI_BIAS_GELU, EPI_BIAS_RESID = 0, 1, 2, 3
+
+
+def _dev(x, dtype=None):
+    if isinstance(x, N.DeviceArray):
+        if dtype is not None and x.dtype != np.dtype(dtype):
+            raise TypeError(f"expected {np.dtype(dtype)}, got {x.dtype}")
+        return x
+    return N.DeviceArray.from_host(np.asarray(x, dtype=dtype if dtype is not None else None))
+
+
+def _float_dtype(x):
+    dt = np.dtype(x.dtype) if hasattr(x, "dtype") else np.dtype(np_backend.dtype)
+    N.np_dtype_code(dt)
+    return dt
+
+
+def fused_rmsnorm_forward(x, gamma, epsilon=1e-5):
+    """Returns (out, x, ms, rms) with ms/rms shaped (rows, 1) like the reference."""
+    dt = _float_dtype(x)
+    xd, gd = _dev(x, dt), _dev(gamma, dt)
+    d = xd.shape[-1]
+    rows = xd.size // d
+    out = N.DeviceArray(xd.shape, dt)
+    ms = N.DeviceArray((rows, 1), np.float32)
+    rms = N.DeviceArray((rows, 1), np.float32)
+    N.check(N.lib.nml_rmsnorm_forward_device(xd.ptr, gd.ptr, out.ptr, ms.ptr, rms.ptr, rows, d,
+                                             float(epsilon), N.np_dtype_code(dt)))
+    return out, xd, ms, rms
+
+
+def fused_gelu_forward(x):
+    """Returns (out, tanh_u) — tanh_u in float32 as in the reference."""
+    dt = _float_dtype(x)
+    xd = _dev(x, dt)
+    out = N.DeviceArray(xd.shape, dt)
+    tu = N.DeviceArray(xd.shape, np.float32)
+    N.check(N.lib.nml_gelu_forward_device(xd.ptr, out.ptr, tu.ptr, xd.size, N.np_dtype_code(dt)))
+    return out, tu
+
+
+def fused_sdpa_forward(q, k, v, scale, mask_arr=None, *, batch=None, num_heads=None):
+    """Causal attention over (bh, seq, dk); ``scale`` is the sqrt(dk) divisor. The
+    reference's GPT always passes the causal mask; other masks are not supported."""
+    if mask_arr is None:
+        raise NotImplementedError("only causal attention (the GPT path) runs on the HIP device")
+    dt = _float_dtype(q)
+    qd, kd, vd = _dev(q, dt), _dev(k, dt), _dev(v, dt)
+    bh, seq, dk = qd.shape
+    out = N.DeviceArray((bh, seq, dk), dt)
+    N.check(N.lib.nml_flash_sdpa_forward_device(qd.ptr, kd.ptr, vd.ptr, out.ptr, bh, seq, dk,
+                                                float(scale), N.np_dtype_code(dt)))
+    return out, None
+
+
+def embedding_lookup(weights, ids, pos_weights=None):
+    """``weights[ids]`` (plus ``pos_weights[s]`` when given) on the device."""
+    dt = _float_dtype(weights)
+    wd = _dev(weights, dt)
+    ids_np = np.asarray(ids, dtype=np.int64)
+    shape = ids_np.shape
+    ids2 = ids_np.reshape(1, -1) if ids_np.ndim != 2 else ids_np
+    vocab, dim = wd.shape
+    if ids2.size and (int(ids2.min()) < 0 or int(ids2.max()) >= vocab):
+        raise ValueError(f"Token ID out of range [0, {vocab})")
+    b, s = ids2.shape
+    if pos_weights is None:
+        pd = N.DeviceArray((max(s, 1), dim), dt)
+        N.check(N.lib.nml_memset(pd.ptr, 0, pd.nbytes))
+    else:
+        pd = _dev(pos_weights, dt)
+    idd = N.DeviceArray.from_host(ids2)
+    out = N.DeviceArray((b, s, dim), dt)
+    N.check(N.lib.nml_embedding_gather_device(wd.ptr, pd.ptr, idd.ptr, out.ptr, b, s, dim, vocab,
+                                              pd.shape[0], None, None, N.np_dtype_code(dt)))
+    return out.reshape(*shape, dim)
+
+
+def linear(x, weights, bias=None, *, epilogue=None, resid=None):
+    """``epi(x @ weights + bias)`` with ``weights`` in the reference layout (in, out)."""
+    dt = _float_dtype(x)
+    xd = _dev(x, dt)
+    w = np.ascontiguousarray(np.asarray(weights, dtype=dt).T)
+    wd = N.DeviceArray.from_host(w)
+    n_out, k = w.shape
+    rows = xd.size // k
+    if epilogue is None:
+        epilogue = EPI_BIAS if bias is not None else EPI_NONE
+    bd = _dev(bias, dt) if bias is not None else None
+    rd = _dev(resid, dt) if resid is not None else None
+    out = N.DeviceArray((rows, n_out), dt)
+    N.check(N.lib.nml_linear_device(xd.ptr, k, wd.ptr, N.ptr(bd), N.ptr(rd), out.ptr, rows, k,
+                                    n_out, int(epilogue), N.np_dtype_code(dt)))
+    return out
+
+
+def fused_tied_crossentropy_forward(hidden, weights, label_indices, ignore_index=None):
+    """Mean CE of ``hidden @ weights.T`` against labels (float)."""
+    dt = _float_dtype(hidden)
+    hd, wd = _dev(hidden, dt), _dev(weights, dt)
+    rows, dim = hd.shape
+    labels = np_backend.as_label_indices(label_indices, batch_size=rows)
+    ld = N.DeviceArray.from_host(labels)
+    loss = C.c_double()
+    has = ignore_index is not None
+    N.check(N.lib.nml_tied_ce_forward_device(hd.ptr, wd.ptr, ld.ptr, rows, dim, wd.shape[0],
+                                             int(ignore_index) if has else 0, int(has),
+                                             C.byref(loss), N.np_dtype_code(dt)))
+    return float(loss.value)
+
+
+def sample_tokens(logits, *, temperature, top_k=0, top_p=1.0, uniforms=None, history=None,
+                  repetition_penalty=1.0):
+    """One token per row of (batch, vocab) logits with ``_sample_logits`` semantics;
+    ``uniforms[b]`` replaces row b's RandomState draw; ``history`` is a list of the
+    token ids already in each row (repetition penalty)."""
+    dt = _float_dtype(logits)
+    ld = _dev(logits, dt)
+    batch, vocab = ld.shape
+    ud = None
+    if temperature > 0:
+        ud = N.DeviceArray.from_host(np.asarray(uniforms, dtype=np.float64).reshape(batch))
+    hd = hl = None
+    stride = 0
+    if history is not None:
+        stride = max(1, max(len(h) for h in history))
+        hist = np.zeros((batch, stride), dtype=np.int64)
+        for b, h in enumerate(history):
+            hist[b, :len(h)] = h
+        hd = N.DeviceArray.from_host(hist)
+        hl = N.DeviceArray.from_host(np.asarray([len(h) for h in history], dtype=np.int32))
+    out = N.DeviceArray((batch,), np.int64)
+    N.check(N.lib.nml_sample_device(ld.ptr, batch, vocab, float(temperature), int(top_k or 0),
+                                    float(top_p if top_p is not None else 1.0),
+                                    float(repetition_penalty), N.ptr(ud), N.ptr(hd), stride,
+                                    N.ptr(hl), out.ptr, N.np_dtype_code(dt)))
+    return out.numpy()

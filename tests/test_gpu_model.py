@@ -1,0 +1,299 @@
+"""End-to-end GPU parity of the GPT path against the reference's own outputs.
+
+Fixtures (tests/golden/*.npz) were written by the real NimbleML CPU path. Tolerances
+fp32 logits ≤ 1e-3, fp16 logits ≤ 3e-2, loss relative
+≤ 1e-4 (fp16 fixtures store the reference's fp16-rounded loss: within that rounding),
+token ids identical wherever the reference's decision margin exceeds the logit
+tolerance (greedy: top-2 gap; sampling: distance of u to a CDF boundary).
+"""
+import numpy as np
+import pytest
+
+from conftest import fixture_config, fixture_weights, golden
+from oracle import gpt_ref as R
+from oracle.weights import GPTConfig, make_weights, random_ids
+
+pytestmark = pytest.mark.gpu
+
+TINY = ["tiny_fp32", "tiny_fp16", "tiny_rich_fp32", "tiny_rich_fp16"]
+
+
+def tol_for(dtype):
+    return 3e-2 if np.dtype(dtype) == np.float16 else 1e-3
+
+
+def build(cfg, w, dtype):
+    import nimbleml_amd as nm
+
+    old = nm.np_backend.dtype
+    nm.set_dtype(np.dtype(dtype).name)
+    try:
+        m = nm.GPT(cfg.vocab_size, cfg.d_model, cfg.num_heads, cfg.num_layers, cfg.max_seq_len,
+                   ff_mult=cfg.ff_mult)
+    finally:
+        nm.set_dtype(np.dtype(old).name)
+    nm.load_arrays(m, w)
+    return m
+
+
+def greedy_margin(logits):
+    top2 = np.sort(np.asarray(logits, np.float64), axis=-1)[..., -2:]
+    return top2[..., 1] - top2[..., 0]
+
+
+def assert_tokens_agree(ours, ref, s0, margins, tol):
+    """Per row, tokens equal up to (and including) the first step whose reference
+    decision margin is ≤ tol (rows are independent). Returns the number of tokens
+    compared."""
+    ours, ref = np.asarray(ours), np.asarray(ref)
+    n = ref.shape[1] - s0
+    compared = 0
+    for b in range(ref.shape[0]):
+        for t in range(n):
+            assert ours[b, s0 + t] == ref[b, s0 + t], f"row {b} step {t}"
+            compared += 1
+            if np.atleast_1d(margins[t])[b] <= tol:
+                break
+    return compared
+
+
+def oracle_greedy_margins(w, cfg, tokens, s0):
+    """Top-2 margins of the reference decision at every step (fp32 oracle, KV form)."""
+    w32 = {k: v.astype(np.float32) for k, v in w.items()}
+    kv = R.KVOracle(w32, cfg.num_heads, cfg.num_layers)
+    lg = kv.step(tokens[:, :s0])[:, -1]
+    out = [greedy_margin(lg)]
+    for t in range(s0, tokens.shape[1] - 1):
+        lg = kv.step(tokens[:, t:t + 1])[:, -1]
+        out.append(greedy_margin(lg))
+    return out
+
+
+@pytest.mark.parametrize("name", TINY)
+def test_tiny_forward_logits(gpu, name):
+    f = golden(name)
+    cfg, w = fixture_weights(f)
+    dt = w["token_emb.weights"].dtype
+    m = build(cfg, w, dt)
+    lg = m.forward(f["greedy"][:, :-1]).numpy().astype(np.float64)
+    assert np.abs(lg - f["greedy_logits"]).max() <= tol_for(dt)
+
+
+@pytest.mark.parametrize("name", TINY)
+def test_tiny_greedy_generate(gpu, name):
+    import nimbleml_amd as nm
+
+    f = golden(name)
+    cfg, w = fixture_weights(f)
+    dt = w["token_emb.weights"].dtype
+    m = build(cfg, w, dt)
+    s0 = f["prompt"].shape[1]
+    n = f["greedy"].shape[1] - s0
+    margins = oracle_greedy_margins(w, cfg, f["greedy"], s0)
+    for use_graph in (True, False):
+        out = nm.generate(m, f["prompt"], max_new_tokens=n, temperature=0.0, use_graph=use_graph)
+        assert out.shape == f["greedy"].shape
+        assert_tokens_agree(out, f["greedy"], s0, margins, tol_for(dt))
+    out = nm.generate(m, f["prompt"], max_new_tokens=n, temperature=0.0, repetition_penalty=1.5)
+    assert np.array_equal(out[:, :s0 + 4], f["greedy_reppen"][:, :s0 + 4])
+
+
+@pytest.mark.parametrize("name", TINY)
+def test_tiny_loss(gpu, name):
+    import ctypes
+
+    from nimbleml_amd import _native as N
+
+    f = golden(name)
+    cfg, w = fixture_weights(f)
+    dt = w["token_emb.weights"].dtype
+    m = build(cfg, w, dt)
+    ref = float(f["loss"])
+    got = m.compute_loss(f["loss_ids"], f["loss_labels"]).item()
+    if dt == np.float16:
+        # The reference returns its loss as an fp16 Tensor; ours is rounded the same way.
+        assert abs(got - ref) <= 2 ** -8 * abs(ref)
+        unrounded = R.compute_loss(w, f["loss_ids"], f["loss_labels"], cfg.num_heads, cfg.num_layers)
+        raw = ctypes.c_double()
+        ids = N.DeviceArray.from_host(f["loss_ids"])
+        lab = N.DeviceArray.from_host(f["loss_labels"].reshape(-1))
+        N.check(N.lib.nml_model_loss(m._device_model(), ids.ptr, lab.ptr, 2, 32, 0, 0,
+                                     ctypes.byref(raw)))
+        assert abs(raw.value - unrounded) <= 1e-3 * abs(unrounded)
+    else:
+        assert abs(got - ref) <= 1e-4 * abs(ref)
+    gi = m.compute_loss(f["loss_ids"], f["loss_ignore_labels"], ignore_index=-100).item()
+    assert abs(gi - float(f["loss_ignore"])) <= (2 ** -8 if dt == np.float16 else 1e-4) * abs(gi)
+    z = m.compute_loss(f["loss_ids"], np.full((2, 32), -100), ignore_index=-100).item()
+    assert z == float(f["loss_all_ignored"]) == 0.0
+
+
+@pytest.mark.parametrize("name", TINY)
+@pytest.mark.parametrize("mode", ["topk", "topp", "reppen"])
+def test_tiny_sampled_generate(gpu, name, mode):
+    """Seeded sampling reproduces the reference's tokens (same global-RNG draws)."""
+    import nimbleml_amd as nm
+
+    f = golden(name)
+    cfg, w = fixture_weights(f)
+    dt = w["token_emb.weights"].dtype
+    m = build(cfg, w, dt)
+    kw = {"topk": dict(temperature=0.8, top_k=50, top_p=1.0), "topp": dict(),
+          "reppen": dict(temperature=0.8, top_k=20, top_p=1.0, repetition_penalty=1.3)}[mode]
+    seed = {"topk": 123, "topp": 321, "reppen": 555}[mode]
+    ref = f[mode + "_tokens"]
+    s0 = f["prompt"].shape[1]
+    np.random.seed(seed)
+    out = nm.generate(m, f["prompt"], max_new_tokens=ref.shape[1] - s0, **kw)
+    # Compare until the first step where the oracle's u lies near a CDF boundary.
+    u = f[mode + "_u"]
+    w32 = {k: v.astype(np.float32) for k, v in w.items()}
+    kv = R.KVOracle(w32, cfg.num_heads, cfg.num_layers)
+    lg = kv.step(ref[:, :s0])[:, -1]
+    live = np.ones(ref.shape[0], dtype=bool)  # rows still compared
+    for t in range(ref.shape[1] - s0):
+        for b in np.nonzero(live)[0]:
+            assert out[b, s0 + t] == ref[b, s0 + t], f"row {b} step {t}"
+            if _u_near_boundary(lg[b], u[t, b], ref[b, :s0 + t], kw, tol_for(dt)):
+                live[b] = False
+        if not live.any():
+            break
+        lg = kv.step(ref[:, s0 + t:s0 + t + 1])[:, -1]
+
+
+def _u_near_boundary(logits, u, hist, kw, tol):
+    """True when perturbing the logits by tol could move u across a CDF boundary."""
+    x = np.asarray(logits, np.float32)
+    x = R.apply_repetition_penalty(x, list(hist), kw.get("repetition_penalty", 1.0))
+    t = kw.get("temperature", 0.8)
+    x = x / t
+    if kw.get("top_k", 0):
+        k = kw["top_k"]
+        th = np.partition(x, -k)[-k]
+        near_k = np.sort(np.abs(x - th))[1] < 2 * tol / t if k < x.size else False
+        if near_k:
+            return True
+        x = np.where(x < th, -1e9, x)
+    p = np.exp(x - x.max())
+    p /= p.sum()
+    if kw.get("top_p", 0.9) < 1.0:
+        # The token is picked by position in the descending order: near-equal logits
+        # around the picked position make its identity ambiguous.
+        order = np.argsort(-x, kind="stable")
+        xs = x[order]
+        cdf = np.cumsum(p[order].astype(np.float64))
+        i = int(np.searchsorted(cdf / cdf[-1], u, side="right"))
+        i = min(i, xs.size - 1)
+        gaps = [abs(xs[i] - xs[j]) for j in (i - 1, i + 1) if 0 <= j < xs.size]
+        if gaps and min(gaps) < 2 * tol / t:
+            return True
+        p = p[order]
+    cdf = np.cumsum(p.astype(np.float64))
+    # a logit change of tol/T moves each probability by about p·2·tol/T
+    return np.min(np.abs(cdf - u)) < 4 * tol / t * max(p.max(), 1e-3) + 1e-6
+
+
+def test_kv_cache_decode_equals_full_reforward(gpu):
+    f = golden("tiny_rich_fp32")
+    cfg, w = fixture_weights(f)
+    m = build(cfg, w, np.float32)
+    ids = f["greedy"]
+    full = m.forward(ids).numpy()
+    lg, cache = m.forward_with_cache(ids[:, :10])
+    assert np.abs(lg.numpy() - full[:, :10]).max() < 1e-5
+    for t in range(10, ids.shape[1]):
+        lg, cache = m.forward_with_cache(ids[:, t:t + 1], cache)
+        assert np.abs(lg.numpy()[:, 0] - full[:, t]).max() < 1e-5
+    assert cache.length == ids.shape[1]
+    with pytest.raises(ValueError, match="exceeds maximum sequence length"):
+        m.forward_with_cache(ids[:, :1], cache)
+
+
+def test_reference_generate_loop_drives_forward_with_cache(gpu):
+    """The reference's loop shape: forward_with_cache + last-row sampling on host."""
+    f = golden("tiny_fp32")
+    cfg, w = fixture_weights(f)
+    m = build(cfg, w, np.float32)
+    s0 = f["prompt"].shape[1]
+    gen = [list(r) for r in f["prompt"]]
+    n = f["greedy"].shape[1] - s0
+    logits, cache = m.forward_with_cache(f["prompt"])
+    for t in range(n):
+        last = logits.numpy()[:, -1]
+        for b in range(2):
+            gen[b].append(int(np.argmax(last[b])))
+        if t + 1 < n:
+            logits, cache = m.forward_with_cache(np.asarray([[g[-1]] for g in gen]), cache)
+    assert np.array_equal(np.asarray(gen), f["greedy"])
+
+
+@pytest.mark.parametrize("name", ["small_fp32", "small_rich_fp32"])
+def test_small_generate_and_logits(gpu, name):
+    import nimbleml_amd as nm
+
+    f = golden(name)
+    cfg, w = fixture_weights(f)
+    m = build(cfg, w, np.float32)
+    s0 = f["prompt"].shape[1]
+    n = f["greedy"].shape[1] - s0
+    out = nm.generate(m, f["prompt"], max_new_tokens=n, temperature=0.0)
+    margins = oracle_greedy_margins(w, cfg, f["greedy"], s0)
+    compared = assert_tokens_agree(out, f["greedy"], s0, margins, 1e-3)
+    assert compared >= f["greedy"].shape[0]
+    for t in f["logit_steps"]:
+        lg = m.forward_last(f["greedy"][:, :s0 + int(t)]).numpy()
+        assert np.abs(lg - f[f"logits_step{int(t)}"]).max() <= 1e-3
+    loss = m.compute_loss(f["loss_ids"], f["loss_labels"]).item()
+    assert abs(loss - float(f["loss"])) <= 1e-4 * abs(float(f["loss"]))
+
+
+def test_small_no_kv_cache_matches_kv_cache(gpu):
+    import nimbleml_amd as nm
+
+    f = golden("small_rich_fp32")
+    cfg, w = fixture_weights(f)
+    m = build(cfg, w, np.float32)
+    a = nm.generate(m, f["prompt"][:2], max_new_tokens=12, temperature=0.0)
+    b = nm.generate(m, f["prompt"][:2], max_new_tokens=12, temperature=0.0, use_kv_cache=False)
+    assert np.array_equal(a, b)
+
+
+def test_small_ragged_batch_rows_equal_single_runs(gpu):
+    """Ragged batch: each row reproduces the reference's batch-1 run of that row."""
+    from nimbleml_amd.generate import _generate_device
+
+    f = golden("small_ragged_fp32")
+    from oracle.weights import SMALL
+
+    w = make_weights(SMALL, seed=23, dtype=np.float32, rich=True)
+    m = build(SMALL, w, np.float32)
+    rows = [f[f"row{r}_prompt"][0] for r in range(3)]
+    plen = np.asarray([len(r) for r in rows], dtype=np.int32)
+    u = np.stack([f[f"row{r}_u"][:, 0] for r in range(3)], axis=1)
+    toks = _generate_device(m, rows, plen, 16, 0.8, 50, 1.0, 1.0, u, True)
+    for r in range(3):
+        ref = f[f"row{r}_tokens"][0]
+        assert np.array_equal(toks[r, :len(ref)], ref), r
+
+
+def test_c3slice_fp16_steps(gpu):
+    """d1024 / 16 heads / vocab 32000 at two layers, fp16: the reference's own logits."""
+    import nimbleml_amd as nm
+
+    f = golden("c3slice_fp16")
+    cfg, w = fixture_weights(f)
+    m = build(cfg, w, np.float16)
+    s0 = f["prompt"].shape[1]
+    n = f["greedy"].shape[1] - s0
+    out = nm.generate(m, f["prompt"], max_new_tokens=n, temperature=0.0)
+    margins = [greedy_margin(f[f"logits_step{t}"]) for t in range(n)]
+    assert_tokens_agree(out, f["greedy"], s0, margins, 3e-2)
+    lg, cache = m.forward_with_cache(f["greedy"][:, :s0])
+    for t in range(n):
+        ref = f[f"logits_step{t}"].astype(np.float64)
+        got = lg.numpy()[:, -1].astype(np.float64)
+        assert np.abs(got - ref).max() <= 3e-2, t
+        if t + 1 < n:
+            lg, cache = m.forward_with_cache(f["greedy"][:, s0 + t:s0 + t + 1], cache)
+    loss = m.compute_loss(f["loss_ids"], f["loss_labels"]).item()
+    assert abs(loss - float(f["loss"])) <= 2 ** -7 * abs(float(f["loss"]))

@@ -1,0 +1,197 @@
+"""GPU parity of each HIP kernel against the oracle / float64 closed forms.
+
+Tolerances: integer work (gather, argmax, sampling choices) bit-exact; fp32 ops
+≤ 1e-5 relative to float64 (GEMMs ≤ 1e-4); fp16 ops within one or two fp16 ulps of
+the oracle's fp16 op-by-op result.
+"""
+import numpy as np
+import pytest
+
+from conftest import golden
+from oracle import gpt_ref as R
+
+pytestmark = pytest.mark.gpu
+
+
+def _k():
+    from nimbleml_amd import kernels
+
+    return kernels
+
+
+def _ulps16(a, b):
+    a = np.asarray(a, np.float16).astype(np.float64)
+    b = np.asarray(b, np.float16).astype(np.float64)
+    scale = np.maximum(np.abs(b), 6.1e-5)
+    return np.abs(a - b) / (scale * 2.0 ** -10)
+
+
+@pytest.mark.parametrize("name", ["ops_fp32", "ops_fp16"])
+def test_rmsnorm_matches_reference_fixture(gpu, name):
+    f = golden(name)
+    out = np.asarray(_k().fused_rmsnorm_forward(f["rms_x"], f["rms_g"])[0])
+    if out.dtype == np.float16:
+        assert _ulps16(out, f["rms_out"]).max() <= 2
+    else:
+        assert np.abs(out - f["rms_out"]).max() < 1e-5
+
+
+@pytest.mark.parametrize("name", ["ops_fp32", "ops_fp16"])
+def test_gelu_matches_reference_fixture(gpu, name):
+    f = golden(name)
+    out, tu = _k().fused_gelu_forward(f["gelu_x"])
+    out = np.asarray(out)
+    if out.dtype == np.float16:
+        assert _ulps16(out, f["gelu_out"]).max() <= 1
+    else:
+        assert np.abs(out - f["gelu_out"]).max() < 2e-6
+    x = f["gelu_x"].astype(np.float64)
+    want_tu = np.tanh(np.sqrt(2 / np.pi) * (x + 0.044715 * x ** 3))
+    assert np.abs(np.asarray(tu) - want_tu).max() < (2e-3 if out.dtype == np.float16 else 1e-6)
+
+
+@pytest.mark.parametrize("name", ["ops_fp32", "ops_fp16"])
+def test_embedding_gather_bit_exact(gpu, name):
+    f = golden(name)
+    out = np.asarray(_k().embedding_lookup(f["emb_w"], f["emb_ids"]))
+    assert np.array_equal(out, f["emb_out"])
+
+
+def test_embedding_with_positions_bit_exact(gpu):
+    rng = np.random.default_rng(0)
+    for dt in (np.float32, np.float16):
+        E = rng.standard_normal((100, 48)).astype(dt)
+        P = rng.standard_normal((20, 48)).astype(dt)
+        ids = rng.integers(0, 100, (3, 17))
+        out = np.asarray(_k().embedding_lookup(E, ids, pos_weights=P))
+        assert np.array_equal(out, R.embed(E, P, ids))
+
+
+@pytest.mark.parametrize("dt", [np.float32, np.float16])
+@pytest.mark.parametrize("rows", [1, 3, 8, 9, 130, 300])
+@pytest.mark.parametrize("epi", [0, 1, 2, 3])
+def test_linear_all_paths(gpu, dt, rows, epi):
+    """GEMV (rows ≤ 8) and MFMA GEMM (rows > 8) with each epilogue, ragged tile edges."""
+    rng = np.random.default_rng(rows * 10 + epi)
+    k, n = 200, 136  # not multiples of the 128 tile
+    x = rng.standard_normal((rows, k)).astype(dt)
+    w = (rng.standard_normal((k, n)) * 0.1).astype(dt)
+    b = rng.standard_normal(n).astype(dt)
+    r = rng.standard_normal((rows, n)).astype(dt)
+    out = np.asarray(_k().linear(x, w, b if epi else None, epilogue=epi,
+                                 resid=r if epi == 3 else None)).astype(np.float64)
+    acc = x.astype(np.float64) @ w.astype(np.float64)
+    if dt == np.float16:
+        acc = acc.astype(np.float16)
+        lin = (acc + b).astype(np.float16) if epi else acc
+        if epi == 2:
+            lin = R.gelu(lin)
+        if epi == 3:
+            lin = (r + lin).astype(np.float16)
+        tol = 3e-3 * max(1.0, np.abs(lin.astype(np.float64)).max())
+        assert np.abs(out - lin.astype(np.float64)).max() <= tol
+    else:
+        lin = acc + b if epi else acc
+        if epi == 2:
+            lin = 0.5 * lin * (1 + np.tanh(np.sqrt(2 / np.pi) * (lin + 0.044715 * lin ** 3)))
+        if epi == 3:
+            lin = r + lin
+        assert np.abs(out - lin).max() <= 1e-4 * max(1.0, np.abs(lin).max())
+
+
+@pytest.mark.parametrize("shape", [(1, 4096, 1024), (2, 1024, 3072), (512, 1024, 1024),
+                                   (700, 256, 4096)])
+def test_linear_real_shapes_fp16(gpu, shape):
+    rows, k, n = shape
+    rng = np.random.default_rng(k)
+    x = rng.standard_normal((rows, k)).astype(np.float16)
+    w = (rng.standard_normal((k, n)) * 0.02).astype(np.float16)
+    out = np.asarray(_k().linear(x, w)).astype(np.float64)
+    want = (x.astype(np.float64) @ w.astype(np.float64)).astype(np.float16).astype(np.float64)
+    assert np.abs(out - want).max() <= 2e-3 * max(1.0, np.abs(want).max())
+
+
+@pytest.mark.parametrize("name", ["ops_fp32", "ops_fp16"])
+def test_sdpa_matches_reference_fixture(gpu, name):
+    f = golden(name)
+    dk = f["sdpa_q"].shape[2]
+    s = f["sdpa_q"].shape[1]
+    out = np.asarray(_k().fused_sdpa_forward(f["sdpa_q"], f["sdpa_k"], f["sdpa_v"], float(dk) ** 0.5,
+                                             R.causal_mask(s, f["sdpa_q"].dtype))[0])
+    tol = 4e-3 if out.dtype == np.float16 else 1e-5
+    assert np.abs(out.astype(np.float64) - f["sdpa_out"]).max() < tol
+
+
+@pytest.mark.parametrize("dk", [8, 16, 32, 64, 128])
+@pytest.mark.parametrize("dt", [np.float32, np.float16])
+def test_sdpa_head_dims(gpu, dk, dt):
+    rng = np.random.default_rng(dk)
+    bh, s = 3, 150
+    q, k, v = (rng.standard_normal((bh, s, dk)).astype(dt) for _ in range(3))
+    out = np.asarray(_k().fused_sdpa_forward(q, k, v, float(dk) ** 0.5, R.causal_mask(s, dt))[0])
+    want = R.sdpa(q.astype(np.float64), k.astype(np.float64), v.astype(np.float64),
+                  float(dk) ** 0.5, R.causal_mask(s, np.float64))
+    assert np.abs(out - want).max() < (6e-3 if dt == np.float16 else 1e-5)
+
+
+@pytest.mark.parametrize("name", ["ops_fp32", "ops_fp16"])
+def test_tied_ce_matches_reference_fixture(gpu, name):
+    f = golden(name)
+    loss = _k().fused_tied_crossentropy_forward(f["ce_h"], f["ce_e"], f["ce_y"])
+    ref = float(f["ce_loss"])
+    assert abs(loss - ref) <= (1e-3 if f["ce_h"].dtype == np.float16 else 1e-5) * abs(ref)
+
+
+def test_tied_ce_ignore_index_and_closed_form(gpu):
+    rng = np.random.default_rng(7)
+    h = rng.standard_normal((300, 64)).astype(np.float32)
+    e = (rng.standard_normal((1000, 64)) * 0.2).astype(np.float32)
+    y = rng.integers(0, 1000, 300)
+    y[::4] = -100
+    loss = _k().fused_tied_crossentropy_forward(h, e, y, ignore_index=-100)
+    keep = y != -100
+    lg = h[keep].astype(np.float64) @ e.T.astype(np.float64)
+    want = np.mean(np.log(np.exp(lg - lg.max(1, keepdims=True)).sum(1)) + lg.max(1)
+                   - lg[np.arange(keep.sum()), y[keep]])
+    assert abs(loss - want) < 1e-5 * abs(want)
+    assert _k().fused_tied_crossentropy_forward(h, e, np.full(300, -100), ignore_index=-100) == 0.0
+
+
+def _distinct_logits(rng, b, v, dt=np.float32):
+    x = rng.standard_normal((b, v)) * 2
+    return x.astype(dt)
+
+
+def test_greedy_argmax_first_index_on_ties(gpu):
+    rng = np.random.default_rng(1)
+    lg = _distinct_logits(rng, 4, 32000, np.float16)
+    lg[1, 100] = lg[1, 20000] = np.float16(50.0)  # tie: first index wins
+    got = _k().sample_tokens(lg, temperature=0.0)
+    assert np.array_equal(got, np.argmax(lg.astype(np.float32), axis=1))
+    assert got[1] == 100
+
+
+@pytest.mark.parametrize("top_k,top_p", [(0, 1.0), (50, 1.0), (1, 1.0), (0, 0.9), (40, 0.5),
+                                         (0, 0.3)])
+def test_sampling_matches_oracle(gpu, top_k, top_p):
+    rng = np.random.default_rng(top_k * 7 + int(top_p * 10))
+    for trial in range(3):
+        lg = _distinct_logits(rng, 6, 4096)
+        u = rng.random(6)
+        got = _k().sample_tokens(lg, temperature=0.8, top_k=top_k, top_p=top_p, uniforms=u)
+        want = [R.sample_logits(lg[b], temperature=0.8, top_k=top_k, top_p=top_p, u=u[b])
+                for b in range(6)]
+        assert list(got) == want, (trial, list(got), want)
+
+
+def test_sampling_with_repetition_penalty(gpu):
+    rng = np.random.default_rng(11)
+    lg = _distinct_logits(rng, 3, 1000)
+    hist = [[1, 5, 5, 9], [int(np.argmax(lg[1]))], list(range(0, 1000, 7))]
+    u = rng.random(3)
+    for temp, k in ((0.0, 0), (0.7, 20)):
+        got = _k().sample_tokens(lg, temperature=temp, top_k=k, uniforms=u, history=hist,
+                                 repetition_penalty=1.7)
+        want = [R.sample_logits(lg[b], temperature=temp, top_k=k, top_p=1.0, u=u[b],
+                                token_ids=hist[b], repetition_penalty=1.7) for b in range(3)]
+        assert list(got) == want
