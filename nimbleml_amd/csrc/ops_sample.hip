@@ -13,8 +13,11 @@
 //   that descending order whose float64 running sum / total exceeds u.
 // No sort is formed: every "k-th largest" and "first descending position whose
 // running mass exceeds a target" is found by a 4-pass, 8-bit radix select over
-// the order-preserving integer image of x, with per-bin counts and masses. Ties
-// in the descending order are taken in ascending index order.
+// the order-preserving integer image of x, with per-bin counts and masses. The
+// descending order is the reference's argsort(probs)[::-1]: equal probabilities
+// come in descending index order, which is what reversing a stable ascending sort
+// gives (NumPy's default argsort is not stable, so the order of exact ties is
+// whatever its sort produced; descending index is the stable reading).
 #include "kernels.hpp"
 
 namespace nml {
@@ -158,10 +161,10 @@ __device__ uint32_t select_kth_key(int V, int k, F key_of, Shared& sh) {
   return prefix;
 }
 
-// First position of the descending order (key desc, index asc) over the elements
-// with in_set(i) whose inclusive running mass (weights w) exceeds `target`.
-// Returns the key τ, the 1-based tie rank j among in-set elements with key τ,
-// and the mass before the τ group.
+// First position of the descending order (key desc, then index desc) over the
+// elements with in_set(i) whose inclusive running mass (weights w, equal for equal
+// keys) exceeds `target`. Returns the key τ and the 1-based rank of that element
+// among the in-set elements with key τ counted in ascending index order.
 template <typename FK, typename FW, typename FS>
 __device__ void select_by_mass(int V, double target, FK key_of, FW weight, FS in_set,
                                uint32_t* tau, int* rank, Shared& sh) {
@@ -211,14 +214,14 @@ __device__ void select_by_mass(int V, double target, FK key_of, FW weight, FS in
     mask |= 255u << shift;
   }
   const int cnt = sh.sel_bin_cnt;
-  int j = 1;
+  int j = 1;  // position within the tie group in walk (descending index) order
   if (cnt > 1) {
     const double w = sh.sel_bin_mass / cnt;
     const double jj = w > 0.0 ? floor((target - sh.sel_cum) / w) + 1.0 : 1.0;
     j = jj < 1.0 ? 1 : (jj > cnt ? cnt : static_cast<int>(jj));
   }
   *tau = prefix;
-  *rank = j;
+  *rank = cnt - j + 1;
 }
 
 // Index of the j-th (1-based, index order) element with pred(i); -1 if none.
@@ -342,8 +345,16 @@ __global__ __launch_bounds__(kThreads) void sample_kernel(SampleArgs a) {
       int j1;
       select_by_mass(V, static_cast<double>(a.top_p), keyp, prob, [](int) { return true; }, &tau1,
                      &j1, sh);
-      // Index of that element; kept = key > τ1, or key == τ1 and index < cut index.
+      // Index of that element; kept = the elements before it in walk order:
+      // key > τ1, or key == τ1 and index > cut index.
       const int cut = find_nth(V, j1, [&](int i) { return keyp(i) == tau1; }, sh);
+      int ties1 = 0;
+      for (int i = threadIdx.x; i < V; i += kThreads) ties1 += keyp(i) == tau1 ? 1 : 0;
+      {
+        int tot = 0;
+        block_excl_scan_i(ties1, &tot, sh);
+        ties1 = tot;
+      }
       // Empty prefix (the crossing element is the top one) keeps that element alone.
       int above = 0;
       for (int i = threadIdx.x; i < V; i += kThreads) above += keyp(i) > tau1 ? 1 : 0;
@@ -352,11 +363,11 @@ __global__ __launch_bounds__(kThreads) void sample_kernel(SampleArgs a) {
         block_excl_scan_i(above, &tot, sh);
         above = tot;
       }
-      const bool single = (above == 0 && j1 == 1);
+      const bool single = (above == 0 && j1 == ties1);  // cut is the largest tied index
       auto kept = [&](int i) {
         const uint32_t k = keyp(i);
         if (single) return i == cut;
-        return k > tau1 || (k == tau1 && i < cut);
+        return k > tau1 || (k == tau1 && i > cut);
       };
       float ks = 0.f;
       for (int i = threadIdx.x; i < V; i += kThreads) ks += kept(i) ? prob(i) : 0.f;
@@ -368,8 +379,9 @@ __global__ __launch_bounds__(kThreads) void sample_kernel(SampleArgs a) {
       block_excl_scan_d(tq, &total, sh);
       uint32_t tau2;
       int j2;
-      select_by_mass(V, u * total, [&](int i) { return fkey(q(i)); }, q, kept, &tau2, &j2, sh);
-      chosen = find_nth(V, j2, [&](int i) { return kept(i) && fkey(q(i)) == tau2; }, sh);
+      // The renormalised list keeps the order of p (generate.py:50-58).
+      select_by_mass(V, u * total, keyp, q, kept, &tau2, &j2, sh);
+      chosen = find_nth(V, j2, [&](int i) { return kept(i) && keyp(i) == tau2; }, sh);
     } else {
       // Index-order float64 CDF; first i with cdf[i] / cdf[-1] > u.
       const int seg = (V + kThreads - 1) / kThreads;

@@ -50,10 +50,10 @@ def assert_tokens_agree(ours, ref, s0, margins, tol):
     compared = 0
     for b in range(ref.shape[0]):
         for t in range(n):
+            if np.atleast_1d(margins[t])[b] <= tol:
+                break  # the reference's own choice is within tolerance of a tie
             assert ours[b, s0 + t] == ref[b, s0 + t], f"row {b} step {t}"
             compared += 1
-            if np.atleast_1d(margins[t])[b] <= tol:
-                break
     return compared
 
 
@@ -151,14 +151,18 @@ def test_tiny_sampled_generate(gpu, name, mode):
     kv = R.KVOracle(w32, cfg.num_heads, cfg.num_layers)
     lg = kv.step(ref[:, :s0])[:, -1]
     live = np.ones(ref.shape[0], dtype=bool)  # rows still compared
+    compared = 0
     for t in range(ref.shape[1] - s0):
         for b in np.nonzero(live)[0]:
-            assert out[b, s0 + t] == ref[b, s0 + t], f"row {b} step {t}"
             if _u_near_boundary(lg[b], u[t, b], ref[b, :s0 + t], kw, tol_for(dt)):
-                live[b] = False
+                live[b] = False  # a logit change within tolerance could flip this draw
+                continue
+            assert out[b, s0 + t] == ref[b, s0 + t], f"row {b} step {t}"
+            compared += 1
         if not live.any():
             break
         lg = kv.step(ref[:, s0 + t:s0 + t + 1])[:, -1]
+    assert compared >= 1
 
 
 def _u_near_boundary(logits, u, hist, kw, tol):

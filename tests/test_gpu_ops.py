@@ -195,3 +195,33 @@ def test_sampling_with_repetition_penalty(gpu):
         want = [R.sample_logits(lg[b], temperature=temp, top_k=k, top_p=1.0, u=u[b],
                                 token_ids=hist[b], repetition_penalty=1.7) for b in range(3)]
         assert list(got) == want
+
+
+@pytest.mark.parametrize("top_k", [0, 30])
+def test_top_p_exact_ties_descending_index(gpu, top_k):
+    """Equal probabilities in the top-p walk come in descending index order — the
+    order argsort(probs)[::-1] gives when the ascending sort is stable
+    (models/generate.py:50). Logits on a coarse grid make many exact ties."""
+    rng = np.random.default_rng(42 + top_k)
+    b, v = 8, 512
+    lg = (rng.integers(-12, 12, (b, v)) * 0.25).astype(np.float32)
+    u = rng.random(b)
+
+    def stable_pick(row, uu):
+        x = row / np.float32(0.8)
+        if top_k:
+            th = np.partition(x, -top_k)[-top_k]
+            x = np.where(x < th, np.float32(-1e9), x)
+        p = np.exp(x - x.max())
+        p = p / p.sum()
+        order = np.argsort(p, kind="stable")[::-1]
+        sp = p[order]
+        cdf = np.cumsum(sp)
+        mask = cdf > 0.9
+        mask[0] = False
+        sp = np.where(mask, 0.0, sp)
+        sp = sp / sp.sum()
+        return int(order[R.choice_from_uniform(sp, uu)])
+
+    got = _k().sample_tokens(lg, temperature=0.8, top_k=top_k, top_p=0.9, uniforms=u)
+    assert list(got) == [stable_pick(lg[i], u[i]) for i in range(b)]
