@@ -168,6 +168,11 @@ int nml_model_generate(nml_model* m, const int64_t* prompts, size_t prompt_strid
  * (embedding … sampling) over `steps` steps of the last generate() call shape. */
 int nml_model_last_decode_ms(nml_model* m, float* ms_per_step);
 
+/* Which decode step the last generate() used: 1 = the persistent one-launch-per-token
+ * kernel (batch 1, d_model 1024, head_dim 64, max_seq_len ≤ 2048), 0 = one launch per
+ * op. Set NIMBLEML_PERSISTENT=0 to force the latter. */
+int nml_model_last_decode_path(nml_model* m, int* persistent);
+
 #ifdef __cplusplus
 }
 #endif

@@ -70,6 +70,7 @@ _SIGS = {
     "nml_model_forward_cached": [vp, vp, vp, sz, sz, vp, i32],
     "nml_model_generate": [vp, vp, sz, PI32, sz, sz, f32, i32, f32, f32, vp, vp, sz, i32],
     "nml_model_last_decode_ms": [vp, C.POINTER(f32)],
+    "nml_model_last_decode_path": [vp, C.POINTER(C.c_int)],
 }
 
 # Parameter kinds (enum nml_param_kind).

@@ -117,4 +117,43 @@ struct SampleArgs {
 };
 int launch_sample(int dt, const SampleArgs& a, hipStream_t st);
 
+// Persistent decode step (batch 1): one launch of kPersistGroups workgroups runs the
+// whole token; see decode_persist.hip.
+constexpr int kPersistGroups = 256;
+constexpr int kPersistMaxLen = 2048;  // attention length bound (max_seq_len)
+
+struct PersistArgs {
+  // Parameters of layer 0; layer l's are at + l·layer_bytes (one arena, same layout
+  // per layer), so no pointer has to be loaded from memory inside the kernel.
+  const void *ln1, *wqkv, *bqkv, *wo, *bo, *ln2, *w1, *b1, *w2, *b2;
+  long long layer_bytes;
+  const void* emb;
+  const void* posw;
+  const void* lnf;
+  void* kc;                    // K cache of layer 0; layer l at + l·kv_layer elements
+  void* vc;
+  long long kv_layer, kv_head; // elements between layers / heads
+  int64_t* tokens;             // token history of the row; tokens[pos] is fed
+  int32_t* pos;                // pos[0]: position of the fed token (advanced when fused)
+  void* logits;                // (V) logits of the step
+  unsigned long long* slots;   // exchange slots, persist_slot_count() entries, zeroed
+  uint32_t* epoch;             // step counter, ≥ 1, advanced by the kernel
+  int* err;                    // bit 0: token/position out of range; bit 2: exchange timeout
+  int V, L, P;
+  int fuse_argmax;             // greedy: write tokens[pos+1] and advance pos in-kernel
+  float scale;                 // sqrt(dk)
+  // Optional phase timestamps (wall_clock64) of each workgroup: trace[g·stride + mark],
+  // stride = persist_trace_stride(L). Null: no tracing.
+  unsigned long long* trace;
+};
+
+// Marks: 0 start, 1 embedded; layer l at 4 + 10·l + {0 P1 loads issued, 1 x in,
+// 2 QKV out, 3 q in, 4 chunks out, 5 merged, 6 attention in, 7 x_mid in, 8 h in,
+// 9 x out}; head at 4 + 10·L + {0 x in, 1 logits out, 2 choice}.
+__host__ __device__ inline int persist_trace_stride(int L) { return 4 + 10 * L + 4; }
+
+bool persist_supported(int dt, int d, int H, int F, int B, int P);
+size_t persist_slot_count(int d, int H);
+int launch_decode_persist(int dt, int d, int H, const PersistArgs& a, hipStream_t st);
+
 }  // namespace nml

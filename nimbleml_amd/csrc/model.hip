@@ -8,6 +8,8 @@
 //   x  = x + (a·W_oᵀ + b_o);  xn = RMSNorm₂(x)
 //   h  = GELU(xn·W₁ᵀ + b₁);   x = x + (h·W₂ᵀ + b₂)
 // then xn = RMSNorm_f(x) and logits = xn·Eᵀ (tied head).
+#include <cstdio>
+#include <cstdlib>
 #include <cstring>
 #include <vector>
 
@@ -61,9 +63,11 @@ struct nml_model {
   Buf kvs;        // K/V scratch for forward() without a cache
   Buf logits_ws;  // logits chunk for compute_loss / generate
   Buf small;      // device counters, positions, loss accumulators
+  Buf persist;    // persistent decode: layer pointer table, exchange slots, epoch
   // decode timing of the last generate()
   float last_decode_ms = 0.f;
   int last_decode_steps = 0;
+  int last_decode_persistent = 0;
 };
 
 struct nml_cache {
@@ -369,6 +373,55 @@ int decode_step(nml_model* m, nml_cache* c, const Acts& a, const int64_t* tokens
   return launch_linear(m->dt, lm, st);
 }
 
+__global__ void set_u32_kernel(uint32_t* p, uint32_t v) {
+  if (threadIdx.x == 0 && blockIdx.x == 0) p[0] = v;
+}
+
+// NIMBLEML_PERSISTENT=0 selects the multi-kernel decode step even where the
+// persistent one applies.
+bool persist_wanted() {
+  const char* e = std::getenv("NIMBLEML_PERSISTENT");
+  return !(e && e[0] == '0');
+}
+
+// Layer-0 parameter pointers with the per-layer stride, zeroed exchange slots and
+// epoch = 1 for a persistent decode. Fails (so the caller uses the multi-kernel
+// step) if the arena does not place every layer at one fixed stride.
+int persist_prepare(nml_model* m, PersistArgs* pa, hipStream_t st) {
+  const Layer& l0 = m->layers[0];
+  const long long stride =
+      m->L > 1 ? static_cast<const char*>(m->layers[1].ln1) - static_cast<const char*>(l0.ln1) : 0;
+  for (int l = 1; l < m->L; ++l) {
+    const Layer& w = m->layers[l];
+    const void* const have[] = {w.ln1, w.wqkv, w.bqkv, w.wo, w.bo, w.ln2, w.w1, w.b1, w.w2, w.b2};
+    const void* const first[] = {l0.ln1, l0.wqkv, l0.bqkv, l0.wo, l0.bo, l0.ln2, l0.w1, l0.b1, l0.w2, l0.b2};
+    for (int k = 0; k < 10; ++k)
+      NML_REQUIRE(static_cast<const char*>(have[k]) == static_cast<const char*>(first[k]) + l * stride,
+                  "persistent decode: layer parameters are not at a fixed stride");
+  }
+  pa->ln1 = l0.ln1;
+  pa->wqkv = l0.wqkv;
+  pa->bqkv = l0.bqkv;
+  pa->wo = l0.wo;
+  pa->bo = l0.bo;
+  pa->ln2 = l0.ln2;
+  pa->w1 = l0.w1;
+  pa->b1 = l0.b1;
+  pa->w2 = l0.w2;
+  pa->b2 = l0.b2;
+  pa->layer_bytes = stride;
+  const size_t sb = align256(persist_slot_count(m->d, m->H) * 8);
+  NML_TRY(m->persist.ensure(sb + 256));
+  char* base = static_cast<char*>(m->persist.p);
+  NML_HIP(hipMemsetAsync(base, 0, sb + 256, st));
+  uint32_t* epoch = reinterpret_cast<uint32_t*>(base + sb);
+  set_u32_kernel<<<1, 64, 0, st>>>(epoch, 1u);
+  NML_LAUNCHED();
+  pa->slots = reinterpret_cast<unsigned long long*>(base);
+  pa->epoch = epoch;
+  return 0;
+}
+
 __global__ void add_scalar_kernel(int32_t* p, int n, int v) {
   const int i = blockIdx.x * blockDim.x + threadIdx.x;
   if (i < n) p[i] += v;
@@ -442,6 +495,7 @@ int nml_model_destroy(nml_model* m) {
   m->kvs.release();
   m->logits_ws.release();
   m->small.release();
+  m->persist.release();
   if (m->arena) (void)hipFree(m->arena);
   delete m;
   return 0;
@@ -727,6 +781,50 @@ int nml_model_generate(nml_model* m, const int64_t* prompts, size_t prompt_strid
 
   Acts a;
   NML_TRY(acts_for(m, B, B, &a));
+  const bool persistent =
+      persist_wanted() && persist_supported(m->dt, m->d, m->H, m->F, B, m->P);
+  PersistArgs pa{};
+  if (persistent) {
+    NML_TRY(persist_prepare(m, &pa, st));
+    pa.emb = m->emb;
+    pa.posw = m->pos;
+    pa.lnf = m->lnf;
+    pa.kc = c->k;
+    pa.vc = c->v;
+    pa.kv_layer = (long long)B * m->H * m->P * m->dk;
+    pa.kv_head = (long long)m->P * m->dk;
+    pa.tokens = tokens_out;
+    pa.pos = sm.pos;
+    pa.logits = logits;
+    pa.err = sm.err;
+    pa.V = m->V;
+    pa.L = m->L;
+    pa.P = m->P;
+    pa.fuse_argmax = (temperature <= 0.f && repetition_penalty == 1.0f) ? 1 : 0;
+    pa.scale = sqrtf((float)m->dk);
+  }
+  // NIMBLEML_PERSIST_TRACE=<file>: phase timestamps of the last persistent step.
+  const char* trace_path = persistent ? std::getenv("NIMBLEML_PERSIST_TRACE") : nullptr;
+  const size_t trace_n = (size_t)kPersistGroups * persist_trace_stride(m->L);
+  Buf trace_buf;
+  struct TraceGuard {
+    Buf* b;
+    ~TraceGuard() { b->release(); }
+  } trace_guard{&trace_buf};
+  if (trace_path && trace_path[0]) {
+    NML_TRY(trace_buf.ensure(trace_n * 8));
+    NML_HIP(hipMemsetAsync(trace_buf.p, 0, trace_n * 8, st));
+    pa.trace = static_cast<unsigned long long*>(trace_buf.p);
+  }
+  // One decode step: feed tokens[pos], choose tokens[pos + 1], advance pos.
+  auto step = [&]() -> int {
+    if (persistent) {
+      NML_TRY(launch_decode_persist(m->dt, m->d, m->H, pa, st));
+      return pa.fuse_argmax ? 0 : launch_sample(m->dt, sa, st);
+    }
+    NML_TRY(decode_step(m, c, a, tokens_out, (long long)out_stride, sm.pos, sm.err, logits, st));
+    return launch_sample(m->dt, sa, st);
+  };
   hipEvent_t e0 = nullptr, e1 = nullptr;
   NML_HIP(hipEventCreate(&e0));
   NML_HIP(hipEventCreate(&e1));
@@ -737,10 +835,9 @@ int nml_model_generate(nml_model* m, const int64_t* prompts, size_t prompt_strid
       hipGraph_t graph = nullptr;
       hipGraphExec_t exec = nullptr;
       NML_HIP(hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal));
-      int r1 = decode_step(m, c, a, tokens_out, (long long)out_stride, sm.pos, sm.err, logits, st);
-      int r2 = r1 == 0 ? launch_sample(m->dt, sa, st) : -1;
+      const int r1 = step();
       hipError_t ec = hipStreamEndCapture(st, &graph);
-      if (r1 != 0 || r2 != 0) {
+      if (r1 != 0) {
         if (graph) (void)hipGraphDestroy(graph);
         return -1;
       }
@@ -756,10 +853,7 @@ int nml_model_generate(nml_model* m, const int64_t* prompts, size_t prompt_strid
       NML_REQUIRE(rc == 0, "hipGraphLaunch failed");
     } else {
       NML_HIP(hipEventRecord(e0, st));
-      for (int t = 0; t < steps; ++t) {
-        NML_TRY(decode_step(m, c, a, tokens_out, (long long)out_stride, sm.pos, sm.err, logits, st));
-        NML_TRY(launch_sample(m->dt, sa, st));
-      }
+      for (int t = 0; t < steps; ++t) NML_TRY(step());
       NML_HIP(hipEventRecord(e1, st));
     }
   } else {
@@ -775,6 +869,18 @@ int nml_model_generate(nml_model* m, const int64_t* prompts, size_t prompt_strid
   (void)hipEventDestroy(e1);
   m->last_decode_ms = ms;
   m->last_decode_steps = steps;
+  m->last_decode_persistent = persistent ? 1 : 0;
+  if (pa.trace) {
+    std::vector<unsigned long long> host(trace_n);
+    NML_HIP(hipMemcpy(host.data(), pa.trace, trace_n * 8, hipMemcpyDeviceToHost));
+    FILE* fp = std::fopen(trace_path, "wb");
+    NML_REQUIRE(fp != nullptr, "cannot write %s", trace_path);
+    const int hdr[3] = {kPersistGroups, persist_trace_stride(m->L), m->L};
+    std::fwrite(hdr, sizeof(hdr), 1, fp);
+    std::fwrite(host.data(), 8, trace_n, fp);
+    std::fclose(fp);
+  }
+  NML_REQUIRE((herr & 4) == 0, "persistent decode: a data exchange timed out");
   NML_REQUIRE(herr == 0, "Token ID out of range [0, %d)", m->V);
   return 0;
 }
@@ -782,6 +888,12 @@ int nml_model_generate(nml_model* m, const int64_t* prompts, size_t prompt_strid
 int nml_model_last_decode_ms(nml_model* m, float* ms_per_step) {
   NML_REQUIRE(m != nullptr, "model is null");
   *ms_per_step = m->last_decode_steps > 0 ? m->last_decode_ms / m->last_decode_steps : 0.f;
+  return 0;
+}
+
+int nml_model_last_decode_path(nml_model* m, int* persistent) {
+  NML_REQUIRE(m != nullptr, "model is null");
+  *persistent = m->last_decode_persistent;
   return 0;
 }
 

@@ -260,6 +260,12 @@ class GPT(Module):
         N.check(N.lib.nml_model_last_decode_ms(self._device_model(), C.byref(ms)))
         return float(ms.value)
 
+    def last_decode_persistent(self) -> bool:
+        """Whether the last generate() ran the persistent one-launch-per-token step."""
+        v = C.c_int()
+        N.check(N.lib.nml_model_last_decode_path(self._device_model(), C.byref(v)))
+        return bool(v.value)
+
     def __del__(self):
         self._dev = None
 
