@@ -48,6 +48,9 @@ struct LinearArgs {
 };
 
 int launch_linear(int dt, const LinearArgs& a, hipStream_t st);
+// Workspace of the split-K skinny GEMM (8 < M ≤ 64) for outputs up to max_n wide.
+// Without it (or when too small) that GEMM runs unsplit. Call outside stream capture.
+int linear_reserve_workspace(int max_n);
 
 int launch_embed(int dt, const int64_t* ids, const void* emb, const void* pos,
                  const int32_t* pos_base, void* out, int B, int S, int d, int V, int P,

@@ -287,7 +287,8 @@ int check_ready(nml_model* m) {
 // One decode step for B rows of a cache: feeds tokens[b][pos[b]] at position
 // pos[b], leaves logits (B, V) in `logits`.
 int decode_step(nml_model* m, nml_cache* c, const Acts& a, const int64_t* tokens,
-                long long tok_stride, int32_t* pos, int* err, void* logits, hipStream_t st) {
+                long long tok_stride, int32_t* pos, int* err, void* logits, int max_len,
+                hipStream_t st) {
   const int B = c->B, d = m->d;
   NML_TRY(launch_embed_decode(m->dt, tokens, tok_stride, pos, m->emb, m->pos, a.x, B, d, m->V,
                               m->P, err, st));
@@ -322,7 +323,7 @@ int decode_step(nml_model* m, nml_cache* c, const Acts& a, const int64_t* tokens
     at.S = 1;
     at.dk = m->dk;
     at.scale = sqrtf((float)m->dk);
-    NML_TRY(launch_attention_decode(m->dt, at, pos, m->P, a.part, st));
+    NML_TRY(launch_attention_decode(m->dt, at, pos, max_len, a.part, st));
     LinearArgs wo{};
     wo.x = a.att;
     wo.lda = d;
@@ -473,6 +474,12 @@ int nml_model_create(int vocab, int d_model, int num_heads, int num_layers, int 
     return -1;
   }
   m->arena_bytes = total;
+  // Split-K workspace of the batched-decode projections (before any graph capture).
+  if (linear_reserve_workspace(4096) != 0) {
+    (void)hipFree(m->arena);
+    delete m;
+    return -1;
+  }
   char* p = static_cast<char*>(m->arena);
   auto take = [&](int kind, int layer) {
     void** slot = param_slot(m, kind, layer);
@@ -781,6 +788,9 @@ int nml_model_generate(nml_model* m, const int64_t* prompts, size_t prompt_strid
 
   Acts a;
   NML_TRY(acts_for(m, B, B, &a));
+  // Attention length bound of the decode steps: the last step feeds position
+  // maxp + max_new - 2 and attends to every key up to it.
+  const int decode_len = maxp + (int)max_new - 1;
   const bool persistent =
       persist_wanted() && persist_supported(m->dt, m->d, m->H, m->F, B, m->P);
   PersistArgs pa{};
@@ -822,7 +832,8 @@ int nml_model_generate(nml_model* m, const int64_t* prompts, size_t prompt_strid
       NML_TRY(launch_decode_persist(m->dt, m->d, m->H, pa, st));
       return pa.fuse_argmax ? 0 : launch_sample(m->dt, sa, st);
     }
-    NML_TRY(decode_step(m, c, a, tokens_out, (long long)out_stride, sm.pos, sm.err, logits, st));
+    NML_TRY(decode_step(m, c, a, tokens_out, (long long)out_stride, sm.pos, sm.err, logits,
+                        decode_len, st));
     return launch_sample(m->dt, sa, st);
   };
   hipEvent_t e0 = nullptr, e1 = nullptr;

@@ -67,6 +67,7 @@ int nml_linear_device(const void* x, size_t ld_x, const void* w_t, const void* b
   NML_REQUIRE(epilogue >= EPI_NONE && epilogue <= EPI_BIAS_RESID,
               "linear: epilogue %d not available here", epilogue);
   NML_REQUIRE(ld_x >= in_f, "linear: ld_x < in_f");
+  NML_TRY(linear_reserve_workspace(4096));
   LinearArgs a{};
   a.x = x;
   a.lda = (long long)ld_x;

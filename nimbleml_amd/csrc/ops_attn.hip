@@ -18,6 +18,7 @@ namespace nml {
 namespace {
 
 constexpr int kTile = 64;
+constexpr int kCombineMax = 1024;  // chunks of one (row, head): max_seq_len ≤ 65536
 
 template <typename T, int DK>
 __global__ __launch_bounds__(64) void attn_prefill_kernel(AttnArgs a) {
@@ -103,8 +104,110 @@ __global__ __launch_bounds__(64) void attn_prefill_kernel(AttnArgs a) {
   }
 }
 
+// 16-byte loads of 8 consecutive elements.
+template <typename T>
+__device__ __forceinline__ void ld8(const T* p, float (&o)[8]) {
+  if constexpr (sizeof(T) == 2) {
+    const half8 v = *reinterpret_cast<const half8*>(p);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) o[e] = static_cast<float>(v[e]);
+  } else {
+    const floatx4 x = *reinterpret_cast<const floatx4*>(p);
+    const floatx4 y = *reinterpret_cast<const floatx4*>(p + 4);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      o[e] = x[e];
+      o[4 + e] = y[e];
+    }
+  }
+}
+
+// Decode attention, one 256-lane workgroup per 64-key chunk of one (row, head):
+// scores with 4 lanes per key (each DK/4 dims, 16-byte loads along the key row),
+// chunk max / Σp in LDS, then P·V with each lane owning 8 dims of a key subset.
+// Writes the chunk's (max, Σp, Σp·v) for the combine pass.
 template <typename T, int DK>
-__global__ __launch_bounds__(64) void attn_decode_kernel(AttnArgs a, const int32_t* __restrict__ pos,
+__global__ __launch_bounds__(256) void attn_decode_kernel(AttnArgs a, const int32_t* __restrict__ pos,
+                                                          int max_chunks, float* __restrict__ part) {
+#pragma clang fp contract(off)
+  constexpr int CH = kTile, DPT = DK / 4, DG = DK / 8, NKS = 256 / DG, KPT = CH / NKS;
+  __shared__ float s_q[DK], s_p[CH], s_red[8];
+  __shared__ float s_o[NKS][DK + 1];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int c = blockIdx.x, bh = blockIdx.y;
+  const int b = bh / a.H, h = bh - (bh / a.H) * a.H;
+  const int len = pos[b] + 1;
+  const int k0 = c * CH;
+  if (k0 >= len) return;  // whole workgroup: the combine pass reads chunks below len only
+  const T* __restrict__ K = static_cast<const T*>(a.k) + b * a.kv_stride_b + h * a.kv_stride_h;
+  const T* __restrict__ Vp = static_cast<const T*>(a.v) + b * a.kv_stride_b + h * a.kv_stride_h;
+  const float scale_t = static_cast<float>(static_cast<T>(a.scale));
+  // issue the chunk's loads first (keys past len clamped to len - 1, never used)
+  const int key = k0 + (tid >> 2), qq = tid & 3;
+  const int keyc = key < len ? key : len - 1;
+  float kr[DPT];
+#pragma unroll
+  for (int e = 0; e < DPT; e += 8) {
+    float t8[8];
+    ld8<T>(K + static_cast<long long>(keyc) * DK + qq * DPT + e, t8);
+#pragma unroll
+    for (int u = 0; u < 8; ++u) kr[e + u] = t8[u];
+  }
+  const int dg = tid % DG, ks = tid / DG;
+  float vr[KPT][8];
+#pragma unroll
+  for (int i = 0; i < KPT; ++i) {
+    const int vk = k0 + ks + i * NKS;
+    ld8<T>(Vp + static_cast<long long>(vk < len ? vk : len - 1) * DK + dg * 8, vr[i]);
+  }
+  if (tid < DK) s_q[tid] = static_cast<float>(static_cast<const T*>(a.q)[static_cast<size_t>(bh) * DK + tid]);
+  __syncthreads();
+  float dot = 0.f;
+#pragma unroll
+  for (int e = 0; e < DPT; ++e) dot += s_q[qq * DPT + e] * kr[e];
+  dot += __shfl_xor(dot, 1, 64);
+  dot += __shfl_xor(dot, 2, 64);
+  const bool valid = key < len;
+  const float sc = valid ? rnd<T>(rnd<T>(dot) / scale_t) : -INFINITY;
+  float mx = wave_max(sc);
+  if (lane == 0) s_red[wave] = mx;
+  __syncthreads();
+  mx = fmaxf(fmaxf(s_red[0], s_red[1]), fmaxf(s_red[2], s_red[3]));
+  const float p = valid ? expf(sc - mx) : 0.f;
+  if (qq == 0) s_p[tid >> 2] = p;
+  float l = wave_sum(qq == 0 ? p : 0.f);
+  if (lane == 0) s_red[4 + wave] = l;
+  __syncthreads();
+  l = (s_red[4] + s_red[5]) + (s_red[6] + s_red[7]);
+  float o[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) o[e] = 0.f;
+#pragma unroll
+  for (int i = 0; i < KPT; ++i) {
+    const int jj = ks + i * NKS;
+    if (k0 + jj < len) {
+      const float pj = s_p[jj];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) o[e] += pj * vr[i][e];
+    }
+  }
+#pragma unroll
+  for (int e = 0; e < 8; ++e) s_o[ks][dg * 8 + e] = o[e];
+  __syncthreads();
+  float* pp = part + (static_cast<size_t>(bh) * max_chunks + c) * (DK + 2);
+  if (tid < DK) {
+    float s = 0.f;
+    for (int k2 = 0; k2 < NKS; ++k2) s += s_o[k2][tid];
+    pp[2 + tid] = s;
+  } else if (tid == DK) {
+    pp[0] = mx;
+    pp[1] = l;
+  }
+}
+
+// Head dims below 32: one 64-lane wave per chunk, each lane scores one key.
+template <typename T, int DK>
+__global__ __launch_bounds__(64) void attn_decode_small_kernel(AttnArgs a, const int32_t* __restrict__ pos,
                                                          int max_chunks, float* __restrict__ part) {
   const int lane = threadIdx.x;
   const int c = blockIdx.x, bh = blockIdx.y;
@@ -148,9 +251,13 @@ __global__ __launch_bounds__(64) void attn_decode_kernel(AttnArgs a, const int32
   }
 }
 
+// Merge of the chunk partials of one (row, head): lane c holds chunk c's (max, Σp) —
+// up to 64 chunks per pass, loaded in parallel — then each lane owns output dims and
+// sums the chunks' Σp·v with weights exp(max_c − M) / Σ_c exp(max_c − M)·Σp_c.
 template <typename T, int DK>
 __global__ __launch_bounds__(64) void attn_combine_kernel(AttnArgs a, const int32_t* __restrict__ pos,
                                                           int max_chunks, const float* __restrict__ part) {
+  __shared__ float s_w[kCombineMax];
   const int lane = threadIdx.x;
   const int bh = blockIdx.x;
   const int b = bh / a.H, h = bh - (bh / a.H) * a.H;
@@ -158,20 +265,169 @@ __global__ __launch_bounds__(64) void attn_combine_kernel(AttnArgs a, const int3
   const int nc = (len + kTile - 1) / kTile;
   const float* pb = part + static_cast<size_t>(bh) * max_chunks * (DK + 2);
   float M = -INFINITY;
-  for (int c = 0; c < nc; ++c) M = fmaxf(M, pb[c * (DK + 2)]);
+  for (int c = lane; c < nc; c += 64) M = fmaxf(M, pb[c * (DK + 2)]);
+  M = wave_max(M);
   float den = 0.f;
-  for (int c = 0; c < nc; ++c) den += __expf(pb[c * (DK + 2)] - M) * pb[c * (DK + 2) + 1];
+  for (int c = lane; c < nc; c += 64) {
+    const float w = expf(pb[c * (DK + 2)] - M);
+    s_w[c] = w;
+    den += w * pb[c * (DK + 2) + 1];
+  }
+  den = wave_sum(den);
+  __syncthreads();
   const float inv = 1.f / den;
   T* out = static_cast<T*>(a.out) + static_cast<size_t>(b) * a.H * DK + h * DK;
   for (int d = lane; d < DK; d += 64) {
     float num = 0.f;
-    for (int c = 0; c < nc; ++c) num += __expf(pb[c * (DK + 2)] - M) * pb[c * (DK + 2) + 2 + d];
+    for (int c = 0; c < nc; ++c) num += s_w[c] * pb[c * (DK + 2) + 2 + d];
     out[d] = static_cast<T>(num * inv);
+  }
+}
+
+// Causal flash attention on the matrix cores (fp16, head dim 64 or 128). A 256-lane
+// workgroup takes 128 queries of one (row, head), 32 per wave, and walks 64-key tiles
+// of the cache staged in LDS (K row-major, V transposed):
+//   Sᵀ = K·Qᵀ    v_mfma_f32_32x32x16_f16, A = 32 keys × 16 dims from LDS, B = Qᵀ
+//                (registers for the whole walk); lane l then holds query l%32 and
+//                keys 8(r/4) + 4(l/32) + r%4 of each 32-key tile in register r;
+//   online softmax per query: lane-local over its 16 keys, one xor-32 shuffle with
+//                the lane holding the other 16 (scores rounded as in the scalar path);
+//   Oᵀ += Vᵀ·Pᵀ  A = Vᵀ (32 dims × 16 keys) from LDS, B = Pᵀ in fp16 straight from the
+//                Sᵀ registers: B's k-slot j of lane l is key 8(j/4) + 4(l/32) + j%4 of
+//                the 16-key block, and A is read with the same key order;
+// so each lane owns one query's output column: the α rescale and the final 1/Σp
+// need no data exchange. Key tiles past a wave's last query are skipped.
+constexpr int kFQ = 128, kFK = 64;
+
+template <int DK>
+__global__ __launch_bounds__(256) void attn_prefill_mfma_kernel(AttnArgs a) {
+#pragma clang fp contract(off)
+  constexpr int KS = DK / 16;  // 16-dim steps of q·k
+  constexpr int OT = DK / 32;  // 32-dim tiles of the output
+  __shared__ half_t Ks[kFK][DK + 8];
+  __shared__ half_t Vt[DK][kFK + 8];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int bh = blockIdx.y;
+  const int b = bh / a.H, h = bh - (bh / a.H) * a.H;
+  const int S = a.S;
+  const int q0 = blockIdx.x * kFQ;
+  const int base = a.pos_base ? a.pos_base[b] : 0;
+  const half_t* __restrict__ Kg = static_cast<const half_t*>(a.k) + b * a.kv_stride_b + h * a.kv_stride_h;
+  const half_t* __restrict__ Vg = static_cast<const half_t*>(a.v) + b * a.kv_stride_b + h * a.kv_stride_h;
+  const half_t* __restrict__ Qg = static_cast<const half_t*>(a.q) + static_cast<size_t>(bh) * S * DK;
+  const float scale_t = static_cast<float>(static_cast<half_t>(a.scale));
+  const int qw = q0 + wave * 32;           // first query of this wave
+  const int myq = qw + (lane & 31);        // this lane's query
+  const int hi = lane >> 5;                // which half of the wave
+  const half8 z8 = {0, 0, 0, 0, 0, 0, 0, 0};
+  half8 qb[KS];
+#pragma unroll
+  for (int ks = 0; ks < KS; ++ks)
+    qb[ks] = myq < S ? *reinterpret_cast<const half8*>(Qg + static_cast<size_t>(myq) * DK + ks * 16 + hi * 8)
+                     : z8;
+  const int kend = base + min(q0 + kFQ, S);  // keys of the workgroup's last query
+  const int wave_last = base + min(qw + 31, S - 1);
+  const int qpos = base + myq;
+  float m = -INFINITY, l = 0.f;
+  floatx16 o[OT];
+#pragma unroll
+  for (int t = 0; t < OT; ++t)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) o[t][r] = 0.f;
+
+  for (int k0 = 0; k0 < kend; k0 += kFK) {
+    __syncthreads();
+    constexpr int CH = kFK * DK / 8;  // 16-byte pieces per tile
+#pragma unroll
+    for (int i = 0; i < CH / 256; ++i) {
+      const int c = tid + 256 * i;
+      const int key = c / (DK / 8), d8 = (c % (DK / 8)) * 8;
+      const bool ok = k0 + key < kend;
+      const half8 kv = ok ? *reinterpret_cast<const half8*>(Kg + static_cast<long long>(k0 + key) * DK + d8) : z8;
+      const half8 vv = ok ? *reinterpret_cast<const half8*>(Vg + static_cast<long long>(k0 + key) * DK + d8) : z8;
+      *reinterpret_cast<half8*>(&Ks[key][d8]) = kv;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) Vt[d8 + e][key] = vv[e];
+    }
+    __syncthreads();
+    if (k0 > wave_last) continue;  // every key of this tile is after this wave's queries
+    floatx16 st[2];
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) st[t][r] = 0.f;
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) {
+        const half8 ka = *reinterpret_cast<const half8*>(&Ks[t * 32 + (lane & 31)][ks * 16 + hi * 8]);
+        st[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ka, qb[ks], st[t], 0, 0, 0);
+      }
+    }
+    float mx = m;
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int key = k0 + t * 32 + 8 * (r >> 2) + 4 * hi + (r & 3);
+        const float s = (key <= qpos && key < kend) ? rnd<half_t>(rnd<half_t>(st[t][r]) / scale_t)
+                                                    : -INFINITY;
+        st[t][r] = s;
+        mx = fmaxf(mx, s);
+      }
+    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+    const float alpha = (mx == -INFINITY) ? 1.f : expf(m - mx);
+    l *= alpha;
+#pragma unroll
+    for (int t = 0; t < OT; ++t)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) o[t][r] *= alpha;
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb) {
+        half8 pb;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          const float s = st[t][8 * kb + j];
+          const float p = (s == -INFINITY) ? 0.f : expf(s - mx);
+          l += p;
+          pb[j] = static_cast<half_t>(p);
+        }
+        const int kblk = t * 32 + kb * 16 + 4 * hi;
+#pragma unroll
+        for (int ot = 0; ot < OT; ++ot) {
+          const half_t* vrow = &Vt[ot * 32 + (lane & 31)][kblk];
+          half8 va;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            va[e] = vrow[e];
+            va[4 + e] = vrow[8 + e];
+          }
+          o[ot] = __builtin_amdgcn_mfma_f32_32x32x16_f16(va, pb, o[ot], 0, 0, 0);
+        }
+      }
+    m = mx;
+  }
+  l += __shfl_xor(l, 32, 64);
+  if (myq < S) {
+    const float inv = 1.f / l;
+    const int hd = a.H * DK;
+    half_t* out = static_cast<half_t*>(a.out) + (static_cast<size_t>(b) * S + myq) * hd + h * DK;
+#pragma unroll
+    for (int ot = 0; ot < OT; ++ot)
+#pragma unroll
+      for (int r = 0; r < 16; ++r)
+        out[ot * 32 + 8 * (r >> 2) + 4 * hi + (r & 3)] = static_cast<half_t>(o[ot][r] * inv);
   }
 }
 
 template <typename T, int DK>
 int prefill_typed(const AttnArgs& a, hipStream_t st) {
+  if constexpr (sizeof(T) == 2 && (DK == 64 || DK == 128)) {
+    dim3 grid((a.S + kFQ - 1) / kFQ, a.B * a.H);
+    attn_prefill_mfma_kernel<DK><<<grid, 256, 0, st>>>(a);
+    NML_LAUNCHED();
+    return 0;
+  }
   dim3 grid((a.S + kTile - 1) / kTile, a.B * a.H);
   attn_prefill_kernel<T, DK><<<grid, 64, 0, st>>>(a);
   NML_LAUNCHED();
@@ -182,7 +438,10 @@ template <typename T, int DK>
 int decode_typed(const AttnArgs& a, const int32_t* pos, int max_len, float* part, hipStream_t st) {
   const int max_chunks = (max_len + kTile - 1) / kTile;
   dim3 grid(max_chunks, a.B * a.H);
-  attn_decode_kernel<T, DK><<<grid, 64, 0, st>>>(a, pos, max_chunks, part);
+  if constexpr (DK >= 32)
+    attn_decode_kernel<T, DK><<<grid, 256, 0, st>>>(a, pos, max_chunks, part);
+  else
+    attn_decode_small_kernel<T, DK><<<grid, 64, 0, st>>>(a, pos, max_chunks, part);
   NML_LAUNCHED();
   attn_combine_kernel<T, DK><<<a.B * a.H, 64, 0, st>>>(a, pos, max_chunks, part);
   NML_LAUNCHED();
@@ -225,7 +484,8 @@ int launch_attention_prefill(int dt, const AttnArgs& a, hipStream_t st) {
 int launch_attention_decode(int dt, const AttnArgs& a, const int32_t* pos, int max_len, float* part,
                             hipStream_t st) {
   if (a.B == 0) return 0;
-  NML_REQUIRE(max_len > 0, "attention decode: max_len must be positive");
+  NML_REQUIRE(max_len > 0 && max_len <= kCombineMax * kTile,
+              "attention decode: max_len %d outside (0, %d]", max_len, kCombineMax * kTile);
   return dt == F16 ? decode_dk<half_t>(a, pos, max_len, part, st)
                    : decode_dk<float>(a, pos, max_len, part, st);
 }

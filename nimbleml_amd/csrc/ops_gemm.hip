@@ -300,8 +300,164 @@ int gemv_dispatch_rpw(const LinearArgs& a, hipStream_t st) {
   return 0;
 }
 
+// ------------------------------------------------------- skinny MFMA GEMM (fp16)
+// 8 < M ≤ 64 rows (batched decode): HBM-bound on W, so the grid is spread over N and,
+// when N is small, over K. A workgroup owns 16 output columns (rows of W) for all M
+// rows and one of S slices of K; its 4 waves take a quarter of the slice each and run
+// v_mfma_f32_16x16x32_f16 with A = those 16 rows of W and B = 16 rows of x per m-tile
+// (MT tiles). The quarters are summed through LDS in a fixed order. With S > 1 each
+// workgroup stores its fp32 tile to the workspace and takes a ticket; the last of the
+// S workgroups of a column tile. Slices 0..S-2 publish their fp32 tile as 64-bit
+// (1 << 32 | value) slots with relaxed device-scope stores (no cache-flushing fences);
+// slice S-1 — dispatched after every other workgroup of the grid, so its bounded
+// wait always ends — polls them, sums the slices in order (independent of arrival
+// order), clears the slots for the next launch and runs the epilogue.
+// Operand layout of the 16x16x32 MFMA: lane l holds A[l%16][(l/16)·8 + 0..7] and
+// B[(l/16)·8 + 0..7][l%16]; the result D[(l/16)·4 + e][l%16], e < 4.
+constexpr int kSkN = 16;
+
+struct SkinnyWs {
+  unsigned long long* part = nullptr;  // [tile][slice < S-1][MT·256] flagged partials, zero between launches
+  size_t part_slots = 0;
+  int tiles = 0;
+};
+SkinnyWs g_skinny;
+
+template <int EPI, int MT, int U>
+__global__ __launch_bounds__(256) void skinny_f16_kernel(LinearArgs a, unsigned long long* ws) {
+  __shared__ float red[4][MT][16][17];
+  const half_t* __restrict__ X = static_cast<const half_t*>(a.x);
+  const half_t* __restrict__ W = static_cast<const half_t*>(a.w);
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int tile = blockIdx.x, n0 = tile * kSkN;
+  const int S = gridDim.y, slice = blockIdx.y;
+  const int M = a.M, N = a.N, K = a.K;
+  const int kq = K / (4 * S);
+  const int kbeg = (slice * 4 + wave) * kq;
+  const int r = lane & 15, kk = (lane >> 4) * 8;
+  const bool nvalid = n0 + r < N;
+  const half_t* wp = W + static_cast<long long>(nvalid ? n0 + r : 0) * K + kbeg + kk;
+  const half_t* xp[MT];
+  bool mvalid[MT];
+#pragma unroll
+  for (int t = 0; t < MT; ++t) {
+    const int m = t * 16 + r;
+    mvalid[t] = m < M;
+    xp[t] = X + static_cast<long long>(mvalid[t] ? m : 0) * a.lda + kbeg + kk;
+  }
+  floatx4 acc[MT];
+#pragma unroll
+  for (int t = 0; t < MT; ++t) acc[t] = floatx4{0.f, 0.f, 0.f, 0.f};
+  const half8 z8 = {0, 0, 0, 0, 0, 0, 0, 0};
+  for (int k = 0; k < kq; k += 32 * U) {
+    half8 av[U], bv[U][MT];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      av[u] = nvalid ? *reinterpret_cast<const half8*>(wp + k + u * 32) : z8;
+#pragma unroll
+      for (int t = 0; t < MT; ++t)
+        bv[u][t] = mvalid[t] ? *reinterpret_cast<const half8*>(xp[t] + k + u * 32) : z8;
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+#pragma unroll
+      for (int t = 0; t < MT; ++t)
+        acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av[u], bv[u][t], acc[t], 0, 0, 0);
+  }
+#pragma unroll
+  for (int t = 0; t < MT; ++t)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) red[wave][t][(lane >> 4) * 4 + e][lane & 15] = acc[t][e];
+  __syncthreads();
+  // thread → outputs o = tid + 256·t: (t, j = m within the tile, i = W row within the tile)
+  float sum[MT];
+#pragma unroll
+  for (int t = 0; t < MT; ++t) {
+    const int j = threadIdx.x >> 4, i = threadIdx.x & 15;
+    sum[t] = ((red[0][t][i][j] + red[1][t][i][j]) + red[2][t][i][j]) + red[3][t][i][j];
+  }
+  if (S > 1) {
+    typedef unsigned long long u64;
+    u64* tile_ws = ws + static_cast<size_t>(tile) * (S - 1) * (MT * 256);
+    if (slice < S - 1) {
+#pragma unroll
+      for (int t = 0; t < MT; ++t)
+        __hip_atomic_store(tile_ws + (static_cast<size_t>(slice) * MT + t) * 256 + threadIdx.x,
+                           (1ull << 32) | __float_as_uint(sum[t]), __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
+      return;
+    }
+    float tot[MT];
+#pragma unroll
+    for (int t = 0; t < MT; ++t) tot[t] = 0.f;
+    for (int q = 0; q < S - 1; ++q) {
+#pragma unroll
+      for (int t = 0; t < MT; ++t) {
+        u64* sl = tile_ws + (static_cast<size_t>(q) * MT + t) * 256 + threadIdx.x;
+        u64 v = __hip_atomic_load(sl, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        for (unsigned spins = 0; (v >> 32) == 0 && spins < (1u << 22); ++spins) {
+          __builtin_amdgcn_s_sleep(1);
+          v = __hip_atomic_load(sl, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+        tot[t] += __uint_as_float(static_cast<uint32_t>(v));
+        // consumed: clear for the next launch, through the same device-coherent path
+        __hip_atomic_store(sl, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
+    }
+#pragma unroll
+    for (int t = 0; t < MT; ++t) sum[t] = tot[t] + sum[t];
+  }
+#pragma unroll
+  for (int t = 0; t < MT; ++t) {
+    const int j = threadIdx.x >> 4, i = threadIdx.x & 15;
+    const int m = t * 16 + j, n = n0 + i;
+    if (m < M && n < N) epilogue<half_t, EPI>(a, m, n, sum[t]);
+  }
+}
+
+// Slices of K: enough workgroups to cover the chip (≥ 256) when N is small, each
+// wave's part of K a multiple of 32, and a workspace large enough.
+int skinny_slices(const LinearArgs& a, int MT) {
+  const int tiles = (a.N + kSkN - 1) / kSkN;
+  int S = 1;
+  while (S < 8 && tiles * S < 256 && a.K % (128 * S * 2) == 0) S *= 2;
+  while (S > 1 && (tiles > g_skinny.tiles ||
+                   static_cast<size_t>(tiles) * (S - 1) * MT * 256 > g_skinny.part_slots))
+    S /= 2;
+  return S;
+}
+
+template <int EPI, int MT>
+int skinny_dispatch_u(const LinearArgs& a, hipStream_t st) {
+  const int S = skinny_slices(a, MT);
+  dim3 grid((a.N + kSkN - 1) / kSkN, S);
+  const int kq = a.K / (4 * S);
+  unsigned long long* ws = g_skinny.part;
+  if (kq % 128 == 0)
+    skinny_f16_kernel<EPI, MT, 4><<<grid, 256, 0, st>>>(a, ws);
+  else if (kq % 64 == 0)
+    skinny_f16_kernel<EPI, MT, 2><<<grid, 256, 0, st>>>(a, ws);
+  else
+    skinny_f16_kernel<EPI, MT, 1><<<grid, 256, 0, st>>>(a, ws);
+  NML_LAUNCHED();
+  return 0;
+}
+
+template <int EPI>
+int skinny_dispatch(const LinearArgs& a, hipStream_t st) {
+  switch ((a.M + 15) / 16) {
+    case 1: return skinny_dispatch_u<EPI, 1>(a, st);
+    case 2: return skinny_dispatch_u<EPI, 2>(a, st);
+    case 3: return skinny_dispatch_u<EPI, 3>(a, st);
+    default: return skinny_dispatch_u<EPI, 4>(a, st);
+  }
+}
+
 template <typename T, int EPI>
 int linear_typed(const LinearArgs& a, hipStream_t st) {
+  if constexpr (sizeof(T) == 2) {
+    if (a.M > 8 && a.M <= 64 && a.K % 128 == 0) return skinny_dispatch<EPI>(a, st);
+  }
   if (a.M <= 8) {
     if (a.M <= 1) return gemv_dispatch_rpw<T, EPI, 1>(a, st);
     if (a.M <= 2) return gemv_dispatch_rpw<T, EPI, 2>(a, st);
@@ -331,6 +487,24 @@ int linear_epi(const LinearArgs& a, hipStream_t st) {
 }
 
 }  // namespace
+
+int linear_reserve_workspace(int max_n) {
+  // Flagged split-K partials for up to 8 slices of 64 rows at N = max_n (16-column
+  // tiles), zeroed. Grow-only; call outside stream capture.
+  const int tiles = (max_n + kSkN - 1) / kSkN;
+  const size_t slots = static_cast<size_t>(tiles) * 7 * 4 * 256;
+  if (tiles <= g_skinny.tiles && slots <= g_skinny.part_slots) return 0;
+  NML_HIP(hipStreamSynchronize(stream()));
+  if (g_skinny.part) NML_HIP(hipFree(g_skinny.part));
+  g_skinny = SkinnyWs{};
+  unsigned long long* p = nullptr;
+  NML_HIP(hipMalloc(&p, slots * 8));
+  NML_HIP(hipMemset(p, 0, slots * 8));
+  g_skinny.part = p;
+  g_skinny.part_slots = slots;
+  g_skinny.tiles = tiles;
+  return 0;
+}
 
 int launch_linear(int dt, const LinearArgs& a, hipStream_t st) {
   if (a.M == 0 || a.N == 0) return 0;

@@ -225,3 +225,48 @@ def test_top_p_exact_ties_descending_index(gpu, top_k):
 
     got = _k().sample_tokens(lg, temperature=0.8, top_k=top_k, top_p=0.9, uniforms=u)
     assert list(got) == [stable_pick(lg[i], u[i]) for i in range(b)]
+
+
+@pytest.mark.parametrize("rows", [9, 17, 32, 33, 64])
+@pytest.mark.parametrize("k", [128, 1024, 4096])
+@pytest.mark.parametrize("epi", [0, 1, 2, 3])
+def test_linear_skinny_fp16(gpu, rows, k, epi):
+    """Batched-decode shapes (8 < rows ≤ 64, K a multiple of 128): the skinny MFMA GEMM."""
+    rng = np.random.default_rng(rows * 100 + k + epi)
+    n = 200  # ragged against the 16-column tile
+    x = rng.standard_normal((rows, k)).astype(np.float16)
+    w = (rng.standard_normal((k, n)) * (1.0 / np.sqrt(k))).astype(np.float16)
+    b = rng.standard_normal(n).astype(np.float16)
+    r = rng.standard_normal((rows, n)).astype(np.float16)
+    out = np.asarray(_k().linear(x, w, b if epi else None, epilogue=epi,
+                                 resid=r if epi == 3 else None)).astype(np.float64)
+    acc = (x.astype(np.float64) @ w.astype(np.float64)).astype(np.float16)
+    lin = (acc + b).astype(np.float16) if epi else acc
+    if epi == 2:
+        lin = R.gelu(lin)
+    if epi == 3:
+        lin = (r + lin).astype(np.float16)
+    want = lin.astype(np.float64)
+    # acc may differ by one fp16 ulp (an fp32 sum in another order, rounded once); each
+    # later rounding adds one ulp of its own operands, so the bound scales with the
+    # operand magnitudes, not with a result that may cancel to ~0.
+    scale = np.abs(acc.astype(np.float64))
+    if epi:
+        scale = scale + np.abs(b.astype(np.float64))
+    if epi == 3:
+        scale = scale + np.abs(r.astype(np.float64))
+    tol = 2.0 * 2.0 ** -10 * (scale + np.abs(want)) + 1e-4
+    assert np.all(np.abs(out - want) <= tol), float(np.max(np.abs(out - want) / tol))
+
+
+@pytest.mark.parametrize("dk", [64, 128])
+def test_sdpa_mfma_long_fp16(gpu, dk):
+    """The matrix-core flash kernel over many 64-key tiles and a ragged last query tile."""
+    rng = np.random.default_rng(dk + 1)
+    bh, s = 2, 1000
+    q, k, v = (rng.standard_normal((bh, s, dk)).astype(np.float16) for _ in range(3))
+    out = np.asarray(_k().fused_sdpa_forward(q, k, v, float(dk) ** 0.5,
+                                             R.causal_mask(s, np.float16))[0]).astype(np.float64)
+    want = R.sdpa(q.astype(np.float64), k.astype(np.float64), v.astype(np.float64),
+                  float(dk) ** 0.5, R.causal_mask(s, np.float64))
+    assert np.abs(out - want).max() < 6e-3

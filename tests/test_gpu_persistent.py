@@ -126,13 +126,16 @@ def test_persistent_logits_match_oracle_fp32(gpu):
         lg = kv.step(out[:, 70 + t:71 + t])[:, -1]
 
 
-def test_persistent_and_multikernel_agree_sampled_fp16(gpu, monkeypatch):
-    """Same uniforms through both decode steps: the same tokens until a near-boundary draw."""
+def test_persistent_and_multikernel_agree_sampled_fp32(gpu, monkeypatch):
+    """Same uniforms through both decode steps give the same tokens. fp32: the two paths
+    differ by ~1e-6 in the logits, far below the top-k gaps and CDF distances that a
+    draw depends on (in fp16 the 50th/51st logit gap of this model is comparable to the
+    fp16 rounding differences, so there the top-k set itself may differ)."""
     import nimbleml_amd as nm
 
     cfg = GPTConfig(8192, 1024, 16, 2, 512)
-    w = make_weights(cfg, seed=9, dtype=np.float16, rich=True)
-    m = _build(cfg, w, np.float16)
+    w = make_weights(cfg, seed=9, dtype=np.float32, rich=True)
+    m = _build(cfg, w, np.float32)
     ids = random_ids((1, 130), cfg.vocab_size, seed=4)
     np.random.seed(11)
     a = nm.generate(m, ids, max_new_tokens=30, temperature=0.8, top_k=50, top_p=1.0)
@@ -141,6 +144,4 @@ def test_persistent_and_multikernel_agree_sampled_fp16(gpu, monkeypatch):
     np.random.seed(11)
     b = nm.generate(m, ids, max_new_tokens=30, temperature=0.8, top_k=50, top_p=1.0)
     assert not m.last_decode_persistent()
-    assert a[0, 130] == b[0, 130]  # first choice comes from the shared prefill
-    same = int(np.argmax(a[0, 130:] != b[0, 130:])) if np.any(a != b) else 30
-    assert same >= 5, same
+    assert np.array_equal(a, b)
