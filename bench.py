@@ -1,24 +1,33 @@
-"""Benchmark: generated tokens/s of the GPT token loop on one MI355X.
+"""Benchmark: generated tokens/s of NimbleML's GPT token loop on one MI355X.
 
-Workload ("C3"): GPT vocab 32000, d_model 1024, 16 heads,
-24 layers, MLP 4x GELU, RMSNorm, max_seq_len 2048, fp16 weights ~N(0, 0.02) (seeded,
-synthetic), batch 1, prompt of 512 uniform ids, greedy decode of 512 new tokens.
-One step = one whole generate() call (prefill + 511 decode steps + on-device
-selection), inputs resident on the device when the timed region starts.
+Headline workload ("C3"): GPT vocab 32000, d_model 1024,
+16 heads, 24 layers, MLP 4x GELU, RMSNorm, max_seq_len 2048, fp16 weights ~N(0, 0.02)
+(seeded, synthetic), batch 1, prompt of 512 uniform ids, greedy decode of 512 new
+tokens. One step = one whole generate() call (prefill + 511 decode steps, each one
+launch of the persistent decode kernel with the greedy choice fused), inputs resident
+on the device when the timed region starts. `value` = generated tokens / wall time.
 
-Prints one JSON line. ``roofline`` is for the decode step (the dominant work):
-algorithmic bytes = every weight once (2·(L·(12d²+11d) + V·d + d) B) plus the K/V
-cache read, 2·2·L·d·ctx B, and written, 2·2·L·d B, per step, averaged over the
-run's contexts 513…1023; divided by the decode time measured with HIP events on
-the library stream around the decode loop. ``cpu_baseline`` times the oracle (the
-reference algorithm restated: full re-forward per token, host sampling) on the
-host cores on a bounded sample.
+`roofline` is for that dominant kernel (one launch per decode token): algorithmic
+bytes per launch = every weight once, 2·(L·(12d²+11d) + V·d + d) B, plus the K/V cache
+read, 2·2·L·d·ctx B, and written, 2·2·L·d B, averaged over the run's contexts
+513…1023; divided by the kernel's average duration, measured with HIP events on the
+library stream around the decode loop. `traffic` (HBM bytes per launch) comes from
+the committed rocprofv3 PMC summary profiles/c3_decode_b1_pmc.md when present.
+
+Two more lines of the same metric ride along (BASELINE.json "batch 1 & 32"):
+  c4: batch 32, prompts U[128,1024], 256 sampled tokens each (T=0.8, top-k 50), HBM
+      roofline of the decode step (weights once + every row's K/V);
+  c5: d2048/L24/V50304 fp16, 4×4096 causal prefill + tied cross-entropy over all
+      16384 positions (compute_loss), MFMA roofline (49.56 TFLOP algorithmic).
+`cpu_baseline` times the oracle (the reference algorithm restated: full re-forward per
+token, host sampling; fp32 because NumPy fp16 has no BLAS path) on a bounded sample.
 """
 from __future__ import annotations
 
 import argparse
 import json
 import os
+import re
 import sys
 import time
 
@@ -27,36 +36,131 @@ import numpy as np
 REPO = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, REPO)
 
-METRIC = BASELINE_METRIC = "generated tokens/sec + % HBM/MFMA roofline, d1024 L24 fp16 GPT, batch 1 & 32"
+METRIC = "generated tokens/sec + % HBM/MFMA roofline, d1024 L24 fp16 GPT, batch 1 & 32"
 HBM_PEAK_GBS = 8000.0
+MFMA_F16_PEAK_TFLOPS = 2500.0
+PMC_SUMMARY = os.path.join(REPO, "profiles", "c3_decode_b1_pmc.md")
 
 
-def c3_bytes_per_step(cfg, ctx):
+def weight_bytes(cfg, es=2):
     d, L, V = cfg.d_model, cfg.num_layers, cfg.vocab_size
-    weights = 2 * (L * (12 * d * d + 11 * d) + V * d + d)
-    kv_read = 2 * 2 * L * d * ctx
-    kv_write = 2 * 2 * L * d
-    return weights + kv_read + kv_write
+    return es * (L * (12 * d * d + 11 * d) + V * d + d)
 
 
-def cpu_baseline(cfg, w16, prompt, tokens=3):
-    """Reference algorithm on the host: fp32 (NumPy fp16 has no BLAS path)."""
-    from oracle import gpt_ref as R
+def kv_bytes(cfg, ctx, es=2):
+    """K/V read over `ctx` keys plus the new key/value written, all layers."""
+    return 2 * es * cfg.num_layers * cfg.d_model * (ctx + 1)
 
+
+def pmc_traffic():
+    """HBM bytes per decode launch from the committed PMC summary, if any."""
+    try:
+        text = open(PMC_SUMMARY).read()
+    except OSError:
+        return None
+    m = re.search(r"traffic_bytes_per_launch:\s*([0-9.]+)", text)
+    return float(m.group(1)) if m else None
+
+
+def cpu_threads():
     try:
         from threadpoolctl import threadpool_info
 
-        threads = max([i.get("num_threads", 1) for i in threadpool_info()] or [1])
+        return max([i.get("num_threads", 1) for i in threadpool_info()] or [1])
     except Exception:
-        threads = os.cpu_count() or 1
+        return os.cpu_count() or 1
+
+
+def cpu_baseline(cfg, w16, prompt, tokens):
+    """Reference algorithm on the host (oracle): fp32, full re-forward per token."""
+    from oracle import gpt_ref as R
+
     w = {k: v.astype(np.float32) for k, v in w16.items()}
     t0 = time.perf_counter()
     R.generate(w, prompt, cfg.num_heads, cfg.num_layers, max_new_tokens=tokens, temperature=0.0)
     dt = time.perf_counter() - t0
-    return {"value": round(tokens / dt, 4), "unit": "tokens/s", "cores": int(threads),
+    return {"value": round(tokens / dt, 4), "unit": "tokens/s", "cores": int(cpu_threads()),
             "kind": "port",
-            "sample": f"C3 shapes, fp32, batch 1, prompt {prompt.shape[1]}, {tokens} greedy tokens "
-                      f"by full re-forward per token as the reference does ({dt:.1f} s)"}
+            "sample": f"C3 shapes at fp32, batch 1, prompt {prompt.shape[1]}, {tokens} greedy tokens, "
+                      f"each a full re-forward as the reference does ({dt:.1f} s)"}
+
+
+def bench_c3(nm, cfg, model, prompt, n, steps, warmup, use_graph):
+    kw = dict(max_new_tokens=n, temperature=0.0, use_graph=use_graph)
+    for _ in range(warmup):
+        nm.generate(model, prompt, **kw)
+    nm._native.synchronize()
+    decode_ms = []
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        out = nm.generate(model, prompt, **kw)
+        decode_ms.append(model.last_decode_ms())
+    nm._native.synchronize()
+    elapsed = time.perf_counter() - t0
+    assert out.shape == (1, prompt.shape[1] + n)
+    ctxs = np.arange(prompt.shape[1] + 1, prompt.shape[1] + n)
+    bytes_avg = float(np.mean([weight_bytes(cfg) + kv_bytes(cfg, c) for c in ctxs]))
+    step_ms = float(np.mean(decode_ms))
+    return elapsed, step_ms, bytes_avg, model.last_decode_persistent()
+
+
+def bench_c4(nm, cfg, model, use_graph, reps=2):
+    rng = np.random.default_rng(5)
+    lens = rng.integers(128, 1025, 32)
+    rows = [rng.integers(0, cfg.vocab_size, int(n)) for n in lens]
+    new = 256
+    kw = dict(max_new_tokens=new, temperature=0.8, top_k=50, top_p=1.0, use_graph=use_graph)
+    np.random.seed(0)
+    nm.generate(model, rows, **kw)  # warm-up
+    nm._native.synchronize()
+    t0 = time.perf_counter()
+    decode_ms = []
+    for _ in range(reps):
+        np.random.seed(0)
+        nm.generate(model, rows, **kw)
+        decode_ms.append(model.last_decode_ms())
+    nm._native.synchronize()
+    elapsed = (time.perf_counter() - t0) / reps
+    # decode step s (1 … new-1) attends len_b + s keys in every row
+    bytes_steps = [weight_bytes(cfg) + sum(kv_bytes(cfg, int(n) + s - 1) for n in lens)
+                   for s in range(1, new)]
+    step_ms = float(np.mean(decode_ms))
+    achieved = float(np.mean(bytes_steps)) / (step_ms * 1e-3) / 1e9
+    return {"workload": "C4: same model, batch 32, prompts U[128,1024], 256 sampled tokens each "
+                        "(T=0.8, top-k 50, top_p 1.0)",
+            "value": round(32 * new / elapsed, 1), "unit": "tokens/s",
+            "ms_per_generate": round(elapsed * 1e3, 2), "decode_ms_per_step": round(step_ms, 4),
+            "roofline": {"bound": "hbm", "kernel": "decode step (all kernels of one token)",
+                         "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                         "frac": round(achieved / HBM_PEAK_GBS, 4)}}
+
+
+def bench_c5(nm, reps=2):
+    from oracle.weights import C5, make_weights, random_ids
+
+    cfg = C5
+    w = make_weights(cfg, seed=7, dtype=np.float16)
+    model = nm.GPT.from_arrays(w, cfg.vocab_size, cfg.d_model, cfg.num_heads, cfg.num_layers,
+                               cfg.max_seq_len, dtype=np.float16)
+    del w
+    model.to_device()
+    ids = random_ids((4, 4096), cfg.vocab_size, seed=1)
+    lab = random_ids((4, 4096), cfg.vocab_size, seed=2)
+    model.compute_loss(ids, lab)  # warm-up
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        loss = model.compute_loss(ids, lab).item()
+    dt = (time.perf_counter() - t0) / reps
+    d, L, V, B, S = cfg.d_model, cfg.num_layers, cfg.vocab_size, 4, 4096
+    flops = 2 * B * S * L * 12 * d * d + L * B * 4 * d * S * (S + 1) / 2 + 2 * B * S * d * V
+    tf = flops / dt / 1e12
+    return {"workload": "C5: GPT V50304 d2048 H16 L24 fp16, 4x4096 causal prefill + tied "
+                        "cross-entropy over 16384 positions (compute_loss)",
+            "value": round(B * S / dt, 1), "unit": "positions/s", "seconds": round(dt, 4),
+            "loss": round(float(loss), 5),
+            "roofline": {"bound": "mfma", "achieved": round(tf, 1), "peak": MFMA_F16_PEAK_TFLOPS,
+                         "unit": "TFLOP/s", "frac": round(tf / MFMA_F16_PEAK_TFLOPS, 4),
+                         "flops": flops}}
 
 
 def main():
@@ -68,68 +172,63 @@ def main():
     ap.add_argument("--prompt", type=int, default=512)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-graph", action="store_true")
+    ap.add_argument("--only-c3", action="store_true", help="skip the batch-32 and prefill lines")
+    ap.add_argument("--cpu-tokens", type=int, default=12)
     args = ap.parse_args()
     if args.gpus != 1:
-        print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported (this path does "
-              f"not shard across GPUs)", file=sys.stderr)
+        print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported: this path does "
+              f"not shard across GPUs (the sharding design is described in DESIGN.md)",
+              file=sys.stderr)
         sys.exit(2)
 
     import nimbleml_amd as nm
-    from nimbleml_amd import _native as N
     from oracle.weights import C3, make_weights, random_ids
 
     cfg = C3
-    N.ensure_init()
+    nm._native.ensure_init()
     w16 = make_weights(cfg, seed=1234, dtype=np.float16)
     model = nm.GPT.from_arrays(w16, cfg.vocab_size, cfg.d_model, cfg.num_heads, cfg.num_layers,
                                cfg.max_seq_len, dtype=np.float16)
     model.to_device()
     prompt = random_ids((1, args.prompt), cfg.vocab_size, seed=99)
     n = args.new_tokens
-    kw = dict(max_new_tokens=n, temperature=0.0, use_graph=not args.no_graph)
+    use_graph = not args.no_graph
 
-    for _ in range(args.warmup):
-        nm.generate(model, prompt, **kw)
-    N.synchronize()
-    decode_ms = []
-    t0 = time.perf_counter()
-    for _ in range(args.steps):
-        out = nm.generate(model, prompt, **kw)
-        decode_ms.append(model.last_decode_ms())
-    N.synchronize()
-    elapsed = time.perf_counter() - t0
-    assert out.shape == (1, args.prompt + n)
-
-    ms_per_step = 1000.0 * elapsed / args.steps
-    value = args.steps * n / elapsed
-    ctxs = np.arange(args.prompt + 1, args.prompt + n)  # attention lengths of the decode steps
-    bytes_avg = float(np.mean([c3_bytes_per_step(cfg, c) for c in ctxs]))
-    step_ms = float(np.mean(decode_ms))
+    elapsed, step_ms, bytes_avg, persistent = bench_c3(nm, cfg, model, prompt, n, args.steps,
+                                                       args.warmup, use_graph)
     achieved = bytes_avg / (step_ms * 1e-3) / 1e9
+    traffic = pmc_traffic() if persistent else None
     result = {
         "metric": METRIC,
-        "value": round(value, 2),
+        "value": round(args.steps * n / elapsed, 2),
         "unit": "tokens/s",
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
-        "ms_per_step": round(ms_per_step, 3),
+        "ms_per_step": round(1000.0 * elapsed / args.steps, 3),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "fp16",
         "data": "synthetic (seeded N(0,0.02) weights, uniform prompt ids)",
-        "config": {"workload": f"C3 decode: GPT V32000 d1024 H16 L24 fp16, batch 1, prompt "
-                               f"{args.prompt}, greedy {n} new tokens",
+        "config": {"workload": f"C3: GPT V32000 d1024 H16 L24 fp16, batch 1, prompt {args.prompt}, "
+                               f"greedy {n} new tokens; one step = one generate() call",
                    "global_batch": 1, "seq_len": args.prompt + n, "parallelism": "none"},
         "decode_ms_per_token": round(step_ms, 4),
-        "roofline": {"bound": "hbm", "kernel": "decode step (embed … sample)",
+        "roofline": {"bound": "hbm",
+                     "kernel": "decode_persist_kernel (one launch per token)" if persistent
+                     else "decode step (all kernels of one token)",
                      "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
-                     "bytes_per_step": round(bytes_avg)},
+                     "frac": round(achieved / HBM_PEAK_GBS, 4),
+                     "traffic": round(traffic) if traffic else None,
+                     "bytes_per_launch": round(bytes_avg)},
     }
+    if not args.only_c3:
+        result["c4"] = bench_c4(nm, cfg, model, use_graph)
+        del model
+        result["c5"] = bench_c5(nm)
     if not args.no_cpu_baseline:
-        result["cpu_baseline"] = cpu_baseline(cfg, w16, prompt)
+        result["cpu_baseline"] = cpu_baseline(cfg, w16, prompt, args.cpu_tokens)
     print(json.dumps(result), flush=True)
 
 
