@@ -296,7 +296,9 @@ __global__ __launch_bounds__(64) void attn_combine_kernel(AttnArgs a, const int3
 //                Sᵀ registers: B's k-slot j of lane l is key 8(j/4) + 4(l/32) + j%4 of
 //                the 16-key block, and A is read with the same key order;
 // so each lane owns one query's output column: the α rescale and the final 1/Σp
-// need no data exchange. Key tiles past a wave's last query are skipped.
+// need no data exchange. Key tiles past a wave's last query are skipped; the next
+// tile's K/V are loaded into registers while the current one is multiplied; query
+// tiles are dispatched last-first (the causal walk is longest for them).
 constexpr int kFQ = 128, kFK = 64;
 
 template <int DK>
@@ -307,10 +309,19 @@ __global__ __launch_bounds__(256) void attn_prefill_mfma_kernel(AttnArgs a) {
   __shared__ half_t Ks[kFK][DK + 8];
   __shared__ half_t Vt[DK][kFK + 8];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int bh = blockIdx.y;
+  // Workgroup n runs on XCD n % 8. Give all query tiles of one (row, head) to one XCD,
+  // one after another, so that head's K/V stay in that XCD's L2.
+  const int nq = gridDim.x;
+  int bh = blockIdx.y, qt = blockIdx.x;
+  if (gridDim.y % 8 == 0) {
+    const int n = blockIdx.x + blockIdx.y * nq;
+    const int slot = n >> 3;
+    bh = (n & 7) + 8 * (slot / nq);
+    qt = slot % nq;
+  }
   const int b = bh / a.H, h = bh - (bh / a.H) * a.H;
   const int S = a.S;
-  const int q0 = blockIdx.x * kFQ;
+  const int q0 = (nq - 1 - qt) * kFQ;
   const int base = a.pos_base ? a.pos_base[b] : 0;
   const half_t* __restrict__ Kg = static_cast<const half_t*>(a.k) + b * a.kv_stride_b + h * a.kv_stride_h;
   const half_t* __restrict__ Vg = static_cast<const half_t*>(a.v) + b * a.kv_stride_b + h * a.kv_stride_h;
@@ -335,21 +346,54 @@ __global__ __launch_bounds__(256) void attn_prefill_mfma_kernel(AttnArgs a) {
 #pragma unroll
     for (int r = 0; r < 16; ++r) o[t][r] = 0.f;
 
+  // Per tile each thread holds CH 16-byte pieces of K (key-major) and CH of V. The V
+  // pieces come as key pairs (keys 2p, 2p+1 of the same 8 dims, p = tid % 32) so the
+  // transposed store is one 4-byte word per dim, 32 lanes covering a contiguous
+  // 128-byte row segment of Vt: no bank conflicts.
+  constexpr int CH = kFK * DK / 8 / 256;
+  constexpr int VG = DK / 8;                  // 8-dim groups of a key
+  half8 kn[CH], vn[CH];
+  auto fetch = [&](int k0) {
+#pragma unroll
+    for (int i = 0; i < CH; ++i) {
+      const int c = tid + 256 * i;
+      const int key = c / VG, d8 = (c % VG) * 8;
+      const bool ok = k0 + key < kend;
+      kn[i] = ok ? *reinterpret_cast<const half8*>(Kg + static_cast<long long>(k0 + key) * DK + d8) : z8;
+    }
+#pragma unroll
+    for (int i = 0; i < CH / 2; ++i) {
+      const int grp = (tid >> 5) + 8 * i;     // 8-dim group
+      const int key = 2 * (tid & 31);
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        const bool ok = k0 + key + u < kend;
+        vn[2 * i + u] = ok ? *reinterpret_cast<const half8*>(Vg + static_cast<long long>(k0 + key + u) * DK + grp * 8)
+                           : z8;
+      }
+    }
+  };
+  fetch(0);
   for (int k0 = 0; k0 < kend; k0 += kFK) {
     __syncthreads();
-    constexpr int CH = kFK * DK / 8;  // 16-byte pieces per tile
 #pragma unroll
-    for (int i = 0; i < CH / 256; ++i) {
+    for (int i = 0; i < CH; ++i) {
       const int c = tid + 256 * i;
-      const int key = c / (DK / 8), d8 = (c % (DK / 8)) * 8;
-      const bool ok = k0 + key < kend;
-      const half8 kv = ok ? *reinterpret_cast<const half8*>(Kg + static_cast<long long>(k0 + key) * DK + d8) : z8;
-      const half8 vv = ok ? *reinterpret_cast<const half8*>(Vg + static_cast<long long>(k0 + key) * DK + d8) : z8;
-      *reinterpret_cast<half8*>(&Ks[key][d8]) = kv;
+      const int key = c / VG, d8 = (c % VG) * 8;
+      *reinterpret_cast<half8*>(&Ks[key][d8]) = kn[i];
+    }
 #pragma unroll
-      for (int e = 0; e < 8; ++e) Vt[d8 + e][key] = vv[e];
+    for (int i = 0; i < CH / 2; ++i) {
+      const int grp = (tid >> 5) + 8 * i, key = 2 * (tid & 31);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        typedef _Float16 half2v __attribute__((ext_vector_type(2)));
+        const half2v pr = {vn[2 * i][e], vn[2 * i + 1][e]};
+        *reinterpret_cast<half2v*>(&Vt[grp * 8 + e][key]) = pr;
+      }
     }
     __syncthreads();
+    if (k0 + kFK < kend) fetch(k0 + kFK);
     if (k0 > wave_last) continue;  // every key of this tile is after this wave's queries
     floatx16 st[2];
 #pragma unroll
@@ -368,13 +412,14 @@ __global__ __launch_bounds__(256) void attn_prefill_mfma_kernel(AttnArgs a) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const int key = k0 + t * 32 + 8 * (r >> 2) + 4 * hi + (r & 3);
-        const float s = (key <= qpos && key < kend) ? rnd<half_t>(rnd<half_t>(st[t][r]) / scale_t)
-                                                    : -INFINITY;
+        const float sv = rnd<half_t>(rnd<half_t>(st[t][r]) / scale_t);
+        const float s = (key <= qpos && key < kend) ? sv : -INFINITY;
         st[t][r] = s;
         mx = fmaxf(mx, s);
       }
     mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-    const float alpha = (mx == -INFINITY) ? 1.f : expf(m - mx);
+    constexpr float kLog2e = 1.4426950408889634f;
+    const float alpha = (mx == -INFINITY) ? 1.f : __builtin_amdgcn_exp2f((m - mx) * kLog2e);
     l *= alpha;
 #pragma unroll
     for (int t = 0; t < OT; ++t)
@@ -388,7 +433,7 @@ __global__ __launch_bounds__(256) void attn_prefill_mfma_kernel(AttnArgs a) {
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
           const float s = st[t][8 * kb + j];
-          const float p = (s == -INFINITY) ? 0.f : expf(s - mx);
+          const float p = (s == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f((s - mx) * kLog2e);
           l += p;
           pb[j] = static_cast<half_t>(p);
         }
