@@ -140,7 +140,7 @@ __device__ __forceinline__ void gather(const u64* slots, uint32_t tag, T* dst, i
 }
 
 __device__ __forceinline__ float block_sum4(float v, float* red) {
-  v = wave_sum(v);
+  v = wave_sum_dpp(v);
   __syncthreads();
   if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
   __syncthreads();
@@ -148,7 +148,7 @@ __device__ __forceinline__ float block_sum4(float v, float* red) {
 }
 
 __device__ __forceinline__ float block_max4(float v, float* red) {
-  v = wave_max(v);
+  v = wave_max_dpp(v);
   __syncthreads();
   if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
   __syncthreads();
@@ -363,7 +363,7 @@ __global__ __launch_bounds__(kT) void decode_persist_kernel(PersistArgs a) {
       rmsnorm_lds<T, D>(s_x, gam, s_xn, s_red);
 #pragma unroll
       for (int i = 0; i < RW_QKV; ++i) {
-        const float acc = wave_sum(dot_slice<T, D>(w[i], s_xn));
+        const float acc = wave_sum_dpp(dot_slice<T, D>(w[i], s_xn));
         if (lane == 0 && rs.live[i]) {
           const float lin = rnd<T>(rnd<T>(acc) + static_cast<float>(braw[i]));
           const int r = rs.row[i];
@@ -420,8 +420,7 @@ __global__ __launch_bounds__(kT) void decode_persist_kernel(PersistArgs a) {
 #pragma unroll
           for (int e = 0; e < DPT; ++e) dot += s_q[qq * DPT + e] * at8<T>(kr[e / 8], e % 8);
         }
-        dot += __shfl_xor(dot, 1, 64);
-        dot += __shfl_xor(dot, 2, 64);
+        dot = quad_sum_dpp(dot);
         const float sc = kvalid ? rnd<T>(rnd<T>(dot) / scale_t) : -INFINITY;
         const float mc = block_max4(sc, s_red);
         const float p = kvalid ? expf(sc - mc) : 0.f;
@@ -511,7 +510,7 @@ __global__ __launch_bounds__(kT) void decode_persist_kernel(PersistArgs a) {
       NML_MARK(mk + 6);
 #pragma unroll
       for (int i = 0; i < RW_WO; ++i) {
-        const float acc = wave_sum(dot_slice<T, D>(w[i], s_xn));
+        const float acc = wave_sum_dpp(dot_slice<T, D>(w[i], s_xn));
         if (lane == 0 && rs.live[i]) {
           const float lin = rnd<T>(rnd<T>(acc) + static_cast<float>(braw[i]));
           put(XM + rs.row[i], tg + 4, enc<T>(static_cast<float>(s_x[rs.row[i]]) + lin));
@@ -546,7 +545,7 @@ __global__ __launch_bounds__(kT) void decode_persist_kernel(PersistArgs a) {
       rmsnorm_lds<T, D>(s_xm, gam, s_xn, s_red);
 #pragma unroll
       for (int i = 0; i < RW_W1; ++i) {
-        const float acc = wave_sum(dot_slice<T, D>(w[i], s_xn));
+        const float acc = wave_sum_dpp(dot_slice<T, D>(w[i], s_xn));
         if (lane == 0 && rs.live[i]) {
           const float lin = rnd<T>(rnd<T>(acc) + static_cast<float>(braw[i]));
           put(HID + rs.row[i], tg + 5, enc<T>(gelu_t<T>(lin)));
@@ -573,7 +572,7 @@ __global__ __launch_bounds__(kT) void decode_persist_kernel(PersistArgs a) {
       NML_MARK(mk + 8);
 #pragma unroll
       for (int i = 0; i < RW_W2; ++i) {
-        const float acc = wave_sum(dot_slice<T, F>(w[i], s_h));
+        const float acc = wave_sum_dpp(dot_slice<T, F>(w[i], s_h));
         if (lane == 0 && rs.live[i]) {
           const float lin = rnd<T>(rnd<T>(acc) + static_cast<float>(braw[i]));
           put(X + rs.row[i], tg + 8, enc<T>(static_cast<float>(s_xm[rs.row[i]]) + lin));
@@ -616,7 +615,7 @@ __global__ __launch_bounds__(kT) void decode_persist_kernel(PersistArgs a) {
     for (int i = 0; i < HR; ++i) load_row<T, D>(E, rn + i < r1 ? rn + i : r0, nxt[i]);
 #pragma unroll
     for (int i = 0; i < HR; ++i) {
-      const float acc = wave_sum(dot_slice<T, D>(cur[i], s_xn));
+      const float acc = wave_sum_dpp(dot_slice<T, D>(cur[i], s_xn));
       const float v = rnd<T>(acc);
       if (rb + i < r1) {
         if (lane == 0) logits[rb + i] = static_cast<T>(v);
