@@ -39,6 +39,26 @@ constexpr int kXcd = 8;
 constexpr int kChunk = 64;          // keys per attention work item
 constexpr int kMaxCh = kPersistMaxLen / kChunk;
 constexpr unsigned kSpinLimit = 1u << 19;
+constexpr int kLine = 16;           // 64-bit slots per 128-byte line
+
+// Exchange-slot regions, in 64-bit slots. Each producing workgroup's slots start on a
+// line of their own: lines shared by producers make their write-through stores and
+// the consumers' polls of that line contend, which measured ~1.5x slower exchanges.
+template <int D, int DK>
+struct SlotLayout {
+  static constexpr int H = D / DK, TEAM = kG / H, F = 4 * D;
+  static constexpr int PCH = (DK + 2 + kLine - 1) / kLine * kLine;  // one chunk's partial
+  static constexpr int X = 0;                           // kG × line: D/kG values of x
+  static constexpr int QKV = X + kG * kLine;            // H·TEAM × line: QKV rows
+  static constexpr int ATT = QKV + H * TEAM * kLine;    // H × DK: attention output
+  static constexpr int XM = ATT + H * DK;               // kG × line: x_mid
+  static constexpr int HID = XM + kG * kLine;           // kG × line: F/kG values of h
+  static constexpr int PART = HID + kG * kLine;         // H·kMaxCh × PCH: chunk partials
+  static constexpr int ARG = PART + H * kMaxCh * PCH;   // kG × line: (best, index)
+  static constexpr int total = ARG + kG * kLine;
+  static_assert(D / kG <= kLine && F / kG <= kLine && 3 * DK / TEAM <= kLine, "lines");
+  static_assert(ATT % kLine == 0 && (DK / 2) % kLine == 0, "line-aligned heads");
+};
 
 typedef unsigned long long u64;
 
@@ -125,18 +145,133 @@ __device__ __forceinline__ void wait_slots(const u64* slots, const int (&idx)[N]
   for (int j = 0; j < N; ++j) out[j] = static_cast<uint32_t>(v[j]);
 }
 
-// dst[i] = payload of slots[i] for i < N (N a multiple of kT).
-template <typename T, int N>
-__device__ __forceinline__ void gather(const u64* slots, uint32_t tag, T* dst, int* err,
-                                       int& bad) {
-  constexpr int PER = N / kT;
-  int idx[PER];
-  uint32_t p[PER];
+// v[j] = slot p[j·stride] once every one carries `tag` (same retry scheme).
+template <int N>
+__device__ __forceinline__ void poll_batch(const u64* p, int stride, uint32_t tag, u64 (&v)[N],
+                                           int* err, int& bad) {
 #pragma unroll
-  for (int j = 0; j < PER; ++j) idx[j] = threadIdx.x + j * kT;
-  wait_slots<PER>(slots, idx, tag, p, err, bad);
+  for (int j = 0; j < N; ++j) v[j] = peek(p + stride * j);
+  for (unsigned spins = 0;; ++spins) {
+    bool all = true;
 #pragma unroll
-  for (int j = 0; j < PER; ++j) dst[threadIdx.x + j * kT] = dec<T>(p[j]);
+    for (int j = 0; j < N; ++j) all = all && static_cast<uint32_t>(v[j] >> 32) == tag;
+    if (all || bad) break;
+    if (give_up(spins, err, bad)) break;
+    __builtin_amdgcn_s_sleep(1);
+#pragma unroll
+    for (int j = 0; j < N; ++j) v[j] = peek(p + stride * j);
+  }
+}
+
+// Values per exchange slot for the FFN hidden vector and the attention output: two
+// fp16 values share one 32-bit payload (element 2k in the low half), fp32 takes one.
+template <typename T>
+constexpr int kPack = sizeof(T) == 2 ? 2 : 1;
+
+template <typename T>
+__device__ __forceinline__ uint32_t pack(float v0, float v1);
+template <>
+__device__ __forceinline__ uint32_t pack<float>(float v0, float) { return __float_as_uint(v0); }
+template <>
+__device__ __forceinline__ uint32_t pack<half_t>(float v0, float v1) {
+  return enc<half_t>(v0) | (enc<half_t>(v1) << 16);
+}
+
+// Producer side: values v0, v1 of rows r, r+1 (r even) of a packed region.
+template <typename T>
+__device__ __forceinline__ void put_pair(u64* region, int r, uint32_t tag, float v0, float v1) {
+  if constexpr (kPack<T> == 2) {
+    put(region + r / 2, tag, pack<T>(v0, v1));
+  } else {
+    put(region + r, tag, pack<T>(v0, 0.f));
+    put(region + r + 1, tag, pack<T>(v1, 0.f));
+  }
+}
+
+// Store one slot payload (PK values) as element e of dst (LDS).
+template <typename T, int PK>
+__device__ __forceinline__ void sink_payload(T* dst, int e, uint32_t p) {
+  if constexpr (PK == 2 || sizeof(T) == 4)
+    reinterpret_cast<uint32_t*>(dst)[e / PK] = p;  // raw packed / fp32 payload
+  else
+    dst[e] = dec<T>(p);
+}
+
+// dst[0..N) from N / PK contiguous slots (a region whose producers own whole lines);
+// thread t takes slots t, t+kT, ….
+template <typename T, int N, int PK>
+__device__ __forceinline__ void gather(const u64* slots, uint32_t tag, T* dst, int* err, int& bad) {
+  constexpr int PER = N / PK / kT;
+  static_assert(PER * PK * kT == N, "gather shape");
+  u64 v[PER];
+  poll_batch<PER>(slots + threadIdx.x, kT, tag, v, err, bad);
+#pragma unroll
+  for (int j = 0; j < PER; ++j)
+    sink_payload<T, PK>(dst, (threadIdx.x + kT * j) * PK, static_cast<uint32_t>(v[j]));
+}
+
+// dst[0..NPROD·VP) from a region where producer p keeps its VP values in SP = VP / PK
+// slots at p·kLine + s. Thread t takes slot t % SP of producers t / SP, t / SP + kT/SP,
+// …, so each wave's load instruction reads 64/SP whole producer lines.
+template <typename T, int NPROD, int VP, int PK>
+__device__ __forceinline__ void gather_lines(const u64* region, uint32_t tag, T* dst, int* err,
+                                             int& bad) {
+  constexpr int SP = VP / PK;
+  static_assert(SP <= kLine && 64 % SP == 0, "slots per producer");
+  constexpr int PPR = kT / SP;  // producers per round of the block's threads
+  constexpr int PER = NPROD / PPR;
+  static_assert(NPROD % PPR == 0, "gather shape");
+  const int sl = threadIdx.x % SP, pq = threadIdx.x / SP;
+  u64 v[PER];
+  poll_batch<PER>(region + pq * kLine + sl, PPR * kLine, tag, v, err, bad);
+#pragma unroll
+  for (int j = 0; j < PER; ++j)
+    sink_payload<T, PK>(dst, (pq + PPR * j) * VP + sl * PK, static_cast<uint32_t>(v[j]));
+}
+
+// The chunk partials of one head (chunks c < nch; at slot c·PCH + k: the chunk's max
+// (k = 0), sum (1) and DK weighted value sums (2…)) into dst[c·(DK+2) + k]. Wave w
+// takes chunks w, w+4, …; its lane l waits for value sum l of each, lanes 0 and 1 also
+// for the max and the sum; 8 chunks per wave per round.
+template <int DK, int PCH>
+__device__ __forceinline__ void gather_partials(const u64* src, int nch, uint32_t tag, float* dst,
+                                                int* err, int& bad) {
+  static_assert(DK == 64 && kT == 256, "one lane per value sum, four waves");
+  const int w = threadIdx.x >> 6, l = threadIdx.x & 63;
+  const u64 want = static_cast<u64>(tag) << 32;
+  for (int c0 = w; c0 < nch; c0 += 32) {
+    u64 v[8], m[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const int c = c0 + 4 * j;
+      v[j] = c < nch ? peek(src + c * PCH + 2 + l) : want;
+      m[j] = (c < nch && l < 2) ? peek(src + c * PCH + l) : want;
+    }
+    for (unsigned spins = 0;; ++spins) {
+      bool all = true;
+#pragma unroll
+      for (int j = 0; j < 8; ++j)
+        all = all && static_cast<uint32_t>(v[j] >> 32) == tag &&
+              static_cast<uint32_t>(m[j] >> 32) == tag;
+      if (all || bad) break;
+      if (give_up(spins, err, bad)) break;
+      __builtin_amdgcn_s_sleep(1);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const int c = c0 + 4 * j;
+        v[j] = c < nch ? peek(src + c * PCH + 2 + l) : want;
+        m[j] = (c < nch && l < 2) ? peek(src + c * PCH + l) : want;
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const int c = c0 + 4 * j;
+      if (c < nch) {
+        dst[c * (DK + 2) + 2 + l] = __uint_as_float(static_cast<uint32_t>(v[j]));
+        if (l < 2) dst[c * (DK + 2) + l] = __uint_as_float(static_cast<uint32_t>(m[j]));
+      }
+    }
+  }
 }
 
 __device__ __forceinline__ float block_sum4(float v, float* red) {
@@ -271,6 +406,8 @@ __global__ __launch_bounds__(kT) void decode_persist_kernel(PersistArgs a) {
   constexpr int NPART = (kMaxCh * (DK + 2) + kT - 1) / kT;
   static_assert(H % kXcd == 0 && kG % H == 0 && (3 * DK) % TEAM == 0, "head teams");
   static_assert(D % kT == 0 && F % kT == 0 && D % kG == 0, "shapes");
+  static_assert(R_QKV == 4 * RW_QKV && R_WO == 4 && R_W2 == 4 && R_W1 == 4 * RW_W1 && RW_W1 % 2 == 0,
+                "every wave owns whole rows (and W1 row pairs) of every phase");
   static_assert(DK % 32 == 0 && DK <= 128 && 3 * DK <= kT, "head dim");
 
   __shared__ __attribute__((aligned(16))) T s_x[D];   // x of the layer
@@ -297,13 +434,14 @@ __global__ __launch_bounds__(kT) void decode_persist_kernel(PersistArgs a) {
   const long long LB = a.layer_bytes;
 
   // slot regions
-  u64* X = slots;
-  u64* QKV = slots + D;
-  u64* ATT = slots + 4 * D;
-  u64* XM = slots + 5 * D;
-  u64* HID = slots + 6 * D;
-  u64* PART = slots + 6 * D + F;
-  u64* ARG = PART + H * kMaxCh * (DK + 2);
+  typedef SlotLayout<D, DK> SL;
+  u64* X = slots + SL::X;
+  u64* QKV = slots + SL::QKV;
+  u64* ATT = slots + SL::ATT;
+  u64* XM = slots + SL::XM;
+  u64* HID = slots + SL::HID;
+  u64* PART = slots + SL::PART;
+  u64* ARG = slots + SL::ARG;
 
   // head team of this workgroup
   const int xcd = g % kXcd, kk = g / kXcd;
@@ -353,7 +491,7 @@ __global__ __launch_bounds__(kT) void decode_persist_kernel(PersistArgs a) {
       for (int j = 0; j < D / kT; ++j) graw[j] = G1[tid + j * kT];
       NML_MARK(mk + 0);
       if (l > 0) {
-        gather<T, D>(X, tg, s_x, err, bad);
+        gather_lines<T, kG, R_W2, 1>(X, tg, s_x, err, bad);
         __syncthreads();
       }
       NML_MARK(mk + 1);
@@ -367,7 +505,7 @@ __global__ __launch_bounds__(kT) void decode_persist_kernel(PersistArgs a) {
         if (lane == 0 && rs.live[i]) {
           const float lin = rnd<T>(rnd<T>(acc) + static_cast<float>(braw[i]));
           const int r = rs.row[i];
-          put(QKV + r, tg + 1, enc<T>(lin));
+          put(QKV + (head * TEAM + tm) * kLine + wave + 4 * i, tg + 1, enc<T>(lin));
           const int part = r / D, j = r % DK;
           if (part > 0) {
             T* cache = static_cast<T*>(part == 1 ? a.kc : a.vc);
@@ -403,8 +541,10 @@ __global__ __launch_bounds__(kT) void decode_persist_kernel(PersistArgs a) {
         if (first) {  // q, and k/v of the new position for the workgroup that owns it
           int idx[1];
           uint32_t pv[1];
-          const int part = tid / DK, j = tid % DK;
-          idx[0] = (tid < DK || (owns_new && tid < 3 * DK)) ? part * D + head * DK + j : -1;
+          const int part = tid / DK, j = tid % DK;  // tid = row within the head's 3·DK
+          idx[0] = (tid < DK || (owns_new && tid < 3 * DK))
+                       ? (head * TEAM + tid / R_QKV) * kLine + tid % R_QKV
+                       : -1;
           wait_slots<1>(QKV, idx, tg + 1, pv, err, bad);
           if (idx[0] >= 0) (part == 0 ? s_q : part == 1 ? s_kn : s_vn)[j] = static_cast<float>(dec<T>(pv[0]));
           first = false;
@@ -447,7 +587,7 @@ __global__ __launch_bounds__(kT) void decode_persist_kernel(PersistArgs a) {
 #pragma unroll
         for (int e = 0; e < 8; ++e) s_o[ks][dg * 8 + e] = o[e];
         __syncthreads();
-        u64* dst = PART + (static_cast<long long>(head) * kMaxCh + c) * (DK + 2);
+        u64* dst = PART + (static_cast<long long>(head) * kMaxCh + c) * SL::PCH;
         if (tid < DK) {
           float s = 0.f;
           for (int k2 = 0; k2 < NKS; ++k2) s += s_o[k2][tid];
@@ -462,19 +602,8 @@ __global__ __launch_bounds__(kT) void decode_persist_kernel(PersistArgs a) {
     }
     // ------------------------------------------------------------------ P2b
     if (tm == 0) {
-      const int n = nch * (DK + 2);
-      const u64* src = PART + static_cast<long long>(head) * kMaxCh * (DK + 2);
-      int idx[NPART];
-      uint32_t pv[NPART];
-#pragma unroll
-      for (int j = 0; j < NPART; ++j) {
-        const int i = tid + j * kT;
-        idx[j] = i < n ? i : -1;
-      }
-      wait_slots<NPART>(src, idx, tg + 2, pv, err, bad);
-#pragma unroll
-      for (int j = 0; j < NPART; ++j)
-        if (idx[j] >= 0) s_part[idx[j]] = __uint_as_float(pv[j]);
+      gather_partials<DK, SL::PCH>(PART + static_cast<long long>(head) * kMaxCh * SL::PCH, nch,
+                                   tg + 2, s_part, err, bad);
       __syncthreads();
       if (tid < DK) {
         float M = -INFINITY;
@@ -485,7 +614,9 @@ __global__ __launch_bounds__(kT) void decode_persist_kernel(PersistArgs a) {
           den += e * s_part[c * (DK + 2) + 1];
           num += e * s_part[c * (DK + 2) + 2 + tid];
         }
-        put(ATT + head * DK + tid, tg + 3, enc<T>(num * (1.f / den)));
+        const float o = num * (1.f / den);
+        const float o1 = __shfl_xor(o, 1, 64);  // dims 2k, 2k+1 share a slot
+        if ((tid & 1) == 0) put_pair<T>(ATT + head * (DK / kPack<T>), tid, tg + 3, o, o1);
       }
       NML_MARK(mk + 5);
     }
@@ -505,7 +636,7 @@ __global__ __launch_bounds__(kT) void decode_persist_kernel(PersistArgs a) {
         braw[i] = Bo[rs.row[i]];
       }
       __syncthreads();  // s_xn is reused for the attention output
-      gather<T, D>(ATT, tg + 3, s_xn, err, bad);
+      gather<T, D, kPack<T>>(ATT, tg + 3, s_xn, err, bad);
       __syncthreads();
       NML_MARK(mk + 6);
 #pragma unroll
@@ -513,7 +644,8 @@ __global__ __launch_bounds__(kT) void decode_persist_kernel(PersistArgs a) {
         const float acc = wave_sum_dpp(dot_slice<T, D>(w[i], s_xn));
         if (lane == 0 && rs.live[i]) {
           const float lin = rnd<T>(rnd<T>(acc) + static_cast<float>(braw[i]));
-          put(XM + rs.row[i], tg + 4, enc<T>(static_cast<float>(s_x[rs.row[i]]) + lin));
+          put(XM + g * kLine + wave + 4 * i, tg + 4,
+              enc<T>(static_cast<float>(s_x[rs.row[i]]) + lin));
         }
       }
     }
@@ -525,18 +657,18 @@ __global__ __launch_bounds__(kT) void decode_persist_kernel(PersistArgs a) {
       RowSlice<T, D> w[RW_W1];
       RowSet<RW_W1> rs;
       T braw[RW_W1];
+      // row pairs (2k, 2k+1), k = wave, wave+4, …: one slot of h carries both
 #pragma unroll
       for (int i = 0; i < RW_W1; ++i) {
-        const int rl = wave + 4 * i;
-        rs.live[i] = rl < R_W1;
-        rs.row[i] = g * R_W1 + (rs.live[i] ? rl : 0);
+        rs.live[i] = true;
+        rs.row[i] = g * R_W1 + 2 * (wave + 4 * (i >> 1)) + (i & 1);
         load_row<T, D>(W, rs.row[i], w[i]);
         braw[i] = B1[rs.row[i]];
       }
       T graw[D / kT];
 #pragma unroll
       for (int j = 0; j < D / kT; ++j) graw[j] = G2[tid + j * kT];
-      gather<T, D>(XM, tg + 4, s_xm, err, bad);
+      gather_lines<T, kG, R_WO, 1>(XM, tg + 4, s_xm, err, bad);
       __syncthreads();
       NML_MARK(mk + 7);
       float gam[D / kT];
@@ -544,12 +676,14 @@ __global__ __launch_bounds__(kT) void decode_persist_kernel(PersistArgs a) {
       for (int j = 0; j < D / kT; ++j) gam[j] = static_cast<float>(graw[j]);
       rmsnorm_lds<T, D>(s_xm, gam, s_xn, s_red);
 #pragma unroll
-      for (int i = 0; i < RW_W1; ++i) {
-        const float acc = wave_sum_dpp(dot_slice<T, D>(w[i], s_xn));
-        if (lane == 0 && rs.live[i]) {
-          const float lin = rnd<T>(rnd<T>(acc) + static_cast<float>(braw[i]));
-          put(HID + rs.row[i], tg + 5, enc<T>(gelu_t<T>(lin)));
+      for (int i = 0; i < RW_W1; i += 2) {
+        float v[2];
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          const float acc = wave_sum_dpp(dot_slice<T, D>(w[i + h], s_xn));
+          v[h] = gelu_t<T>(rnd<T>(rnd<T>(acc) + static_cast<float>(braw[i + h])));
         }
+        if (lane == 0) put_pair<T>(HID + g * kLine, rs.row[i] - g * R_W1, tg + 5, v[0], v[1]);
       }
     }
     // ------------------------------------------------------------------ P5
@@ -567,7 +701,7 @@ __global__ __launch_bounds__(kT) void decode_persist_kernel(PersistArgs a) {
         load_row<T, F>(W, rs.row[i], w[i]);
         braw[i] = B2[rs.row[i]];
       }
-      gather<T, F>(HID, tg + 5, s_h, err, bad);
+      gather_lines<T, kG, R_W1, kPack<T>>(HID, tg + 5, s_h, err, bad);
       __syncthreads();
       NML_MARK(mk + 8);
 #pragma unroll
@@ -575,7 +709,8 @@ __global__ __launch_bounds__(kT) void decode_persist_kernel(PersistArgs a) {
         const float acc = wave_sum_dpp(dot_slice<T, F>(w[i], s_h));
         if (lane == 0 && rs.live[i]) {
           const float lin = rnd<T>(rnd<T>(acc) + static_cast<float>(braw[i]));
-          put(X + rs.row[i], tg + 8, enc<T>(static_cast<float>(s_xm[rs.row[i]]) + lin));
+          put(X + g * kLine + wave + 4 * i, tg + 8,
+              enc<T>(static_cast<float>(s_xm[rs.row[i]]) + lin));
         }
       }
       NML_MARK(mk + 9);
@@ -597,7 +732,7 @@ __global__ __launch_bounds__(kT) void decode_persist_kernel(PersistArgs a) {
     T graw[D / kT];
 #pragma unroll
     for (int j = 0; j < D / kT; ++j) graw[j] = static_cast<const T*>(a.lnf)[tid + j * kT];
-    gather<T, D>(X, tgh, s_x, err, bad);
+    gather_lines<T, kG, R_W2, 1>(X, tgh, s_x, err, bad);
     __syncthreads();
     NML_MARK(mh + 0);
     float gam[D / kT];
@@ -642,12 +777,12 @@ __global__ __launch_bounds__(kT) void decode_persist_kernel(PersistArgs a) {
         bb = s_red[w2];
         ii = s_redi[w2];
       }
-    put(ARG + 2 * g, tgh + 1, __float_as_uint(bb));
-    put(ARG + 2 * g + 1, tgh + 1, static_cast<uint32_t>(ii));
+    put(ARG + g * kLine, tgh + 1, __float_as_uint(bb));
+    put(ARG + g * kLine + 1, tgh + 1, static_cast<uint32_t>(ii));
   }
   if (g == 0) {
     __syncthreads();
-    int idx[2] = {2 * tid, 2 * tid + 1};
+    int idx[2] = {tid * kLine, tid * kLine + 1};
     uint32_t pv[2];
     wait_slots<2>(ARG, idx, tgh + 1, pv, err, bad);
     float b = __uint_as_float(pv[0]);
@@ -715,8 +850,10 @@ bool persist_supported(int dt, int d, int H, int F, int B, int P) {
 }
 
 size_t persist_slot_count(int d, int H) {
-  const int dk = d / H, F = 4 * d;
-  return static_cast<size_t>(6 * d + F) + static_cast<size_t>(H) * kMaxCh * (dk + 2) + 2 * kG;
+  // the persistent kernel exists for d = 1024, head dim 64 only (persist_supported)
+  (void)d;
+  (void)H;
+  return SlotLayout<1024, 64>::total;
 }
 
 int launch_decode_persist(int dt, int d, int H, const PersistArgs& a, hipStream_t st) {
