@@ -87,6 +87,14 @@ __device__ __forceinline__ float wave_max_dpp(float v) {
   return fmaxf(fmaxf(lane_f(v, 0), lane_f(v, 16)), fmaxf(lane_f(v, 32), lane_f(v, 48)));
 }
 
+// Sum over the 16 lanes of each row (lanes 16k..16k+15), the same value in every lane.
+__device__ __forceinline__ float row16_sum_dpp(float v) {
+  v += dpp_move<kDppXor1>(v);
+  v += dpp_move<kDppXor2>(v);
+  v += dpp_move<kDppHalfMirror>(v);
+  return v + dpp_move<kDppMirror>(v);
+}
+
 // Sum over the 4 lanes of each quad (lanes 4k..4k+3), in every lane of the quad.
 __device__ __forceinline__ float quad_sum_dpp(float v) {
   v += dpp_move<kDppXor1>(v);

@@ -45,7 +45,18 @@ struct LinearArgs {
   int M, N, K;
   int epi;
   QKVDst qkv;
+  // Decode fusion of RMSNorm into the fp16 skinny GEMM (linear_norm_fusable): x is
+  // normalised on load, gain norm_g (K values), from ssq_in = per-row sums of squares
+  // of x in 16-column pieces, laid out (M, K/16); and an EPI_BIAS_RESID GEMM writes
+  // the same sums of its output to ssq_out, (M, N/16). Null: not used.
+  const float* ssq_in;
+  const void* norm_g;
+  float norm_eps;
+  float* ssq_out;
 };
+
+// Whether launch_linear can fuse RMSNorm into this GEMM (ssq_in / ssq_out above).
+bool linear_norm_fusable(int dt, int M, int K, int N);
 
 int launch_linear(int dt, const LinearArgs& a, hipStream_t st);
 // Workspace of the split-K skinny GEMM (8 < M ≤ 64) for outputs up to max_n wide.

@@ -135,13 +135,15 @@ struct Acts {
   void* att; // (R, d) merged attention output
   void* h;   // (R, F) FFN hidden
   float* part;  // decode partials
+  float* ssq;   // decode: (Bdec, d/16) sums of squares of x in 16-column pieces
 };
 
 int acts_for(nml_model* m, int R, int Bdec, Acts* a) {
   const size_t rd = align256((size_t)R * m->d * m->es);
   const size_t rf = align256((size_t)R * m->F * m->es);
   const size_t part = Bdec ? align256(attention_decode_workspace(Bdec, m->H, m->dk, m->P)) : 0;
-  NML_TRY(m->ws.ensure(4 * rd + rf + part));
+  const size_t ssq = Bdec ? align256((size_t)Bdec * (m->d / 16 + 1) * sizeof(float)) : 0;
+  NML_TRY(m->ws.ensure(4 * rd + rf + part + ssq));
   char* b = static_cast<char*>(m->ws.p);
   a->x = b;
   a->xn = b + rd;
@@ -149,6 +151,7 @@ int acts_for(nml_model* m, int R, int Bdec, Acts* a) {
   a->att = b + 3 * rd;
   a->h = b + 4 * rd;
   a->part = part ? reinterpret_cast<float*>(b + 4 * rd + rf) : nullptr;
+  a->ssq = ssq ? reinterpret_cast<float*>(b + 4 * rd + rf + part) : nullptr;
   return 0;
 }
 
@@ -293,14 +296,28 @@ int decode_step(nml_model* m, nml_cache* c, const Acts& a, const int64_t* tokens
   NML_TRY(launch_embed_decode(m->dt, tokens, tok_stride, pos, m->emb, m->pos, a.x, B, d, m->V,
                               m->P, err, st));
   const size_t layer_kv = (size_t)B * m->H * m->P * m->dk * m->es;
+  // RMSNorm fused into the GEMMs that consume it (fp16, 8 < B ≤ 64): the residual GEMMs
+  // (W_o, W2) leave per-piece sums of squares of x in a.ssq, and QKV, W1 and the head
+  // normalise x on load; layer 0's input (the embedding) still takes the RMSNorm kernel.
+  const char* fuse_env = std::getenv("NIMBLEML_FUSE_NORM");  // "0": separate RMSNorm kernels
+  const bool fuse = !(fuse_env && fuse_env[0] == '0') && a.ssq && linear_norm_fusable(m->dt, B, d, d) &&
+                    linear_norm_fusable(m->dt, B, d, 3 * d) &&
+                    linear_norm_fusable(m->dt, B, d, m->F) && linear_norm_fusable(m->dt, B, m->F, d) &&
+                    linear_norm_fusable(m->dt, B, d, m->V);
   for (int l = 0; l < m->L; ++l) {
     const Layer& w = m->layers[l];
     void* kl = static_cast<char*>(c->k) + l * layer_kv;
     void* vl = static_cast<char*>(c->v) + l * layer_kv;
     const long long sb = (long long)m->H * m->P * m->dk, sh = (long long)m->P * m->dk;
-    NML_TRY(launch_rmsnorm(m->dt, a.x, w.ln1, a.xn, nullptr, nullptr, B, d, kEps, st));
+    const bool fuse_in = fuse && l > 0;
+    if (!fuse_in) NML_TRY(launch_rmsnorm(m->dt, a.x, w.ln1, a.xn, nullptr, nullptr, B, d, kEps, st));
     LinearArgs qkv{};
-    qkv.x = a.xn;
+    qkv.x = fuse_in ? a.x : a.xn;
+    if (fuse_in) {
+      qkv.ssq_in = a.ssq;
+      qkv.norm_g = w.ln1;
+      qkv.norm_eps = kEps;
+    }
     qkv.lda = d;
     qkv.w = w.wqkv;
     qkv.bias = w.bqkv;
@@ -335,10 +352,16 @@ int decode_step(nml_model* m, nml_cache* c, const Acts& a, const int64_t* tokens
     wo.N = d;
     wo.K = d;
     wo.epi = EPI_BIAS_RESID;
+    if (fuse) wo.ssq_out = a.ssq;
     NML_TRY(launch_linear(m->dt, wo, st));
-    NML_TRY(launch_rmsnorm(m->dt, a.x, w.ln2, a.xn, nullptr, nullptr, B, d, kEps, st));
+    if (!fuse) NML_TRY(launch_rmsnorm(m->dt, a.x, w.ln2, a.xn, nullptr, nullptr, B, d, kEps, st));
     LinearArgs f1{};
-    f1.x = a.xn;
+    f1.x = fuse ? a.x : a.xn;
+    if (fuse) {
+      f1.ssq_in = a.ssq;
+      f1.norm_g = w.ln2;
+      f1.norm_eps = kEps;
+    }
     f1.lda = d;
     f1.w = w.w1;
     f1.bias = w.b1;
@@ -359,11 +382,17 @@ int decode_step(nml_model* m, nml_cache* c, const Acts& a, const int64_t* tokens
     f2.N = d;
     f2.K = m->F;
     f2.epi = EPI_BIAS_RESID;
+    if (fuse) f2.ssq_out = a.ssq;
     NML_TRY(launch_linear(m->dt, f2, st));
   }
-  NML_TRY(launch_rmsnorm(m->dt, a.x, m->lnf, a.xn, nullptr, nullptr, B, d, kEps, st));
+  if (!fuse) NML_TRY(launch_rmsnorm(m->dt, a.x, m->lnf, a.xn, nullptr, nullptr, B, d, kEps, st));
   LinearArgs lm{};
-  lm.x = a.xn;
+  lm.x = fuse ? a.x : a.xn;
+  if (fuse) {
+    lm.ssq_in = a.ssq;
+    lm.norm_g = m->lnf;
+    lm.norm_eps = kEps;
+  }
   lm.lda = d;
   lm.w = m->emb;
   lm.out = logits;

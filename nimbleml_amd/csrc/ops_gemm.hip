@@ -16,20 +16,27 @@ namespace nml {
 
 namespace {
 
+// Stores the output element (m, n) and returns its stored value.
 template <typename T, int EPI>
-__device__ __forceinline__ void epilogue(const LinearArgs& a, int m, int n, float acc) {
+__device__ __forceinline__ float epilogue(const LinearArgs& a, int m, int n, float acc) {
   T* out = static_cast<T*>(a.out);
   const size_t idx = static_cast<size_t>(m) * a.N + n;
   if constexpr (EPI == EPI_NONE) {
     out[idx] = static_cast<T>(acc);
+    return rnd<T>(acc);
   } else {
     const float lin = rnd<T>(rnd<T>(acc) + static_cast<float>(static_cast<const T*>(a.bias)[n]));
     if constexpr (EPI == EPI_BIAS) {
       out[idx] = static_cast<T>(lin);
+      return lin;
     } else if constexpr (EPI == EPI_BIAS_GELU) {
-      out[idx] = static_cast<T>(gelu_t<T>(lin));
+      const float v = rnd<T>(gelu_t<T>(lin));
+      out[idx] = static_cast<T>(v);
+      return v;
     } else if constexpr (EPI == EPI_BIAS_RESID) {
-      out[idx] = static_cast<T>(static_cast<float>(static_cast<const T*>(a.resid)[idx]) + lin);
+      const float v = rnd<T>(static_cast<float>(static_cast<const T*>(a.resid)[idx]) + lin);
+      out[idx] = static_cast<T>(v);
+      return v;
     } else {  // EPI_QKV
       const QKVDst& q = a.qkv;
       const int which = n / q.d;
@@ -45,6 +52,7 @@ __device__ __forceinline__ void epilogue(const LinearArgs& a, int m, int n, floa
         kv[b * q.kv_stride_b + h * q.kv_stride_h + static_cast<long long>(pos) * q.dk + j] =
             static_cast<T>(lin);
       }
+      return lin;
     }
   }
 }
@@ -305,15 +313,21 @@ int gemv_dispatch_rpw(const LinearArgs& a, hipStream_t st) {
 // when N is small, over K. A workgroup owns 16 output columns (rows of W) for all M
 // rows and one of S slices of K; its 4 waves take a quarter of the slice each and run
 // v_mfma_f32_16x16x32_f16 with A = those 16 rows of W and B = 16 rows of x per m-tile
-// (MT tiles). The quarters are summed through LDS in a fixed order. With S > 1 each
-// workgroup stores its fp32 tile to the workspace and takes a ticket; the last of the
-// S workgroups of a column tile. Slices 0..S-2 publish their fp32 tile as 64-bit
+// (MT tiles). The quarters are summed through LDS in a fixed order. With S > 1,
+// slices 0..S-2 publish their fp32 tile as 64-bit
 // (1 << 32 | value) slots with relaxed device-scope stores (no cache-flushing fences);
 // slice S-1 — dispatched after every other workgroup of the grid, so its bounded
 // wait always ends — polls them, sums the slices in order (independent of arrival
 // order), clears the slots for the next launch and runs the epilogue.
 // Operand layout of the 16x16x32 MFMA: lane l holds A[l%16][(l/16)·8 + 0..7] and
 // B[(l/16)·8 + 0..7][l%16]; the result D[(l/16)·4 + e][l%16], e < 4.
+//
+// NORM (decode RMSNorm fused into the GEMM that consumes it, kernels/fused_rmsnorm.py:
+// 360-369): the producer of x (an EPI_BIAS_RESID GEMM) also wrote the sums of
+// squares rnd(v·v) of its rounded outputs per 16-column piece (ssq_out); this kernel
+// sums a row's pieces in a fixed order, takes inv = rnd(1 / sqrt(mean + eps)) and
+// normalises each loaded x piece as rnd(rnd(x·inv)·g) with two fp16 multiplies — the
+// rounding points of the separate RMSNorm kernel.
 constexpr int kSkN = 16;
 
 struct SkinnyWs {
@@ -323,9 +337,11 @@ struct SkinnyWs {
 };
 SkinnyWs g_skinny;
 
-template <int EPI, int MT, int U>
+template <int EPI, int MT, int U, bool NORM>
 __global__ __launch_bounds__(256) void skinny_f16_kernel(LinearArgs a, unsigned long long* ws) {
+#pragma clang fp contract(off)
   __shared__ float red[4][MT][16][17];
+  __shared__ half_t s_inv[MT * 16];
   const half_t* __restrict__ X = static_cast<const half_t*>(a.x);
   const half_t* __restrict__ W = static_cast<const half_t*>(a.w);
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -349,6 +365,28 @@ __global__ __launch_bounds__(256) void skinny_f16_kernel(LinearArgs a, unsigned 
 #pragma unroll
   for (int t = 0; t < MT; ++t) acc[t] = floatx4{0.f, 0.f, 0.f, 0.f};
   const half8 z8 = {0, 0, 0, 0, 0, 0, 0, 0};
+  half8 inv8[MT];
+  const half_t* gp = nullptr;
+  if constexpr (NORM) {
+    // thread → row tid/4 and every 4th 16-column piece of it; quads then sum in order
+    const int row = threadIdx.x >> 2, q = threadIdx.x & 3, np = K / 16;
+    float s = 0.f;
+    if (row < M)
+      for (int p = q; p < np; p += 4) s += a.ssq_in[static_cast<size_t>(row) * np + p];
+    s = quad_sum_dpp(s);
+    if (q == 0 && row < MT * 16) {
+      float inv = 0.f;  // rows past M load zeros and stay zero
+      if (row < M) inv = rnd<half_t>(1.0f / sqrtf(s / static_cast<float>(K) + a.norm_eps));
+      s_inv[row] = static_cast<half_t>(inv);
+    }
+    __syncthreads();
+#pragma unroll
+    for (int t = 0; t < MT; ++t) {
+      const half_t v = s_inv[t * 16 + r];
+      inv8[t] = half8{v, v, v, v, v, v, v, v};
+    }
+    gp = static_cast<const half_t*>(a.norm_g) + kbeg + kk;
+  }
   for (int k = 0; k < kq; k += 32 * U) {
     half8 av[U], bv[U][MT];
 #pragma unroll
@@ -357,6 +395,14 @@ __global__ __launch_bounds__(256) void skinny_f16_kernel(LinearArgs a, unsigned 
 #pragma unroll
       for (int t = 0; t < MT; ++t)
         bv[u][t] = mvalid[t] ? *reinterpret_cast<const half8*>(xp[t] + k + u * 32) : z8;
+    }
+    if constexpr (NORM) {
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const half8 g8 = *reinterpret_cast<const half8*>(gp + k + u * 32);
+#pragma unroll
+        for (int t = 0; t < MT; ++t) bv[u][t] = (bv[u][t] * inv8[t]) * g8;
+      }
     }
 #pragma unroll
     for (int u = 0; u < U; ++u)
@@ -411,36 +457,55 @@ __global__ __launch_bounds__(256) void skinny_f16_kernel(LinearArgs a, unsigned 
   for (int t = 0; t < MT; ++t) {
     const int j = threadIdx.x >> 4, i = threadIdx.x & 15;
     const int m = t * 16 + j, n = n0 + i;
-    if (m < M && n < N) epilogue<half_t, EPI>(a, m, n, sum[t]);
+    float v = 0.f;
+    if (m < M && n < N) v = epilogue<half_t, EPI>(a, m, n, sum[t]);
+    if constexpr (EPI == EPI_BIAS_RESID) {
+      if (a.ssq_out) {  // this tile's piece of the row's sum of squares (16 lanes = 1 row)
+        const float sq = row16_sum_dpp(rnd<half_t>(v * v));
+        if (i == 0 && m < M) a.ssq_out[static_cast<size_t>(m) * (N / kSkN) + tile] = sq;
+      }
+    }
   }
 }
 
-// Slices of K: enough workgroups to cover the chip (≥ 256) when N is small, each
-// wave's part of K a multiple of 32, and a workspace large enough.
+// Slices of K: about 1024 columns of K per workgroup (measured on MI355X with weights
+// streamed from HBM: unsplit is fastest for K = 1024 at N = 1024…4096, four slices for
+// K = 4096), each wave's part of K a multiple of 32, and a workspace large enough.
 int skinny_slices(const LinearArgs& a, int MT) {
   const int tiles = (a.N + kSkN - 1) / kSkN;
   int S = 1;
-  while (S < 8 && tiles * S < 256 && a.K % (128 * S * 2) == 0) S *= 2;
+  while (S < 8 && a.K / S > 1024 && a.K % (128 * S * 2) == 0) S *= 2;
   while (S > 1 && (tiles > g_skinny.tiles ||
                    static_cast<size_t>(tiles) * (S - 1) * MT * 256 > g_skinny.part_slots))
     S /= 2;
   return S;
 }
 
-template <int EPI, int MT>
-int skinny_dispatch_u(const LinearArgs& a, hipStream_t st) {
+template <int EPI, int MT, bool NORM>
+int skinny_launch(const LinearArgs& a, hipStream_t st) {
   const int S = skinny_slices(a, MT);
   dim3 grid((a.N + kSkN - 1) / kSkN, S);
   const int kq = a.K / (4 * S);
   unsigned long long* ws = g_skinny.part;
   if (kq % 128 == 0)
-    skinny_f16_kernel<EPI, MT, 4><<<grid, 256, 0, st>>>(a, ws);
+    skinny_f16_kernel<EPI, MT, 4, NORM><<<grid, 256, 0, st>>>(a, ws);
   else if (kq % 64 == 0)
-    skinny_f16_kernel<EPI, MT, 2><<<grid, 256, 0, st>>>(a, ws);
+    skinny_f16_kernel<EPI, MT, 2, NORM><<<grid, 256, 0, st>>>(a, ws);
   else
-    skinny_f16_kernel<EPI, MT, 1><<<grid, 256, 0, st>>>(a, ws);
+    skinny_f16_kernel<EPI, MT, 1, NORM><<<grid, 256, 0, st>>>(a, ws);
   NML_LAUNCHED();
   return 0;
+}
+
+template <int EPI, int MT>
+int skinny_dispatch_u(const LinearArgs& a, hipStream_t st) {
+  if (a.ssq_in) {
+    if constexpr (EPI == EPI_NONE || EPI == EPI_BIAS_GELU || EPI == EPI_QKV)
+      return skinny_launch<EPI, MT, true>(a, st);
+    set_error("linear: fused RMSNorm is not available with epilogue %d", EPI);
+    return -1;
+  }
+  return skinny_launch<EPI, MT, false>(a, st);
 }
 
 template <int EPI>
@@ -453,10 +518,16 @@ int skinny_dispatch(const LinearArgs& a, hipStream_t st) {
   }
 }
 
+bool skinny_applies(int dt, int M, int K) { return dt == F16 && M > 8 && M <= 64 && K % 128 == 0; }
+
 template <typename T, int EPI>
 int linear_typed(const LinearArgs& a, hipStream_t st) {
   if constexpr (sizeof(T) == 2) {
-    if (a.M > 8 && a.M <= 64 && a.K % 128 == 0) return skinny_dispatch<EPI>(a, st);
+    if (skinny_applies(F16, a.M, a.K)) return skinny_dispatch<EPI>(a, st);
+  }
+  if (a.ssq_in || a.ssq_out) {
+    set_error("linear: fused RMSNorm needs the fp16 skinny path (8 < rows <= 64)");
+    return -1;
   }
   if (a.M <= 8) {
     if (a.M <= 1) return gemv_dispatch_rpw<T, EPI, 1>(a, st);
@@ -519,7 +590,15 @@ int launch_linear(int dt, const LinearArgs& a, hipStream_t st) {
   NML_REQUIRE(a.epi != EPI_QKV || (a.qkv.d > 0 && a.qkv.dk > 0 && a.N == 3 * a.qkv.d &&
                                    a.M == a.qkv.S * (a.M / a.qkv.S)),
               "linear: bad QKV destination");
+  NML_REQUIRE(!a.ssq_in || (a.norm_g != nullptr && linear_norm_fusable(dt, a.M, a.K, a.N)),
+              "linear: fused RMSNorm needs a gain and the fp16 skinny shape");
+  NML_REQUIRE(!a.ssq_out || (a.epi == EPI_BIAS_RESID && linear_norm_fusable(dt, a.M, a.K, a.N)),
+              "linear: sums of squares are written by an fp16 skinny residual GEMM only");
   return dt == F16 ? linear_epi<half_t>(a, st) : linear_epi<float>(a, st);
+}
+
+bool linear_norm_fusable(int dt, int M, int K, int N) {
+  return skinny_applies(dt, M, K) && K % kSkN == 0 && N % kSkN == 0;
 }
 
 }  // namespace nml

@@ -12,7 +12,10 @@ from oracle.weights import GPTConfig, make_weights
 pytestmark = pytest.mark.gpu
 
 
-def test_ragged_batch_rows_match_oracle_fp16(gpu):
+@pytest.mark.parametrize("lens", [[20, 300, 64, 65, 129, 7, 250, 33, 190, 100, 140, 41],
+                                  [5 + 13 * i for i in range(40)]])
+def test_ragged_batch_rows_match_oracle_fp16(gpu, lens):
+    """12 rows (one 16-row MFMA tile) and 40 rows (three tiles, the last partly empty)."""
     import nimbleml_amd as nm
 
     cfg = GPTConfig(4096, 1024, 16, 2, 1024)
@@ -20,7 +23,6 @@ def test_ragged_batch_rows_match_oracle_fp16(gpu):
     m = nm.GPT.from_arrays(w, cfg.vocab_size, cfg.d_model, cfg.num_heads, cfg.num_layers,
                            cfg.max_seq_len, dtype=np.float16)
     rng = np.random.default_rng(3)
-    lens = [20, 300, 64, 65, 129, 7, 250, 33, 190, 100, 140, 41]
     rows = [rng.integers(0, cfg.vocab_size, n) for n in lens]
     new = 20
     out = nm.generate(m, rows, max_new_tokens=new, temperature=0.0)
@@ -61,3 +63,25 @@ def test_cached_prefill_with_offset_matches_full_forward_fp16(gpu):
     want = R.forward({k: v.astype(np.float32) for k, v in w.items()}, ids, cfg.num_heads,
                      cfg.num_layers)
     assert np.abs(full - want).max() <= 3e-2
+
+
+def test_fused_rmsnorm_decode_matches_separate_kernels_fp16(gpu, monkeypatch):
+    """The batched decode step with RMSNorm fused into the projections that consume it
+    (sums of squares from the residual GEMMs) and with the separate RMSNorm kernels: the
+    rounding points are the same, only the fp32 order of the mean's sum differs, so
+    the sampled tokens (same uniforms) agree."""
+    import nimbleml_amd as nm
+
+    cfg = GPTConfig(4096, 1024, 16, 3, 512)
+    w = make_weights(cfg, seed=23, dtype=np.float16, rich=True)
+    m = nm.GPT.from_arrays(w, cfg.vocab_size, cfg.d_model, cfg.num_heads, cfg.num_layers,
+                           cfg.max_seq_len, dtype=np.float16)
+    rng = np.random.default_rng(9)
+    rows = [rng.integers(0, cfg.vocab_size, int(n)) for n in rng.integers(30, 200, 24)]
+    np.random.seed(4)
+    fused = nm.generate(m, rows, max_new_tokens=24, temperature=0.0)
+    monkeypatch.setenv("NIMBLEML_FUSE_NORM", "0")
+    np.random.seed(4)
+    sep = nm.generate(m, rows, max_new_tokens=24, temperature=0.0)
+    same = sum(np.array_equal(np.asarray(a), np.asarray(b)) for a, b in zip(fused, sep))
+    assert same >= len(rows) - 1, same
