@@ -91,10 +91,12 @@ struct AttnArgs {
 };
 int launch_attention_prefill(int dt, const AttnArgs& a, hipStream_t st);
 
-// One new query per sequence at position pos[b] (keys 0..pos[b]). `part` is a
-// float workspace of B·H·max_chunks·(dk + 2); `max_len` bounds pos[b] + 1.
+// One new query per sequence at position pos[b] (keys 0..pos[b]). `ws` is a workspace
+// of attention_decode_workspace(B, H, dk, max_len) bytes, zeroed once before the first
+// launch (outside stream capture); each launch leaves it zeroed again. `max_len`
+// bounds pos[b] + 1.
 int launch_attention_decode(int dt, const AttnArgs& a, const int32_t* pos, int max_len,
-                            float* part, hipStream_t st);
+                            void* ws, hipStream_t st);
 size_t attention_decode_workspace(int B, int H, int dk, int max_len);
 
 // Row-wise cross-entropy over (rows, V) logits of storage type T. Writes the

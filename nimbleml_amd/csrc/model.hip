@@ -134,7 +134,7 @@ struct Acts {
   void* q;   // (R, d) head-major queries
   void* att; // (R, d) merged attention output
   void* h;   // (R, F) FFN hidden
-  float* part;  // decode partials
+  void* part;   // decode attention workspace (zeroed before a decode loop)
   float* ssq;   // decode: (Bdec, d/16) sums of squares of x in 16-column pieces
 };
 
@@ -150,7 +150,7 @@ int acts_for(nml_model* m, int R, int Bdec, Acts* a) {
   a->q = b + 2 * rd;
   a->att = b + 3 * rd;
   a->h = b + 4 * rd;
-  a->part = part ? reinterpret_cast<float*>(b + 4 * rd + rf) : nullptr;
+  a->part = part ? static_cast<void*>(b + 4 * rd + rf) : nullptr;
   a->ssq = ssq ? reinterpret_cast<float*>(b + 4 * rd + rf + part) : nullptr;
   return 0;
 }
@@ -817,6 +817,7 @@ int nml_model_generate(nml_model* m, const int64_t* prompts, size_t prompt_strid
 
   Acts a;
   NML_TRY(acts_for(m, B, B, &a));
+  NML_HIP(hipMemsetAsync(a.part, 0, attention_decode_workspace(B, m->H, m->dk, m->P), st));
   // Attention length bound of the decode steps: the last step feeds position
   // maxp + max_new - 2 and attends to every key up to it.
   const int decode_len = maxp + (int)max_new - 1;

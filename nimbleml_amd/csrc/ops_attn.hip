@@ -20,6 +20,10 @@ namespace {
 constexpr int kTile = 64;
 constexpr int kCombineMax = 1024;  // chunks of one (row, head): max_seq_len ≤ 65536
 
+// Ticket counters of the one-launch decode attention, one per (row, head), padded to
+// whole 256-byte blocks so the group partials after them start line-aligned.
+inline size_t decode_ticket_bytes(int bh) { return (static_cast<size_t>(bh) * 4 + 255) / 256 * 256; }
+
 template <typename T, int DK>
 __global__ __launch_bounds__(64) void attn_prefill_kernel(AttnArgs a) {
   __shared__ T Ks[kTile][DK];
@@ -122,87 +126,192 @@ __device__ __forceinline__ void ld8(const T* p, float (&o)[8]) {
   }
 }
 
-// Decode attention, one 256-lane workgroup per 64-key chunk of one (row, head):
-// scores with 4 lanes per key (each DK/4 dims, 16-byte loads along the key row),
-// chunk max / Σp in LDS, then P·V with each lane owning 8 dims of a key subset.
-// Writes the chunk's (max, Σp, Σp·v) for the combine pass.
+// Decode attention for head dims ≥ 32, one launch: a 256-lane workgroup takes a group
+// of G 64-key chunks of one (row, head) — all their K/V rows are loaded up front
+// (clamped into [0, len), the clamped ones never used) — scores every key with 4
+// lanes per key (DK/4 dims each), takes the group's max and Σp with one block
+// reduction each, and P·V with each lane owning 8 dims of a key subset. The group's
+// (max, Σp, Σp·v) go out as flagged 64-bit slots (1 << 32 | value, relaxed
+// device-scope stores, no fences), then the workgroup takes a ticket for its (row,
+// head); the one that draws the last ticket waits for every group's slots (bounded),
+// merges them (softmax rescaling, attention.py:140-142 over the concatenated keys),
+// writes the head's output and returns the slots and the ticket counter to zero for
+// the next launch.
+// slots per group partial: DK + 2 rounded up to whole 128-byte lines
+constexpr int dec_slots(int dk) { return (dk + 2 + 15) / 16 * 16; }
+
 template <typename T, int DK>
-__global__ __launch_bounds__(256) void attn_decode_kernel(AttnArgs a, const int32_t* __restrict__ pos,
-                                                          int max_chunks, float* __restrict__ part) {
+constexpr int dec_groups() {  // chunks per group: K/V registers bounded
+  return DK * static_cast<int>(sizeof(T)) <= 128 ? 4 : DK * static_cast<int>(sizeof(T)) <= 256 ? 2 : 1;
+}
+
+template <typename T, int DK, int G>
+__global__ __launch_bounds__(256) void attn_decode_group_kernel(AttnArgs a, const int32_t* __restrict__ pos,
+                                                                int max_groups,
+                                                                unsigned long long* __restrict__ part,
+                                                                unsigned* __restrict__ tickets) {
 #pragma clang fp contract(off)
-  constexpr int CH = kTile, DPT = DK / 4, DG = DK / 8, NKS = 256 / DG, KPT = CH / NKS;
-  __shared__ float s_q[DK], s_p[CH], s_red[8];
+  typedef unsigned long long u64;
+  constexpr int CH = kTile, KG = CH * G, DPT = DK / 4, DG = DK / 8, NKS = 256 / DG, KPT = CH / NKS;
+  constexpr int PS = dec_slots(DK);
+  static_assert(DK >= 32 && KPT >= 1, "decode group shape");
+  __shared__ float s_q[DK], s_p[KG], s_red[16];
   __shared__ float s_o[NKS][DK + 1];
+  __shared__ int s_last;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int c = blockIdx.x, bh = blockIdx.y;
+  const int grp = blockIdx.x, bh = blockIdx.y;
   const int b = bh / a.H, h = bh - (bh / a.H) * a.H;
   const int len = pos[b] + 1;
-  const int k0 = c * CH;
-  if (k0 >= len) return;  // whole workgroup: the combine pass reads chunks below len only
+  const int k0 = grp * KG;
+  if (k0 >= len) return;  // whole workgroup: groups at or past len take no ticket
+  const int ng = (len + KG - 1) / KG;
   const T* __restrict__ K = static_cast<const T*>(a.k) + b * a.kv_stride_b + h * a.kv_stride_h;
   const T* __restrict__ Vp = static_cast<const T*>(a.v) + b * a.kv_stride_b + h * a.kv_stride_h;
   const float scale_t = static_cast<float>(static_cast<T>(a.scale));
-  // issue the chunk's loads first (keys past len clamped to len - 1, never used)
-  const int key = k0 + (tid >> 2), qq = tid & 3;
-  const int keyc = key < len ? key : len - 1;
-  float kr[DPT];
+  const int qq = tid & 3, dg = tid % DG, ks = tid / DG;
+  float kr[G][DPT];
+  float vr[G][KPT][8];
 #pragma unroll
-  for (int e = 0; e < DPT; e += 8) {
-    float t8[8];
-    ld8<T>(K + static_cast<long long>(keyc) * DK + qq * DPT + e, t8);
+  for (int j = 0; j < G; ++j) {
+    const int key = k0 + j * CH + (tid >> 2);
+    const int keyc = key < len ? key : len - 1;
 #pragma unroll
-    for (int u = 0; u < 8; ++u) kr[e + u] = t8[u];
-  }
-  const int dg = tid % DG, ks = tid / DG;
-  float vr[KPT][8];
+    for (int e = 0; e < DPT; e += 8) {
+      float t8[8];
+      ld8<T>(K + static_cast<long long>(keyc) * DK + qq * DPT + e, t8);
 #pragma unroll
-  for (int i = 0; i < KPT; ++i) {
-    const int vk = k0 + ks + i * NKS;
-    ld8<T>(Vp + static_cast<long long>(vk < len ? vk : len - 1) * DK + dg * 8, vr[i]);
+      for (int u = 0; u < 8; ++u) kr[j][e + u] = t8[u];
+    }
+#pragma unroll
+    for (int i = 0; i < KPT; ++i) {
+      const int vk = k0 + j * CH + ks + i * NKS;
+      ld8<T>(Vp + static_cast<long long>(vk < len ? vk : len - 1) * DK + dg * 8, vr[j][i]);
+    }
   }
   if (tid < DK) s_q[tid] = static_cast<float>(static_cast<const T*>(a.q)[static_cast<size_t>(bh) * DK + tid]);
   __syncthreads();
-  float dot = 0.f;
+  float sc[G];
+  float mx = -INFINITY;
 #pragma unroll
-  for (int e = 0; e < DPT; ++e) dot += s_q[qq * DPT + e] * kr[e];
-  dot += __shfl_xor(dot, 1, 64);
-  dot += __shfl_xor(dot, 2, 64);
-  const bool valid = key < len;
-  const float sc = valid ? rnd<T>(rnd<T>(dot) / scale_t) : -INFINITY;
-  float mx = wave_max(sc);
+  for (int j = 0; j < G; ++j) {
+    float dot = 0.f;
+#pragma unroll
+    for (int e = 0; e < DPT; ++e) dot += s_q[qq * DPT + e] * kr[j][e];
+    dot = quad_sum_dpp(dot);
+    const bool valid = k0 + j * CH + (tid >> 2) < len;
+    sc[j] = valid ? rnd<T>(rnd<T>(dot) / scale_t) : -INFINITY;
+    mx = fmaxf(mx, sc[j]);
+  }
+  mx = wave_max_dpp(mx);
   if (lane == 0) s_red[wave] = mx;
   __syncthreads();
   mx = fmaxf(fmaxf(s_red[0], s_red[1]), fmaxf(s_red[2], s_red[3]));
-  const float p = valid ? expf(sc - mx) : 0.f;
-  if (qq == 0) s_p[tid >> 2] = p;
-  float l = wave_sum(qq == 0 ? p : 0.f);
-  if (lane == 0) s_red[4 + wave] = l;
+  float lsum = 0.f;
+#pragma unroll
+  for (int j = 0; j < G; ++j) {
+    const float p = expf(sc[j] - mx);  // exp(-inf) = 0 for keys past len
+    if (qq == 0) {
+      s_p[j * CH + (tid >> 2)] = p;
+      lsum += p;
+    }
+  }
+  lsum = wave_sum_dpp(lsum);
+  if (lane == 0) s_red[4 + wave] = lsum;
   __syncthreads();
-  l = (s_red[4] + s_red[5]) + (s_red[6] + s_red[7]);
+  const float l = (s_red[4] + s_red[5]) + (s_red[6] + s_red[7]);
   float o[8];
 #pragma unroll
   for (int e = 0; e < 8; ++e) o[e] = 0.f;
 #pragma unroll
-  for (int i = 0; i < KPT; ++i) {
-    const int jj = ks + i * NKS;
-    if (k0 + jj < len) {
-      const float pj = s_p[jj];
+  for (int j = 0; j < G; ++j)
 #pragma unroll
-      for (int e = 0; e < 8; ++e) o[e] += pj * vr[i][e];
+    for (int i = 0; i < KPT; ++i) {
+      const int jj = j * CH + ks + i * NKS;
+      if (k0 + jj < len) {
+        const float pj = s_p[jj];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) o[e] += pj * vr[j][i][e];
+      }
     }
-  }
 #pragma unroll
   for (int e = 0; e < 8; ++e) s_o[ks][dg * 8 + e] = o[e];
   __syncthreads();
-  float* pp = part + (static_cast<size_t>(bh) * max_chunks + c) * (DK + 2);
+  u64* const pb = part + static_cast<size_t>(bh) * max_groups * PS;
+  const u64 flag = 1ull << 32;
   if (tid < DK) {
-    float s = 0.f;
-    for (int k2 = 0; k2 < NKS; ++k2) s += s_o[k2][tid];
-    pp[2 + tid] = s;
+    float sm = 0.f;
+    for (int k2 = 0; k2 < NKS; ++k2) sm += s_o[k2][tid];
+    __hip_atomic_store(pb + grp * PS + 2 + tid, flag | __float_as_uint(sm), __ATOMIC_RELAXED,
+                       __HIP_MEMORY_SCOPE_AGENT);
   } else if (tid == DK) {
-    pp[0] = mx;
-    pp[1] = l;
+    __hip_atomic_store(pb + grp * PS, flag | __float_as_uint(mx), __ATOMIC_RELAXED,
+                       __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(pb + grp * PS + 1, flag | __float_as_uint(l), __ATOMIC_RELAXED,
+                       __HIP_MEMORY_SCOPE_AGENT);
   }
+  __syncthreads();  // every slot of this group issued before the ticket
+  if (tid == 0)
+    s_last = __hip_atomic_fetch_add(tickets + bh, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+             static_cast<unsigned>(ng - 1);
+  __syncthreads();
+  if (!s_last) return;
+  // Last group of (b, h): the others have taken their tickets, so their slots are
+  // issued; wait (bounded) until each is visible — 8 groups' slots in flight at a
+  // time — then merge in group order.
+  if (tid < DK) {
+    constexpr int NB = 8;
+    float mg[NB], lg[NB], og[NB];
+    float M = -INFINITY, den = 0.f, num = 0.f;
+    for (int g0 = 0; g0 < ng; g0 += NB) {
+      u64 vm[NB], vl[NB], vo[NB];
+      const u64 ok = 1ull << 32;
+#pragma unroll
+      for (int j = 0; j < NB; ++j) {
+        const bool in = g0 + j < ng;
+        u64* sl = pb + (g0 + j) * PS;
+        vm[j] = in ? __hip_atomic_load(sl, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : ok;
+        vl[j] = in ? __hip_atomic_load(sl + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : ok;
+        vo[j] = in ? __hip_atomic_load(sl + 2 + tid, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : ok;
+      }
+      for (unsigned spins = 0; spins < (1u << 22); ++spins) {
+        bool all = true;
+#pragma unroll
+        for (int j = 0; j < NB; ++j) all = all && (vm[j] >> 32) && (vl[j] >> 32) && (vo[j] >> 32);
+        if (all) break;
+        __builtin_amdgcn_s_sleep(1);
+#pragma unroll
+        for (int j = 0; j < NB; ++j) {
+          u64* sl = pb + (g0 + j) * PS;
+          if (!(vm[j] >> 32)) vm[j] = __hip_atomic_load(sl, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          if (!(vl[j] >> 32)) vl[j] = __hip_atomic_load(sl + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          if (!(vo[j] >> 32))
+            vo[j] = __hip_atomic_load(sl + 2 + tid, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+      }
+#pragma unroll
+      for (int j = 0; j < NB; ++j) {
+        mg[j] = __uint_as_float(static_cast<uint32_t>(vm[j]));
+        lg[j] = __uint_as_float(static_cast<uint32_t>(vl[j]));
+        og[j] = __uint_as_float(static_cast<uint32_t>(vo[j]));
+      }
+      // online merge over this batch of groups (in group order)
+#pragma unroll
+      for (int j = 0; j < NB; ++j) {
+        if (g0 + j >= ng) break;
+        const float Mn = fmaxf(M, mg[j]);
+        const float c = expf(M - Mn), w = expf(mg[j] - Mn);
+        den = den * c + w * lg[j];
+        num = num * c + w * og[j];
+        M = Mn;
+      }
+    }
+    T* out = static_cast<T*>(a.out) + static_cast<size_t>(b) * a.H * DK + h * DK;
+    out[tid] = static_cast<T>(num * (1.f / den));
+  }
+  __syncthreads();  // every read of the slots done before they are cleared
+  for (int i = tid; i < ng * PS; i += 256)
+    __hip_atomic_store(pb + i, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  if (tid == 0) __hip_atomic_store(tickets + bh, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // Head dims below 32: one 64-lane wave per chunk, each lane scores one key.
@@ -480,16 +589,25 @@ int prefill_typed(const AttnArgs& a, hipStream_t st) {
 }
 
 template <typename T, int DK>
-int decode_typed(const AttnArgs& a, const int32_t* pos, int max_len, float* part, hipStream_t st) {
-  const int max_chunks = (max_len + kTile - 1) / kTile;
-  dim3 grid(max_chunks, a.B * a.H);
-  if constexpr (DK >= 32)
-    attn_decode_kernel<T, DK><<<grid, 256, 0, st>>>(a, pos, max_chunks, part);
-  else
-    attn_decode_small_kernel<T, DK><<<grid, 64, 0, st>>>(a, pos, max_chunks, part);
-  NML_LAUNCHED();
-  attn_combine_kernel<T, DK><<<a.B * a.H, 64, 0, st>>>(a, pos, max_chunks, part);
-  NML_LAUNCHED();
+int decode_typed(const AttnArgs& a, const int32_t* pos, int max_len, void* ws, hipStream_t st) {
+  if constexpr (DK >= 32) {
+    constexpr int G = dec_groups<T, DK>();
+    const int max_groups = (max_len + kTile * G - 1) / (kTile * G);
+    unsigned* tickets = static_cast<unsigned*>(ws);
+    unsigned long long* part = reinterpret_cast<unsigned long long*>(
+        static_cast<char*>(ws) + decode_ticket_bytes(a.B * a.H));
+    attn_decode_group_kernel<T, DK, G><<<dim3(max_groups, a.B * a.H), 256, 0, st>>>(
+        a, pos, max_groups, part, tickets);
+    NML_LAUNCHED();
+  } else {
+    const int max_chunks = (max_len + kTile - 1) / kTile;
+    float* part = static_cast<float*>(ws);
+    attn_decode_small_kernel<T, DK><<<dim3(max_chunks, a.B * a.H), 64, 0, st>>>(a, pos, max_chunks,
+                                                                               part);
+    NML_LAUNCHED();
+    attn_combine_kernel<T, DK><<<a.B * a.H, 64, 0, st>>>(a, pos, max_chunks, part);
+    NML_LAUNCHED();
+  }
   return 0;
 }
 
@@ -510,15 +628,19 @@ int prefill_dk(const AttnArgs& a, hipStream_t st) {
 }
 
 template <typename T>
-int decode_dk(const AttnArgs& a, const int32_t* pos, int max_len, float* part, hipStream_t st) {
-  NML_DK_SWITCH(a.dk, decode_typed, a, pos, max_len, part, st);
+int decode_dk(const AttnArgs& a, const int32_t* pos, int max_len, void* ws, hipStream_t st) {
+  NML_DK_SWITCH(a.dk, decode_typed, a, pos, max_len, ws, st);
 }
 
 }  // namespace
 
 size_t attention_decode_workspace(int B, int H, int dk, int max_len) {
+  // head dims ≥ 32: tickets, then flagged group partials (at most 4 chunks a group
+  // never fewer than 1); below: float chunk partials for the combine pass
   const size_t chunks = (max_len + kTile - 1) / kTile;
-  return static_cast<size_t>(B) * H * chunks * (dk + 2) * sizeof(float);
+  const size_t grouped = decode_ticket_bytes(B * H) + static_cast<size_t>(B) * H * chunks * dec_slots(dk) * 8;
+  const size_t plain = static_cast<size_t>(B) * H * chunks * (dk + 2) * sizeof(float);
+  return grouped > plain ? grouped : plain;
 }
 
 int launch_attention_prefill(int dt, const AttnArgs& a, hipStream_t st) {
@@ -526,13 +648,13 @@ int launch_attention_prefill(int dt, const AttnArgs& a, hipStream_t st) {
   return dt == F16 ? prefill_dk<half_t>(a, st) : prefill_dk<float>(a, st);
 }
 
-int launch_attention_decode(int dt, const AttnArgs& a, const int32_t* pos, int max_len, float* part,
+int launch_attention_decode(int dt, const AttnArgs& a, const int32_t* pos, int max_len, void* ws,
                             hipStream_t st) {
   if (a.B == 0) return 0;
   NML_REQUIRE(max_len > 0 && max_len <= kCombineMax * kTile,
               "attention decode: max_len %d outside (0, %d]", max_len, kCombineMax * kTile);
-  return dt == F16 ? decode_dk<half_t>(a, pos, max_len, part, st)
-                   : decode_dk<float>(a, pos, max_len, part, st);
+  return dt == F16 ? decode_dk<half_t>(a, pos, max_len, ws, st)
+                   : decode_dk<float>(a, pos, max_len, ws, st);
 }
 
 }  // namespace nml
