@@ -142,23 +142,103 @@ __device__ uint32_t select_kth_key(int V, int k, F key_of, Shared& sh) {
       if ((key & mask) == prefix) atomicAdd(&sh.hist_cnt[(key >> shift) & 255u], 1);
     }
     __syncthreads();
-    if (threadIdx.x == 0) {
-      int cum = 0, kk = sh.sel_k, chosen = 0;
-      for (int bin = 255; bin >= 0; --bin) {
-        if (cum + sh.hist_cnt[bin] >= kk) {
-          chosen = bin;
-          break;
-        }
-        cum += sh.hist_cnt[bin];
+    if (threadIdx.x < 64) {
+      // wave 0: lane l owns bins 255-4l … 252-4l (descending); an exclusive prefix of
+      // the lanes' counts finds the bin holding the k-th largest key
+      const int l = threadIdx.x, kk = sh.sel_k;
+      int c4[4], own = 0;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        c4[e] = sh.hist_cnt[255 - 4 * l - e];
+        own += c4[e];
       }
-      sh.sel_k = kk - cum;
-      sh.sel_prefix = prefix | (static_cast<uint32_t>(chosen) << shift);
+      int inc = own;
+#pragma unroll
+      for (int o = 1; o < 64; o <<= 1) {
+        const int t = __shfl_up(inc, o, 64);
+        if (l >= o) inc += t;
+      }
+      int cum = inc - own;
+      if (cum < kk && inc >= kk) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          if (cum + c4[e] >= kk) {
+            sh.sel_k = kk - cum;
+            sh.sel_prefix = prefix | (static_cast<uint32_t>(255 - 4 * l - e) << shift);
+            break;
+          }
+          cum += c4[e];
+        }
+      }
     }
     __syncthreads();
     prefix = sh.sel_prefix;
     mask |= 255u << shift;
   }
   return prefix;
+}
+
+// Top-k sampling without top-p (generate.py:43-47, then RandomState.choice): every
+// element below the k-th largest scaled logit becomes -1e9, whose exp(x − max)
+// underflows to exactly 0, so only the candidates x ≥ threshold carry mass. They are
+// gathered in index order and the max, Σ exp, probabilities and the float64
+// index-order CDF are taken over them; returns the first candidate index whose
+// cdf / total exceeds u (V − 1 if rounding leaves none, as the full scan does), or
+// -1 when the candidates do not fit (the caller then runs the full scan).
+constexpr int kCandMax = 2048;
+
+template <typename T>
+__device__ int sample_topk_candidates(const Row<T>& row, float thresh, double u, Shared& sh,
+                                      int* cand, float* candx) {
+  const int V = row.V;
+  const int seg = (V + kThreads - 1) / kThreads;
+  const int lo = threadIdx.x * seg, hi = min(V, lo + seg);
+  int c = 0;
+  for (int i = lo; i < hi; ++i) c += row.scaled(i) >= thresh ? 1 : 0;
+  int n = 0;
+  int off = block_excl_scan_i(c, &n, sh);
+  if (n > kCandMax) return -1;
+  for (int i = lo; i < hi; ++i) {
+    const float x = row.scaled(i);
+    if (x >= thresh) {
+      cand[off] = i;
+      candx[off] = x;
+      ++off;
+    }
+  }
+  __syncthreads();
+  if (threadIdx.x < 64) {
+    const int l = threadIdx.x;
+    float mx = -INFINITY;
+    for (int j = l; j < n; j += 64) mx = fmaxf(mx, candx[j]);
+    mx = wave_max(mx);
+    float se = 0.f;
+    for (int j = l; j < n; j += 64) se += expf(candx[j] - mx);
+    se = wave_sum(se);
+    double total = 0.0;
+    for (int j = l; j < n; j += 64) total += static_cast<double>(expf(candx[j] - mx) / se);
+    total = wave_sum_d(total);
+    // index-order running sums, 64 candidates per round
+    double carry = 0.0;
+    int found = 0x7fffffff;
+    for (int j0 = 0; j0 < n && found == 0x7fffffff; j0 += 64) {
+      const int j = j0 + l;
+      const double pj = j < n ? static_cast<double>(expf(candx[j] - mx) / se) : 0.0;
+      double inc = pj;
+#pragma unroll
+      for (int o = 1; o < 64; o <<= 1) {
+        const double t = __shfl_up(inc, o, 64);
+        if (l >= o) inc += t;
+      }
+      const bool hit = j < n && (carry + inc) / total > u;
+      const unsigned long long hits = __ballot(hit);
+      if (hits) found = cand[j0 + __ffsll(static_cast<long long>(hits)) - 1];
+      carry += __shfl(inc, 63, 64);
+    }
+    if (l == 0) sh.found_index = found == 0x7fffffff ? V - 1 : found;
+  }
+  __syncthreads();
+  return sh.found_index;
 }
 
 // First position of the descending order (key desc, then index desc) over the
@@ -251,6 +331,8 @@ __device__ int find_nth(int V, int j, FP pred, Shared& sh) {
 template <typename T>
 __global__ __launch_bounds__(kThreads) void sample_kernel(SampleArgs a) {
   __shared__ Shared sh;
+  __shared__ int s_cand[kCandMax];
+  __shared__ float s_candx[kCandMax];
   const int b = blockIdx.x;
   const int V = a.V;
   const bool gen = a.pos != nullptr;
@@ -339,7 +421,12 @@ __global__ __launch_bounds__(kThreads) void sample_kernel(SampleArgs a) {
     auto prob = [&](int i) { return expf(xm(i) - mx) / se; };
     auto keyp = [&](int i) { return fkey(prob(i)); };
 
-    if (a.top_p > 0.f && a.top_p < 1.f) {
+    const bool use_p = a.top_p > 0.f && a.top_p < 1.f;
+    chosen = -1;
+    if (use_k && !use_p) chosen = sample_topk_candidates(row, thresh, u, sh, s_cand, s_candx);
+    if (chosen >= 0) {
+      // sampled among the top-k candidates
+    } else if (use_p) {
       // Cut: first descending position whose running mass exceeds top_p.
       uint32_t tau1;
       int j1;

@@ -184,6 +184,24 @@ def test_sampling_matches_oracle(gpu, top_k, top_p):
         assert list(got) == want, (trial, list(got), want)
 
 
+@pytest.mark.parametrize("top_k,grid", [(30, True), (3000, False), (4096, False)])
+def test_top_k_sampling_ties_and_large_k(gpu, top_k, grid):
+    """Top-k without top-p: exact ties at the k-th largest logit (all tied elements are
+    kept, generate.py:43-46), and k past the candidate buffer (2048) or equal to V (the
+    device then takes the full-vocabulary scan)."""
+    rng = np.random.default_rng(top_k + grid)
+    b, v = 6, 4096
+    if grid:
+        lg = (rng.integers(-12, 12, (b, v)) * 0.25).astype(np.float32)
+    else:
+        lg = _distinct_logits(rng, b, v)
+    u = rng.random(b)
+    got = _k().sample_tokens(lg, temperature=0.8, top_k=top_k, top_p=1.0, uniforms=u)
+    want = [R.sample_logits(lg[i], temperature=0.8, top_k=top_k, top_p=1.0, u=u[i])
+            for i in range(b)]
+    assert list(got) == want
+
+
 def test_sampling_with_repetition_penalty(gpu):
     rng = np.random.default_rng(11)
     lg = _distinct_logits(rng, 3, 1000)
