@@ -173,6 +173,8 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-graph", action="store_true")
     ap.add_argument("--only-c3", action="store_true", help="skip the batch-32 and prefill lines")
+    ap.add_argument("--only", choices=["c3", "c4", "c5"], default=None,
+                    help="run one workload only (for profiling); c4/c5 print their own line")
     ap.add_argument("--cpu-tokens", type=int, default=12)
     args = ap.parse_args()
     if args.gpus != 1:
@@ -186,6 +188,9 @@ def main():
 
     cfg = C3
     nm._native.ensure_init()
+    if args.only == "c5":
+        print(json.dumps({"c5": bench_c5(nm)}), flush=True)
+        return
     w16 = make_weights(cfg, seed=1234, dtype=np.float16)
     model = nm.GPT.from_arrays(w16, cfg.vocab_size, cfg.d_model, cfg.num_heads, cfg.num_layers,
                                cfg.max_seq_len, dtype=np.float16)
@@ -193,6 +198,9 @@ def main():
     prompt = random_ids((1, args.prompt), cfg.vocab_size, seed=99)
     n = args.new_tokens
     use_graph = not args.no_graph
+    if args.only == "c4":
+        print(json.dumps({"c4": bench_c4(nm, cfg, model, use_graph)}), flush=True)
+        return
 
     elapsed, step_ms, bytes_avg, persistent = bench_c3(nm, cfg, model, prompt, n, args.steps,
                                                        args.warmup, use_graph)
@@ -223,7 +231,7 @@ def main():
                      "traffic": round(traffic) if traffic else None,
                      "bytes_per_launch": round(bytes_avg)},
     }
-    if not args.only_c3:
+    if not (args.only_c3 or args.only == "c3"):
         result["c4"] = bench_c4(nm, cfg, model, use_graph)
         del model
         result["c5"] = bench_c5(nm)

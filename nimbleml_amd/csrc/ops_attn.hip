@@ -6,11 +6,13 @@
 // fp16 divisor); the softmax itself runs online in fp32 (flash form), so no
 // (S, S) score matrix exists.
 //
-//  * prefill: one wave per 64 queries of one (sequence, head); K/V tiles of 64
-//    keys staged in LDS; online softmax over 16-key sub-tiles.
-//  * decode: split-K. One wave per 64-key chunk of one (sequence, head): each lane
-//    scores one key, the wave forms the chunk's (max, sum, Σp·v) partial; a
-//    combine pass merges the chunks.
+//  * prefill, fp16 head dim 64/128: attn_prefill_mfma_kernel — MFMA flash
+//    attention, 128 queries per workgroup, 64-key K/V tiles in LDS (see its comment);
+//    other types / head dims: attn_prefill_kernel, one wave per 64 queries, scalar.
+//  * decode, head dim ≥ 32: attn_decode_group_kernel — split-K in one launch: each
+//    workgroup scores a group of 64-key chunks of one (sequence, head) and publishes
+//    its (max, Σp, Σp·v) as flagged slots; the last workgroup of the (sequence, head)
+//    merges them. Head dims 8/16: attn_decode_small_kernel + attn_combine_kernel.
 #include "kernels.hpp"
 
 namespace nml {

@@ -10,6 +10,8 @@
 //    registers while the current one is multiplied.
 //  * gemv: M ≤ 8 activation rows (decode). One wave per output row (or four),
 //    16-byte loads along K, fp32 accumulation, wave-reduced.
+//  * skinny_f16: 8 < M ≤ 64 rows (batched decode), MFMA 16×16×32 with optional split-K
+//    and a fused RMSNorm of x (see its comment).
 #include "kernels.hpp"
 
 namespace nml {
