@@ -44,19 +44,23 @@ constexpr int kLine = 16;           // 64-bit slots per 128-byte line
 // Exchange-slot regions, in 64-bit slots. Each producing workgroup's slots start on a
 // line of their own: lines shared by producers make their write-through stores and
 // the consumers' polls of that line contend, which measured ~1.5x slower exchanges.
+constexpr int lines_of(int slots) { return (slots + kLine - 1) / kLine * kLine; }
+
 template <int D, int DK>
 struct SlotLayout {
   static constexpr int H = D / DK, TEAM = kG / H, F = 4 * D;
-  static constexpr int PCH = (DK + 2 + kLine - 1) / kLine * kLine;  // one chunk's partial
-  static constexpr int X = 0;                           // kG × line: D/kG values of x
-  static constexpr int QKV = X + kG * kLine;            // H·TEAM × line: QKV rows
-  static constexpr int ATT = QKV + H * TEAM * kLine;    // H × DK: attention output
-  static constexpr int XM = ATT + H * DK;               // kG × line: x_mid
-  static constexpr int HID = XM + kG * kLine;           // kG × line: F/kG values of h
-  static constexpr int PART = HID + kG * kLine;         // H·kMaxCh × PCH: chunk partials
-  static constexpr int ARG = PART + H * kMaxCh * PCH;   // kG × line: (best, index)
+  static constexpr int PCH = lines_of(DK + 2);   // one chunk's partial
+  static constexpr int SX = lines_of(D / kG);    // per producer: D/kG values of x (x_mid)
+  static constexpr int SQ = lines_of(3 * DK / TEAM);  // per team member: its QKV rows
+  static constexpr int SH = lines_of(F / kG);    // per producer: F/kG values of h
+  static constexpr int X = 0;
+  static constexpr int QKV = X + kG * SX;
+  static constexpr int ATT = QKV + H * TEAM * SQ;   // H × DK: attention output
+  static constexpr int XM = ATT + H * DK;
+  static constexpr int HID = XM + kG * SX;
+  static constexpr int PART = HID + kG * SH;        // H·kMaxCh × PCH: chunk partials
+  static constexpr int ARG = PART + H * kMaxCh * PCH;  // kG × line: (best, index)
   static constexpr int total = ARG + kG * kLine;
-  static_assert(D / kG <= kLine && F / kG <= kLine && 3 * DK / TEAM <= kLine, "lines");
   static_assert(ATT % kLine == 0 && (DK / 2) % kLine == 0, "line-aligned heads");
 };
 
@@ -211,19 +215,19 @@ __device__ __forceinline__ void gather(const u64* slots, uint32_t tag, T* dst, i
 }
 
 // dst[0..NPROD·VP) from a region where producer p keeps its VP values in SP = VP / PK
-// slots at p·kLine + s. Thread t takes slot t % SP of producers t / SP, t / SP + kT/SP,
-// …, so each wave's load instruction reads 64/SP whole producer lines.
-template <typename T, int NPROD, int VP, int PK>
+// slots at p·LS + s (LS: whole lines). Thread t takes slot t % SP of producers t / SP,
+// t / SP + kT/SP, …, so each wave's load instruction reads whole producer lines.
+template <typename T, int NPROD, int VP, int PK, int LS>
 __device__ __forceinline__ void gather_lines(const u64* region, uint32_t tag, T* dst, int* err,
                                              int& bad) {
   constexpr int SP = VP / PK;
-  static_assert(SP <= kLine && 64 % SP == 0, "slots per producer");
+  static_assert(SP <= LS && 64 % SP == 0, "slots per producer");
   constexpr int PPR = kT / SP;  // producers per round of the block's threads
   constexpr int PER = NPROD / PPR;
   static_assert(NPROD % PPR == 0, "gather shape");
   const int sl = threadIdx.x % SP, pq = threadIdx.x / SP;
   u64 v[PER];
-  poll_batch<PER>(region + pq * kLine + sl, PPR * kLine, tag, v, err, bad);
+  poll_batch<PER>(region + pq * LS + sl, PPR * LS, tag, v, err, bad);
 #pragma unroll
   for (int j = 0; j < PER; ++j)
     sink_payload<T, PK>(dst, (pq + PPR * j) * VP + sl * PK, static_cast<uint32_t>(v[j]));
@@ -406,7 +410,8 @@ __global__ __launch_bounds__(kT) void decode_persist_kernel(PersistArgs a) {
   constexpr int NPART = (kMaxCh * (DK + 2) + kT - 1) / kT;
   static_assert(H % kXcd == 0 && kG % H == 0 && (3 * DK) % TEAM == 0, "head teams");
   static_assert(D % kT == 0 && F % kT == 0 && D % kG == 0, "shapes");
-  static_assert(R_QKV == 4 * RW_QKV && R_WO == 4 && R_W2 == 4 && R_W1 == 4 * RW_W1 && RW_W1 % 2 == 0,
+  static_assert(R_QKV == 4 * RW_QKV && R_WO == 4 * RW_WO && R_W2 == 4 * RW_W2 && R_W1 == 4 * RW_W1 &&
+                    RW_W1 % 2 == 0,
                 "every wave owns whole rows (and W1 row pairs) of every phase");
   static_assert(DK % 32 == 0 && DK <= 128 && 3 * DK <= kT, "head dim");
 
@@ -491,7 +496,7 @@ __global__ __launch_bounds__(kT) void decode_persist_kernel(PersistArgs a) {
       for (int j = 0; j < D / kT; ++j) graw[j] = G1[tid + j * kT];
       NML_MARK(mk + 0);
       if (l > 0) {
-        gather_lines<T, kG, R_W2, 1>(X, tg, s_x, err, bad);
+        gather_lines<T, kG, R_W2, 1, SL::SX>(X, tg, s_x, err, bad);
         __syncthreads();
       }
       NML_MARK(mk + 1);
@@ -505,7 +510,7 @@ __global__ __launch_bounds__(kT) void decode_persist_kernel(PersistArgs a) {
         if (lane == 0 && rs.live[i]) {
           const float lin = rnd<T>(rnd<T>(acc) + static_cast<float>(braw[i]));
           const int r = rs.row[i];
-          put(QKV + (head * TEAM + tm) * kLine + wave + 4 * i, tg + 1, enc<T>(lin));
+          put(QKV + (head * TEAM + tm) * SL::SQ + wave + 4 * i, tg + 1, enc<T>(lin));
           const int part = r / D, j = r % DK;
           if (part > 0) {
             T* cache = static_cast<T*>(part == 1 ? a.kc : a.vc);
@@ -543,7 +548,7 @@ __global__ __launch_bounds__(kT) void decode_persist_kernel(PersistArgs a) {
           uint32_t pv[1];
           const int part = tid / DK, j = tid % DK;  // tid = row within the head's 3·DK
           idx[0] = (tid < DK || (owns_new && tid < 3 * DK))
-                       ? (head * TEAM + tid / R_QKV) * kLine + tid % R_QKV
+                       ? (head * TEAM + tid / R_QKV) * SL::SQ + tid % R_QKV
                        : -1;
           wait_slots<1>(QKV, idx, tg + 1, pv, err, bad);
           if (idx[0] >= 0) (part == 0 ? s_q : part == 1 ? s_kn : s_vn)[j] = static_cast<float>(dec<T>(pv[0]));
@@ -644,7 +649,7 @@ __global__ __launch_bounds__(kT) void decode_persist_kernel(PersistArgs a) {
         const float acc = wave_sum_dpp(dot_slice<T, D>(w[i], s_xn));
         if (lane == 0 && rs.live[i]) {
           const float lin = rnd<T>(rnd<T>(acc) + static_cast<float>(braw[i]));
-          put(XM + g * kLine + wave + 4 * i, tg + 4,
+          put(XM + g * SL::SX + wave + 4 * i, tg + 4,
               enc<T>(static_cast<float>(s_x[rs.row[i]]) + lin));
         }
       }
@@ -668,7 +673,7 @@ __global__ __launch_bounds__(kT) void decode_persist_kernel(PersistArgs a) {
       T graw[D / kT];
 #pragma unroll
       for (int j = 0; j < D / kT; ++j) graw[j] = G2[tid + j * kT];
-      gather_lines<T, kG, R_WO, 1>(XM, tg + 4, s_xm, err, bad);
+      gather_lines<T, kG, R_WO, 1, SL::SX>(XM, tg + 4, s_xm, err, bad);
       __syncthreads();
       NML_MARK(mk + 7);
       float gam[D / kT];
@@ -683,7 +688,7 @@ __global__ __launch_bounds__(kT) void decode_persist_kernel(PersistArgs a) {
           const float acc = wave_sum_dpp(dot_slice<T, D>(w[i + h], s_xn));
           v[h] = gelu_t<T>(rnd<T>(rnd<T>(acc) + static_cast<float>(braw[i + h])));
         }
-        if (lane == 0) put_pair<T>(HID + g * kLine, rs.row[i] - g * R_W1, tg + 5, v[0], v[1]);
+        if (lane == 0) put_pair<T>(HID + g * SL::SH, rs.row[i] - g * R_W1, tg + 5, v[0], v[1]);
       }
     }
     // ------------------------------------------------------------------ P5
@@ -701,7 +706,7 @@ __global__ __launch_bounds__(kT) void decode_persist_kernel(PersistArgs a) {
         load_row<T, F>(W, rs.row[i], w[i]);
         braw[i] = B2[rs.row[i]];
       }
-      gather_lines<T, kG, R_W1, kPack<T>>(HID, tg + 5, s_h, err, bad);
+      gather_lines<T, kG, R_W1, kPack<T>, SL::SH>(HID, tg + 5, s_h, err, bad);
       __syncthreads();
       NML_MARK(mk + 8);
 #pragma unroll
@@ -709,7 +714,7 @@ __global__ __launch_bounds__(kT) void decode_persist_kernel(PersistArgs a) {
         const float acc = wave_sum_dpp(dot_slice<T, F>(w[i], s_h));
         if (lane == 0 && rs.live[i]) {
           const float lin = rnd<T>(rnd<T>(acc) + static_cast<float>(braw[i]));
-          put(X + g * kLine + wave + 4 * i, tg + 8,
+          put(X + g * SL::SX + wave + 4 * i, tg + 8,
               enc<T>(static_cast<float>(s_xm[rs.row[i]]) + lin));
         }
       }
@@ -732,7 +737,7 @@ __global__ __launch_bounds__(kT) void decode_persist_kernel(PersistArgs a) {
     T graw[D / kT];
 #pragma unroll
     for (int j = 0; j < D / kT; ++j) graw[j] = static_cast<const T*>(a.lnf)[tid + j * kT];
-    gather_lines<T, kG, R_W2, 1>(X, tgh, s_x, err, bad);
+    gather_lines<T, kG, R_W2, 1, SL::SX>(X, tgh, s_x, err, bad);
     __syncthreads();
     NML_MARK(mh + 0);
     float gam[D / kT];
@@ -782,11 +787,11 @@ __global__ __launch_bounds__(kT) void decode_persist_kernel(PersistArgs a) {
   }
   if (g == 0) {
     __syncthreads();
-    int idx[2] = {tid * kLine, tid * kLine + 1};
+    int idx[2] = {tid < kG ? tid * kLine : -1, tid < kG ? tid * kLine + 1 : -1};
     uint32_t pv[2];
     wait_slots<2>(ARG, idx, tgh + 1, pv, err, bad);
-    float b = __uint_as_float(pv[0]);
-    int i = static_cast<int>(pv[1]);
+    float b = tid < kG ? __uint_as_float(pv[0]) : -INFINITY;
+    int i = tid < kG ? static_cast<int>(pv[1]) : 0x7fffffff;
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) {
       const float ob = __shfl_xor(b, o, 64);
