@@ -12,6 +12,8 @@
 //    16-byte loads along K, fp32 accumulation, wave-reduced.
 //  * skinny_f16: 8 < M ≤ 64 rows (batched decode), MFMA 16×16×32 with optional split-K
 //    and a fused RMSNorm of x (see its comment).
+#include <cstdlib>
+
 #include "kernels.hpp"
 
 namespace nml {
@@ -146,6 +148,178 @@ __global__ __launch_bounds__(256) void gemm_f16_kernel(LinearArgs a) {
         const int n = n0 + wn * 64 + j * 32 + (lane & 31);
         if (m < M && n < N) epilogue<half_t, EPI>(a, m, n, acc[i][j][r]);
       }
+}
+
+// ------------------------------------------------ fp16 MFMA GEMM, 256×256 block tile
+// For large M·N (prefill, compute_loss): a 512-lane workgroup owns a 256×256 tile; its
+// 8 waves (2×4, two per SIMD, so one multiplies while the other waits) each own
+// 128×64 = 4×2 MFMA 32×32×16 tiles (128 fp32 accumulators), so each A fragment read
+// from LDS feeds 2 MFMAs and each B fragment 4. K advances in stages of 32 through
+// a ring of 4 LDS buffers filled by direct-to-LDS loads (global_load_lds_dwordx4: lane
+// l of a wave writes bytes 16l…16l+15 of a 1 KiB block): three stages are in flight
+// while one is multiplied, and one barrier per stage both publishes a stage and frees
+// the buffer that the stage three ahead reuses.
+// The compiler cannot tell which ring buffer an LDS read touches, and it would wait for
+// every outstanding direct-to-LDS load before each one (and before every workgroup
+// barrier). So the waits are explicit here: a raw s_barrier, s_waitcnt vmcnt(n) for
+// exactly the stages issued after the one about to be read, and fragment reads as
+// ds_read_b128 statements whose results pass through the s_waitcnt lgkmcnt(0) that
+// guards them.
+// LDS rows are 64 B (32 halves); the 16-byte chunk c of row r sits at position
+// c ^ ((r / 4) & 3), so the 16 rows of one 256-byte bank cycle of a fragment read
+// cover all 64 banks. Workgroups are spread XCD-aware (workgroup b runs on XCD b % 8
+// and takes a contiguous range of tiles), grouped GM m-bands at a time so the
+// workgroups resident on one XCD share A bands and B tiles in its L2.
+constexpr int kHM = 256, kHN = 256, kHK = 32, kHStages = 4;
+constexpr int kHStageBytes = (kHM + kHN) * kHK * 2;  // 32 KiB: A then B
+
+__device__ __forceinline__ uint32_t swz_off(int row, int chunk) {
+  return static_cast<uint32_t>(row * 64 + ((chunk ^ ((row >> 2) & 3)) << 4));
+}
+
+__device__ __forceinline__ half8 lds_read16(uint32_t addr) {
+  half8 v;
+  asm volatile("ds_read_b128 %0, %1" : "=v"(v) : "v"(addr));
+  return v;
+}
+
+constexpr int kHT = 512;  // 8 waves: 2 per SIMD, so one multiplies while the other waits
+
+template <int EPI, int GM>
+__global__ __launch_bounds__(kHT, 1) void gemm_f16_big_kernel(LinearArgs a, int tiles_n, int tiles) {
+  extern __shared__ __attribute__((aligned(1024))) char lds_raw[];
+  const half_t* __restrict__ X = static_cast<const half_t*>(a.x);
+  const half_t* __restrict__ W = static_cast<const half_t*>(a.w);
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave >> 2, wn = wave & 3;  // 2 × 4 waves of 128 × 64
+  // XCD-aware tile order (tiles is a multiple of 8), GM m-bands per group
+  const int b = blockIdx.x;
+  const int t = (b & 7) * (tiles >> 3) + (b >> 3);
+  const int tiles_m = tiles / tiles_n;
+  const int group = t / (GM * tiles_n), first = group * GM;
+  const int gm = tiles_m - first < GM ? tiles_m - first : GM;
+  const int in = t - group * GM * tiles_n;
+  const int m0 = (first + in % gm) * kHM, n0 = (in / gm) * kHN;
+  const int M = a.M, N = a.N, K = a.K;
+  const long long lda = a.lda;
+  const uint32_t lds0 = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(lds_raw));
+
+  // Direct-to-LDS loads of one stage: A and B are 256 rows × 4 chunks each = 16 blocks
+  // of 16 rows; wave w issues blocks 2w, 2w+1 of each. Lane l of block q carries row
+  // 16q + l/4 at chunk position l % 4, i.e. global chunk (l % 4) ^ ((row / 4) & 3).
+  // Rows past M or N read row M-1 / N-1 (never stored).
+  const int lrow = lane >> 2, lpos = lane & 3;
+  auto issue = [&](int s) {
+    const int k0 = s * kHK;
+    char* stage = lds_raw + (s % kHStages) * kHStageBytes;
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int q = wave * 2 + j;
+      const int row = 16 * q + lrow;
+      const int ch = lpos ^ ((row >> 2) & 3);
+      const int gmr = m0 + row < M ? m0 + row : M - 1;
+      const int gnr = n0 + row < N ? n0 + row : N - 1;
+      // (address-space casts: global source, LDS destination)
+      __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)(X + gmr * lda + k0 + ch * 8),
+                                       (__attribute__((address_space(3))) void*)(stage + q * 1024), 16, 0, 0);
+      __builtin_amdgcn_global_load_lds(
+          (const __attribute__((address_space(1))) void*)(W + static_cast<long long>(gnr) * K + k0 + ch * 8),
+          (__attribute__((address_space(3))) void*)(stage + kHM * kHK * 2 + q * 1024), 16, 0, 0);
+    }
+  };
+
+  floatx16 acc[4][2];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
+
+  // per-lane fragment rows within a stage (the chunk is XORed in below)
+  uint32_t offa[4], offb[2];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) offa[i] = static_cast<uint32_t>(wm * 128 + i * 32 + (lane & 31));
+#pragma unroll
+  for (int j = 0; j < 2; ++j) offb[j] = static_cast<uint32_t>(wn * 64 + j * 32 + (lane & 31));
+
+  const int S = K / kHK;
+  for (int s = 0; s < kHStages - 1 && s < S; ++s) issue(s);
+  for (int s = 0; s < S; ++s) {
+    // this wave's loads of stage s have landed once at most the later stages' remain
+    const int later = (S - 1 < s + kHStages - 2 ? S - 1 : s + kHStages - 2) - s;
+    if (later >= 2)
+      asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
+    else if (later == 1)
+      asm volatile("s_waitcnt vmcnt(4)" ::: "memory");
+    else
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __builtin_amdgcn_s_barrier();  // every wave's loads of stage s landed; stage s-1 done
+    if (s + kHStages - 1 < S) issue(s + kHStages - 1);
+    const uint32_t base = lds0 + static_cast<uint32_t>((s % kHStages) * kHStageBytes);
+#pragma unroll
+    for (int kk = 0; kk < kHK / 16; ++kk) {
+      const int ch = 2 * kk + (lane >> 5);
+      half8 fa[4], fb[2];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) fa[i] = lds_read16(base + swz_off(offa[i], ch));
+#pragma unroll
+      for (int j = 0; j < 2; ++j) fb[j] = lds_read16(base + kHM * kHK * 2 + swz_off(offb[j], ch));
+      asm volatile("s_waitcnt lgkmcnt(0)"
+                   : "+v"(fa[0]), "+v"(fa[1]), "+v"(fa[2]), "+v"(fa[3]), "+v"(fb[0]), "+v"(fb[1]));
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(fa[i], fb[j], acc[i][j], 0, 0, 0);
+    }
+  }
+
+  // D layout of a 32×32 MFMA tile: lane l, register r → row 8(r/4) + 4(l/32) + r%4, col l%32.
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int m = m0 + wm * 128 + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+        const int n = n0 + wn * 64 + j * 32 + (lane & 31);
+        if (m < M && n < N) epilogue<half_t, EPI>(a, m, n, acc[i][j][r]);
+      }
+}
+
+constexpr size_t kBigLds = static_cast<size_t>(kHStages) * kHStageBytes;  // 128 KiB
+
+template <int EPI, int GM>
+int gemm_big_launch_gm(const LinearArgs& a, hipStream_t st) {
+  static bool attr = false;
+  if (!attr) {
+    NML_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(&gemm_f16_big_kernel<EPI, GM>),
+                                hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(kBigLds)));
+    attr = true;
+  }
+  const int tiles_n = (a.N + kHN - 1) / kHN, tiles_m = (a.M + kHM - 1) / kHM;
+  const int tiles = tiles_n * tiles_m;
+  gemm_f16_big_kernel<EPI, GM><<<tiles, kHT, kBigLds, st>>>(a, tiles_n, tiles);
+  NML_LAUNCHED();
+  return 0;
+}
+
+template <int EPI>
+int gemm_big_launch(const LinearArgs& a, hipStream_t st) {
+  const char* e = std::getenv("NIMBLEML_BIG_GM");
+  const int gm = e ? atoi(e) : 4;
+  if (gm == 1) return gemm_big_launch_gm<EPI, 1>(a, st);
+  if (gm == 8) return gemm_big_launch_gm<EPI, 8>(a, st);
+  return gemm_big_launch_gm<EPI, 4>(a, st);
+}
+
+bool big_gemm_applies(const LinearArgs& a) {
+  if (std::getenv("NIMBLEML_BIG_GEMM") && std::getenv("NIMBLEML_BIG_GEMM")[0] == '0') return false;
+  const long long tm = (a.M + kHM - 1) / kHM, tn = (a.N + kHN - 1) / kHN;
+  return a.K % kHK == 0 && a.lda % 8 == 0 && a.M >= 1024 && (tm * tn) % 8 == 0 && tm * tn >= 256 &&
+         (reinterpret_cast<uintptr_t>(a.x) & 15) == 0;
 }
 
 // ---------------------------------------------------------------- fp32 MFMA GEMM
@@ -536,6 +710,9 @@ int linear_typed(const LinearArgs& a, hipStream_t st) {
     if (a.M <= 2) return gemv_dispatch_rpw<T, EPI, 2>(a, st);
     if (a.M <= 4) return gemv_dispatch_rpw<T, EPI, 4>(a, st);
     return gemv_dispatch_rpw<T, EPI, 8>(a, st);
+  }
+  if constexpr (sizeof(T) == 2) {
+    if (big_gemm_applies(a)) return gemm_big_launch<EPI>(a, st);
   }
   dim3 grid((a.N + kBN - 1) / kBN, (a.M + kBM - 1) / kBM);
   if constexpr (sizeof(T) == 2)

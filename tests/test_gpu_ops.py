@@ -277,6 +277,34 @@ def test_linear_skinny_fp16(gpu, rows, k, epi):
     assert np.all(np.abs(out - want) <= tol), float(np.max(np.abs(out - want) / tol))
 
 
+@pytest.mark.parametrize("rows,k,n,epi", [(4096, 256, 4096, 0), (4096, 192, 4224, 1),
+                                          (4096, 128, 4224, 2), (3000, 256, 4224, 3)])
+def test_linear_big_tile_fp16(gpu, rows, k, n, epi):
+    """Prefill-sized shapes (≥ 256 tiles of 256×256): the large-tile MFMA GEMM, with a
+    ragged last column tile (n = 4224) and a ragged last row tile (rows = 3000)."""
+    rng = np.random.default_rng(rows + k + n + epi)
+    x = rng.standard_normal((rows, k)).astype(np.float16)
+    w = (rng.standard_normal((k, n)) * (1.0 / np.sqrt(k))).astype(np.float16)
+    b = rng.standard_normal(n).astype(np.float16)
+    r = rng.standard_normal((rows, n)).astype(np.float16)
+    out = np.asarray(_k().linear(x, w, b if epi else None, epilogue=epi,
+                                 resid=r if epi == 3 else None)).astype(np.float64)
+    acc = (x.astype(np.float64) @ w.astype(np.float64)).astype(np.float16)
+    lin = (acc + b).astype(np.float16) if epi else acc
+    if epi == 2:
+        lin = R.gelu(lin)
+    if epi == 3:
+        lin = (r + lin).astype(np.float16)
+    want = lin.astype(np.float64)
+    scale = np.abs(acc.astype(np.float64))
+    if epi:
+        scale = scale + np.abs(b.astype(np.float64))
+    if epi == 3:
+        scale = scale + np.abs(r.astype(np.float64))
+    tol = 2.0 * 2.0 ** -10 * (scale + np.abs(want)) + 1e-4
+    assert np.all(np.abs(out - want) <= tol), float(np.max(np.abs(out - want) / tol))
+
+
 @pytest.mark.parametrize("dk", [64, 128])
 def test_sdpa_mfma_long_fp16(gpu, dk):
     """The matrix-core flash kernel over many 64-key tiles and a ragged last query tile."""
