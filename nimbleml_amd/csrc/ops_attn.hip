@@ -438,6 +438,11 @@ __global__ __launch_bounds__(256) void attn_prefill_mfma_kernel(AttnArgs a) {
   const half_t* __restrict__ Vg = static_cast<const half_t*>(a.v) + b * a.kv_stride_b + h * a.kv_stride_h;
   const half_t* __restrict__ Qg = static_cast<const half_t*>(a.q) + static_cast<size_t>(bh) * S * DK;
   const float scale_t = static_cast<float>(static_cast<half_t>(a.scale));
+  // rnd(rnd(q·k) / s) for fp16 s = p / 2^e (DK 64: s = 8; DK 128: s = 181/16): the
+  // fp32 product with the correctly rounded reciprocal rounds to the same fp16 value —
+  // the exact quotient of an fp16 by s is never within 2^-19 (relative) of an fp16
+  // rounding midpoint, far beyond the product's 2^-23 error.
+  const float rscale = 1.0f / scale_t;
   const int qw = q0 + wave * 32;           // first query of this wave
   const int myq = qw + (lane & 31);        // this lane's query
   const int hi = lane >> 5;                // which half of the wave
@@ -518,16 +523,27 @@ __global__ __launch_bounds__(256) void attn_prefill_mfma_kernel(AttnArgs a) {
       }
     }
     float mx = m;
+    if (k0 + kFK - 1 > base + qw) {  // the tile reaches past some query of this wave: mask
 #pragma unroll
-    for (int t = 0; t < 2; ++t)
+      for (int t = 0; t < 2; ++t)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int key = k0 + t * 32 + 8 * (r >> 2) + 4 * hi + (r & 3);
-        const float sv = rnd<half_t>(rnd<half_t>(st[t][r]) / scale_t);
-        const float s = (key <= qpos && key < kend) ? sv : -INFINITY;
-        st[t][r] = s;
-        mx = fmaxf(mx, s);
-      }
+        for (int r = 0; r < 16; ++r) {
+          const int key = k0 + t * 32 + 8 * (r >> 2) + 4 * hi + (r & 3);
+          const float sv = rnd<half_t>(rnd<half_t>(st[t][r]) * rscale);
+          const float s = (key <= qpos && key < kend) ? sv : -INFINITY;
+          st[t][r] = s;
+          mx = fmaxf(mx, s);
+        }
+    } else {  // every key of the tile precedes every query of the wave
+#pragma unroll
+      for (int t = 0; t < 2; ++t)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const float s = rnd<half_t>(rnd<half_t>(st[t][r]) * rscale);
+          st[t][r] = s;
+          mx = fmaxf(mx, s);
+        }
+    }
     mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
     constexpr float kLog2e = 1.4426950408889634f;
     const float alpha = (mx == -INFINITY) ? 1.f : __builtin_amdgcn_exp2f((m - mx) * kLog2e);
@@ -543,8 +559,9 @@ __global__ __launch_bounds__(256) void attn_prefill_mfma_kernel(AttnArgs a) {
         half8 pb;
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
-          const float s = st[t][8 * kb + j];
-          const float p = (s == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f((s - mx) * kLog2e);
+          // mx is finite (key 0 precedes every query, and tiles run from key 0), so a
+          // masked score gives exp2(-inf) = 0
+          const float p = __builtin_amdgcn_exp2f((st[t][8 * kb + j] - mx) * kLog2e);
           l += p;
           pb[j] = static_cast<half_t>(p);
         }

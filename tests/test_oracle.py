@@ -249,3 +249,17 @@ def test_weight_names_match_reference_layout():
     assert names[0] == "token_emb.weights" and names[-1] == "ln.gamma"
     assert "blocks.layers.2.ffn.dense2.biases" in names
     assert len(names) == 3 + 14 * 3
+
+
+@pytest.mark.parametrize("dk", [64, 128])
+def test_score_division_by_reciprocal_is_exact_fp16(dk):
+    """The MFMA attention kernel computes the fp16 score rnd(rnd(q·k) / s) as
+    rnd(x · (1/s)) in fp32 (x = rnd(q·k), s = fp16(sqrt(dk))). Over every finite fp16 x
+    this equals the correctly rounded quotient, which is what NumPy's fp16 division in
+    the reference gives."""
+    x = np.arange(65536, dtype=np.uint16).view(np.float16)
+    x = x[np.isfinite(x)]
+    s = np.float16(np.sqrt(dk))
+    want = (x.astype(np.float64) / np.float64(s)).astype(np.float16)
+    got = (x.astype(np.float32) * (np.float32(1.0) / np.float32(s))).astype(np.float16)
+    assert np.array_equal(want.view(np.uint16), got.view(np.uint16))
