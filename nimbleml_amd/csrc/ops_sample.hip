@@ -178,59 +178,44 @@ __device__ uint32_t select_kth_key(int V, int k, F key_of, Shared& sh) {
   return prefix;
 }
 
-// Top-k sampling without top-p (generate.py:43-47, then RandomState.choice): every
-// element below the k-th largest scaled logit becomes -1e9, whose exp(x − max)
-// underflows to exactly 0, so only the candidates x ≥ threshold carry mass. They are
-// gathered in index order and the max, Σ exp, probabilities and the float64
-// index-order CDF are taken over them; returns the first candidate index whose
-// cdf / total exceeds u (V − 1 if rounding leaves none, as the full scan does), or
-// -1 when the candidates do not fit (the caller then runs the full scan).
+// Most candidates (elements ≥ a top-k threshold or its lower bound) held in LDS.
 constexpr int kCandMax = 2048;
 
+// Wave 0 draws over n candidates (index order, candx = scaled logits) keeping those
+// ≥ thresh: max, Σ exp, probabilities and the float64 index-order CDF; returns the first
+// kept index whose cdf / total exceeds u (V − 1 if rounding leaves none, as the full
+// scan does). All threads must call it (barriers).
 template <typename T>
-__device__ int sample_topk_candidates(const Row<T>& row, float thresh, double u, Shared& sh,
-                                      int* cand, float* candx) {
-  const int V = row.V;
-  const int seg = (V + kThreads - 1) / kThreads;
-  const int lo = threadIdx.x * seg, hi = min(V, lo + seg);
-  int c = 0;
-  for (int i = lo; i < hi; ++i) c += row.scaled(i) >= thresh ? 1 : 0;
-  int n = 0;
-  int off = block_excl_scan_i(c, &n, sh);
-  if (n > kCandMax) return -1;
-  for (int i = lo; i < hi; ++i) {
-    const float x = row.scaled(i);
-    if (x >= thresh) {
-      cand[off] = i;
-      candx[off] = x;
-      ++off;
-    }
-  }
-  __syncthreads();
+__device__ int draw_candidates(int V, int n, float thresh, double u, Shared& sh, const int* cand,
+                               const float* candx) {
   if (threadIdx.x < 64) {
     const int l = threadIdx.x;
     float mx = -INFINITY;
-    for (int j = l; j < n; j += 64) mx = fmaxf(mx, candx[j]);
+    for (int j = l; j < n; j += 64)
+      if (candx[j] >= thresh) mx = fmaxf(mx, candx[j]);
     mx = wave_max(mx);
     float se = 0.f;
-    for (int j = l; j < n; j += 64) se += expf(candx[j] - mx);
+    for (int j = l; j < n; j += 64)
+      if (candx[j] >= thresh) se += expf(candx[j] - mx);
     se = wave_sum(se);
     double total = 0.0;
-    for (int j = l; j < n; j += 64) total += static_cast<double>(expf(candx[j] - mx) / se);
+    for (int j = l; j < n; j += 64)
+      if (candx[j] >= thresh) total += static_cast<double>(expf(candx[j] - mx) / se);
     total = wave_sum_d(total);
     // index-order running sums, 64 candidates per round
     double carry = 0.0;
     int found = 0x7fffffff;
     for (int j0 = 0; j0 < n && found == 0x7fffffff; j0 += 64) {
       const int j = j0 + l;
-      const double pj = j < n ? static_cast<double>(expf(candx[j] - mx) / se) : 0.0;
+      const bool keep = j < n && candx[j] >= thresh;
+      const double pj = keep ? static_cast<double>(expf(candx[j] - mx) / se) : 0.0;
       double inc = pj;
 #pragma unroll
       for (int o = 1; o < 64; o <<= 1) {
         const double t = __shfl_up(inc, o, 64);
         if (l >= o) inc += t;
       }
-      const bool hit = j < n && (carry + inc) / total > u;
+      const bool hit = keep && (carry + inc) / total > u;
       const unsigned long long hits = __ballot(hit);
       if (hits) found = cand[j0 + __ffsll(static_cast<long long>(hits)) - 1];
       carry += __shfl(inc, 63, 64);
@@ -239,6 +224,65 @@ __device__ int sample_topk_candidates(const Row<T>& row, float thresh, double u,
   }
   __syncthreads();
   return sh.found_index;
+}
+
+// Gather the elements with scaled logit ≥ lo into cand / candx in index order; returns
+// their count, or -1 if more than kCandMax.
+template <typename T>
+__device__ int gather_candidates(const Row<T>& row, float lo, Shared& sh, int* cand, float* candx) {
+  const int V = row.V;
+  const int seg = (V + kThreads - 1) / kThreads;
+  const int b0 = threadIdx.x * seg, b1 = min(V, b0 + seg);
+  int c = 0;
+  for (int i = b0; i < b1; ++i) c += row.scaled(i) >= lo ? 1 : 0;
+  int n = 0;
+  int off = block_excl_scan_i(c, &n, sh);
+  if (n > kCandMax) return -1;
+  for (int i = b0; i < b1; ++i) {
+    const float x = row.scaled(i);
+    if (x >= lo) {
+      cand[off] = i;
+      candx[off] = x;
+      ++off;
+    }
+  }
+  __syncthreads();
+  return n;
+}
+
+// Top-k sampling without top-p (generate.py:43-47, then RandomState.choice): every
+// element below the k-th largest scaled logit T becomes -1e9, whose exp(x − max)
+// underflows to exactly 0, so only the elements ≥ T carry mass. T is found without a
+// pass over the whole row per radix digit: the k-th largest of the 1024 per-thread
+// maxima is a lower bound L ≤ T (at most k threads can hold an element ≥ T), the
+// elements ≥ L are gathered (all of the top k among them), and T is selected among
+// those. Returns the chosen index, or -1 (k > 1024 or too many candidates: the caller
+// runs the full scan).
+template <typename T>
+__device__ int sample_topk_fast(const Row<T>& row, int k, double u, Shared& sh, int* cand,
+                                float* candx, uint32_t* tkeys) {
+  const int V = row.V;
+  if (k > kThreads) return -1;
+  float tm = -INFINITY;
+  for (int i = threadIdx.x; i < V; i += kThreads) tm = fmaxf(tm, row.scaled(i));
+  tkeys[threadIdx.x] = fkey(tm);
+  __syncthreads();
+  const uint32_t lk = select_kth_key(kThreads, k, [&](int i) { return tkeys[i]; }, sh);
+  const float lo = __uint_as_float((lk & 0x80000000u) ? (lk & 0x7fffffffu) : ~lk);
+  const int n = gather_candidates(row, lo, sh, cand, candx);
+  if (n < 0) return -1;
+  const uint32_t tk = select_kth_key(n, k, [&](int j) { return fkey(candx[j]); }, sh);
+  const float thresh = __uint_as_float((tk & 0x80000000u) ? (tk & 0x7fffffffu) : ~tk);
+  return draw_candidates<T>(V, n, thresh, u, sh, cand, candx);
+}
+
+// The same draw with T already known (the full-scan path): gathers the elements ≥ T.
+template <typename T>
+__device__ int sample_topk_candidates(const Row<T>& row, float thresh, double u, Shared& sh,
+                                      int* cand, float* candx) {
+  const int n = gather_candidates(row, thresh, sh, cand, candx);
+  if (n < 0) return -1;
+  return draw_candidates<T>(row.V, n, thresh, u, sh, cand, candx);
 }
 
 // First position of the descending order (key desc, then index desc) over the
@@ -328,17 +372,41 @@ __device__ int find_nth(int V, int j, FP pred, Shared& sh) {
   return sh.found_index;
 }
 
+// Logits rows up to this size (V ≤ 51,456 fp16 entries) are staged in LDS once, so the
+// selection passes re-read LDS rather than HBM/L2.
+constexpr int kRowCacheBytes = 100 * 1024 + 512;
+
 template <typename T>
 __global__ __launch_bounds__(kThreads) void sample_kernel(SampleArgs a) {
   __shared__ Shared sh;
+  __shared__ __attribute__((aligned(16))) char s_row[kRowCacheBytes];
   __shared__ int s_cand[kCandMax];
   __shared__ float s_candx[kCandMax];
+  __shared__ uint32_t s_tkeys[kThreads];
   const int b = blockIdx.x;
   const int V = a.V;
   const bool gen = a.pos != nullptr;
   const int p_cur = gen ? a.pos[b] : (a.hist_len ? a.hist_len[b] - 1 : -1);
   Row<T> row;
   row.lg = static_cast<const T*>(a.logits) + b * a.logits_stride;
+  // The selection passes re-read the row many times: with room for it, stage it in LDS
+  // once (all 16-byte loads of the row in flight together) and let every pass read LDS.
+  if (a.V * static_cast<int>(sizeof(T)) <= kRowCacheBytes) {
+    T* cache = reinterpret_cast<T*>(s_row);
+    constexpr int E = 16 / sizeof(T);
+    const int nv = a.V / E;
+    const bool aligned = (reinterpret_cast<uintptr_t>(row.lg) & 15) == 0;
+    if (aligned) {
+      typedef int iv4 __attribute__((ext_vector_type(4)));
+      for (int i = threadIdx.x; i < nv; i += kThreads)
+        reinterpret_cast<iv4*>(cache)[i] = reinterpret_cast<const iv4*>(row.lg)[i];
+      for (int i = nv * E + threadIdx.x; i < a.V; i += kThreads) cache[i] = row.lg[i];
+    } else {
+      for (int i = threadIdx.x; i < a.V; i += kThreads) cache[i] = row.lg[i];
+    }
+    __syncthreads();
+    row.lg = cache;
+  }
   row.V = V;
   row.pen = a.rep_penalty;
   row.temperature = a.temperature;
@@ -399,10 +467,14 @@ __global__ __launch_bounds__(kThreads) void sample_kernel(SampleArgs a) {
   } else {
     const long long ui = gen ? static_cast<long long>(p_cur + 1 - a.plen[b]) * a.B + b : b;
     const double u = a.uniforms[ui];
-    // top-k threshold on the temperature-scaled logits
+    const bool use_p = a.top_p > 0.f && a.top_p < 1.f;
     bool use_k = a.top_k > 0;
+    chosen = -1;
+    if (use_k && !use_p)
+      chosen = sample_topk_fast(row, a.top_k < V ? a.top_k : V, u, sh, s_cand, s_candx, s_tkeys);
+    // top-k threshold on the temperature-scaled logits
     float thresh = -INFINITY;
-    if (use_k) {
+    if (use_k && chosen < 0) {
       const int k = a.top_k < V ? a.top_k : V;
       const uint32_t tk = select_kth_key(V, k, [&](int i) { return fkey(row.scaled(i)); }, sh);
       const uint32_t bits = (tk & 0x80000000u) ? (tk & 0x7fffffffu) : ~tk;
@@ -421,9 +493,7 @@ __global__ __launch_bounds__(kThreads) void sample_kernel(SampleArgs a) {
     auto prob = [&](int i) { return expf(xm(i) - mx) / se; };
     auto keyp = [&](int i) { return fkey(prob(i)); };
 
-    const bool use_p = a.top_p > 0.f && a.top_p < 1.f;
-    chosen = -1;
-    if (use_k && !use_p) chosen = sample_topk_candidates(row, thresh, u, sh, s_cand, s_candx);
+    if (use_k && !use_p && chosen < 0) chosen = sample_topk_candidates(row, thresh, u, sh, s_cand, s_candx);
     if (chosen >= 0) {
       // sampled among the top-k candidates
     } else if (use_p) {
