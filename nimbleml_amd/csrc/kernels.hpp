@@ -33,6 +33,9 @@ struct QKVDst {
   long long kv_stride_b;
   long long kv_stride_h;
   int S, H, dk, d;
+  // Packed ragged rows: row m is position s of sequence b, row_seg[m] = (b << 16) | s
+  // (s < 65536); q keeps the padded (B, H, S, dk) layout. Null: b = m / S, s = m % S.
+  const int32_t* row_seg;
 };
 
 struct LinearArgs {
@@ -88,6 +91,10 @@ struct AttnArgs {
   long long kv_stride_b, kv_stride_h;
   int B, H, S, dk;
   float scale;  // the reference's sqrt(dk) divisor (attention.py:135)
+  // Ragged prefill: sequence b has seq_len[b] ≤ S queries (q stays padded to S per
+  // (b, head)) and its output rows start at row_start[b]. Null: S each, rows b·S + s.
+  const int32_t* seq_len;
+  const int32_t* row_start;
 };
 int launch_attention_prefill(int dt, const AttnArgs& a, hipStream_t st);
 

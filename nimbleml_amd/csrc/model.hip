@@ -64,6 +64,7 @@ struct nml_model {
   Buf logits_ws;  // logits chunk for compute_loss / generate
   Buf small;      // device counters, positions, loss accumulators
   Buf persist;    // persistent decode: layer pointer table, exchange slots, epoch
+  Buf ragged;     // packed ragged prefill: row table, lengths, row starts
   // decode timing of the last generate()
   float last_decode_ms = 0.f;
   int last_decode_steps = 0;
@@ -184,13 +185,24 @@ struct KVView {
   long long sb, sh;
 };
 
-// The transformer trunk over R = B·S rows already embedded in acts.x. Leaves the
-// final-normed hidden states in acts.xn. pos_base (device, B) gives each row's
-// first position (null → 0); kv(l) gives layer l's K/V destination.
+// Sequences of different lengths packed row after row (device arrays): row r is
+// position s of sequence b with row_seg[r] = (b << 16) | s; sequence b has seq_len[b]
+// rows starting at row_start[b]; R rows in all.
+struct Ragged {
+  const int32_t* row_seg;
+  const int32_t* seq_len;
+  const int32_t* row_start;
+  int R;
+};
+
+// The transformer trunk over R = B·S rows already embedded in acts.x (or rg->R packed
+// ragged rows, S then being the longest length). Leaves the final-normed hidden states
+// in acts.xn. pos_base (device, B) gives each row's first position (null → 0); kv(l)
+// gives layer l's K/V destination.
 template <typename KVF>
 int trunk(nml_model* m, const Acts& a, int B, int S, const int32_t* pos_base, KVF kv,
-          hipStream_t st) {
-  const int R = B * S, d = m->d;
+          hipStream_t st, const Ragged* rg = nullptr) {
+  const int R = rg ? rg->R : B * S, d = m->d;
   for (int l = 0; l < m->L; ++l) {
     const Layer& w = m->layers[l];
     const KVView c = kv(l);
@@ -204,7 +216,8 @@ int trunk(nml_model* m, const Acts& a, int B, int S, const int32_t* pos_base, KV
     qkv.N = 3 * d;
     qkv.K = d;
     qkv.epi = EPI_QKV;
-    qkv.qkv = QKVDst{a.q, c.k, c.v, pos_base, c.sb, c.sh, S, m->H, m->dk, d};
+    qkv.qkv = QKVDst{a.q, c.k, c.v, pos_base, c.sb, c.sh, S, m->H, m->dk, d,
+                     rg ? rg->row_seg : nullptr};
     NML_TRY(launch_linear(m->dt, qkv, st));
     AttnArgs at{};
     at.q = a.q;
@@ -219,6 +232,10 @@ int trunk(nml_model* m, const Acts& a, int B, int S, const int32_t* pos_base, KV
     at.S = S;
     at.dk = m->dk;
     at.scale = sqrtf((float)m->dk);
+    if (rg) {
+      at.seq_len = rg->seq_len;
+      at.row_start = rg->row_start;
+    }
     NML_TRY(launch_attention_prefill(m->dt, at, st));
     LinearArgs wo{};
     wo.x = a.att;
@@ -457,6 +474,19 @@ __global__ void add_scalar_kernel(int32_t* p, int n, int v) {
   if (i < n) p[i] += v;
 }
 
+// dst row b = src row row_start[b] + seq_len[b] − 1 (the last position of each packed
+// sequence), rows of `bytes` bytes, a multiple of 16.
+__global__ void gather_last_rows_kernel(const char* __restrict__ src, const int32_t* __restrict__ row_start,
+                                        const int32_t* __restrict__ seq_len, char* __restrict__ dst,
+                                        int bytes) {
+  typedef int iv4 __attribute__((ext_vector_type(4)));
+  const int b = blockIdx.x;
+  const size_t r = static_cast<size_t>(row_start[b]) + seq_len[b] - 1;
+  const iv4* s = reinterpret_cast<const iv4*>(src + r * bytes);
+  iv4* o = reinterpret_cast<iv4*>(dst + static_cast<size_t>(b) * bytes);
+  for (int i = threadIdx.x; i < bytes / 16; i += blockDim.x) o[i] = s[i];
+}
+
 __global__ void copy_rows_kernel(const int64_t* __restrict__ src, long long sstride,
                                  int64_t* __restrict__ dst, long long dstride,
                                  const int32_t* __restrict__ lens) {
@@ -532,6 +562,7 @@ int nml_model_destroy(nml_model* m) {
   m->logits_ws.release();
   m->small.release();
   m->persist.release();
+  m->ragged.release();
   if (m->arena) (void)hipFree(m->arena);
   delete m;
   return 0;
@@ -753,7 +784,8 @@ int nml_model_generate(nml_model* m, const int64_t* prompts, size_t prompt_strid
   NML_TRY(m->logits_ws.ensure(lb));
   void* logits = m->logits_ws.p;
 
-  // Prefill: one batched pass when all prompts have the same length, else per row.
+  // Prefill: one batched pass; prompts of different lengths are packed row after row
+  // (the GEMMs see Σ prompt_len rows, attention runs per sequence over its own length).
   const size_t layer_kv = (size_t)B * m->H * m->P * m->dk * m->es;
   const long long sb = (long long)m->H * m->P * m->dk, sh = (long long)m->P * m->dk;
   NML_HIP(hipMemsetAsync(sm.zeros, 0, B * 4, st));
@@ -778,21 +810,43 @@ int nml_model_generate(nml_model* m, const int64_t* prompts, size_t prompt_strid
                   st));
     NML_TRY(head(m, a, B, S, logits, 1, st));
   } else {
-    for (int b = 0; b < B; ++b) {
-      const int S = plen[b];
-      Acts a;
-      NML_TRY(acts_for(m, S, B, &a));
+    // Packed rows: (b << 16) | s per row, then the lengths and row starts.
+    std::vector<int32_t> tab;
+    int R = 0;
+    for (int b = 0; b < B; ++b) R += plen[b];
+    NML_REQUIRE(maxp < 65536 && B < 32768, "ragged prefill: %d prompts up to %d long", B, maxp);
+    NML_REQUIRE(((size_t)m->d * m->es) % 16 == 0, "ragged prefill: row of %d not 16-byte sized", m->d);
+    tab.reserve((size_t)R + 2 * B + 1);
+    for (int b = 0; b < B; ++b)
+      for (int s = 0; s < plen[b]; ++s) tab.push_back((b << 16) | s);
+    tab.insert(tab.end(), plen.begin(), plen.end());
+    std::vector<int32_t> starts(B);
+    for (int b = 0, r = 0; b < B; r += plen[b], ++b) starts[b] = r;
+    tab.insert(tab.end(), starts.begin(), starts.end());
+    NML_TRY(m->ragged.ensure(tab.size() * 4));
+    const int32_t* dtab = static_cast<const int32_t*>(m->ragged.p);
+    NML_HIP(hipMemcpyAsync(m->ragged.p, tab.data(), tab.size() * 4, hipMemcpyHostToDevice, st));
+    const Ragged rg{dtab, dtab + R, dtab + R + B, R};
+    // activations sized for the padded (B, maxp) query layout
+    Acts a;
+    NML_TRY(acts_for(m, B * maxp, B, &a));
+    for (int b = 0; b < B; ++b)
       NML_TRY(launch_embed(m->dt, prompts + (size_t)b * prompt_stride, m->emb, m->pos, nullptr,
-                           a.x, 1, S, m->d, m->V, m->P, sm.err, st));
-      NML_TRY(trunk(m, a, 1, S, sm.zeros,
-                    [&](int l) {
-                      return KVView{static_cast<char*>(c->k) + l * layer_kv + b * sb * m->es,
-                                    static_cast<char*>(c->v) + l * layer_kv + b * sb * m->es, sb,
-                                    sh};
-                    },
-                    st));
-      NML_TRY(head(m, a, 1, S, static_cast<char*>(logits) + (size_t)b * m->V * m->es, 1, st));
-    }
+                           static_cast<char*>(a.x) + (size_t)starts[b] * m->d * m->es, 1, plen[b],
+                           m->d, m->V, m->P, sm.err, st));
+    NML_TRY(trunk(m, a, B, maxp, sm.zeros,
+                  [&](int l) {
+                    return KVView{static_cast<char*>(c->k) + l * layer_kv,
+                                  static_cast<char*>(c->v) + l * layer_kv, sb, sh};
+                  },
+                  st, &rg));
+    gather_last_rows_kernel<<<B, 128, 0, st>>>(static_cast<const char*>(a.xn), rg.row_start,
+                                               rg.seq_len, static_cast<char*>(a.att),
+                                               m->d * (int)m->es);
+    NML_LAUNCHED();
+    Acts last = a;
+    last.xn = a.att;
+    NML_TRY(head(m, last, B, 1, logits, 1, st));
   }
   // pos[b] = prompt_len[b] − 1, then the first choice advances it to prompt_len[b].
   std::vector<int32_t> pos0(B);

@@ -34,16 +34,18 @@ __global__ __launch_bounds__(64) void attn_prefill_kernel(AttnArgs a) {
   const int bh = blockIdx.y;
   const int b = bh / a.H, h = bh - (bh / a.H) * a.H;
   const int s = blockIdx.x * kTile + lane;
+  const int S = a.seq_len ? a.seq_len[b] : a.S;
+  if (static_cast<int>(blockIdx.x) * kTile >= S) return;  // past a ragged sequence's end
   const int base = a.pos_base ? a.pos_base[b] : 0;
   const int qpos = base + s;
-  const int last_s = min(a.S, (blockIdx.x + 1) * kTile) - 1;
+  const int last_s = min(S, (blockIdx.x + 1) * kTile) - 1;
   const int kv_end = base + last_s + 1;
   const float scale_t = static_cast<float>(static_cast<T>(a.scale));
   const T* __restrict__ K = static_cast<const T*>(a.k) + b * a.kv_stride_b + h * a.kv_stride_h;
   const T* __restrict__ Vp = static_cast<const T*>(a.v) + b * a.kv_stride_b + h * a.kv_stride_h;
 
   float q[DK];
-  const bool valid = s < a.S;
+  const bool valid = s < S;
   {
     const T* qp = static_cast<const T*>(a.q) + ((static_cast<size_t>(bh) * a.S) + (valid ? s : 0)) * DK;
 #pragma unroll
@@ -103,7 +105,8 @@ __global__ __launch_bounds__(64) void attn_prefill_kernel(AttnArgs a) {
   }
   if (valid) {
     const int hd = a.H * DK;
-    T* out = static_cast<T*>(a.out) + (static_cast<size_t>(b) * a.S + s) * hd + h * DK;
+    const size_t row = (a.row_start ? a.row_start[b] : static_cast<size_t>(b) * a.S) + s;
+    T* out = static_cast<T*>(a.out) + row * hd + h * DK;
     const float inv = 1.f / l;
 #pragma unroll
     for (int d = 0; d < DK; ++d) out[d] = static_cast<T>(o[d] * inv);
@@ -431,12 +434,13 @@ __global__ __launch_bounds__(256) void attn_prefill_mfma_kernel(AttnArgs a) {
     qt = slot % nq;
   }
   const int b = bh / a.H, h = bh - (bh / a.H) * a.H;
-  const int S = a.S;
+  const int S = a.seq_len ? a.seq_len[b] : a.S;
   const int q0 = (nq - 1 - qt) * kFQ;
+  if (q0 >= S) return;  // past a ragged sequence's end (uniform over the workgroup)
   const int base = a.pos_base ? a.pos_base[b] : 0;
   const half_t* __restrict__ Kg = static_cast<const half_t*>(a.k) + b * a.kv_stride_b + h * a.kv_stride_h;
   const half_t* __restrict__ Vg = static_cast<const half_t*>(a.v) + b * a.kv_stride_b + h * a.kv_stride_h;
-  const half_t* __restrict__ Qg = static_cast<const half_t*>(a.q) + static_cast<size_t>(bh) * S * DK;
+  const half_t* __restrict__ Qg = static_cast<const half_t*>(a.q) + static_cast<size_t>(bh) * a.S * DK;
   const float scale_t = static_cast<float>(static_cast<half_t>(a.scale));
   // rnd(rnd(q·k) / s) for fp16 s = p / 2^e (DK 64: s = 8; DK 128: s = 181/16): the
   // fp32 product with the correctly rounded reciprocal rounds to the same fp16 value —
@@ -584,7 +588,8 @@ __global__ __launch_bounds__(256) void attn_prefill_mfma_kernel(AttnArgs a) {
   if (myq < S) {
     const float inv = 1.f / l;
     const int hd = a.H * DK;
-    half_t* out = static_cast<half_t*>(a.out) + (static_cast<size_t>(b) * S + myq) * hd + h * DK;
+    const size_t row = (a.row_start ? a.row_start[b] : static_cast<size_t>(b) * S) + myq;
+    half_t* out = static_cast<half_t*>(a.out) + row * hd + h * DK;
 #pragma unroll
     for (int ot = 0; ot < OT; ++ot)
 #pragma unroll

@@ -46,7 +46,15 @@ __device__ __forceinline__ float epilogue(const LinearArgs& a, int m, int n, flo
       const int which = n / q.d;
       const int within = n - which * q.d;
       const int h = within / q.dk, j = within - h * q.dk;
-      const int b = m / q.S, s = m - b * q.S;
+      int b, s;
+      if (q.row_seg) {
+        const int rs = q.row_seg[m];
+        b = rs >> 16;
+        s = rs & 0xffff;
+      } else {
+        b = m / q.S;
+        s = m - b * q.S;
+      }
       if (which == 0) {
         T* qp = static_cast<T*>(q.q);
         qp[((static_cast<size_t>(b) * q.H + h) * q.S + s) * q.dk + j] = static_cast<T>(lin);
@@ -767,7 +775,7 @@ int launch_linear(int dt, const LinearArgs& a, hipStream_t st) {
   NML_REQUIRE(a.epi == EPI_NONE || a.bias != nullptr, "linear: epilogue %d needs a bias", a.epi);
   NML_REQUIRE(a.epi != EPI_BIAS_RESID || a.resid != nullptr, "linear: residual pointer missing");
   NML_REQUIRE(a.epi != EPI_QKV || (a.qkv.d > 0 && a.qkv.dk > 0 && a.N == 3 * a.qkv.d &&
-                                   a.M == a.qkv.S * (a.M / a.qkv.S)),
+                                   (a.qkv.row_seg || a.M == a.qkv.S * (a.M / a.qkv.S))),
               "linear: bad QKV destination");
   NML_REQUIRE(!a.ssq_in || (a.norm_g != nullptr && linear_norm_fusable(dt, a.M, a.K, a.N)),
               "linear: fused RMSNorm needs a gain and the fp16 skinny shape");
