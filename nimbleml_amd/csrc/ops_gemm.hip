@@ -20,16 +20,18 @@ namespace nml {
 
 namespace {
 
-// Stores the output element (m, n) and returns its stored value.
+// Stores the output element (m, n) and returns its stored value, given the bias b[n]
+// and residual r[m][n] as floats (ignored by the epilogues that do not use them).
 template <typename T, int EPI>
-__device__ __forceinline__ float epilogue(const LinearArgs& a, int m, int n, float acc) {
+__device__ __forceinline__ float epilogue_with(const LinearArgs& a, int m, int n, float acc,
+                                               float bias_v, float resid_v) {
   T* out = static_cast<T*>(a.out);
   const size_t idx = static_cast<size_t>(m) * a.N + n;
   if constexpr (EPI == EPI_NONE) {
     out[idx] = static_cast<T>(acc);
     return rnd<T>(acc);
   } else {
-    const float lin = rnd<T>(rnd<T>(acc) + static_cast<float>(static_cast<const T*>(a.bias)[n]));
+    const float lin = rnd<T>(rnd<T>(acc) + bias_v);
     if constexpr (EPI == EPI_BIAS) {
       out[idx] = static_cast<T>(lin);
       return lin;
@@ -38,7 +40,7 @@ __device__ __forceinline__ float epilogue(const LinearArgs& a, int m, int n, flo
       out[idx] = static_cast<T>(v);
       return v;
     } else if constexpr (EPI == EPI_BIAS_RESID) {
-      const float v = rnd<T>(static_cast<float>(static_cast<const T*>(a.resid)[idx]) + lin);
+      const float v = rnd<T>(resid_v + lin);
       out[idx] = static_cast<T>(v);
       return v;
     } else {  // EPI_QKV
@@ -67,6 +69,15 @@ __device__ __forceinline__ float epilogue(const LinearArgs& a, int m, int n, flo
       return lin;
     }
   }
+}
+
+template <typename T, int EPI>
+__device__ __forceinline__ float epilogue(const LinearArgs& a, int m, int n, float acc) {
+  float bias_v = 0.f, resid_v = 0.f;
+  if constexpr (EPI != EPI_NONE) bias_v = static_cast<float>(static_cast<const T*>(a.bias)[n]);
+  if constexpr (EPI == EPI_BIAS_RESID)
+    resid_v = static_cast<float>(static_cast<const T*>(a.resid)[static_cast<size_t>(m) * a.N + n]);
+  return epilogue_with<T, EPI>(a, m, n, acc, bias_v, resid_v);
 }
 
 constexpr int kBM = 128, kBN = 128;
@@ -525,7 +536,6 @@ template <int EPI, int MT, int U, bool NORM>
 __global__ __launch_bounds__(256) void skinny_f16_kernel(LinearArgs a, unsigned long long* ws) {
 #pragma clang fp contract(off)
   __shared__ float red[4][MT][16][17];
-  __shared__ half_t s_inv[MT * 16];
   const half_t* __restrict__ X = static_cast<const half_t*>(a.x);
   const half_t* __restrict__ W = static_cast<const half_t*>(a.w);
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -549,50 +559,100 @@ __global__ __launch_bounds__(256) void skinny_f16_kernel(LinearArgs a, unsigned 
 #pragma unroll
   for (int t = 0; t < MT; ++t) acc[t] = floatx4{0.f, 0.f, 0.f, 0.f};
   const half8 z8 = {0, 0, 0, 0, 0, 0, 0, 0};
-  half8 inv8[MT];
-  const half_t* gp = nullptr;
-  if constexpr (NORM) {
-    // thread → row tid/4 and every 4th 16-column piece of it; quads then sum in order
-    const int row = threadIdx.x >> 2, q = threadIdx.x & 3, np = K / 16;
-    float s = 0.f;
-    if (row < M)
-      for (int p = q; p < np; p += 4) s += a.ssq_in[static_cast<size_t>(row) * np + p];
-    s = quad_sum_dpp(s);
-    if (q == 0 && row < MT * 16) {
-      float inv = 0.f;  // rows past M load zeros and stay zero
-      if (row < M) inv = rnd<half_t>(1.0f / sqrtf(s / static_cast<float>(K) + a.norm_eps));
-      s_inv[row] = static_cast<half_t>(inv);
-    }
-    __syncthreads();
+  // The epilogue's bias and residual (written before this launch) are loaded now, in
+  // the same round trip as the operands, by the workgroup that stores the output.
+  // Addresses are clamped in bounds and the loads unconditional, so that no wait for
+  // them is forced where branches join.
+  const int ej = threadIdx.x >> 4, ei = threadIdx.x & 15;
+  const int ec = n0 + ei < N ? n0 + ei : N - 1;
+  float pre_b = 0.f, pre_r[MT];
+  if constexpr (EPI != EPI_NONE) pre_b = static_cast<float>(static_cast<const half_t*>(a.bias)[ec]);
 #pragma unroll
-    for (int t = 0; t < MT; ++t) {
-      const half_t v = s_inv[t * 16 + r];
-      inv8[t] = half8{v, v, v, v, v, v, v, v};
+  for (int t = 0; t < MT; ++t) {
+    pre_r[t] = 0.f;
+    if constexpr (EPI == EPI_BIAS_RESID) {
+      const int m = t * 16 + ej < M ? t * 16 + ej : M - 1;
+      pre_r[t] = static_cast<float>(static_cast<const half_t*>(a.resid)[static_cast<size_t>(m) * N + ec]);
     }
-    gp = static_cast<const half_t*>(a.norm_g) + kbeg + kk;
   }
-  for (int k = 0; k < kq; k += 32 * U) {
-    half8 av[U], bv[U][MT];
+  // Operands of one step of U 32-wide k blocks (and the RMSNorm gains with NORM). The
+  // first step is issued before the RMSNorm statistics so both share a round trip.
+  half8 av[U], bv[U][MT], gv[U];
+  const half_t* gp = NORM ? static_cast<const half_t*>(a.norm_g) + kbeg + kk : nullptr;
+  auto load = [&](int k) {
 #pragma unroll
-    for (int u = 0; u < U; ++u) {
-      av[u] = nvalid ? *reinterpret_cast<const half8*>(wp + k + u * 32) : z8;
+    for (int u = 0; u < U; ++u) {  // wp, xp point at row 0 where invalid: zeroed after
+      const half8 w8 = *reinterpret_cast<const half8*>(wp + k + u * 32);
+      av[u] = nvalid ? w8 : z8;
+#pragma unroll
+      for (int t = 0; t < MT; ++t) {
+        const half8 x8 = *reinterpret_cast<const half8*>(xp[t] + k + u * 32);
+        bv[u][t] = mvalid[t] ? x8 : z8;
+      }
+      if constexpr (NORM) gv[u] = *reinterpret_cast<const half8*>(gp + k + u * 32);
+    }
+  };
+  load(0);
+  half8 inv8[MT];
+  if constexpr (NORM) {
+    // Lane group g = lane / 16 sums the g-th quarter of the K/16 pieces of rows t·16 + r
+    // in order; the quarters are added as (q0 + q1) + (q2 + q3) by lane exchanges (the
+    // same value in all four groups). No barrier: these loads overlap the operands'.
+    const int np = K / 16, nq4 = np / 4, g = lane >> 4;
+    float sqs[MT];
+    const float* sps[MT];
+#pragma unroll
+    for (int t = 0; t < MT; ++t) {  // rows clamped to 0 past M (their result is discarded)
+      const int row = t * 16 + r;
+      sps[t] = a.ssq_in + static_cast<size_t>(row < M ? row : 0) * np + g * nq4;
+      sqs[t] = 0.f;
+    }
+    if (nq4 == 16) {  // K = 1024: every tile's quarter in one batch of 16-byte loads
+      floatx4 v4[MT][4];
 #pragma unroll
       for (int t = 0; t < MT; ++t)
-        bv[u][t] = mvalid[t] ? *reinterpret_cast<const half8*>(xp[t] + k + u * 32) : z8;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v4[t][e] = *reinterpret_cast<const floatx4*>(sps[t] + 4 * e);
+#pragma unroll
+      for (int t = 0; t < MT; ++t)
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+#pragma unroll
+          for (int c = 0; c < 4; ++c) sqs[t] += v4[t][e][c];
+    } else {
+#pragma unroll
+      for (int t = 0; t < MT; ++t)
+        for (int j = 0; j < nq4; j += 2) {  // nq4 is even: K is a multiple of 128
+          const float2 v2 = *reinterpret_cast<const float2*>(sps[t] + j);
+          sqs[t] += v2.x;
+          sqs[t] += v2.y;
+        }
     }
+#pragma unroll
+    for (int t = 0; t < MT; ++t) {
+      const int row = t * 16 + r;
+      float sq = sqs[t];
+      sq += __shfl_xor(sq, 16, 64);
+      sq += __shfl_xor(sq, 32, 64);
+      float inv = 0.f;  // rows past M load zeros and stay zero
+      if (row < M) inv = rnd<half_t>(1.0f / sqrtf(sq / static_cast<float>(K) + a.norm_eps));
+      const half_t hv = static_cast<half_t>(inv);
+      inv8[t] = half8{hv, hv, hv, hv, hv, hv, hv, hv};
+    }
+  }
+  for (int k = 0; k < kq; k += 32 * U) {
     if constexpr (NORM) {
 #pragma unroll
-      for (int u = 0; u < U; ++u) {
-        const half8 g8 = *reinterpret_cast<const half8*>(gp + k + u * 32);
+      for (int u = 0; u < U; ++u)
 #pragma unroll
-        for (int t = 0; t < MT; ++t) bv[u][t] = (bv[u][t] * inv8[t]) * g8;
-      }
+        for (int t = 0; t < MT; ++t) bv[u][t] = (bv[u][t] * inv8[t]) * gv[u];
     }
 #pragma unroll
     for (int u = 0; u < U; ++u)
 #pragma unroll
       for (int t = 0; t < MT; ++t)
         acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av[u], bv[u][t], acc[t], 0, 0, 0);
+    if (k + 32 * U < kq) load(k + 32 * U);
   }
 #pragma unroll
   for (int t = 0; t < MT; ++t)
@@ -639,10 +699,10 @@ __global__ __launch_bounds__(256) void skinny_f16_kernel(LinearArgs a, unsigned 
   }
 #pragma unroll
   for (int t = 0; t < MT; ++t) {
-    const int j = threadIdx.x >> 4, i = threadIdx.x & 15;
+    const int j = ej, i = ei;
     const int m = t * 16 + j, n = n0 + i;
     float v = 0.f;
-    if (m < M && n < N) v = epilogue<half_t, EPI>(a, m, n, sum[t]);
+    if (m < M && n < N) v = epilogue_with<half_t, EPI>(a, m, n, sum[t], pre_b, pre_r[t]);
     if constexpr (EPI == EPI_BIAS_RESID) {
       if (a.ssq_out) {  // this tile's piece of the row's sum of squares (16 lanes = 1 row)
         const float sq = row16_sum_dpp(rnd<half_t>(v * v));
@@ -671,7 +731,9 @@ int skinny_launch(const LinearArgs& a, hipStream_t st) {
   dim3 grid((a.N + kSkN - 1) / kSkN, S);
   const int kq = a.K / (4 * S);
   unsigned long long* ws = g_skinny.part;
-  if (kq % 128 == 0)
+  if (kq == 256)  // every operand of the wave in one round trip
+    skinny_f16_kernel<EPI, MT, 8, NORM><<<grid, 256, 0, st>>>(a, ws);
+  else if (kq % 128 == 0)
     skinny_f16_kernel<EPI, MT, 4, NORM><<<grid, 256, 0, st>>>(a, ws);
   else if (kq % 64 == 0)
     skinny_f16_kernel<EPI, MT, 2, NORM><<<grid, 256, 0, st>>>(a, ws);
