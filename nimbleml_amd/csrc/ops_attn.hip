@@ -22,9 +22,6 @@ namespace {
 constexpr int kTile = 64;
 constexpr int kCombineMax = 1024;  // chunks of one (row, head): max_seq_len ≤ 65536
 
-// Ticket counters of the one-launch decode attention, one per (row, head), padded to
-// whole 256-byte blocks so the group partials after them start line-aligned.
-inline size_t decode_ticket_bytes(int bh) { return (static_cast<size_t>(bh) * 4 + 255) / 256 * 256; }
 
 template <typename T, int DK>
 __global__ __launch_bounds__(64) void attn_prefill_kernel(AttnArgs a) {
@@ -135,13 +132,13 @@ __device__ __forceinline__ void ld8(const T* p, float (&o)[8]) {
 // of G 64-key chunks of one (row, head) — all their K/V rows are loaded up front
 // (clamped into [0, len), the clamped ones never used) — scores every key with 4
 // lanes per key (DK/4 dims each), takes the group's max and Σp with one block
-// reduction each, and P·V with each lane owning 8 dims of a key subset. The group's
-// (max, Σp, Σp·v) go out as flagged 64-bit slots (1 << 32 | value, relaxed
-// device-scope stores, no fences), then the workgroup takes a ticket for its (row,
-// head); the one that draws the last ticket waits for every group's slots (bounded),
-// merges them (softmax rescaling, attention.py:140-142 over the concatenated keys),
-// writes the head's output and returns the slots and the ticket counter to zero for
-// the next launch.
+// reduction each, and P·V with each lane owning 8 dims of a key subset. Every group
+// but the last of its (row, head) publishes (max, Σp, Σp·v) as flagged 64-bit slots
+// (1 << 32 | value, relaxed device-scope stores, no fences) and exits. The last group
+// — later in dispatch order than its siblings (x is the fastest grid index), so its
+// bounded wait always ends — waits for their slots, merges them with its own partial
+// (softmax rescaling, attention.py:140-142 over the concatenated keys), writes the
+// head's output and returns the slots to zero for the next launch.
 // slots per group partial: DK + 2 rounded up to whole 128-byte lines
 constexpr int dec_slots(int dk) { return (dk + 2 + 15) / 16 * 16; }
 
@@ -153,8 +150,7 @@ constexpr int dec_groups() {  // chunks per group: K/V registers bounded
 template <typename T, int DK, int G>
 __global__ __launch_bounds__(256) void attn_decode_group_kernel(AttnArgs a, const int32_t* __restrict__ pos,
                                                                 int max_groups,
-                                                                unsigned long long* __restrict__ part,
-                                                                unsigned* __restrict__ tickets) {
+                                                                unsigned long long* __restrict__ part) {
 #pragma clang fp contract(off)
   typedef unsigned long long u64;
   constexpr int CH = kTile, KG = CH * G, DPT = DK / 4, DG = DK / 8, NKS = 256 / DG, KPT = CH / NKS;
@@ -162,13 +158,12 @@ __global__ __launch_bounds__(256) void attn_decode_group_kernel(AttnArgs a, cons
   static_assert(DK >= 32 && KPT >= 1, "decode group shape");
   __shared__ float s_q[DK], s_p[KG], s_red[16];
   __shared__ float s_o[NKS][DK + 1];
-  __shared__ int s_last;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int grp = blockIdx.x, bh = blockIdx.y;
   const int b = bh / a.H, h = bh - (bh / a.H) * a.H;
   const int len = pos[b] + 1;
   const int k0 = grp * KG;
-  if (k0 >= len) return;  // whole workgroup: groups at or past len take no ticket
+  if (k0 >= len) return;  // whole workgroup: groups at or past len do nothing
   const int ng = (len + KG - 1) / KG;
   const T* __restrict__ K = static_cast<const T*>(a.k) + b * a.kv_stride_b + h * a.kv_stride_h;
   const T* __restrict__ Vp = static_cast<const T*>(a.v) + b * a.kv_stride_b + h * a.kv_stride_h;
@@ -243,36 +238,35 @@ __global__ __launch_bounds__(256) void attn_decode_group_kernel(AttnArgs a, cons
   __syncthreads();
   u64* const pb = part + static_cast<size_t>(bh) * max_groups * PS;
   const u64 flag = 1ull << 32;
-  if (tid < DK) {
-    float sm = 0.f;
-    for (int k2 = 0; k2 < NKS; ++k2) sm += s_o[k2][tid];
-    __hip_atomic_store(pb + grp * PS + 2 + tid, flag | __float_as_uint(sm), __ATOMIC_RELAXED,
-                       __HIP_MEMORY_SCOPE_AGENT);
-  } else if (tid == DK) {
-    __hip_atomic_store(pb + grp * PS, flag | __float_as_uint(mx), __ATOMIC_RELAXED,
-                       __HIP_MEMORY_SCOPE_AGENT);
-    __hip_atomic_store(pb + grp * PS + 1, flag | __float_as_uint(l), __ATOMIC_RELAXED,
-                       __HIP_MEMORY_SCOPE_AGENT);
+  float own = 0.f;
+  if (tid < DK)
+    for (int k2 = 0; k2 < NKS; ++k2) own += s_o[k2][tid];
+  if (grp != ng - 1) {  // publish this group's partial and leave
+    if (tid < DK) {
+      __hip_atomic_store(pb + grp * PS + 2 + tid, flag | __float_as_uint(own), __ATOMIC_RELAXED,
+                         __HIP_MEMORY_SCOPE_AGENT);
+    } else if (tid == DK) {
+      __hip_atomic_store(pb + grp * PS, flag | __float_as_uint(mx), __ATOMIC_RELAXED,
+                         __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(pb + grp * PS + 1, flag | __float_as_uint(l), __ATOMIC_RELAXED,
+                         __HIP_MEMORY_SCOPE_AGENT);
+    }
+    return;
   }
-  __syncthreads();  // every slot of this group issued before the ticket
-  if (tid == 0)
-    s_last = __hip_atomic_fetch_add(tickets + bh, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
-             static_cast<unsigned>(ng - 1);
-  __syncthreads();
-  if (!s_last) return;
-  // Last group of (b, h): the others have taken their tickets, so their slots are
-  // issued; wait (bounded) until each is visible — 8 groups' slots in flight at a
-  // time — then merge in group order.
+  // The last group of (b, h) — dispatched after its siblings, which wait on nothing —
+  // waits (bounded) for their slots, 8 groups' slots in flight at a time, and merges
+  // them in group order, its own partial last.
   if (tid < DK) {
     constexpr int NB = 8;
     float mg[NB], lg[NB], og[NB];
     float M = -INFINITY, den = 0.f, num = 0.f;
-    for (int g0 = 0; g0 < ng; g0 += NB) {
+    const int np = ng - 1;
+    for (int g0 = 0; g0 < np; g0 += NB) {
       u64 vm[NB], vl[NB], vo[NB];
       const u64 ok = 1ull << 32;
 #pragma unroll
       for (int j = 0; j < NB; ++j) {
-        const bool in = g0 + j < ng;
+        const bool in = g0 + j < np;
         u64* sl = pb + (g0 + j) * PS;
         vm[j] = in ? __hip_atomic_load(sl, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : ok;
         vl[j] = in ? __hip_atomic_load(sl + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : ok;
@@ -302,7 +296,7 @@ __global__ __launch_bounds__(256) void attn_decode_group_kernel(AttnArgs a, cons
       // online merge over this batch of groups (in group order)
 #pragma unroll
       for (int j = 0; j < NB; ++j) {
-        if (g0 + j >= ng) break;
+        if (g0 + j >= np) break;
         const float Mn = fmaxf(M, mg[j]);
         const float c = expf(M - Mn), w = expf(mg[j] - Mn);
         den = den * c + w * lg[j];
@@ -310,16 +304,20 @@ __global__ __launch_bounds__(256) void attn_decode_group_kernel(AttnArgs a, cons
         M = Mn;
       }
     }
+    {  // this group
+      const float Mn = fmaxf(M, mx);
+      const float c = expf(M - Mn), w = expf(mx - Mn);
+      den = den * c + w * l;
+      num = num * c + w * own;
+    }
     T* out = static_cast<T*>(a.out) + static_cast<size_t>(b) * a.H * DK + h * DK;
     out[tid] = static_cast<T>(num * (1.f / den));
   }
   __syncthreads();  // every read of the slots done before they are cleared
-  for (int i = tid; i < ng * PS; i += 256)
+  for (int i = tid; i < (ng - 1) * PS; i += 256)
     __hip_atomic_store(pb + i, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  if (tid == 0) __hip_atomic_store(tickets + bh, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// Head dims below 32: one 64-lane wave per chunk, each lane scores one key.
 template <typename T, int DK>
 __global__ __launch_bounds__(64) void attn_decode_small_kernel(AttnArgs a, const int32_t* __restrict__ pos,
                                                          int max_chunks, float* __restrict__ part) {
@@ -598,6 +596,7 @@ __global__ __launch_bounds__(256) void attn_prefill_mfma_kernel(AttnArgs a) {
   }
 }
 
+
 template <typename T, int DK>
 int prefill_typed(const AttnArgs& a, hipStream_t st) {
   if constexpr (sizeof(T) == 2 && (DK == 64 || DK == 128)) {
@@ -617,11 +616,9 @@ int decode_typed(const AttnArgs& a, const int32_t* pos, int max_len, void* ws, h
   if constexpr (DK >= 32) {
     constexpr int G = dec_groups<T, DK>();
     const int max_groups = (max_len + kTile * G - 1) / (kTile * G);
-    unsigned* tickets = static_cast<unsigned*>(ws);
-    unsigned long long* part = reinterpret_cast<unsigned long long*>(
-        static_cast<char*>(ws) + decode_ticket_bytes(a.B * a.H));
+    unsigned long long* part = static_cast<unsigned long long*>(ws);
     attn_decode_group_kernel<T, DK, G><<<dim3(max_groups, a.B * a.H), 256, 0, st>>>(
-        a, pos, max_groups, part, tickets);
+        a, pos, max_groups, part);
     NML_LAUNCHED();
   } else {
     const int max_chunks = (max_len + kTile - 1) / kTile;
@@ -659,10 +656,10 @@ int decode_dk(const AttnArgs& a, const int32_t* pos, int max_len, void* ws, hipS
 }  // namespace
 
 size_t attention_decode_workspace(int B, int H, int dk, int max_len) {
-  // head dims ≥ 32: tickets, then flagged group partials (at most 4 chunks a group
+  // head dims ≥ 32: flagged group partials (at most 4 chunks a group
   // never fewer than 1); below: float chunk partials for the combine pass
   const size_t chunks = (max_len + kTile - 1) / kTile;
-  const size_t grouped = decode_ticket_bytes(B * H) + static_cast<size_t>(B) * H * chunks * dec_slots(dk) * 8;
+  const size_t grouped = static_cast<size_t>(B) * H * chunks * dec_slots(dk) * 8;
   const size_t plain = static_cast<size_t>(B) * H * chunks * (dk + 2) * sizeof(float);
   return grouped > plain ? grouped : plain;
 }
