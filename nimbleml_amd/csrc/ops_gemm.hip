@@ -80,6 +80,37 @@ __device__ __forceinline__ float epilogue(const LinearArgs& a, int m, int n, flo
   return epilogue_with<T, EPI>(a, m, n, acc, bias_v, resid_v);
 }
 
+// Epilogue of one 32×32 MFMA tile, fp16: this lane's 16 accumulators are rows
+// mb + 8(r/4) + r%4 of column n (D layout of v_mfma_f32_32x32x16_f16). The residual
+// operands are loaded first, all together (addresses clamped in bounds, loads
+// unconditional, so no wait is forced between them); bias_v is b[n].
+template <int EPI>
+__device__ __forceinline__ void epilogue_tile32(const LinearArgs& a, int mb, int n, const floatx16& acc,
+                                                float bias_v) {
+  const int M = a.M, N = a.N;
+  float res[16];
+#pragma unroll
+  for (int r = 0; r < 16; ++r) {
+    res[r] = 0.f;
+    if constexpr (EPI == EPI_BIAS_RESID) {
+      const int m = mb + 8 * (r >> 2) + (r & 3);
+      const size_t mc = m < M ? m : M - 1;
+      res[r] = static_cast<float>(static_cast<const half_t*>(a.resid)[mc * N + (n < N ? n : N - 1)]);
+    }
+  }
+#pragma unroll
+  for (int r = 0; r < 16; ++r) {
+    const int m = mb + 8 * (r >> 2) + (r & 3);
+    if (m < M && n < N) epilogue_with<half_t, EPI>(a, m, n, acc[r], bias_v, res[r]);
+  }
+}
+
+template <int EPI>
+__device__ __forceinline__ float bias_at(const LinearArgs& a, int n) {
+  if constexpr (EPI == EPI_NONE) return 0.f;
+  return static_cast<float>(static_cast<const half_t*>(a.bias)[n < a.N ? n : a.N - 1]);
+}
+
 constexpr int kBM = 128, kBN = 128;
 
 // ---------------------------------------------------------------- fp16 MFMA GEMM
@@ -157,16 +188,15 @@ __global__ __launch_bounds__(256) void gemm_f16_kernel(LinearArgs a) {
   }
 
   // D layout of a 32×32 MFMA tile: lane l, register r → row 8(r/4) + 4(l/32) + r%4, col l%32.
-#pragma unroll
-  for (int i = 0; i < 2; ++i)
-#pragma unroll
-    for (int j = 0; j < 2; ++j)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int m = m0 + wm * 64 + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-        const int n = n0 + wn * 64 + j * 32 + (lane & 31);
-        if (m < M && n < N) epilogue<half_t, EPI>(a, m, n, acc[i][j][r]);
-      }
+  {  // written out: a loop here is not always unrolled, and acc must stay in registers
+    const int na = n0 + wn * 64 + (lane & 31), nb = na + 32;
+    const float ba = bias_at<EPI>(a, na), bb = bias_at<EPI>(a, nb);
+    const int mb = m0 + wm * 64 + 4 * (lane >> 5);
+    epilogue_tile32<EPI>(a, mb, na, acc[0][0], ba);
+    epilogue_tile32<EPI>(a, mb, nb, acc[0][1], bb);
+    epilogue_tile32<EPI>(a, mb + 32, na, acc[1][0], ba);
+    epilogue_tile32<EPI>(a, mb + 32, nb, acc[1][1], bb);
+  }
 }
 
 // ------------------------------------------------ fp16 MFMA GEMM, 256×256 block tile
@@ -189,11 +219,14 @@ __global__ __launch_bounds__(256) void gemm_f16_kernel(LinearArgs a) {
 // cover all 64 banks. Workgroups are spread XCD-aware (workgroup b runs on XCD b % 8
 // and takes a contiguous range of tiles), grouped GM m-bands at a time so the
 // workgroups resident on one XCD share A bands and B tiles in its L2.
-constexpr int kHM = 256, kHN = 256, kHK = 32, kHStages = 4;
-constexpr int kHStageBytes = (kHM + kHN) * kHK * 2;  // 32 KiB: A then B
+constexpr int kHM = 256, kHN = 256, kHK = 64, kHStages = 2;
+constexpr int kHStageBytes = (kHM + kHN) * kHK * 2;  // 64 KiB: A then B
 
+// A stage row is 128 bytes (8 chunks of 16). Chunk c of row r sits at position
+// c ^ ((r / 2) & 7): the 16 lanes of a ds_read_b128 phase (rows r…r+15, one chunk) then
+// cover all 64 banks once.
 __device__ __forceinline__ uint32_t swz_off(int row, int chunk) {
-  return static_cast<uint32_t>(row * 64 + ((chunk ^ ((row >> 2) & 3)) << 4));
+  return static_cast<uint32_t>(row * 128 + ((chunk ^ ((row >> 1) & 7)) << 4));
 }
 
 __device__ __forceinline__ half8 lds_read16(uint32_t addr) {
@@ -224,19 +257,19 @@ __global__ __launch_bounds__(kHT, 1) void gemm_f16_big_kernel(LinearArgs a, int 
   const long long lda = a.lda;
   const uint32_t lds0 = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(lds_raw));
 
-  // Direct-to-LDS loads of one stage: A and B are 256 rows × 4 chunks each = 16 blocks
-  // of 16 rows; wave w issues blocks 2w, 2w+1 of each. Lane l of block q carries row
-  // 16q + l/4 at chunk position l % 4, i.e. global chunk (l % 4) ^ ((row / 4) & 3).
+  // Direct-to-LDS loads of one stage: A and B are 256 rows × 8 chunks each = 32 blocks
+  // of 8 full 128-byte rows; wave w issues blocks 4w…4w+3 of each. Lane l of block q
+  // carries row 8q + l/8 at chunk position l % 8, i.e. global chunk (l % 8) ^ ((row / 2) & 7).
   // Rows past M or N read row M-1 / N-1 (never stored).
-  const int lrow = lane >> 2, lpos = lane & 3;
+  const int lrow = lane >> 3, lpos = lane & 7;
   auto issue = [&](int s) {
     const int k0 = s * kHK;
     char* stage = lds_raw + (s % kHStages) * kHStageBytes;
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      const int q = wave * 2 + j;
-      const int row = 16 * q + lrow;
-      const int ch = lpos ^ ((row >> 2) & 3);
+    for (int j = 0; j < 4; ++j) {
+      const int q = wave * 4 + j;
+      const int row = 8 * q + lrow;
+      const int ch = lpos ^ ((row >> 1) & 7);
       const int gmr = m0 + row < M ? m0 + row : M - 1;
       const int gnr = n0 + row < N ? n0 + row : N - 1;
       // (address-space casts: global source, LDS destination)
@@ -263,49 +296,72 @@ __global__ __launch_bounds__(kHT, 1) void gemm_f16_big_kernel(LinearArgs a, int 
 #pragma unroll
   for (int j = 0; j < 2; ++j) offb[j] = static_cast<uint32_t>(wn * 64 + j * 32 + (lane & 31));
 
+  // Double-buffered stages, software-pipelined fragments: the next 16-wide k step's
+  // fragments are read from LDS while the current step's MFMAs run. Stage t's barrier
+  // (every wave's loads of t landed, every wave done reading t - 1) is followed by the
+  // loads of stage t + 1 into t - 1's buffer; before a stage's last step each wave has
+  // its fragments in registers, so the next barrier may release the buffer.
   const int S = K / kHK;
-  for (int s = 0; s < kHStages - 1 && s < S; ++s) issue(s);
+  auto wait_stage = [&](int t) {
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    if (t + 1 < S) issue(t + 1);
+  };
+  half8 fa0[4], fb0[2], fa1[4], fb1[2];
+  auto read = [&](half8 (&fa)[4], half8 (&fb)[2], int t, int kk) {
+    const uint32_t base = lds0 + static_cast<uint32_t>((t % kHStages) * kHStageBytes);
+    const int ch = 2 * kk + (lane >> 5);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) fa[i] = lds_read16(base + swz_off(offa[i], ch));
+#pragma unroll
+    for (int j = 0; j < 2; ++j) fb[j] = lds_read16(base + kHM * kHK * 2 + swz_off(offb[j], ch));
+  };
+  auto mma = [&](const half8 (&fa)[4], const half8 (&fb)[2]) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(fa[i], fb[j], acc[i][j], 0, 0, 0);
+  };
+#define NML_LGKM(n, fa, fb)                                                                    \
+  asm volatile("s_waitcnt lgkmcnt(" #n ")"                                                     \
+               : "+v"(fa[0]), "+v"(fa[1]), "+v"(fa[2]), "+v"(fa[3]), "+v"(fb[0]), "+v"(fb[1]))
+  issue(0);
+  wait_stage(0);
+  read(fa0, fb0, 0, 0);
   for (int s = 0; s < S; ++s) {
-    // this wave's loads of stage s have landed once at most the later stages' remain
-    const int later = (S - 1 < s + kHStages - 2 ? S - 1 : s + kHStages - 2) - s;
-    if (later >= 2)
-      asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
-    else if (later == 1)
-      asm volatile("s_waitcnt vmcnt(4)" ::: "memory");
-    else
-      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    __builtin_amdgcn_s_barrier();  // every wave's loads of stage s landed; stage s-1 done
-    if (s + kHStages - 1 < S) issue(s + kHStages - 1);
-    const uint32_t base = lds0 + static_cast<uint32_t>((s % kHStages) * kHStageBytes);
-#pragma unroll
-    for (int kk = 0; kk < kHK / 16; ++kk) {
-      const int ch = 2 * kk + (lane >> 5);
-      half8 fa[4], fb[2];
-#pragma unroll
-      for (int i = 0; i < 4; ++i) fa[i] = lds_read16(base + swz_off(offa[i], ch));
-#pragma unroll
-      for (int j = 0; j < 2; ++j) fb[j] = lds_read16(base + kHM * kHK * 2 + swz_off(offb[j], ch));
-      asm volatile("s_waitcnt lgkmcnt(0)"
-                   : "+v"(fa[0]), "+v"(fa[1]), "+v"(fa[2]), "+v"(fa[3]), "+v"(fb[0]), "+v"(fb[1]));
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-#pragma unroll
-        for (int j = 0; j < 2; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(fa[i], fb[j], acc[i][j], 0, 0, 0);
+    read(fa1, fb1, s, 1);
+    NML_LGKM(6, fa0, fb0);
+    mma(fa0, fb0);
+    read(fa0, fb0, s, 2);
+    NML_LGKM(6, fa1, fb1);
+    mma(fa1, fb1);
+    read(fa1, fb1, s, 3);
+    NML_LGKM(6, fa0, fb0);
+    mma(fa0, fb0);
+    NML_LGKM(0, fa1, fb1);
+    if (s + 1 < S) {
+      wait_stage(s + 1);
+      read(fa0, fb0, s + 1, 0);
     }
+    mma(fa1, fb1);
   }
+#undef NML_LGKM
 
   // D layout of a 32×32 MFMA tile: lane l, register r → row 8(r/4) + 4(l/32) + r%4, col l%32.
-#pragma unroll
-  for (int i = 0; i < 4; ++i)
-#pragma unroll
-    for (int j = 0; j < 2; ++j)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int m = m0 + wm * 128 + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-        const int n = n0 + wn * 64 + j * 32 + (lane & 31);
-        if (m < M && n < N) epilogue<half_t, EPI>(a, m, n, acc[i][j][r]);
-      }
+  {  // written out: a loop here is not always unrolled, and acc must stay in registers
+    const int na = n0 + wn * 64 + (lane & 31), nb = na + 32;
+    const float ba = bias_at<EPI>(a, na), bb = bias_at<EPI>(a, nb);
+    const int mb = m0 + wm * 128 + 4 * (lane >> 5);
+    epilogue_tile32<EPI>(a, mb, na, acc[0][0], ba);
+    epilogue_tile32<EPI>(a, mb, nb, acc[0][1], bb);
+    epilogue_tile32<EPI>(a, mb + 32, na, acc[1][0], ba);
+    epilogue_tile32<EPI>(a, mb + 32, nb, acc[1][1], bb);
+    epilogue_tile32<EPI>(a, mb + 64, na, acc[2][0], ba);
+    epilogue_tile32<EPI>(a, mb + 64, nb, acc[2][1], bb);
+    epilogue_tile32<EPI>(a, mb + 96, na, acc[3][0], ba);
+    epilogue_tile32<EPI>(a, mb + 96, nb, acc[3][1], bb);
+  }
 }
 
 constexpr size_t kBigLds = static_cast<size_t>(kHStages) * kHStageBytes;  // 128 KiB
