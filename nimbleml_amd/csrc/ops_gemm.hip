@@ -88,6 +88,53 @@ template <int EPI>
 __device__ __forceinline__ void epilogue_tile32(const LinearArgs& a, int mb, int n, const floatx16& acc,
                                                 float bias_v) {
   const int M = a.M, N = a.N;
+  if constexpr (EPI == EPI_QKV) {
+    // The head-major scatter of epilogue_with, with the column's destination worked out
+    // once per tile and each row's (sequence, position) stepped from the tile's first
+    // row instead of divided out per element.
+    if (n >= N) return;
+    const QKVDst& q = a.qkv;
+    const int which = n / q.d, within = n - which * q.d;
+    const int h = within / q.dk, j = within - h * q.dk;
+    half_t* const dst = static_cast<half_t*>(which == 0 ? q.q : which == 1 ? q.k : q.v);
+    int rb[16], rp[16];  // each row's sequence and position
+    if (q.row_seg) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int m = mb + 8 * (r >> 2) + (r & 3);
+        const int v = q.row_seg[m < M ? m : M - 1];
+        rb[r] = v >> 16;
+        rp[r] = v & 0xffff;
+      }
+    } else {
+      int b = mb / q.S, s0 = mb - b * q.S;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        int s = s0 + 8 * (r >> 2) + (r & 3), bb = b;
+        while (s >= q.S) {  // rows past the tile's first sequence (once at most for S ≥ 32)
+          s -= q.S;
+          ++bb;
+        }
+        rb[r] = bb;
+        rp[r] = s;
+      }
+    }
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int m = mb + 8 * (r >> 2) + (r & 3);
+      if (m >= M) continue;
+      const int b = rb[r], s = rp[r];
+      const float lin = rnd<half_t>(rnd<half_t>(acc[r]) + bias_v);
+      if (which == 0) {
+        dst[((static_cast<size_t>(b) * q.H + h) * q.S + s) * q.dk + j] = static_cast<half_t>(lin);
+      } else {
+        const int pos = (q.pos_base ? q.pos_base[b] : 0) + s;
+        dst[b * q.kv_stride_b + h * q.kv_stride_h + static_cast<long long>(pos) * q.dk + j] =
+            static_cast<half_t>(lin);
+      }
+    }
+    return;
+  }
   float res[16];
 #pragma unroll
   for (int r = 0; r < 16; ++r) {
