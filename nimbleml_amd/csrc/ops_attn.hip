@@ -414,7 +414,7 @@ __global__ __launch_bounds__(64) void attn_combine_kernel(AttnArgs a, const int3
 constexpr int kFQ = 128, kFK = 64;
 
 template <int DK>
-__global__ __launch_bounds__(256) void attn_prefill_mfma_kernel(AttnArgs a) {
+__global__ __launch_bounds__(256, 2) void attn_prefill_mfma_kernel(AttnArgs a) {
 #pragma clang fp contract(off)
   constexpr int KS = DK / 16;  // 16-dim steps of q·k
   constexpr int OT = DK / 32;  // 32-dim tiles of the output
@@ -550,10 +550,14 @@ __global__ __launch_bounds__(256) void attn_prefill_mfma_kernel(AttnArgs a) {
     constexpr float kLog2e = 1.4426950408889634f;
     const float alpha = (mx == -INFINITY) ? 1.f : __builtin_amdgcn_exp2f((m - mx) * kLog2e);
     l *= alpha;
+    // alpha is exactly 1 where the running max did not grow; the accumulators are
+    // rescaled only when some lane's max grew (rare after the first tiles)
+    if (__any(mx > m)) {
 #pragma unroll
-    for (int t = 0; t < OT; ++t)
+      for (int t = 0; t < OT; ++t)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) o[t][r] *= alpha;
+        for (int r = 0; r < 16; ++r) o[t][r] *= alpha;
+    }
 #pragma unroll
     for (int t = 0; t < 2; ++t)
 #pragma unroll
