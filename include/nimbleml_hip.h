@@ -110,6 +110,11 @@ enum nml_param_kind {
   NML_P_TOKEN_EMB = 0, /* (vocab, d)        token_emb.weights            */
   NML_P_POS_EMB = 1,   /* (max_seq, d)      pos_emb.weights              */
   NML_P_LN_F = 2,      /* (d)               ln.gamma                     */
+  NML_P_ROPE_COS = 3,  /* (max_seq, dk/2)   cos(p·θ_i), utils/rope.py:12-19, in the compute
+                        *                   dtype as apply_rope_flat casts it (:37-38)   */
+  NML_P_ROPE_SIN = 4,  /* (max_seq, dk/2)   sin(p·θ_i); once both are set the model uses
+                        *                   rotary positions (GPT(use_rope=True),
+                        *                   models/gpt.py:46-51) and ignores pos_emb     */
   NML_P_LN1 = 10,      /* (d)               blocks.layers.i.ln1.gamma    */
   NML_P_WQKV = 11,     /* (3d, d)           [W_q | W_k | W_v]ᵀ           */
   NML_P_BQKV = 12,     /* (3d)              [b_q | b_k | b_v]            */

@@ -75,6 +75,7 @@ _SIGS = {
 
 # Parameter kinds (enum nml_param_kind).
 P_TOKEN_EMB, P_POS_EMB, P_LN_F = 0, 1, 2
+P_ROPE_COS, P_ROPE_SIN = 3, 4
 P_LN1, P_WQKV, P_BQKV, P_WO, P_BO, P_LN2, P_W1, P_B1, P_W2, P_B2 = range(10, 20)
 
 F32, F16 = 0, 1

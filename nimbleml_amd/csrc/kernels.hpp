@@ -74,6 +74,14 @@ int launch_embed_decode(int dt, const int64_t* tokens, long long tok_stride, con
                         const void* emb, const void* posw, void* out, int B, int d, int V, int P,
                         int* err, hipStream_t st);
 
+// Rotary positions on q (B, H, S, dk) and the K rows just written to the cache, in place
+// (utils/rope.py:22-44, GPT-NeoX half split): row s of sequence b sits at position
+// pos_base[b] + s (pos_base null → s); rows s ≥ seq_len[b] are skipped when seq_len is
+// given. cos/sin: (max_len, dk/2) in the compute dtype.
+int launch_rope(int dt, void* q, void* k, long long kv_stride_b, long long kv_stride_h, int B,
+                int H, int S, int dk, const int32_t* pos_base, const int32_t* seq_len,
+                const void* cos, const void* sin, int max_len, hipStream_t st);
+
 int launch_rmsnorm(int dt, const void* x, const void* g, void* out, float* ms, float* rms,
                    int rows, int d, float eps, hipStream_t st);
 int launch_gelu(int dt, const void* x, void* out, float* tanh_u, size_t n, hipStream_t st);

@@ -58,6 +58,9 @@ struct nml_model {
   void* arena = nullptr;
   size_t arena_bytes = 0;
   void *emb = nullptr, *pos = nullptr, *lnf = nullptr;
+  // rotary positions (GPT(use_rope=True)): (P, dk/2) cos and sin tables; on once both set
+  void *rope_cos = nullptr, *rope_sin = nullptr;
+  bool rope_cos_set = false, rope_sin_set = false;
   std::vector<Layer> layers;
   Buf ws;         // activations
   Buf kvs;        // K/V scratch for forward() without a cache
@@ -87,6 +90,8 @@ size_t param_elems(const nml_model* m, int kind) {
   switch (kind) {
     case NML_P_TOKEN_EMB: return (size_t)m->V * d;
     case NML_P_POS_EMB: return (size_t)m->P * d;
+    case NML_P_ROPE_COS:
+    case NML_P_ROPE_SIN: return (size_t)m->P * (m->dk / 2);
     case NML_P_LN_F:
     case NML_P_LN1:
     case NML_P_LN2:
@@ -107,6 +112,8 @@ void** param_slot(nml_model* m, int kind, int layer) {
     case NML_P_TOKEN_EMB: return &m->emb;
     case NML_P_POS_EMB: return &m->pos;
     case NML_P_LN_F: return &m->lnf;
+    case NML_P_ROPE_COS: return &m->rope_cos;
+    case NML_P_ROPE_SIN: return &m->rope_sin;
   }
   if (layer < 0 || layer >= m->L) return nullptr;
   Layer& l = m->layers[layer];
@@ -155,6 +162,11 @@ int acts_for(nml_model* m, int R, int Bdec, Acts* a) {
   a->ssq = ssq ? reinterpret_cast<float*>(b + 4 * rd + rf + part) : nullptr;
   return 0;
 }
+
+bool rope_on(const nml_model* m) { return m->rope_cos_set && m->rope_sin_set; }
+
+// Learned position table for the embedding; none with rotary positions.
+const void* posw(const nml_model* m) { return rope_on(m) ? nullptr : m->pos; }
 
 // Small device scratch: [0] int err, then B int32 positions etc.
 struct Small {
@@ -219,6 +231,9 @@ int trunk(nml_model* m, const Acts& a, int B, int S, const int32_t* pos_base, KV
     qkv.qkv = QKVDst{a.q, c.k, c.v, pos_base, c.sb, c.sh, S, m->H, m->dk, d,
                      rg ? rg->row_seg : nullptr};
     NML_TRY(launch_linear(m->dt, qkv, st));
+    if (rope_on(m))  // models/gpt.py:62-64 → _fused_arrays.py:95-98
+      NML_TRY(launch_rope(m->dt, a.q, c.k, c.sb, c.sh, B, m->H, S, m->dk, pos_base,
+                          rg ? rg->seq_len : nullptr, m->rope_cos, m->rope_sin, m->P, st));
     AttnArgs at{};
     at.q = a.q;
     at.k = c.k;
@@ -310,7 +325,7 @@ int decode_step(nml_model* m, nml_cache* c, const Acts& a, const int64_t* tokens
                 long long tok_stride, int32_t* pos, int* err, void* logits, int max_len,
                 hipStream_t st) {
   const int B = c->B, d = m->d;
-  NML_TRY(launch_embed_decode(m->dt, tokens, tok_stride, pos, m->emb, m->pos, a.x, B, d, m->V,
+  NML_TRY(launch_embed_decode(m->dt, tokens, tok_stride, pos, m->emb, posw(m), a.x, B, d, m->V,
                               m->P, err, st));
   const size_t layer_kv = (size_t)B * m->H * m->P * m->dk * m->es;
   // RMSNorm fused into the GEMMs that consume it (fp16, 8 < B ≤ 64): the residual GEMMs
@@ -344,6 +359,9 @@ int decode_step(nml_model* m, nml_cache* c, const Acts& a, const int64_t* tokens
     qkv.epi = EPI_QKV;
     qkv.qkv = QKVDst{a.q, kl, vl, pos, sb, sh, 1, m->H, m->dk, d};
     NML_TRY(launch_linear(m->dt, qkv, st));
+    if (rope_on(m))
+      NML_TRY(launch_rope(m->dt, a.q, kl, sb, sh, B, m->H, 1, m->dk, pos, nullptr, m->rope_cos,
+                          m->rope_sin, m->P, st));
     AttnArgs at{};
     at.q = a.q;
     at.k = kl;
@@ -524,7 +542,8 @@ int nml_model_create(int vocab, int d_model, int num_heads, int num_layers, int 
   m->layers.resize(num_layers);
   size_t total = align256(param_elems(m, NML_P_TOKEN_EMB) * m->es) +
                  align256(param_elems(m, NML_P_POS_EMB) * m->es) +
-                 align256(param_elems(m, NML_P_LN_F) * m->es);
+                 align256(param_elems(m, NML_P_LN_F) * m->es) +
+                 2 * align256(param_elems(m, NML_P_ROPE_COS) * m->es);
   for (int k : kLayerKinds) total += (size_t)num_layers * align256(param_elems(m, k) * m->es);
   hipError_t e = hipMalloc(&m->arena, total);
   if (e != hipSuccess) {
@@ -548,6 +567,8 @@ int nml_model_create(int vocab, int d_model, int num_heads, int num_layers, int 
   take(NML_P_TOKEN_EMB, 0);
   take(NML_P_POS_EMB, 0);
   take(NML_P_LN_F, 0);
+  take(NML_P_ROPE_COS, 0);
+  take(NML_P_ROPE_SIN, 0);
   for (int l = 0; l < num_layers; ++l)
     for (int k : kLayerKinds) take(k, l);
   *out = m;
@@ -576,6 +597,8 @@ int nml_model_set_param(nml_model* m, int kind, int layer, const void* host, siz
   NML_REQUIRE(bytes == want, "parameter kind %d: expected %zu bytes, got %zu", kind, want, bytes);
   NML_HIP(hipMemcpyAsync(*slot, host, bytes, hipMemcpyHostToDevice, nml::stream()));
   NML_HIP(hipStreamSynchronize(nml::stream()));
+  if (kind == NML_P_ROPE_COS) m->rope_cos_set = true;
+  if (kind == NML_P_ROPE_SIN) m->rope_sin_set = true;
   return 0;
 }
 
@@ -601,7 +624,7 @@ int nml_model_forward(nml_model* m, const int64_t* ids, size_t batch, size_t seq
   NML_TRY(m->kvs.ensure(2 * kvb));
   void* kbuf = m->kvs.p;
   void* vbuf = static_cast<char*>(m->kvs.p) + kvb;
-  NML_TRY(launch_embed(m->dt, ids, m->emb, m->pos, nullptr, a.x, B, S, m->d, m->V, m->P, nullptr,
+  NML_TRY(launch_embed(m->dt, ids, m->emb, posw(m), nullptr, a.x, B, S, m->d, m->V, m->P, nullptr,
                        st));
   const long long sb = (long long)m->H * S * m->dk, sh = (long long)S * m->dk;
   NML_TRY(trunk(m, a, B, S, nullptr, [&](int) { return KVView{kbuf, vbuf, sb, sh}; }, st));
@@ -628,7 +651,7 @@ int nml_model_loss(nml_model* m, const int64_t* ids, const int64_t* labels, size
   Small sm;
   NML_TRY(small_for(m, 1, &sm));
   NML_HIP(hipMemsetAsync(sm.err, 0, sizeof(int), st));
-  NML_TRY(launch_embed(m->dt, ids, m->emb, m->pos, nullptr, a.x, B, S, m->d, m->V, m->P, sm.err,
+  NML_TRY(launch_embed(m->dt, ids, m->emb, posw(m), nullptr, a.x, B, S, m->d, m->V, m->P, sm.err,
                        st));
   const long long sb = (long long)m->H * S * m->dk, sh = (long long)S * m->dk;
   NML_TRY(trunk(m, a, B, S, nullptr, [&](int) { return KVView{kbuf, vbuf, sb, sh}; }, st));
@@ -722,7 +745,7 @@ int nml_model_forward_cached(nml_model* m, nml_cache* c, const int64_t* ids, siz
   hipStream_t st = nml::stream();
   Acts a;
   NML_TRY(acts_for(m, B * S, 0, &a));
-  NML_TRY(launch_embed(m->dt, ids, m->emb, m->pos, c->len_dev, a.x, B, S, m->d, m->V, m->P,
+  NML_TRY(launch_embed(m->dt, ids, m->emb, posw(m), c->len_dev, a.x, B, S, m->d, m->V, m->P,
                        nullptr, st));
   const size_t layer_kv = (size_t)B * m->H * m->P * m->dk * m->es;
   const long long sb = (long long)m->H * m->P * m->dk, sh = (long long)m->P * m->dk;
@@ -795,11 +818,11 @@ int nml_model_generate(nml_model* m, const int64_t* prompts, size_t prompt_strid
     NML_TRY(acts_for(m, B * S, B, &a));
     if ((int)prompt_stride != S) {
       for (int b = 0; b < B; ++b)
-        NML_TRY(launch_embed(m->dt, prompts + (size_t)b * prompt_stride, m->emb, m->pos, nullptr,
+        NML_TRY(launch_embed(m->dt, prompts + (size_t)b * prompt_stride, m->emb, posw(m), nullptr,
                              static_cast<char*>(a.x) + (size_t)b * S * m->d * m->es, 1, S, m->d,
                              m->V, m->P, sm.err, st));
     } else {
-      NML_TRY(launch_embed(m->dt, prompts, m->emb, m->pos, nullptr, a.x, B, S, m->d, m->V, m->P,
+      NML_TRY(launch_embed(m->dt, prompts, m->emb, posw(m), nullptr, a.x, B, S, m->d, m->V, m->P,
                            sm.err, st));
     }
     NML_TRY(trunk(m, a, B, S, sm.zeros,
@@ -831,7 +854,7 @@ int nml_model_generate(nml_model* m, const int64_t* prompts, size_t prompt_strid
     Acts a;
     NML_TRY(acts_for(m, B * maxp, B, &a));
     for (int b = 0; b < B; ++b)
-      NML_TRY(launch_embed(m->dt, prompts + (size_t)b * prompt_stride, m->emb, m->pos, nullptr,
+      NML_TRY(launch_embed(m->dt, prompts + (size_t)b * prompt_stride, m->emb, posw(m), nullptr,
                            static_cast<char*>(a.x) + (size_t)starts[b] * m->d * m->es, 1, plen[b],
                            m->d, m->V, m->P, sm.err, st));
     NML_TRY(trunk(m, a, B, maxp, sm.zeros,
@@ -875,8 +898,8 @@ int nml_model_generate(nml_model* m, const int64_t* prompts, size_t prompt_strid
   // Attention length bound of the decode steps: the last step feeds position
   // maxp + max_new - 2 and attends to every key up to it.
   const int decode_len = maxp + (int)max_new - 1;
-  const bool persistent =
-      persist_wanted() && persist_supported(m->dt, m->d, m->H, m->F, B, m->P);
+  const bool persistent = persist_wanted() && !rope_on(m) &&
+                          persist_supported(m->dt, m->d, m->H, m->F, B, m->P);
   PersistArgs pa{};
   if (persistent) {
     NML_TRY(persist_prepare(m, &pa, st));

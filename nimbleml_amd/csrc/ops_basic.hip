@@ -8,7 +8,8 @@ namespace {
 
 // x = E[ids] + P[pos]  (models/gpt.py:85-86; gather kernels/embedding_scatter.py:25-36,
 // position prefix layers/embedding.py:72-118). fp16 + fp16 computed in fp32 and rounded
-// once is the correctly rounded fp16 sum, i.e. NumPy's fp16 add: bit-exact.
+// once is the correctly rounded fp16 sum, i.e. NumPy's fp16 add: bit-exact. With rotary
+// positions there is no P (posw null, models/gpt.py:85): x = E[ids].
 template <typename T>
 __global__ __launch_bounds__(256) void embed_kernel(const int64_t* __restrict__ ids,
                                                     const T* __restrict__ emb,
@@ -27,6 +28,10 @@ __global__ __launch_bounds__(256) void embed_kernel(const int64_t* __restrict__ 
     return;
   }
   const T* e = emb + static_cast<size_t>(id) * d;
+  if (!posw) {
+    for (int j = threadIdx.x; j < d; j += blockDim.x) o[j] = e[j];
+    return;
+  }
   const T* q = posw + static_cast<size_t>(p) * d;
   for (int j = threadIdx.x; j < d; j += blockDim.x)
     o[j] = static_cast<T>(static_cast<float>(e[j]) + static_cast<float>(q[j]));
@@ -47,9 +52,46 @@ __global__ __launch_bounds__(256) void embed_decode_kernel(
     return;
   }
   const T* e = emb + static_cast<size_t>(id) * d;
+  if (!posw) {
+    for (int j = threadIdx.x; j < d; j += blockDim.x) o[j] = e[j];
+    return;
+  }
   const T* q = posw + static_cast<size_t>(p) * d;
   for (int j = threadIdx.x; j < d; j += blockDim.x)
     o[j] = static_cast<T>(static_cast<float>(e[j]) + static_cast<float>(q[j]));
+}
+
+// Rotary positions, GPT-NeoX half split (utils/rope.py:22-44): dims (i, i + dk/2) of a
+// row at position p become (x1·c − x2·s, x1·s + x2·c) with c = cos[p][i], s = sin[p][i]
+// in the compute dtype; each product and the sum/difference is one op of the storage
+// type (fp16: float32 result rounded once to fp16, NumPy's fp16 op; no contraction).
+// One thread per (row, pair); q and the cached K row are rotated in place.
+template <typename T>
+__global__ __launch_bounds__(256) void rope_kernel(T* __restrict__ q, T* __restrict__ k,
+                                                   long long sb, long long sh, int H, int S,
+                                                   int dk, const int32_t* __restrict__ pos_base,
+                                                   const int32_t* __restrict__ seq_len,
+                                                   const T* __restrict__ cosv,
+                                                   const T* __restrict__ sinv, int max_len) {
+#pragma clang fp contract(off)
+  const int half = dk / 2;
+  const int bh = blockIdx.y, b = bh / H, h = bh - b * H;
+  const int idx = blockIdx.x * blockDim.x + threadIdx.x;  // row · half + pair
+  const int s = idx / half, i = idx - s * half;
+  if (s >= S || (seq_len && s >= seq_len[b])) return;
+  const int p = (pos_base ? pos_base[b] : 0) + s;
+  if (p < 0 || p >= max_len) return;
+  const float c = static_cast<float>(cosv[static_cast<size_t>(p) * half + i]);
+  const float sn = static_cast<float>(sinv[static_cast<size_t>(p) * half + i]);
+  auto rot = [&](T* row) {
+    const float x1 = static_cast<float>(row[i]), x2 = static_cast<float>(row[i + half]);
+    const float a = rnd<T>(rnd<T>(x1 * c) - rnd<T>(x2 * sn));
+    const float bb = rnd<T>(rnd<T>(x1 * sn) + rnd<T>(x2 * c));
+    row[i] = static_cast<T>(a);
+    row[i + half] = static_cast<T>(bb);
+  };
+  rot(q + (static_cast<size_t>(bh) * S + s) * dk);
+  rot(k + b * sb + h * sh + static_cast<long long>(p) * dk);
 }
 
 // RMSNorm (kernels/fused_rmsnorm.py:360-369).
@@ -129,6 +171,27 @@ int launch_embed(int dt, const int64_t* ids, const void* emb, const void* pos,
   else
     embed_kernel<float><<<grid, block, 0, st>>>(ids, (const float*)emb, (const float*)pos,
                                                 pos_base, (float*)out, S, d, V, P, err);
+  NML_LAUNCHED();
+  return 0;
+}
+
+int launch_rope(int dt, void* q, void* k, long long kv_stride_b, long long kv_stride_h, int B,
+                int H, int S, int dk, const int32_t* pos_base, const int32_t* seq_len,
+                const void* cos, const void* sin, int max_len, hipStream_t st) {
+  if (B * H * S == 0) return 0;
+  NML_REQUIRE(dk % 2 == 0, "rope: head_dim %d must be even", dk);
+  const int n = S * (dk / 2);
+  dim3 grid((n + 255) / 256, B * H);
+  if (dt == F16)
+    rope_kernel<half_t><<<grid, 256, 0, st>>>(static_cast<half_t*>(q), static_cast<half_t*>(k),
+                                              kv_stride_b, kv_stride_h, H, S, dk, pos_base, seq_len,
+                                              static_cast<const half_t*>(cos),
+                                              static_cast<const half_t*>(sin), max_len);
+  else
+    rope_kernel<float><<<grid, 256, 0, st>>>(static_cast<float*>(q), static_cast<float*>(k),
+                                             kv_stride_b, kv_stride_h, H, S, dk, pos_base, seq_len,
+                                             static_cast<const float*>(cos),
+                                             static_cast<const float*>(sin), max_len);
   NML_LAUNCHED();
   return 0;
 }

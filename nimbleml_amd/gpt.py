@@ -65,8 +65,6 @@ class GPT(Module):
             raise ValueError("fused_trunk requires fused_blocks=True.")
         if not fused_blocks:
             raise ValueError("nimbleml_amd implements the fused_blocks=True path of GPT.")
-        if use_rope:
-            raise NotImplementedError("use_rope is not part of this HIP path yet.")
         self.vocab_size = vocab_size
         self.d_model = d_model
         self.num_heads = num_heads
@@ -76,12 +74,22 @@ class GPT(Module):
         self.fused_blocks = fused_blocks
         self.fused_trunk = fused_trunk
         self.gradient_checkpointing = bool(gradient_checkpointing)
-        self.use_rope = False
+        self.use_rope = bool(use_rope)
         self.token_emb = Embedding(vocab_size, d_model)
-        self.pos_emb = Embedding(max_seq_len, d_model)
+        # rotary positions replace the learned table (models/gpt.py:46-53)
+        self.pos_emb = None if self.use_rope else Embedding(max_seq_len, d_model)
+        if self.use_rope:
+            from nimbleml_amd.rope import build_rope_cache
+
+            self._rope_cos, self._rope_sin = build_rope_cache(max_seq_len, d_model // num_heads)
+        else:
+            self._rope_cos = self._rope_sin = None
         block_modules = [FusedTransformerBlock(d_model, num_heads, ff_mult,
                                                gradient_checkpointing=gradient_checkpointing)
                          for _ in range(num_layers)]
+        if self.use_rope:
+            for block in block_modules:
+                block.mha._rope_cache = (self._rope_cos, self._rope_sin)
         self.ln = RMSNorm(d_model)
         self.blocks = (FusedGPTTrunk(block_modules, self.ln) if fused_trunk
                        else Sequential(*block_modules))
@@ -97,7 +105,8 @@ class GPT(Module):
         params = []
         for layer in (self.token_emb, self.blocks):
             params.extend(layer.parameters())
-        params.extend(self.pos_emb.parameters())
+        if self.pos_emb is not None:
+            params.extend(self.pos_emb.parameters())
         if not self.fused_trunk:
             params.extend(self.ln.parameters())
         return params
@@ -112,9 +121,15 @@ class GPT(Module):
         def a(t, shape=None):
             return np.ascontiguousarray(np.asarray(t.data, dtype=dt).reshape(shape or t.shape))
 
-        out = [(N.P_TOKEN_EMB, 0, a(self.token_emb.weights)),
-               (N.P_POS_EMB, 0, a(self.pos_emb.weights)),
-               (N.P_LN_F, 0, a(self.ln.gamma))]
+        out = [(N.P_TOKEN_EMB, 0, a(self.token_emb.weights)), (N.P_LN_F, 0, a(self.ln.gamma))]
+        if self.use_rope:
+            # the first half of each row, cast to the compute dtype as apply_rope_flat
+            # casts it (utils/rope.py:36-38)
+            half = (self.d_model // self.num_heads) // 2
+            out += [(N.P_ROPE_COS, 0, np.ascontiguousarray(self._rope_cos[:, :half].astype(dt))),
+                    (N.P_ROPE_SIN, 0, np.ascontiguousarray(self._rope_sin[:, :half].astype(dt)))]
+        else:
+            out.append((N.P_POS_EMB, 0, a(self.pos_emb.weights)))
         for i, blk in enumerate(self._block_list):
             m = blk.mha
             wqkv = np.concatenate([a(m.W_q.weights), a(m.W_k.weights), a(m.W_v.weights)], axis=1)

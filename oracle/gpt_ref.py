@@ -27,10 +27,40 @@ def embed(tok_w, pos_w, ids):
     """
     ids = np.asarray(ids, dtype=np.int64)
     s = ids.shape[1]
+    x = tok_w[ids.reshape(-1)].reshape(ids.shape[0], s, tok_w.shape[1])
+    if pos_w is None:  # rotary positions: no learned table (models/gpt.py:85)
+        return x
     if s > pos_w.shape[0]:
         raise ValueError(f"Sequence length {s} exceeds maximum sequence length {pos_w.shape[0]}")
-    x = tok_w[ids.reshape(-1)].reshape(ids.shape[0], s, tok_w.shape[1])
     return x + pos_w[:s]
+
+
+def rope_cache(seq_len, head_dim, base=10000.0):
+    """utils/rope.py:12-19: float32 ``(cos, sin)``, ``(seq_len, head_dim)``, both halves of
+    a row holding ``position · base^(-i/half)``."""
+    half = head_dim // 2
+    inv_freq = 1.0 / (base ** (np.arange(0, half, dtype=np.float32) / float(half)))
+    t = np.arange(seq_len, dtype=np.float32)
+    freqs = np.outer(t, inv_freq)
+    emb = np.concatenate([freqs, freqs], axis=-1)
+    return np.cos(emb).astype(np.float32), np.sin(emb).astype(np.float32)
+
+
+def apply_rope(x, cos, sin, offset=0):
+    """utils/rope.py:22-44 (GPT-NeoX half split) on ``x`` (..., seq, head_dim): pair
+    (i, i + half) rotated by position·θ_i, the tables cast to x's dtype first. ``offset``
+    is the first row's position (0 in the reference, which re-forwards from position 0;
+    the incremental oracle feeds later positions)."""
+    seq = x.shape[-2]
+    half = x.shape[-1] // 2
+    c = cos[offset:offset + seq, :half].astype(x.dtype, copy=False)
+    s = sin[offset:offset + seq, :half].astype(x.dtype, copy=False)
+    x1 = x[..., :half]
+    x2 = x[..., half:]
+    out = np.empty_like(x)
+    out[..., :half] = x1 * c - x2 * s
+    out[..., half:] = x1 * s + x2 * c
+    return out
 
 
 def rmsnorm(x, gamma, eps=RMS_EPS):
@@ -89,8 +119,9 @@ def _merge_heads(a, b, s, h, dk):
     return np.transpose(a.reshape(b, h, s, dk), (0, 2, 1, 3)).reshape(b, s, h * dk)
 
 
-def mha(x, w, prefix, num_heads, mask):
-    """neural_network/_fused_arrays.py:52-126 (no RoPE)."""
+def mha(x, w, prefix, num_heads, mask, rope=None):
+    """neural_network/_fused_arrays.py:52-126; rope = (cos, sin) rotates q and k after the
+    head split (:95-98)."""
     b, s, d = x.shape
     dk = d // num_heads
     scale = float(dk) ** 0.5  # neural_network/attention.py:135
@@ -103,6 +134,9 @@ def mha(x, w, prefix, num_heads, mask):
     q = _split_heads(qkv[:, :d].reshape(b, s, d), b, s, num_heads, dk)
     k = _split_heads(qkv[:, d:2 * d].reshape(b, s, d), b, s, num_heads, dk)
     v = _split_heads(qkv[:, 2 * d:].reshape(b, s, d), b, s, num_heads, dk)
+    if rope is not None:
+        q = apply_rope(q, rope[0], rope[1])
+        k = apply_rope(k, rope[0], rope[1])
     att = sdpa(q, k, v, scale, mask)
     merged = _merge_heads(att, b, s, num_heads, dk).reshape(b * s, d)
     out = merged @ w[prefix + "W_o.weights"]
@@ -122,22 +156,25 @@ def ffn(x, w, prefix):
     return out.reshape(shape)
 
 
-def block(x, w, i, num_heads, mask):
+def block(x, w, i, num_heads, mask, rope=None):
     """neural_network/_fused_arrays.py:251-284: x + MHA(LN1(x)); x + FFN(LN2(x))."""
     p = f"blocks.layers.{i}."
     b, s, d = x.shape
     n1 = rmsnorm(x.reshape(b * s, d), w[p + "ln1.gamma"]).reshape(x.shape)
-    x_mid = x + mha(n1, w, p + "mha.", num_heads, mask)
+    x_mid = x + mha(n1, w, p + "mha.", num_heads, mask, rope)
     n2 = rmsnorm(x_mid.reshape(b * s, d), w[p + "ln2.gamma"]).reshape(x.shape)
     return x_mid + ffn(n2, w, p + "ffn.")
 
 
-def hidden_states(w, ids, num_heads, num_layers):
-    """models/gpt.py:76-90 (``fused_blocks=True``, no RoPE, no fused trunk)."""
-    x = embed(w["token_emb.weights"], w["pos_emb.weights"], ids)
+def hidden_states(w, ids, num_heads, num_layers, rope=None):
+    """models/gpt.py:76-90 (``fused_blocks=True``, no fused trunk); rope = the (cos, sin)
+    cache of a ``use_rope=True`` model, which has no pos_emb."""
+    if rope is not None and np.asarray(ids).shape[1] > rope[0].shape[0]:
+        raise ValueError("Sequence length exceeds maximum sequence length")
+    x = embed(w["token_emb.weights"], None if rope is not None else w["pos_emb.weights"], ids)
     mask = causal_mask(x.shape[1], x.dtype)
     for i in range(num_layers):
-        x = block(x, w, i, num_heads, mask)
+        x = block(x, w, i, num_heads, mask, rope)
     b, s, d = x.shape
     return rmsnorm(x.reshape(b * s, d), w["ln.gamma"]).reshape(x.shape)
 
@@ -148,9 +185,9 @@ def tied_logits(h, emb):
     return np.matmul(h.reshape(b * s, d), np.swapaxes(emb, -2, -1)).reshape(b, s, emb.shape[0])
 
 
-def forward(w, ids, num_heads, num_layers):
+def forward(w, ids, num_heads, num_layers, rope=None):
     """``GPT.forward`` (models/gpt.py:92-121): all-position logits (B, S, V)."""
-    return tied_logits(hidden_states(w, ids, num_heads, num_layers), w["token_emb.weights"])
+    return tied_logits(hidden_states(w, ids, num_heads, num_layers, rope), w["token_emb.weights"])
 
 
 def crossentropy(logits, labels):
@@ -169,11 +206,11 @@ def crossentropy(logits, labels):
     return float(np.sum(per_sample) / n)
 
 
-def compute_loss(w, ids, labels, num_heads, num_layers, ignore_index=None):
+def compute_loss(w, ids, labels, num_heads, num_layers, ignore_index=None, rope=None):
     """``GPT.compute_loss`` (models/gpt.py:123-137) → ``forward_tied``
     (losses/cross_entropy.py:109-148) → kernels/fused_tied_crossentropy.py:8-24.
     ``ignore_index`` rows are dropped first (losses/_ce_prepare.py:46-69)."""
-    h = hidden_states(w, ids, num_heads, num_layers)
+    h = hidden_states(w, ids, num_heads, num_layers, rope)
     b, s, d = h.shape
     h2d = h.reshape(b * s, d)
     labels = np.asarray(labels, dtype=np.int64).reshape(-1)
@@ -240,7 +277,7 @@ def sample_logits(logits_1d, *, temperature, top_k, top_p, u=None, token_ids=Non
 
 
 def generate(w, ids, num_heads, num_layers, *, max_new_tokens=64, temperature=0.8, top_k=0,
-             top_p=0.9, eos_id=None, repetition_penalty=1.0, uniforms=None):
+             top_p=0.9, eos_id=None, repetition_penalty=1.0, uniforms=None, rope=None):
     """models/generate.py:62-119 for a model without ``forward_with_cache`` (the
     reference ``GPT``): every step re-forwards the whole sequence and samples each
     row from its last-position logits. ``uniforms[t][b]`` replaces the t-th step's
@@ -253,7 +290,7 @@ def generate(w, ids, num_heads, num_layers, *, max_new_tokens=64, temperature=0.
     generated = [list(ids[b].tolist()) for b in range(batch)]
     for t in range(max_new_tokens):
         cur = np.asarray(generated, dtype=np.int64)
-        logits = forward(w, cur, num_heads, num_layers)
+        logits = forward(w, cur, num_heads, num_layers, rope)
         for b in range(batch):
             u = None if uniforms is None else uniforms[t][b]
             tok = sample_logits(logits[b, -1], temperature=temperature, top_k=top_k, top_p=top_p,
@@ -275,8 +312,9 @@ class KVOracle:
     on tokens 0..t. Used where a full re-forward per token is too slow.
     """
 
-    def __init__(self, w, num_heads, num_layers):
+    def __init__(self, w, num_heads, num_layers, rope=None):
         self.w = w
+        self.rope = rope
         self.h = num_heads
         self.n_layers = num_layers
         self.k = [None] * num_layers  # (B*H, t, dk)
@@ -288,8 +326,9 @@ class KVOracle:
         w = self.w
         ids = np.asarray(ids, dtype=np.int64)
         b, s = ids.shape
-        pos = w["pos_emb.weights"][self.t:self.t + s]
-        x = w["token_emb.weights"][ids.reshape(-1)].reshape(b, s, -1) + pos
+        x = w["token_emb.weights"][ids.reshape(-1)].reshape(b, s, -1)
+        if self.rope is None:
+            x = x + w["pos_emb.weights"][self.t:self.t + s]
         d = x.shape[-1]
         dk = d // self.h
         scale = float(dk) ** 0.5
@@ -305,6 +344,9 @@ class KVOracle:
             q = _split_heads(qkv[:, :d], b, s, self.h, dk)
             k = _split_heads(qkv[:, d:2 * d], b, s, self.h, dk)
             v = _split_heads(qkv[:, 2 * d:], b, s, self.h, dk)
+            if self.rope is not None:
+                q = apply_rope(q, self.rope[0], self.rope[1], self.t)
+                k = apply_rope(k, self.rope[0], self.rope[1], self.t)
             self.k[i] = k if self.k[i] is None else np.concatenate([self.k[i], k], axis=1)
             self.v[i] = v if self.v[i] is None else np.concatenate([self.v[i], v], axis=1)
             att = sdpa(q, self.k[i], self.v[i], scale, mask)
