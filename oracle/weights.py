@@ -110,3 +110,18 @@ def make_weights(cfg: GPTConfig, seed: int = 0, dtype=np.float32, rich: bool = F
 def random_ids(shape, vocab: int, seed: int) -> np.ndarray:
     """Uniform token ids in [0, vocab) as int64."""
     return np.random.default_rng([seed, 7919]).integers(0, vocab, size=shape, dtype=np.int64)
+
+
+ROPE_QK_SCALE = 6.0
+
+
+def rope_weights(w: dict) -> dict:
+    """Parameters of a ``use_rope=True`` model from :func:`make_weights` output (apply
+    before any cast): no ``pos_emb.weights`` (models/gpt.py:46), and W_q, W_k scaled by
+    ROPE_QK_SCALE so that q·k is large enough for rotary positions to move the logits
+    visibly (a test choice, not a reference default)."""
+    out = {k: v for k, v in w.items() if k != "pos_emb.weights"}
+    for k in out:
+        if k.endswith("mha.W_q.weights") or k.endswith("mha.W_k.weights"):
+            out[k] = out[k] * np.float32(ROPE_QK_SCALE)
+    return out

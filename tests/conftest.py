@@ -29,9 +29,15 @@ def fixture_config(f):
 def fixture_weights(f, dtype=None):
     from oracle.weights import make_weights
 
+    from oracle.weights import rope_weights
+
     cfg = fixture_config(f)
     if dtype is None:
         dtype = np.float16 if str(f["dtype"]) == "float16" else np.float32
+    if "rope" in f.files and int(f["rope"]):  # rotary-position fixtures (weights changed in fp32)
+        w = rope_weights(make_weights(cfg, seed=int(f["seed"]), dtype=np.float32,
+                                      rich=bool(int(f["rich"]))))
+        return cfg, {k: v.astype(dtype) for k, v in w.items()}
     return cfg, make_weights(cfg, seed=int(f["seed"]), dtype=dtype, rich=bool(int(f["rich"])))
 
 

@@ -38,6 +38,8 @@ CASES = {
     "small_rich_fp32": ("SMALL", "float32", True),
     "small_ragged_fp32": ("SMALL", "float32", True),
     "c3slice_fp16": ("C3SLICE", "float16", True),
+    "tiny_rope_fp32": ("TINY", "float32", True),
+    "tiny_rope_fp16": ("TINY", "float16", True),
     "ops_fp32": (None, "float32", False),
     "ops_fp16": (None, "float16", False),
 }
@@ -52,11 +54,12 @@ def _config(name):
     return {"TINY": TINY, "SMALL": SMALL}[name]
 
 
-def _build_model(cfg, w):
+def _build_model(cfg, w, use_rope=False):
     import NimbleML
 
     model = NimbleML.GPT(cfg.vocab_size, cfg.d_model, cfg.num_heads, cfg.num_layers,
-                         cfg.max_seq_len, ff_mult=cfg.ff_mult, fused_blocks=True)
+                         cfg.max_seq_len, ff_mult=cfg.ff_mult, fused_blocks=True,
+                         use_rope=use_rope)
     with tempfile.TemporaryDirectory() as tmp:
         path = os.path.join(tmp, "w.npz")
         np.savez(path, **w)
@@ -99,13 +102,31 @@ def run_model_case(name, cfg_name, dtype, rich):
     cfg = _config(cfg_name)
     npdt = np.float16 if dtype == "float16" else np.float32
     seed = {"tiny": 11, "small": 23, "c3slice": 37}[name.split("_")[0]]
+    from oracle.weights import rope_weights
+
+    use_rope = "rope" in name
     w = make_weights(cfg, seed=seed, dtype=np.float32, rich=rich)
-    model = _build_model(cfg, w)
+    if use_rope:
+        w = rope_weights(w)
+    model = _build_model(cfg, w, use_rope)
     out = {"config": np.array([cfg.vocab_size, cfg.d_model, cfg.num_heads, cfg.num_layers,
                                cfg.max_seq_len, cfg.ff_mult], dtype=np.int64),
-           "seed": np.array(seed), "rich": np.array(int(rich)), "dtype": np.array(dtype)}
+           "seed": np.array(seed), "rich": np.array(int(rich)), "dtype": np.array(dtype),
+           "rope": np.array(int(use_rope))}
 
-    if cfg_name == "TINY":
+    if use_rope:
+        b, s0, n = 2, 8, 24
+        ids = random_ids((b, s0), cfg.vocab_size, seed)
+        out["prompt"] = ids
+        out["greedy"] = _gen(model, ids, None, n, temperature=0.0)
+        out["greedy_logits"] = _forward_last(model, out["greedy"][:, :-1])
+        lids = random_ids((2, 32), cfg.vocab_size, seed + 1)
+        labels = random_ids((2, 32), cfg.vocab_size, seed + 2)
+        out["loss_ids"], out["loss_labels"] = lids, labels
+        out["loss"] = np.array(_loss(model, lids, labels))
+        out["topk_tokens"] = _gen(model, ids, 123, n, temperature=0.8, top_k=50, top_p=1.0)
+        out["topk_u"] = _uniforms(123, n, b)
+    elif cfg_name == "TINY":
         b, s0, n = 2, 8, 24
         ids = random_ids((b, s0), cfg.vocab_size, seed)
         out["prompt"] = ids

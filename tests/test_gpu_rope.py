@@ -87,3 +87,41 @@ def test_rope_ragged_greedy_decode_fp16(gpu, lens):
             compared += 1
             lg = kv.step(got[None, len(r) + t:len(r) + t + 1])[0, -1]
     assert compared >= 3 * len(rows), compared
+
+
+@pytest.mark.parametrize("name", ["tiny_rope_fp32", "tiny_rope_fp16"])
+def test_rope_reference_fixture(gpu, name):
+    """Against the reference's own use_rope=True run (tests/golden/make_golden.py):
+    all-position logits within the logit tolerance, the loss, and greedy tokens while
+    the oracle's decision margin exceeds that tolerance."""
+    import nimbleml_amd as nm
+    from conftest import fixture_weights, golden
+
+    f = golden(name)
+    cfg, w = fixture_weights(f)
+    dt = w["token_emb.weights"].dtype
+    tol = 3e-2 if dt == np.float16 else 1e-3
+    m = nm.GPT.from_arrays(w, cfg.vocab_size, cfg.d_model, cfg.num_heads, cfg.num_layers,
+                           cfg.max_seq_len, ff_mult=cfg.ff_mult, dtype=dt, use_rope=True)
+    lg = m.forward(f["greedy"][:, :-1]).numpy().astype(np.float64)
+    assert np.abs(lg - f["greedy_logits"].astype(np.float64)).max() <= tol
+    got = m.compute_loss(f["loss_ids"], f["loss_labels"]).item()
+    assert abs(got - float(f["loss"])) <= (2 ** -8 if dt == np.float16 else 1e-4) * abs(got)
+    s0 = f["prompt"].shape[1]
+    n = f["greedy"].shape[1] - s0
+    out = nm.generate(m, f["prompt"], max_new_tokens=n, temperature=0.0)
+    rope = R.rope_cache(cfg.max_seq_len, cfg.d_model // cfg.num_heads)
+    kv = R.KVOracle({k: v.astype(np.float32) for k, v in w.items()}, cfg.num_heads,
+                    cfg.num_layers, rope)
+    ref = f["greedy"]
+    lgo = kv.step(ref[:, :s0])[:, -1]
+    compared = 0
+    alive = np.ones(ref.shape[0], bool)
+    for t in range(n):
+        top2 = np.sort(lgo.astype(np.float64), axis=-1)[:, -2:]
+        alive &= (top2[:, 1] - top2[:, 0]) > tol
+        for b in np.nonzero(alive)[0]:
+            assert out[b, s0 + t] == ref[b, s0 + t], (b, t)
+            compared += 1
+        lgo = kv.step(ref[:, s0 + t:s0 + t + 1])[:, -1]
+    assert compared >= n, compared

@@ -112,3 +112,35 @@ def test_use_rope_model_has_no_position_table():
     names = {n for n, _ in nm.saveload.named_parameters(m)}
     assert "pos_emb.weights" not in names and "token_emb.weights" in names
     assert m._rope_cos.shape == (16, 8)
+
+
+def _rope_fixture(name):
+    from conftest import fixture_weights, golden
+
+    f = golden(name)
+    cfg, w = fixture_weights(f)
+    assert int(f["rope"]) == 1 and "pos_emb.weights" not in w
+    return f, cfg, w, R.rope_cache(cfg.max_seq_len, cfg.d_model // cfg.num_heads)
+
+
+def test_oracle_matches_reference_rope_fixtures():
+    """The reference's own use_rope=True GPT (tests/golden/make_golden.py): greedy tokens,
+    all-position logits, the loss and top-k sampled tokens."""
+    for name in ("tiny_rope_fp32", "tiny_rope_fp16"):
+        f, cfg, w, rope = _rope_fixture(name)
+        H, L = cfg.num_heads, cfg.num_layers
+        n = f["greedy"].shape[1] - f["prompt"].shape[1]
+        g = R.generate(w, f["prompt"], H, L, max_new_tokens=n, temperature=0.0, rope=rope)
+        assert np.array_equal(g, f["greedy"]), name
+        lg = R.forward(w, f["greedy"][:, :-1], H, L, rope)
+        ref = f["greedy_logits"]
+        if ref.dtype == np.float16:
+            assert np.array_equal(lg, ref), name  # fp16: bit-exact op-by-op restatement
+        else:
+            assert np.abs(lg - ref).max() < 1e-5, name
+        loss = R.compute_loss(w, f["loss_ids"], f["loss_labels"], H, L, rope=rope)
+        rnd = np.float16 if ref.dtype == np.float16 else np.float32
+        assert float(rnd(loss)) == float(f["loss"]), name
+        toks = R.generate(w, f["prompt"], H, L, max_new_tokens=n, uniforms=f["topk_u"],
+                          temperature=0.8, top_k=50, top_p=1.0, rope=rope)
+        assert np.array_equal(toks, f["topk_tokens"]), name
