@@ -176,6 +176,9 @@ def main():
     ap.add_argument("--only", choices=["c3", "c4", "c5"], default=None,
                     help="run one workload only (for profiling); c4/c5 print their own line")
     ap.add_argument("--cpu-tokens", type=int, default=12)
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="only copy 256 MiB device to device three times (the known-size "
+                         "reference for scaling the FETCH_SIZE / WRITE_SIZE counters)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported: this path does "
@@ -188,6 +191,16 @@ def main():
 
     cfg = C3
     nm._native.ensure_init()
+    if args.copy_calibration:
+        N = nm._native
+        nbytes = 256 << 20
+        src, dst = N.DeviceArray((nbytes,), "uint8"), N.DeviceArray((nbytes,), "uint8")
+        N.check(N.lib.nml_memset(src.ptr, 1, nbytes))
+        for _ in range(3):
+            N.check(N.lib.nml_memcpy_d2d(dst.ptr, src.ptr, nbytes))
+        N.synchronize()
+        print(json.dumps({"copy_calibration_bytes": nbytes, "copies": 3}), flush=True)
+        return
     if args.only == "c5":
         print(json.dumps({"c5": bench_c5(nm)}), flush=True)
         return
