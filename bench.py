@@ -135,6 +135,32 @@ def bench_c4(nm, cfg, model, use_graph, reps=2):
                          "frac": round(achieved / HBM_PEAK_GBS, 4)}}
 
 
+def bench_adamw(nm, n=337_100_000, steps=20):
+    """AdamW over one float32 buffer the size of the C3 model (337.1 M parameters): the
+    step reads param, grad, m, v and writes param, m, v — 28 B per element."""
+    N = nm._native
+    from nimbleml_amd import kernels as K
+
+    bufs = [N.DeviceArray((n,), np.float32) for _ in range(4)]
+    for b, val in zip(bufs, (1, 0, 0, 0)):
+        N.check(N.lib.nml_memset(b.ptr, val, b.nbytes))
+    p, g, m, v = bufs
+    args = (1e-3, 0.9, 0.999, 0.1, 0.001, 1e-8, 0.01)
+    K.adamw_step(p, g, m, v, *args)
+    N.synchronize()
+    t = N.Timer()
+    t.start()
+    for _ in range(steps):
+        K.adamw_step(p, g, m, v, *args)
+    ms = t.stop() / steps
+    gbs = 28.0 * n / (ms * 1e-3) / 1e9
+    return {"workload": "AdamW step, float32 state, 337.1 M parameters (the C3 model's count)",
+            "ms_per_step": round(ms, 4), "elements": n,
+            "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS,
+                         "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4),
+                         "bytes_per_element": 28}}
+
+
 def bench_c5(nm, reps=2):
     from oracle.weights import C5, make_weights, random_ids
 
@@ -173,7 +199,7 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-graph", action="store_true")
     ap.add_argument("--only-c3", action="store_true", help="skip the batch-32 and prefill lines")
-    ap.add_argument("--only", choices=["c3", "c4", "c5"], default=None,
+    ap.add_argument("--only", choices=["c3", "c4", "c5", "adamw"], default=None,
                     help="run one workload only (for profiling); c4/c5 print their own line")
     ap.add_argument("--cpu-tokens", type=int, default=12)
     ap.add_argument("--copy-calibration", action="store_true",
@@ -203,6 +229,9 @@ def main():
         return
     if args.only == "c5":
         print(json.dumps({"c5": bench_c5(nm)}), flush=True)
+        return
+    if args.only == "adamw":
+        print(json.dumps({"adamw": bench_adamw(nm)}), flush=True)
         return
     w16 = make_weights(cfg, seed=1234, dtype=np.float16)
     model = nm.GPT.from_arrays(w16, cfg.vocab_size, cfg.d_model, cfg.num_heads, cfg.num_layers,

@@ -102,6 +102,20 @@ int nml_sample_device(const void* logits, size_t batch, size_t vocab, float temp
                       const int64_t* history, size_t history_stride, const int32_t* hist_len,
                       int64_t* out_ids, int dtype);
 
+/* Optimizer step, float32 state, in place on device buffers.
+ * adamw_step (native/src/module.cpp:175-188 → adamw_step_cpu, native/src/adamw.cpp:6-20):
+ * the same operation order, so results equal the reference's bit for bit. n elements;
+ * all four buffers 16-byte aligned. */
+int nml_adamw_step_device(float* param, const float* grad, float* m, float* v, size_t n, float lr,
+                          float beta1, float beta2, float bias1, float bias2, float eps,
+                          float weight_decay);
+/* clip_grad_norm (module.cpp:190-200 → clip_grad_norm_cpu, adamw.cpp:22-37): the global L2
+ * norm of n_tensors gradients (device pointers in a host array, element counts in sizes),
+ * accumulated in float64; when it exceeds max_norm every gradient is scaled by
+ * max_norm / (norm + 1e-6). Writes the norm (float) to *norm; returns when done. */
+int nml_clip_grad_norm_device(float* const* grads, const size_t* sizes, size_t n_tensors,
+                              float max_norm, float* norm);
+
 /* ------------------------------------------------------------ GPT model ---- */
 
 /* Parameter kinds for nml_model_set_param. Host data must already be in device

@@ -1,0 +1,207 @@
+// Optimizer step on the device: AdamW over float32 state and the global-norm gradient
+// clip, the reference's native CPU kernels (native/src/adamw.cpp:6-37, bound as
+// adamw_step / clip_grad_norm in native/src/module.cpp:175-200). Both are HBM-bound
+// elementwise passes.
+#include <vector>
+
+#include "kernels.hpp"
+#include "nimbleml_hip.h"
+
+namespace nml {
+
+namespace {
+
+typedef float floatv4 __attribute__((ext_vector_type(4)));
+
+// One element of adamw_step_cpu, in its operation order (float32, no contraction):
+//   m = β1·m + (1−β1)·g;  v = β2·v + ((1−β2)·g)·g;  s = (lr·(m/bias1)) / (√(v/bias2) + ε)
+//   p = p·(1 − lr·wd)  (only when wd ≠ 0);  p = p − s
+struct AdamW {
+  float lr, b1, b2, bias1, bias2, eps, decay;
+  bool wd;
+  __device__ __forceinline__ void operator()(float& p, float g, float& m, float& v) const {
+#pragma clang fp contract(off)
+    m = b1 * m + (1.0f - b1) * g;
+    v = b2 * v + (1.0f - b2) * g * g;
+    const float mhat = m / bias1;
+    const float vhat = v / bias2;
+    const float s = lr * mhat / (sqrtf(vhat) + eps);
+    if (wd) p *= decay;
+    p -= s;
+  }
+};
+
+// 16-byte vectors for the bulk (grid-stride), one element per lane for the tail.
+__global__ __launch_bounds__(256) void adamw_kernel(float* __restrict__ p, const float* __restrict__ g,
+                                                   float* __restrict__ m, float* __restrict__ v,
+                                                   size_t n, AdamW op) {
+  const size_t nv = n / 4;
+  const size_t stride = static_cast<size_t>(gridDim.x) * blockDim.x;
+  const size_t first = static_cast<size_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  for (size_t i = first; i < nv; i += stride) {
+    floatv4 pp = reinterpret_cast<floatv4*>(p)[i];
+    const floatv4 gg = reinterpret_cast<const floatv4*>(g)[i];
+    floatv4 mm = reinterpret_cast<floatv4*>(m)[i];
+    floatv4 vv = reinterpret_cast<floatv4*>(v)[i];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      float pe = pp[e], me = mm[e], ve = vv[e];
+      op(pe, gg[e], me, ve);
+      pp[e] = pe;
+      mm[e] = me;
+      vv[e] = ve;
+    }
+    reinterpret_cast<floatv4*>(p)[i] = pp;
+    reinterpret_cast<floatv4*>(m)[i] = mm;
+    reinterpret_cast<floatv4*>(v)[i] = vv;
+  }
+  for (size_t j = nv * 4 + first; j < n; j += stride) op(p[j], g[j], m[j], v[j]);
+}
+
+// A piece of one gradient tensor: the clip's passes run over a flat list of pieces so one
+// launch covers every tensor.
+struct Piece {
+  float* ptr;
+  long long len;
+};
+constexpr long long kPiece = 1 << 16;
+
+// Σ g² of each piece in float64 (the reference accumulates double(g)·g in double).
+__global__ __launch_bounds__(256) void sumsq_kernel(const Piece* __restrict__ pieces,
+                                                    double* __restrict__ partial) {
+  __shared__ double red[4];
+  const Piece pc = pieces[blockIdx.x];
+  double s = 0.0;
+  for (long long i = threadIdx.x; i < pc.len; i += blockDim.x) {
+    const double x = pc.ptr[i];
+    s += x * x;
+  }
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) s += __shfl_xor(s, o, 64);
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = s;
+  __syncthreads();
+  if (threadIdx.x == 0) partial[blockIdx.x] = (red[0] + red[1]) + (red[2] + red[3]);
+}
+
+// Pieces' sums in a fixed order → norm = float(√total); scale = max_norm / (norm + 1e-6)
+// when norm > max_norm and norm > 0, else 1 (clip_grad_norm_cpu, adamw.cpp:22-37).
+__global__ __launch_bounds__(256) void clip_scale_kernel(const double* __restrict__ partial, int np,
+                                                         float max_norm, float* __restrict__ out) {
+  __shared__ double red[4];
+  double s = 0.0;
+  for (int i = threadIdx.x; i < np; i += blockDim.x) s += partial[i];
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) s += __shfl_xor(s, o, 64);
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = s;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    const double total = (red[0] + red[1]) + (red[2] + red[3]);
+    const float norm = static_cast<float>(sqrt(total));
+    out[0] = norm;
+    out[1] = (norm > max_norm && norm > 0.0f) ? max_norm / (norm + 1e-6f) : 1.0f;
+  }
+}
+
+__global__ __launch_bounds__(256) void clip_apply_kernel(const Piece* __restrict__ pieces,
+                                                         const float* __restrict__ ns) {
+  const float scale = ns[1];
+  if (scale == 1.0f) return;  // no clip: the gradients stay untouched, as in the reference
+  const Piece pc = pieces[blockIdx.x];
+  for (long long i = threadIdx.x; i < pc.len; i += blockDim.x) pc.ptr[i] *= scale;
+}
+
+}  // namespace
+
+int launch_adamw(float* p, const float* g, float* m, float* v, size_t n, float lr, float beta1,
+                 float beta2, float bias1, float bias2, float eps, float weight_decay,
+                 hipStream_t st) {
+#pragma clang fp contract(off)
+  if (n == 0) return 0;
+  NML_REQUIRE(((reinterpret_cast<uintptr_t>(p) | reinterpret_cast<uintptr_t>(g) |
+                reinterpret_cast<uintptr_t>(m) | reinterpret_cast<uintptr_t>(v)) & 15) == 0,
+              "adamw: buffers must be 16-byte aligned");
+  const float decay = 1.0f - lr * weight_decay;  // float, as adamw.cpp:16 computes it
+  AdamW op{lr, beta1, beta2, bias1, bias2, eps, decay, weight_decay != 0.0f};
+  // One 16-byte vector per thread (the whole grid in flight at once measured fastest:
+  // 0.70 of HBM peak at 337 M elements, against 0.56 for a 2048-block grid stride).
+  const size_t nv = (n + 3) / 4;
+  const size_t blocks = nv / 256 + 1;
+  NML_REQUIRE(blocks <= 0x7fffffff, "adamw: %zu elements exceed one launch", n);
+  adamw_kernel<<<static_cast<int>(blocks), 256, 0, st>>>(p, g, m, v, n, op);
+  NML_LAUNCHED();
+  return 0;
+}
+
+// Workspace of the clip: pieces, per-piece partial sums, then (norm, scale).
+struct ClipWs {
+  void* p = nullptr;
+  size_t bytes = 0;
+};
+static ClipWs g_clip;
+
+int launch_clip_grad_norm(float* const* grads, const size_t* sizes, size_t n_tensors,
+                          float max_norm, float* norm_out, hipStream_t st) {
+  std::vector<Piece> pieces;
+  for (size_t t = 0; t < n_tensors; ++t) {
+    NML_REQUIRE(sizes[t] == 0 || grads[t] != nullptr, "clip_grad_norm: tensor %zu is null", t);
+    for (long long o = 0; o < static_cast<long long>(sizes[t]); o += kPiece) {
+      const long long len = static_cast<long long>(sizes[t]) - o < kPiece
+                                ? static_cast<long long>(sizes[t]) - o : kPiece;
+      pieces.push_back(Piece{grads[t] + o, len});
+    }
+  }
+  if (pieces.empty()) {
+    *norm_out = 0.0f;
+    return 0;
+  }
+  const size_t np = pieces.size();
+  const size_t off_part = (np * sizeof(Piece) + 255) / 256 * 256;
+  const size_t off_ns = off_part + (np * sizeof(double) + 255) / 256 * 256;
+  const size_t need = off_ns + 256;
+  if (need > g_clip.bytes) {
+    if (g_clip.p) {
+      NML_HIP(hipStreamSynchronize(st));
+      NML_HIP(hipFree(g_clip.p));
+      g_clip = ClipWs{};
+    }
+    NML_HIP(hipMalloc(&g_clip.p, need));
+    g_clip.bytes = need;
+  }
+  char* ws = static_cast<char*>(g_clip.p);
+  Piece* dpieces = reinterpret_cast<Piece*>(ws);
+  double* partial = reinterpret_cast<double*>(ws + off_part);
+  float* ns = reinterpret_cast<float*>(ws + off_ns);
+  NML_HIP(hipMemcpyAsync(dpieces, pieces.data(), np * sizeof(Piece), hipMemcpyHostToDevice, st));
+  sumsq_kernel<<<static_cast<int>(np), 256, 0, st>>>(dpieces, partial);
+  NML_LAUNCHED();
+  clip_scale_kernel<<<1, 256, 0, st>>>(partial, static_cast<int>(np), max_norm, ns);
+  NML_LAUNCHED();
+  clip_apply_kernel<<<static_cast<int>(np), 256, 0, st>>>(dpieces, ns);
+  NML_LAUNCHED();
+  float host_ns[2];
+  NML_HIP(hipMemcpyAsync(host_ns, ns, sizeof(host_ns), hipMemcpyDeviceToHost, st));
+  NML_HIP(hipStreamSynchronize(st));
+  *norm_out = host_ns[0];
+  return 0;
+}
+
+}  // namespace nml
+
+extern "C" {
+
+int nml_adamw_step_device(float* param, const float* grad, float* m, float* v, size_t n, float lr,
+                          float beta1, float beta2, float bias1, float bias2, float eps,
+                          float weight_decay) {
+  return nml::launch_adamw(param, grad, m, v, n, lr, beta1, beta2, bias1, bias2, eps, weight_decay,
+                           nml::stream());
+}
+
+int nml_clip_grad_norm_device(float* const* grads, const size_t* sizes, size_t n_tensors,
+                              float max_norm, float* norm) {
+  NML_REQUIRE(norm != nullptr, "clip_grad_norm: norm output is null");
+  NML_REQUIRE(n_tensors == 0 || (grads != nullptr && sizes != nullptr),
+              "clip_grad_norm: tensor lists are null");
+  return nml::launch_clip_grad_norm(grads, sizes, n_tensors, max_norm, norm, nml::stream());
+}
+
+}  // extern "C"

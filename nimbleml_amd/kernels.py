@@ -9,6 +9,8 @@ Each takes host arrays or ``DeviceArray``s in the compute dtype and returns
   fused_tied_crossentropy_forward  kernels/fused_tied_crossentropy.py:8-24 (loss only)
   linear                      the `x @ W + b` of neural_network/_fused_arrays.py:25-30
   sample_tokens               models/generate.py:23-59 on a (batch, vocab) logits block
+  adamw_step                  native adamw_step (native/src/adamw.cpp:6-20), in place
+  clip_grad_norm              native clip_grad_norm (native/src/adamw.cpp:22-37), in place
 """
 from __future__ import annotations
 
@@ -156,3 +158,34 @@ def sample_tokens(logits, *, temperature, top_k=0, top_p=1.0, uniforms=None, his
                                     float(repetition_penalty), N.ptr(ud), N.ptr(hd), stride,
                                     N.ptr(hl), out.ptr, N.np_dtype_code(dt)))
     return out.numpy()
+
+
+def adamw_step(param, grad, m, v, lr, beta1, beta2, bias1, bias2, eps, weight_decay):
+    """AdamW update of float32 ``DeviceArray``s in place, the reference native kernel's
+    arithmetic (``native.adamw_step``, module.cpp:175-188): bias1/bias2 are the caller's
+    ``1 − β^t`` bias corrections, as optimizers/adam.py:93-94 passes them."""
+    arrs = [param, grad, m, v]
+    for a in arrs:
+        if not isinstance(a, N.DeviceArray) or a.dtype != np.float32:
+            raise TypeError("adamw_step takes float32 DeviceArrays")
+    n = param.size
+    if any(a.size != n for a in arrs):
+        raise ValueError("adamw_step: param, grad, m and v must have the same size")
+    N.check(N.lib.nml_adamw_step_device(param.ptr, grad.ptr, m.ptr, v.ptr, n, float(lr),
+                                        float(beta1), float(beta2), float(bias1), float(bias2),
+                                        float(eps), float(weight_decay)))
+
+
+def clip_grad_norm(grads, max_norm):
+    """Global L2 norm of float32 gradient ``DeviceArray``s, scaled in place to max_norm
+    when above it (``native.clip_grad_norm``, module.cpp:190-200). Returns the norm."""
+    grads = list(grads)
+    for g in grads:
+        if not isinstance(g, N.DeviceArray) or g.dtype != np.float32:
+            raise TypeError("clip_grad_norm takes float32 DeviceArrays")
+    ptrs = (C.c_void_p * max(1, len(grads)))(*[g.ptr for g in grads])
+    sizes = (C.c_size_t * max(1, len(grads)))(*[g.size for g in grads])
+    norm = C.c_float()
+    N.check(N.lib.nml_clip_grad_norm_device(ptrs, sizes, len(grads), float(max_norm),
+                                            C.byref(norm)))
+    return float(norm.value)
