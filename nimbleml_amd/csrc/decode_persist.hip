@@ -725,7 +725,7 @@ __global__ __launch_bounds__(kT) void decode_persist_kernel(PersistArgs a) {
 
   // ---------------------------------------------------------------- head
   const uint32_t tgh = base + 8u * a.L;
-  constexpr int HR = 4;  // rows per wave per round
+  constexpr int HR = 8;  // rows per wave per round
   const int r0 = static_cast<int>((static_cast<long long>(g) * a.V) / kG);
   const int r1 = static_cast<int>((static_cast<long long>(g + 1) * a.V) / kG);
   const T* E = emb;
