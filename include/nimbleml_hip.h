@@ -163,6 +163,29 @@ int nml_model_forward(nml_model* m, const int64_t* ids, size_t batch, size_t seq
 int nml_model_loss(nml_model* m, const int64_t* ids, const int64_t* labels, size_t batch,
                    size_t seq, int64_t ignore_index, int has_ignore, double* loss);
 
+/* ---- training (float32 models) -------------------------------------------------------
+ * compute_loss with the autograd graph kept, then loss.backward() (models/gpt.py:123-137;
+ * Tensor.backward, utils/tensor.py:286-332; the array-level backward of
+ * neural_network/_fused_arrays.py:129-377 and kernels/fused_tied_crossentropy.py:27-48).
+ * Gradients live on the device in a float32 arena laid out like the parameters: weight
+ * gradients are (out, in) like the device weights, and accumulate over backward calls
+ * (Tensor._accumulate_grad, utils/tensor.py:334-352) until nml_model_zero_grad. */
+
+/* Tensor.zero_grad (utils/tensor.py:271-279) for every parameter at once; allocates the
+ * gradient arena on first use. */
+int nml_model_zero_grad(nml_model* m);
+/* Device pointer of the float32 gradient of parameter (kind, layer), same shape as the
+ * parameter (Tensor.grad). */
+int nml_model_grad_ptr(nml_model* m, int kind, int layer, void** ptr);
+/* GPT.compute_loss (models/gpt.py:123-137) keeping the activations its backward needs;
+ * ids and labels (device int64) are copied. Same loss as nml_model_loss. */
+int nml_model_loss_train(nml_model* m, const int64_t* ids, const int64_t* labels, size_t batch,
+                         size_t seq, int64_t ignore_index, int has_ignore, double* loss);
+/* loss.backward(grad) after nml_model_loss_train (repeatable, as with retain_graph): adds grad_scale ×
+ * d(loss)/d(parameter) to every gradient (losses/cross_entropy.py:166-191, grad_scale =
+ * output.grad). Returns after the device finishes. */
+int nml_model_backward(nml_model* m, double grad_scale);
+
 /* KV cache for batch rows: K and V per layer, (batch, heads, max_seq, head_dim) each.
  * The seam generate() probes for (models/generate.py:93-100). */
 int nml_cache_create(nml_model* m, size_t batch, nml_cache** out);

@@ -66,6 +66,10 @@ _SIGS = {
     "nml_model_param_ptr": [vp, i32, i32, C.POINTER(vp)],
     "nml_model_forward": [vp, vp, sz, sz, vp, i32],
     "nml_model_loss": [vp, vp, vp, sz, sz, i64, i32, C.POINTER(C.c_double)],
+    "nml_model_zero_grad": [vp],
+    "nml_model_grad_ptr": [vp, i32, i32, C.POINTER(C.c_void_p)],
+    "nml_model_loss_train": [vp, vp, vp, sz, sz, i64, i32, C.POINTER(C.c_double)],
+    "nml_model_backward": [vp, C.c_double],
     "nml_cache_create": [vp, sz, C.POINTER(vp)],
     "nml_cache_destroy": [vp],
     "nml_cache_length": [vp, C.POINTER(sz)],

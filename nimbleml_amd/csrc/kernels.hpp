@@ -103,6 +103,9 @@ struct AttnArgs {
   // (b, head)) and its output rows start at row_start[b]. Null: S each, rows b·S + s.
   const int32_t* seq_len;
   const int32_t* row_start;
+  // Training: per (sequence, head, query) log Σ exp(score − max) + max of the softmax,
+  // (B, H, S) floats (float32 models only). Null: not written.
+  float* lse;
 };
 int launch_attention_prefill(int dt, const AttnArgs& a, hipStream_t st);
 
@@ -147,6 +150,67 @@ struct SampleArgs {
   int64_t* out_ids;         // optional (B) copy of the chosen ids
 };
 int launch_sample(int dt, const SampleArgs& a, hipStream_t st);
+
+// ------------------------------------------------------------ training (float32)
+// General GEMM of the backward pass: C(m, n) = Σ_k A(m, k)·B(n, k) over fp32 operands,
+// A(m, k) = a[m·lda + k] when a_kc (k contiguous) else a[k·lda + m]; B(n, k) likewise
+// with b, ldb, b_kc. C is row-major at ldc. Output modes: set, add (gradient
+// accumulation), or set to C·gelu'(aux(m, n)) (the GELU backward, aux = pre-activation
+// at ldaux).
+struct GemmBwdArgs {
+  const float* a;
+  long long lda;
+  const float* b;
+  long long ldb;
+  float* c;
+  long long ldc;
+  const float* aux;
+  long long ldaux;
+  int M, N, K;
+};
+enum GemmBwdOut : int { GB_SET = 0, GB_ADD = 1, GB_GELU = 2 };
+int launch_gemm_bwd(const GemmBwdArgs& g, bool a_kc, bool b_kc, int out, hipStream_t st);
+
+// RMSNorm backward over rows × d (kernels/fused_rmsnorm.py:208-217): dx = result, or
+// dx += result when acc; dgamma += Σ_rows dy·x/rms. part: scratch of
+// rmsnorm_bwd_parts(rows) · d floats.
+int rmsnorm_bwd_parts(int rows);
+int launch_rmsnorm_bwd(const float* dy, const float* x, const float* gamma, float* dx, int acc,
+                       float* dgamma, float* part, int rows, int d, float eps, hipStream_t st);
+// out[n] += Σ_rows a[r·lda + n] (bias gradients); part: colsum_parts(rows) · n floats.
+int colsum_parts(int rows);
+int launch_colsum(const float* a, long long lda, int rows, int n, float* out, float* part,
+                  hipStream_t st);
+// In place: logits rows → (softmax − onehot(label))·scale, ignored rows → 0
+// (kernels/fused_crossentropy.py:33-50).
+int launch_ce_grad(float* logits, int rows, int V, const int64_t* labels, long long ignore_index,
+                   int has_ignore, float scale, hipStream_t st);
+
+// Causal attention backward for one layer (kernels/fused_sdpa.py:26-29, :81-88). q, k, v
+// head-major (B, H, S, dk) as the forward saw them (after RoPE); o and dout merged-head
+// (B·S, H·dk); lse from the forward; dvec scratch (B, H, S). Writes dq, dk, dv into
+// dqkv (B·S, 3·H·dk) at column offsets 0, H·dk, 2·H·dk.
+struct AttnBwdArgs {
+  const float* q;
+  const float* k;
+  const float* v;
+  const float* o;
+  const float* dout;
+  const float* lse;
+  float* dvec;
+  float* dqkv;
+  int B, H, S, dk;
+  float scale;  // sqrt(dk), the divisor of the scores
+};
+int launch_attention_backward(const AttnBwdArgs& a, hipStream_t st);
+// RoPE backward on dqkv rows (the dq and dk parts): pair (i, i + dk/2) of row b·S + s
+// rotated by −θ at position s (cos/sin: (max_len, dk/2)).
+int launch_rope_backward(float* dqkv, int rows, int S, int H, int dk, const float* cos,
+                         const float* sin, hipStream_t st);
+// Embedding backward: dE[ids[r]] += g[r] (token rows), dpos[s] += Σ_b g[b·S + s]
+// (dpos null: none).
+int launch_embed_backward(const float* g, const int64_t* ids, float* demb, float* dpos, int B,
+                          int S, int d, int V, hipStream_t st);
 
 // Persistent decode step (batch 1): one launch of kPersistGroups workgroups runs the
 // whole token; see decode_persist.hip.

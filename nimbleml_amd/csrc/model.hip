@@ -13,66 +13,9 @@
 #include <cstring>
 #include <vector>
 
-#include "kernels.hpp"
-#include "nimbleml_hip.h"
+#include "model.hpp"
 
 using namespace nml;
-
-namespace {
-
-constexpr float kEps = 1e-5f;  // RMSNorm epsilon (layers/rms_norm.py:16)
-
-struct Layer {
-  void *ln1, *wqkv, *bqkv, *wo, *bo, *ln2, *w1, *b1, *w2, *b2;
-};
-
-struct Buf {
-  void* p = nullptr;
-  size_t bytes = 0;
-  int ensure(size_t want) {
-    if (want <= bytes) return 0;
-    if (p) {
-      NML_HIP(hipStreamSynchronize(nml::stream()));
-      NML_HIP(hipFree(p));
-      p = nullptr;
-      bytes = 0;
-    }
-    NML_HIP(hipMalloc(&p, want));
-    bytes = want;
-    return 0;
-  }
-  void release() {
-    if (p) (void)hipFree(p);
-    p = nullptr;
-    bytes = 0;
-  }
-};
-
-inline size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
-
-}  // namespace
-
-struct nml_model {
-  int V, d, H, L, P, F, dt, dk;
-  size_t es;
-  void* arena = nullptr;
-  size_t arena_bytes = 0;
-  void *emb = nullptr, *pos = nullptr, *lnf = nullptr;
-  // rotary positions (GPT(use_rope=True)): (P, dk/2) cos and sin tables; on once both set
-  void *rope_cos = nullptr, *rope_sin = nullptr;
-  bool rope_cos_set = false, rope_sin_set = false;
-  std::vector<Layer> layers;
-  Buf ws;         // activations
-  Buf kvs;        // K/V scratch for forward() without a cache
-  Buf logits_ws;  // logits chunk for compute_loss / generate
-  Buf small;      // device counters, positions, loss accumulators
-  Buf persist;    // persistent decode: layer pointer table, exchange slots, epoch
-  Buf ragged;     // packed ragged prefill: row table, lengths, row starts
-  // decode timing of the last generate()
-  float last_decode_ms = 0.f;
-  int last_decode_steps = 0;
-  int last_decode_persistent = 0;
-};
 
 struct nml_cache {
   nml_model* m;
@@ -83,7 +26,7 @@ struct nml_cache {
   std::vector<int32_t> len;    // host mirror
 };
 
-namespace {
+namespace nml {
 
 size_t param_elems(const nml_model* m, int kind) {
   const size_t d = m->d, F = m->F;
@@ -132,8 +75,18 @@ void** param_slot(nml_model* m, int kind, int layer) {
   return nullptr;
 }
 
-const int kLayerKinds[] = {NML_P_LN1, NML_P_WQKV, NML_P_BQKV, NML_P_WO, NML_P_BO,
-                           NML_P_LN2, NML_P_W1,   NML_P_B1,   NML_P_W2, NML_P_B2};
+const int kLayerKinds[10] = {NML_P_LN1, NML_P_WQKV, NML_P_BQKV, NML_P_WO, NML_P_BO,
+                             NML_P_LN2, NML_P_W1,   NML_P_B1,   NML_P_W2, NML_P_B2};
+
+int check_ready(nml_model* m) {
+  NML_REQUIRE(m != nullptr, "model is null");
+  NML_REQUIRE(m->emb && m->pos && m->lnf, "model parameters not uploaded");
+  return 0;
+}
+
+}  // namespace nml
+
+namespace {
 
 // Activation workspace for R rows (B·S) of one forward.
 struct Acts {
@@ -162,11 +115,6 @@ int acts_for(nml_model* m, int R, int Bdec, Acts* a) {
   a->ssq = ssq ? reinterpret_cast<float*>(b + 4 * rd + rf + part) : nullptr;
   return 0;
 }
-
-bool rope_on(const nml_model* m) { return m->rope_cos_set && m->rope_sin_set; }
-
-// Learned position table for the embedding; none with rotary positions.
-const void* posw(const nml_model* m) { return rope_on(m) ? nullptr : m->pos; }
 
 // Small device scratch: [0] int err, then B int32 positions etc.
 struct Small {
@@ -313,11 +261,6 @@ int head(nml_model* m, const Acts& a, int B, int S, void* logits, int last_only,
   return launch_linear(m->dt, lm, st);
 }
 
-int check_ready(nml_model* m) {
-  NML_REQUIRE(m != nullptr, "model is null");
-  NML_REQUIRE(m->emb && m->pos && m->lnf, "model parameters not uploaded");
-  return 0;
-}
 
 // One decode step for B rows of a cache: feeds tokens[b][pos[b]] at position
 // pos[b], leaves logits (B, V) in `logits`.
@@ -584,6 +527,7 @@ int nml_model_destroy(nml_model* m) {
   m->small.release();
   m->persist.release();
   m->ragged.release();
+  train_release(m);
   if (m->arena) (void)hipFree(m->arena);
   delete m;
   return 0;

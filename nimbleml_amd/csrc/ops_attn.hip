@@ -107,6 +107,7 @@ __global__ __launch_bounds__(64) void attn_prefill_kernel(AttnArgs a) {
     const float inv = 1.f / l;
 #pragma unroll
     for (int d = 0; d < DK; ++d) out[d] = static_cast<T>(o[d] * inv);
+    if (a.lse) a.lse[static_cast<size_t>(bh) * a.S + s] = m + logf(l);
   }
 }
 
@@ -604,6 +605,7 @@ __global__ __launch_bounds__(256, 2) void attn_prefill_mfma_kernel(AttnArgs a) {
 template <typename T, int DK>
 int prefill_typed(const AttnArgs& a, hipStream_t st) {
   if constexpr (sizeof(T) == 2 && (DK == 64 || DK == 128)) {
+    NML_REQUIRE(a.lse == nullptr, "attention: the log-sum-exp output needs a float32 model");
     dim3 grid((a.S + kFQ - 1) / kFQ, a.B * a.H);
     attn_prefill_mfma_kernel<DK><<<grid, 256, 0, st>>>(a);
     NML_LAUNCHED();

@@ -1,0 +1,620 @@
+// Backward of compute_loss on the device (float32 models): the GEMM of the backward's
+// transposed products, and the backward of RMSNorm, GELU (fused into a GEMM epilogue),
+// the cross-entropy, causal attention, RoPE and the embeddings, plus the column sums
+// behind the bias and gain gradients.
+//
+//  * gemm_bwd_kernel: 128 × 128 tile, 4 waves of 64 × 64, MFMA 32×32×2 fp32; either
+//    operand read k-contiguous (rows of a row-major matrix) or m/n-contiguous (columns),
+//    staged through LDS as [k][row] so every MFMA fragment read is a contiguous row.
+//  * attention backward: per (sequence, head), one kernel owns a tile of keys and
+//    walks the queries after it (dK, dV), another owns a tile of queries and walks the
+//    keys before it (dQ); both recompute P = exp(q·k/√dk − lse) from the forward's
+//    log-sum-exp, so no (S × S) matrix is kept.
+//  * reductions over rows (bias / gain gradients) go through per-block partial rows
+//    and a second pass in a fixed order: the result does not depend on scheduling.
+#include "kernels.hpp"
+
+namespace nml {
+
+namespace {
+
+// ------------------------------------------------------------------ backward GEMM
+constexpr int kGM = 128, kGK = 16, kGPad = 4;
+
+// gelu'(x) of native/src/gelu.cpp:23-33 (tanh recomputed from x as the forward did).
+__device__ __forceinline__ float gelu_grad(float x) {
+#pragma clang fp contract(off)
+  const float x3 = x * x * x;
+  const float tu = tanhf(0.7978845608028654f * (x + 0.044715f * x3));
+  const float du_dx = 0.7978845608028654f * (1.0f + 0.134145f * x * x);
+  const float sech2 = 1.0f - tu * tu;
+  return 0.5f * (1.0f + tu) + 0.5f * x * sech2 * du_dx;
+}
+
+// One operand tile (128 rows × 16 k) into LDS as S[k][row]. KC: element (r, k) at
+// p[r·ld + k] (4 lanes per row, 16-byte loads along k, transposed on the LDS store);
+// otherwise at p[k·ld + r] (32 lanes per k row, 16-byte loads and stores). Out-of-range
+// rows / k read as 0. Two 16-byte vectors per thread.
+template <bool KC>
+__device__ __forceinline__ void tile_load(const float* __restrict__ p, long long ld, int r0,
+                                          int R, int k0, int K, floatx4 (&v)[2]) {
+  const int tid = threadIdx.x;
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const int c = tid + 256 * i;
+    const floatx4 zero = {0.f, 0.f, 0.f, 0.f};
+    if constexpr (KC) {
+      const int row = c >> 2, kc = (c & 3) * 4;
+      const bool ok = r0 + row < R && k0 + kc < K;
+      v[i] = ok ? *reinterpret_cast<const floatx4*>(p + static_cast<long long>(r0 + row) * ld + k0 + kc)
+                : zero;
+    } else {
+      const int kr = c >> 5, rc = (c & 31) * 4;
+      const bool ok = k0 + kr < K && r0 + rc < R;
+      v[i] = ok ? *reinterpret_cast<const floatx4*>(p + static_cast<long long>(k0 + kr) * ld + r0 + rc)
+                : zero;
+    }
+  }
+}
+
+template <bool KC>
+__device__ __forceinline__ void tile_store(float (*S)[kGM + kGPad], const floatx4 (&v)[2]) {
+  const int tid = threadIdx.x;
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const int c = tid + 256 * i;
+    if constexpr (KC) {
+      const int row = c >> 2, kc = (c & 3) * 4;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) S[kc + j][row] = v[i][j];
+    } else {
+      const int kr = c >> 5, rc = (c & 31) * 4;
+      *reinterpret_cast<floatx4*>(&S[kr][rc]) = v[i];
+    }
+  }
+}
+
+template <bool A_KC, bool B_KC, int OUT>
+__global__ __launch_bounds__(256) void gemm_bwd_kernel(GemmBwdArgs g) {
+  __shared__ __attribute__((aligned(16))) float As[kGK][kGM + kGPad];
+  __shared__ __attribute__((aligned(16))) float Bs[kGK][kGM + kGPad];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int wm = wave >> 1, wn = wave & 1;
+  const int m0 = blockIdx.y * kGM, n0 = blockIdx.x * kGM;
+  const int M = g.M, N = g.N, K = g.K;
+
+  floatx16 acc[2][2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
+
+  floatx4 ra[2], rb[2];
+  tile_load<A_KC>(g.a, g.lda, m0, M, 0, K, ra);
+  tile_load<B_KC>(g.b, g.ldb, n0, N, 0, K, rb);
+  tile_store<A_KC>(As, ra);
+  tile_store<B_KC>(Bs, rb);
+  __syncthreads();
+  for (int k0 = 0; k0 < K; k0 += kGK) {
+    const bool more = k0 + kGK < K;
+    if (more) {  // next tile's loads in flight while this one multiplies
+      tile_load<A_KC>(g.a, g.lda, m0, M, k0 + kGK, K, ra);
+      tile_load<B_KC>(g.b, g.ldb, n0, N, k0 + kGK, K, rb);
+    }
+#pragma unroll
+    for (int kk = 0; kk < kGK; kk += 2) {
+      float fa[2], fb[2];
+#pragma unroll
+      for (int i = 0; i < 2; ++i) fa[i] = As[kk + (lane >> 5)][wm * 64 + i * 32 + (lane & 31)];
+#pragma unroll
+      for (int j = 0; j < 2; ++j) fb[j] = Bs[kk + (lane >> 5)][wn * 64 + j * 32 + (lane & 31)];
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(fa[i], fb[j], acc[i][j], 0, 0, 0);
+    }
+    __syncthreads();
+    if (more) {
+      tile_store<A_KC>(As, ra);
+      tile_store<B_KC>(Bs, rb);
+    }
+    __syncthreads();
+  }
+
+  // D layout of a 32×32 MFMA tile: lane l, register r → row 8(r/4) + 4(l/32) + r%4, col l%32.
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int m = m0 + wm * 64 + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+        const int n = n0 + wn * 64 + j * 32 + (lane & 31);
+        if (m < M && n < N) {
+          float* c = g.c + static_cast<long long>(m) * g.ldc + n;
+          const float v = acc[i][j][r];
+          if constexpr (OUT == GB_SET) *c = v;
+          else if constexpr (OUT == GB_ADD) *c += v;
+          else *c = v * gelu_grad(g.aux[static_cast<long long>(m) * g.ldaux + n]);
+        }
+      }
+}
+
+template <bool A_KC, bool B_KC>
+int gemm_bwd_out(const GemmBwdArgs& g, int out, hipStream_t st) {
+  const dim3 grid((g.N + kGM - 1) / kGM, (g.M + kGM - 1) / kGM);
+  switch (out) {
+    case GB_SET: gemm_bwd_kernel<A_KC, B_KC, GB_SET><<<grid, 256, 0, st>>>(g); break;
+    case GB_ADD: gemm_bwd_kernel<A_KC, B_KC, GB_ADD><<<grid, 256, 0, st>>>(g); break;
+    case GB_GELU: gemm_bwd_kernel<A_KC, B_KC, GB_GELU><<<grid, 256, 0, st>>>(g); break;
+    default: set_error("gemm_bwd: unknown output mode %d", out); return -1;
+  }
+  NML_LAUNCHED();
+  return 0;
+}
+
+// ------------------------------------------------------------- RMSNorm backward
+constexpr int kNormRowsPerBlock = 16;
+
+// One block per 16 rows, each thread NC columns c = tid + 256·j. Per row (fp32, the
+// order of kernels/fused_rmsnorm.py:208-217): ms = Σx²/d, rms = √(ms + ε),
+// gxh = dy·γ, dot = Σ gxh·x, coef = (2/d)·(−½·dot·(ms + ε)^(−3/2)),
+// dx = gxh/rms + x·coef; the block's Σ dy·(x/rms) per column goes to part[block].
+template <int NC>
+__global__ __launch_bounds__(256) void rmsnorm_bwd_kernel(const float* __restrict__ dy,
+                                                          const float* __restrict__ x,
+                                                          const float* __restrict__ gam,
+                                                          float* __restrict__ dx, int acc,
+                                                          float* __restrict__ part, int rows,
+                                                          int d, float eps) {
+#pragma clang fp contract(off)
+  __shared__ float red[2][4];
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  float gv[NC], gacc[NC];
+#pragma unroll
+  for (int j = 0; j < NC; ++j) {
+    const int c = tid + 256 * j;
+    gv[j] = c < d ? gam[c] : 0.f;
+    gacc[j] = 0.f;
+  }
+  const int r0 = blockIdx.x * kNormRowsPerBlock;
+  const int r1 = min(rows, r0 + kNormRowsPerBlock);
+  for (int r = r0; r < r1; ++r) {
+    const float* xr = x + static_cast<long long>(r) * d;
+    const float* gr = dy + static_cast<long long>(r) * d;
+    float xv[NC], dv[NC], ssq = 0.f, dot = 0.f;
+#pragma unroll
+    for (int j = 0; j < NC; ++j) {
+      const int c = tid + 256 * j;
+      xv[j] = c < d ? xr[c] : 0.f;
+      dv[j] = c < d ? gr[c] : 0.f;
+      ssq += xv[j] * xv[j];
+      dot += (dv[j] * gv[j]) * xv[j];
+    }
+    ssq = wave_sum(ssq);
+    dot = wave_sum(dot);
+    if (lane == 0) {
+      red[0][w] = ssq;
+      red[1][w] = dot;
+    }
+    __syncthreads();
+    const float ms = ((red[0][0] + red[0][1]) + (red[0][2] + red[0][3])) / static_cast<float>(d);
+    const float rdot = (red[1][0] + red[1][1]) + (red[1][2] + red[1][3]);
+    __syncthreads();  // red is rewritten by the next row
+    const float rms = sqrtf(ms + eps);
+    const float grad_ms = rdot * -0.5f / ((ms + eps) * rms);
+    const float coef = (2.0f / static_cast<float>(d)) * grad_ms;
+    float* o = dx + static_cast<long long>(r) * d;
+#pragma unroll
+    for (int j = 0; j < NC; ++j) {
+      const int c = tid + 256 * j;
+      if (c < d) {
+        const float v = (dv[j] * gv[j]) / rms + xv[j] * coef;
+        o[c] = acc ? o[c] + v : v;
+        gacc[j] += dv[j] * (xv[j] / rms);
+      }
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < NC; ++j) {
+    const int c = tid + 256 * j;
+    if (c < d) part[static_cast<long long>(blockIdx.x) * d + c] = gacc[j];
+  }
+}
+
+// out[c] += Σ_p part[p·n + c], p in order.
+__global__ __launch_bounds__(256) void parts_reduce_kernel(const float* __restrict__ part,
+                                                           int nparts, int n,
+                                                           float* __restrict__ out) {
+  const int c = blockIdx.x * 256 + threadIdx.x;
+  if (c >= n) return;
+  float s = 0.f;
+  for (int p = 0; p < nparts; ++p) s += part[static_cast<long long>(p) * n + c];
+  out[c] += s;
+}
+
+// ---------------------------------------------------------------- column sums
+constexpr int kColRows = 64;
+
+__global__ __launch_bounds__(256) void colsum_part_kernel(const float* __restrict__ a,
+                                                          long long lda, int rows, int n,
+                                                          float* __restrict__ part) {
+  const int c = blockIdx.x * 256 + threadIdx.x;
+  if (c >= n) return;
+  const int r0 = blockIdx.y * kColRows, r1 = min(rows, r0 + kColRows);
+  float s = 0.f;
+  for (int r = r0; r < r1; ++r) s += a[static_cast<long long>(r) * lda + c];
+  part[static_cast<long long>(blockIdx.y) * n + c] = s;
+}
+
+// -------------------------------------------------------- cross-entropy backward
+// One block per row: probs = exp(l − max)·(1/Σexp), probs[label] −= 1, × scale.
+__global__ __launch_bounds__(256) void ce_grad_kernel(float* __restrict__ lg, int V,
+                                                      const int64_t* __restrict__ labels,
+                                                      long long ignore_index, int has_ignore,
+                                                      float scale) {
+  __shared__ float red[4];
+  float* p = lg + static_cast<long long>(blockIdx.x) * V;
+  const long long label = labels[blockIdx.x];
+  if (has_ignore && label == ignore_index) {
+    for (int i = threadIdx.x; i < V; i += 256) p[i] = 0.f;
+    return;
+  }
+  float mx = -INFINITY;
+  for (int i = threadIdx.x; i < V; i += 256) mx = fmaxf(mx, p[i]);
+  mx = wave_max(mx);
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = mx;
+  __syncthreads();
+  mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+  float se = 0.f;
+  for (int i = threadIdx.x; i < V; i += 256) se += expf(p[i] - mx);
+  se = block_sum(se, red);
+  const float inv = 1.0f / se;
+  for (int i = threadIdx.x; i < V; i += 256) {
+    float v = expf(p[i] - mx) * inv;
+    if (i == label) v -= 1.0f;
+    p[i] = v * scale;
+  }
+}
+
+// ------------------------------------------------------------ attention backward
+// dvec[(b·H + h)·S + s] = Σ_c dout·o over the head's columns (= Σ_j P·dP of the
+// softmax backward, kernels/fused_sdpa.py:26-29).
+__global__ __launch_bounds__(256) void attn_bwd_dot_kernel(AttnBwdArgs a) {
+  const int t = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
+  const int R = a.B * a.S;
+  if (t >= R * a.H) return;
+  const int r = t / a.H, h = t - (t / a.H) * a.H;
+  const int b = r / a.S, s = r - (r / a.S) * a.S;
+  const long long off = static_cast<long long>(r) * a.H * a.dk + h * a.dk;
+  float v = 0.f;
+  for (int c = lane; c < a.dk; c += 64) v += a.dout[off + c] * a.o[off + c];
+  v = wave_sum(v);
+  if (lane == 0) a.dvec[(static_cast<long long>(b) * a.H + h) * a.S + s] = v;
+}
+
+// Shared per-tile step: thread t scores EPT (query i, key j) pairs of a BT × BT tile,
+// i = t / TPR, j = (t % TPR)·EPT + e: p = exp(q·k/scale − lse_i) where key ≤ query (both
+// inside the sequence), else 0; ds = p·(dO_i·v_j − D_i)/scale.
+template <int DK, int BT>
+struct AttnTile {
+  static constexpr int EPT = BT * BT / 256;
+  static constexpr int TPR = BT / EPT;
+  float Qs[BT][DK + 1];
+  float dOs[BT][DK + 1];
+  float Ks[BT][DK + 1];
+  float Vs[BT][DK + 1];
+  float Ps[BT][BT + 1];
+  float dSs[BT][BT + 1];
+  float lse[BT];
+  float D[BT];
+
+  __device__ void scores(int q_lo, int k_lo, int S, float scale) {
+    const int t = threadIdx.x;
+    const int i = t / TPR, j0 = (t % TPR) * EPT;
+    const int qi = q_lo + i;
+#pragma unroll
+    for (int e = 0; e < EPT; ++e) {
+      const int j = j0 + e, kj = k_lo + j;
+      float p = 0.f, ds = 0.f;
+      if (kj <= qi && qi < S) {
+        float dot = 0.f, dp = 0.f;
+#pragma unroll 8
+        for (int c = 0; c < DK; ++c) {
+          dot += Qs[i][c] * Ks[j][c];
+          dp += dOs[i][c] * Vs[j][c];
+        }
+        p = expf(dot / scale - lse[i]);
+        ds = p * (dp - D[i]) / scale;
+      }
+      Ps[i][j] = p;
+      dSs[i][j] = ds;
+    }
+  }
+};
+
+// rows [lo, lo + BT) of a head-major (B·H, S, DK) tensor into dst (0 past S)
+template <int DK, int BT>
+__device__ __forceinline__ void load_rows(float (*dst)[DK + 1], const float* __restrict__ src,
+                                          int lo, int S) {
+  for (int e = threadIdx.x; e < BT * DK; e += 256) {
+    const int r = e / DK, c = e - (e / DK) * DK;
+    dst[r][c] = lo + r < S ? src[static_cast<long long>(lo + r) * DK + c] : 0.f;
+  }
+}
+
+// rows [lo, lo + BT) of head h of a merged (B·S, H·DK) tensor
+template <int DK, int BT>
+__device__ __forceinline__ void load_merged(float (*dst)[DK + 1], const float* __restrict__ src,
+                                            int b, int h, int H, int lo, int S) {
+  for (int e = threadIdx.x; e < BT * DK; e += 256) {
+    const int r = e / DK, c = e - (e / DK) * DK;
+    dst[r][c] = lo + r < S ? src[(static_cast<long long>(b) * S + lo + r) * H * DK + h * DK + c]
+                           : 0.f;
+  }
+}
+
+// dK, dV of BT keys: walk the query tiles from the key tile on (causal).
+template <int DK, int BT>
+__global__ __launch_bounds__(256) void attn_bwd_dkdv_kernel(AttnBwdArgs a) {
+  __shared__ AttnTile<DK, BT> sh;
+  constexpr int TPK = 256 / BT;       // threads per key row of the output
+  constexpr int NCOL = (DK + TPK - 1) / TPK;
+  const int bh = blockIdx.y, b = bh / a.H, h = bh - (bh / a.H) * a.H;
+  const int S = a.S, k_lo = blockIdx.x * BT;
+  const long long hoff = static_cast<long long>(bh) * S * DK;
+  load_rows<DK, BT>(sh.Ks, a.k + hoff, k_lo, S);
+  load_rows<DK, BT>(sh.Vs, a.v + hoff, k_lo, S);
+  const int jo = threadIdx.x / TPK, co = threadIdx.x % TPK;
+  float dk[NCOL], dv[NCOL];
+#pragma unroll
+  for (int u = 0; u < NCOL; ++u) dk[u] = dv[u] = 0.f;
+  for (int q_lo = k_lo; q_lo < S; q_lo += BT) {
+    __syncthreads();  // the previous tile's readers are done
+    load_rows<DK, BT>(sh.Qs, a.q + hoff, q_lo, S);
+    load_merged<DK, BT>(sh.dOs, a.dout, b, h, a.H, q_lo, S);
+    for (int i = threadIdx.x; i < BT; i += 256) {
+      const bool ok = q_lo + i < S;
+      sh.lse[i] = ok ? a.lse[static_cast<long long>(bh) * S + q_lo + i] : 0.f;
+      sh.D[i] = ok ? a.dvec[static_cast<long long>(bh) * S + q_lo + i] : 0.f;
+    }
+    __syncthreads();
+    sh.scores(q_lo, k_lo, S, a.scale);
+    __syncthreads();
+#pragma unroll
+    for (int u = 0; u < NCOL; ++u) {
+      const int c = co + TPK * u;
+      if (c < DK) {
+        float sv = 0.f, sk = 0.f;
+#pragma unroll 8
+        for (int i = 0; i < BT; ++i) {
+          sv += sh.Ps[i][jo] * sh.dOs[i][c];
+          sk += sh.dSs[i][jo] * sh.Qs[i][c];
+        }
+        dv[u] += sv;
+        dk[u] += sk;
+      }
+    }
+  }
+  const int key = k_lo + jo;
+  if (key < S) {
+    const int d = a.H * DK;
+    float* row = a.dqkv + (static_cast<long long>(b) * S + key) * 3 * d + h * DK;
+#pragma unroll
+    for (int u = 0; u < NCOL; ++u) {
+      const int c = co + TPK * u;
+      if (c < DK) {
+        row[d + c] = dk[u];
+        row[2 * d + c] = dv[u];
+      }
+    }
+  }
+}
+
+// dQ of BT queries: walk the key tiles up to the query tile (causal).
+template <int DK, int BT>
+__global__ __launch_bounds__(256) void attn_bwd_dq_kernel(AttnBwdArgs a) {
+  __shared__ AttnTile<DK, BT> sh;
+  constexpr int TPK = 256 / BT;
+  constexpr int NCOL = (DK + TPK - 1) / TPK;
+  const int bh = blockIdx.y, b = bh / a.H, h = bh - (bh / a.H) * a.H;
+  const int S = a.S, q_lo = blockIdx.x * BT;
+  const long long hoff = static_cast<long long>(bh) * S * DK;
+  load_rows<DK, BT>(sh.Qs, a.q + hoff, q_lo, S);
+  load_merged<DK, BT>(sh.dOs, a.dout, b, h, a.H, q_lo, S);
+  for (int i = threadIdx.x; i < BT; i += 256) {
+    const bool ok = q_lo + i < S;
+    sh.lse[i] = ok ? a.lse[static_cast<long long>(bh) * S + q_lo + i] : 0.f;
+    sh.D[i] = ok ? a.dvec[static_cast<long long>(bh) * S + q_lo + i] : 0.f;
+  }
+  const int io = threadIdx.x / TPK, co = threadIdx.x % TPK;
+  float dq[NCOL];
+#pragma unroll
+  for (int u = 0; u < NCOL; ++u) dq[u] = 0.f;
+  const int k_end = min(S, q_lo + BT);
+  for (int k_lo = 0; k_lo < k_end; k_lo += BT) {
+    __syncthreads();
+    load_rows<DK, BT>(sh.Ks, a.k + hoff, k_lo, S);
+    load_rows<DK, BT>(sh.Vs, a.v + hoff, k_lo, S);
+    __syncthreads();
+    sh.scores(q_lo, k_lo, S, a.scale);
+    __syncthreads();
+#pragma unroll
+    for (int u = 0; u < NCOL; ++u) {
+      const int c = co + TPK * u;
+      if (c < DK) {
+        float s = 0.f;
+#pragma unroll 8
+        for (int j = 0; j < BT; ++j) s += sh.dSs[io][j] * sh.Ks[j][c];
+        dq[u] += s;
+      }
+    }
+  }
+  const int q = q_lo + io;
+  if (q < S) {
+    const int d = a.H * DK;
+    float* row = a.dqkv + (static_cast<long long>(b) * S + q) * 3 * d + h * DK;
+#pragma unroll
+    for (int u = 0; u < NCOL; ++u) {
+      const int c = co + TPK * u;
+      if (c < DK) row[c] = dq[u];
+    }
+  }
+}
+
+template <int DK>
+int attn_bwd_dk(const AttnBwdArgs& a, hipStream_t st) {
+  constexpr int BT = DK >= 128 ? 16 : 32;
+  const dim3 grid((a.S + BT - 1) / BT, a.B * a.H);
+  attn_bwd_dkdv_kernel<DK, BT><<<grid, 256, 0, st>>>(a);
+  NML_LAUNCHED();
+  attn_bwd_dq_kernel<DK, BT><<<grid, 256, 0, st>>>(a);
+  NML_LAUNCHED();
+  return 0;
+}
+
+// --------------------------------------------------------------- RoPE backward
+__global__ __launch_bounds__(256) void rope_bwd_kernel(float* __restrict__ dqkv, int rows, int S,
+                                                       int H, int dk, const float* __restrict__ cs,
+                                                       const float* __restrict__ sn) {
+#pragma clang fp contract(off)
+  const int half = dk / 2;
+  const long long n = static_cast<long long>(rows) * 2 * H * half;
+  const long long t = static_cast<long long>(blockIdx.x) * 256 + threadIdx.x;
+  if (t >= n) return;
+  const int i = static_cast<int>(t % half);
+  const long long u = t / half;
+  const int h = static_cast<int>(u % H);
+  const int which = static_cast<int>((u / H) % 2);
+  const int r = static_cast<int>(u / (2 * H));
+  const int s = r % S;
+  const int d = H * dk;
+  float* p = dqkv + static_cast<long long>(r) * 3 * d + which * d + h * dk;
+  const float c = cs[static_cast<long long>(s) * half + i], si = sn[static_cast<long long>(s) * half + i];
+  const float x1 = p[i], x2 = p[i + half];
+  p[i] = x1 * c + x2 * si;
+  p[i + half] = x2 * c - x1 * si;
+}
+
+// ---------------------------------------------------------- embedding backward
+__global__ __launch_bounds__(256) void embed_bwd_tok_kernel(const float* __restrict__ g,
+                                                            const int64_t* __restrict__ ids,
+                                                            float* __restrict__ demb, int d, int V) {
+  const int r = blockIdx.x;
+  const long long id = ids[r];
+  if (id < 0 || id >= V) return;
+  for (int c = threadIdx.x; c < d; c += 256)
+    atomicAdd(demb + id * d + c, g[static_cast<long long>(r) * d + c]);
+}
+
+__global__ __launch_bounds__(256) void embed_bwd_pos_kernel(const float* __restrict__ g,
+                                                            float* __restrict__ dpos, int B, int S,
+                                                            int d) {
+  const int s = blockIdx.y, c = blockIdx.x * 256 + threadIdx.x;
+  if (c >= d) return;
+  float v = 0.f;
+  for (int b = 0; b < B; ++b) v += g[(static_cast<long long>(b) * S + s) * d + c];
+  dpos[static_cast<long long>(s) * d + c] += v;
+}
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
+
+}  // namespace
+
+int launch_gemm_bwd(const GemmBwdArgs& g, bool a_kc, bool b_kc, int out, hipStream_t st) {
+  if (g.M == 0 || g.N == 0) return 0;
+  NML_REQUIRE(g.K > 0, "gemm_bwd: K must be positive");
+  NML_REQUIRE(aligned16(g.a) && aligned16(g.b) && g.lda % 4 == 0 && g.ldb % 4 == 0,
+              "gemm_bwd: operands must be 16-byte aligned with strides a multiple of 4");
+  NML_REQUIRE(a_kc ? g.K % 4 == 0 : g.M % 4 == 0, "gemm_bwd: A's contiguous extent must be a multiple of 4");
+  NML_REQUIRE(b_kc ? g.K % 4 == 0 : g.N % 4 == 0, "gemm_bwd: B's contiguous extent must be a multiple of 4");
+  NML_REQUIRE(out != GB_GELU || g.aux != nullptr, "gemm_bwd: the GELU backward needs the pre-activation");
+  if (a_kc) return b_kc ? gemm_bwd_out<true, true>(g, out, st) : gemm_bwd_out<true, false>(g, out, st);
+  return b_kc ? gemm_bwd_out<false, true>(g, out, st) : gemm_bwd_out<false, false>(g, out, st);
+}
+
+int rmsnorm_bwd_parts(int rows) { return (rows + kNormRowsPerBlock - 1) / kNormRowsPerBlock; }
+
+int launch_rmsnorm_bwd(const float* dy, const float* x, const float* gamma, float* dx, int acc,
+                       float* dgamma, float* part, int rows, int d, float eps, hipStream_t st) {
+  if (rows == 0) return 0;
+  NML_REQUIRE(d > 0 && d <= 256 * 32, "rmsnorm backward: d=%d outside (0, 8192]", d);
+  const int blocks = rmsnorm_bwd_parts(rows);
+  const int nc = (d + 255) / 256;
+#define NML_NORM_BWD(NCV) \
+  rmsnorm_bwd_kernel<NCV><<<blocks, 256, 0, st>>>(dy, x, gamma, dx, acc, part, rows, d, eps)
+  if (nc <= 1) NML_NORM_BWD(1);
+  else if (nc <= 2) NML_NORM_BWD(2);
+  else if (nc <= 4) NML_NORM_BWD(4);
+  else if (nc <= 8) NML_NORM_BWD(8);
+  else if (nc <= 16) NML_NORM_BWD(16);
+  else NML_NORM_BWD(32);
+#undef NML_NORM_BWD
+  NML_LAUNCHED();
+  parts_reduce_kernel<<<(d + 255) / 256, 256, 0, st>>>(part, blocks, d, dgamma);
+  NML_LAUNCHED();
+  return 0;
+}
+
+int colsum_parts(int rows) { return (rows + kColRows - 1) / kColRows; }
+
+int launch_colsum(const float* a, long long lda, int rows, int n, float* out, float* part,
+                  hipStream_t st) {
+  if (rows == 0 || n == 0) return 0;
+  const int parts = colsum_parts(rows);
+  colsum_part_kernel<<<dim3((n + 255) / 256, parts), 256, 0, st>>>(a, lda, rows, n, part);
+  NML_LAUNCHED();
+  parts_reduce_kernel<<<(n + 255) / 256, 256, 0, st>>>(part, parts, n, out);
+  NML_LAUNCHED();
+  return 0;
+}
+
+int launch_ce_grad(float* logits, int rows, int V, const int64_t* labels, long long ignore_index,
+                   int has_ignore, float scale, hipStream_t st) {
+  if (rows == 0) return 0;
+  ce_grad_kernel<<<rows, 256, 0, st>>>(logits, V, labels, ignore_index, has_ignore, scale);
+  NML_LAUNCHED();
+  return 0;
+}
+
+int launch_attention_backward(const AttnBwdArgs& a, hipStream_t st) {
+  if (a.B * a.S == 0) return 0;
+  const long long pairs = static_cast<long long>(a.B) * a.S * a.H;
+  attn_bwd_dot_kernel<<<static_cast<int>((pairs + 3) / 4), 256, 0, st>>>(a);
+  NML_LAUNCHED();
+  switch (a.dk) {
+    case 8: return attn_bwd_dk<8>(a, st);
+    case 16: return attn_bwd_dk<16>(a, st);
+    case 32: return attn_bwd_dk<32>(a, st);
+    case 64: return attn_bwd_dk<64>(a, st);
+    case 128: return attn_bwd_dk<128>(a, st);
+  }
+  set_error("attention backward: head_dim %d unsupported (8, 16, 32, 64, 128)", a.dk);
+  return -1;
+}
+
+int launch_rope_backward(float* dqkv, int rows, int S, int H, int dk, const float* cos,
+                         const float* sin, hipStream_t st) {
+  const long long n = static_cast<long long>(rows) * 2 * H * (dk / 2);
+  if (n == 0) return 0;
+  rope_bwd_kernel<<<static_cast<int>((n + 255) / 256), 256, 0, st>>>(dqkv, rows, S, H, dk, cos, sin);
+  NML_LAUNCHED();
+  return 0;
+}
+
+int launch_embed_backward(const float* g, const int64_t* ids, float* demb, float* dpos, int B,
+                          int S, int d, int V, hipStream_t st) {
+  if (B * S == 0) return 0;
+  embed_bwd_tok_kernel<<<B * S, 256, 0, st>>>(g, ids, demb, d, V);
+  NML_LAUNCHED();
+  if (dpos) {
+    embed_bwd_pos_kernel<<<dim3((d + 255) / 256, S), 256, 0, st>>>(g, dpos, B, S, d);
+    NML_LAUNCHED();
+  }
+  return 0;
+}
+
+}  // namespace nml

@@ -1,0 +1,371 @@
+// Training on the device (float32 models): compute_loss keeping what the backward needs,
+// then loss.backward() into a gradient arena laid out like the parameter arena
+// (models/gpt.py:123-137 with the reference's autograd: losses/cross_entropy.py:109-192,
+// kernels/fused_tied_crossentropy.py:27-48, neural_network/_fused_arrays.py:129-377,
+// kernels/fused_rmsnorm.py:208-217, kernels/embedding_scatter.py:39-60).
+//
+// Saved per layer l over R = B·S rows: the block input X[l], N1 = RMSNorm₁(X[l]), q/k/v
+// head-major (after RoPE), the merged attention output, the softmax log-sum-exp, the
+// mid-block residual XM, N2 = RMSNorm₂(XM), the FFN pre-activation and GELU output; then
+// X[L] and the final-normed H. The logits are not kept: the backward forms them again
+// chunk by chunk (one more head GEMM instead of R·V floats).
+//
+// Backward, with G the gradient of the residual stream (R, d):
+//   head:  dlogits = (softmax − onehot)·scale/n;  dH = dlogits·E;  dE += dlogitsᵀ·H
+//   final: G = RMSNormᵀ(dH)
+//   block: dW₂ += Gᵀ·hid, db₂ += Σ G, dpre = (G·W₂)∘gelu'(pre), dW₁ += dpreᵀ·N2,
+//          db₁ += Σ dpre, G += RMSNorm₂ᵀ(dpre·W₁);
+//          dW_o += Gᵀ·att, db_o += Σ G, datt = G·W_o → attention backward → dqkv
+//          (RoPE inverse on dq, dk), dW_qkv += dqkvᵀ·N1, db_qkv += Σ dqkv,
+//          G += RMSNorm₁ᵀ(dqkv·W_qkv)
+//   embeddings: dE[ids] += G, dpos[s] += Σ_b G
+// Weight gradients are (out, in) like the device weights.
+#include <cstring>
+
+#include "model.hpp"
+
+namespace nml {
+
+struct TrainState {
+  Buf grads;    // float32, same layout and size as the parameter arena
+  Buf acts;     // saved activations of the last loss_train
+  Buf scratch;  // backward scratch
+  Buf io;       // ids and labels of the last loss_train, loss accumulators
+  int B = 0, S = 0;
+  bool saved = false;
+  long long ignore_index = 0;
+  int has_ignore = 0;
+  double n_valid = 0.0;
+};
+
+void train_release(nml_model* m) {
+  if (!m->train) return;
+  m->train->grads.release();
+  m->train->acts.release();
+  m->train->scratch.release();
+  m->train->io.release();
+  delete m->train;
+  m->train = nullptr;
+}
+
+namespace {
+
+// Saved activations of R rows, carved from one buffer.
+struct Saved {
+  float *x, *n1, *q, *k, *v, *att, *lse, *xm, *n2, *pre, *hid;  // layer 0; + l·stride
+  size_t stride;                                                  // floats per layer
+  float* xl;  // X[L]
+  float* hf;  // final-normed
+};
+
+size_t saved_floats(const nml_model* m, int B, int S, Saved* s, float* base) {
+  const size_t R = (size_t)B * S, rd = align256(R * m->d * 4) / 4, rf = align256(R * m->F * 4) / 4;
+  const size_t rl = align256((size_t)B * m->H * S * 4) / 4;
+  const size_t per = 8 * rd + 2 * rf + rl;
+  if (s) {
+    float* p = base;
+    s->x = p; p += rd;
+    s->n1 = p; p += rd;
+    s->q = p; p += rd;
+    s->k = p; p += rd;
+    s->v = p; p += rd;
+    s->att = p; p += rd;
+    s->xm = p; p += rd;
+    s->n2 = p; p += rd;
+    s->pre = p; p += rf;
+    s->hid = p; p += rf;
+    s->lse = p;
+    s->stride = per;
+    s->xl = base + per * m->L;
+    s->hf = s->xl + rd;
+  }
+  return per * m->L + 2 * rd;
+}
+
+inline float* at(float* p, const Saved& s, int l) { return p + s.stride * l; }
+
+// Gradient of parameter (kind, layer): same offset in the gradient arena.
+float* grad_of(nml_model* m, void* param) {
+  return reinterpret_cast<float*>(static_cast<char*>(m->train->grads.p) +
+                                  (static_cast<char*>(param) - static_cast<char*>(m->arena)));
+}
+
+int ensure_train(nml_model* m) {
+  NML_REQUIRE(m->dt == F32, "training on the device needs a float32 model");
+  if (!m->train) m->train = new TrainState();
+  TrainState* t = m->train;
+  if (!t->grads.p) {
+    NML_TRY(t->grads.ensure(m->arena_bytes));
+    NML_HIP(hipMemsetAsync(t->grads.p, 0, m->arena_bytes, nml::stream()));
+  }
+  return 0;
+}
+
+// Rows per logits chunk: at most 512 MiB of float32 logits at once.
+size_t logits_chunk(const nml_model* m, size_t R) {
+  size_t chunk = R;
+  while (chunk > 1 && chunk * m->V * 4 > ((size_t)512 << 20)) chunk = (chunk + 1) / 2;
+  return chunk;
+}
+
+LinearArgs lin(const void* x, long long lda, const void* w, const void* bias, void* out, int M,
+               int N, int K, int epi, const void* resid = nullptr) {
+  LinearArgs a{};
+  a.x = x;
+  a.lda = lda;
+  a.w = w;
+  a.bias = bias;
+  a.out = out;
+  a.resid = resid;
+  a.M = M;
+  a.N = N;
+  a.K = K;
+  a.epi = epi;
+  return a;
+}
+
+GemmBwdArgs gb(const float* a, long long lda, const float* b, long long ldb, float* c,
+               long long ldc, int M, int N, int K, const float* aux = nullptr,
+               long long ldaux = 0) {
+  GemmBwdArgs g{};
+  g.a = a;
+  g.lda = lda;
+  g.b = b;
+  g.ldb = ldb;
+  g.c = c;
+  g.ldc = ldc;
+  g.aux = aux;
+  g.ldaux = ldaux;
+  g.M = M;
+  g.N = N;
+  g.K = K;
+  return g;
+}
+
+}  // namespace
+
+}  // namespace nml
+
+using namespace nml;
+
+extern "C" {
+
+int nml_model_zero_grad(nml_model* m) {
+  NML_TRY(check_ready(m));
+  NML_TRY(ensure_train(m));
+  NML_HIP(hipMemsetAsync(m->train->grads.p, 0, m->arena_bytes, nml::stream()));
+  NML_HIP(hipStreamSynchronize(nml::stream()));
+  return 0;
+}
+
+int nml_model_grad_ptr(nml_model* m, int kind, int layer, void** ptr) {
+  NML_TRY(check_ready(m));
+  NML_REQUIRE(kind != NML_P_ROPE_COS && kind != NML_P_ROPE_SIN,
+              "rotary tables are buffers, not parameters: no gradient");
+  void** slot = param_slot(m, kind, layer);
+  NML_REQUIRE(slot != nullptr, "unknown parameter kind %d / layer %d", kind, layer);
+  NML_TRY(ensure_train(m));
+  *ptr = grad_of(m, *slot);
+  return 0;
+}
+
+int nml_model_loss_train(nml_model* m, const int64_t* ids, const int64_t* labels, size_t batch,
+                         size_t seq, int64_t ignore_index, int has_ignore, double* loss) {
+  NML_TRY(check_ready(m));
+  NML_REQUIRE(seq <= (size_t)m->P, "Sequence length %zu exceeds maximum sequence length %d", seq,
+              m->P);
+  NML_TRY(ensure_train(m));
+  TrainState* t = m->train;
+  t->saved = false;
+  const int B = (int)batch, S = (int)seq, R = B * S, d = m->d, F = m->F;
+  if (R == 0) {
+    *loss = 0.0;
+    return 0;
+  }
+  hipStream_t st = nml::stream();
+  Saved sv;
+  NML_TRY(t->acts.ensure(saved_floats(m, B, S, nullptr, nullptr) * 4));
+  saved_floats(m, B, S, &sv, static_cast<float*>(t->acts.p));
+  // io: ids, labels, then err / loss accumulators, per-row loss and validity
+  const size_t ib = align256((size_t)R * 8), rb = align256((size_t)R * 4);
+  NML_TRY(t->io.ensure(2 * ib + 512 + 2 * rb));
+  char* io = static_cast<char*>(t->io.p);
+  int64_t* dids = reinterpret_cast<int64_t*>(io);
+  int64_t* dlab = reinterpret_cast<int64_t*>(io + ib);
+  int* err = reinterpret_cast<int*>(io + 2 * ib);
+  double* acc = reinterpret_cast<double*>(io + 2 * ib + 256);
+  float* row_loss = reinterpret_cast<float*>(io + 2 * ib + 512);
+  int* row_valid = reinterpret_cast<int*>(io + 2 * ib + 512 + rb);
+  NML_HIP(hipMemcpyAsync(dids, ids, (size_t)R * 8, hipMemcpyDeviceToDevice, st));
+  NML_HIP(hipMemcpyAsync(dlab, labels, (size_t)R * 8, hipMemcpyDeviceToDevice, st));
+  NML_HIP(hipMemsetAsync(err, 0, sizeof(int), st));
+
+  NML_TRY(launch_embed(F32, dids, m->emb, posw(m), nullptr, sv.x, B, S, d, m->V, m->P, err, st));
+  const long long sb = (long long)m->H * S * m->dk, sh = (long long)S * m->dk;
+  for (int l = 0; l < m->L; ++l) {
+    const Layer& w = m->layers[l];
+    float *x = at(sv.x, sv, l), *n1 = at(sv.n1, sv, l), *q = at(sv.q, sv, l),
+          *k = at(sv.k, sv, l), *v = at(sv.v, sv, l), *att = at(sv.att, sv, l),
+          *lse = at(sv.lse, sv, l), *xm = at(sv.xm, sv, l), *n2 = at(sv.n2, sv, l),
+          *pre = at(sv.pre, sv, l), *hid = at(sv.hid, sv, l);
+    float* xnext = l + 1 < m->L ? at(sv.x, sv, l + 1) : sv.xl;
+    NML_TRY(launch_rmsnorm(F32, x, w.ln1, n1, nullptr, nullptr, R, d, kEps, st));
+    LinearArgs qkv = lin(n1, d, w.wqkv, w.bqkv, nullptr, R, 3 * d, d, EPI_QKV);
+    qkv.qkv = QKVDst{q, k, v, nullptr, sb, sh, S, m->H, m->dk, d, nullptr};
+    NML_TRY(launch_linear(F32, qkv, st));
+    if (rope_on(m))
+      NML_TRY(launch_rope(F32, q, k, sb, sh, B, m->H, S, m->dk, nullptr, nullptr, m->rope_cos,
+                          m->rope_sin, m->P, st));
+    AttnArgs a{};
+    a.q = q;
+    a.k = k;
+    a.v = v;
+    a.out = att;
+    a.kv_stride_b = sb;
+    a.kv_stride_h = sh;
+    a.B = B;
+    a.H = m->H;
+    a.S = S;
+    a.dk = m->dk;
+    a.scale = sqrtf((float)m->dk);
+    a.lse = lse;
+    NML_TRY(launch_attention_prefill(F32, a, st));
+    NML_TRY(launch_linear(F32, lin(att, d, w.wo, w.bo, xm, R, d, d, EPI_BIAS_RESID, x), st));
+    NML_TRY(launch_rmsnorm(F32, xm, w.ln2, n2, nullptr, nullptr, R, d, kEps, st));
+    NML_TRY(launch_linear(F32, lin(n2, d, w.w1, w.b1, pre, R, F, d, EPI_BIAS), st));
+    NML_TRY(launch_gelu(F32, pre, hid, nullptr, (size_t)R * F, st));
+    NML_TRY(launch_linear(F32, lin(hid, F, w.w2, w.b2, xnext, R, d, F, EPI_BIAS_RESID, xm), st));
+  }
+  NML_TRY(launch_rmsnorm(F32, sv.xl, m->lnf, sv.hf, nullptr, nullptr, R, d, kEps, st));
+
+  const size_t chunk = logits_chunk(m, R);
+  NML_TRY(m->logits_ws.ensure(align256(chunk * m->V * 4)));
+  for (size_t r0 = 0; r0 < (size_t)R; r0 += chunk) {
+    const int n = (int)(((size_t)R - r0 < chunk) ? (size_t)R - r0 : chunk);
+    NML_TRY(launch_linear(F32, lin(sv.hf + r0 * d, d, m->emb, nullptr, m->logits_ws.p, n, m->V, d,
+                                   EPI_NONE), st));
+    NML_TRY(launch_ce_rows(F32, m->logits_ws.p, n, m->V, dlab + r0, ignore_index, has_ignore,
+                           row_loss, row_valid, err, st));
+    NML_TRY(launch_ce_reduce(row_loss, row_valid, n, acc, r0 > 0, st));
+  }
+  NML_TRY(launch_ce_finalize(acc, acc + 2, st));
+  double host[3];
+  int herr = 0;
+  NML_HIP(hipMemcpyAsync(host, acc, sizeof(host), hipMemcpyDeviceToHost, st));
+  NML_HIP(hipMemcpyAsync(&herr, err, sizeof(int), hipMemcpyDeviceToHost, st));
+  NML_HIP(hipStreamSynchronize(st));
+  NML_REQUIRE((herr & 1) == 0, "Token ID out of range [0, %d)", m->V);
+  NML_REQUIRE((herr & 2) == 0, "label out of range [0, %d)", m->V);
+  *loss = host[2];
+  t->B = B;
+  t->S = S;
+  t->ignore_index = ignore_index;
+  t->has_ignore = has_ignore;
+  t->n_valid = host[1];
+  t->saved = true;
+  return 0;
+}
+
+int nml_model_backward(nml_model* m, double grad_scale) {
+  NML_TRY(check_ready(m));
+  NML_REQUIRE(m->train && m->train->saved,
+              "backward: no saved forward (call nml_model_loss_train first)");
+  TrainState* t = m->train;
+  const int B = t->B, S = t->S, R = B * S, d = m->d, F = m->F, V = m->V;
+  if (t->n_valid <= 0.0) return 0;  // every label ignored: the loss is a constant 0
+  hipStream_t st = nml::stream();
+  Saved sv;
+  saved_floats(m, B, S, &sv, static_cast<float*>(t->acts.p));
+  const size_t ib = align256((size_t)R * 8);
+  const int64_t* dids = reinterpret_cast<const int64_t*>(t->io.p);
+  const int64_t* dlab = reinterpret_cast<const int64_t*>(static_cast<char*>(t->io.p) + ib);
+
+  // scratch: G, DX (R, d); DQKV (R, 3d); DPRE (R, F); dvec (B, H, S); row-sum partials
+  const size_t rd = align256((size_t)R * d * 4), r3 = align256((size_t)R * 3 * d * 4),
+               rf = align256((size_t)R * F * 4), rv = align256((size_t)B * m->H * S * 4);
+  const int widest = F > 3 * d ? F : 3 * d;
+  const size_t pn = (size_t)(rmsnorm_bwd_parts(R) > colsum_parts(R) ? rmsnorm_bwd_parts(R)
+                                                                     : colsum_parts(R)) *
+                    widest;
+  NML_TRY(t->scratch.ensure(2 * rd + r3 + rf + rv + align256(pn * 4)));
+  char* sp = static_cast<char*>(t->scratch.p);
+  float* G = reinterpret_cast<float*>(sp);
+  float* DX = reinterpret_cast<float*>(sp + rd);
+  float* DQKV = reinterpret_cast<float*>(sp + 2 * rd);
+  float* DPRE = reinterpret_cast<float*>(sp + 2 * rd + r3);
+  float* DVEC = reinterpret_cast<float*>(sp + 2 * rd + r3 + rf);
+  float* PART = reinterpret_cast<float*>(sp + 2 * rd + r3 + rf + rv);
+  const float* E = static_cast<const float*>(m->emb);
+  float* dE = grad_of(m, m->emb);
+
+  // tied head + cross-entropy, chunk by chunk; dH lands in DX
+  const float scale = static_cast<float>(grad_scale / t->n_valid);
+  const size_t chunk = logits_chunk(m, R);
+  NML_TRY(m->logits_ws.ensure(align256(chunk * V * 4)));
+  float* lg = static_cast<float*>(m->logits_ws.p);
+  for (size_t r0 = 0; r0 < (size_t)R; r0 += chunk) {
+    const int n = (int)(((size_t)R - r0 < chunk) ? (size_t)R - r0 : chunk);
+    const float* h = sv.hf + r0 * d;
+    NML_TRY(launch_linear(F32, lin(h, d, E, nullptr, lg, n, V, d, EPI_NONE), st));
+    NML_TRY(launch_ce_grad(lg, n, V, dlab + r0, t->ignore_index, t->has_ignore, scale, st));
+    NML_TRY(launch_gemm_bwd(gb(lg, V, E, d, DX + r0 * d, d, n, d, V), true, false, GB_SET, st));
+    NML_TRY(launch_gemm_bwd(gb(lg, V, h, d, dE, d, V, d, n), false, false, GB_ADD, st));
+  }
+  NML_TRY(launch_rmsnorm_bwd(DX, sv.xl, static_cast<const float*>(m->lnf), G, 0,
+                             grad_of(m, m->lnf), PART, R, d, kEps, st));
+
+  for (int l = m->L - 1; l >= 0; --l) {
+    const Layer& w = m->layers[l];
+    const float *x = at(sv.x, sv, l), *n1 = at(sv.n1, sv, l), *q = at(sv.q, sv, l),
+                *k = at(sv.k, sv, l), *v = at(sv.v, sv, l), *att = at(sv.att, sv, l),
+                *lse = at(sv.lse, sv, l), *xm = at(sv.xm, sv, l), *n2 = at(sv.n2, sv, l),
+                *pre = at(sv.pre, sv, l), *hid = at(sv.hid, sv, l);
+    // FFN (_fused_arrays.py:225-248)
+    NML_TRY(launch_gemm_bwd(gb(G, d, hid, F, grad_of(m, w.w2), F, d, F, R), false, false, GB_ADD, st));
+    NML_TRY(launch_colsum(G, d, R, d, grad_of(m, w.b2), PART, st));
+    NML_TRY(launch_gemm_bwd(gb(G, d, static_cast<const float*>(w.w2), F, DPRE, F, R, F, d, pre, F),
+                            true, false, GB_GELU, st));
+    NML_TRY(launch_gemm_bwd(gb(DPRE, F, n2, d, grad_of(m, w.w1), d, F, d, R), false, false, GB_ADD, st));
+    NML_TRY(launch_colsum(DPRE, F, R, F, grad_of(m, w.b1), PART, st));
+    NML_TRY(launch_gemm_bwd(gb(DPRE, F, static_cast<const float*>(w.w1), d, DX, d, R, d, F), true,
+                            false, GB_SET, st));
+    NML_TRY(launch_rmsnorm_bwd(DX, xm, static_cast<const float*>(w.ln2), G, 1, grad_of(m, w.ln2),
+                               PART, R, d, kEps, st));
+    // MHA (_fused_arrays.py:129-184)
+    NML_TRY(launch_gemm_bwd(gb(G, d, att, d, grad_of(m, w.wo), d, d, d, R), false, false, GB_ADD, st));
+    NML_TRY(launch_colsum(G, d, R, d, grad_of(m, w.bo), PART, st));
+    NML_TRY(launch_gemm_bwd(gb(G, d, static_cast<const float*>(w.wo), d, DX, d, R, d, d), true,
+                            false, GB_SET, st));
+    AttnBwdArgs ab{};
+    ab.q = q;
+    ab.k = k;
+    ab.v = v;
+    ab.o = att;
+    ab.dout = DX;
+    ab.lse = lse;
+    ab.dvec = DVEC;
+    ab.dqkv = DQKV;
+    ab.B = B;
+    ab.H = m->H;
+    ab.S = S;
+    ab.dk = m->dk;
+    ab.scale = sqrtf((float)m->dk);
+    NML_TRY(launch_attention_backward(ab, st));
+    if (rope_on(m))
+      NML_TRY(launch_rope_backward(DQKV, R, S, m->H, m->dk, static_cast<const float*>(m->rope_cos),
+                                   static_cast<const float*>(m->rope_sin), st));
+    NML_TRY(launch_gemm_bwd(gb(DQKV, 3 * d, n1, d, grad_of(m, w.wqkv), d, 3 * d, d, R), false,
+                            false, GB_ADD, st));
+    NML_TRY(launch_colsum(DQKV, 3 * d, R, 3 * d, grad_of(m, w.bqkv), PART, st));
+    NML_TRY(launch_gemm_bwd(gb(DQKV, 3 * d, static_cast<const float*>(w.wqkv), d, DX, d, R, d, 3 * d),
+                            true, false, GB_SET, st));
+    NML_TRY(launch_rmsnorm_bwd(DX, x, static_cast<const float*>(w.ln1), G, 1, grad_of(m, w.ln1),
+                               PART, R, d, kEps, st));
+  }
+  NML_TRY(launch_embed_backward(G, dids, dE, rope_on(m) ? nullptr : grad_of(m, m->pos), B, S, d, V,
+                                st));
+  NML_HIP(hipStreamSynchronize(st));
+  return 0;
+}
+
+}  // extern "C"

@@ -227,7 +227,13 @@ class GPT(Module):
 
     def compute_loss(self, input_ids, labels, ignore_index=None):
         """Mean tied-head cross-entropy (models/gpt.py:123-137); logits are formed in
-        row chunks on the device and never all at once."""
+        row chunks on the device and never all at once.
+
+        On a float32 model whose parameters require gradients the device keeps what the
+        backward needs, and ``loss.backward()`` adds every parameter's gradient to its
+        ``grad`` (losses/cross_entropy.py:166-191 and the array-level backward of
+        neural_network/_fused_arrays.py). float16 models return a loss without a graph.
+        """
         ids = _ids_array(input_ids)
         self._check_ids(ids)
         b, s = ids.shape
@@ -237,13 +243,59 @@ class GPT(Module):
         dlab = N.DeviceArray.from_host(lab)
         loss = C.c_double()
         has_ign = ignore_index is not None
-        N.check(N.lib.nml_model_loss(h, dids.ptr, dlab.ptr, b, s,
-                                     int(ignore_index) if has_ign else 0, int(has_ign),
-                                     C.byref(loss)))
+        train = self._dtype == np.float32 and any(p.requires_grad for p in self.parameters())
+        fn = N.lib.nml_model_loss_train if train else N.lib.nml_model_loss
+        N.check(fn(h, dids.ptr, dlab.ptr, b, s, int(ignore_index) if has_ign else 0,
+                   int(has_ign), C.byref(loss)))
         # The reference wraps the loss in a compute-dtype Tensor (losses/cross_entropy.py:158-164).
-        out = Tensor([0.0], ())
+        out = Tensor([0.0], (), requires_grad=train)
         out.data = np.asarray([loss.value], dtype=self._dtype)
+        if train:
+            dev = self._dev
+
+            def _backward():
+                if self._dev is not dev:
+                    raise RuntimeError("parameters were re-uploaded since this loss was "
+                                       "computed; compute the loss again")
+                N.check(N.lib.nml_model_zero_grad(h))
+                N.check(N.lib.nml_model_backward(h, float(out.grad[0])))
+                self._pull_grads()
+
+            out._backward = _backward
         return out
+
+    def _grad_array(self, kind, layer, shape):
+        """Device gradient of parameter (kind, layer) as a host float32 array."""
+        ptr = C.c_void_p()
+        N.check(N.lib.nml_model_grad_ptr(self._dev.handle, kind, layer, C.byref(ptr)))
+        out = np.empty(shape, dtype=np.float32)
+        N.check(N.lib.nml_memcpy_d2h(out.ctypes.data, ptr, out.nbytes))
+        return out
+
+    def _pull_grads(self):
+        """Add the device gradients of one backward to the parameters' ``grad``, in the
+        reference layouts ((in, out) weights, Q/K/V split)."""
+        d, f = self.d_model, self.ff_mult * self.d_model
+        g = self._grad_array
+        self.token_emb.weights._accumulate_grad(g(N.P_TOKEN_EMB, 0, (self.vocab_size, d)))
+        if self.pos_emb is not None:
+            self.pos_emb.weights._accumulate_grad(g(N.P_POS_EMB, 0, (self.max_seq_len, d)))
+        self.ln.gamma._accumulate_grad(g(N.P_LN_F, 0, (d,)))
+        for i, blk in enumerate(self._block_list):
+            m = blk.mha
+            wqkv = g(N.P_WQKV, i, (3 * d, d))
+            bqkv = g(N.P_BQKV, i, (3 * d,))
+            for j, dense in enumerate((m.W_q, m.W_k, m.W_v)):
+                dense.weights._accumulate_grad(wqkv[j * d:(j + 1) * d].T)
+                dense.biases._accumulate_grad(bqkv[j * d:(j + 1) * d])
+            m.W_o.weights._accumulate_grad(g(N.P_WO, i, (d, d)).T)
+            m.W_o.biases._accumulate_grad(g(N.P_BO, i, (d,)))
+            blk.ln1.gamma._accumulate_grad(g(N.P_LN1, i, (d,)))
+            blk.ln2.gamma._accumulate_grad(g(N.P_LN2, i, (d,)))
+            blk.ffn.dense1.weights._accumulate_grad(g(N.P_W1, i, (f, d)).T)
+            blk.ffn.dense1.biases._accumulate_grad(g(N.P_B1, i, (f,)))
+            blk.ffn.dense2.weights._accumulate_grad(g(N.P_W2, i, (d, f)).T)
+            blk.ffn.dense2.biases._accumulate_grad(g(N.P_B2, i, (d,)))
 
     @classmethod
     def from_arrays(cls, arrays, vocab_size, d_model, num_heads, num_layers, max_seq_len,

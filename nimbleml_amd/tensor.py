@@ -4,7 +4,12 @@ A flat buffer plus a shape. Float data is coerced to the compute dtype
 (tensor.py:147-153); ``from_int64`` keeps token ids as int64 (tensor.py:194-214).
 ``data`` is a host ``numpy.ndarray`` for parameters and inputs, or a
 ``DeviceArray`` for results left on the GPU (logits); ``np.asarray(t.data)``
-works for both. Autograd is not part of this path.
+works for both.
+
+Autograd covers the one graph this path builds: the loss of ``GPT.compute_loss``
+on a float32 model, whose ``backward()`` runs the whole backward on the device and
+accumulates each parameter's ``grad`` (tensor.py:271-352 for ``zero_grad``,
+``backward`` and ``_accumulate_grad``).
 """
 from __future__ import annotations
 
@@ -29,6 +34,7 @@ class Tensor:
         self.grad = None
         self._op = _op
         self._prev = set(_children)
+        self._backward = None
 
     @classmethod
     def from_int64(cls, data, shape):
@@ -42,6 +48,7 @@ class Tensor:
         obj.grad = None
         obj._op = ""
         obj._prev = set()
+        obj._backward = None
         return obj
 
     @property
@@ -66,6 +73,39 @@ class Tensor:
 
     def item(self) -> float:
         return float(np.asarray(self.data).reshape(-1)[0])
+
+    # ------------------------------------------------------------------ autograd
+    def zero_grad(self, set_to_none: bool = False):
+        """tensor.py:271-279."""
+        if set_to_none:
+            self.grad = None
+        else:
+            self.grad = np.zeros(self.size, dtype=np_backend.dtype)
+
+    def _accumulate_grad(self, grad):
+        """tensor.py:334-352: add ``grad`` (flattened, compute dtype) into ``self.grad``."""
+        if not self.requires_grad:
+            return
+        grad = np.asarray(grad).reshape(-1).astype(np_backend.dtype, copy=False)
+        if self.grad is None:
+            self.grad = grad.copy()
+        else:
+            self.grad = self.grad + grad
+
+    def backward(self, grad=None, retain_graph=False):
+        """tensor.py:286-332 for a scalar loss: seed ``grad`` (default 1) and run the
+        recorded backward once (the graph is released unless ``retain_graph``)."""
+        if grad is None:
+            if self.size != 1:
+                raise ValueError("grad must be specified for non-scalar tensors.")
+            grad = np.array([1.0], dtype=np_backend.dtype)
+        self.grad = np.asarray(grad, dtype=np_backend.dtype).reshape(-1)
+        fn = self._backward
+        if fn is None:
+            return
+        if not retain_graph:
+            self._backward = None
+        fn()
 
     def __repr__(self):
         return f"Tensor(shape={self.shape}, data={self.data})"

@@ -1,0 +1,186 @@
+"""Training on the device: ``compute_loss`` then ``loss.backward()`` on float32 models,
+every parameter's gradient against the float64 backward oracle (``oracle/grad_ref.py``,
+pinned by finite differences in test_grad_oracle.py).
+
+Tolerance: for each parameter tensor, max |device − oracle| ≤ 2e-5 · max |oracle| + 1e-7
+(float32 products and sums in another order; the mistakes this test is for — a wrong
+index, transposed operand or dropped term — move a gradient by O(1) of its size).
+Head dims 8, 16, 32, 64 and 128 cover every attention-backward tile shape; sequence
+lengths that are not tile multiples cover the partial tiles."""
+import ctypes as C
+
+import numpy as np
+import pytest
+
+from oracle import gpt_ref as R
+from oracle import grad_ref as G
+from oracle.weights import GPTConfig, make_weights, random_ids
+
+pytestmark = pytest.mark.gpu
+
+RTOL = 2e-5
+
+
+def _model(cfg, seed, rope=False, scale=4.0):
+    import nimbleml_amd as nm
+
+    w = make_weights(cfg, seed=seed, dtype=np.float32, rich=True)
+    for k in w:  # larger weights: attention and GELU away from their linear regimes
+        if k.endswith(".weights") and "emb" not in k:
+            w[k] = (w[k] * np.float32(scale)).astype(np.float32)
+    if rope:
+        w.pop("pos_emb.weights")
+    m = nm.GPT.from_arrays(w, cfg.vocab_size, cfg.d_model, cfg.num_heads, cfg.num_layers,
+                           cfg.max_seq_len, dtype=np.float32, use_rope=rope)
+    return m, w
+
+
+def _named_grads(m):
+    """The model's parameter grads under the reference names."""
+    out = {"token_emb.weights": m.token_emb.weights, "ln.gamma": m.ln.gamma}
+    if m.pos_emb is not None:
+        out["pos_emb.weights"] = m.pos_emb.weights
+    for i, blk in enumerate(m._block_list):
+        p = f"blocks.layers.{i}."
+        out[p + "ln1.gamma"] = blk.ln1.gamma
+        out[p + "ln2.gamma"] = blk.ln2.gamma
+        for n in ("W_q", "W_k", "W_v", "W_o"):
+            d = getattr(blk.mha, n)
+            out[p + f"mha.{n}.weights"] = d.weights
+            out[p + f"mha.{n}.biases"] = d.biases
+        for n in ("dense1", "dense2"):
+            d = getattr(blk.ffn, n)
+            out[p + f"ffn.{n}.weights"] = d.weights
+            out[p + f"ffn.{n}.biases"] = d.biases
+    return {k: (None if t.grad is None else np.asarray(t.grad).reshape(t.shape))
+            for k, t in out.items()}
+
+
+def _compare(got, want, factor=1.0):
+    worst = 0.0
+    for k, ref in want.items():
+        assert k in got and got[k] is not None, k
+        g = got[k].astype(np.float64)
+        ref = factor * ref
+        err = np.abs(g - ref).max()
+        bound = RTOL * np.abs(ref).max() + 1e-7
+        assert err <= bound, (k, err, bound)
+        if not k.endswith("W_k.biases"):  # identically 0: softmax ignores a per-row shift
+            worst = max(worst, err / np.abs(ref).max())
+    return worst
+
+
+def _oracle(w, cfg, ids, labels, ignore=None, rope=None, grad_scale=1.0):
+    w64 = {k: v.astype(np.float64) for k, v in w.items()}
+    if rope is not None:
+        rope = (rope[0].astype(np.float64), rope[1].astype(np.float64))
+    return G.loss_and_grads(w64, ids, labels, cfg.num_heads, cfg.num_layers, ignore_index=ignore,
+                            rope=rope, grad_scale=grad_scale)
+
+
+CASES = [
+    # (vocab, d, heads, layers, max_seq), batch, seq
+    ((48, 32, 4, 2, 16), 2, 7),        # dk 8, one partial tile
+    ((256, 64, 4, 2, 64), 3, 37),      # dk 16, two tiles, ragged end
+    ((512, 128, 4, 2, 96), 2, 96),     # dk 32, three full tiles
+    ((512, 128, 2, 2, 128), 2, 70),    # dk 64
+    ((1024, 256, 2, 1, 64), 2, 45),    # dk 128 (16-row tiles)
+]
+
+
+@pytest.mark.parametrize("dims,b,s", CASES)
+def test_backward_matches_oracle(gpu, dims, b, s):
+    cfg = GPTConfig(*dims)
+    m, w = _model(cfg, seed=21)
+    ids = random_ids((b, s), cfg.vocab_size, seed=5)
+    labels = random_ids((b * s,), cfg.vocab_size, seed=6)
+    loss = m.compute_loss(ids, labels)
+    assert loss.requires_grad
+    want_loss, want = _oracle(w, cfg, ids, labels)
+    assert abs(loss.item() - want_loss) <= 1e-5 * abs(want_loss)
+    loss.backward()
+    got = _named_grads(m)
+    print("worst relative gradient error", _compare(got, want))
+    # q·(k + b) shifts every score of a row by q·b: the key bias gets no gradient
+    for i in range(cfg.num_layers):
+        p = f"blocks.layers.{i}.mha."
+        assert np.abs(got[p + "W_k.biases"]).max() <= 1e-5 * np.abs(got[p + "W_q.biases"]).max()
+
+
+def test_ignore_index_grad_scale_and_accumulation(gpu):
+    cfg = GPTConfig(256, 64, 4, 2, 64)
+    m, w = _model(cfg, seed=22)
+    ids = random_ids((2, 33), cfg.vocab_size, seed=7)
+    labels = random_ids((66,), cfg.vocab_size, seed=8)
+    labels[::3] = -1
+    loss = m.compute_loss(ids, labels, ignore_index=-1)
+    want_loss, want = _oracle(w, cfg, ids, labels, ignore=-1)
+    assert abs(loss.item() - want_loss) <= 1e-5 * abs(want_loss)
+    loss.backward(np.array([0.5], np.float32))
+    _compare(_named_grads(m), want, factor=0.5)
+    # grads accumulate over backward calls (Tensor._accumulate_grad) ...
+    loss2 = m.compute_loss(ids, labels, ignore_index=-1)
+    loss2.backward()
+    _compare(_named_grads(m), want, factor=1.5)
+    # ... until zero_grad
+    for p in m.parameters():
+        p.zero_grad()
+    m.compute_loss(ids, labels, ignore_index=-1).backward()
+    _compare(_named_grads(m), want)
+
+
+def test_all_labels_ignored_gives_zero_loss_and_grads(gpu):
+    cfg = GPTConfig(48, 32, 4, 2, 16)
+    m, _ = _model(cfg, seed=23)
+    ids = random_ids((2, 5), cfg.vocab_size, seed=9)
+    loss = m.compute_loss(ids, np.full(10, -7), ignore_index=-7)
+    assert loss.item() == 0.0
+    loss.backward()
+    assert all(not np.any(g) for g in _named_grads(m).values())
+
+
+@pytest.mark.parametrize("dims,b,s", [((256, 64, 4, 2, 64), 2, 40), ((512, 128, 2, 1, 96), 2, 80)])
+def test_backward_with_rope(gpu, dims, b, s):
+    cfg = GPTConfig(*dims)
+    m, w = _model(cfg, seed=24, rope=True)
+    ids = random_ids((b, s), cfg.vocab_size, seed=10)
+    labels = random_ids((b * s,), cfg.vocab_size, seed=11)
+    loss = m.compute_loss(ids, labels)
+    rope = R.rope_cache(cfg.max_seq_len, cfg.d_model // cfg.num_heads)
+    want_loss, want = _oracle(w, cfg, ids, labels, rope=rope)
+    assert abs(loss.item() - want_loss) <= 1e-5 * abs(want_loss)
+    loss.backward()
+    got = _named_grads(m)
+    assert "pos_emb.weights" not in got
+    _compare(got, want)
+
+
+def test_c_abi_backward_accumulates_and_matches_loss(gpu):
+    """Through the C-ABI directly: loss_train equals compute_loss's plain loss, two
+    nml_model_backward calls double every gradient, zero_grad clears them."""
+    from nimbleml_amd import _native as N
+
+    cfg = GPTConfig(256, 64, 4, 2, 64)
+    m, w = _model(cfg, seed=25)
+    ids = random_ids((2, 30), cfg.vocab_size, seed=12)
+    labels = random_ids((60,), cfg.vocab_size, seed=13)
+    h = m._device_model()
+    dids = N.DeviceArray.from_host(ids)
+    dlab = N.DeviceArray.from_host(labels)
+    plain, trained = C.c_double(), C.c_double()
+    N.check(N.lib.nml_model_loss(h, dids.ptr, dlab.ptr, 2, 30, 0, 0, C.byref(plain)))
+    N.check(N.lib.nml_model_zero_grad(h))
+    N.check(N.lib.nml_model_loss_train(h, dids.ptr, dlab.ptr, 2, 30, 0, 0, C.byref(trained)))
+    assert abs(plain.value - trained.value) <= 1e-6 * abs(plain.value)
+    N.check(N.lib.nml_model_backward(h, 1.0))
+    one = m._grad_array(N.P_W1, 1, (cfg.d_ff, cfg.d_model))
+    N.check(N.lib.nml_model_backward(h, 1.0))
+    two = m._grad_array(N.P_W1, 1, (cfg.d_ff, cfg.d_model))
+    assert np.abs(two - 2 * one).max() <= 1e-6 * np.abs(one).max()
+    _, want = _oracle(w, cfg, ids, labels)
+    ref = want["blocks.layers.1.ffn.dense1.weights"].T
+    assert np.abs(one - ref).max() <= RTOL * np.abs(ref).max()
+    N.check(N.lib.nml_model_zero_grad(h))
+    assert not np.any(m._grad_array(N.P_W1, 1, (cfg.d_ff, cfg.d_model)))
+    with pytest.raises(RuntimeError):
+        N.check(N.lib.nml_model_grad_ptr(h, N.P_ROPE_COS, 0, C.byref(C.c_void_p())))
