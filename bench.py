@@ -161,6 +161,53 @@ def bench_adamw(nm, n=337_100_000, steps=20):
                          "bytes_per_element": 28}}
 
 
+MFMA_F32_PEAK_TFLOPS = 157.3
+
+
+def bench_train(nm, batch=4, seq=1024, steps=3):
+    """One training step of the C3 architecture in float32: compute_loss keeping the
+    activations (nml_model_loss_train) and loss.backward() into the device gradients
+    (nml_model_backward), batch × seq tokens. Algorithmic flops: 3× the forward's
+    (GEMMs 2·rows·12·d²·L + head 2·rows·d·V, attention 4·d·S(S+1)/2 per sequence and
+    layer), i.e. without the backward's recomputation of the logits and scores."""
+    import ctypes as C
+
+    from oracle.weights import C3, make_weights, random_ids
+
+    N = nm._native
+    cfg = C3
+    w = make_weights(cfg, seed=11, dtype=np.float32)
+    model = nm.GPT.from_arrays(w, cfg.vocab_size, cfg.d_model, cfg.num_heads, cfg.num_layers,
+                               cfg.max_seq_len, dtype=np.float32)
+    del w
+    h = model._device_model()
+    ids = N.DeviceArray.from_host(random_ids((batch, seq), cfg.vocab_size, seed=3))
+    lab = N.DeviceArray.from_host(random_ids((batch * seq,), cfg.vocab_size, seed=4))
+    loss = C.c_double()
+    N.check(N.lib.nml_model_zero_grad(h))
+
+    def step():
+        N.check(N.lib.nml_model_loss_train(h, ids.ptr, lab.ptr, batch, seq, 0, 0, C.byref(loss)))
+        N.check(N.lib.nml_model_backward(h, 1.0))
+
+    step()  # warm-up (allocates the saved activations)
+    t = N.Timer()
+    t.start()
+    for _ in range(steps):
+        step()
+    ms = t.stop() / steps
+    d, L, V, R = cfg.d_model, cfg.num_layers, cfg.vocab_size, batch * seq
+    fwd = 2 * R * L * 12 * d * d + L * batch * 4 * d * seq * (seq + 1) / 2 + 2 * R * d * V
+    tf = 3 * fwd / (ms * 1e-3) / 1e12
+    return {"workload": f"train step: GPT V32000 d1024 H16 L24 float32, batch {batch} x {seq}, "
+                        "compute_loss + backward on the device",
+            "value": round(R / (ms * 1e-3), 1), "unit": "tokens/s", "ms_per_step": round(ms, 3),
+            "loss": round(loss.value, 5),
+            "roofline": {"bound": "mfma", "achieved": round(tf, 1), "peak": MFMA_F32_PEAK_TFLOPS,
+                         "unit": "TFLOP/s", "frac": round(tf / MFMA_F32_PEAK_TFLOPS, 4),
+                         "flops": 3 * fwd}}
+
+
 def bench_c5(nm, reps=2):
     from oracle.weights import C5, make_weights, random_ids
 
@@ -199,7 +246,7 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-graph", action="store_true")
     ap.add_argument("--only-c3", action="store_true", help="skip the batch-32 and prefill lines")
-    ap.add_argument("--only", choices=["c3", "c4", "c5", "adamw"], default=None,
+    ap.add_argument("--only", choices=["c3", "c4", "c5", "adamw", "train"], default=None,
                     help="run one workload only (for profiling); c4/c5 print their own line")
     ap.add_argument("--cpu-tokens", type=int, default=12)
     ap.add_argument("--copy-calibration", action="store_true",
@@ -232,6 +279,9 @@ def main():
         return
     if args.only == "adamw":
         print(json.dumps({"adamw": bench_adamw(nm)}), flush=True)
+        return
+    if args.only == "train":
+        print(json.dumps({"train": bench_train(nm)}), flush=True)
         return
     w16 = make_weights(cfg, seed=1234, dtype=np.float16)
     model = nm.GPT.from_arrays(w16, cfg.vocab_size, cfg.d_model, cfg.num_heads, cfg.num_layers,
@@ -277,6 +327,7 @@ def main():
         result["c4"] = bench_c4(nm, cfg, model, use_graph)
         del model
         result["c5"] = bench_c5(nm)
+        result["train"] = bench_train(nm)
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline(cfg, w16, prompt, args.cpu_tokens)
     print(json.dumps(result), flush=True)
