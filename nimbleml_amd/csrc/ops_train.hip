@@ -12,6 +12,8 @@
 //    log-sum-exp, so no (S × S) matrix is kept.
 //  * reductions over rows (bias / gain gradients) go through per-block partial rows
 //    and a second pass in a fixed order: the result does not depend on scheduling.
+#include <cstdlib>
+
 #include "kernels.hpp"
 
 namespace nml {
@@ -465,8 +467,251 @@ __global__ __launch_bounds__(256) void attn_bwd_dq_kernel(AttnBwdArgs a) {
   }
 }
 
+// ---- MFMA variant (head dims 64 and 128): 64 keys × 64 queries per step, 4 waves.
+// Wave w = (wq, wk) = (w / 2, w % 2) takes the 32 × 32 sub-tile of queries 32·wq… and keys
+// 32·wk…; MFMA 32×32×2 fp32 throughout. A 32 × 32 result tile in registers holds, in
+// lane l and register r, row 8(r/4) + 4(l/32) + r%4 and column l%32; the products that
+// reduce over that row index take the registers themselves as their A operand (lane l
+// supplies rows f(r) for k = 0 and f(r) + 4 for k = 1, which only reorders the sum), so
+// P and dS never go through LDS. Tiles in LDS are [row][DK + 1] fp32.
+constexpr int kAT = 64;
+
+template <int DK>
+constexpr size_t attn_mfma_lds() {
+  return (4 * kAT * (DK + 1) + 2 * kAT) * sizeof(float);
+}
+
+// rows [lo, lo + 64) of a head-major (S, DK) slice into a [64][DK + 1] tile (0 past S)
+template <int DK>
+__device__ __forceinline__ void tile_rows(float* dst, const float* __restrict__ src, int lo, int S) {
+  for (int e = threadIdx.x; e < kAT * DK / 4; e += 256) {
+    const int r = e / (DK / 4), c = (e - r * (DK / 4)) * 4;
+    floatx4 v = {0.f, 0.f, 0.f, 0.f};
+    if (lo + r < S) v = *reinterpret_cast<const floatx4*>(src + static_cast<long long>(lo + r) * DK + c);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) dst[r * (DK + 1) + c + j] = v[j];
+  }
+}
+
+// rows [lo, lo + 64) of head h of a merged (B·S, H·DK) tensor
+template <int DK>
+__device__ __forceinline__ void tile_merged(float* dst, const float* __restrict__ src, int b, int h,
+                                            int H, int lo, int S) {
+  for (int e = threadIdx.x; e < kAT * DK / 4; e += 256) {
+    const int r = e / (DK / 4), c = (e - r * (DK / 4)) * 4;
+    floatx4 v = {0.f, 0.f, 0.f, 0.f};
+    if (lo + r < S)
+      v = *reinterpret_cast<const floatx4*>(src + (static_cast<long long>(b) * S + lo + r) * H * DK +
+                                            h * DK + c);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) dst[r * (DK + 1) + c + j] = v[j];
+  }
+}
+
+__device__ __forceinline__ int d_row(int r, int lane) { return 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3); }
+
+// dK, dV of 64 keys; the query tiles from the key tile on.
+template <int DK>
+__global__ __launch_bounds__(256) void attn_bwd_dkdv_mfma(AttnBwdArgs a) {
+  extern __shared__ float lds[];
+  constexpr int P = DK + 1, NJ = DK / 32;
+  float* Ks = lds;
+  float* Vs = Ks + kAT * P;
+  float* Qs = Vs + kAT * P;
+  float* Os = Qs + kAT * P;
+  float* Ls = Os + kAT * P;
+  float* Ds = Ls + kAT;
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, wq = w >> 1, wk = w & 1;
+  const int l32 = lane & 31, hi = lane >> 5;
+  const int bh = blockIdx.y, b = bh / a.H, h = bh - (bh / a.H) * a.H;
+  const int S = a.S, k_lo = blockIdx.x * kAT;
+  const long long hoff = static_cast<long long>(bh) * S * DK;
+  tile_rows<DK>(Ks, a.k + hoff, k_lo, S);
+  tile_rows<DK>(Vs, a.v + hoff, k_lo, S);
+  floatx16 dv[NJ], dk[NJ];
+#pragma unroll
+  for (int j = 0; j < NJ; ++j)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) dv[j][r] = dk[j][r] = 0.f;
+  const int key = k_lo + 32 * wk + l32;  // this lane's key (column of S)
+  const float scale = a.scale;
+  for (int q_lo = k_lo; q_lo < S; q_lo += kAT) {
+    __syncthreads();
+    tile_rows<DK>(Qs, a.q + hoff, q_lo, S);
+    tile_merged<DK>(Os, a.dout, b, h, a.H, q_lo, S);
+    if (threadIdx.x < kAT) {
+      const int q = q_lo + threadIdx.x;
+      Ls[threadIdx.x] = q < S ? a.lse[static_cast<long long>(bh) * S + q] : 0.f;
+      Ds[threadIdx.x] = q < S ? a.dvec[static_cast<long long>(bh) * S + q] : 0.f;
+    }
+    __syncthreads();
+    floatx16 sc, dp;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) sc[r] = dp[r] = 0.f;
+    const float* qa = Qs + (32 * wq + l32) * P + hi;
+    const float* oa = Os + (32 * wq + l32) * P + hi;
+    const float* kb = Ks + (32 * wk + l32) * P + hi;
+    const float* vb = Vs + (32 * wk + l32) * P + hi;
+#pragma unroll 8
+    for (int c0 = 0; c0 < DK; c0 += 2) {
+      sc = __builtin_amdgcn_mfma_f32_32x32x2f32(qa[c0], kb[c0], sc, 0, 0, 0);
+      dp = __builtin_amdgcn_mfma_f32_32x32x2f32(oa[c0], vb[c0], dp, 0, 0, 0);
+    }
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int ql = 32 * wq + d_row(r, lane), q = q_lo + ql;
+      float p = 0.f;
+      if (key <= q && q < S) p = expf(sc[r] / scale - Ls[ql]);
+      sc[r] = p;
+      dp[r] = p * (dp[r] - Ds[ql]) / scale;
+    }
+    // dV[key][c] += Σ_q P[q][key]·dO[q][c];  dK[key][c] += Σ_q dS[q][key]·Q[q][c]
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int ql = 32 * wq + d_row(r, lane);
+#pragma unroll
+      for (int j = 0; j < NJ; ++j) {
+        dv[j] = __builtin_amdgcn_mfma_f32_32x32x2f32(sc[r], Os[ql * P + 32 * j + l32], dv[j], 0, 0, 0);
+        dk[j] = __builtin_amdgcn_mfma_f32_32x32x2f32(dp[r], Qs[ql * P + 32 * j + l32], dk[j], 0, 0, 0);
+      }
+    }
+  }
+  // the two query halves (wq = 0, 1) of each key half meet in LDS
+  __syncthreads();
+  float* red = Qs;  // 2 key halves × (dv, dk) × NJ × 16 × 64 floats
+  if (wq == 1) {
+#pragma unroll
+    for (int j = 0; j < NJ; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        red[(((wk * 2 + 0) * NJ + j) * 16 + r) * 64 + lane] = dv[j][r];
+        red[(((wk * 2 + 1) * NJ + j) * 16 + r) * 64 + lane] = dk[j][r];
+      }
+  }
+  __syncthreads();
+  if (wq == 0) {
+    const int d = a.H * DK;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int kk = k_lo + 32 * wk + d_row(r, lane);
+      if (kk < S) {
+        float* row = a.dqkv + (static_cast<long long>(b) * S + kk) * 3 * d + h * DK;
+#pragma unroll
+        for (int j = 0; j < NJ; ++j) {
+          row[d + 32 * j + l32] = dk[j][r] + red[(((wk * 2 + 1) * NJ + j) * 16 + r) * 64 + lane];
+          row[2 * d + 32 * j + l32] = dv[j][r] + red[(((wk * 2 + 0) * NJ + j) * 16 + r) * 64 + lane];
+        }
+      }
+    }
+  }
+}
+
+// dQ of 64 queries; the key tiles up to the query tile. Wave w = (wk, wq) = (w / 2, w % 2)
+// computes Sᵀ (keys as rows) so that its registers feed dQ = dS·K as the A operand.
+template <int DK>
+__global__ __launch_bounds__(256) void attn_bwd_dq_mfma(AttnBwdArgs a) {
+  extern __shared__ float lds[];
+  constexpr int P = DK + 1, NJ = DK / 32;
+  float* Ks = lds;
+  float* Vs = Ks + kAT * P;
+  float* Qs = Vs + kAT * P;
+  float* Os = Qs + kAT * P;
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, wk = w >> 1, wq = w & 1;
+  const int l32 = lane & 31, hi = lane >> 5;
+  const int bh = blockIdx.y, b = bh / a.H, h = bh - (bh / a.H) * a.H;
+  const int S = a.S, q_lo = blockIdx.x * kAT;
+  const long long hoff = static_cast<long long>(bh) * S * DK;
+  tile_rows<DK>(Qs, a.q + hoff, q_lo, S);
+  tile_merged<DK>(Os, a.dout, b, h, a.H, q_lo, S);
+  const int q = q_lo + 32 * wq + l32;  // this lane's query (column of Sᵀ)
+  const float lse = q < S ? a.lse[static_cast<long long>(bh) * S + q] : 0.f;
+  const float dd = q < S ? a.dvec[static_cast<long long>(bh) * S + q] : 0.f;
+  floatx16 dq[NJ];
+#pragma unroll
+  for (int j = 0; j < NJ; ++j)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) dq[j][r] = 0.f;
+  const int k_end = min(S, q_lo + kAT);
+  for (int k_lo = 0; k_lo < k_end; k_lo += kAT) {
+    __syncthreads();
+    tile_rows<DK>(Ks, a.k + hoff, k_lo, S);
+    tile_rows<DK>(Vs, a.v + hoff, k_lo, S);
+    __syncthreads();
+    floatx16 sc, dp;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) sc[r] = dp[r] = 0.f;
+    const float* ka = Ks + (32 * wk + l32) * P + hi;
+    const float* va = Vs + (32 * wk + l32) * P + hi;
+    const float* qb = Qs + (32 * wq + l32) * P + hi;
+    const float* ob = Os + (32 * wq + l32) * P + hi;
+#pragma unroll 8
+    for (int c0 = 0; c0 < DK; c0 += 2) {
+      sc = __builtin_amdgcn_mfma_f32_32x32x2f32(ka[c0], qb[c0], sc, 0, 0, 0);
+      dp = __builtin_amdgcn_mfma_f32_32x32x2f32(va[c0], ob[c0], dp, 0, 0, 0);
+    }
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int kk = k_lo + 32 * wk + d_row(r, lane);
+      float p = 0.f;
+      if (kk <= q && q < S) p = expf(sc[r] / a.scale - lse);
+      dp[r] = p * (dp[r] - dd) / a.scale;
+    }
+    // dQ[q][c] += Σ_key dS[q][key]·K[key][c]
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int kl = 32 * wk + d_row(r, lane);
+#pragma unroll
+      for (int j = 0; j < NJ; ++j)
+        dq[j] = __builtin_amdgcn_mfma_f32_32x32x2f32(dp[r], Ks[kl * P + 32 * j + l32], dq[j], 0, 0, 0);
+    }
+  }
+  __syncthreads();
+  float* red = Ks;  // 2 query halves × NJ × 16 × 64 floats
+  if (wk == 1) {
+#pragma unroll
+    for (int j = 0; j < NJ; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) red[((wq * NJ + j) * 16 + r) * 64 + lane] = dq[j][r];
+  }
+  __syncthreads();
+  if (wk == 0) {
+    const int d = a.H * DK;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int qq = q_lo + 32 * wq + d_row(r, lane);
+      if (qq < S) {
+        float* row = a.dqkv + (static_cast<long long>(b) * S + qq) * 3 * d + h * DK;
+#pragma unroll
+        for (int j = 0; j < NJ; ++j) row[32 * j + l32] = dq[j][r] + red[((wq * NJ + j) * 16 + r) * 64 + lane];
+      }
+    }
+  }
+}
+
+template <int DK>
+int attn_bwd_mfma(const AttnBwdArgs& a, hipStream_t st) {
+  constexpr size_t lds = attn_mfma_lds<DK>();
+  static bool attr = false;
+  if (!attr) {
+    NML_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(&attn_bwd_dkdv_mfma<DK>),
+                                hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds)));
+    NML_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(&attn_bwd_dq_mfma<DK>),
+                                hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds)));
+    attr = true;
+  }
+  const dim3 grid((a.S + kAT - 1) / kAT, a.B * a.H);
+  attn_bwd_dkdv_mfma<DK><<<grid, 256, lds, st>>>(a);
+  NML_LAUNCHED();
+  attn_bwd_dq_mfma<DK><<<grid, 256, lds, st>>>(a);
+  NML_LAUNCHED();
+  return 0;
+}
+
 template <int DK>
 int attn_bwd_dk(const AttnBwdArgs& a, hipStream_t st) {
+  if constexpr (DK == 64 || DK == 128) {
+    if (!std::getenv("NIMBLEML_ATTN_BWD_VALU")) return attn_bwd_mfma<DK>(a, st);
+  }
   constexpr int BT = DK >= 128 ? 16 : 32;
   const dim3 grid((a.S + BT - 1) / BT, a.B * a.H);
   attn_bwd_dkdv_kernel<DK, BT><<<grid, 256, 0, st>>>(a);
