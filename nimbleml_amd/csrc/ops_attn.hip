@@ -13,6 +13,8 @@
 //    workgroup scores a group of 64-key chunks of one (sequence, head) and publishes
 //    its (max, Σp, Σp·v) as flagged slots; the last workgroup of the (sequence, head)
 //    merges them. Head dims 8/16: attn_decode_small_kernel + attn_combine_kernel.
+#include <cstdlib>
+
 #include "kernels.hpp"
 
 namespace nml {
@@ -602,8 +604,149 @@ __global__ __launch_bounds__(256, 2) void attn_prefill_mfma_kernel(AttnArgs a) {
 }
 
 
+// fp32 causal prefill on MFMA 32×32×2 (head dims 64 and 128): 4 waves × 32 queries per
+// block, key tiles of 64 through LDS. Each wave computes Sᵀ = K·Qᵀ (keys as rows) so
+// that lane l and lane l ^ 32 own query l % 32: the online-softmax state is per lane,
+// and Oᵀ = Vᵀ·Pᵀ takes the probabilities straight from the registers (lane l supplies
+// key rows f(r) for k = 0 and f(r) + 4 for k = 1 of the 32 × 32 tile, which only
+// reorders the sum). Scores are q·k / scale in fp32 as in attn_prefill_kernel.
+constexpr int kF32Q = 128, kF32K = 64;
+
+template <int DK>
+constexpr size_t f32_mfma_lds() {
+  return 2 * kF32K * (DK + 1) * sizeof(float);
+}
+
+template <int DK>
+__global__ __launch_bounds__(256) void attn_prefill_f32_mfma(AttnArgs a) {
+  extern __shared__ float lds[];
+  constexpr int P = DK + 1, NJ = DK / 32;
+  float* Ks = lds;
+  float* Vs = lds + kF32K * P;
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, l32 = lane & 31, hi = lane >> 5;
+  const int bh = blockIdx.y, b = bh / a.H, h = bh - (bh / a.H) * a.H;
+  const int S = a.seq_len ? a.seq_len[b] : a.S;
+  const int q0 = blockIdx.x * kF32Q;
+  if (q0 >= S) return;  // past a ragged sequence's end (uniform over the block)
+  const int base = a.pos_base ? a.pos_base[b] : 0;
+  const int s = q0 + 32 * w + l32;
+  const bool valid = s < S;
+  const int qpos = base + (valid ? s : S - 1);
+  const int kv_end = base + min(S, q0 + kF32Q);                  // keys of the block
+  const int wave_last = base + min(S - 1, q0 + 32 * w + 31);     // last key this wave needs
+  const float* __restrict__ K = static_cast<const float*>(a.k) + b * a.kv_stride_b + h * a.kv_stride_h;
+  const float* __restrict__ V = static_cast<const float*>(a.v) + b * a.kv_stride_b + h * a.kv_stride_h;
+  float qr[DK / 2];  // Q[s][2i + hi]: the B operand of Sᵀ
+  {
+    const float* qp = static_cast<const float*>(a.q) +
+                      (static_cast<size_t>(bh) * a.S + (valid ? s : S - 1)) * DK + hi;
+#pragma unroll
+    for (int i = 0; i < DK / 2; ++i) qr[i] = qp[2 * i];
+  }
+  floatx16 o[NJ];
+#pragma unroll
+  for (int j = 0; j < NJ; ++j)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) o[j][r] = 0.f;
+  float m = -INFINITY, l = 0.f;
+  for (int k0 = 0; k0 < kv_end; k0 += kF32K) {
+    __syncthreads();
+    for (int e = threadIdx.x; e < kF32K * DK / 4; e += 256) {
+      const int r = e / (DK / 4), c = (e - r * (DK / 4)) * 4;
+      floatx4 kv = {0.f, 0.f, 0.f, 0.f}, vv = kv;
+      if (k0 + r < kv_end) {
+        kv = *reinterpret_cast<const floatx4*>(K + static_cast<long long>(k0 + r) * DK + c);
+        vv = *reinterpret_cast<const floatx4*>(V + static_cast<long long>(k0 + r) * DK + c);
+      }
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        Ks[r * P + c + j] = kv[j];
+        Vs[r * P + c + j] = vv[j];
+      }
+    }
+    __syncthreads();
+    if (k0 > wave_last) continue;  // every key of the tile is after this wave's queries
+    floatx16 sc[2];
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) sc[t][r] = 0.f;
+      const float* ka = Ks + (32 * t + l32) * P + hi;
+#pragma unroll
+      for (int i = 0; i < DK / 2; ++i)
+        sc[t] = __builtin_amdgcn_mfma_f32_32x32x2f32(ka[2 * i], qr[i], sc[t], 0, 0, 0);
+    }
+    float mloc = -INFINITY;
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int key = k0 + 32 * t + 8 * (r >> 2) + 4 * hi + (r & 3);
+        const float v = key <= qpos ? sc[t][r] / a.scale : -INFINITY;
+        sc[t][r] = v;
+        mloc = fmaxf(mloc, v);
+      }
+    mloc = fmaxf(mloc, __shfl_xor(mloc, 32, 64));
+    // finite: the first tile holds key 0, which every query sees
+    const float mn = fmaxf(m, mloc);
+    const float alpha = expf(m - mn);
+    float lsum = 0.f;
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const float p = expf(sc[t][r] - mn);
+        sc[t][r] = p;
+        lsum += p;
+      }
+    l = l * alpha + (lsum + __shfl_xor(lsum, 32, 64));
+    m = mn;
+#pragma unroll
+    for (int j = 0; j < NJ; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) o[j][r] *= alpha;
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const float* vrow = Vs + (32 * t + 8 * (r >> 2) + 4 * hi + (r & 3)) * P + l32;
+#pragma unroll
+        for (int j = 0; j < NJ; ++j)
+          o[j] = __builtin_amdgcn_mfma_f32_32x32x2f32(vrow[32 * j], sc[t][r], o[j], 0, 0, 0);
+      }
+  }
+  if (valid) {
+    const size_t row = (a.row_start ? a.row_start[b] : static_cast<size_t>(b) * a.S) + s;
+    float* out = static_cast<float*>(a.out) + row * a.H * DK + h * DK;
+    const float inv = 1.f / l;
+#pragma unroll
+    for (int j = 0; j < NJ; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) out[32 * j + 8 * (r >> 2) + 4 * hi + (r & 3)] = o[j][r] * inv;
+    if (a.lse && hi == 0) a.lse[static_cast<size_t>(bh) * a.S + s] = m + logf(l);
+  }
+}
+
+template <int DK>
+int prefill_f32_mfma(const AttnArgs& a, hipStream_t st) {
+  constexpr size_t lds = f32_mfma_lds<DK>();
+  static bool attr = false;
+  if (!attr) {
+    NML_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(&attn_prefill_f32_mfma<DK>),
+                                hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds)));
+    attr = true;
+  }
+  dim3 grid((a.S + kF32Q - 1) / kF32Q, a.B * a.H);
+  attn_prefill_f32_mfma<DK><<<grid, 256, lds, st>>>(a);
+  NML_LAUNCHED();
+  return 0;
+}
+
 template <typename T, int DK>
 int prefill_typed(const AttnArgs& a, hipStream_t st) {
+  if constexpr (sizeof(T) == 4 && (DK == 64 || DK == 128)) {
+    if (!std::getenv("NIMBLEML_ATTN_F32_SCALAR")) return prefill_f32_mfma<DK>(a, st);
+  }
   if constexpr (sizeof(T) == 2 && (DK == 64 || DK == 128)) {
     NML_REQUIRE(a.lse == nullptr, "attention: the log-sum-exp output needs a float32 model");
     dim3 grid((a.S + kFQ - 1) / kFQ, a.B * a.H);
