@@ -76,14 +76,19 @@ __device__ __forceinline__ void tile_store(float (*S)[kGM + kGPad], const floatx
   }
 }
 
+// Split K (gridDim.z > 1): block z multiplies k in [z·kchunk, (z + 1)·kchunk) and writes
+// its partial product to c + z·zstride (OUT = GB_SET), summed afterwards in a fixed order.
 template <bool A_KC, bool B_KC, int OUT>
-__global__ __launch_bounds__(256) void gemm_bwd_kernel(GemmBwdArgs g) {
+__global__ __launch_bounds__(256) void gemm_bwd_kernel(GemmBwdArgs g, int kchunk, long long zstride) {
   __shared__ __attribute__((aligned(16))) float As[kGK][kGM + kGPad];
   __shared__ __attribute__((aligned(16))) float Bs[kGK][kGM + kGPad];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int wm = wave >> 1, wn = wave & 1;
   const int m0 = blockIdx.y * kGM, n0 = blockIdx.x * kGM;
-  const int M = g.M, N = g.N, K = g.K;
+  const int M = g.M, N = g.N;
+  const int kbeg = blockIdx.z * kchunk;
+  const int K = min(g.K, kbeg + kchunk);
+  g.c += blockIdx.z * zstride;
 
   floatx16 acc[2][2];
 #pragma unroll
@@ -94,12 +99,12 @@ __global__ __launch_bounds__(256) void gemm_bwd_kernel(GemmBwdArgs g) {
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
 
   floatx4 ra[2], rb[2];
-  tile_load<A_KC>(g.a, g.lda, m0, M, 0, K, ra);
-  tile_load<B_KC>(g.b, g.ldb, n0, N, 0, K, rb);
+  tile_load<A_KC>(g.a, g.lda, m0, M, kbeg, K, ra);
+  tile_load<B_KC>(g.b, g.ldb, n0, N, kbeg, K, rb);
   tile_store<A_KC>(As, ra);
   tile_store<B_KC>(Bs, rb);
   __syncthreads();
-  for (int k0 = 0; k0 < K; k0 += kGK) {
+  for (int k0 = kbeg; k0 < K; k0 += kGK) {
     const bool more = k0 + kGK < K;
     if (more) {  // next tile's loads in flight while this one multiplies
       tile_load<A_KC>(g.a, g.lda, m0, M, k0 + kGK, K, ra);
@@ -145,13 +150,62 @@ __global__ __launch_bounds__(256) void gemm_bwd_kernel(GemmBwdArgs g) {
       }
 }
 
+// c[m·ldc + n] += Σ_z part[z·M·N + m·N + n], z in order.
+__global__ __launch_bounds__(256) void splitk_reduce_kernel(const float* __restrict__ part, int splits,
+                                                            int M, int N, float* __restrict__ c,
+                                                            long long ldc) {
+  const long long i = static_cast<long long>(blockIdx.x) * 256 + threadIdx.x;
+  const long long mn = static_cast<long long>(M) * N;
+  if (i >= mn) return;
+  float s = 0.f;
+  for (int z = 0; z < splits; ++z) s += part[z * mn + i];
+  const int m = static_cast<int>(i / N), n = static_cast<int>(i - static_cast<long long>(m) * N);
+  c[static_cast<long long>(m) * ldc + n] += s;
+}
+
+// Split-K partials of the weight-gradient GEMMs (grow-only; training is never captured).
+struct SplitWs {
+  float* p = nullptr;
+  size_t floats = 0;
+};
+SplitWs g_split;
+
 template <bool A_KC, bool B_KC>
 int gemm_bwd_out(const GemmBwdArgs& g, int out, hipStream_t st) {
-  const dim3 grid((g.N + kGM - 1) / kGM, (g.M + kGM - 1) / kGM);
+  const int tn = (g.N + kGM - 1) / kGM, tm = (g.M + kGM - 1) / kGM;
+  // Few output tiles and a long K (a weight gradient, K = rows): split K so that the
+  // grid holds ≥ 1024 blocks, each K slice ≥ 512 long.
+  int splits = 1;
+  if (out == GB_ADD) {
+    while (splits < 16 && tn * tm * splits < 1024 && g.K / (2 * splits) >= 512) splits *= 2;
+  }
+  if (splits > 1) {
+    const size_t need = static_cast<size_t>(splits) * g.M * g.N;
+    if (need > g_split.floats) {
+      NML_HIP(hipStreamSynchronize(st));
+      if (g_split.p) NML_HIP(hipFree(g_split.p));
+      g_split = SplitWs{};
+      NML_HIP(hipMalloc(&g_split.p, need * sizeof(float)));
+      g_split.floats = need;
+    }
+    const int kchunk = ((g.K + splits - 1) / splits + kGK - 1) / kGK * kGK;
+    GemmBwdArgs p = g;
+    p.c = g_split.p;
+    p.ldc = g.N;
+    const dim3 grid(tn, tm, splits);
+    gemm_bwd_kernel<A_KC, B_KC, GB_SET><<<grid, 256, 0, st>>>(p, kchunk, static_cast<long long>(g.M) * g.N);
+    NML_LAUNCHED();
+    const long long mn = static_cast<long long>(g.M) * g.N;
+    splitk_reduce_kernel<<<static_cast<int>((mn + 255) / 256), 256, 0, st>>>(g_split.p, splits, g.M,
+                                                                              g.N, g.c, g.ldc);
+    NML_LAUNCHED();
+    return 0;
+  }
+  const dim3 grid(tn, tm);
   switch (out) {
-    case GB_SET: gemm_bwd_kernel<A_KC, B_KC, GB_SET><<<grid, 256, 0, st>>>(g); break;
-    case GB_ADD: gemm_bwd_kernel<A_KC, B_KC, GB_ADD><<<grid, 256, 0, st>>>(g); break;
-    case GB_GELU: gemm_bwd_kernel<A_KC, B_KC, GB_GELU><<<grid, 256, 0, st>>>(g); break;
+    case GB_SET: gemm_bwd_kernel<A_KC, B_KC, GB_SET><<<grid, 256, 0, st>>>(g, g.K, 0); break;
+    case GB_ADD: gemm_bwd_kernel<A_KC, B_KC, GB_ADD><<<grid, 256, 0, st>>>(g, g.K, 0); break;
+    case GB_GELU: gemm_bwd_kernel<A_KC, B_KC, GB_GELU><<<grid, 256, 0, st>>>(g, g.K, 0); break;
     default: set_error("gemm_bwd: unknown output mode %d", out); return -1;
   }
   NML_LAUNCHED();
@@ -227,15 +281,25 @@ __global__ __launch_bounds__(256) void rmsnorm_bwd_kernel(const float* __restric
   }
 }
 
-// out[c] += Σ_p part[p·n + c], p in order.
+// out[c] += Σ_p part[p·n + c]: 32 columns per block, 8 thread rows each summing every
+// 8th part, then the 8 row sums in order (a fixed order: deterministic).
 __global__ __launch_bounds__(256) void parts_reduce_kernel(const float* __restrict__ part,
                                                            int nparts, int n,
                                                            float* __restrict__ out) {
-  const int c = blockIdx.x * 256 + threadIdx.x;
-  if (c >= n) return;
+  __shared__ float red[8][33];
+  const int tx = threadIdx.x & 31, ty = threadIdx.x >> 5;
+  const int c = blockIdx.x * 32 + tx;
   float s = 0.f;
-  for (int p = 0; p < nparts; ++p) s += part[static_cast<long long>(p) * n + c];
-  out[c] += s;
+  if (c < n)
+    for (int p = ty; p < nparts; p += 8) s += part[static_cast<long long>(p) * n + c];
+  red[ty][tx] = s;
+  __syncthreads();
+  if (ty == 0 && c < n) {
+    float t = 0.f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) t += red[i][tx];
+    out[c] += t;
+  }
 }
 
 // ---------------------------------------------------------------- column sums
@@ -799,7 +863,7 @@ int launch_rmsnorm_bwd(const float* dy, const float* x, const float* gamma, floa
   else NML_NORM_BWD(32);
 #undef NML_NORM_BWD
   NML_LAUNCHED();
-  parts_reduce_kernel<<<(d + 255) / 256, 256, 0, st>>>(part, blocks, d, dgamma);
+  parts_reduce_kernel<<<(d + 31) / 32, 256, 0, st>>>(part, blocks, d, dgamma);
   NML_LAUNCHED();
   return 0;
 }
@@ -812,7 +876,7 @@ int launch_colsum(const float* a, long long lda, int rows, int n, float* out, fl
   const int parts = colsum_parts(rows);
   colsum_part_kernel<<<dim3((n + 255) / 256, parts), 256, 0, st>>>(a, lda, rows, n, part);
   NML_LAUNCHED();
-  parts_reduce_kernel<<<(n + 255) / 256, 256, 0, st>>>(part, parts, n, out);
+  parts_reduce_kernel<<<(n + 31) / 32, 256, 0, st>>>(part, parts, n, out);
   NML_LAUNCHED();
   return 0;
 }

@@ -85,6 +85,7 @@ CASES = [
     ((512, 128, 4, 2, 96), 2, 96),     # dk 32, three full tiles
     ((512, 128, 2, 2, 128), 2, 70),    # dk 64
     ((1024, 256, 2, 1, 64), 2, 45),    # dk 128 (16-row tiles)
+    ((256, 128, 2, 1, 512), 2, 512),   # 1024 rows: weight gradients split over K
 ]
 
 
