@@ -649,22 +649,34 @@ __global__ __launch_bounds__(256) void attn_prefill_f32_mfma(AttnArgs a) {
 #pragma unroll
     for (int r = 0; r < 16; ++r) o[j][r] = 0.f;
   float m = -INFINITY, l = 0.f;
-  for (int k0 = 0; k0 < kv_end; k0 += kF32K) {
-    __syncthreads();
-    for (int e = threadIdx.x; e < kF32K * DK / 4; e += 256) {
+  // the next K/V tile is loaded into registers while the current one multiplies
+  floatx4 nk[DK / 16], nv[DK / 16];
+  auto fetch = [&](int k0) {
+#pragma unroll
+    for (int i = 0; i < DK / 16; ++i) {
+      const int e = threadIdx.x + 256 * i;
       const int r = e / (DK / 4), c = (e - r * (DK / 4)) * 4;
-      floatx4 kv = {0.f, 0.f, 0.f, 0.f}, vv = kv;
-      if (k0 + r < kv_end) {
-        kv = *reinterpret_cast<const floatx4*>(K + static_cast<long long>(k0 + r) * DK + c);
-        vv = *reinterpret_cast<const floatx4*>(V + static_cast<long long>(k0 + r) * DK + c);
-      }
+      const floatx4 z = {0.f, 0.f, 0.f, 0.f};
+      const bool ok = k0 + r < kv_end;
+      nk[i] = ok ? *reinterpret_cast<const floatx4*>(K + static_cast<long long>(k0 + r) * DK + c) : z;
+      nv[i] = ok ? *reinterpret_cast<const floatx4*>(V + static_cast<long long>(k0 + r) * DK + c) : z;
+    }
+  };
+  fetch(0);
+  for (int k0 = 0; k0 < kv_end; k0 += kF32K) {
+    __syncthreads();  // every wave is done with the previous tile
+#pragma unroll
+    for (int i = 0; i < DK / 16; ++i) {
+      const int e = threadIdx.x + 256 * i;
+      const int r = e / (DK / 4), c = (e - r * (DK / 4)) * 4;
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        Ks[r * P + c + j] = kv[j];
-        Vs[r * P + c + j] = vv[j];
+        Ks[r * P + c + j] = nk[i][j];
+        Vs[r * P + c + j] = nv[i][j];
       }
     }
     __syncthreads();
+    if (k0 + kF32K < kv_end) fetch(k0 + kF32K);
     if (k0 > wave_last) continue;  // every key of the tile is after this wave's queries
     floatx16 sc[2];
 #pragma unroll

@@ -574,9 +574,35 @@ __device__ __forceinline__ void tile_merged(float* dst, const float* __restrict_
 
 __device__ __forceinline__ int d_row(int r, int lane) { return 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3); }
 
+// A 64 × DK tile staged through registers (DK/16 16-byte vectors per thread) so that the
+// next tile's loads are in flight while the current one multiplies.
+template <int DK>
+struct TileRegs {
+  floatx4 v[DK / 16];
+  // rows [lo, lo + 64) of a row-major source with row stride ld (0 past S)
+  __device__ __forceinline__ void load(const float* __restrict__ src, long long ld, int lo, int S) {
+#pragma unroll
+    for (int i = 0; i < DK / 16; ++i) {
+      const int e = threadIdx.x + 256 * i;
+      const int r = e / (DK / 4), c = (e - r * (DK / 4)) * 4;
+      const floatx4 z = {0.f, 0.f, 0.f, 0.f};
+      v[i] = lo + r < S ? *reinterpret_cast<const floatx4*>(src + static_cast<long long>(lo + r) * ld + c) : z;
+    }
+  }
+  __device__ __forceinline__ void store(float* dst) const {
+#pragma unroll
+    for (int i = 0; i < DK / 16; ++i) {
+      const int e = threadIdx.x + 256 * i;
+      const int r = e / (DK / 4), c = (e - r * (DK / 4)) * 4;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) dst[r * (DK + 1) + c + j] = v[i][j];
+    }
+  }
+};
+
 // dK, dV of 64 keys; the query tiles from the key tile on.
 template <int DK>
-__global__ __launch_bounds__(256) void attn_bwd_dkdv_mfma(AttnBwdArgs a) {
+__global__ __launch_bounds__(256, 2) void attn_bwd_dkdv_mfma(AttnBwdArgs a) {
   extern __shared__ float lds[];
   constexpr int P = DK + 1, NJ = DK / 32;
   float* Ks = lds;
@@ -598,17 +624,30 @@ __global__ __launch_bounds__(256) void attn_bwd_dkdv_mfma(AttnBwdArgs a) {
 #pragma unroll
     for (int r = 0; r < 16; ++r) dv[j][r] = dk[j][r] = 0.f;
   const int key = k_lo + 32 * wk + l32;  // this lane's key (column of S)
-  const float scale = a.scale;
-  for (int q_lo = k_lo; q_lo < S; q_lo += kAT) {
-    __syncthreads();
-    tile_rows<DK>(Qs, a.q + hoff, q_lo, S);
-    tile_merged<DK>(Os, a.dout, b, h, a.H, q_lo, S);
+  const float inv_scale = 1.0f / a.scale;
+  const float* dout_b = a.dout + static_cast<long long>(b) * S * a.H * DK + h * DK;
+  TileRegs<DK> nq, no;
+  float nl = 0.f, nd = 0.f;
+  auto fetch = [&](int lo) {
+    nq.load(a.q + hoff, DK, lo, S);
+    no.load(dout_b, static_cast<long long>(a.H) * DK, lo, S);
     if (threadIdx.x < kAT) {
-      const int q = q_lo + threadIdx.x;
-      Ls[threadIdx.x] = q < S ? a.lse[static_cast<long long>(bh) * S + q] : 0.f;
-      Ds[threadIdx.x] = q < S ? a.dvec[static_cast<long long>(bh) * S + q] : 0.f;
+      const int q = lo + threadIdx.x;
+      nl = q < S ? a.lse[static_cast<long long>(bh) * S + q] : 0.f;
+      nd = q < S ? a.dvec[static_cast<long long>(bh) * S + q] : 0.f;
+    }
+  };
+  fetch(k_lo);
+  for (int q_lo = k_lo; q_lo < S; q_lo += kAT) {
+    __syncthreads();  // every wave is done with the previous tile
+    nq.store(Qs);
+    no.store(Os);
+    if (threadIdx.x < kAT) {
+      Ls[threadIdx.x] = nl;
+      Ds[threadIdx.x] = nd;
     }
     __syncthreads();
+    if (q_lo + kAT < S) fetch(q_lo + kAT);
     floatx16 sc, dp;
 #pragma unroll
     for (int r = 0; r < 16; ++r) sc[r] = dp[r] = 0.f;
@@ -625,9 +664,9 @@ __global__ __launch_bounds__(256) void attn_bwd_dkdv_mfma(AttnBwdArgs a) {
     for (int r = 0; r < 16; ++r) {
       const int ql = 32 * wq + d_row(r, lane), q = q_lo + ql;
       float p = 0.f;
-      if (key <= q && q < S) p = expf(sc[r] / scale - Ls[ql]);
+      if (key <= q && q < S) p = expf(sc[r] * inv_scale - Ls[ql]);
       sc[r] = p;
-      dp[r] = p * (dp[r] - Ds[ql]) / scale;
+      dp[r] = p * (dp[r] - Ds[ql]) * inv_scale;
     }
     // dV[key][c] += Σ_q P[q][key]·dO[q][c];  dK[key][c] += Σ_q dS[q][key]·Q[q][c]
 #pragma unroll
@@ -696,11 +735,19 @@ __global__ __launch_bounds__(256) void attn_bwd_dq_mfma(AttnBwdArgs a) {
 #pragma unroll
     for (int r = 0; r < 16; ++r) dq[j][r] = 0.f;
   const int k_end = min(S, q_lo + kAT);
+  const float inv_scale = 1.0f / a.scale;
+  TileRegs<DK> nk, nv;
+  nk.load(a.k + hoff, DK, 0, S);
+  nv.load(a.v + hoff, DK, 0, S);
   for (int k_lo = 0; k_lo < k_end; k_lo += kAT) {
+    __syncthreads();  // every wave is done with the previous tile
+    nk.store(Ks);
+    nv.store(Vs);
     __syncthreads();
-    tile_rows<DK>(Ks, a.k + hoff, k_lo, S);
-    tile_rows<DK>(Vs, a.v + hoff, k_lo, S);
-    __syncthreads();
+    if (k_lo + kAT < k_end) {
+      nk.load(a.k + hoff, DK, k_lo + kAT, S);
+      nv.load(a.v + hoff, DK, k_lo + kAT, S);
+    }
     floatx16 sc, dp;
 #pragma unroll
     for (int r = 0; r < 16; ++r) sc[r] = dp[r] = 0.f;
@@ -717,8 +764,8 @@ __global__ __launch_bounds__(256) void attn_bwd_dq_mfma(AttnBwdArgs a) {
     for (int r = 0; r < 16; ++r) {
       const int kk = k_lo + 32 * wk + d_row(r, lane);
       float p = 0.f;
-      if (kk <= q && q < S) p = expf(sc[r] / a.scale - lse);
-      dp[r] = p * (dp[r] - dd) / a.scale;
+      if (kk <= q && q < S) p = expf(sc[r] * inv_scale - lse);
+      dp[r] = p * (dp[r] - dd) * inv_scale;
     }
     // dQ[q][c] += Σ_key dS[q][key]·K[key][c]
 #pragma unroll

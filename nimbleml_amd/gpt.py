@@ -248,8 +248,15 @@ class GPT(Module):
         N.check(fn(h, dids.ptr, dlab.ptr, b, s, int(ignore_index) if has_ign else 0,
                    int(has_ign), C.byref(loss)))
         # The reference wraps the loss in a compute-dtype Tensor (losses/cross_entropy.py:158-164).
-        out = Tensor([0.0], (), requires_grad=train)
+        wants_grad = any(p.requires_grad for p in self.parameters())
+        out = Tensor([0.0], (), requires_grad=wants_grad)
         out.data = np.asarray([loss.value], dtype=self._dtype)
+        if wants_grad and not train:
+            def _refuse():
+                raise RuntimeError("loss.backward() on the device needs a float32 model "
+                                   f"(this one computes in {self._dtype})")
+
+            out._backward = _refuse
         if train:
             dev = self._dev
 

@@ -185,3 +185,17 @@ def test_c_abi_backward_accumulates_and_matches_loss(gpu):
     assert not np.any(m._grad_array(N.P_W1, 1, (cfg.d_ff, cfg.d_model)))
     with pytest.raises(RuntimeError):
         N.check(N.lib.nml_model_grad_ptr(h, N.P_ROPE_COS, 0, C.byref(C.c_void_p())))
+
+
+def test_float16_backward_is_refused(gpu):
+    import nimbleml_amd as nm
+
+    cfg = GPTConfig(48, 32, 4, 1, 16)
+    w = make_weights(cfg, seed=26, dtype=np.float16)
+    m = nm.GPT.from_arrays(w, cfg.vocab_size, cfg.d_model, cfg.num_heads, cfg.num_layers,
+                           cfg.max_seq_len, dtype=np.float16)
+    ids = random_ids((1, 6), cfg.vocab_size, seed=14)
+    loss = m.compute_loss(ids, random_ids((6,), cfg.vocab_size, seed=15))
+    assert np.isfinite(loss.item())
+    with pytest.raises(RuntimeError, match="float32"):
+        loss.backward()
