@@ -131,6 +131,66 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(const T* __restrict__ x,
   }
 }
 
+// The same RMSNorm with one wave per row (4 rows per workgroup): each lane keeps its NV
+// 16-byte vectors of the row in registers between the sum of squares (DPP wave sum, no
+// LDS, no barrier) and the scaling, so the row is read once. Requires d ≤ NV·64 vectors.
+template <typename T, int NV>
+__global__ __launch_bounds__(256) void rmsnorm_wave_kernel(const T* __restrict__ x,
+                                                           const T* __restrict__ g,
+                                                           T* __restrict__ out, float* __restrict__ ms,
+                                                           float* __restrict__ rmsv, int rows, int d,
+                                                           float eps) {
+#pragma clang fp contract(off)
+  typedef float vf __attribute__((ext_vector_type(4)));
+  constexpr int E = 16 / sizeof(T);  // elements per vector
+  typedef T vec __attribute__((ext_vector_type(E)));
+  const int lane = threadIdx.x & 63;
+  const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= rows) return;  // whole waves
+  const int nvec = d / E;
+  const vec* xr = reinterpret_cast<const vec*>(x + static_cast<size_t>(row) * d);
+  vec xv[NV];
+  float acc = 0.f;
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    const int c = lane + 64 * i;
+    if (c < nvec) {
+      xv[i] = xr[c];
+#pragma unroll
+      for (int e = 0; e < E; ++e) {
+        const float v = static_cast<float>(xv[i][e]);
+        acc += rnd<T>(v * v);
+      }
+    }
+  }
+  const float m = wave_sum_dpp(acc) / static_cast<float>(d);
+  const float r = sqrtf(m + eps);
+  if (lane == 0) {
+    if (ms) ms[row] = m;
+    if (rmsv) rmsv[row] = r;
+  }
+  const vec* gv = reinterpret_cast<const vec*>(g);
+  vec* o = reinterpret_cast<vec*>(out + static_cast<size_t>(row) * d);
+  const float inv = rnd<T>(1.0f / r);
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    const int c = lane + 64 * i;
+    if (c < nvec) {
+      const vec gg = gv[c];
+      vec y;
+#pragma unroll
+      for (int e = 0; e < E; ++e) {
+        const float v = static_cast<float>(xv[i][e]);
+        if constexpr (sizeof(T) == 2)
+          y[e] = static_cast<T>(rnd<T>(v * inv) * static_cast<float>(gg[e]));
+        else
+          y[e] = static_cast<T>((v / r) * static_cast<float>(gg[e]));
+      }
+      o[c] = y;
+    }
+  }
+}
+
 // GELU with the reference's (out, tanh_u) outputs (native/src/gelu.cpp:12-21).
 template <typename T>
 __global__ __launch_bounds__(256) void gelu_kernel(const T* __restrict__ x, T* __restrict__ out,
@@ -214,6 +274,29 @@ int launch_embed_decode(int dt, const int64_t* tokens, long long tok_stride, con
 int launch_rmsnorm(int dt, const void* x, const void* g, void* out, float* ms, float* rms,
                    int rows, int d, float eps, hipStream_t st) {
   if (rows == 0) return 0;
+  const int E = dt == F16 ? 8 : 4;
+  const bool vec_ok = d % E == 0 && ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(g) |
+                                      reinterpret_cast<uintptr_t>(out)) & 15) == 0;
+  const int nv = (d / E + 63) / 64;
+  if (vec_ok && nv <= 8) {
+    const int blocks = (rows + 3) / 4;
+#define NML_RMS_WAVE(T, NVV) \
+  rmsnorm_wave_kernel<T, NVV><<<blocks, 256, 0, st>>>((const T*)x, (const T*)g, (T*)out, ms, rms, rows, d, eps)
+    if (dt == F16) {
+      if (nv <= 1) NML_RMS_WAVE(half_t, 1);
+      else if (nv <= 2) NML_RMS_WAVE(half_t, 2);
+      else if (nv <= 4) NML_RMS_WAVE(half_t, 4);
+      else NML_RMS_WAVE(half_t, 8);
+    } else {
+      if (nv <= 1) NML_RMS_WAVE(float, 1);
+      else if (nv <= 2) NML_RMS_WAVE(float, 2);
+      else if (nv <= 4) NML_RMS_WAVE(float, 4);
+      else NML_RMS_WAVE(float, 8);
+    }
+#undef NML_RMS_WAVE
+    NML_LAUNCHED();
+    return 0;
+  }
   if (dt == F16)
     rmsnorm_kernel<half_t><<<rows, 256, 0, st>>>((const half_t*)x, (const half_t*)g,
                                                  (half_t*)out, ms, rms, d, eps);
