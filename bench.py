@@ -165,9 +165,10 @@ MFMA_F32_PEAK_TFLOPS = 157.3
 
 
 def bench_train(nm, batch=4, seq=1024, steps=3):
-    """One training step of the C3 architecture in float32: compute_loss keeping the
-    activations (nml_model_loss_train) and loss.backward() into the device gradients
-    (nml_model_backward), batch × seq tokens. Algorithmic flops: 3× the forward's
+    """One training step of the C3 architecture in float32: zero_grad, compute_loss keeping
+    the activations (nml_model_loss_train), loss.backward() into the device gradients
+    (nml_model_backward) and AdamW over every parameter (nml_model_adamw_step), batch × seq
+    tokens. Algorithmic flops: 3× the forward's
     (GEMMs 2·rows·12·d²·L + head 2·rows·d·V, attention 4·d·S(S+1)/2 per sequence and
     layer), i.e. without the backward's recomputation of the logits and scores."""
     import ctypes as C
@@ -184,11 +185,16 @@ def bench_train(nm, batch=4, seq=1024, steps=3):
     ids = N.DeviceArray.from_host(random_ids((batch, seq), cfg.vocab_size, seed=3))
     lab = N.DeviceArray.from_host(random_ids((batch * seq,), cfg.vocab_size, seed=4))
     loss = C.c_double()
-    N.check(N.lib.nml_model_zero_grad(h))
+    t_step = [0]
 
     def step():
+        t_step[0] += 1
+        t = t_step[0]
+        N.check(N.lib.nml_model_zero_grad(h))
         N.check(N.lib.nml_model_loss_train(h, ids.ptr, lab.ptr, batch, seq, 0, 0, C.byref(loss)))
         N.check(N.lib.nml_model_backward(h, 1.0))
+        N.check(N.lib.nml_model_adamw_step(h, 1e-4, 0.9, 0.999, 1 - 0.9 ** t, 1 - 0.999 ** t,
+                                           1e-8, 0.01))
 
     step()  # warm-up (allocates the saved activations)
     t = N.Timer()
@@ -200,7 +206,7 @@ def bench_train(nm, batch=4, seq=1024, steps=3):
     fwd = 2 * R * L * 12 * d * d + L * batch * 4 * d * seq * (seq + 1) / 2 + 2 * R * d * V
     tf = 3 * fwd / (ms * 1e-3) / 1e12
     return {"workload": f"train step: GPT V32000 d1024 H16 L24 float32, batch {batch} x {seq}, "
-                        "compute_loss + backward on the device",
+                        "zero_grad + compute_loss + backward + AdamW on the device",
             "value": round(R / (ms * 1e-3), 1), "unit": "tokens/s", "ms_per_step": round(ms, 3),
             "loss": round(loss.value, 5),
             "roofline": {"bound": "mfma", "achieved": round(tf, 1), "peak": MFMA_F32_PEAK_TFLOPS,

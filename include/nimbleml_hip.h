@@ -186,6 +186,18 @@ int nml_model_loss_train(nml_model* m, const int64_t* ids, const int64_t* labels
  * output.grad). Returns after the device finishes. */
 int nml_model_backward(nml_model* m, double grad_scale);
 
+/* AdamW.step() over every parameter of the model (optimizers/adam.py:85-128 with the
+ * native float32 update of adamw_step, native/src/adamw.cpp:6-20, in its operation order):
+ * the device parameters are updated in place from the gradient arena, with first and second
+ * moments kept on the device (zero before the first call). bias_corr1/2 = 1 − β^t as the
+ * caller's step count gives them (adam.py:91-93). Every parameter takes weight_decay (one
+ * parameter group); the rotary tables are buffers and are left alone. */
+int nml_model_adamw_step(nml_model* m, float lr, float beta1, float beta2, float bias_corr1,
+                         float bias_corr2, float eps, float weight_decay);
+/* Device pointers of the AdamW moments of parameter (kind, layer) (the optimizer's m[i],
+ * v[i], adam.py:64-83), for checkpoints and tests. */
+int nml_model_adam_moments(nml_model* m, int kind, int layer, void** first, void** second);
+
 /* KV cache for batch rows: K and V per layer, (batch, heads, max_seq, head_dim) each.
  * The seam generate() probes for (models/generate.py:93-100). */
 int nml_cache_create(nml_model* m, size_t batch, nml_cache** out);

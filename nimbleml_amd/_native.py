@@ -70,6 +70,8 @@ _SIGS = {
     "nml_model_grad_ptr": [vp, i32, i32, C.POINTER(C.c_void_p)],
     "nml_model_loss_train": [vp, vp, vp, sz, sz, i64, i32, C.POINTER(C.c_double)],
     "nml_model_backward": [vp, C.c_double],
+    "nml_model_adamw_step": [vp, f32, f32, f32, f32, f32, f32, f32],
+    "nml_model_adam_moments": [vp, i32, i32, C.POINTER(C.c_void_p), C.POINTER(C.c_void_p)],
     "nml_cache_create": [vp, sz, C.POINTER(vp)],
     "nml_cache_destroy": [vp],
     "nml_cache_length": [vp, C.POINTER(sz)],

@@ -212,6 +212,12 @@ int launch_rope_backward(float* dqkv, int rows, int S, int H, int dk, const floa
 int launch_embed_backward(const float* g, const int64_t* ids, float* demb, float* dpos, int B,
                           int S, int d, int V, hipStream_t st);
 
+// AdamW over n float32 elements in place (native/src/adamw.cpp:6-20 operation order);
+// buffers 16-byte aligned.
+int launch_adamw(float* p, const float* g, float* m, float* v, size_t n, float lr, float beta1,
+                 float beta2, float bias1, float bias2, float eps, float weight_decay,
+                 hipStream_t st);
+
 // Persistent decode step (batch 1): one launch of kPersistGroups workgroups runs the
 // whole token; see decode_persist.hip.
 constexpr int kPersistGroups = 256;

@@ -28,6 +28,7 @@ namespace nml {
 
 struct TrainState {
   Buf grads;    // float32, same layout and size as the parameter arena
+  Buf moments;  // AdamW first and second moments, two more arenas of that layout
   Buf acts;     // saved activations of the last loss_train
   Buf scratch;  // backward scratch
   Buf io;       // ids and labels of the last loss_train, loss accumulators
@@ -41,6 +42,7 @@ struct TrainState {
 void train_release(nml_model* m) {
   if (!m->train) return;
   m->train->grads.release();
+  m->train->moments.release();
   m->train->acts.release();
   m->train->scratch.release();
   m->train->io.release();
@@ -365,6 +367,48 @@ int nml_model_backward(nml_model* m, double grad_scale) {
   NML_TRY(launch_embed_backward(G, dids, dE, rope_on(m) ? nullptr : grad_of(m, m->pos), B, S, d, V,
                                 st));
   NML_HIP(hipStreamSynchronize(st));
+  return 0;
+}
+
+int nml_model_adamw_step(nml_model* m, float lr, float beta1, float beta2, float bias_corr1,
+                         float bias_corr2, float eps, float weight_decay) {
+  NML_TRY(check_ready(m));
+  NML_TRY(ensure_train(m));
+  TrainState* t = m->train;
+  const size_t bytes = m->arena_bytes;
+  if (!t->moments.p) {
+    NML_TRY(t->moments.ensure(2 * bytes));
+    NML_HIP(hipMemsetAsync(t->moments.p, 0, 2 * bytes, nml::stream()));
+  }
+  // Every parameter, as two ranges of the arena around the rotary tables (buffers, not
+  // parameters). Alignment gaps between parameters carry zero gradients and moments.
+  char* base = static_cast<char*>(m->arena);
+  const size_t rope_lo = static_cast<char*>(m->rope_cos) - base;
+  const size_t rope_hi = static_cast<char*>(m->rope_sin) - base +
+                         align256(param_elems(m, NML_P_ROPE_SIN) * m->es);
+  const size_t ranges[2][2] = {{0, rope_lo}, {rope_hi, bytes}};
+  char* g = static_cast<char*>(t->grads.p);
+  char* mm = static_cast<char*>(t->moments.p);
+  for (const auto& r : ranges) {
+    if (r[1] <= r[0]) continue;
+    NML_TRY(launch_adamw(reinterpret_cast<float*>(base + r[0]), reinterpret_cast<float*>(g + r[0]),
+                         reinterpret_cast<float*>(mm + r[0]),
+                         reinterpret_cast<float*>(mm + bytes + r[0]), (r[1] - r[0]) / 4, lr, beta1,
+                         beta2, bias_corr1, bias_corr2, eps, weight_decay, nml::stream()));
+  }
+  return 0;
+}
+
+int nml_model_adam_moments(nml_model* m, int kind, int layer, void** first, void** second) {
+  NML_TRY(check_ready(m));
+  NML_REQUIRE(kind != NML_P_ROPE_COS && kind != NML_P_ROPE_SIN,
+              "rotary tables are buffers, not parameters: no optimizer state");
+  void** slot = param_slot(m, kind, layer);
+  NML_REQUIRE(slot != nullptr, "unknown parameter kind %d / layer %d", kind, layer);
+  NML_REQUIRE(m->train && m->train->moments.p, "no optimizer state yet (call nml_model_adamw_step)");
+  const size_t off = static_cast<char*>(*slot) - static_cast<char*>(m->arena);
+  *first = static_cast<char*>(m->train->moments.p) + off;
+  *second = static_cast<char*>(m->train->moments.p) + m->arena_bytes + off;
   return 0;
 }
 

@@ -199,3 +199,96 @@ def test_float16_backward_is_refused(gpu):
     assert np.isfinite(loss.item())
     with pytest.raises(RuntimeError, match="float32"):
         loss.backward()
+
+
+def _dev(N, ptr, shape):
+    out = np.empty(shape, np.float32)
+    N.check(N.lib.nml_memcpy_d2h(out.ctypes.data, ptr, out.nbytes))
+    return out
+
+
+def _param_slots(cfg, rope):
+    from nimbleml_amd import _native as N
+
+    d, f = cfg.d_model, cfg.d_ff
+    slots = [(N.P_TOKEN_EMB, 0, (cfg.vocab_size, d)), (N.P_LN_F, 0, (d,))]
+    if not rope:
+        slots.append((N.P_POS_EMB, 0, (cfg.max_seq_len, d)))
+    for i in range(cfg.num_layers):
+        slots += [(N.P_LN1, i, (d,)), (N.P_WQKV, i, (3 * d, d)), (N.P_BQKV, i, (3 * d,)),
+                  (N.P_WO, i, (d, d)), (N.P_BO, i, (d,)), (N.P_LN2, i, (d,)),
+                  (N.P_W1, i, (f, d)), (N.P_B1, i, (f,)), (N.P_W2, i, (d, f)), (N.P_B2, i, (d,))]
+    return slots
+
+
+@pytest.mark.parametrize("rope", [False, True])
+def test_model_adamw_step_bit_exact(gpu, rope):
+    """nml_model_adamw_step over the gradient arena equals the reference's float32
+    adamw_step (oracle/optim_ref.py, pinned bit for bit to the compiled reference) applied
+    to every parameter with the device's own gradients, over two steps; the rotary tables
+    are not touched."""
+    from nimbleml_amd import _native as N
+    from oracle.optim_ref import adamw_step
+
+    cfg = GPTConfig(256, 64, 4, 2, 64)
+    m, _ = _model(cfg, seed=27, rope=rope)
+    h = m._device_model()
+    ids = N.DeviceArray.from_host(random_ids((2, 24), cfg.vocab_size, seed=16))
+    lab = N.DeviceArray.from_host(random_ids((48,), cfg.vocab_size, seed=17))
+    slots = _param_slots(cfg, rope)
+
+    def ptr(fn, kind, layer):
+        p = C.c_void_p()
+        N.check(fn(h, kind, layer, C.byref(p)))
+        return p
+
+    if rope:
+        cos0 = _dev(N, ptr(N.lib.nml_model_param_ptr, N.P_ROPE_COS, 0), (cfg.max_seq_len, 8))
+    params = {(k, l): _dev(N, ptr(N.lib.nml_model_param_ptr, k, l), s) for k, l, s in slots}
+    mom = {key: (np.zeros_like(p), np.zeros_like(p)) for key, p in params.items()}
+    lr, b1, b2, eps, wd = 1e-3, 0.9, 0.999, 1e-8, 0.01
+    for t in (1, 2):
+        loss = C.c_double()
+        N.check(N.lib.nml_model_zero_grad(h))
+        N.check(N.lib.nml_model_loss_train(h, ids.ptr, lab.ptr, 2, 24, 0, 0, C.byref(loss)))
+        N.check(N.lib.nml_model_backward(h, 1.0))
+        bc1, bc2 = 1.0 - b1 ** t, 1.0 - b2 ** t
+        for k, l, s in slots:
+            g = _dev(N, ptr(N.lib.nml_model_grad_ptr, k, l), s)
+            adamw_step(params[(k, l)], g, *mom[(k, l)], lr, b1, b2, bc1, bc2, eps, wd)
+        N.check(N.lib.nml_model_adamw_step(h, lr, b1, b2, bc1, bc2, eps, wd))
+        for k, l, s in slots:
+            got = _dev(N, ptr(N.lib.nml_model_param_ptr, k, l), s)
+            assert np.array_equal(got, params[(k, l)]), (t, k, l)
+            m1, m2 = C.c_void_p(), C.c_void_p()
+            N.check(N.lib.nml_model_adam_moments(h, k, l, C.byref(m1), C.byref(m2)))
+            assert np.array_equal(_dev(N, m1, s), mom[(k, l)][0]), (t, k, l)
+            assert np.array_equal(_dev(N, m2, s), mom[(k, l)][1]), (t, k, l)
+    if rope:
+        assert np.array_equal(_dev(N, ptr(N.lib.nml_model_param_ptr, N.P_ROPE_COS, 0),
+                                   (cfg.max_seq_len, 8)), cos0)
+
+
+def test_device_training_loop_lowers_the_loss(gpu):
+    """compute_loss → backward → AdamW on the device for a few steps on one batch: the
+    first loss equals the oracle's, and every step lowers the loss."""
+    from nimbleml_amd import _native as N
+
+    cfg = GPTConfig(256, 64, 4, 2, 64)
+    m, w = _model(cfg, seed=28)
+    h = m._device_model()
+    ids_h = random_ids((2, 32), cfg.vocab_size, seed=18)
+    lab_h = random_ids((64,), cfg.vocab_size, seed=19)
+    ids, lab = N.DeviceArray.from_host(ids_h), N.DeviceArray.from_host(lab_h)
+    losses = []
+    for t in range(1, 7):
+        loss = C.c_double()
+        N.check(N.lib.nml_model_zero_grad(h))
+        N.check(N.lib.nml_model_loss_train(h, ids.ptr, lab.ptr, 2, 32, 0, 0, C.byref(loss)))
+        N.check(N.lib.nml_model_backward(h, 1.0))
+        N.check(N.lib.nml_model_adamw_step(h, 3e-3, 0.9, 0.999, 1 - 0.9 ** t, 1 - 0.999 ** t,
+                                           1e-8, 0.0))
+        losses.append(loss.value)
+    want0, _ = _oracle(w, cfg, ids_h, lab_h)
+    assert abs(losses[0] - want0) <= 1e-5 * want0
+    assert all(b < a for a, b in zip(losses, losses[1:])), losses
