@@ -281,6 +281,72 @@ __global__ __launch_bounds__(256) void rmsnorm_bwd_kernel(const float* __restric
   }
 }
 
+// The same with one wave per 16 rows (4 waves per workgroup): a lane keeps NV 16-byte
+// vectors of the row, the row sums are DPP wave sums (no LDS, no barrier), and the wave's
+// Σ dy·(x/rms) per column goes to part[wave].
+template <int NV>
+__global__ __launch_bounds__(256) void rmsnorm_bwd_wave_kernel(const float* __restrict__ dy,
+                                                               const float* __restrict__ x,
+                                                               const float* __restrict__ gam,
+                                                               float* __restrict__ dx, int acc,
+                                                               float* __restrict__ part, int rows,
+                                                               int d, float eps) {
+#pragma clang fp contract(off)
+  const int lane = threadIdx.x & 63;
+  const int wv = blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int r0 = wv * kNormRowsPerBlock;
+  if (r0 >= rows) return;  // whole waves
+  const int nvec = d / 4, r1 = min(rows, r0 + kNormRowsPerBlock);
+  floatx4 gv[NV], ga[NV];
+  const floatx4 z = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    const int c = lane + 64 * i;
+    gv[i] = c < nvec ? reinterpret_cast<const floatx4*>(gam)[c] : z;
+    ga[i] = z;
+  }
+  for (int r = r0; r < r1; ++r) {
+    const floatx4* xr = reinterpret_cast<const floatx4*>(x + static_cast<long long>(r) * d);
+    const floatx4* gr = reinterpret_cast<const floatx4*>(dy + static_cast<long long>(r) * d);
+    floatx4 xv[NV], dv[NV];
+    float ssq = 0.f, dot = 0.f;
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+      const int c = lane + 64 * i;
+      xv[i] = c < nvec ? xr[c] : z;
+      dv[i] = c < nvec ? gr[c] : z;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        ssq += xv[i][e] * xv[i][e];
+        dot += (dv[i][e] * gv[i][e]) * xv[i][e];
+      }
+    }
+    const float ms = wave_sum_dpp(ssq) / static_cast<float>(d);
+    const float rdot = wave_sum_dpp(dot);
+    const float rms = sqrtf(ms + eps);
+    const float coef = (2.0f / static_cast<float>(d)) * (rdot * -0.5f / ((ms + eps) * rms));
+    floatx4* o = reinterpret_cast<floatx4*>(dx + static_cast<long long>(r) * d);
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+      const int c = lane + 64 * i;
+      if (c < nvec) {
+        floatx4 v = acc ? o[c] : z;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          v[e] += (dv[i][e] * gv[i][e]) / rms + xv[i][e] * coef;
+          ga[i][e] += dv[i][e] * (xv[i][e] / rms);
+        }
+        o[c] = v;
+      }
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    const int c = lane + 64 * i;
+    if (c < nvec) reinterpret_cast<floatx4*>(part + static_cast<long long>(wv) * d)[c] = ga[i];
+  }
+}
+
 // out[c] += Σ_p part[p·n + c]: 32 columns per block, 8 thread rows each summing every
 // 8th part, then the 8 row sums in order (a fixed order: deterministic).
 __global__ __launch_bounds__(256) void parts_reduce_kernel(const float* __restrict__ part,
@@ -899,6 +965,24 @@ int launch_rmsnorm_bwd(const float* dy, const float* x, const float* gamma, floa
   if (rows == 0) return 0;
   NML_REQUIRE(d > 0 && d <= 256 * 32, "rmsnorm backward: d=%d outside (0, 8192]", d);
   const int blocks = rmsnorm_bwd_parts(rows);
+  const int nv = (d / 4 + 63) / 64;
+  const bool vec_ok = d % 4 == 0 && ((reinterpret_cast<uintptr_t>(dy) | reinterpret_cast<uintptr_t>(x) |
+                                      reinterpret_cast<uintptr_t>(gamma) |
+                                      reinterpret_cast<uintptr_t>(dx)) & 15) == 0;
+  if (vec_ok && nv <= 8) {
+    const int wblocks = (blocks + 3) / 4;
+#define NML_NORM_BWD_W(NVV) \
+  rmsnorm_bwd_wave_kernel<NVV><<<wblocks, 256, 0, st>>>(dy, x, gamma, dx, acc, part, rows, d, eps)
+    if (nv <= 1) NML_NORM_BWD_W(1);
+    else if (nv <= 2) NML_NORM_BWD_W(2);
+    else if (nv <= 4) NML_NORM_BWD_W(4);
+    else NML_NORM_BWD_W(8);
+#undef NML_NORM_BWD_W
+    NML_LAUNCHED();
+    parts_reduce_kernel<<<(d + 31) / 32, 256, 0, st>>>(part, blocks, d, dgamma);
+    NML_LAUNCHED();
+    return 0;
+  }
   const int nc = (d + 255) / 256;
 #define NML_NORM_BWD(NCV) \
   rmsnorm_bwd_kernel<NCV><<<blocks, 256, 0, st>>>(dy, x, gamma, dx, acc, part, rows, d, eps)

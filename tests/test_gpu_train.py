@@ -292,3 +292,26 @@ def test_device_training_loop_lowers_the_loss(gpu):
     want0, _ = _oracle(w, cfg, ids_h, lab_h)
     assert abs(losses[0] - want0) <= 1e-5 * want0
     assert all(b < a for a, b in zip(losses, losses[1:])), losses
+
+
+@pytest.mark.parametrize("flags", [{"fused_trunk": True}, {"gradient_checkpointing": True}])
+def test_backward_with_trunk_flags(gpu, flags):
+    """fused_trunk (the final RMSNorm inside the trunk module) and gradient_checkpointing
+    (a memory/recompute trade in the reference, same gradients) give the oracle's gradients
+    under the same parameter names."""
+    import nimbleml_amd as nm
+
+    cfg = GPTConfig(256, 64, 4, 2, 64)
+    w = make_weights(cfg, seed=29, dtype=np.float32, rich=True)
+    arrays = w
+    if flags.get("fused_trunk"):  # FusedGPTTrunk's checkpoint names (blocks.blocks.i, blocks.ln)
+        arrays = {k.replace("blocks.layers.", "blocks.blocks."): v for k, v in w.items()}
+        arrays["blocks.ln.gamma"] = w["ln.gamma"]  # the same RMSNorm under both names
+    m = nm.GPT.from_arrays(arrays, cfg.vocab_size, cfg.d_model, cfg.num_heads, cfg.num_layers,
+                           cfg.max_seq_len, dtype=np.float32, **flags)
+    ids = random_ids((2, 20), cfg.vocab_size, seed=20)
+    labels = random_ids((40,), cfg.vocab_size, seed=21)
+    m.compute_loss(ids, labels).backward()
+    _, want = _oracle(w, cfg, ids, labels)
+    _compare(_named_grads(m), want)
+    assert all(p.grad is not None for p in m.parameters())
