@@ -164,7 +164,7 @@ def bench_adamw(nm, n=337_100_000, steps=20):
 MFMA_F32_PEAK_TFLOPS = 157.3
 
 
-def bench_train(nm, batch=4, seq=1024, steps=3):
+def bench_train(nm, batch=4, seq=1024, steps=3, dtype=np.float32):
     """One training step of the C3 architecture in float32: zero_grad, compute_loss keeping
     the activations (nml_model_loss_train), loss.backward() into the device gradients
     (nml_model_backward) and AdamW over every parameter (nml_model_adamw_step), batch × seq
@@ -177,9 +177,9 @@ def bench_train(nm, batch=4, seq=1024, steps=3):
 
     N = nm._native
     cfg = C3
-    w = make_weights(cfg, seed=11, dtype=np.float32)
+    w = make_weights(cfg, seed=11, dtype=dtype)
     model = nm.GPT.from_arrays(w, cfg.vocab_size, cfg.d_model, cfg.num_heads, cfg.num_layers,
-                               cfg.max_seq_len, dtype=np.float32)
+                               cfg.max_seq_len, dtype=dtype)
     del w
     h = model._device_model()
     ids = N.DeviceArray.from_host(random_ids((batch, seq), cfg.vocab_size, seed=3))
@@ -205,7 +205,8 @@ def bench_train(nm, batch=4, seq=1024, steps=3):
     d, L, V, R = cfg.d_model, cfg.num_layers, cfg.vocab_size, batch * seq
     fwd = 2 * R * L * 12 * d * d + L * batch * 4 * d * seq * (seq + 1) / 2 + 2 * R * d * V
     tf = 3 * fwd / (ms * 1e-3) / 1e12
-    return {"workload": f"train step: GPT V32000 d1024 H16 L24 float32, batch {batch} x {seq}, "
+    name = "float32" if dtype == np.float32 else "float16 (float32 gradients and masters)"
+    return {"workload": f"train step: GPT V32000 d1024 H16 L24 {name}, batch {batch} x {seq}, "
                         "zero_grad + compute_loss + backward + AdamW on the device",
             "value": round(R / (ms * 1e-3), 1), "unit": "tokens/s", "ms_per_step": round(ms, 3),
             "loss": round(loss.value, 5),
@@ -225,11 +226,14 @@ def bench_c5(nm, reps=2):
     model.to_device()
     ids = random_ids((4, 4096), cfg.vocab_size, seed=1)
     lab = random_ids((4, 4096), cfg.vocab_size, seed=2)
-    model.compute_loss(ids, lab)  # warm-up
-    t0 = time.perf_counter()
-    for _ in range(reps):
-        loss = model.compute_loss(ids, lab).item()
-    dt = (time.perf_counter() - t0) / reps
+    from nimbleml_amd.grad_mode import no_grad
+
+    with no_grad():  # the loss alone: no activations kept for a backward
+        model.compute_loss(ids, lab)  # warm-up
+        t0 = time.perf_counter()
+        for _ in range(reps):
+            loss = model.compute_loss(ids, lab).item()
+        dt = (time.perf_counter() - t0) / reps
     d, L, V, B, S = cfg.d_model, cfg.num_layers, cfg.vocab_size, 4, 4096
     flops = 2 * B * S * L * 12 * d * d + L * B * 4 * d * S * (S + 1) / 2 + 2 * B * S * d * V
     tf = flops / dt / 1e12
@@ -252,7 +256,7 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-graph", action="store_true")
     ap.add_argument("--only-c3", action="store_true", help="skip the batch-32 and prefill lines")
-    ap.add_argument("--only", choices=["c3", "c4", "c5", "adamw", "train"], default=None,
+    ap.add_argument("--only", choices=["c3", "c4", "c5", "adamw", "train", "train16"], default=None,
                     help="run one workload only (for profiling); c4/c5 print their own line")
     ap.add_argument("--cpu-tokens", type=int, default=12)
     ap.add_argument("--copy-calibration", action="store_true",
@@ -288,6 +292,9 @@ def main():
         return
     if args.only == "train":
         print(json.dumps({"train": bench_train(nm)}), flush=True)
+        return
+    if args.only == "train16":
+        print(json.dumps({"train16": bench_train(nm, dtype=np.float16)}), flush=True)
         return
     w16 = make_weights(cfg, seed=1234, dtype=np.float16)
     model = nm.GPT.from_arrays(w16, cfg.vocab_size, cfg.d_model, cfg.num_heads, cfg.num_layers,

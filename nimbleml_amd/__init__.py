@@ -9,6 +9,7 @@ include/nimbleml_hip.h. Importing requires the built library
 from nimbleml_amd import np_backend
 from nimbleml_amd._native import DeviceArray
 from nimbleml_amd.generate import generate
+from nimbleml_amd.grad_mode import enable_grad, is_grad_enabled, no_grad
 from nimbleml_amd.gpt import GPT, KVCache
 from nimbleml_amd.layers import (Dense, Embedding, FeedForward, FusedGPTTrunk,
                                  FusedTransformerBlock, Module, MultiHeadAttention, RMSNorm,
@@ -21,5 +22,5 @@ __all__ = [
     "GPT", "KVCache", "generate", "Tensor", "DeviceArray", "Dense", "Embedding", "RMSNorm",
     "MultiHeadAttention", "FeedForward", "FusedTransformerBlock", "FusedGPTTrunk", "Module",
     "Sequential", "save", "load", "load_arrays", "named_parameters", "device", "using_gpu",
-    "set_device", "set_dtype", "np_backend",
+    "set_device", "set_dtype", "np_backend", "no_grad", "enable_grad", "is_grad_enabled",
 ]

@@ -151,66 +151,72 @@ struct SampleArgs {
 };
 int launch_sample(int dt, const SampleArgs& a, hipStream_t st);
 
-// ------------------------------------------------------------ training (float32)
-// General GEMM of the backward pass: C(m, n) = Σ_k A(m, k)·B(n, k) over fp32 operands,
-// A(m, k) = a[m·lda + k] when a_kc (k contiguous) else a[k·lda + m]; B(n, k) likewise
-// with b, ldb, b_kc. C is row-major at ldc. Output modes: set, add (gradient
-// accumulation), or set to C·gelu'(aux(m, n)) (the GELU backward, aux = pre-activation
-// at ldaux).
+// ------------------------------------------------------------ training
+// Every launch takes the model's storage type dt (F32 or F16) for the activation-side
+// tensors; parameter gradients, partial sums and the softmax statistics are float32.
+//
+// General GEMM of the backward pass: C(m, n) = Σ_k A(m, k)·B(n, k), A(m, k) = a[m·lda + k]
+// when a_kc (k contiguous) else a[k·lda + m]; B(n, k) likewise with b, ldb, b_kc; operands
+// of type dt, fp32 products and sums. C is row-major at ldc: GB_SET stores dt, GB_ADD adds
+// fp32(dt(acc)) to an fp32 C (gradient accumulation), GB_GELU stores dt(dt(acc)·gelu'(aux))
+// with aux the pre-activation (dt) at ldaux.
 struct GemmBwdArgs {
-  const float* a;
+  const void* a;
   long long lda;
-  const float* b;
+  const void* b;
   long long ldb;
-  float* c;
+  void* c;
   long long ldc;
-  const float* aux;
+  const void* aux;
   long long ldaux;
   int M, N, K;
 };
 enum GemmBwdOut : int { GB_SET = 0, GB_ADD = 1, GB_GELU = 2 };
-int launch_gemm_bwd(const GemmBwdArgs& g, bool a_kc, bool b_kc, int out, hipStream_t st);
+int launch_gemm_bwd(int dt, const GemmBwdArgs& g, bool a_kc, bool b_kc, int out, hipStream_t st);
 
-// RMSNorm backward over rows × d (kernels/fused_rmsnorm.py:208-217): dx = result, or
-// dx += result when acc; dgamma += Σ_rows dy·x/rms. part: scratch of
+// RMSNorm backward over rows × d (kernels/fused_rmsnorm.py:195-217): dx = result, or
+// dx += result when acc; dgamma (fp32) += Σ_rows dy·x̂. part: scratch of
 // rmsnorm_bwd_parts(rows) · d floats.
 int rmsnorm_bwd_parts(int rows);
-int launch_rmsnorm_bwd(const float* dy, const float* x, const float* gamma, float* dx, int acc,
+int launch_rmsnorm_bwd(int dt, const void* dy, const void* x, const void* gamma, void* dx, int acc,
                        float* dgamma, float* part, int rows, int d, float eps, hipStream_t st);
-// out[n] += Σ_rows a[r·lda + n] (bias gradients); part: colsum_parts(rows) · n floats.
+// out[n] (fp32) += Σ_rows a[r·lda + n] (bias gradients); part: colsum_parts(rows) · n floats.
 int colsum_parts(int rows);
-int launch_colsum(const float* a, long long lda, int rows, int n, float* out, float* part,
+int launch_colsum(int dt, const void* a, long long lda, int rows, int n, float* out, float* part,
                   hipStream_t st);
 // In place: logits rows → (softmax − onehot(label))·scale, ignored rows → 0
 // (kernels/fused_crossentropy.py:33-50).
-int launch_ce_grad(float* logits, int rows, int V, const int64_t* labels, long long ignore_index,
-                   int has_ignore, float scale, hipStream_t st);
+int launch_ce_grad(int dt, void* logits, int rows, int V, const int64_t* labels,
+                   long long ignore_index, int has_ignore, float scale, hipStream_t st);
 
 // Causal attention backward for one layer (kernels/fused_sdpa.py:26-29, :81-88). q, k, v
 // head-major (B, H, S, dk) as the forward saw them (after RoPE); o and dout merged-head
-// (B·S, H·dk); lse from the forward; dvec scratch (B, H, S). Writes dq, dk, dv into
-// dqkv (B·S, 3·H·dk) at column offsets 0, H·dk, 2·H·dk.
+// (B·S, H·dk); lse from the forward; dvec scratch (B, H, S) floats. Writes dq, dk, dv
+// into dqkv (B·S, 3·H·dk) at column offsets 0, H·dk, 2·H·dk (all of type dt).
 struct AttnBwdArgs {
-  const float* q;
-  const float* k;
-  const float* v;
-  const float* o;
-  const float* dout;
+  const void* q;
+  const void* k;
+  const void* v;
+  const void* o;
+  const void* dout;
   const float* lse;
   float* dvec;
-  float* dqkv;
+  void* dqkv;
   int B, H, S, dk;
   float scale;  // sqrt(dk), the divisor of the scores
 };
-int launch_attention_backward(const AttnBwdArgs& a, hipStream_t st);
+int launch_attention_backward(int dt, const AttnBwdArgs& a, hipStream_t st);
 // RoPE backward on dqkv rows (the dq and dk parts): pair (i, i + dk/2) of row b·S + s
-// rotated by −θ at position s (cos/sin: (max_len, dk/2)).
-int launch_rope_backward(float* dqkv, int rows, int S, int H, int dk, const float* cos,
-                         const float* sin, hipStream_t st);
+// rotated by −θ at position s (cos/sin: (max_len, dk/2) of type dt).
+int launch_rope_backward(int dt, void* dqkv, int rows, int S, int H, int dk, const void* cos,
+                         const void* sin, hipStream_t st);
 // Embedding backward: dE[ids[r]] += g[r] (token rows), dpos[s] += Σ_b g[b·S + s]
-// (dpos null: none).
-int launch_embed_backward(const float* g, const int64_t* ids, float* demb, float* dpos, int B,
+// (dpos null: none); g of type dt, dE and dpos fp32.
+int launch_embed_backward(int dt, const void* g, const int64_t* ids, float* demb, float* dpos, int B,
                           int S, int d, int V, hipStream_t st);
+
+// Elementwise dtype conversion (F16 → F32 or F32 → F16, round to nearest even).
+int launch_convert(int src_dt, const void* src, int dst_dt, void* dst, size_t n, hipStream_t st);
 
 // AdamW over n float32 elements in place (native/src/adamw.cpp:6-20 operation order);
 // buffers 16-byte aligned.

@@ -590,6 +590,7 @@ __global__ __launch_bounds__(256, 2) void attn_prefill_mfma_kernel(AttnArgs a) {
     m = mx;
   }
   l += __shfl_xor(l, 32, 64);
+  if (myq < S && a.lse && hi == 0) a.lse[static_cast<size_t>(bh) * a.S + myq] = m + logf(l);
   if (myq < S) {
     const float inv = 1.f / l;
     const int hd = a.H * DK;
@@ -760,7 +761,6 @@ int prefill_typed(const AttnArgs& a, hipStream_t st) {
     if (!std::getenv("NIMBLEML_ATTN_F32_SCALAR")) return prefill_f32_mfma<DK>(a, st);
   }
   if constexpr (sizeof(T) == 2 && (DK == 64 || DK == 128)) {
-    NML_REQUIRE(a.lse == nullptr, "attention: the log-sum-exp output needs a float32 model");
     dim3 grid((a.S + kFQ - 1) / kFQ, a.B * a.H);
     attn_prefill_mfma_kernel<DK><<<grid, 256, 0, st>>>(a);
     NML_LAUNCHED();

@@ -1,7 +1,11 @@
-// Backward of compute_loss on the device (float32 models): the GEMM of the backward's
-// transposed products, and the backward of RMSNorm, GELU (fused into a GEMM epilogue),
-// the cross-entropy, causal attention, RoPE and the embeddings, plus the column sums
-// behind the bias and gain gradients.
+// Backward of compute_loss on the device: the GEMM of the backward's transposed products,
+// and the backward of RMSNorm, GELU (fused into a GEMM epilogue), the cross-entropy, causal
+// attention, RoPE and the embeddings, plus the column sums behind the bias and gain
+// gradients. Every kernel takes the model's storage type T (float or fp16): fp16 operands
+// are widened to fp32 on load (products of fp16 values are exact in fp32, as in NumPy's
+// fp16 matmul with fp32 accumulation), activation gradients are stored in T, parameter
+// gradients accumulate in fp32, and the fp16 branches keep the reference's fp16 rounding
+// points where the reference writes them op by op (RMSNorm, GELU, cross-entropy, RoPE).
 //
 //  * gemm_bwd_kernel: 128 × 128 tile, 4 waves of 64 × 64, MFMA 32×32×2 fp32; either
 //    operand read k-contiguous (rows of a row-major matrix) or m/n-contiguous (columns),
@@ -20,8 +24,32 @@ namespace nml {
 
 namespace {
 
+// 4 consecutive elements as fp32 (16-byte float or 8-byte fp16 load) and back.
+template <typename T>
+__device__ __forceinline__ floatx4 ld4(const T* p) {
+  if constexpr (sizeof(T) == 4) {
+    return *reinterpret_cast<const floatx4*>(p);
+  } else {
+    const half4 h = *reinterpret_cast<const half4*>(p);
+    const floatx4 v = {static_cast<float>(h[0]), static_cast<float>(h[1]), static_cast<float>(h[2]),
+                       static_cast<float>(h[3])};
+    return v;
+  }
+}
+template <typename T>
+__device__ __forceinline__ void st4(T* p, floatx4 v) {
+  if constexpr (sizeof(T) == 4) {
+    *reinterpret_cast<floatx4*>(p) = v;
+  } else {
+    const half4 h = {static_cast<half_t>(v[0]), static_cast<half_t>(v[1]), static_cast<half_t>(v[2]),
+                     static_cast<half_t>(v[3])};
+    *reinterpret_cast<half4*>(p) = h;
+  }
+}
+
 // ------------------------------------------------------------------ backward GEMM
 constexpr int kGM = 128, kGK = 16, kGPad = 4;
+constexpr int kGBPart = 3;  // split-K partial: fp32, unrounded
 
 // gelu'(x) of native/src/gelu.cpp:23-33 (tanh recomputed from x as the forward did).
 __device__ __forceinline__ float gelu_grad(float x) {
@@ -33,12 +61,38 @@ __device__ __forceinline__ float gelu_grad(float x) {
   return 0.5f * (1.0f + tu) + 0.5f * x * sech2 * du_dx;
 }
 
+// fp16: g·gelu'(x) in the fp16 ops of kernels/fused_gelu.py:97-102 (tu as the fp16 forward
+// forms it, kernels/fused_gelu.py:67; each product and sum rounded to fp16).
+__device__ __forceinline__ float gelu_grad_f16(float g, float x) {
+#pragma clang fp contract(off)
+  const float k = static_cast<float>(static_cast<half_t>(0.7978845608028654f));
+  const float c = static_cast<float>(static_cast<half_t>(0.044715f));
+  const float dc = static_cast<float>(static_cast<half_t>(0.134145f));
+  float t = rnd<half_t>(c * x);
+  t = rnd<half_t>(t * x);
+  t = rnd<half_t>(t * x);
+  t = rnd<half_t>(x + t);
+  t = rnd<half_t>(k * t);
+  const float tu = rnd<half_t>(tanhf(t));
+  float du = rnd<half_t>(dc * x);
+  du = rnd<half_t>(du * x);
+  du = rnd<half_t>(1.0f + du);
+  du = rnd<half_t>(k * du);
+  const float sech2 = rnd<half_t>(1.0f - rnd<half_t>(tu * tu));
+  const float a = rnd<half_t>(0.5f * rnd<half_t>(1.0f + tu));
+  float b = rnd<half_t>(0.5f * x);
+  b = rnd<half_t>(b * sech2);
+  b = rnd<half_t>(b * du);
+  const float d = rnd<half_t>(a + b);
+  return rnd<half_t>(g * d);
+}
+
 // One operand tile (128 rows × 16 k) into LDS as S[k][row]. KC: element (r, k) at
 // p[r·ld + k] (4 lanes per row, 16-byte loads along k, transposed on the LDS store);
 // otherwise at p[k·ld + r] (32 lanes per k row, 16-byte loads and stores). Out-of-range
 // rows / k read as 0. Two 16-byte vectors per thread.
-template <bool KC>
-__device__ __forceinline__ void tile_load(const float* __restrict__ p, long long ld, int r0,
+template <bool KC, typename T>
+__device__ __forceinline__ void tile_load(const T* __restrict__ p, long long ld, int r0,
                                           int R, int k0, int K, floatx4 (&v)[2]) {
   const int tid = threadIdx.x;
 #pragma unroll
@@ -48,13 +102,11 @@ __device__ __forceinline__ void tile_load(const float* __restrict__ p, long long
     if constexpr (KC) {
       const int row = c >> 2, kc = (c & 3) * 4;
       const bool ok = r0 + row < R && k0 + kc < K;
-      v[i] = ok ? *reinterpret_cast<const floatx4*>(p + static_cast<long long>(r0 + row) * ld + k0 + kc)
-                : zero;
+      v[i] = ok ? ld4(p + static_cast<long long>(r0 + row) * ld + k0 + kc) : zero;
     } else {
       const int kr = c >> 5, rc = (c & 31) * 4;
       const bool ok = k0 + kr < K && r0 + rc < R;
-      v[i] = ok ? *reinterpret_cast<const floatx4*>(p + static_cast<long long>(k0 + kr) * ld + r0 + rc)
-                : zero;
+      v[i] = ok ? ld4(p + static_cast<long long>(k0 + kr) * ld + r0 + rc) : zero;
     }
   }
 }
@@ -78,7 +130,9 @@ __device__ __forceinline__ void tile_store(float (*S)[kGM + kGPad], const floatx
 
 // Split K (gridDim.z > 1): block z multiplies k in [z·kchunk, (z + 1)·kchunk) and writes
 // its partial product to c + z·zstride (OUT = GB_SET), summed afterwards in a fixed order.
-template <bool A_KC, bool B_KC, int OUT>
+// T: operand type (and the output type of GB_SET / GB_GELU); GB_ADD adds fp32(T(acc)) to
+// an fp32 output (the reference forms the gradient in T, then accumulates it in fp32).
+template <bool A_KC, bool B_KC, int OUT, typename T>
 __global__ __launch_bounds__(256) void gemm_bwd_kernel(GemmBwdArgs g, int kchunk, long long zstride) {
   __shared__ __attribute__((aligned(16))) float As[kGK][kGM + kGPad];
   __shared__ __attribute__((aligned(16))) float Bs[kGK][kGM + kGPad];
@@ -88,7 +142,8 @@ __global__ __launch_bounds__(256) void gemm_bwd_kernel(GemmBwdArgs g, int kchunk
   const int M = g.M, N = g.N;
   const int kbeg = blockIdx.z * kchunk;
   const int K = min(g.K, kbeg + kchunk);
-  g.c += blockIdx.z * zstride;
+  const T* __restrict__ ga = static_cast<const T*>(g.a);
+  const T* __restrict__ gbp = static_cast<const T*>(g.b);
 
   floatx16 acc[2][2];
 #pragma unroll
@@ -99,16 +154,16 @@ __global__ __launch_bounds__(256) void gemm_bwd_kernel(GemmBwdArgs g, int kchunk
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
 
   floatx4 ra[2], rb[2];
-  tile_load<A_KC>(g.a, g.lda, m0, M, kbeg, K, ra);
-  tile_load<B_KC>(g.b, g.ldb, n0, N, kbeg, K, rb);
+  tile_load<A_KC>(ga, g.lda, m0, M, kbeg, K, ra);
+  tile_load<B_KC>(gbp, g.ldb, n0, N, kbeg, K, rb);
   tile_store<A_KC>(As, ra);
   tile_store<B_KC>(Bs, rb);
   __syncthreads();
   for (int k0 = kbeg; k0 < K; k0 += kGK) {
     const bool more = k0 + kGK < K;
     if (more) {  // next tile's loads in flight while this one multiplies
-      tile_load<A_KC>(g.a, g.lda, m0, M, k0 + kGK, K, ra);
-      tile_load<B_KC>(g.b, g.ldb, n0, N, k0 + kGK, K, rb);
+      tile_load<A_KC>(ga, g.lda, m0, M, k0 + kGK, K, ra);
+      tile_load<B_KC>(gbp, g.ldb, n0, N, k0 + kGK, K, rb);
     }
 #pragma unroll
     for (int kk = 0; kk < kGK; kk += 2) {
@@ -141,16 +196,27 @@ __global__ __launch_bounds__(256) void gemm_bwd_kernel(GemmBwdArgs g, int kchunk
         const int m = m0 + wm * 64 + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
         const int n = n0 + wn * 64 + j * 32 + (lane & 31);
         if (m < M && n < N) {
-          float* c = g.c + static_cast<long long>(m) * g.ldc + n;
+          const long long ci = blockIdx.z * zstride + static_cast<long long>(m) * g.ldc + n;
           const float v = acc[i][j][r];
-          if constexpr (OUT == GB_SET) *c = v;
-          else if constexpr (OUT == GB_ADD) *c += v;
-          else *c = v * gelu_grad(g.aux[static_cast<long long>(m) * g.ldaux + n]);
+          if constexpr (OUT == kGBPart) {
+            static_cast<float*>(g.c)[ci] = v;
+          } else if constexpr (OUT == GB_ADD) {
+            static_cast<float*>(g.c)[ci] += rnd<T>(v);
+          } else if constexpr (OUT == GB_SET) {
+            static_cast<T*>(g.c)[ci] = static_cast<T>(v);
+          } else {
+            const float x = static_cast<float>(static_cast<const T*>(g.aux)[static_cast<long long>(m) * g.ldaux + n]);
+            if constexpr (sizeof(T) == 4)
+              static_cast<T*>(g.c)[ci] = v * gelu_grad(x);
+            else
+              static_cast<T*>(g.c)[ci] = static_cast<T>(gelu_grad_f16(rnd<T>(v), x));
+          }
         }
       }
 }
 
-// c[m·ldc + n] += Σ_z part[z·M·N + m·N + n], z in order.
+// c[m·ldc + n] += T(Σ_z part[z·M·N + m·N + n]), z in order.
+template <typename T>
 __global__ __launch_bounds__(256) void splitk_reduce_kernel(const float* __restrict__ part, int splits,
                                                             int M, int N, float* __restrict__ c,
                                                             long long ldc) {
@@ -160,7 +226,7 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(const float* __restr
   float s = 0.f;
   for (int z = 0; z < splits; ++z) s += part[z * mn + i];
   const int m = static_cast<int>(i / N), n = static_cast<int>(i - static_cast<long long>(m) * N);
-  c[static_cast<long long>(m) * ldc + n] += s;
+  c[static_cast<long long>(m) * ldc + n] += rnd<T>(s);
 }
 
 // Split-K partials of the weight-gradient GEMMs (grow-only; training is never captured).
@@ -170,7 +236,7 @@ struct SplitWs {
 };
 SplitWs g_split;
 
-template <bool A_KC, bool B_KC>
+template <bool A_KC, bool B_KC, typename T>
 int gemm_bwd_out(const GemmBwdArgs& g, int out, hipStream_t st) {
   const int tn = (g.N + kGM - 1) / kGM, tm = (g.M + kGM - 1) / kGM;
   // Few output tiles and a long K (a weight gradient, K = rows): split K so that the
@@ -193,19 +259,19 @@ int gemm_bwd_out(const GemmBwdArgs& g, int out, hipStream_t st) {
     p.c = g_split.p;
     p.ldc = g.N;
     const dim3 grid(tn, tm, splits);
-    gemm_bwd_kernel<A_KC, B_KC, GB_SET><<<grid, 256, 0, st>>>(p, kchunk, static_cast<long long>(g.M) * g.N);
+    gemm_bwd_kernel<A_KC, B_KC, kGBPart, T><<<grid, 256, 0, st>>>(p, kchunk, static_cast<long long>(g.M) * g.N);
     NML_LAUNCHED();
     const long long mn = static_cast<long long>(g.M) * g.N;
-    splitk_reduce_kernel<<<static_cast<int>((mn + 255) / 256), 256, 0, st>>>(g_split.p, splits, g.M,
-                                                                              g.N, g.c, g.ldc);
+    splitk_reduce_kernel<T><<<static_cast<int>((mn + 255) / 256), 256, 0, st>>>(
+        g_split.p, splits, g.M, g.N, static_cast<float*>(g.c), g.ldc);
     NML_LAUNCHED();
     return 0;
   }
   const dim3 grid(tn, tm);
   switch (out) {
-    case GB_SET: gemm_bwd_kernel<A_KC, B_KC, GB_SET><<<grid, 256, 0, st>>>(g, g.K, 0); break;
-    case GB_ADD: gemm_bwd_kernel<A_KC, B_KC, GB_ADD><<<grid, 256, 0, st>>>(g, g.K, 0); break;
-    case GB_GELU: gemm_bwd_kernel<A_KC, B_KC, GB_GELU><<<grid, 256, 0, st>>>(g, g.K, 0); break;
+    case GB_SET: gemm_bwd_kernel<A_KC, B_KC, GB_SET, T><<<grid, 256, 0, st>>>(g, g.K, 0); break;
+    case GB_ADD: gemm_bwd_kernel<A_KC, B_KC, GB_ADD, T><<<grid, 256, 0, st>>>(g, g.K, 0); break;
+    case GB_GELU: gemm_bwd_kernel<A_KC, B_KC, GB_GELU, T><<<grid, 256, 0, st>>>(g, g.K, 0); break;
     default: set_error("gemm_bwd: unknown output mode %d", out); return -1;
   }
   NML_LAUNCHED();
@@ -281,17 +347,22 @@ __global__ __launch_bounds__(256) void rmsnorm_bwd_kernel(const float* __restric
   }
 }
 
-// The same with one wave per 16 rows (4 waves per workgroup): a lane keeps NV 16-byte
-// vectors of the row, the row sums are DPP wave sums (no LDS, no barrier), and the wave's
-// Σ dy·(x/rms) per column goes to part[wave].
-template <int NV>
-__global__ __launch_bounds__(256) void rmsnorm_bwd_wave_kernel(const float* __restrict__ dy,
-                                                               const float* __restrict__ x,
-                                                               const float* __restrict__ gam,
-                                                               float* __restrict__ dx, int acc,
+// The same with one wave per 16 rows (4 waves per workgroup): a lane keeps NV vectors of
+// 4 elements of the row, the row sums are DPP wave sums (no LDS, no barrier), and the
+// wave's dγ contribution per column goes to part[wave]. fp16 (kernels/fused_rmsnorm.py:
+// 195-206): ms recomputed as the forward forms it (fp16 squares, fp32 sum), inv = fp16(1/rms),
+// x̂ = x·inv, dγ += Σ dy·x̂ (fp16 products, fp32 sum), gxh = dy·γ, dot = Σ gxh·x (fp16
+// products, fp32 sum), coef = fp16((2/d)·dot·(−½)·(ms + ε)^(−3/2)), dx = gxh·inv + x·coef,
+// every product and sum rounded to fp16 (and the residual add too, as grad_mid += …).
+template <typename T, int NV>
+__global__ __launch_bounds__(256) void rmsnorm_bwd_wave_kernel(const T* __restrict__ dy,
+                                                               const T* __restrict__ x,
+                                                               const T* __restrict__ gam,
+                                                               T* __restrict__ dx, int acc,
                                                                float* __restrict__ part, int rows,
                                                                int d, float eps) {
 #pragma clang fp contract(off)
+  constexpr bool H = sizeof(T) == 2;
   const int lane = threadIdx.x & 63;
   const int wv = blockIdx.x * 4 + (threadIdx.x >> 6);
   const int r0 = wv * kNormRowsPerBlock;
@@ -302,41 +373,58 @@ __global__ __launch_bounds__(256) void rmsnorm_bwd_wave_kernel(const float* __re
 #pragma unroll
   for (int i = 0; i < NV; ++i) {
     const int c = lane + 64 * i;
-    gv[i] = c < nvec ? reinterpret_cast<const floatx4*>(gam)[c] : z;
+    gv[i] = c < nvec ? ld4(gam + 4 * c) : z;
     ga[i] = z;
   }
   for (int r = r0; r < r1; ++r) {
-    const floatx4* xr = reinterpret_cast<const floatx4*>(x + static_cast<long long>(r) * d);
-    const floatx4* gr = reinterpret_cast<const floatx4*>(dy + static_cast<long long>(r) * d);
+    const T* xr = x + static_cast<long long>(r) * d;
+    const T* gr = dy + static_cast<long long>(r) * d;
     floatx4 xv[NV], dv[NV];
     float ssq = 0.f, dot = 0.f;
 #pragma unroll
     for (int i = 0; i < NV; ++i) {
       const int c = lane + 64 * i;
-      xv[i] = c < nvec ? xr[c] : z;
-      dv[i] = c < nvec ? gr[c] : z;
+      xv[i] = c < nvec ? ld4(xr + 4 * c) : z;
+      dv[i] = c < nvec ? ld4(gr + 4 * c) : z;
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        ssq += xv[i][e] * xv[i][e];
-        dot += (dv[i][e] * gv[i][e]) * xv[i][e];
+        if constexpr (H) {
+          ssq += rnd<T>(xv[i][e] * xv[i][e]);
+          dot += rnd<T>(rnd<T>(dv[i][e] * gv[i][e]) * xv[i][e]);
+        } else {
+          ssq += xv[i][e] * xv[i][e];
+          dot += (dv[i][e] * gv[i][e]) * xv[i][e];
+        }
       }
     }
     const float ms = wave_sum_dpp(ssq) / static_cast<float>(d);
     const float rdot = wave_sum_dpp(dot);
     const float rms = sqrtf(ms + eps);
-    const float coef = (2.0f / static_cast<float>(d)) * (rdot * -0.5f / ((ms + eps) * rms));
-    floatx4* o = reinterpret_cast<floatx4*>(dx + static_cast<long long>(r) * d);
+    float inv = 0.f, coef;
+    if constexpr (H) {
+      inv = rnd<T>(1.0f / rms);
+      coef = rnd<T>((2.0f / static_cast<float>(d)) * (rdot * -0.5f * powf(ms + eps, -1.5f)));
+    } else {
+      coef = (2.0f / static_cast<float>(d)) * (rdot * -0.5f / ((ms + eps) * rms));
+    }
+    T* o = dx + static_cast<long long>(r) * d;
 #pragma unroll
     for (int i = 0; i < NV; ++i) {
       const int c = lane + 64 * i;
       if (c < nvec) {
-        floatx4 v = acc ? o[c] : z;
+        floatx4 v = acc ? ld4(o + 4 * c) : z;
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          v[e] += (dv[i][e] * gv[i][e]) / rms + xv[i][e] * coef;
-          ga[i][e] += dv[i][e] * (xv[i][e] / rms);
+          if constexpr (H) {
+            const float gx = rnd<T>(rnd<T>(rnd<T>(dv[i][e] * gv[i][e]) * inv) + rnd<T>(xv[i][e] * coef));
+            v[e] = acc ? rnd<T>(v[e] + gx) : gx;
+            ga[i][e] += rnd<T>(dv[i][e] * rnd<T>(xv[i][e] * inv));
+          } else {
+            v[e] += (dv[i][e] * gv[i][e]) / rms + xv[i][e] * coef;
+            ga[i][e] += dv[i][e] * (xv[i][e] / rms);
+          }
         }
-        o[c] = v;
+        st4(o + 4 * c, v);
       }
     }
   }
@@ -371,50 +459,57 @@ __global__ __launch_bounds__(256) void parts_reduce_kernel(const float* __restri
 // ---------------------------------------------------------------- column sums
 constexpr int kColRows = 64;
 
-__global__ __launch_bounds__(256) void colsum_part_kernel(const float* __restrict__ a,
+template <typename T>
+__global__ __launch_bounds__(256) void colsum_part_kernel(const T* __restrict__ a,
                                                           long long lda, int rows, int n,
                                                           float* __restrict__ part) {
   const int c = blockIdx.x * 256 + threadIdx.x;
   if (c >= n) return;
   const int r0 = blockIdx.y * kColRows, r1 = min(rows, r0 + kColRows);
   float s = 0.f;
-  for (int r = r0; r < r1; ++r) s += a[static_cast<long long>(r) * lda + c];
+  for (int r = r0; r < r1; ++r) s += static_cast<float>(a[static_cast<long long>(r) * lda + c]);
   part[static_cast<long long>(blockIdx.y) * n + c] = s;
 }
 
 // -------------------------------------------------------- cross-entropy backward
-// One block per row: probs = exp(l − max)·(1/Σexp), probs[label] −= 1, × scale.
-__global__ __launch_bounds__(256) void ce_grad_kernel(float* __restrict__ lg, int V,
+// One block per row: probs = exp(l − max)·(1/Σexp), probs[label] −= 1, × scale. fp16: the
+// shift, exp and products rounded to fp16, Σexp in fp32 and 1/Σexp and scale cast to fp16
+// (kernels/fused_crossentropy.py:41-49 with the forward's fp32 sum, :20-24).
+template <typename T>
+__global__ __launch_bounds__(256) void ce_grad_kernel(T* __restrict__ lg, int V,
                                                       const int64_t* __restrict__ labels,
                                                       long long ignore_index, int has_ignore,
                                                       float scale) {
+#pragma clang fp contract(off)
   __shared__ float red[4];
-  float* p = lg + static_cast<long long>(blockIdx.x) * V;
+  T* p = lg + static_cast<long long>(blockIdx.x) * V;
   const long long label = labels[blockIdx.x];
   if (has_ignore && label == ignore_index) {
-    for (int i = threadIdx.x; i < V; i += 256) p[i] = 0.f;
+    for (int i = threadIdx.x; i < V; i += 256) p[i] = static_cast<T>(0.f);
     return;
   }
   float mx = -INFINITY;
-  for (int i = threadIdx.x; i < V; i += 256) mx = fmaxf(mx, p[i]);
+  for (int i = threadIdx.x; i < V; i += 256) mx = fmaxf(mx, static_cast<float>(p[i]));
   mx = wave_max(mx);
   if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = mx;
   __syncthreads();
   mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
   float se = 0.f;
-  for (int i = threadIdx.x; i < V; i += 256) se += expf(p[i] - mx);
+  for (int i = threadIdx.x; i < V; i += 256) se += rnd<T>(expf(rnd<T>(static_cast<float>(p[i]) - mx)));
   se = block_sum(se, red);
-  const float inv = 1.0f / se;
+  const float inv = rnd<T>(1.0f / se);
+  const float sc = rnd<T>(scale);
   for (int i = threadIdx.x; i < V; i += 256) {
-    float v = expf(p[i] - mx) * inv;
-    if (i == label) v -= 1.0f;
-    p[i] = v * scale;
+    float v = rnd<T>(rnd<T>(expf(rnd<T>(static_cast<float>(p[i]) - mx))) * inv);
+    if (i == label) v = rnd<T>(v - 1.0f);
+    p[i] = static_cast<T>(v * sc);
   }
 }
 
 // ------------------------------------------------------------ attention backward
 // dvec[(b·H + h)·S + s] = Σ_c dout·o over the head's columns (= Σ_j P·dP of the
 // softmax backward, kernels/fused_sdpa.py:26-29).
+template <typename T>
 __global__ __launch_bounds__(256) void attn_bwd_dot_kernel(AttnBwdArgs a) {
   const int t = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
   const int R = a.B * a.S;
@@ -423,15 +518,30 @@ __global__ __launch_bounds__(256) void attn_bwd_dot_kernel(AttnBwdArgs a) {
   const int b = r / a.S, s = r - (r / a.S) * a.S;
   const long long off = static_cast<long long>(r) * a.H * a.dk + h * a.dk;
   float v = 0.f;
-  for (int c = lane; c < a.dk; c += 64) v += a.dout[off + c] * a.o[off + c];
+  const T* dout = static_cast<const T*>(a.dout);
+  const T* o = static_cast<const T*>(a.o);
+  for (int c = lane; c < a.dk; c += 64) v += static_cast<float>(dout[off + c]) * static_cast<float>(o[off + c]);
   v = wave_sum(v);
   if (lane == 0) a.dvec[(static_cast<long long>(b) * a.H + h) * a.S + s] = v;
+}
+
+// The forward's score of q·k: q·k·(1/scale) in fp32; fp16 rnd(rnd(q·k)·(1/fp16(scale))),
+// the rounding of the fp16 prefill kernel.
+template <typename T>
+__device__ __forceinline__ float attn_score(float dot, float mul) {
+  if constexpr (sizeof(T) == 4) return dot * mul;
+  else return rnd<T>(rnd<T>(dot) * mul);
+}
+template <typename T>
+__device__ __forceinline__ float score_mul(float scale) {
+  if constexpr (sizeof(T) == 4) return 1.0f / scale;
+  else return 1.0f / static_cast<float>(static_cast<T>(scale));
 }
 
 // Shared per-tile step: thread t scores EPT (query i, key j) pairs of a BT × BT tile,
 // i = t / TPR, j = (t % TPR)·EPT + e: p = exp(q·k/scale − lse_i) where key ≤ query (both
 // inside the sequence), else 0; ds = p·(dO_i·v_j − D_i)/scale.
-template <int DK, int BT>
+template <int DK, int BT, typename T>
 struct AttnTile {
   static constexpr int EPT = BT * BT / 256;
   static constexpr int TPR = BT / EPT;
@@ -445,6 +555,7 @@ struct AttnTile {
   float D[BT];
 
   __device__ void scores(int q_lo, int k_lo, int S, float scale) {
+    const float mul = score_mul<T>(scale), inv_scale = 1.0f / scale;
     const int t = threadIdx.x;
     const int i = t / TPR, j0 = (t % TPR) * EPT;
     const int qi = q_lo + i;
@@ -459,8 +570,8 @@ struct AttnTile {
           dot += Qs[i][c] * Ks[j][c];
           dp += dOs[i][c] * Vs[j][c];
         }
-        p = expf(dot / scale - lse[i]);
-        ds = p * (dp - D[i]) / scale;
+        p = expf(attn_score<T>(dot, mul) - lse[i]);
+        ds = p * (dp - D[i]) * inv_scale;
       }
       Ps[i][j] = p;
       dSs[i][j] = ds;
@@ -469,45 +580,49 @@ struct AttnTile {
 };
 
 // rows [lo, lo + BT) of a head-major (B·H, S, DK) tensor into dst (0 past S)
-template <int DK, int BT>
-__device__ __forceinline__ void load_rows(float (*dst)[DK + 1], const float* __restrict__ src,
+template <int DK, int BT, typename T>
+__device__ __forceinline__ void load_rows(float (*dst)[DK + 1], const T* __restrict__ src,
                                           int lo, int S) {
   for (int e = threadIdx.x; e < BT * DK; e += 256) {
     const int r = e / DK, c = e - (e / DK) * DK;
-    dst[r][c] = lo + r < S ? src[static_cast<long long>(lo + r) * DK + c] : 0.f;
+    dst[r][c] = lo + r < S ? static_cast<float>(src[static_cast<long long>(lo + r) * DK + c]) : 0.f;
   }
 }
 
 // rows [lo, lo + BT) of head h of a merged (B·S, H·DK) tensor
-template <int DK, int BT>
-__device__ __forceinline__ void load_merged(float (*dst)[DK + 1], const float* __restrict__ src,
+template <int DK, int BT, typename T>
+__device__ __forceinline__ void load_merged(float (*dst)[DK + 1], const T* __restrict__ src,
                                             int b, int h, int H, int lo, int S) {
   for (int e = threadIdx.x; e < BT * DK; e += 256) {
     const int r = e / DK, c = e - (e / DK) * DK;
-    dst[r][c] = lo + r < S ? src[(static_cast<long long>(b) * S + lo + r) * H * DK + h * DK + c]
+    dst[r][c] = lo + r < S ? static_cast<float>(src[(static_cast<long long>(b) * S + lo + r) * H * DK + h * DK + c])
                            : 0.f;
   }
 }
 
 // dK, dV of BT keys: walk the query tiles from the key tile on (causal).
-template <int DK, int BT>
+template <int DK, int BT, typename T>
 __global__ __launch_bounds__(256) void attn_bwd_dkdv_kernel(AttnBwdArgs a) {
-  __shared__ AttnTile<DK, BT> sh;
+  __shared__ AttnTile<DK, BT, T> sh;
+  const T* qg = static_cast<const T*>(a.q);
+  const T* kg = static_cast<const T*>(a.k);
+  const T* vg = static_cast<const T*>(a.v);
+  const T* og = static_cast<const T*>(a.dout);
   constexpr int TPK = 256 / BT;       // threads per key row of the output
   constexpr int NCOL = (DK + TPK - 1) / TPK;
   const int bh = blockIdx.y, b = bh / a.H, h = bh - (bh / a.H) * a.H;
   const int S = a.S, k_lo = blockIdx.x * BT;
   const long long hoff = static_cast<long long>(bh) * S * DK;
-  load_rows<DK, BT>(sh.Ks, a.k + hoff, k_lo, S);
-  load_rows<DK, BT>(sh.Vs, a.v + hoff, k_lo, S);
+  load_rows<DK, BT>(sh.Ks, kg + hoff, k_lo, S);
+  load_rows<DK, BT>(sh.Vs, vg + hoff, k_lo, S);
   const int jo = threadIdx.x / TPK, co = threadIdx.x % TPK;
   float dk[NCOL], dv[NCOL];
 #pragma unroll
   for (int u = 0; u < NCOL; ++u) dk[u] = dv[u] = 0.f;
   for (int q_lo = k_lo; q_lo < S; q_lo += BT) {
     __syncthreads();  // the previous tile's readers are done
-    load_rows<DK, BT>(sh.Qs, a.q + hoff, q_lo, S);
-    load_merged<DK, BT>(sh.dOs, a.dout, b, h, a.H, q_lo, S);
+    load_rows<DK, BT>(sh.Qs, qg + hoff, q_lo, S);
+    load_merged<DK, BT>(sh.dOs, og, b, h, a.H, q_lo, S);
     for (int i = threadIdx.x; i < BT; i += 256) {
       const bool ok = q_lo + i < S;
       sh.lse[i] = ok ? a.lse[static_cast<long long>(bh) * S + q_lo + i] : 0.f;
@@ -534,29 +649,33 @@ __global__ __launch_bounds__(256) void attn_bwd_dkdv_kernel(AttnBwdArgs a) {
   const int key = k_lo + jo;
   if (key < S) {
     const int d = a.H * DK;
-    float* row = a.dqkv + (static_cast<long long>(b) * S + key) * 3 * d + h * DK;
+    T* row = static_cast<T*>(a.dqkv) + (static_cast<long long>(b) * S + key) * 3 * d + h * DK;
 #pragma unroll
     for (int u = 0; u < NCOL; ++u) {
       const int c = co + TPK * u;
       if (c < DK) {
-        row[d + c] = dk[u];
-        row[2 * d + c] = dv[u];
+        row[d + c] = static_cast<T>(dk[u]);
+        row[2 * d + c] = static_cast<T>(dv[u]);
       }
     }
   }
 }
 
 // dQ of BT queries: walk the key tiles up to the query tile (causal).
-template <int DK, int BT>
+template <int DK, int BT, typename T>
 __global__ __launch_bounds__(256) void attn_bwd_dq_kernel(AttnBwdArgs a) {
-  __shared__ AttnTile<DK, BT> sh;
+  __shared__ AttnTile<DK, BT, T> sh;
+  const T* qg = static_cast<const T*>(a.q);
+  const T* kg = static_cast<const T*>(a.k);
+  const T* vg = static_cast<const T*>(a.v);
+  const T* og = static_cast<const T*>(a.dout);
   constexpr int TPK = 256 / BT;
   constexpr int NCOL = (DK + TPK - 1) / TPK;
   const int bh = blockIdx.y, b = bh / a.H, h = bh - (bh / a.H) * a.H;
   const int S = a.S, q_lo = blockIdx.x * BT;
   const long long hoff = static_cast<long long>(bh) * S * DK;
-  load_rows<DK, BT>(sh.Qs, a.q + hoff, q_lo, S);
-  load_merged<DK, BT>(sh.dOs, a.dout, b, h, a.H, q_lo, S);
+  load_rows<DK, BT>(sh.Qs, qg + hoff, q_lo, S);
+  load_merged<DK, BT>(sh.dOs, og, b, h, a.H, q_lo, S);
   for (int i = threadIdx.x; i < BT; i += 256) {
     const bool ok = q_lo + i < S;
     sh.lse[i] = ok ? a.lse[static_cast<long long>(bh) * S + q_lo + i] : 0.f;
@@ -569,8 +688,8 @@ __global__ __launch_bounds__(256) void attn_bwd_dq_kernel(AttnBwdArgs a) {
   const int k_end = min(S, q_lo + BT);
   for (int k_lo = 0; k_lo < k_end; k_lo += BT) {
     __syncthreads();
-    load_rows<DK, BT>(sh.Ks, a.k + hoff, k_lo, S);
-    load_rows<DK, BT>(sh.Vs, a.v + hoff, k_lo, S);
+    load_rows<DK, BT>(sh.Ks, kg + hoff, k_lo, S);
+    load_rows<DK, BT>(sh.Vs, vg + hoff, k_lo, S);
     __syncthreads();
     sh.scores(q_lo, k_lo, S, a.scale);
     __syncthreads();
@@ -588,11 +707,11 @@ __global__ __launch_bounds__(256) void attn_bwd_dq_kernel(AttnBwdArgs a) {
   const int q = q_lo + io;
   if (q < S) {
     const int d = a.H * DK;
-    float* row = a.dqkv + (static_cast<long long>(b) * S + q) * 3 * d + h * DK;
+    T* row = static_cast<T*>(a.dqkv) + (static_cast<long long>(b) * S + q) * 3 * d + h * DK;
 #pragma unroll
     for (int u = 0; u < NCOL; ++u) {
       const int c = co + TPK * u;
-      if (c < DK) row[c] = dq[u];
+      if (c < DK) row[c] = static_cast<T>(dq[u]);
     }
   }
 }
@@ -612,27 +731,25 @@ constexpr size_t attn_mfma_lds() {
 }
 
 // rows [lo, lo + 64) of a head-major (S, DK) slice into a [64][DK + 1] tile (0 past S)
-template <int DK>
-__device__ __forceinline__ void tile_rows(float* dst, const float* __restrict__ src, int lo, int S) {
+template <int DK, typename T>
+__device__ __forceinline__ void tile_rows(float* dst, const T* __restrict__ src, int lo, int S) {
   for (int e = threadIdx.x; e < kAT * DK / 4; e += 256) {
     const int r = e / (DK / 4), c = (e - r * (DK / 4)) * 4;
     floatx4 v = {0.f, 0.f, 0.f, 0.f};
-    if (lo + r < S) v = *reinterpret_cast<const floatx4*>(src + static_cast<long long>(lo + r) * DK + c);
+    if (lo + r < S) v = ld4(src + static_cast<long long>(lo + r) * DK + c);
 #pragma unroll
     for (int j = 0; j < 4; ++j) dst[r * (DK + 1) + c + j] = v[j];
   }
 }
 
 // rows [lo, lo + 64) of head h of a merged (B·S, H·DK) tensor
-template <int DK>
-__device__ __forceinline__ void tile_merged(float* dst, const float* __restrict__ src, int b, int h,
+template <int DK, typename T>
+__device__ __forceinline__ void tile_merged(float* dst, const T* __restrict__ src, int b, int h,
                                             int H, int lo, int S) {
   for (int e = threadIdx.x; e < kAT * DK / 4; e += 256) {
     const int r = e / (DK / 4), c = (e - r * (DK / 4)) * 4;
     floatx4 v = {0.f, 0.f, 0.f, 0.f};
-    if (lo + r < S)
-      v = *reinterpret_cast<const floatx4*>(src + (static_cast<long long>(b) * S + lo + r) * H * DK +
-                                            h * DK + c);
+    if (lo + r < S) v = ld4(src + (static_cast<long long>(b) * S + lo + r) * H * DK + h * DK + c);
 #pragma unroll
     for (int j = 0; j < 4; ++j) dst[r * (DK + 1) + c + j] = v[j];
   }
@@ -642,17 +759,17 @@ __device__ __forceinline__ int d_row(int r, int lane) { return 8 * (r >> 2) + 4 
 
 // A 64 × DK tile staged through registers (DK/16 16-byte vectors per thread) so that the
 // next tile's loads are in flight while the current one multiplies.
-template <int DK>
+template <int DK, typename T>
 struct TileRegs {
   floatx4 v[DK / 16];
   // rows [lo, lo + 64) of a row-major source with row stride ld (0 past S)
-  __device__ __forceinline__ void load(const float* __restrict__ src, long long ld, int lo, int S) {
+  __device__ __forceinline__ void load(const T* __restrict__ src, long long ld, int lo, int S) {
 #pragma unroll
     for (int i = 0; i < DK / 16; ++i) {
       const int e = threadIdx.x + 256 * i;
       const int r = e / (DK / 4), c = (e - r * (DK / 4)) * 4;
       const floatx4 z = {0.f, 0.f, 0.f, 0.f};
-      v[i] = lo + r < S ? *reinterpret_cast<const floatx4*>(src + static_cast<long long>(lo + r) * ld + c) : z;
+      v[i] = lo + r < S ? ld4(src + static_cast<long long>(lo + r) * ld + c) : z;
     }
   }
   __device__ __forceinline__ void store(float* dst) const {
@@ -667,7 +784,7 @@ struct TileRegs {
 };
 
 // dK, dV of 64 keys; the query tiles from the key tile on.
-template <int DK>
+template <int DK, typename T>
 __global__ __launch_bounds__(256, 2) void attn_bwd_dkdv_mfma(AttnBwdArgs a) {
   extern __shared__ float lds[];
   constexpr int P = DK + 1, NJ = DK / 32;
@@ -682,20 +799,21 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dkdv_mfma(AttnBwdArgs a) {
   const int bh = blockIdx.y, b = bh / a.H, h = bh - (bh / a.H) * a.H;
   const int S = a.S, k_lo = blockIdx.x * kAT;
   const long long hoff = static_cast<long long>(bh) * S * DK;
-  tile_rows<DK>(Ks, a.k + hoff, k_lo, S);
-  tile_rows<DK>(Vs, a.v + hoff, k_lo, S);
+  tile_rows<DK>(Ks, static_cast<const T*>(a.k) + hoff, k_lo, S);
+  tile_rows<DK>(Vs, static_cast<const T*>(a.v) + hoff, k_lo, S);
   floatx16 dv[NJ], dk[NJ];
 #pragma unroll
   for (int j = 0; j < NJ; ++j)
 #pragma unroll
     for (int r = 0; r < 16; ++r) dv[j][r] = dk[j][r] = 0.f;
   const int key = k_lo + 32 * wk + l32;  // this lane's key (column of S)
-  const float inv_scale = 1.0f / a.scale;
-  const float* dout_b = a.dout + static_cast<long long>(b) * S * a.H * DK + h * DK;
-  TileRegs<DK> nq, no;
+  const float inv_scale = 1.0f / a.scale, mul = score_mul<T>(a.scale);
+  const T* dout_b = static_cast<const T*>(a.dout) + static_cast<long long>(b) * S * a.H * DK + h * DK;
+  const T* qg = static_cast<const T*>(a.q);
+  TileRegs<DK, T> nq, no;
   float nl = 0.f, nd = 0.f;
   auto fetch = [&](int lo) {
-    nq.load(a.q + hoff, DK, lo, S);
+    nq.load(qg + hoff, DK, lo, S);
     no.load(dout_b, static_cast<long long>(a.H) * DK, lo, S);
     if (threadIdx.x < kAT) {
       const int q = lo + threadIdx.x;
@@ -730,7 +848,7 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dkdv_mfma(AttnBwdArgs a) {
     for (int r = 0; r < 16; ++r) {
       const int ql = 32 * wq + d_row(r, lane), q = q_lo + ql;
       float p = 0.f;
-      if (key <= q && q < S) p = expf(sc[r] * inv_scale - Ls[ql]);
+      if (key <= q && q < S) p = expf(attn_score<T>(sc[r], mul) - Ls[ql]);
       sc[r] = p;
       dp[r] = p * (dp[r] - Ds[ql]) * inv_scale;
     }
@@ -764,11 +882,11 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dkdv_mfma(AttnBwdArgs a) {
     for (int r = 0; r < 16; ++r) {
       const int kk = k_lo + 32 * wk + d_row(r, lane);
       if (kk < S) {
-        float* row = a.dqkv + (static_cast<long long>(b) * S + kk) * 3 * d + h * DK;
+        T* row = static_cast<T*>(a.dqkv) + (static_cast<long long>(b) * S + kk) * 3 * d + h * DK;
 #pragma unroll
         for (int j = 0; j < NJ; ++j) {
-          row[d + 32 * j + l32] = dk[j][r] + red[(((wk * 2 + 1) * NJ + j) * 16 + r) * 64 + lane];
-          row[2 * d + 32 * j + l32] = dv[j][r] + red[(((wk * 2 + 0) * NJ + j) * 16 + r) * 64 + lane];
+          row[d + 32 * j + l32] = static_cast<T>(dk[j][r] + red[(((wk * 2 + 1) * NJ + j) * 16 + r) * 64 + lane]);
+          row[2 * d + 32 * j + l32] = static_cast<T>(dv[j][r] + red[(((wk * 2 + 0) * NJ + j) * 16 + r) * 64 + lane]);
         }
       }
     }
@@ -777,7 +895,7 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dkdv_mfma(AttnBwdArgs a) {
 
 // dQ of 64 queries; the key tiles up to the query tile. Wave w = (wk, wq) = (w / 2, w % 2)
 // computes Sᵀ (keys as rows) so that its registers feed dQ = dS·K as the A operand.
-template <int DK>
+template <int DK, typename T>
 __global__ __launch_bounds__(256) void attn_bwd_dq_mfma(AttnBwdArgs a) {
   extern __shared__ float lds[];
   constexpr int P = DK + 1, NJ = DK / 32;
@@ -790,8 +908,10 @@ __global__ __launch_bounds__(256) void attn_bwd_dq_mfma(AttnBwdArgs a) {
   const int bh = blockIdx.y, b = bh / a.H, h = bh - (bh / a.H) * a.H;
   const int S = a.S, q_lo = blockIdx.x * kAT;
   const long long hoff = static_cast<long long>(bh) * S * DK;
-  tile_rows<DK>(Qs, a.q + hoff, q_lo, S);
-  tile_merged<DK>(Os, a.dout, b, h, a.H, q_lo, S);
+  const T* kg = static_cast<const T*>(a.k);
+  const T* vg = static_cast<const T*>(a.v);
+  tile_rows<DK>(Qs, static_cast<const T*>(a.q) + hoff, q_lo, S);
+  tile_merged<DK>(Os, static_cast<const T*>(a.dout), b, h, a.H, q_lo, S);
   const int q = q_lo + 32 * wq + l32;  // this lane's query (column of Sᵀ)
   const float lse = q < S ? a.lse[static_cast<long long>(bh) * S + q] : 0.f;
   const float dd = q < S ? a.dvec[static_cast<long long>(bh) * S + q] : 0.f;
@@ -801,18 +921,18 @@ __global__ __launch_bounds__(256) void attn_bwd_dq_mfma(AttnBwdArgs a) {
 #pragma unroll
     for (int r = 0; r < 16; ++r) dq[j][r] = 0.f;
   const int k_end = min(S, q_lo + kAT);
-  const float inv_scale = 1.0f / a.scale;
-  TileRegs<DK> nk, nv;
-  nk.load(a.k + hoff, DK, 0, S);
-  nv.load(a.v + hoff, DK, 0, S);
+  const float inv_scale = 1.0f / a.scale, mul = score_mul<T>(a.scale);
+  TileRegs<DK, T> nk, nv;
+  nk.load(kg + hoff, DK, 0, S);
+  nv.load(vg + hoff, DK, 0, S);
   for (int k_lo = 0; k_lo < k_end; k_lo += kAT) {
     __syncthreads();  // every wave is done with the previous tile
     nk.store(Ks);
     nv.store(Vs);
     __syncthreads();
     if (k_lo + kAT < k_end) {
-      nk.load(a.k + hoff, DK, k_lo + kAT, S);
-      nv.load(a.v + hoff, DK, k_lo + kAT, S);
+      nk.load(kg + hoff, DK, k_lo + kAT, S);
+      nv.load(vg + hoff, DK, k_lo + kAT, S);
     }
     floatx16 sc, dp;
 #pragma unroll
@@ -830,7 +950,7 @@ __global__ __launch_bounds__(256) void attn_bwd_dq_mfma(AttnBwdArgs a) {
     for (int r = 0; r < 16; ++r) {
       const int kk = k_lo + 32 * wk + d_row(r, lane);
       float p = 0.f;
-      if (kk <= q && q < S) p = expf(sc[r] * inv_scale - lse);
+      if (kk <= q && q < S) p = expf(attn_score<T>(sc[r], mul) - lse);
       dp[r] = p * (dp[r] - dd) * inv_scale;
     }
     // dQ[q][c] += Σ_key dS[q][key]·K[key][c]
@@ -857,51 +977,55 @@ __global__ __launch_bounds__(256) void attn_bwd_dq_mfma(AttnBwdArgs a) {
     for (int r = 0; r < 16; ++r) {
       const int qq = q_lo + 32 * wq + d_row(r, lane);
       if (qq < S) {
-        float* row = a.dqkv + (static_cast<long long>(b) * S + qq) * 3 * d + h * DK;
+        T* row = static_cast<T*>(a.dqkv) + (static_cast<long long>(b) * S + qq) * 3 * d + h * DK;
 #pragma unroll
-        for (int j = 0; j < NJ; ++j) row[32 * j + l32] = dq[j][r] + red[((wq * NJ + j) * 16 + r) * 64 + lane];
+        for (int j = 0; j < NJ; ++j)
+          row[32 * j + l32] = static_cast<T>(dq[j][r] + red[((wq * NJ + j) * 16 + r) * 64 + lane]);
       }
     }
   }
 }
 
-template <int DK>
+template <int DK, typename T>
 int attn_bwd_mfma(const AttnBwdArgs& a, hipStream_t st) {
   constexpr size_t lds = attn_mfma_lds<DK>();
   static bool attr = false;
   if (!attr) {
-    NML_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(&attn_bwd_dkdv_mfma<DK>),
+    NML_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(&attn_bwd_dkdv_mfma<DK, T>),
                                 hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds)));
-    NML_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(&attn_bwd_dq_mfma<DK>),
+    NML_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(&attn_bwd_dq_mfma<DK, T>),
                                 hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds)));
     attr = true;
   }
   const dim3 grid((a.S + kAT - 1) / kAT, a.B * a.H);
-  attn_bwd_dkdv_mfma<DK><<<grid, 256, lds, st>>>(a);
+  attn_bwd_dkdv_mfma<DK, T><<<grid, 256, lds, st>>>(a);
   NML_LAUNCHED();
-  attn_bwd_dq_mfma<DK><<<grid, 256, lds, st>>>(a);
+  attn_bwd_dq_mfma<DK, T><<<grid, 256, lds, st>>>(a);
   NML_LAUNCHED();
   return 0;
 }
 
-template <int DK>
+template <int DK, typename T>
 int attn_bwd_dk(const AttnBwdArgs& a, hipStream_t st) {
   if constexpr (DK == 64 || DK == 128) {
-    if (!std::getenv("NIMBLEML_ATTN_BWD_VALU")) return attn_bwd_mfma<DK>(a, st);
+    if (!std::getenv("NIMBLEML_ATTN_BWD_VALU")) return attn_bwd_mfma<DK, T>(a, st);
   }
   constexpr int BT = DK >= 128 ? 16 : 32;
   const dim3 grid((a.S + BT - 1) / BT, a.B * a.H);
-  attn_bwd_dkdv_kernel<DK, BT><<<grid, 256, 0, st>>>(a);
+  attn_bwd_dkdv_kernel<DK, BT, T><<<grid, 256, 0, st>>>(a);
   NML_LAUNCHED();
-  attn_bwd_dq_kernel<DK, BT><<<grid, 256, 0, st>>>(a);
+  attn_bwd_dq_kernel<DK, BT, T><<<grid, 256, 0, st>>>(a);
   NML_LAUNCHED();
   return 0;
 }
 
 // --------------------------------------------------------------- RoPE backward
-__global__ __launch_bounds__(256) void rope_bwd_kernel(float* __restrict__ dqkv, int rows, int S,
-                                                       int H, int dk, const float* __restrict__ cs,
-                                                       const float* __restrict__ sn) {
+// The inverse rotation (utils/rope.py with inverse=True: sin negated), each product and
+// sum in T (fp16 rounding points of apply_rope_flat).
+template <typename T>
+__global__ __launch_bounds__(256) void rope_bwd_kernel(T* __restrict__ dqkv, int rows, int S,
+                                                       int H, int dk, const T* __restrict__ cs,
+                                                       const T* __restrict__ sn) {
 #pragma clang fp contract(off)
   const int half = dk / 2;
   const long long n = static_cast<long long>(rows) * 2 * H * half;
@@ -914,78 +1038,124 @@ __global__ __launch_bounds__(256) void rope_bwd_kernel(float* __restrict__ dqkv,
   const int r = static_cast<int>(u / (2 * H));
   const int s = r % S;
   const int d = H * dk;
-  float* p = dqkv + static_cast<long long>(r) * 3 * d + which * d + h * dk;
-  const float c = cs[static_cast<long long>(s) * half + i], si = sn[static_cast<long long>(s) * half + i];
-  const float x1 = p[i], x2 = p[i + half];
-  p[i] = x1 * c + x2 * si;
-  p[i + half] = x2 * c - x1 * si;
+  T* p = dqkv + static_cast<long long>(r) * 3 * d + which * d + h * dk;
+  const float c = static_cast<float>(cs[static_cast<long long>(s) * half + i]);
+  const float si = static_cast<float>(sn[static_cast<long long>(s) * half + i]);
+  const float x1 = static_cast<float>(p[i]), x2 = static_cast<float>(p[i + half]);
+  p[i] = static_cast<T>(rnd<T>(x1 * c) + rnd<T>(x2 * si));
+  p[i + half] = static_cast<T>(rnd<T>(x2 * c) - rnd<T>(x1 * si));
 }
 
 // ---------------------------------------------------------- embedding backward
-__global__ __launch_bounds__(256) void embed_bwd_tok_kernel(const float* __restrict__ g,
+template <typename T>
+__global__ __launch_bounds__(256) void embed_bwd_tok_kernel(const T* __restrict__ g,
                                                             const int64_t* __restrict__ ids,
                                                             float* __restrict__ demb, int d, int V) {
   const int r = blockIdx.x;
   const long long id = ids[r];
   if (id < 0 || id >= V) return;
   for (int c = threadIdx.x; c < d; c += 256)
-    atomicAdd(demb + id * d + c, g[static_cast<long long>(r) * d + c]);
+    atomicAdd(demb + id * d + c, static_cast<float>(g[static_cast<long long>(r) * d + c]));
 }
 
-__global__ __launch_bounds__(256) void embed_bwd_pos_kernel(const float* __restrict__ g,
+template <typename T>
+__global__ __launch_bounds__(256) void embed_bwd_pos_kernel(const T* __restrict__ g,
                                                             float* __restrict__ dpos, int B, int S,
                                                             int d) {
   const int s = blockIdx.y, c = blockIdx.x * 256 + threadIdx.x;
   if (c >= d) return;
   float v = 0.f;
-  for (int b = 0; b < B; ++b) v += g[(static_cast<long long>(b) * S + s) * d + c];
+  for (int b = 0; b < B; ++b) v += static_cast<float>(g[(static_cast<long long>(b) * S + s) * d + c]);
   dpos[static_cast<long long>(s) * d + c] += v;
 }
 
-bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
+template <typename S, typename D>
+__global__ __launch_bounds__(256) void convert_kernel(const S* __restrict__ src, D* __restrict__ dst,
+                                                      size_t n) {
+  const size_t i = static_cast<size_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (i < n) dst[i] = static_cast<D>(static_cast<float>(src[i]));
+}
 
 }  // namespace
 
-int launch_gemm_bwd(const GemmBwdArgs& g, bool a_kc, bool b_kc, int out, hipStream_t st) {
+int launch_gemm_bwd(int dt, const GemmBwdArgs& g, bool a_kc, bool b_kc, int out, hipStream_t st) {
   if (g.M == 0 || g.N == 0) return 0;
   NML_REQUIRE(g.K > 0, "gemm_bwd: K must be positive");
-  NML_REQUIRE(aligned16(g.a) && aligned16(g.b) && g.lda % 4 == 0 && g.ldb % 4 == 0,
-              "gemm_bwd: operands must be 16-byte aligned with strides a multiple of 4");
+  const uintptr_t al = dt == F16 ? 7 : 15;
+  NML_REQUIRE(((reinterpret_cast<uintptr_t>(g.a) | reinterpret_cast<uintptr_t>(g.b)) & al) == 0 &&
+                  g.lda % 4 == 0 && g.ldb % 4 == 0,
+              "gemm_bwd: operands must be aligned to 4 elements with strides a multiple of 4");
   NML_REQUIRE(a_kc ? g.K % 4 == 0 : g.M % 4 == 0, "gemm_bwd: A's contiguous extent must be a multiple of 4");
   NML_REQUIRE(b_kc ? g.K % 4 == 0 : g.N % 4 == 0, "gemm_bwd: B's contiguous extent must be a multiple of 4");
   NML_REQUIRE(out != GB_GELU || g.aux != nullptr, "gemm_bwd: the GELU backward needs the pre-activation");
-  if (a_kc) return b_kc ? gemm_bwd_out<true, true>(g, out, st) : gemm_bwd_out<true, false>(g, out, st);
-  return b_kc ? gemm_bwd_out<false, true>(g, out, st) : gemm_bwd_out<false, false>(g, out, st);
+  if (dt == F16) {
+    if (a_kc) return b_kc ? gemm_bwd_out<true, true, half_t>(g, out, st) : gemm_bwd_out<true, false, half_t>(g, out, st);
+    return b_kc ? gemm_bwd_out<false, true, half_t>(g, out, st) : gemm_bwd_out<false, false, half_t>(g, out, st);
+  }
+  if (a_kc) return b_kc ? gemm_bwd_out<true, true, float>(g, out, st) : gemm_bwd_out<true, false, float>(g, out, st);
+  return b_kc ? gemm_bwd_out<false, true, float>(g, out, st) : gemm_bwd_out<false, false, float>(g, out, st);
+}
+
+int launch_convert(int src_dt, const void* src, int dst_dt, void* dst, size_t n, hipStream_t st) {
+  if (n == 0) return 0;
+  const size_t blocks = (n + 255) / 256;
+  NML_REQUIRE(blocks <= 0x7fffffff, "convert: %zu elements exceed one launch", n);
+  if (src_dt == F16 && dst_dt == F32)
+    convert_kernel<half_t, float><<<static_cast<int>(blocks), 256, 0, st>>>(
+        static_cast<const half_t*>(src), static_cast<float*>(dst), n);
+  else if (src_dt == F32 && dst_dt == F16)
+    convert_kernel<float, half_t><<<static_cast<int>(blocks), 256, 0, st>>>(
+        static_cast<const float*>(src), static_cast<half_t*>(dst), n);
+  else {
+    set_error("convert: unsupported dtypes %d -> %d", src_dt, dst_dt);
+    return -1;
+  }
+  NML_LAUNCHED();
+  return 0;
 }
 
 int rmsnorm_bwd_parts(int rows) { return (rows + kNormRowsPerBlock - 1) / kNormRowsPerBlock; }
 
-int launch_rmsnorm_bwd(const float* dy, const float* x, const float* gamma, float* dx, int acc,
+int launch_rmsnorm_bwd(int dt, const void* dy, const void* x, const void* gamma, void* dx, int acc,
                        float* dgamma, float* part, int rows, int d, float eps, hipStream_t st) {
   if (rows == 0) return 0;
-  NML_REQUIRE(d > 0 && d <= 256 * 32, "rmsnorm backward: d=%d outside (0, 8192]", d);
   const int blocks = rmsnorm_bwd_parts(rows);
   const int nv = (d / 4 + 63) / 64;
+  const uintptr_t al = dt == F16 ? 7 : 15;
   const bool vec_ok = d % 4 == 0 && ((reinterpret_cast<uintptr_t>(dy) | reinterpret_cast<uintptr_t>(x) |
                                       reinterpret_cast<uintptr_t>(gamma) |
-                                      reinterpret_cast<uintptr_t>(dx)) & 15) == 0;
+                                      reinterpret_cast<uintptr_t>(dx)) & al) == 0;
   if (vec_ok && nv <= 8) {
     const int wblocks = (blocks + 3) / 4;
-#define NML_NORM_BWD_W(NVV) \
-  rmsnorm_bwd_wave_kernel<NVV><<<wblocks, 256, 0, st>>>(dy, x, gamma, dx, acc, part, rows, d, eps)
-    if (nv <= 1) NML_NORM_BWD_W(1);
-    else if (nv <= 2) NML_NORM_BWD_W(2);
-    else if (nv <= 4) NML_NORM_BWD_W(4);
-    else NML_NORM_BWD_W(8);
+#define NML_NORM_BWD_W(T, NVV)                                                                   \
+  rmsnorm_bwd_wave_kernel<T, NVV><<<wblocks, 256, 0, st>>>((const T*)dy, (const T*)x, (const T*)gamma, \
+                                                          (T*)dx, acc, part, rows, d, eps)
+    if (dt == F16) {
+      if (nv <= 1) NML_NORM_BWD_W(half_t, 1);
+      else if (nv <= 2) NML_NORM_BWD_W(half_t, 2);
+      else if (nv <= 4) NML_NORM_BWD_W(half_t, 4);
+      else NML_NORM_BWD_W(half_t, 8);
+    } else {
+      if (nv <= 1) NML_NORM_BWD_W(float, 1);
+      else if (nv <= 2) NML_NORM_BWD_W(float, 2);
+      else if (nv <= 4) NML_NORM_BWD_W(float, 4);
+      else NML_NORM_BWD_W(float, 8);
+    }
 #undef NML_NORM_BWD_W
     NML_LAUNCHED();
     parts_reduce_kernel<<<(d + 31) / 32, 256, 0, st>>>(part, blocks, d, dgamma);
     NML_LAUNCHED();
     return 0;
   }
+  NML_REQUIRE(dt == F32, "rmsnorm backward: fp16 needs d %% 4 == 0, d <= 2048 and aligned rows");
+  NML_REQUIRE(d > 0 && d <= 256 * 32, "rmsnorm backward: d=%d outside (0, 8192]", d);
   const int nc = (d + 255) / 256;
+  const float* fdy = static_cast<const float*>(dy);
+  const float* fx = static_cast<const float*>(x);
+  const float* fg = static_cast<const float*>(gamma);
+  float* fdx = static_cast<float*>(dx);
 #define NML_NORM_BWD(NCV) \
-  rmsnorm_bwd_kernel<NCV><<<blocks, 256, 0, st>>>(dy, x, gamma, dx, acc, part, rows, d, eps)
+  rmsnorm_bwd_kernel<NCV><<<blocks, 256, 0, st>>>(fdy, fx, fg, fdx, acc, part, rows, d, eps)
   if (nc <= 1) NML_NORM_BWD(1);
   else if (nc <= 2) NML_NORM_BWD(2);
   else if (nc <= 4) NML_NORM_BWD(4);
@@ -1001,57 +1171,86 @@ int launch_rmsnorm_bwd(const float* dy, const float* x, const float* gamma, floa
 
 int colsum_parts(int rows) { return (rows + kColRows - 1) / kColRows; }
 
-int launch_colsum(const float* a, long long lda, int rows, int n, float* out, float* part,
+int launch_colsum(int dt, const void* a, long long lda, int rows, int n, float* out, float* part,
                   hipStream_t st) {
   if (rows == 0 || n == 0) return 0;
   const int parts = colsum_parts(rows);
-  colsum_part_kernel<<<dim3((n + 255) / 256, parts), 256, 0, st>>>(a, lda, rows, n, part);
+  const dim3 grid((n + 255) / 256, parts);
+  if (dt == F16)
+    colsum_part_kernel<half_t><<<grid, 256, 0, st>>>(static_cast<const half_t*>(a), lda, rows, n, part);
+  else
+    colsum_part_kernel<float><<<grid, 256, 0, st>>>(static_cast<const float*>(a), lda, rows, n, part);
   NML_LAUNCHED();
   parts_reduce_kernel<<<(n + 31) / 32, 256, 0, st>>>(part, parts, n, out);
   NML_LAUNCHED();
   return 0;
 }
 
-int launch_ce_grad(float* logits, int rows, int V, const int64_t* labels, long long ignore_index,
-                   int has_ignore, float scale, hipStream_t st) {
+int launch_ce_grad(int dt, void* logits, int rows, int V, const int64_t* labels,
+                   long long ignore_index, int has_ignore, float scale, hipStream_t st) {
   if (rows == 0) return 0;
-  ce_grad_kernel<<<rows, 256, 0, st>>>(logits, V, labels, ignore_index, has_ignore, scale);
+  if (dt == F16)
+    ce_grad_kernel<half_t><<<rows, 256, 0, st>>>(static_cast<half_t*>(logits), V, labels, ignore_index,
+                                                 has_ignore, scale);
+  else
+    ce_grad_kernel<float><<<rows, 256, 0, st>>>(static_cast<float*>(logits), V, labels, ignore_index,
+                                                has_ignore, scale);
   NML_LAUNCHED();
   return 0;
 }
 
-int launch_attention_backward(const AttnBwdArgs& a, hipStream_t st) {
-  if (a.B * a.S == 0) return 0;
+template <typename T>
+int attention_backward_t(const AttnBwdArgs& a, hipStream_t st) {
   const long long pairs = static_cast<long long>(a.B) * a.S * a.H;
-  attn_bwd_dot_kernel<<<static_cast<int>((pairs + 3) / 4), 256, 0, st>>>(a);
+  attn_bwd_dot_kernel<T><<<static_cast<int>((pairs + 3) / 4), 256, 0, st>>>(a);
   NML_LAUNCHED();
   switch (a.dk) {
-    case 8: return attn_bwd_dk<8>(a, st);
-    case 16: return attn_bwd_dk<16>(a, st);
-    case 32: return attn_bwd_dk<32>(a, st);
-    case 64: return attn_bwd_dk<64>(a, st);
-    case 128: return attn_bwd_dk<128>(a, st);
+    case 8: return attn_bwd_dk<8, T>(a, st);
+    case 16: return attn_bwd_dk<16, T>(a, st);
+    case 32: return attn_bwd_dk<32, T>(a, st);
+    case 64: return attn_bwd_dk<64, T>(a, st);
+    case 128: return attn_bwd_dk<128, T>(a, st);
   }
   set_error("attention backward: head_dim %d unsupported (8, 16, 32, 64, 128)", a.dk);
   return -1;
 }
 
-int launch_rope_backward(float* dqkv, int rows, int S, int H, int dk, const float* cos,
-                         const float* sin, hipStream_t st) {
+int launch_attention_backward(int dt, const AttnBwdArgs& a, hipStream_t st) {
+  if (a.B * a.S == 0) return 0;
+  return dt == F16 ? attention_backward_t<half_t>(a, st) : attention_backward_t<float>(a, st);
+}
+
+int launch_rope_backward(int dt, void* dqkv, int rows, int S, int H, int dk, const void* cos,
+                         const void* sin, hipStream_t st) {
   const long long n = static_cast<long long>(rows) * 2 * H * (dk / 2);
   if (n == 0) return 0;
-  rope_bwd_kernel<<<static_cast<int>((n + 255) / 256), 256, 0, st>>>(dqkv, rows, S, H, dk, cos, sin);
+  const int blocks = static_cast<int>((n + 255) / 256);
+  if (dt == F16)
+    rope_bwd_kernel<half_t><<<blocks, 256, 0, st>>>(static_cast<half_t*>(dqkv), rows, S, H, dk,
+                                                    static_cast<const half_t*>(cos),
+                                                    static_cast<const half_t*>(sin));
+  else
+    rope_bwd_kernel<float><<<blocks, 256, 0, st>>>(static_cast<float*>(dqkv), rows, S, H, dk,
+                                                   static_cast<const float*>(cos),
+                                                   static_cast<const float*>(sin));
   NML_LAUNCHED();
   return 0;
 }
 
-int launch_embed_backward(const float* g, const int64_t* ids, float* demb, float* dpos, int B,
+int launch_embed_backward(int dt, const void* g, const int64_t* ids, float* demb, float* dpos, int B,
                           int S, int d, int V, hipStream_t st) {
   if (B * S == 0) return 0;
-  embed_bwd_tok_kernel<<<B * S, 256, 0, st>>>(g, ids, demb, d, V);
+  if (dt == F16)
+    embed_bwd_tok_kernel<half_t><<<B * S, 256, 0, st>>>(static_cast<const half_t*>(g), ids, demb, d, V);
+  else
+    embed_bwd_tok_kernel<float><<<B * S, 256, 0, st>>>(static_cast<const float*>(g), ids, demb, d, V);
   NML_LAUNCHED();
   if (dpos) {
-    embed_bwd_pos_kernel<<<dim3((d + 255) / 256, S), 256, 0, st>>>(g, dpos, B, S, d);
+    const dim3 grid((d + 255) / 256, S);
+    if (dt == F16)
+      embed_bwd_pos_kernel<half_t><<<grid, 256, 0, st>>>(static_cast<const half_t*>(g), dpos, B, S, d);
+    else
+      embed_bwd_pos_kernel<float><<<grid, 256, 0, st>>>(static_cast<const float*>(g), dpos, B, S, d);
     NML_LAUNCHED();
   }
   return 0;

@@ -1,5 +1,6 @@
-// Training on the device (float32 models): compute_loss keeping what the backward needs,
-// then loss.backward() into a gradient arena laid out like the parameter arena
+// Training on the device (float32 and float16 models): compute_loss keeping what the
+// backward needs, then loss.backward() into a float32 gradient arena laid out like the
+// parameter arena (one element per parameter element)
 // (models/gpt.py:123-137 with the reference's autograd: losses/cross_entropy.py:109-192,
 // kernels/fused_tied_crossentropy.py:27-48, neural_network/_fused_arrays.py:129-377,
 // kernels/fused_rmsnorm.py:208-217, kernels/embedding_scatter.py:39-60).
@@ -27,8 +28,9 @@
 namespace nml {
 
 struct TrainState {
-  Buf grads;    // float32, same layout and size as the parameter arena
-  Buf moments;  // AdamW first and second moments, two more arenas of that layout
+  Buf grads;    // float32, one element per parameter element, the parameter arena's layout
+  Buf moments;  // AdamW first and second moments, two more float32 arenas of that layout
+  Buf masters;  // fp16 models: float32 master copies of the parameters (optimizers/adam.py:75-81)
   Buf acts;     // saved activations of the last loss_train
   Buf scratch;  // backward scratch
   Buf io;       // ids and labels of the last loss_train, loss accumulators
@@ -43,6 +45,7 @@ void train_release(nml_model* m) {
   if (!m->train) return;
   m->train->grads.release();
   m->train->moments.release();
+  m->train->masters.release();
   m->train->acts.release();
   m->train->scratch.release();
   m->train->io.release();
@@ -52,20 +55,22 @@ void train_release(nml_model* m) {
 
 namespace {
 
-// Saved activations of R rows, carved from one buffer.
+// Saved activations of R rows (storage type, es bytes each), carved from one buffer; the
+// log-sum-exp rows are float32.
 struct Saved {
-  float *x, *n1, *q, *k, *v, *att, *lse, *xm, *n2, *pre, *hid;  // layer 0; + l·stride
-  size_t stride;                                                  // floats per layer
-  float* xl;  // X[L]
-  float* hf;  // final-normed
+  char *x, *n1, *q, *k, *v, *att, *xm, *n2, *pre, *hid;  // layer 0; + l·stride
+  float* lse;
+  size_t stride;  // bytes per layer
+  char* xl;       // X[L]
+  char* hf;       // final-normed
 };
 
-size_t saved_floats(const nml_model* m, int B, int S, Saved* s, float* base) {
-  const size_t R = (size_t)B * S, rd = align256(R * m->d * 4) / 4, rf = align256(R * m->F * 4) / 4;
-  const size_t rl = align256((size_t)B * m->H * S * 4) / 4;
+size_t saved_bytes(const nml_model* m, int B, int S, Saved* s, char* base) {
+  const size_t R = (size_t)B * S, rd = align256(R * m->d * m->es), rf = align256(R * m->F * m->es);
+  const size_t rl = align256((size_t)B * m->H * S * 4);
   const size_t per = 8 * rd + 2 * rf + rl;
   if (s) {
-    float* p = base;
+    char* p = base;
     s->x = p; p += rd;
     s->n1 = p; p += rd;
     s->q = p; p += rd;
@@ -76,7 +81,7 @@ size_t saved_floats(const nml_model* m, int B, int S, Saved* s, float* base) {
     s->n2 = p; p += rd;
     s->pre = p; p += rf;
     s->hid = p; p += rf;
-    s->lse = p;
+    s->lse = reinterpret_cast<float*>(p);
     s->stride = per;
     s->xl = base + per * m->L;
     s->hf = s->xl + rd;
@@ -84,29 +89,35 @@ size_t saved_floats(const nml_model* m, int B, int S, Saved* s, float* base) {
   return per * m->L + 2 * rd;
 }
 
-inline float* at(float* p, const Saved& s, int l) { return p + s.stride * l; }
+inline char* at(char* p, const Saved& s, int l) { return p + s.stride * l; }
+inline float* at(float* p, const Saved& s, int l) {
+  return reinterpret_cast<float*>(reinterpret_cast<char*>(p) + s.stride * l);
+}
 
-// Gradient of parameter (kind, layer): same offset in the gradient arena.
-float* grad_of(nml_model* m, void* param) {
-  return reinterpret_cast<float*>(static_cast<char*>(m->train->grads.p) +
-                                  (static_cast<char*>(param) - static_cast<char*>(m->arena)));
+// The float32 arenas hold one element per parameter element: parameter byte offset / es.
+size_t f32_bytes(const nml_model* m) { return m->arena_bytes / m->es * 4; }
+size_t f32_off(const nml_model* m, const void* param) {
+  return static_cast<size_t>(static_cast<const char*>(param) - static_cast<const char*>(m->arena)) /
+         m->es * 4;
+}
+float* grad_of(nml_model* m, const void* param) {
+  return reinterpret_cast<float*>(static_cast<char*>(m->train->grads.p) + f32_off(m, param));
 }
 
 int ensure_train(nml_model* m) {
-  NML_REQUIRE(m->dt == F32, "training on the device needs a float32 model");
   if (!m->train) m->train = new TrainState();
   TrainState* t = m->train;
   if (!t->grads.p) {
-    NML_TRY(t->grads.ensure(m->arena_bytes));
-    NML_HIP(hipMemsetAsync(t->grads.p, 0, m->arena_bytes, nml::stream()));
+    NML_TRY(t->grads.ensure(f32_bytes(m)));
+    NML_HIP(hipMemsetAsync(t->grads.p, 0, f32_bytes(m), nml::stream()));
   }
   return 0;
 }
 
-// Rows per logits chunk: at most 512 MiB of float32 logits at once.
+// Rows per logits chunk: at most 512 MiB of logits at once.
 size_t logits_chunk(const nml_model* m, size_t R) {
   size_t chunk = R;
-  while (chunk > 1 && chunk * m->V * 4 > ((size_t)512 << 20)) chunk = (chunk + 1) / 2;
+  while (chunk > 1 && chunk * m->V * m->es > ((size_t)512 << 20)) chunk = (chunk + 1) / 2;
   return chunk;
 }
 
@@ -126,9 +137,8 @@ LinearArgs lin(const void* x, long long lda, const void* w, const void* bias, vo
   return a;
 }
 
-GemmBwdArgs gb(const float* a, long long lda, const float* b, long long ldb, float* c,
-               long long ldc, int M, int N, int K, const float* aux = nullptr,
-               long long ldaux = 0) {
+GemmBwdArgs gb(const void* a, long long lda, const void* b, long long ldb, void* c, long long ldc,
+               int M, int N, int K, const void* aux = nullptr, long long ldaux = 0) {
   GemmBwdArgs g{};
   g.a = a;
   g.lda = lda;
@@ -144,6 +154,19 @@ GemmBwdArgs gb(const float* a, long long lda, const float* b, long long ldb, flo
   return g;
 }
 
+// Parameter element ranges of the arena around the rotary tables (buffers, not
+// parameters): [first, second) pairs in elements.
+void param_ranges(const nml_model* m, size_t (&r)[2][2]) {
+  const size_t total = m->arena_bytes / m->es;
+  const size_t lo = static_cast<size_t>(static_cast<char*>(m->rope_cos) - static_cast<char*>(m->arena)) / m->es;
+  const size_t hi = (static_cast<size_t>(static_cast<char*>(m->rope_sin) - static_cast<char*>(m->arena)) +
+                     align256(param_elems(m, NML_P_ROPE_SIN) * m->es)) / m->es;
+  r[0][0] = 0;
+  r[0][1] = lo;
+  r[1][0] = hi;
+  r[1][1] = total;
+}
+
 }  // namespace
 
 }  // namespace nml
@@ -155,7 +178,7 @@ extern "C" {
 int nml_model_zero_grad(nml_model* m) {
   NML_TRY(check_ready(m));
   NML_TRY(ensure_train(m));
-  NML_HIP(hipMemsetAsync(m->train->grads.p, 0, m->arena_bytes, nml::stream()));
+  NML_HIP(hipMemsetAsync(m->train->grads.p, 0, f32_bytes(m), nml::stream()));
   NML_HIP(hipStreamSynchronize(nml::stream()));
   return 0;
 }
@@ -179,15 +202,16 @@ int nml_model_loss_train(nml_model* m, const int64_t* ids, const int64_t* labels
   NML_TRY(ensure_train(m));
   TrainState* t = m->train;
   t->saved = false;
-  const int B = (int)batch, S = (int)seq, R = B * S, d = m->d, F = m->F;
+  const int B = (int)batch, S = (int)seq, R = B * S, d = m->d, F = m->F, dt = m->dt;
+  const size_t es = m->es;
   if (R == 0) {
     *loss = 0.0;
     return 0;
   }
   hipStream_t st = nml::stream();
   Saved sv;
-  NML_TRY(t->acts.ensure(saved_floats(m, B, S, nullptr, nullptr) * 4));
-  saved_floats(m, B, S, &sv, static_cast<float*>(t->acts.p));
+  NML_TRY(t->acts.ensure(saved_bytes(m, B, S, nullptr, nullptr)));
+  saved_bytes(m, B, S, &sv, static_cast<char*>(t->acts.p));
   // io: ids, labels, then err / loss accumulators, per-row loss and validity
   const size_t ib = align256((size_t)R * 8), rb = align256((size_t)R * 4);
   NML_TRY(t->io.ensure(2 * ib + 512 + 2 * rb));
@@ -202,21 +226,21 @@ int nml_model_loss_train(nml_model* m, const int64_t* ids, const int64_t* labels
   NML_HIP(hipMemcpyAsync(dlab, labels, (size_t)R * 8, hipMemcpyDeviceToDevice, st));
   NML_HIP(hipMemsetAsync(err, 0, sizeof(int), st));
 
-  NML_TRY(launch_embed(F32, dids, m->emb, posw(m), nullptr, sv.x, B, S, d, m->V, m->P, err, st));
+  NML_TRY(launch_embed(dt, dids, m->emb, posw(m), nullptr, sv.x, B, S, d, m->V, m->P, err, st));
   const long long sb = (long long)m->H * S * m->dk, sh = (long long)S * m->dk;
   for (int l = 0; l < m->L; ++l) {
     const Layer& w = m->layers[l];
-    float *x = at(sv.x, sv, l), *n1 = at(sv.n1, sv, l), *q = at(sv.q, sv, l),
-          *k = at(sv.k, sv, l), *v = at(sv.v, sv, l), *att = at(sv.att, sv, l),
-          *lse = at(sv.lse, sv, l), *xm = at(sv.xm, sv, l), *n2 = at(sv.n2, sv, l),
-          *pre = at(sv.pre, sv, l), *hid = at(sv.hid, sv, l);
-    float* xnext = l + 1 < m->L ? at(sv.x, sv, l + 1) : sv.xl;
-    NML_TRY(launch_rmsnorm(F32, x, w.ln1, n1, nullptr, nullptr, R, d, kEps, st));
+    char *x = at(sv.x, sv, l), *n1 = at(sv.n1, sv, l), *q = at(sv.q, sv, l), *k = at(sv.k, sv, l),
+         *v = at(sv.v, sv, l), *att = at(sv.att, sv, l), *xm = at(sv.xm, sv, l),
+         *n2 = at(sv.n2, sv, l), *pre = at(sv.pre, sv, l), *hid = at(sv.hid, sv, l);
+    float* lse = at(sv.lse, sv, l);
+    char* xnext = l + 1 < m->L ? at(sv.x, sv, l + 1) : sv.xl;
+    NML_TRY(launch_rmsnorm(dt, x, w.ln1, n1, nullptr, nullptr, R, d, kEps, st));
     LinearArgs qkv = lin(n1, d, w.wqkv, w.bqkv, nullptr, R, 3 * d, d, EPI_QKV);
     qkv.qkv = QKVDst{q, k, v, nullptr, sb, sh, S, m->H, m->dk, d, nullptr};
-    NML_TRY(launch_linear(F32, qkv, st));
+    NML_TRY(launch_linear(dt, qkv, st));
     if (rope_on(m))
-      NML_TRY(launch_rope(F32, q, k, sb, sh, B, m->H, S, m->dk, nullptr, nullptr, m->rope_cos,
+      NML_TRY(launch_rope(dt, q, k, sb, sh, B, m->H, S, m->dk, nullptr, nullptr, m->rope_cos,
                           m->rope_sin, m->P, st));
     AttnArgs a{};
     a.q = q;
@@ -231,22 +255,22 @@ int nml_model_loss_train(nml_model* m, const int64_t* ids, const int64_t* labels
     a.dk = m->dk;
     a.scale = sqrtf((float)m->dk);
     a.lse = lse;
-    NML_TRY(launch_attention_prefill(F32, a, st));
-    NML_TRY(launch_linear(F32, lin(att, d, w.wo, w.bo, xm, R, d, d, EPI_BIAS_RESID, x), st));
-    NML_TRY(launch_rmsnorm(F32, xm, w.ln2, n2, nullptr, nullptr, R, d, kEps, st));
-    NML_TRY(launch_linear(F32, lin(n2, d, w.w1, w.b1, pre, R, F, d, EPI_BIAS), st));
-    NML_TRY(launch_gelu(F32, pre, hid, nullptr, (size_t)R * F, st));
-    NML_TRY(launch_linear(F32, lin(hid, F, w.w2, w.b2, xnext, R, d, F, EPI_BIAS_RESID, xm), st));
+    NML_TRY(launch_attention_prefill(dt, a, st));
+    NML_TRY(launch_linear(dt, lin(att, d, w.wo, w.bo, xm, R, d, d, EPI_BIAS_RESID, x), st));
+    NML_TRY(launch_rmsnorm(dt, xm, w.ln2, n2, nullptr, nullptr, R, d, kEps, st));
+    NML_TRY(launch_linear(dt, lin(n2, d, w.w1, w.b1, pre, R, F, d, EPI_BIAS), st));
+    NML_TRY(launch_gelu(dt, pre, hid, nullptr, (size_t)R * F, st));
+    NML_TRY(launch_linear(dt, lin(hid, F, w.w2, w.b2, xnext, R, d, F, EPI_BIAS_RESID, xm), st));
   }
-  NML_TRY(launch_rmsnorm(F32, sv.xl, m->lnf, sv.hf, nullptr, nullptr, R, d, kEps, st));
+  NML_TRY(launch_rmsnorm(dt, sv.xl, m->lnf, sv.hf, nullptr, nullptr, R, d, kEps, st));
 
   const size_t chunk = logits_chunk(m, R);
-  NML_TRY(m->logits_ws.ensure(align256(chunk * m->V * 4)));
+  NML_TRY(m->logits_ws.ensure(align256(chunk * m->V * es)));
   for (size_t r0 = 0; r0 < (size_t)R; r0 += chunk) {
     const int n = (int)(((size_t)R - r0 < chunk) ? (size_t)R - r0 : chunk);
-    NML_TRY(launch_linear(F32, lin(sv.hf + r0 * d, d, m->emb, nullptr, m->logits_ws.p, n, m->V, d,
-                                   EPI_NONE), st));
-    NML_TRY(launch_ce_rows(F32, m->logits_ws.p, n, m->V, dlab + r0, ignore_index, has_ignore,
+    NML_TRY(launch_linear(dt, lin(sv.hf + r0 * d * es, d, m->emb, nullptr, m->logits_ws.p, n, m->V,
+                                  d, EPI_NONE), st));
+    NML_TRY(launch_ce_rows(dt, m->logits_ws.p, n, m->V, dlab + r0, ignore_index, has_ignore,
                            row_loss, row_valid, err, st));
     NML_TRY(launch_ce_reduce(row_loss, row_valid, n, acc, r0 > 0, st));
   }
@@ -273,71 +297,69 @@ int nml_model_backward(nml_model* m, double grad_scale) {
   NML_REQUIRE(m->train && m->train->saved,
               "backward: no saved forward (call nml_model_loss_train first)");
   TrainState* t = m->train;
-  const int B = t->B, S = t->S, R = B * S, d = m->d, F = m->F, V = m->V;
+  const int B = t->B, S = t->S, R = B * S, d = m->d, F = m->F, V = m->V, dt = m->dt;
+  const size_t es = m->es;
   if (t->n_valid <= 0.0) return 0;  // every label ignored: the loss is a constant 0
   hipStream_t st = nml::stream();
   Saved sv;
-  saved_floats(m, B, S, &sv, static_cast<float*>(t->acts.p));
+  saved_bytes(m, B, S, &sv, static_cast<char*>(t->acts.p));
   const size_t ib = align256((size_t)R * 8);
   const int64_t* dids = reinterpret_cast<const int64_t*>(t->io.p);
   const int64_t* dlab = reinterpret_cast<const int64_t*>(static_cast<char*>(t->io.p) + ib);
 
-  // scratch: G, DX (R, d); DQKV (R, 3d); DPRE (R, F); dvec (B, H, S); row-sum partials
-  const size_t rd = align256((size_t)R * d * 4), r3 = align256((size_t)R * 3 * d * 4),
-               rf = align256((size_t)R * F * 4), rv = align256((size_t)B * m->H * S * 4);
+  // scratch (storage type): G, DX (R, d); DQKV (R, 3d); DPRE (R, F); then float32 dvec
+  // (B, H, S) and row-sum partials
+  const size_t rd = align256((size_t)R * d * es), r3 = align256((size_t)R * 3 * d * es),
+               rf = align256((size_t)R * F * es), rv = align256((size_t)B * m->H * S * 4);
   const int widest = F > 3 * d ? F : 3 * d;
   const size_t pn = (size_t)(rmsnorm_bwd_parts(R) > colsum_parts(R) ? rmsnorm_bwd_parts(R)
                                                                      : colsum_parts(R)) *
                     widest;
   NML_TRY(t->scratch.ensure(2 * rd + r3 + rf + rv + align256(pn * 4)));
   char* sp = static_cast<char*>(t->scratch.p);
-  float* G = reinterpret_cast<float*>(sp);
-  float* DX = reinterpret_cast<float*>(sp + rd);
-  float* DQKV = reinterpret_cast<float*>(sp + 2 * rd);
-  float* DPRE = reinterpret_cast<float*>(sp + 2 * rd + r3);
+  char* G = sp;
+  char* DX = sp + rd;
+  char* DQKV = sp + 2 * rd;
+  char* DPRE = sp + 2 * rd + r3;
   float* DVEC = reinterpret_cast<float*>(sp + 2 * rd + r3 + rf);
   float* PART = reinterpret_cast<float*>(sp + 2 * rd + r3 + rf + rv);
-  const float* E = static_cast<const float*>(m->emb);
+  const void* E = m->emb;
   float* dE = grad_of(m, m->emb);
 
   // tied head + cross-entropy, chunk by chunk; dH lands in DX
   const float scale = static_cast<float>(grad_scale / t->n_valid);
   const size_t chunk = logits_chunk(m, R);
-  NML_TRY(m->logits_ws.ensure(align256(chunk * V * 4)));
-  float* lg = static_cast<float*>(m->logits_ws.p);
+  NML_TRY(m->logits_ws.ensure(align256(chunk * V * es)));
+  void* lg = m->logits_ws.p;
   for (size_t r0 = 0; r0 < (size_t)R; r0 += chunk) {
     const int n = (int)(((size_t)R - r0 < chunk) ? (size_t)R - r0 : chunk);
-    const float* h = sv.hf + r0 * d;
-    NML_TRY(launch_linear(F32, lin(h, d, E, nullptr, lg, n, V, d, EPI_NONE), st));
-    NML_TRY(launch_ce_grad(lg, n, V, dlab + r0, t->ignore_index, t->has_ignore, scale, st));
-    NML_TRY(launch_gemm_bwd(gb(lg, V, E, d, DX + r0 * d, d, n, d, V), true, false, GB_SET, st));
-    NML_TRY(launch_gemm_bwd(gb(lg, V, h, d, dE, d, V, d, n), false, false, GB_ADD, st));
+    const char* h = sv.hf + r0 * d * es;
+    NML_TRY(launch_linear(dt, lin(h, d, E, nullptr, lg, n, V, d, EPI_NONE), st));
+    NML_TRY(launch_ce_grad(dt, lg, n, V, dlab + r0, t->ignore_index, t->has_ignore, scale, st));
+    NML_TRY(launch_gemm_bwd(dt, gb(lg, V, E, d, DX + r0 * d * es, d, n, d, V), true, false, GB_SET, st));
+    NML_TRY(launch_gemm_bwd(dt, gb(lg, V, h, d, dE, d, V, d, n), false, false, GB_ADD, st));
   }
-  NML_TRY(launch_rmsnorm_bwd(DX, sv.xl, static_cast<const float*>(m->lnf), G, 0,
-                             grad_of(m, m->lnf), PART, R, d, kEps, st));
+  NML_TRY(launch_rmsnorm_bwd(dt, DX, sv.xl, m->lnf, G, 0, grad_of(m, m->lnf), PART, R, d, kEps, st));
 
   for (int l = m->L - 1; l >= 0; --l) {
     const Layer& w = m->layers[l];
-    const float *x = at(sv.x, sv, l), *n1 = at(sv.n1, sv, l), *q = at(sv.q, sv, l),
-                *k = at(sv.k, sv, l), *v = at(sv.v, sv, l), *att = at(sv.att, sv, l),
-                *lse = at(sv.lse, sv, l), *xm = at(sv.xm, sv, l), *n2 = at(sv.n2, sv, l),
-                *pre = at(sv.pre, sv, l), *hid = at(sv.hid, sv, l);
+    const char *x = at(sv.x, sv, l), *n1 = at(sv.n1, sv, l), *q = at(sv.q, sv, l),
+               *k = at(sv.k, sv, l), *v = at(sv.v, sv, l), *att = at(sv.att, sv, l),
+               *xm = at(sv.xm, sv, l), *n2 = at(sv.n2, sv, l), *pre = at(sv.pre, sv, l),
+               *hid = at(sv.hid, sv, l);
+    const float* lse = at(sv.lse, sv, l);
     // FFN (_fused_arrays.py:225-248)
-    NML_TRY(launch_gemm_bwd(gb(G, d, hid, F, grad_of(m, w.w2), F, d, F, R), false, false, GB_ADD, st));
-    NML_TRY(launch_colsum(G, d, R, d, grad_of(m, w.b2), PART, st));
-    NML_TRY(launch_gemm_bwd(gb(G, d, static_cast<const float*>(w.w2), F, DPRE, F, R, F, d, pre, F),
-                            true, false, GB_GELU, st));
-    NML_TRY(launch_gemm_bwd(gb(DPRE, F, n2, d, grad_of(m, w.w1), d, F, d, R), false, false, GB_ADD, st));
-    NML_TRY(launch_colsum(DPRE, F, R, F, grad_of(m, w.b1), PART, st));
-    NML_TRY(launch_gemm_bwd(gb(DPRE, F, static_cast<const float*>(w.w1), d, DX, d, R, d, F), true,
-                            false, GB_SET, st));
-    NML_TRY(launch_rmsnorm_bwd(DX, xm, static_cast<const float*>(w.ln2), G, 1, grad_of(m, w.ln2),
-                               PART, R, d, kEps, st));
+    NML_TRY(launch_gemm_bwd(dt, gb(G, d, hid, F, grad_of(m, w.w2), F, d, F, R), false, false, GB_ADD, st));
+    NML_TRY(launch_colsum(dt, G, d, R, d, grad_of(m, w.b2), PART, st));
+    NML_TRY(launch_gemm_bwd(dt, gb(G, d, w.w2, F, DPRE, F, R, F, d, pre, F), true, false, GB_GELU, st));
+    NML_TRY(launch_gemm_bwd(dt, gb(DPRE, F, n2, d, grad_of(m, w.w1), d, F, d, R), false, false, GB_ADD, st));
+    NML_TRY(launch_colsum(dt, DPRE, F, R, F, grad_of(m, w.b1), PART, st));
+    NML_TRY(launch_gemm_bwd(dt, gb(DPRE, F, w.w1, d, DX, d, R, d, F), true, false, GB_SET, st));
+    NML_TRY(launch_rmsnorm_bwd(dt, DX, xm, w.ln2, G, 1, grad_of(m, w.ln2), PART, R, d, kEps, st));
     // MHA (_fused_arrays.py:129-184)
-    NML_TRY(launch_gemm_bwd(gb(G, d, att, d, grad_of(m, w.wo), d, d, d, R), false, false, GB_ADD, st));
-    NML_TRY(launch_colsum(G, d, R, d, grad_of(m, w.bo), PART, st));
-    NML_TRY(launch_gemm_bwd(gb(G, d, static_cast<const float*>(w.wo), d, DX, d, R, d, d), true,
-                            false, GB_SET, st));
+    NML_TRY(launch_gemm_bwd(dt, gb(G, d, att, d, grad_of(m, w.wo), d, d, d, R), false, false, GB_ADD, st));
+    NML_TRY(launch_colsum(dt, G, d, R, d, grad_of(m, w.bo), PART, st));
+    NML_TRY(launch_gemm_bwd(dt, gb(G, d, w.wo, d, DX, d, R, d, d), true, false, GB_SET, st));
     AttnBwdArgs ab{};
     ab.q = q;
     ab.k = k;
@@ -352,20 +374,17 @@ int nml_model_backward(nml_model* m, double grad_scale) {
     ab.S = S;
     ab.dk = m->dk;
     ab.scale = sqrtf((float)m->dk);
-    NML_TRY(launch_attention_backward(ab, st));
+    NML_TRY(launch_attention_backward(dt, ab, st));
     if (rope_on(m))
-      NML_TRY(launch_rope_backward(DQKV, R, S, m->H, m->dk, static_cast<const float*>(m->rope_cos),
-                                   static_cast<const float*>(m->rope_sin), st));
-    NML_TRY(launch_gemm_bwd(gb(DQKV, 3 * d, n1, d, grad_of(m, w.wqkv), d, 3 * d, d, R), false,
+      NML_TRY(launch_rope_backward(dt, DQKV, R, S, m->H, m->dk, m->rope_cos, m->rope_sin, st));
+    NML_TRY(launch_gemm_bwd(dt, gb(DQKV, 3 * d, n1, d, grad_of(m, w.wqkv), d, 3 * d, d, R), false,
                             false, GB_ADD, st));
-    NML_TRY(launch_colsum(DQKV, 3 * d, R, 3 * d, grad_of(m, w.bqkv), PART, st));
-    NML_TRY(launch_gemm_bwd(gb(DQKV, 3 * d, static_cast<const float*>(w.wqkv), d, DX, d, R, d, 3 * d),
-                            true, false, GB_SET, st));
-    NML_TRY(launch_rmsnorm_bwd(DX, x, static_cast<const float*>(w.ln1), G, 1, grad_of(m, w.ln1),
-                               PART, R, d, kEps, st));
+    NML_TRY(launch_colsum(dt, DQKV, 3 * d, R, 3 * d, grad_of(m, w.bqkv), PART, st));
+    NML_TRY(launch_gemm_bwd(dt, gb(DQKV, 3 * d, w.wqkv, d, DX, d, R, d, 3 * d), true, false, GB_SET, st));
+    NML_TRY(launch_rmsnorm_bwd(dt, DX, x, w.ln1, G, 1, grad_of(m, w.ln1), PART, R, d, kEps, st));
   }
-  NML_TRY(launch_embed_backward(G, dids, dE, rope_on(m) ? nullptr : grad_of(m, m->pos), B, S, d, V,
-                                st));
+  NML_TRY(launch_embed_backward(dt, G, dids, dE, rope_on(m) ? nullptr : grad_of(m, m->pos), B, S, d,
+                                V, st));
   NML_HIP(hipStreamSynchronize(st));
   return 0;
 }
@@ -375,26 +394,34 @@ int nml_model_adamw_step(nml_model* m, float lr, float beta1, float beta2, float
   NML_TRY(check_ready(m));
   NML_TRY(ensure_train(m));
   TrainState* t = m->train;
-  const size_t bytes = m->arena_bytes;
+  hipStream_t st = nml::stream();
+  const size_t fb = f32_bytes(m), n_all = m->arena_bytes / m->es;
   if (!t->moments.p) {
-    NML_TRY(t->moments.ensure(2 * bytes));
-    NML_HIP(hipMemsetAsync(t->moments.p, 0, 2 * bytes, nml::stream()));
+    NML_TRY(t->moments.ensure(2 * fb));
+    NML_HIP(hipMemsetAsync(t->moments.p, 0, 2 * fb, st));
   }
-  // Every parameter, as two ranges of the arena around the rotary tables (buffers, not
-  // parameters). Alignment gaps between parameters carry zero gradients and moments.
-  char* base = static_cast<char*>(m->arena);
-  const size_t rope_lo = static_cast<char*>(m->rope_cos) - base;
-  const size_t rope_hi = static_cast<char*>(m->rope_sin) - base +
-                         align256(param_elems(m, NML_P_ROPE_SIN) * m->es);
-  const size_t ranges[2][2] = {{0, rope_lo}, {rope_hi, bytes}};
-  char* g = static_cast<char*>(t->grads.p);
-  char* mm = static_cast<char*>(t->moments.p);
+  // float32 parameters are updated in place; fp16 ones through float32 masters, taken from
+  // the parameters on the first step and rounded back after every step (adam.py:75-81,
+  // :238-245)
+  float* master = static_cast<float*>(m->arena);
+  if (m->dt == F16) {
+    if (!t->masters.p) {
+      NML_TRY(t->masters.ensure(fb));
+      NML_TRY(launch_convert(F16, m->arena, F32, t->masters.p, n_all, st));
+    }
+    master = static_cast<float*>(t->masters.p);
+  }
+  size_t ranges[2][2];
+  param_ranges(m, ranges);
+  float* g = static_cast<float*>(t->grads.p);
+  float* mm = static_cast<float*>(t->moments.p);
   for (const auto& r : ranges) {
     if (r[1] <= r[0]) continue;
-    NML_TRY(launch_adamw(reinterpret_cast<float*>(base + r[0]), reinterpret_cast<float*>(g + r[0]),
-                         reinterpret_cast<float*>(mm + r[0]),
-                         reinterpret_cast<float*>(mm + bytes + r[0]), (r[1] - r[0]) / 4, lr, beta1,
-                         beta2, bias_corr1, bias_corr2, eps, weight_decay, nml::stream()));
+    NML_TRY(launch_adamw(master + r[0], g + r[0], mm + r[0], mm + n_all + r[0], r[1] - r[0], lr,
+                         beta1, beta2, bias_corr1, bias_corr2, eps, weight_decay, st));
+    if (m->dt == F16)
+      NML_TRY(launch_convert(F32, master + r[0], F16, static_cast<char*>(m->arena) + r[0] * m->es,
+                             r[1] - r[0], st));
   }
   return 0;
 }
@@ -406,9 +433,9 @@ int nml_model_adam_moments(nml_model* m, int kind, int layer, void** first, void
   void** slot = param_slot(m, kind, layer);
   NML_REQUIRE(slot != nullptr, "unknown parameter kind %d / layer %d", kind, layer);
   NML_REQUIRE(m->train && m->train->moments.p, "no optimizer state yet (call nml_model_adamw_step)");
-  const size_t off = static_cast<char*>(*slot) - static_cast<char*>(m->arena);
+  const size_t off = f32_off(m, *slot);
   *first = static_cast<char*>(m->train->moments.p) + off;
-  *second = static_cast<char*>(m->train->moments.p) + m->arena_bytes + off;
+  *second = static_cast<char*>(m->train->moments.p) + f32_bytes(m) + off;
   return 0;
 }
 

@@ -15,6 +15,7 @@ import numpy as np
 
 from nimbleml_amd import _native as N
 from nimbleml_amd import np_backend
+from nimbleml_amd.grad_mode import is_grad_enabled
 from nimbleml_amd.layers import (Embedding, FusedGPTTrunk, FusedTransformerBlock, Module,
                                  RMSNorm, Sequential)
 from nimbleml_amd.tensor import Tensor
@@ -229,10 +230,12 @@ class GPT(Module):
         """Mean tied-head cross-entropy (models/gpt.py:123-137); logits are formed in
         row chunks on the device and never all at once.
 
-        On a float32 model whose parameters require gradients the device keeps what the
-        backward needs, and ``loss.backward()`` adds every parameter's gradient to its
-        ``grad`` (losses/cross_entropy.py:166-191 and the array-level backward of
-        neural_network/_fused_arrays.py). float16 models return a loss without a graph.
+        When gradients are enabled (``grad_mode``) and the parameters require them, the
+        device keeps what the backward needs, and
+        ``loss.backward()`` adds every parameter's gradient to its ``grad``
+        (losses/cross_entropy.py:166-191 and the array-level backward of
+        neural_network/_fused_arrays.py): in the compute dtype, or float32 where an optimizer
+        pinned ``_grad_dtype`` (optimizers/optimizer.py:33-38).
         """
         ids = _ids_array(input_ids)
         self._check_ids(ids)
@@ -243,20 +246,13 @@ class GPT(Module):
         dlab = N.DeviceArray.from_host(lab)
         loss = C.c_double()
         has_ign = ignore_index is not None
-        train = self._dtype == np.float32 and any(p.requires_grad for p in self.parameters())
+        train = is_grad_enabled() and any(p.requires_grad for p in self.parameters())
         fn = N.lib.nml_model_loss_train if train else N.lib.nml_model_loss
         N.check(fn(h, dids.ptr, dlab.ptr, b, s, int(ignore_index) if has_ign else 0,
                    int(has_ign), C.byref(loss)))
         # The reference wraps the loss in a compute-dtype Tensor (losses/cross_entropy.py:158-164).
-        wants_grad = any(p.requires_grad for p in self.parameters())
-        out = Tensor([0.0], (), requires_grad=wants_grad)
+        out = Tensor([0.0], (), requires_grad=train)
         out.data = np.asarray([loss.value], dtype=self._dtype)
-        if wants_grad and not train:
-            def _refuse():
-                raise RuntimeError("loss.backward() on the device needs a float32 model "
-                                   f"(this one computes in {self._dtype})")
-
-            out._backward = _refuse
         if train:
             dev = self._dev
 

@@ -80,13 +80,16 @@ class Tensor:
         if set_to_none:
             self.grad = None
         else:
-            self.grad = np.zeros(self.size, dtype=np_backend.dtype)
+            gdt = getattr(self, "_grad_dtype", None) or np_backend.dtype
+            self.grad = np.zeros(self.size, dtype=gdt)
 
     def _accumulate_grad(self, grad):
-        """tensor.py:334-352: add ``grad`` (flattened, compute dtype) into ``self.grad``."""
+        """tensor.py:334-352: add ``grad`` (flattened) into ``self.grad``, in the compute dtype
+        or the wider ``_grad_dtype`` an optimizer pins under fp16 (optimizers/optimizer.py:33-38)."""
         if not self.requires_grad:
             return
-        grad = np.asarray(grad).reshape(-1).astype(np_backend.dtype, copy=False)
+        gdt = getattr(self, "_grad_dtype", None) or np_backend.dtype
+        grad = np.asarray(grad).reshape(-1).astype(gdt, copy=False)
         if self.grad is None:
             self.grad = grad.copy()
         else:
