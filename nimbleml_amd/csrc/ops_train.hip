@@ -215,6 +215,128 @@ __global__ __launch_bounds__(256) void gemm_bwd_kernel(GemmBwdArgs g, int kchunk
       }
 }
 
+// ---- fp16 operands on the fp16 MFMA (32×32×16, fp32 accumulation): 128 × 128 tiles,
+// 32-wide k tiles, 4 waves of 64 × 64. LDS holds each operand as [row][k] (k contiguous, a
+// 16-byte fragment per lane and k step); k-contiguous operands are copied in 16-byte
+// pieces, the others (8 consecutive rows at one k per piece) are transposed on the store.
+constexpr int kHK16 = 64, kHP16 = kHK16 + 8;  // k tile, LDS row pitch (halves)
+constexpr int kHV16 = kGM * kHK16 / 8 / 256;    // 16-byte pieces per thread per operand tile
+
+template <bool KC>
+__device__ __forceinline__ void tile16_load(const half_t* __restrict__ p, long long ld, int r0,
+                                            int R, int k0, int K, half8 (&v)[kHV16]) {
+  const half8 z = {0, 0, 0, 0, 0, 0, 0, 0};
+#pragma unroll
+  for (int i = 0; i < kHV16; ++i) {
+    const int c = threadIdx.x + 256 * i;
+    if constexpr (KC) {
+      const int row = c / (kHK16 / 8), kc = (c % (kHK16 / 8)) * 8;
+      const bool ok = r0 + row < R && k0 + kc < K;
+      v[i] = ok ? *reinterpret_cast<const half8*>(p + static_cast<long long>(r0 + row) * ld + k0 + kc) : z;
+    } else {
+      const int kr = c >> 4, rc = (c & 15) * 8;
+      const bool ok = k0 + kr < K && r0 + rc < R;
+      v[i] = ok ? *reinterpret_cast<const half8*>(p + static_cast<long long>(k0 + kr) * ld + r0 + rc) : z;
+    }
+  }
+}
+
+template <bool KC>
+__device__ __forceinline__ void tile16_store(half_t (*S)[kHP16], const half8 (&v)[kHV16]) {
+#pragma unroll
+  for (int i = 0; i < kHV16; ++i) {
+    const int c = threadIdx.x + 256 * i;
+    if constexpr (KC) {
+      const int row = c / (kHK16 / 8), kc = (c % (kHK16 / 8)) * 8;
+      *reinterpret_cast<half8*>(&S[row][kc]) = v[i];
+    } else {
+      const int kr = c >> 4, rc = (c & 15) * 8;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) S[rc + j][kr] = v[i][j];
+    }
+  }
+}
+
+template <bool A_KC, bool B_KC, int OUT>
+__global__ __launch_bounds__(256) void gemm_bwd_f16_kernel(GemmBwdArgs g, int kchunk, long long zstride) {
+  __shared__ __attribute__((aligned(16))) half_t As[kGM][kHP16];
+  __shared__ __attribute__((aligned(16))) half_t Bs[kGM][kHP16];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int wm = wave >> 1, wn = wave & 1;
+  const int m0 = blockIdx.y * kGM, n0 = blockIdx.x * kGM;
+  const int M = g.M, N = g.N;
+  const int kbeg = blockIdx.z * kchunk;
+  const int K = min(g.K, kbeg + kchunk);
+  const half_t* __restrict__ ga = static_cast<const half_t*>(g.a);
+  const half_t* __restrict__ gbp = static_cast<const half_t*>(g.b);
+
+  floatx16 acc[2][2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
+
+  half8 ra[kHV16], rb[kHV16];
+  tile16_load<A_KC>(ga, g.lda, m0, M, kbeg, K, ra);
+  tile16_load<B_KC>(gbp, g.ldb, n0, N, kbeg, K, rb);
+  tile16_store<A_KC>(As, ra);
+  tile16_store<B_KC>(Bs, rb);
+  __syncthreads();
+  const int fr = lane & 31, fk = (lane >> 5) * 8;
+  for (int k0 = kbeg; k0 < K; k0 += kHK16) {
+    const bool more = k0 + kHK16 < K;
+    if (more) {  // next tile's loads in flight while this one multiplies
+      tile16_load<A_KC>(ga, g.lda, m0, M, k0 + kHK16, K, ra);
+      tile16_load<B_KC>(gbp, g.ldb, n0, N, k0 + kHK16, K, rb);
+    }
+#pragma unroll
+    for (int ks = 0; ks < kHK16; ks += 16) {
+      half8 fa[2], fb[2];
+#pragma unroll
+      for (int i = 0; i < 2; ++i) fa[i] = *reinterpret_cast<const half8*>(&As[wm * 64 + i * 32 + fr][ks + fk]);
+#pragma unroll
+      for (int j = 0; j < 2; ++j) fb[j] = *reinterpret_cast<const half8*>(&Bs[wn * 64 + j * 32 + fr][ks + fk]);
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(fa[i], fb[j], acc[i][j], 0, 0, 0);
+    }
+    __syncthreads();
+    if (more) {
+      tile16_store<A_KC>(As, ra);
+      tile16_store<B_KC>(Bs, rb);
+    }
+    __syncthreads();
+  }
+
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int m = m0 + wm * 64 + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+        const int n = n0 + wn * 64 + j * 32 + (lane & 31);
+        if (m < M && n < N) {
+          const long long ci = blockIdx.z * zstride + static_cast<long long>(m) * g.ldc + n;
+          const float v = acc[i][j][r];
+          if constexpr (OUT == kGBPart) {
+            static_cast<float*>(g.c)[ci] = v;
+          } else if constexpr (OUT == GB_ADD) {
+            static_cast<float*>(g.c)[ci] += rnd<half_t>(v);
+          } else if constexpr (OUT == GB_SET) {
+            static_cast<half_t*>(g.c)[ci] = static_cast<half_t>(v);
+          } else {
+            const float x = static_cast<float>(static_cast<const half_t*>(g.aux)[static_cast<long long>(m) * g.ldaux + n]);
+            static_cast<half_t*>(g.c)[ci] = static_cast<half_t>(gelu_grad_f16(rnd<half_t>(v), x));
+          }
+        }
+      }
+}
+
 // c[m·ldc + n] += T(Σ_z part[z·M·N + m·N + n]), z in order.
 template <typename T>
 __global__ __launch_bounds__(256) void splitk_reduce_kernel(const float* __restrict__ part, int splits,
@@ -237,7 +359,7 @@ struct SplitWs {
 SplitWs g_split;
 
 template <bool A_KC, bool B_KC, typename T>
-int gemm_bwd_out(const GemmBwdArgs& g, int out, hipStream_t st) {
+int gemm_bwd_out(const GemmBwdArgs& g, int out, hipStream_t st, bool mfma16 = false) {
   const int tn = (g.N + kGM - 1) / kGM, tm = (g.M + kGM - 1) / kGM;
   // Few output tiles and a long K (a weight gradient, K = rows): split K so that the
   // grid holds ≥ 1024 blocks, each K slice ≥ 512 long.
@@ -254,12 +376,19 @@ int gemm_bwd_out(const GemmBwdArgs& g, int out, hipStream_t st) {
       NML_HIP(hipMalloc(&g_split.p, need * sizeof(float)));
       g_split.floats = need;
     }
-    const int kchunk = ((g.K + splits - 1) / splits + kGK - 1) / kGK * kGK;
+    const int kchunk = ((g.K + splits - 1) / splits + kHK16 - 1) / kHK16 * kHK16;
     GemmBwdArgs p = g;
     p.c = g_split.p;
     p.ldc = g.N;
     const dim3 grid(tn, tm, splits);
-    gemm_bwd_kernel<A_KC, B_KC, kGBPart, T><<<grid, 256, 0, st>>>(p, kchunk, static_cast<long long>(g.M) * g.N);
+    if constexpr (sizeof(T) == 2) {
+      if (mfma16)
+        gemm_bwd_f16_kernel<A_KC, B_KC, kGBPart><<<grid, 256, 0, st>>>(p, kchunk, static_cast<long long>(g.M) * g.N);
+      else
+        gemm_bwd_kernel<A_KC, B_KC, kGBPart, T><<<grid, 256, 0, st>>>(p, kchunk, static_cast<long long>(g.M) * g.N);
+    } else {
+      gemm_bwd_kernel<A_KC, B_KC, kGBPart, T><<<grid, 256, 0, st>>>(p, kchunk, static_cast<long long>(g.M) * g.N);
+    }
     NML_LAUNCHED();
     const long long mn = static_cast<long long>(g.M) * g.N;
     splitk_reduce_kernel<T><<<static_cast<int>((mn + 255) / 256), 256, 0, st>>>(
@@ -268,6 +397,18 @@ int gemm_bwd_out(const GemmBwdArgs& g, int out, hipStream_t st) {
     return 0;
   }
   const dim3 grid(tn, tm);
+  if constexpr (sizeof(T) == 2) {
+    if (mfma16) {
+      switch (out) {
+        case GB_SET: gemm_bwd_f16_kernel<A_KC, B_KC, GB_SET><<<grid, 256, 0, st>>>(g, g.K, 0); break;
+        case GB_ADD: gemm_bwd_f16_kernel<A_KC, B_KC, GB_ADD><<<grid, 256, 0, st>>>(g, g.K, 0); break;
+        case GB_GELU: gemm_bwd_f16_kernel<A_KC, B_KC, GB_GELU><<<grid, 256, 0, st>>>(g, g.K, 0); break;
+        default: set_error("gemm_bwd: unknown output mode %d", out); return -1;
+      }
+      NML_LAUNCHED();
+      return 0;
+    }
+  }
   switch (out) {
     case GB_SET: gemm_bwd_kernel<A_KC, B_KC, GB_SET, T><<<grid, 256, 0, st>>>(g, g.K, 0); break;
     case GB_ADD: gemm_bwd_kernel<A_KC, B_KC, GB_ADD, T><<<grid, 256, 0, st>>>(g, g.K, 0); break;
@@ -1089,8 +1230,14 @@ int launch_gemm_bwd(int dt, const GemmBwdArgs& g, bool a_kc, bool b_kc, int out,
   NML_REQUIRE(b_kc ? g.K % 4 == 0 : g.N % 4 == 0, "gemm_bwd: B's contiguous extent must be a multiple of 4");
   NML_REQUIRE(out != GB_GELU || g.aux != nullptr, "gemm_bwd: the GELU backward needs the pre-activation");
   if (dt == F16) {
-    if (a_kc) return b_kc ? gemm_bwd_out<true, true, half_t>(g, out, st) : gemm_bwd_out<true, false, half_t>(g, out, st);
-    return b_kc ? gemm_bwd_out<false, true, half_t>(g, out, st) : gemm_bwd_out<false, false, half_t>(g, out, st);
+    // 16-byte fp16 pieces: the contiguous extent of each operand a multiple of 8 elements
+    const bool m16 = !std::getenv("NIMBLEML_TRAIN_F16_WIDEN") &&
+                     ((reinterpret_cast<uintptr_t>(g.a) | reinterpret_cast<uintptr_t>(g.b)) & 15) == 0 &&
+                     g.lda % 8 == 0 && g.ldb % 8 == 0 && (a_kc ? g.K % 8 == 0 : g.M % 8 == 0) &&
+                     (b_kc ? g.K % 8 == 0 : g.N % 8 == 0);
+    if (a_kc)
+      return b_kc ? gemm_bwd_out<true, true, half_t>(g, out, st, m16) : gemm_bwd_out<true, false, half_t>(g, out, st, m16);
+    return b_kc ? gemm_bwd_out<false, true, half_t>(g, out, st, m16) : gemm_bwd_out<false, false, half_t>(g, out, st, m16);
   }
   if (a_kc) return b_kc ? gemm_bwd_out<true, true, float>(g, out, st) : gemm_bwd_out<true, false, float>(g, out, st);
   return b_kc ? gemm_bwd_out<false, true, float>(g, out, st) : gemm_bwd_out<false, false, float>(g, out, st);
