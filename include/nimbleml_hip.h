@@ -163,7 +163,7 @@ int nml_model_forward(nml_model* m, const int64_t* ids, size_t batch, size_t seq
 int nml_model_loss(nml_model* m, const int64_t* ids, const int64_t* labels, size_t batch,
                    size_t seq, int64_t ignore_index, int has_ignore, double* loss);
 
-/* ---- training (float32 models) -------------------------------------------------------
+/* ---- training (float32 and float16 models) -------------------------------------------
  * compute_loss with the autograd graph kept, then loss.backward() (models/gpt.py:123-137;
  * Tensor.backward, utils/tensor.py:286-332; the array-level backward of
  * neural_network/_fused_arrays.py:129-377 and kernels/fused_tied_crossentropy.py:27-48).
