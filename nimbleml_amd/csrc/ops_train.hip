@@ -234,9 +234,10 @@ __device__ __forceinline__ void tile16_load(const half_t* __restrict__ p, long l
       const bool ok = r0 + row < R && k0 + kc < K;
       v[i] = ok ? *reinterpret_cast<const half8*>(p + static_cast<long long>(r0 + row) * ld + k0 + kc) : z;
     } else {
-      const int kr = c >> 4, rc = (c & 15) * 8;
-      const bool ok = k0 + kr < K && r0 + rc < R;
-      v[i] = ok ? *reinterpret_cast<const half8*>(p + static_cast<long long>(k0 + kr) * ld + r0 + rc) : z;
+      // a 4 (k) × 8 (rows) block per thread: rows 8·(t % 16)…, k 4·(t / 16) + i
+      const int rb = (threadIdx.x & 15) * 8, kr = (threadIdx.x >> 4) * 4 + i;
+      const bool ok = k0 + kr < K && r0 + rb < R;
+      v[i] = ok ? *reinterpret_cast<const half8*>(p + static_cast<long long>(k0 + kr) * ld + r0 + rb) : z;
     }
   }
 }
@@ -249,10 +250,13 @@ __device__ __forceinline__ void tile16_store(half_t (*S)[kHP16], const half8 (&v
     if constexpr (KC) {
       const int row = c / (kHK16 / 8), kc = (c % (kHK16 / 8)) * 8;
       *reinterpret_cast<half8*>(&S[row][kc]) = v[i];
-    } else {
-      const int kr = c >> 4, rc = (c & 15) * 8;
+    } else if (i == 0) {  // the 4 × 8 block transposed in registers: one 8-byte store per row
+      const int rb = (threadIdx.x & 15) * 8, kq = (threadIdx.x >> 4) * 4;
 #pragma unroll
-      for (int j = 0; j < 8; ++j) S[rc + j][kr] = v[i][j];
+      for (int j = 0; j < 8; ++j) {
+        const half4 w = {v[0][j], v[1][j], v[2][j], v[3][j]};
+        *reinterpret_cast<half4*>(&S[rb + j][kq]) = w;
+      }
     }
   }
 }
