@@ -1131,6 +1131,268 @@ __global__ __launch_bounds__(256) void attn_bwd_dq_mfma(AttnBwdArgs a) {
   }
 }
 
+// ---- fp16 models on the fp16 MFMA (32×32×16, head dims 64 and 128): the same two kernels
+// and wave layout as above with fp16 tiles in LDS — [row][dim] for the products that reduce
+// over the head dimension, and a transposed [dim][row] copy of the operand that the
+// P / dS products reduce over by rows (Q and dO in the dK/dV kernel, K in the dQ kernel).
+// P and dS are rounded to fp16 where they enter the MFMA (the reference's fp16 backward
+// holds them in fp16). A 16-row step of those products takes rows f(r) (k slots 0–7) and
+// f(r) + 4 (slots 8–15) from registers r = 8s … 8s + 7, i.e. rows 16s + {0–3, 8–11} and
+// 16s + {4–7, 12–15}: two 8-byte reads of the transposed copy per fragment.
+template <int DK>
+constexpr size_t attn_f16_lds() {
+  return (static_cast<size_t>(4) * kAT * (DK + 8) + 2 * DK * (kAT + 8)) * sizeof(half_t) +
+         2 * kAT * sizeof(float);
+}
+
+// rows [lo, lo + 64) of a (row stride ld) fp16 source: natural [row][DK + 8] copy into X
+// and, when XT is given, the transposed [dim][64 + 8] copy, in blocks of 4 rows × 8 dims
+// (block b of 16·DK/8: rows 4·(b / (DK/8)) …, dims 8·(b % (DK/8)) …) taken by threads
+// first … first + 16·DK/8 − 1.
+template <int DK>
+__device__ __forceinline__ void stage16(half_t* X, half_t* XT, const half_t* __restrict__ src, long long ld,
+                                        int lo, int S, int first) {
+  constexpr int PA = DK + 8, PT = kAT + 8, NB = 16 * DK / 8;
+  const int b = static_cast<int>(threadIdx.x) - first;
+  if (b < 0 || b >= NB) return;
+  const int r0 = 4 * (b / (DK / 8)), c = 8 * (b % (DK / 8));
+  const half8 z = {0, 0, 0, 0, 0, 0, 0, 0};
+  half8 v[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+    v[i] = lo + r0 + i < S ? *reinterpret_cast<const half8*>(src + static_cast<long long>(lo + r0 + i) * ld + c) : z;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) *reinterpret_cast<half8*>(X + (r0 + i) * PA + c) = v[i];
+  if (XT) {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const half4 w = {v[0][j], v[1][j], v[2][j], v[3][j]};
+      *reinterpret_cast<half4*>(XT + (c + j) * PT + r0) = w;
+    }
+  }
+}
+
+// A 16-row fragment of a transposed [dim][64 + 8] tile: dims d0 + l % 32, rows of step s
+// within the 32-row block rb as the register layout pairs them.
+__device__ __forceinline__ half8 frag_t(const half_t* XT, int d0, int rb, int s, int lane) {
+  constexpr int PT = kAT + 8;
+  const half_t* p = XT + (d0 + (lane & 31)) * PT + rb + 16 * s + 4 * (lane >> 5);
+  const half4 lo = *reinterpret_cast<const half4*>(p);
+  const half4 hi = *reinterpret_cast<const half4*>(p + 8);
+  const half8 f = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+  return f;
+}
+
+__device__ __forceinline__ half8 regs16(const floatx16& v, int s) {
+  half8 f;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) f[j] = static_cast<half_t>(v[8 * s + j]);
+  return f;
+}
+
+template <int DK>
+__global__ __launch_bounds__(256, 2) void attn_bwd_dkdv_f16(AttnBwdArgs a) {
+  extern __shared__ __attribute__((aligned(16))) half_t lds16[];
+  constexpr int PA = DK + 8, PT = kAT + 8, NJ = DK / 32;
+  half_t* Ks = lds16;
+  half_t* Vs = Ks + kAT * PA;
+  half_t* Qs = Vs + kAT * PA;
+  half_t* Os = Qs + kAT * PA;
+  half_t* QT = Os + kAT * PA;
+  half_t* OT = QT + DK * PT;
+  float* Ls = reinterpret_cast<float*>(OT + DK * PT);
+  float* Ds = Ls + kAT;
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, wq = w >> 1, wk = w & 1;
+  const int l32 = lane & 31, hi = lane >> 5;
+  const int bh = blockIdx.y, b = bh / a.H, h = bh - (bh / a.H) * a.H;
+  const int S = a.S, k_lo = blockIdx.x * kAT;
+  const long long hoff = static_cast<long long>(bh) * S * DK;
+  const half_t* qg = static_cast<const half_t*>(a.q) + hoff;
+  const half_t* og = static_cast<const half_t*>(a.dout) + static_cast<long long>(b) * S * a.H * DK + h * DK;
+  constexpr int NB = 16 * DK / 8;
+  stage16<DK>(Ks, nullptr, static_cast<const half_t*>(a.k) + hoff, DK, k_lo, S, 0);
+  stage16<DK>(Vs, nullptr, static_cast<const half_t*>(a.v) + hoff, DK, k_lo, S, NB % 256);
+  floatx16 dv[NJ], dk[NJ];
+#pragma unroll
+  for (int j = 0; j < NJ; ++j)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) dv[j][r] = dk[j][r] = 0.f;
+  const int key = k_lo + 32 * wk + l32;
+  const float inv_scale = 1.0f / a.scale, mul = score_mul<half_t>(a.scale);
+  for (int q_lo = k_lo; q_lo < S; q_lo += kAT) {
+    __syncthreads();
+    stage16<DK>(Qs, QT, qg, DK, q_lo, S, 0);
+    stage16<DK>(Os, OT, og, static_cast<long long>(a.H) * DK, q_lo, S, NB % 256);
+    if (threadIdx.x < kAT) {
+      const int q = q_lo + threadIdx.x;
+      Ls[threadIdx.x] = q < S ? a.lse[static_cast<long long>(bh) * S + q] : 0.f;
+      Ds[threadIdx.x] = q < S ? a.dvec[static_cast<long long>(bh) * S + q] : 0.f;
+    }
+    __syncthreads();
+    floatx16 sc, dp;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) sc[r] = dp[r] = 0.f;
+#pragma unroll
+    for (int c0 = 0; c0 < DK; c0 += 16) {
+      const half8 qa = *reinterpret_cast<const half8*>(Qs + (32 * wq + l32) * PA + c0 + 8 * hi);
+      const half8 kb = *reinterpret_cast<const half8*>(Ks + (32 * wk + l32) * PA + c0 + 8 * hi);
+      const half8 oa = *reinterpret_cast<const half8*>(Os + (32 * wq + l32) * PA + c0 + 8 * hi);
+      const half8 vb = *reinterpret_cast<const half8*>(Vs + (32 * wk + l32) * PA + c0 + 8 * hi);
+      sc = __builtin_amdgcn_mfma_f32_32x32x16_f16(qa, kb, sc, 0, 0, 0);
+      dp = __builtin_amdgcn_mfma_f32_32x32x16_f16(oa, vb, dp, 0, 0, 0);
+    }
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int ql = 32 * wq + d_row(r, lane), q = q_lo + ql;
+      float p = 0.f;
+      if (key <= q && q < S) p = expf(attn_score<half_t>(sc[r], mul) - Ls[ql]);
+      sc[r] = p;
+      dp[r] = p * (dp[r] - Ds[ql]) * inv_scale;
+    }
+#pragma unroll
+    for (int st = 0; st < 2; ++st) {
+      const half8 pa = regs16(sc, st), sa = regs16(dp, st);
+#pragma unroll
+      for (int j = 0; j < NJ; ++j) {
+        dv[j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(pa, frag_t(OT, 32 * j, 32 * wq, st, lane), dv[j], 0, 0, 0);
+        dk[j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(sa, frag_t(QT, 32 * j, 32 * wq, st, lane), dk[j], 0, 0, 0);
+      }
+    }
+  }
+  __syncthreads();
+  float* red = reinterpret_cast<float*>(Qs);  // 2 key halves × (dv, dk) × NJ × 16 × 64 floats
+  if (wq == 1) {
+#pragma unroll
+    for (int j = 0; j < NJ; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        red[(((wk * 2 + 0) * NJ + j) * 16 + r) * 64 + lane] = dv[j][r];
+        red[(((wk * 2 + 1) * NJ + j) * 16 + r) * 64 + lane] = dk[j][r];
+      }
+  }
+  __syncthreads();
+  if (wq == 0) {
+    const int d = a.H * DK;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int kk = k_lo + 32 * wk + d_row(r, lane);
+      if (kk < S) {
+        half_t* row = static_cast<half_t*>(a.dqkv) + (static_cast<long long>(b) * S + kk) * 3 * d + h * DK;
+#pragma unroll
+        for (int j = 0; j < NJ; ++j) {
+          row[d + 32 * j + l32] = static_cast<half_t>(dk[j][r] + red[(((wk * 2 + 1) * NJ + j) * 16 + r) * 64 + lane]);
+          row[2 * d + 32 * j + l32] = static_cast<half_t>(dv[j][r] + red[(((wk * 2 + 0) * NJ + j) * 16 + r) * 64 + lane]);
+        }
+      }
+    }
+  }
+}
+
+template <int DK>
+__global__ __launch_bounds__(256, 2) void attn_bwd_dq_f16(AttnBwdArgs a) {
+  extern __shared__ __attribute__((aligned(16))) half_t lds16[];
+  constexpr int PA = DK + 8, NJ = DK / 32, NB = 16 * DK / 8;
+  half_t* Ks = lds16;
+  half_t* Vs = Ks + kAT * PA;
+  half_t* Qs = Vs + kAT * PA;
+  half_t* Os = Qs + kAT * PA;
+  half_t* KT = Os + kAT * PA;
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, wk = w >> 1, wq = w & 1;
+  const int l32 = lane & 31, hi = lane >> 5;
+  const int bh = blockIdx.y, b = bh / a.H, h = bh - (bh / a.H) * a.H;
+  const int S = a.S, q_lo = blockIdx.x * kAT;
+  const long long hoff = static_cast<long long>(bh) * S * DK;
+  const half_t* kg = static_cast<const half_t*>(a.k) + hoff;
+  const half_t* vg = static_cast<const half_t*>(a.v) + hoff;
+  stage16<DK>(Qs, nullptr, static_cast<const half_t*>(a.q) + hoff, DK, q_lo, S, 0);
+  stage16<DK>(Os, nullptr,
+              static_cast<const half_t*>(a.dout) + static_cast<long long>(b) * S * a.H * DK + h * DK,
+              static_cast<long long>(a.H) * DK, q_lo, S, NB % 256);
+  const int q = q_lo + 32 * wq + l32;
+  const float lse = q < S ? a.lse[static_cast<long long>(bh) * S + q] : 0.f;
+  const float dd = q < S ? a.dvec[static_cast<long long>(bh) * S + q] : 0.f;
+  const float inv_scale = 1.0f / a.scale, mul = score_mul<half_t>(a.scale);
+  floatx16 dq[NJ];
+#pragma unroll
+  for (int j = 0; j < NJ; ++j)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) dq[j][r] = 0.f;
+  const int k_end = min(S, q_lo + kAT);
+  for (int k_lo = 0; k_lo < k_end; k_lo += kAT) {
+    __syncthreads();
+    stage16<DK>(Ks, KT, kg, DK, k_lo, S, 0);
+    stage16<DK>(Vs, nullptr, vg, DK, k_lo, S, NB % 256);
+    __syncthreads();
+    floatx16 sc, dp;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) sc[r] = dp[r] = 0.f;
+#pragma unroll
+    for (int c0 = 0; c0 < DK; c0 += 16) {
+      const half8 ka = *reinterpret_cast<const half8*>(Ks + (32 * wk + l32) * PA + c0 + 8 * hi);
+      const half8 qb = *reinterpret_cast<const half8*>(Qs + (32 * wq + l32) * PA + c0 + 8 * hi);
+      const half8 va = *reinterpret_cast<const half8*>(Vs + (32 * wk + l32) * PA + c0 + 8 * hi);
+      const half8 ob = *reinterpret_cast<const half8*>(Os + (32 * wq + l32) * PA + c0 + 8 * hi);
+      sc = __builtin_amdgcn_mfma_f32_32x32x16_f16(ka, qb, sc, 0, 0, 0);
+      dp = __builtin_amdgcn_mfma_f32_32x32x16_f16(va, ob, dp, 0, 0, 0);
+    }
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int kk = k_lo + 32 * wk + d_row(r, lane);
+      float p = 0.f;
+      if (kk <= q && q < S) p = expf(attn_score<half_t>(sc[r], mul) - lse);
+      dp[r] = p * (dp[r] - dd) * inv_scale;
+    }
+#pragma unroll
+    for (int st = 0; st < 2; ++st) {
+      const half8 sa = regs16(dp, st);
+#pragma unroll
+      for (int j = 0; j < NJ; ++j)
+        dq[j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(sa, frag_t(KT, 32 * j, 32 * wk, st, lane), dq[j], 0, 0, 0);
+    }
+  }
+  __syncthreads();
+  float* red = reinterpret_cast<float*>(lds16);  // 2 query halves × NJ × 16 × 64 floats
+  if (wk == 1) {
+#pragma unroll
+    for (int j = 0; j < NJ; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) red[((wq * NJ + j) * 16 + r) * 64 + lane] = dq[j][r];
+  }
+  __syncthreads();
+  if (wk == 0) {
+    const int d = a.H * DK;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int qq = q_lo + 32 * wq + d_row(r, lane);
+      if (qq < S) {
+        half_t* row = static_cast<half_t*>(a.dqkv) + (static_cast<long long>(b) * S + qq) * 3 * d + h * DK;
+#pragma unroll
+        for (int j = 0; j < NJ; ++j)
+          row[32 * j + l32] = static_cast<half_t>(dq[j][r] + red[((wq * NJ + j) * 16 + r) * 64 + lane]);
+      }
+    }
+  }
+}
+
+template <int DK>
+int attn_bwd_f16(const AttnBwdArgs& a, hipStream_t st) {
+  constexpr size_t lds = attn_f16_lds<DK>();
+  static bool attr = false;
+  if (!attr) {
+    NML_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(&attn_bwd_dkdv_f16<DK>),
+                                hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds)));
+    NML_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(&attn_bwd_dq_f16<DK>),
+                                hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds)));
+    attr = true;
+  }
+  const dim3 grid((a.S + kAT - 1) / kAT, a.B * a.H);
+  attn_bwd_dkdv_f16<DK><<<grid, 256, lds, st>>>(a);
+  NML_LAUNCHED();
+  attn_bwd_dq_f16<DK><<<grid, 256, lds, st>>>(a);
+  NML_LAUNCHED();
+  return 0;
+}
+
 template <int DK, typename T>
 int attn_bwd_mfma(const AttnBwdArgs& a, hipStream_t st) {
   constexpr size_t lds = attn_mfma_lds<DK>();
@@ -1153,7 +1415,12 @@ int attn_bwd_mfma(const AttnBwdArgs& a, hipStream_t st) {
 template <int DK, typename T>
 int attn_bwd_dk(const AttnBwdArgs& a, hipStream_t st) {
   if constexpr (DK == 64 || DK == 128) {
-    if (!std::getenv("NIMBLEML_ATTN_BWD_VALU")) return attn_bwd_mfma<DK, T>(a, st);
+    if (!std::getenv("NIMBLEML_ATTN_BWD_VALU")) {
+      if constexpr (sizeof(T) == 2) {
+        if (!std::getenv("NIMBLEML_TRAIN_F16_WIDEN")) return attn_bwd_f16<DK>(a, st);
+      }
+      return attn_bwd_mfma<DK, T>(a, st);
+    }
   }
   constexpr int BT = DK >= 128 ? 16 : 32;
   const dim3 grid((a.S + BT - 1) / BT, a.B * a.H);

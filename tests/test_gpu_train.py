@@ -193,7 +193,8 @@ def test_backward_fp16(gpu, dims, b, s):
     """float16 models: the loss equals the fp16 oracle's (the reference's fp16 rounding),
     and the gradients (kept float32, as under an optimizer's _grad_dtype) match the float64
     gradient at the same fp16 weights within 1.5e-2 of each tensor's largest gradient
-    (measured ≤ 4.5e-3): the fp16 rounding of the activations and activation gradients."""
+    (measured ≤ 7.4e-3): the fp16 rounding of the activations, activation gradients and the
+    fp16 P and dS of the attention backward."""
     import nimbleml_amd as nm
 
     cfg = GPTConfig(*dims)
