@@ -425,6 +425,7 @@ int gemm_bwd_out(const GemmBwdArgs& g, int out, hipStream_t st, bool mfma16 = fa
 
 // ------------------------------------------------------------- RMSNorm backward
 constexpr int kNormRowsPerBlock = 16;
+constexpr int kNormRowsPerWave = 4;  // wave kernel: enough waves to fill the chip at 4k rows
 
 // One block per 16 rows, each thread NC columns c = tid + 256·j. Per row (fp32, the
 // order of kernels/fused_rmsnorm.py:208-217): ms = Σx²/d, rms = √(ms + ε),
@@ -492,7 +493,7 @@ __global__ __launch_bounds__(256) void rmsnorm_bwd_kernel(const float* __restric
   }
 }
 
-// The same with one wave per 16 rows (4 waves per workgroup): a lane keeps NV vectors of
+// The same with one wave per 4 rows (4 waves per workgroup): a lane keeps NV vectors of
 // 4 elements of the row, the row sums are DPP wave sums (no LDS, no barrier), and the
 // wave's dγ contribution per column goes to part[wave]. fp16 (kernels/fused_rmsnorm.py:
 // 195-206): ms recomputed as the forward forms it (fp16 squares, fp32 sum), inv = fp16(1/rms),
@@ -510,9 +511,9 @@ __global__ __launch_bounds__(256) void rmsnorm_bwd_wave_kernel(const T* __restri
   constexpr bool H = sizeof(T) == 2;
   const int lane = threadIdx.x & 63;
   const int wv = blockIdx.x * 4 + (threadIdx.x >> 6);
-  const int r0 = wv * kNormRowsPerBlock;
+  const int r0 = wv * kNormRowsPerWave;
   if (r0 >= rows) return;  // whole waves
-  const int nvec = d / 4, r1 = min(rows, r0 + kNormRowsPerBlock);
+  const int nvec = d / 4, r1 = min(rows, r0 + kNormRowsPerWave);
   floatx4 gv[NV], ga[NV];
   const floatx4 z = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -1532,19 +1533,20 @@ int launch_convert(int src_dt, const void* src, int dst_dt, void* dst, size_t n,
   return 0;
 }
 
-int rmsnorm_bwd_parts(int rows) { return (rows + kNormRowsPerBlock - 1) / kNormRowsPerBlock; }
+int rmsnorm_bwd_parts(int rows) { return (rows + kNormRowsPerWave - 1) / kNormRowsPerWave; }
 
 int launch_rmsnorm_bwd(int dt, const void* dy, const void* x, const void* gamma, void* dx, int acc,
                        float* dgamma, float* part, int rows, int d, float eps, hipStream_t st) {
   if (rows == 0) return 0;
-  const int blocks = rmsnorm_bwd_parts(rows);
+  const int waves = (rows + kNormRowsPerWave - 1) / kNormRowsPerWave;
+  const int blocks = (rows + kNormRowsPerBlock - 1) / kNormRowsPerBlock;
   const int nv = (d / 4 + 63) / 64;
   const uintptr_t al = dt == F16 ? 7 : 15;
   const bool vec_ok = d % 4 == 0 && ((reinterpret_cast<uintptr_t>(dy) | reinterpret_cast<uintptr_t>(x) |
                                       reinterpret_cast<uintptr_t>(gamma) |
                                       reinterpret_cast<uintptr_t>(dx)) & al) == 0;
   if (vec_ok && nv <= 8) {
-    const int wblocks = (blocks + 3) / 4;
+    const int wblocks = (waves + 3) / 4;
 #define NML_NORM_BWD_W(T, NVV)                                                                   \
   rmsnorm_bwd_wave_kernel<T, NVV><<<wblocks, 256, 0, st>>>((const T*)dy, (const T*)x, (const T*)gamma, \
                                                           (T*)dx, acc, part, rows, d, eps)
@@ -1561,7 +1563,7 @@ int launch_rmsnorm_bwd(int dt, const void* dy, const void* x, const void* gamma,
     }
 #undef NML_NORM_BWD_W
     NML_LAUNCHED();
-    parts_reduce_kernel<<<(d + 31) / 32, 256, 0, st>>>(part, blocks, d, dgamma);
+    parts_reduce_kernel<<<(d + 31) / 32, 256, 0, st>>>(part, waves, d, dgamma);
     NML_LAUNCHED();
     return 0;
   }
