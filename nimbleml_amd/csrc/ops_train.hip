@@ -494,8 +494,8 @@ __global__ __launch_bounds__(256) void rmsnorm_bwd_kernel(const float* __restric
 }
 
 // The same with one wave per 4 rows (4 waves per workgroup): a lane keeps NV vectors of
-// 4 elements of the row, the row sums are DPP wave sums (no LDS, no barrier), and the
-// wave's dγ contribution per column goes to part[wave]. fp16 (kernels/fused_rmsnorm.py:
+// 4 elements of the row and the row sums are DPP wave sums; the four waves' dγ
+// contributions are summed in order through LDS into part[workgroup]. fp16 (kernels/fused_rmsnorm.py:
 // 195-206): ms recomputed as the forward forms it (fp16 squares, fp32 sum), inv = fp16(1/rms),
 // x̂ = x·inv, dγ += Σ dy·x̂ (fp16 products, fp32 sum), gxh = dy·γ, dot = Σ gxh·x (fp16
 // products, fp32 sum), coef = fp16((2/d)·dot·(−½)·(ms + ε)^(−3/2)), dx = gxh·inv + x·coef,
@@ -509,11 +509,11 @@ __global__ __launch_bounds__(256) void rmsnorm_bwd_wave_kernel(const T* __restri
                                                                int d, float eps) {
 #pragma clang fp contract(off)
   constexpr bool H = sizeof(T) == 2;
-  const int lane = threadIdx.x & 63;
-  const int wv = blockIdx.x * 4 + (threadIdx.x >> 6);
+  __shared__ floatx4 red[4][NV * 64];
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int wv = blockIdx.x * 4 + w;
   const int r0 = wv * kNormRowsPerWave;
-  if (r0 >= rows) return;  // whole waves
-  const int nvec = d / 4, r1 = min(rows, r0 + kNormRowsPerWave);
+  const int nvec = d / 4, r1 = min(rows, r0 + kNormRowsPerWave);  // r1 ≤ r0 past the end
   floatx4 gv[NV], ga[NV];
   const floatx4 z = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -575,9 +575,16 @@ __global__ __launch_bounds__(256) void rmsnorm_bwd_wave_kernel(const T* __restri
     }
   }
 #pragma unroll
-  for (int i = 0; i < NV; ++i) {
-    const int c = lane + 64 * i;
-    if (c < nvec) reinterpret_cast<floatx4*>(part + static_cast<long long>(wv) * d)[c] = ga[i];
+  for (int i = 0; i < NV; ++i) red[w][lane + 64 * i] = ga[i];
+  __syncthreads();
+  for (int c = threadIdx.x; c < nvec; c += 256) {
+    floatx4 t = red[0][c];
+#pragma unroll
+    for (int j = 1; j < 4; ++j) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) t[e] += red[j][c][e];
+    }
+    reinterpret_cast<floatx4*>(part + static_cast<long long>(blockIdx.x) * d)[c] = t;
   }
 }
 
@@ -1563,7 +1570,7 @@ int launch_rmsnorm_bwd(int dt, const void* dy, const void* x, const void* gamma,
     }
 #undef NML_NORM_BWD_W
     NML_LAUNCHED();
-    parts_reduce_kernel<<<(d + 31) / 32, 256, 0, st>>>(part, waves, d, dgamma);
+    parts_reduce_kernel<<<(d + 31) / 32, 256, 0, st>>>(part, wblocks, d, dgamma);
     NML_LAUNCHED();
     return 0;
   }
