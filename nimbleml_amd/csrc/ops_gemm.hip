@@ -14,6 +14,7 @@
 //    and a fused RMSNorm of x (see its comment).
 #include <cstdlib>
 
+#include "gemm_big.hpp"
 #include "kernels.hpp"
 
 namespace nml {
@@ -80,14 +81,58 @@ __device__ __forceinline__ float epilogue(const LinearArgs& a, int m, int n, flo
   return epilogue_with<T, EPI>(a, m, n, acc, bias_v, resid_v);
 }
 
+// fp16 GELU of every fp16 argument, indexed by its bit pattern: the reference's fp16 GELU
+// (gelu_f16, nine roundings and a tanh, ~80 VALU instructions) is a function of its fp16
+// argument alone, so the direct-to-LDS GEMM's epilogue reads it from this 128 KiB table
+// (L2-resident) with one load. Filled by gelu16_tab_kernel from gelu_f16 itself.
+__device__ half_t g_gelu16_tab[65536];
+
+__global__ __launch_bounds__(256) void gelu16_tab_kernel() {
+  const int i = blockIdx.x * 256 + threadIdx.x;
+  const half_t x = __builtin_bit_cast(half_t, static_cast<uint16_t>(i));
+  g_gelu16_tab[i] = static_cast<half_t>(rnd<half_t>(gelu_f16(static_cast<float>(x))));
+}
+
+// Fills the table once per device before its first use (on `st`; inside a stream
+// capture the fill is captured too and the table counts as filled only after an eager fill).
+int gelu16_tab_ready(hipStream_t st) {
+  static bool done[64] = {};
+  int dev = 0;
+  NML_HIP(hipGetDevice(&dev));
+  if (dev >= 0 && dev < 64 && done[dev]) return 0;
+  hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+  NML_HIP(hipStreamIsCapturing(st, &cs));
+  gelu16_tab_kernel<<<256, 256, 0, st>>>();
+  NML_LAUNCHED();
+  if (cs == hipStreamCaptureStatusNone) {
+    NML_HIP(hipStreamSynchronize(st));  // visible to every stream from now on
+    if (dev >= 0 && dev < 64) done[dev] = true;
+  }
+  return 0;
+}
+
 // Epilogue of one 32×32 MFMA tile, fp16: this lane's 16 accumulators are rows
 // mb + 8(r/4) + r%4 of column n (D layout of v_mfma_f32_32x32x16_f16). The residual
 // operands are loaded first, all together (addresses clamped in bounds, loads
 // unconditional, so no wait is forced between them); bias_v is b[n].
-template <int EPI>
+// TAB: the GELU epilogue reads g_gelu16_tab (filled) instead of evaluating gelu_f16.
+template <int EPI, bool TAB = false>
 __device__ __forceinline__ void epilogue_tile32(const LinearArgs& a, int mb, int n, const floatx16& acc,
                                                 float bias_v) {
   const int M = a.M, N = a.N;
+  if constexpr (TAB && EPI == EPI_BIAS_GELU) {
+    if (n >= N) return;
+    half_t* out = static_cast<half_t*>(a.out);
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int m = mb + 8 * (r >> 2) + (r & 3);
+      if (m < M) {
+        const half_t lin = static_cast<half_t>(rnd<half_t>(acc[r]) + bias_v);
+        out[static_cast<size_t>(m) * N + n] = g_gelu16_tab[__builtin_bit_cast(uint16_t, lin)];
+      }
+    }
+    return;
+  }
   if constexpr (EPI == EPI_QKV) {
     // The head-major scatter of epilogue_with, with the column's destination worked out
     // once per tile and each row's (sequence, position) stepped from the tile's first
@@ -248,200 +293,104 @@ __global__ __launch_bounds__(256) void gemm_f16_kernel(LinearArgs a) {
 
 // ------------------------------------------------ fp16 MFMA GEMM, 256×256 block tile
 // For large M·N (prefill, compute_loss): a 512-lane workgroup owns a 256×256 tile; its
-// 8 waves (2×4, two per SIMD, so one multiplies while the other waits) each own
-// 128×64 = 4×2 MFMA 32×32×16 tiles (128 fp32 accumulators), so each A fragment read
-// from LDS feeds 2 MFMAs and each B fragment 4. K advances in stages of 32 through
-// a ring of 4 LDS buffers filled by direct-to-LDS loads (global_load_lds_dwordx4: lane
-// l of a wave writes bytes 16l…16l+15 of a 1 KiB block): three stages are in flight
-// while one is multiplied, and one barrier per stage both publishes a stage and frees
-// the buffer that the stage three ahead reuses.
-// The compiler cannot tell which ring buffer an LDS read touches, and it would wait for
-// every outstanding direct-to-LDS load before each one (and before every workgroup
-// barrier). So the waits are explicit here: a raw s_barrier, s_waitcnt vmcnt(n) for
-// exactly the stages issued after the one about to be read, and fragment reads as
-// ds_read_b128 statements whose results pass through the s_waitcnt lgkmcnt(0) that
-// guards them.
-// LDS rows are 64 B (32 halves); the 16-byte chunk c of row r sits at position
-// c ^ ((r / 4) & 3), so the 16 rows of one 256-byte bank cycle of a fragment read
-// cover all 64 banks. Workgroups are spread XCD-aware (workgroup b runs on XCD b % 8
-// and takes a contiguous range of tiles), grouped GM m-bands at a time so the
-// workgroups resident on one XCD share A bands and B tiles in its L2.
-constexpr int kHM = 256, kHN = 256, kHK = 64, kHStages = 2;
-constexpr int kHStageBytes = (kHM + kHN) * kHK * 2;  // 64 KiB: A then B
+// 8 waves (2×4, two per SIMD) each own 128×64 = 4×2 MFMA 32×32×16 tiles (128 fp32
+// accumulators), so each A fragment read from LDS feeds 2 MFMAs and each B fragment 4.
+// The main loop (stages of 64 k-columns double-buffered in 128 KiB of LDS by
+// direct-to-LDS loads) is big::mainloop. Tiles are ordered XCD by XCD (workgroup b runs
+// on XCD b % 8 and takes a contiguous range of tiles), grouped GM m-bands at a time so
+// the workgroups resident on one XCD share A bands and B tiles in its L2.
+constexpr int kHM = 256, kHN = 256, kHK = big::kK;
+constexpr int kHT = big::kThreads;
 
-// A stage row is 128 bytes (8 chunks of 16). Chunk c of row r sits at position
-// c ^ ((r / 2) & 7): the 16 lanes of a ds_read_b128 phase (rows r…r+15, one chunk) then
-// cover all 64 banks once.
-__device__ __forceinline__ uint32_t swz_off(int row, int chunk) {
-  return static_cast<uint32_t>(row * 128 + ((chunk ^ ((row >> 1) & 7)) << 4));
-}
-
-__device__ __forceinline__ half8 lds_read16(uint32_t addr) {
-  half8 v;
-  asm volatile("ds_read_b128 %0, %1" : "=v"(v) : "v"(addr));
-  return v;
-}
-
-constexpr int kHT = 512;  // 8 waves: 2 per SIMD, so one multiplies while the other waits
-
-template <int EPI, int GM>
-__global__ __launch_bounds__(kHT, 1) void gemm_f16_big_kernel(LinearArgs a, int tiles_n, int tiles) {
+template <int EPI, int GM, int TM, int TN>
+__global__ __launch_bounds__(kHT, TM == 256 ? 1 : 2) void gemm_f16_big_kernel(LinearArgs a, int tiles_n, int tiles) {
   extern __shared__ __attribute__((aligned(1024))) char lds_raw[];
-  const half_t* __restrict__ X = static_cast<const half_t*>(a.x);
-  const half_t* __restrict__ W = static_cast<const half_t*>(a.w);
-  const int tid = threadIdx.x, lane = tid & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int wm = wave >> 2, wn = wave & 3;  // 2 × 4 waves of 128 × 64
-  // XCD-aware tile order (tiles is a multiple of 8), GM m-bands per group
-  const int b = blockIdx.x;
-  const int t = (b & 7) * (tiles >> 3) + (b >> 3);
+  constexpr int IA = TM / 64, JB = TN / 128;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) >> 6);
+  const int wm = wave >> 2, wn = wave & 3;  // 2 × 4 waves of TM/2 × TN/4
+  // XCD-aware tile order, GM m-bands per group
+  const int t = big::xcd_tile(blockIdx.x, tiles);
   const int tiles_m = tiles / tiles_n;
   const int group = t / (GM * tiles_n), first = group * GM;
   const int gm = tiles_m - first < GM ? tiles_m - first : GM;
   const int in = t - group * GM * tiles_n;
-  const int m0 = (first + in % gm) * kHM, n0 = (in / gm) * kHN;
-  const int M = a.M, N = a.N, K = a.K;
-  const long long lda = a.lda;
-  const uint32_t lds0 = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(lds_raw));
+  const int m0 = (first + in % gm) * TM, n0 = (in / gm) * TN;
 
-  // Direct-to-LDS loads of one stage: A and B are 256 rows × 8 chunks each = 32 blocks
-  // of 8 full 128-byte rows; wave w issues blocks 4w…4w+3 of each. Lane l of block q
-  // carries row 8q + l/8 at chunk position l % 8, i.e. global chunk (l % 8) ^ ((row / 2) & 7).
-  // Rows past M or N read row M-1 / N-1 (never stored).
-  const int lrow = lane >> 3, lpos = lane & 7;
-  auto issue = [&](int s) {
-    const int k0 = s * kHK;
-    char* stage = lds_raw + (s % kHStages) * kHStageBytes;
+  floatx16 acc[IA][JB];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int q = wave * 4 + j;
-      const int row = 8 * q + lrow;
-      const int ch = lpos ^ ((row >> 1) & 7);
-      const int gmr = m0 + row < M ? m0 + row : M - 1;
-      const int gnr = n0 + row < N ? n0 + row : N - 1;
-      // (address-space casts: global source, LDS destination)
-      __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)(X + gmr * lda + k0 + ch * 8),
-                                       (__attribute__((address_space(3))) void*)(stage + q * 1024), 16, 0, 0);
-      __builtin_amdgcn_global_load_lds(
-          (const __attribute__((address_space(1))) void*)(W + static_cast<long long>(gnr) * K + k0 + ch * 8),
-          (__attribute__((address_space(3))) void*)(stage + kHM * kHK * 2 + q * 1024), 16, 0, 0);
-    }
-  };
-
-  floatx16 acc[4][2];
+  for (int i = 0; i < IA; ++i)
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
-#pragma unroll
-    for (int j = 0; j < 2; ++j)
+    for (int j = 0; j < JB; ++j)
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
-
-  // per-lane fragment rows within a stage (the chunk is XORed in below)
-  uint32_t offa[4], offb[2];
-#pragma unroll
-  for (int i = 0; i < 4; ++i) offa[i] = static_cast<uint32_t>(wm * 128 + i * 32 + (lane & 31));
-#pragma unroll
-  for (int j = 0; j < 2; ++j) offb[j] = static_cast<uint32_t>(wn * 64 + j * 32 + (lane & 31));
-
-  // Double-buffered stages, software-pipelined fragments: the next 16-wide k step's
-  // fragments are read from LDS while the current step's MFMAs run. Stage t's barrier
-  // (every wave's loads of t landed, every wave done reading t - 1) is followed by the
-  // loads of stage t + 1 into t - 1's buffer; before a stage's last step each wave has
-  // its fragments in registers, so the next barrier may release the buffer.
-  const int S = K / kHK;
-  auto wait_stage = [&](int t) {
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    __builtin_amdgcn_s_barrier();
-    if (t + 1 < S) issue(t + 1);
-  };
-  half8 fa0[4], fb0[2], fa1[4], fb1[2];
-  auto read = [&](half8 (&fa)[4], half8 (&fb)[2], int t, int kk) {
-    const uint32_t base = lds0 + static_cast<uint32_t>((t % kHStages) * kHStageBytes);
-    const int ch = 2 * kk + (lane >> 5);
-#pragma unroll
-    for (int i = 0; i < 4; ++i) fa[i] = lds_read16(base + swz_off(offa[i], ch));
-#pragma unroll
-    for (int j = 0; j < 2; ++j) fb[j] = lds_read16(base + kHM * kHK * 2 + swz_off(offb[j], ch));
-  };
-  auto mma = [&](const half8 (&fa)[4], const half8 (&fb)[2]) {
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-#pragma unroll
-      for (int j = 0; j < 2; ++j)
-        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(fa[i], fb[j], acc[i][j], 0, 0, 0);
-  };
-#define NML_LGKM(n, fa, fb)                                                                    \
-  asm volatile("s_waitcnt lgkmcnt(" #n ")"                                                     \
-               : "+v"(fa[0]), "+v"(fa[1]), "+v"(fa[2]), "+v"(fa[3]), "+v"(fb[0]), "+v"(fb[1]))
-  issue(0);
-  wait_stage(0);
-  read(fa0, fb0, 0, 0);
-  for (int s = 0; s < S; ++s) {
-    read(fa1, fb1, s, 1);
-    NML_LGKM(6, fa0, fb0);
-    mma(fa0, fb0);
-    read(fa0, fb0, s, 2);
-    NML_LGKM(6, fa1, fb1);
-    mma(fa1, fb1);
-    read(fa1, fb1, s, 3);
-    NML_LGKM(6, fa0, fb0);
-    mma(fa0, fb0);
-    NML_LGKM(0, fa1, fb1);
-    if (s + 1 < S) {
-      wait_stage(s + 1);
-      read(fa0, fb0, s + 1, 0);
-    }
-    mma(fa1, fb1);
-  }
-#undef NML_LGKM
+  big::mainloop<TM, TN>(static_cast<const half_t*>(a.x), a.lda, static_cast<const half_t*>(a.w), a.K, a.M,
+                        a.N, 0, a.K / kHK, m0, n0, lds_raw, acc);
 
   // D layout of a 32×32 MFMA tile: lane l, register r → row 8(r/4) + 4(l/32) + r%4, col l%32.
-  {  // written out: a loop here is not always unrolled, and acc must stay in registers
-    const int na = n0 + wn * 64 + (lane & 31), nb = na + 32;
-    const float ba = bias_at<EPI>(a, na), bb = bias_at<EPI>(a, nb);
-    const int mb = m0 + wm * 128 + 4 * (lane >> 5);
-    epilogue_tile32<EPI>(a, mb, na, acc[0][0], ba);
-    epilogue_tile32<EPI>(a, mb, nb, acc[0][1], bb);
-    epilogue_tile32<EPI>(a, mb + 32, na, acc[1][0], ba);
-    epilogue_tile32<EPI>(a, mb + 32, nb, acc[1][1], bb);
-    epilogue_tile32<EPI>(a, mb + 64, na, acc[2][0], ba);
-    epilogue_tile32<EPI>(a, mb + 64, nb, acc[2][1], bb);
-    epilogue_tile32<EPI>(a, mb + 96, na, acc[3][0], ba);
-    epilogue_tile32<EPI>(a, mb + 96, nb, acc[3][1], bb);
+  // Written out: a loop here is not always unrolled, and acc must stay in registers.
+  const int na = n0 + wn * (TN / 4) + (lane & 31);
+  const float ba = bias_at<EPI>(a, na);
+  const int mb = m0 + wm * (TM / 2) + 4 * (lane >> 5);
+  if constexpr (TM == 256 && TN == 256) {
+    const int nb = na + 32;
+    const float bb = bias_at<EPI>(a, nb);
+    epilogue_tile32<EPI, true>(a, mb, na, acc[0][0], ba);
+    epilogue_tile32<EPI, true>(a, mb, nb, acc[0][1], bb);
+    epilogue_tile32<EPI, true>(a, mb + 32, na, acc[1][0], ba);
+    epilogue_tile32<EPI, true>(a, mb + 32, nb, acc[1][1], bb);
+    epilogue_tile32<EPI, true>(a, mb + 64, na, acc[2][0], ba);
+    epilogue_tile32<EPI, true>(a, mb + 64, nb, acc[2][1], bb);
+    epilogue_tile32<EPI, true>(a, mb + 96, na, acc[3][0], ba);
+    epilogue_tile32<EPI, true>(a, mb + 96, nb, acc[3][1], bb);
+  } else {
+    static_assert(TM == 128 && TN == 128, "tile");
+    epilogue_tile32<EPI, true>(a, mb, na, acc[0][0], ba);
+    epilogue_tile32<EPI, true>(a, mb + 32, na, acc[1][0], ba);
   }
 }
 
-constexpr size_t kBigLds = static_cast<size_t>(kHStages) * kHStageBytes;  // 128 KiB
-
-template <int EPI, int GM>
+template <int EPI, int GM, int TM, int TN>
 int gemm_big_launch_gm(const LinearArgs& a, hipStream_t st) {
   static bool attr = false;
+  constexpr size_t lds = big::Shape<TM, TN>::Lds;  // 128 KiB (256 × 256) or 64 KiB (128 × 128)
   if (!attr) {
-    NML_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(&gemm_f16_big_kernel<EPI, GM>),
-                                hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(kBigLds)));
+    NML_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(&gemm_f16_big_kernel<EPI, GM, TM, TN>),
+                                hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds)));
     attr = true;
   }
-  const int tiles_n = (a.N + kHN - 1) / kHN, tiles_m = (a.M + kHM - 1) / kHM;
+  const int tiles_n = (a.N + TN - 1) / TN, tiles_m = (a.M + TM - 1) / TM;
   const int tiles = tiles_n * tiles_m;
-  gemm_f16_big_kernel<EPI, GM><<<tiles, kHT, kBigLds, st>>>(a, tiles_n, tiles);
+  gemm_f16_big_kernel<EPI, GM, TM, TN><<<tiles, kHT, lds, st>>>(a, tiles_n, tiles);
   NML_LAUNCHED();
   return 0;
 }
 
-template <int EPI>
-int gemm_big_launch(const LinearArgs& a, hipStream_t st) {
-  const char* e = std::getenv("NIMBLEML_BIG_GM");
-  const int gm = e ? atoi(e) : 4;
-  if (gm == 1) return gemm_big_launch_gm<EPI, 1>(a, st);
-  if (gm == 8) return gemm_big_launch_gm<EPI, 8>(a, st);
-  return gemm_big_launch_gm<EPI, 4>(a, st);
+// 256 × 256 tiles where they fill the chip (≥ 256 of them), else 128 × 128 tiles on the
+// same main loop (two workgroups per CU).
+bool big_gemm_wide(const LinearArgs& a) {
+  const long long tm = (a.M + kHM - 1) / kHM, tn = (a.N + kHN - 1) / kHN;
+  return a.M >= 1024 && (tm * tn) % 8 == 0 && tm * tn >= 256;
 }
 
+template <int EPI>
+int gemm_big_launch(const LinearArgs& a, hipStream_t st) {
+  if constexpr (EPI == EPI_BIAS_GELU) NML_TRY(gelu16_tab_ready(st));
+  if (!big_gemm_wide(a)) return gemm_big_launch_gm<EPI, 4, 128, 128>(a, st);
+  const char* e = std::getenv("NIMBLEML_BIG_GM");
+  const int gm = e ? atoi(e) : 4;
+  if (gm == 1) return gemm_big_launch_gm<EPI, 1, kHM, kHN>(a, st);
+  if (gm == 8) return gemm_big_launch_gm<EPI, 8, kHM, kHN>(a, st);
+  return gemm_big_launch_gm<EPI, 4, kHM, kHN>(a, st);
+}
+
+// The direct-to-LDS kernels: K a multiple of 64, 16-byte aligned rows, and enough rows
+// for 128-row tiles to be mostly full.
 bool big_gemm_applies(const LinearArgs& a) {
   if (std::getenv("NIMBLEML_BIG_GEMM") && std::getenv("NIMBLEML_BIG_GEMM")[0] == '0') return false;
-  const long long tm = (a.M + kHM - 1) / kHM, tn = (a.N + kHN - 1) / kHN;
-  return a.K % kHK == 0 && a.lda % 8 == 0 && a.M >= 1024 && (tm * tn) % 8 == 0 && tm * tn >= 256 &&
-         (reinterpret_cast<uintptr_t>(a.x) & 15) == 0;
+  if (a.K % kHK != 0 || a.lda % 8 != 0 || (reinterpret_cast<uintptr_t>(a.x) & 15) != 0) return false;
+  if (big_gemm_wide(a)) return true;
+  return a.M >= 256 && !(std::getenv("NIMBLEML_BIG_GEMM") && std::getenv("NIMBLEML_BIG_GEMM")[0] == 'w');
 }
 
 // ---------------------------------------------------------------- fp32 MFMA GEMM

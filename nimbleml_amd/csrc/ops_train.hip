@@ -18,6 +18,7 @@
 //    and a second pass in a fixed order: the result does not depend on scheduling.
 #include <cstdlib>
 
+#include "gemm_big.hpp"
 #include "kernels.hpp"
 
 namespace nml {
@@ -63,7 +64,9 @@ __device__ __forceinline__ float gelu_grad(float x) {
 
 // fp16: g·gelu'(x) in the fp16 ops of kernels/fused_gelu.py:97-102 (tu as the fp16 forward
 // forms it, kernels/fused_gelu.py:67; each product and sum rounded to fp16).
-__device__ __forceinline__ float gelu_grad_f16(float g, float x) {
+// The factor gelu'(x) of the fp16 branch, a function of the fp16 x alone;
+// gelu_grad_f16(g, x) = fp16(g · factor).
+__device__ __forceinline__ float gelu_grad_f16_factor(float x) {
 #pragma clang fp contract(off)
   const float k = static_cast<float>(static_cast<half_t>(0.7978845608028654f));
   const float c = static_cast<float>(static_cast<half_t>(0.044715f));
@@ -83,8 +86,36 @@ __device__ __forceinline__ float gelu_grad_f16(float g, float x) {
   float b = rnd<half_t>(0.5f * x);
   b = rnd<half_t>(b * sech2);
   b = rnd<half_t>(b * du);
-  const float d = rnd<half_t>(a + b);
-  return rnd<half_t>(g * d);
+  return rnd<half_t>(a + b);
+}
+
+__device__ __forceinline__ float gelu_grad_f16(float g, float x) {
+#pragma clang fp contract(off)
+  return rnd<half_t>(g * gelu_grad_f16_factor(x));
+}
+
+// gelu_grad_f16_factor of every fp16 x, indexed by its bit pattern (128 KiB, L2-resident):
+// the direct-to-LDS backward GEMM's GELU epilogue reads the factor with one load instead
+// of ~70 VALU instructions. Filled from gelu_grad_f16_factor itself.
+__device__ half_t g_dgelu16_tab[65536];
+
+__global__ __launch_bounds__(256) void dgelu16_tab_kernel() {
+  const int i = blockIdx.x * 256 + threadIdx.x;
+  const half_t x = __builtin_bit_cast(half_t, static_cast<uint16_t>(i));
+  g_dgelu16_tab[i] = static_cast<half_t>(gelu_grad_f16_factor(static_cast<float>(x)));
+}
+
+// Once per device before the first use (training is never captured).
+int dgelu16_tab_ready(hipStream_t st) {
+  static bool done[64] = {};
+  int dev = 0;
+  NML_HIP(hipGetDevice(&dev));
+  if (dev >= 0 && dev < 64 && done[dev]) return 0;
+  dgelu16_tab_kernel<<<256, 256, 0, st>>>();
+  NML_LAUNCHED();
+  NML_HIP(hipStreamSynchronize(st));
+  if (dev >= 0 && dev < 64) done[dev] = true;
+  return 0;
 }
 
 // One operand tile (128 rows × 16 k) into LDS as S[k][row]. KC: element (r, k) at
@@ -361,6 +392,194 @@ struct SplitWs {
   size_t floats = 0;
 };
 SplitWs g_split;
+
+// ------------------------------------------- float16 backward GEMM on big::mainloop
+// The backward's products read one operand (dX = dY·W: W) or both (dW = dYᵀ·X) across k.
+// Those operands are first transposed into a workspace (transpose16_kernel, HBM-bound,
+// a few µs per weight) so that both are k-contiguous rows, and the product then runs on
+// the prefill GEMM's direct-to-LDS main loop: 256 × 256 tiles where they fill the chip,
+// 128 × 128 tiles (two workgroups per CU) otherwise, and split K for the weight
+// gradients whose output tiles are few.
+
+// dst[c·ldd + r] = src[r·lds + c] for r < rows, c < cols (fp16; rows and cols multiples
+// of 8, strides multiples of 8, both 16-byte aligned); one 64 × 64 tile per workgroup.
+__global__ __launch_bounds__(256) void transpose16_kernel(const half_t* __restrict__ src, long long lds,
+                                                          int rows, int cols, half_t* __restrict__ dst,
+                                                          long long ldd) {
+  __shared__ half_t t[64][66];  // row stride 132 bytes: column reads spread over the banks
+  const int r0 = blockIdx.y * 64, c0 = blockIdx.x * 64, tid = threadIdx.x;
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const int p = tid + 256 * i, r = p >> 3, c8 = (p & 7) * 8;
+    if (r0 + r < rows && c0 + c8 < cols) {
+      const half8 v = *reinterpret_cast<const half8*>(src + static_cast<long long>(r0 + r) * lds + c0 + c8);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) t[r][c8 + e] = v[e];
+    }
+  }
+  __syncthreads();
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const int p = tid + 256 * i, c = p >> 3, r8 = (p & 7) * 8;
+    if (c0 + c < cols && r0 + r8 < rows) {
+      half8 v;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) v[e] = t[r8 + e][c];
+      *reinterpret_cast<half8*>(dst + static_cast<long long>(c0 + c) * ldd + r0 + r8) = v;
+    }
+  }
+}
+
+// c (m, n) = out(Σ_k a[m·lda + k] · b[n·ldb + k]) over this split's k range, output modes
+// as gemm_bwd_f16_kernel. Workgroup b → (split, tile) through the XCD-aware order;
+// `tiles_m` m-tiles per column of tiles.
+template <int TM, int TN, int OUT>
+__global__ __launch_bounds__(big::kThreads, TM == 256 ? 1 : 2) void gemm_bwd_big_kernel(
+    GemmBwdArgs g, int tiles_m, int tiles, int splits, int kchunk, long long zstride) {
+  extern __shared__ __attribute__((aligned(1024))) char lds_raw[];
+  constexpr int IA = TM / 64, JB = TN / 128;
+  const int u = big::xcd_tile(blockIdx.x, tiles * splits);
+  const int z = u % splits, tile = u / splits;
+  const int m0 = (tile % tiles_m) * TM, n0 = (tile / tiles_m) * TN;
+  const int kbeg = z * kchunk;
+  const int klen = min(kchunk, g.K - kbeg);
+  floatx16 acc[IA][JB];
+#pragma unroll
+  for (int i = 0; i < IA; ++i)
+#pragma unroll
+    for (int j = 0; j < JB; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
+  big::mainloop<TM, TN>(static_cast<const half_t*>(g.a), g.lda, static_cast<const half_t*>(g.b), g.ldb, g.M,
+                        g.N, kbeg, klen / big::kK, m0, n0, lds_raw, acc);
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int wm = wave >> 2, wn = wave & 3;
+#pragma unroll
+  for (int i = 0; i < IA; ++i)
+#pragma unroll
+    for (int j = 0; j < JB; ++j) {
+      const int n = n0 + wn * (TN / 4) + j * 32 + (lane & 31);
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int m = m0 + wm * (TM / 2) + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+        if (m < g.M && n < g.N) {
+          const long long ci = z * zstride + static_cast<long long>(m) * g.ldc + n;
+          const float v = acc[i][j][r];
+          if constexpr (OUT == kGBPart) {
+            static_cast<float*>(g.c)[ci] = v;
+          } else if constexpr (OUT == GB_ADD) {
+            static_cast<float*>(g.c)[ci] += rnd<half_t>(v);
+          } else if constexpr (OUT == GB_SET) {
+            static_cast<half_t*>(g.c)[ci] = static_cast<half_t>(v);
+          } else {
+            const half_t x = static_cast<const half_t*>(g.aux)[static_cast<long long>(m) * g.ldaux + n];
+            const float f = static_cast<float>(g_dgelu16_tab[__builtin_bit_cast(uint16_t, x)]);
+            static_cast<half_t*>(g.c)[ci] = static_cast<half_t>(rnd<half_t>(rnd<half_t>(v) * f));
+          }
+        }
+      }
+    }
+}
+
+// Grow-only device workspaces (training is never captured into a graph).
+struct Ws {
+  void* p = nullptr;
+  size_t bytes = 0;
+};
+Ws g_tws;  // transposed operands
+
+int ws_ensure(Ws& w, size_t bytes, hipStream_t st) {
+  if (bytes <= w.bytes) return 0;
+  NML_HIP(hipStreamSynchronize(st));
+  if (w.p) NML_HIP(hipFree(w.p));
+  w = Ws{};
+  NML_HIP(hipMalloc(&w.p, bytes));
+  w.bytes = bytes;
+  return 0;
+}
+
+template <int TM, int TN, int OUT>
+int big_bwd_launch(const GemmBwdArgs& g, int splits, int kchunk, long long zstride, hipStream_t st) {
+  static bool attr = false;
+  const void* fn = reinterpret_cast<const void*>(&gemm_bwd_big_kernel<TM, TN, OUT>);
+  if (!attr) {
+    NML_HIP(hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                static_cast<int>(big::Shape<TM, TN>::Lds)));
+    attr = true;
+  }
+  const int tiles_m = (g.M + TM - 1) / TM, tiles = tiles_m * ((g.N + TN - 1) / TN);
+  gemm_bwd_big_kernel<TM, TN, OUT><<<tiles * splits, big::kThreads, big::Shape<TM, TN>::Lds, st>>>(
+      g, tiles_m, tiles, splits, kchunk, zstride);
+  NML_LAUNCHED();
+  return 0;
+}
+
+template <int TM, int TN>
+int big_bwd_out(const GemmBwdArgs& g, int out, int splits, int kchunk, long long zstride, hipStream_t st) {
+  switch (out) {
+    case GB_SET: return big_bwd_launch<TM, TN, GB_SET>(g, splits, kchunk, zstride, st);
+    case GB_ADD: return big_bwd_launch<TM, TN, GB_ADD>(g, splits, kchunk, zstride, st);
+    case GB_GELU: return big_bwd_launch<TM, TN, GB_GELU>(g, splits, kchunk, zstride, st);
+    case kGBPart: return big_bwd_launch<TM, TN, kGBPart>(g, splits, kchunk, zstride, st);
+    default: set_error("gemm_bwd: unknown output mode %d", out); return -1;
+  }
+}
+
+// The float16 product on big::mainloop; K a multiple of big::kK, operands as
+// launch_gemm_bwd's 16-byte conditions.
+int gemm_bwd_big(const GemmBwdArgs& g0, bool a_kc, bool b_kc, int out, hipStream_t st) {
+  if (out == GB_GELU) NML_TRY(dgelu16_tab_ready(st));
+  GemmBwdArgs g = g0;
+  const long long M = g.M, N = g.N, K = g.K;
+  const size_t at = a_kc ? 0 : static_cast<size_t>(M * K), bt = b_kc ? 0 : static_cast<size_t>(N * K);
+  if (at + bt) {
+    if (ws_ensure(g_tws, (at + bt) * sizeof(half_t), st) != 0) return -1;
+    half_t* ws = static_cast<half_t*>(g_tws.p);
+    if (!a_kc) {  // a: (k, m) at a[k·lda + m]
+      transpose16_kernel<<<dim3((g.M + 63) / 64, (g.K + 63) / 64), 256, 0, st>>>(
+          static_cast<const half_t*>(g.a), g.lda, g.K, g.M, ws, K);
+      NML_LAUNCHED();
+      g.a = ws;
+      g.lda = K;
+    }
+    if (!b_kc) {  // b: (k, n) at b[k·ldb + n]
+      transpose16_kernel<<<dim3((g.N + 63) / 64, (g.K + 63) / 64), 256, 0, st>>>(
+          static_cast<const half_t*>(g.b), g.ldb, g.K, g.N, ws + at, K);
+      NML_LAUNCHED();
+      g.b = ws + at;
+      g.ldb = K;
+    }
+  }
+  // 128 × 128 tiles, two workgroups per CU (256 × 256 tiles measured slower here: the
+  // backward's products have at most 4096 × 4096 outputs, one round of large tiles, and
+  // the GELU-backward epilogue then overlaps nothing)
+  const long long tiles = ((M + 127) / 128) * ((N + 127) / 128);
+  // Split K (accumulating outputs only): while the grid is short of two workgroups per CU
+  // and each slice keeps ≥ 1024 of k.
+  int splits = 1;
+  if (out == GB_ADD)
+    while (splits < 16 && tiles * splits < 512 && K / (2 * splits) >= 1024) splits *= 2;
+  const int steps = static_cast<int>(K / big::kK);
+  const int kchunk = (steps + splits - 1) / splits * big::kK;
+  splits = static_cast<int>((K + kchunk - 1) / kchunk);  // no empty slice
+  if (splits == 1) return big_bwd_out<128, 128>(g, out, 1, kchunk, 0, st);
+  const size_t need = static_cast<size_t>(splits) * M * N;
+  if (need > g_split.floats) {
+    NML_HIP(hipStreamSynchronize(st));
+    if (g_split.p) NML_HIP(hipFree(g_split.p));
+    g_split = SplitWs{};
+    NML_HIP(hipMalloc(&g_split.p, need * sizeof(float)));
+    g_split.floats = need;
+  }
+  GemmBwdArgs p = g;
+  p.c = g_split.p;
+  p.ldc = g.N;
+  NML_TRY((big_bwd_out<128, 128>(p, kGBPart, splits, kchunk, M * N, st)));
+  splitk_reduce_kernel<half_t><<<static_cast<int>((M * N + 255) / 256), 256, 0, st>>>(
+      g_split.p, splits, g.M, g.N, static_cast<float*>(g.c), g.ldc);
+  NML_LAUNCHED();
+  return 0;
+}
 
 template <bool A_KC, bool B_KC, typename T>
 int gemm_bwd_out(const GemmBwdArgs& g, int out, hipStream_t st, bool mfma16 = false) {
@@ -1514,6 +1733,8 @@ int launch_gemm_bwd(int dt, const GemmBwdArgs& g, bool a_kc, bool b_kc, int out,
                      ((reinterpret_cast<uintptr_t>(g.a) | reinterpret_cast<uintptr_t>(g.b)) & 15) == 0 &&
                      g.lda % 8 == 0 && g.ldb % 8 == 0 && (a_kc ? g.K % 8 == 0 : g.M % 8 == 0) &&
                      (b_kc ? g.K % 8 == 0 : g.N % 8 == 0);
+    const char* bigenv = std::getenv("NIMBLEML_TRAIN_F16_BIG");
+    if (m16 && g.K % big::kK == 0 && !(bigenv && bigenv[0] == '0')) return gemm_bwd_big(g, a_kc, b_kc, out, st);
     if (a_kc)
       return b_kc ? gemm_bwd_out<true, true, half_t>(g, out, st, m16) : gemm_bwd_out<true, false, half_t>(g, out, st, m16);
     return b_kc ? gemm_bwd_out<false, true, half_t>(g, out, st, m16) : gemm_bwd_out<false, false, half_t>(g, out, st, m16);

@@ -278,10 +278,13 @@ def test_linear_skinny_fp16(gpu, rows, k, epi):
 
 
 @pytest.mark.parametrize("rows,k,n,epi", [(4096, 256, 4096, 0), (4096, 192, 4224, 1),
-                                          (4096, 128, 4224, 2), (3000, 256, 4224, 3)])
+                                          (4096, 128, 4224, 2), (3000, 256, 4224, 3),
+                                          (1024, 192, 3072, 1), (700, 256, 1000, 3),
+                                          (300, 128, 520, 2), (515, 64, 136, 0)])
 def test_linear_big_tile_fp16(gpu, rows, k, n, epi):
-    """Prefill-sized shapes (≥ 256 tiles of 256×256): the large-tile MFMA GEMM, with a
-    ragged last column tile (n = 4224) and a ragged last row tile (rows = 3000)."""
+    """Prefill-sized shapes on the direct-to-LDS MFMA GEMM: 256×256 tiles where there are
+    ≥ 256 of them, 128×128 tiles below that (the last four shapes), with ragged last column
+    tiles (n = 4224, 1000, 520, 136) and ragged last row tiles (rows = 3000, 700, 300, 515)."""
     rng = np.random.default_rng(rows + k + n + epi)
     x = rng.standard_normal((rows, k)).astype(np.float16)
     w = (rng.standard_normal((k, n)) * (1.0 / np.sqrt(k))).astype(np.float16)

@@ -188,7 +188,7 @@ def test_c_abi_backward_accumulates_and_matches_loss(gpu):
 
 
 @pytest.mark.parametrize("dims,b,s", [((256, 64, 4, 2, 64), 2, 40), ((512, 128, 2, 2, 96), 2, 70),
-                                      ((512, 256, 2, 1, 64), 2, 33)])
+                                      ((512, 256, 2, 1, 64), 2, 33), ((256, 128, 2, 1, 128), 2, 128)])
 def test_backward_fp16(gpu, dims, b, s):
     """float16 models: the loss equals the fp16 oracle's (the reference's fp16 rounding),
     and the gradients (kept float32, as under an optimizer's _grad_dtype) match the float64
@@ -225,6 +225,32 @@ def test_backward_fp16(gpu, dims, b, s):
         if not k.endswith("W_k.biases"):
             worst = max(worst, err / np.abs(ref).max())
     print("worst relative gradient error (fp16)", worst)
+
+
+def test_backward_fp16_direct_to_lds_path_matches_register_path(gpu, monkeypatch):
+    """The float16 backward GEMMs on the direct-to-LDS main loop (operands read across k
+    transposed first; split K for the weight gradients, 2048 rows) against the
+    register-staged kernel (NIMBLEML_TRAIN_F16_BIG=0) on the same model and batch: the two
+    differ only in the fp32 summation order, so every gradient agrees within 2e-3 of the
+    tensor's largest."""
+    import nimbleml_amd as nm
+
+    cfg = GPTConfig(512, 128, 2, 2, 512)
+    w16 = {k: v.astype(np.float16) for k, v in make_weights(cfg, seed=32, rich=True).items()}
+    ids = random_ids((4, 512), cfg.vocab_size, seed=26)
+    labels = random_ids((4 * 512,), cfg.vocab_size, seed=27)
+    grads = []
+    for big in ("1", "0"):
+        monkeypatch.setenv("NIMBLEML_TRAIN_F16_BIG", big)
+        m = nm.GPT.from_arrays(w16, cfg.vocab_size, cfg.d_model, cfg.num_heads, cfg.num_layers,
+                               cfg.max_seq_len, dtype=np.float16)
+        for p in m.parameters():
+            p._grad_dtype = np.float32
+        m.compute_loss(ids, labels).backward()
+        grads.append(_named_grads(m))
+    for k, ref in grads[1].items():
+        err = np.abs(grads[0][k].astype(np.float64) - ref).max()
+        assert err <= 2e-3 * np.abs(ref).max() + 1e-6, (k, err, np.abs(ref).max())
 
 
 def test_model_adamw_step_fp16_masters(gpu):
