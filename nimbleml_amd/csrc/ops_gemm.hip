@@ -81,58 +81,14 @@ __device__ __forceinline__ float epilogue(const LinearArgs& a, int m, int n, flo
   return epilogue_with<T, EPI>(a, m, n, acc, bias_v, resid_v);
 }
 
-// fp16 GELU of every fp16 argument, indexed by its bit pattern: the reference's fp16 GELU
-// (gelu_f16, nine roundings and a tanh, ~80 VALU instructions) is a function of its fp16
-// argument alone, so the direct-to-LDS GEMM's epilogue reads it from this 128 KiB table
-// (L2-resident) with one load. Filled by gelu16_tab_kernel from gelu_f16 itself.
-__device__ half_t g_gelu16_tab[65536];
-
-__global__ __launch_bounds__(256) void gelu16_tab_kernel() {
-  const int i = blockIdx.x * 256 + threadIdx.x;
-  const half_t x = __builtin_bit_cast(half_t, static_cast<uint16_t>(i));
-  g_gelu16_tab[i] = static_cast<half_t>(rnd<half_t>(gelu_f16(static_cast<float>(x))));
-}
-
-// Fills the table once per device before its first use (on `st`; inside a stream
-// capture the fill is captured too and the table counts as filled only after an eager fill).
-int gelu16_tab_ready(hipStream_t st) {
-  static bool done[64] = {};
-  int dev = 0;
-  NML_HIP(hipGetDevice(&dev));
-  if (dev >= 0 && dev < 64 && done[dev]) return 0;
-  hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
-  NML_HIP(hipStreamIsCapturing(st, &cs));
-  gelu16_tab_kernel<<<256, 256, 0, st>>>();
-  NML_LAUNCHED();
-  if (cs == hipStreamCaptureStatusNone) {
-    NML_HIP(hipStreamSynchronize(st));  // visible to every stream from now on
-    if (dev >= 0 && dev < 64) done[dev] = true;
-  }
-  return 0;
-}
-
 // Epilogue of one 32×32 MFMA tile, fp16: this lane's 16 accumulators are rows
 // mb + 8(r/4) + r%4 of column n (D layout of v_mfma_f32_32x32x16_f16). The residual
 // operands are loaded first, all together (addresses clamped in bounds, loads
 // unconditional, so no wait is forced between them); bias_v is b[n].
-// TAB: the GELU epilogue reads g_gelu16_tab (filled) instead of evaluating gelu_f16.
-template <int EPI, bool TAB = false>
+template <int EPI>
 __device__ __forceinline__ void epilogue_tile32(const LinearArgs& a, int mb, int n, const floatx16& acc,
                                                 float bias_v) {
   const int M = a.M, N = a.N;
-  if constexpr (TAB && EPI == EPI_BIAS_GELU) {
-    if (n >= N) return;
-    half_t* out = static_cast<half_t*>(a.out);
-#pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const int m = mb + 8 * (r >> 2) + (r & 3);
-      if (m < M) {
-        const half_t lin = static_cast<half_t>(rnd<half_t>(acc[r]) + bias_v);
-        out[static_cast<size_t>(m) * N + n] = g_gelu16_tab[__builtin_bit_cast(uint16_t, lin)];
-      }
-    }
-    return;
-  }
   if constexpr (EPI == EPI_QKV) {
     // The head-major scatter of epilogue_with, with the column's destination worked out
     // once per tile and each row's (sequence, position) stepped from the tile's first
@@ -303,7 +259,7 @@ constexpr int kHM = 256, kHN = 256, kHK = big::kK;
 constexpr int kHT = big::kThreads;
 
 template <int EPI, int GM, int TM, int TN>
-__global__ __launch_bounds__(kHT, TM == 256 ? 1 : 2) void gemm_f16_big_kernel(LinearArgs a, int tiles_n, int tiles) {
+__global__ __launch_bounds__(kHT, TM == 256 ? 1 : 4) void gemm_f16_big_kernel(LinearArgs a, int tiles_n, int tiles) {
   extern __shared__ __attribute__((aligned(1024))) char lds_raw[];
   constexpr int IA = TM / 64, JB = TN / 128;
   const int lane = threadIdx.x & 63;
@@ -335,18 +291,18 @@ __global__ __launch_bounds__(kHT, TM == 256 ? 1 : 2) void gemm_f16_big_kernel(Li
   if constexpr (TM == 256 && TN == 256) {
     const int nb = na + 32;
     const float bb = bias_at<EPI>(a, nb);
-    epilogue_tile32<EPI, true>(a, mb, na, acc[0][0], ba);
-    epilogue_tile32<EPI, true>(a, mb, nb, acc[0][1], bb);
-    epilogue_tile32<EPI, true>(a, mb + 32, na, acc[1][0], ba);
-    epilogue_tile32<EPI, true>(a, mb + 32, nb, acc[1][1], bb);
-    epilogue_tile32<EPI, true>(a, mb + 64, na, acc[2][0], ba);
-    epilogue_tile32<EPI, true>(a, mb + 64, nb, acc[2][1], bb);
-    epilogue_tile32<EPI, true>(a, mb + 96, na, acc[3][0], ba);
-    epilogue_tile32<EPI, true>(a, mb + 96, nb, acc[3][1], bb);
+    epilogue_tile32<EPI>(a, mb, na, acc[0][0], ba);
+    epilogue_tile32<EPI>(a, mb, nb, acc[0][1], bb);
+    epilogue_tile32<EPI>(a, mb + 32, na, acc[1][0], ba);
+    epilogue_tile32<EPI>(a, mb + 32, nb, acc[1][1], bb);
+    epilogue_tile32<EPI>(a, mb + 64, na, acc[2][0], ba);
+    epilogue_tile32<EPI>(a, mb + 64, nb, acc[2][1], bb);
+    epilogue_tile32<EPI>(a, mb + 96, na, acc[3][0], ba);
+    epilogue_tile32<EPI>(a, mb + 96, nb, acc[3][1], bb);
   } else {
     static_assert(TM == 128 && TN == 128, "tile");
-    epilogue_tile32<EPI, true>(a, mb, na, acc[0][0], ba);
-    epilogue_tile32<EPI, true>(a, mb + 32, na, acc[1][0], ba);
+    epilogue_tile32<EPI>(a, mb, na, acc[0][0], ba);
+    epilogue_tile32<EPI>(a, mb + 32, na, acc[1][0], ba);
   }
 }
 
@@ -375,7 +331,6 @@ bool big_gemm_wide(const LinearArgs& a) {
 
 template <int EPI>
 int gemm_big_launch(const LinearArgs& a, hipStream_t st) {
-  if constexpr (EPI == EPI_BIAS_GELU) NML_TRY(gelu16_tab_ready(st));
   if (!big_gemm_wide(a)) return gemm_big_launch_gm<EPI, 4, 128, 128>(a, st);
   const char* e = std::getenv("NIMBLEML_BIG_GM");
   const int gm = e ? atoi(e) : 4;

@@ -434,7 +434,7 @@ __global__ __launch_bounds__(256) void transpose16_kernel(const half_t* __restri
 // as gemm_bwd_f16_kernel. Workgroup b → (split, tile) through the XCD-aware order;
 // `tiles_m` m-tiles per column of tiles.
 template <int TM, int TN, int OUT>
-__global__ __launch_bounds__(big::kThreads, TM == 256 ? 1 : 2) void gemm_bwd_big_kernel(
+__global__ __launch_bounds__(big::kThreads, TM == 256 ? 1 : 4) void gemm_bwd_big_kernel(
     GemmBwdArgs g, int tiles_m, int tiles, int splits, int kchunk, long long zstride) {
   extern __shared__ __attribute__((aligned(1024))) char lds_raw[];
   constexpr int IA = TM / 64, JB = TN / 128;
@@ -443,6 +443,8 @@ __global__ __launch_bounds__(big::kThreads, TM == 256 ? 1 : 2) void gemm_bwd_big
   const int m0 = (tile % tiles_m) * TM, n0 = (tile / tiles_m) * TN;
   const int kbeg = z * kchunk;
   const int klen = min(kchunk, g.K - kbeg);
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int wm = wave >> 2, wn = wave & 3;
   floatx16 acc[IA][JB];
 #pragma unroll
   for (int i = 0; i < IA; ++i)
@@ -452,29 +454,42 @@ __global__ __launch_bounds__(big::kThreads, TM == 256 ? 1 : 2) void gemm_bwd_big
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
   big::mainloop<TM, TN>(static_cast<const half_t*>(g.a), g.lda, static_cast<const half_t*>(g.b), g.ldb, g.M,
                         g.N, kbeg, klen / big::kK, m0, n0, lds_raw, acc);
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int wm = wave >> 2, wn = wave & 3;
+  // Epilogue: every load of a 32 × 32 tile (the GELU factors, the accumulated outputs) is
+  // issued before the first store, at clamped addresses, so the tile waits once.
 #pragma unroll
   for (int i = 0; i < IA; ++i)
 #pragma unroll
     for (int j = 0; j < JB; ++j) {
       const int n = n0 + wn * (TN / 4) + j * 32 + (lane & 31);
+      const int nc = min(n, g.N - 1);
+      const int mb = m0 + wm * (TM / 2) + i * 32 + 4 * (lane >> 5);
+      float in[16];
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        const int m = m0 + wm * (TM / 2) + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+        in[r] = 0.f;
+        if constexpr (OUT == GB_GELU) {
+          const int mc = min(mb + 8 * (r >> 2) + (r & 3), g.M - 1);
+          const half_t x = static_cast<const half_t*>(g.aux)[static_cast<long long>(mc) * g.ldaux + nc];
+          in[r] = static_cast<float>(g_dgelu16_tab[__builtin_bit_cast(uint16_t, x)]);
+        } else if constexpr (OUT == GB_ADD) {
+          const int mc = min(mb + 8 * (r >> 2) + (r & 3), g.M - 1);
+          in[r] = static_cast<const float*>(g.c)[static_cast<long long>(mc) * g.ldc + nc];
+        }
+      }
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int m = mb + 8 * (r >> 2) + (r & 3);
         if (m < g.M && n < g.N) {
           const long long ci = z * zstride + static_cast<long long>(m) * g.ldc + n;
           const float v = acc[i][j][r];
           if constexpr (OUT == kGBPart) {
             static_cast<float*>(g.c)[ci] = v;
           } else if constexpr (OUT == GB_ADD) {
-            static_cast<float*>(g.c)[ci] += rnd<half_t>(v);
+            static_cast<float*>(g.c)[ci] = in[r] + rnd<half_t>(v);
           } else if constexpr (OUT == GB_SET) {
             static_cast<half_t*>(g.c)[ci] = static_cast<half_t>(v);
-          } else {
-            const half_t x = static_cast<const half_t*>(g.aux)[static_cast<long long>(m) * g.ldaux + n];
-            const float f = static_cast<float>(g_dgelu16_tab[__builtin_bit_cast(uint16_t, x)]);
-            static_cast<half_t*>(g.c)[ci] = static_cast<half_t>(rnd<half_t>(rnd<half_t>(v) * f));
+          } else {  // gelu_grad_f16(fp16(v), pre) = fp16(fp16(v) · factor(pre))
+            static_cast<half_t*>(g.c)[ci] = static_cast<half_t>(rnd<half_t>(rnd<half_t>(v) * in[r]));
           }
         }
       }
