@@ -222,7 +222,7 @@ int launch_convert(int src_dt, const void* src, int dst_dt, void* dst, size_t n,
 // buffers 16-byte aligned.
 int launch_adamw(float* p, const float* g, float* m, float* v, size_t n, float lr, float beta1,
                  float beta2, float bias1, float bias2, float eps, float weight_decay,
-                 hipStream_t st);
+                 hipStream_t st, void* p16 = nullptr);
 
 // Persistent decode step (batch 1): one launch of kPersistGroups workgroups runs the
 // whole token; see decode_persist.hip.

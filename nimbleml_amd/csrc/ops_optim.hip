@@ -32,9 +32,12 @@ struct AdamW {
 };
 
 // 16-byte vectors for the bulk (grid-stride), one element per lane for the tail.
+// H16: also writes fp16(p) to p16 (a float16 model's parameters from its float32 masters,
+// in the same pass instead of a separate conversion).
+template <bool H16>
 __global__ __launch_bounds__(256) void adamw_kernel(float* __restrict__ p, const float* __restrict__ g,
                                                    float* __restrict__ m, float* __restrict__ v,
-                                                   size_t n, AdamW op) {
+                                                   half_t* __restrict__ p16, size_t n, AdamW op) {
   const size_t nv = n / 4;
   const size_t stride = static_cast<size_t>(gridDim.x) * blockDim.x;
   const size_t first = static_cast<size_t>(blockIdx.x) * blockDim.x + threadIdx.x;
@@ -54,8 +57,16 @@ __global__ __launch_bounds__(256) void adamw_kernel(float* __restrict__ p, const
     reinterpret_cast<floatv4*>(p)[i] = pp;
     reinterpret_cast<floatv4*>(m)[i] = mm;
     reinterpret_cast<floatv4*>(v)[i] = vv;
+    if constexpr (H16) {
+      const half4 h = {static_cast<half_t>(pp[0]), static_cast<half_t>(pp[1]), static_cast<half_t>(pp[2]),
+                       static_cast<half_t>(pp[3])};
+      reinterpret_cast<half4*>(p16)[i] = h;
+    }
   }
-  for (size_t j = nv * 4 + first; j < n; j += stride) op(p[j], g[j], m[j], v[j]);
+  for (size_t j = nv * 4 + first; j < n; j += stride) {
+    op(p[j], g[j], m[j], v[j]);
+    if constexpr (H16) p16[j] = static_cast<half_t>(p[j]);
+  }
 }
 
 // A piece of one gradient tensor: the clip's passes run over a flat list of pieces so one
@@ -114,9 +125,10 @@ __global__ __launch_bounds__(256) void clip_apply_kernel(const Piece* __restrict
 
 int launch_adamw(float* p, const float* g, float* m, float* v, size_t n, float lr, float beta1,
                  float beta2, float bias1, float bias2, float eps, float weight_decay,
-                 hipStream_t st) {
+                 hipStream_t st, void* p16) {
 #pragma clang fp contract(off)
   if (n == 0) return 0;
+  NML_REQUIRE((reinterpret_cast<uintptr_t>(p16) & 7) == 0, "adamw: fp16 copy must be 8-byte aligned");
   NML_REQUIRE(((reinterpret_cast<uintptr_t>(p) | reinterpret_cast<uintptr_t>(g) |
                 reinterpret_cast<uintptr_t>(m) | reinterpret_cast<uintptr_t>(v)) & 15) == 0,
               "adamw: buffers must be 16-byte aligned");
@@ -127,7 +139,10 @@ int launch_adamw(float* p, const float* g, float* m, float* v, size_t n, float l
   const size_t nv = (n + 3) / 4;
   const size_t blocks = nv / 256 + 1;
   NML_REQUIRE(blocks <= 0x7fffffff, "adamw: %zu elements exceed one launch", n);
-  adamw_kernel<<<static_cast<int>(blocks), 256, 0, st>>>(p, g, m, v, n, op);
+  if (p16)
+    adamw_kernel<true><<<static_cast<int>(blocks), 256, 0, st>>>(p, g, m, v, static_cast<half_t*>(p16), n, op);
+  else
+    adamw_kernel<false><<<static_cast<int>(blocks), 256, 0, st>>>(p, g, m, v, nullptr, n, op);
   NML_LAUNCHED();
   return 0;
 }

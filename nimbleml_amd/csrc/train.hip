@@ -417,11 +417,10 @@ int nml_model_adamw_step(nml_model* m, float lr, float beta1, float beta2, float
   float* mm = static_cast<float*>(t->moments.p);
   for (const auto& r : ranges) {
     if (r[1] <= r[0]) continue;
+    // (fp16 models: the parameters rounded from the updated masters in the same pass)
     NML_TRY(launch_adamw(master + r[0], g + r[0], mm + r[0], mm + n_all + r[0], r[1] - r[0], lr,
-                         beta1, beta2, bias_corr1, bias_corr2, eps, weight_decay, st));
-    if (m->dt == F16)
-      NML_TRY(launch_convert(F32, master + r[0], F16, static_cast<char*>(m->arena) + r[0] * m->es,
-                             r[1] - r[0], st));
+                         beta1, beta2, bias_corr1, bias_corr2, eps, weight_decay, st,
+                         m->dt == F16 ? static_cast<char*>(m->arena) + r[0] * m->es : nullptr));
   }
   return 0;
 }
