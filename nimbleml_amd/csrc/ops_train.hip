@@ -893,6 +893,70 @@ __global__ __launch_bounds__(256) void ce_grad_kernel(T* __restrict__ lg, int V,
   }
 }
 
+// The same arithmetic with the row held in registers (one HBM read and one write per
+// element instead of three reads): thread t owns the 16-byte chunks t, t + 256, … of the
+// row (NCH of them at most); V a multiple of the chunk's element count. The partial sums
+// of Σexp run over a different element order than ce_grad_kernel's.
+template <typename T, int NCH>
+__global__ __launch_bounds__(256) void ce_grad_reg_kernel(T* __restrict__ lg, int V,
+                                                          const int64_t* __restrict__ labels,
+                                                          long long ignore_index, int has_ignore,
+                                                          float scale) {
+#pragma clang fp contract(off)
+  constexpr int E = 16 / static_cast<int>(sizeof(T));
+  typedef T vec_t __attribute__((ext_vector_type(E)));
+  __shared__ float red[4];
+  vec_t* p = reinterpret_cast<vec_t*>(lg + static_cast<long long>(blockIdx.x) * V);
+  const int nch = V / E, tid = threadIdx.x;
+  const long long label = labels[blockIdx.x];
+  if (has_ignore && label == ignore_index) {
+    vec_t z;
+#pragma unroll
+    for (int e = 0; e < E; ++e) z[e] = static_cast<T>(0.f);
+    for (int c = tid; c < nch; c += 256) p[c] = z;
+    return;
+  }
+  vec_t r[NCH];
+  float mx = -INFINITY;
+#pragma unroll
+  for (int k = 0; k < NCH; ++k) {
+    const int c = tid + 256 * k;
+    if (c < nch) {
+      r[k] = p[c];
+#pragma unroll
+      for (int e = 0; e < E; ++e) mx = fmaxf(mx, static_cast<float>(r[k][e]));
+    }
+  }
+  mx = wave_max(mx);
+  if ((tid & 63) == 0) red[tid >> 6] = mx;
+  __syncthreads();
+  mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+  float se = 0.f;
+#pragma unroll
+  for (int k = 0; k < NCH; ++k)
+    if (tid + 256 * k < nch) {
+#pragma unroll
+      for (int e = 0; e < E; ++e) se += rnd<T>(expf(rnd<T>(static_cast<float>(r[k][e]) - mx)));
+    }
+  se = block_sum(se, red);
+  const float inv = rnd<T>(1.0f / se);
+  const float sc = rnd<T>(scale);
+#pragma unroll
+  for (int k = 0; k < NCH; ++k) {
+    const int c = tid + 256 * k;
+    if (c < nch) {
+      vec_t o;
+#pragma unroll
+      for (int e = 0; e < E; ++e) {
+        float v = rnd<T>(rnd<T>(expf(rnd<T>(static_cast<float>(r[k][e]) - mx))) * inv);
+        if (c * E + e == label) v = rnd<T>(v - 1.0f);
+        o[e] = static_cast<T>(v * sc);
+      }
+      p[c] = o;
+    }
+  }
+}
+
 // ------------------------------------------------------------ attention backward
 // dvec[(b·H + h)·S + s] = Σ_c dout·o over the head's columns (= Σ_j P·dP of the
 // softmax backward, kernels/fused_sdpa.py:26-29).
@@ -1852,6 +1916,24 @@ int launch_colsum(int dt, const void* a, long long lda, int rows, int n, float* 
 int launch_ce_grad(int dt, void* logits, int rows, int V, const int64_t* labels,
                    long long ignore_index, int has_ignore, float scale, hipStream_t st) {
   if (rows == 0) return 0;
+  // rows in registers when the row is whole 16-byte chunks, ≤ 8192 of them, and aligned
+  const int E = dt == F16 ? 8 : 4;
+  const int nch = V / E, per = (nch + 255) / 256;
+  if (V % E == 0 && per <= 32 && (reinterpret_cast<uintptr_t>(logits) & 15) == 0) {
+    if (dt == F16) {
+      half_t* l = static_cast<half_t*>(logits);
+      if (per <= 4) ce_grad_reg_kernel<half_t, 4><<<rows, 256, 0, st>>>(l, V, labels, ignore_index, has_ignore, scale);
+      else if (per <= 16) ce_grad_reg_kernel<half_t, 16><<<rows, 256, 0, st>>>(l, V, labels, ignore_index, has_ignore, scale);
+      else ce_grad_reg_kernel<half_t, 32><<<rows, 256, 0, st>>>(l, V, labels, ignore_index, has_ignore, scale);
+    } else {
+      float* l = static_cast<float*>(logits);
+      if (per <= 4) ce_grad_reg_kernel<float, 4><<<rows, 256, 0, st>>>(l, V, labels, ignore_index, has_ignore, scale);
+      else if (per <= 16) ce_grad_reg_kernel<float, 16><<<rows, 256, 0, st>>>(l, V, labels, ignore_index, has_ignore, scale);
+      else ce_grad_reg_kernel<float, 32><<<rows, 256, 0, st>>>(l, V, labels, ignore_index, has_ignore, scale);
+    }
+    NML_LAUNCHED();
+    return 0;
+  }
   if (dt == F16)
     ce_grad_kernel<half_t><<<rows, 256, 0, st>>>(static_cast<half_t*>(logits), V, labels, ignore_index,
                                                  has_ignore, scale);

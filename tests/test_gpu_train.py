@@ -253,6 +253,47 @@ def test_backward_fp16_direct_to_lds_path_matches_register_path(gpu, monkeypatch
         assert err <= 2e-3 * np.abs(ref).max() + 1e-6, (k, err, np.abs(ref).max())
 
 
+@pytest.mark.parametrize("dt", ["fp32", "fp16"])
+def test_backward_large_vocab(gpu, dt):
+    """Vocabularies of 20000 (fp32) and 16384 (fp16): the cross-entropy backward holds each
+    logits row in registers (16-byte chunks, 20 and 8 per thread). fp32: every gradient
+    within RTOL of the float64 oracle; fp16: the token-embedding and W1 gradients within
+    1.5e-2 of the largest, with grad_scale 1024 so that the fp16 logits gradient
+    (≈ 1/(rows·V)) stays clear of fp16's subnormal range."""
+    from nimbleml_amd import _native as N
+    import nimbleml_amd as nm
+
+    if dt == "fp32":
+        cfg = GPTConfig(20000, 64, 2, 1, 32)
+        m, w = _model(cfg, seed=33)
+    else:
+        cfg = GPTConfig(16384, 64, 2, 1, 32)
+        w = {k: v.astype(np.float16) for k, v in make_weights(cfg, seed=33, rich=True).items()}
+        m = nm.GPT.from_arrays(w, cfg.vocab_size, cfg.d_model, cfg.num_heads, cfg.num_layers,
+                               cfg.max_seq_len, dtype=np.float16)
+    ids = random_ids((2, 16), cfg.vocab_size, seed=28)
+    labels = random_ids((32,), cfg.vocab_size, seed=29)
+    if dt == "fp32":
+        m.compute_loss(ids, labels).backward()
+        _, want = _oracle(w, cfg, ids, labels)
+        _compare(_named_grads(m), want)
+        return
+    h = m._device_model()
+    dids = N.DeviceArray.from_host(ids)
+    dlab = N.DeviceArray.from_host(labels)
+    loss = C.c_double()
+    N.check(N.lib.nml_model_zero_grad(h))
+    N.check(N.lib.nml_model_loss_train(h, dids.ptr, dlab.ptr, 2, 16, 0, 0, C.byref(loss)))
+    N.check(N.lib.nml_model_backward(h, 1024.0))
+    _, want = _oracle(w, cfg, ids, labels, grad_scale=1024.0)
+    got = {"token_emb.weights": m._grad_array(N.P_TOKEN_EMB, 0, (cfg.vocab_size, cfg.d_model)),
+           "blocks.layers.0.ffn.dense1.weights": m._grad_array(N.P_W1, 0, (cfg.d_ff, cfg.d_model)).T}
+    for k, g in got.items():
+        ref = want[k]
+        err = np.abs(g.astype(np.float64) - ref).max()
+        assert err <= 1.5e-2 * np.abs(ref).max(), (k, err, np.abs(ref).max())
+
+
 def test_model_adamw_step_fp16_masters(gpu):
     """fp16 models: AdamW runs on float32 masters taken from the parameters, and the
     parameters become the masters rounded to fp16 (optimizers/adam.py:75-81, :238-245), bit
