@@ -56,6 +56,9 @@ struct LinearArgs {
   const void* norm_g;
   float norm_eps;
   float* ssq_out;
+  // EPI_BIAS_GELU with more than 64 rows: also writes the pre-activation x·Wᵀ + b, (M, N),
+  // the value the GELU was taken of (the training forward keeps it). Null: not written.
+  void* pre_out;
 };
 
 // Whether launch_linear can fuse RMSNorm into this GEMM (ssq_in / ssq_out above).

@@ -39,6 +39,7 @@ __device__ __forceinline__ float epilogue_with(const LinearArgs& a, int m, int n
     } else if constexpr (EPI == EPI_BIAS_GELU) {
       const float v = rnd<T>(gelu_t<T>(lin));
       out[idx] = static_cast<T>(v);
+      if (a.pre_out) static_cast<T*>(a.pre_out)[idx] = static_cast<T>(lin);
       return v;
     } else if constexpr (EPI == EPI_BIAS_RESID) {
       const float v = rnd<T>(resid_v + lin);
@@ -848,6 +849,8 @@ int launch_linear(int dt, const LinearArgs& a, hipStream_t st) {
               "linear: bad QKV destination");
   NML_REQUIRE(!a.ssq_in || (a.norm_g != nullptr && linear_norm_fusable(dt, a.M, a.K, a.N)),
               "linear: fused RMSNorm needs a gain and the fp16 skinny shape");
+  NML_REQUIRE(!a.pre_out || (a.epi == EPI_BIAS_GELU && a.M > 64),
+              "linear: the pre-activation copy needs the GELU epilogue and more than 64 rows");
   NML_REQUIRE(!a.ssq_out || (a.epi == EPI_BIAS_RESID && linear_norm_fusable(dt, a.M, a.K, a.N)),
               "linear: sums of squares are written by an fp16 skinny residual GEMM only");
   return dt == F16 ? linear_epi<half_t>(a, st) : linear_epi<float>(a, st);

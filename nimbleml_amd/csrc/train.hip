@@ -258,8 +258,14 @@ int nml_model_loss_train(nml_model* m, const int64_t* ids, const int64_t* labels
     NML_TRY(launch_attention_prefill(dt, a, st));
     NML_TRY(launch_linear(dt, lin(att, d, w.wo, w.bo, xm, R, d, d, EPI_BIAS_RESID, x), st));
     NML_TRY(launch_rmsnorm(dt, xm, w.ln2, n2, nullptr, nullptr, R, d, kEps, st));
-    NML_TRY(launch_linear(dt, lin(n2, d, w.w1, w.b1, pre, R, F, d, EPI_BIAS), st));
-    NML_TRY(launch_gelu(dt, pre, hid, nullptr, (size_t)R * F, st));
+    if (R > 64) {  // GELU in the GEMM's epilogue, which also keeps the pre-activation
+      LinearArgs f1 = lin(n2, d, w.w1, w.b1, hid, R, F, d, EPI_BIAS_GELU);
+      f1.pre_out = pre;
+      NML_TRY(launch_linear(dt, f1, st));
+    } else {
+      NML_TRY(launch_linear(dt, lin(n2, d, w.w1, w.b1, pre, R, F, d, EPI_BIAS), st));
+      NML_TRY(launch_gelu(dt, pre, hid, nullptr, (size_t)R * F, st));
+    }
     NML_TRY(launch_linear(dt, lin(hid, F, w.w2, w.b2, xnext, R, d, F, EPI_BIAS_RESID, xm), st));
   }
   NML_TRY(launch_rmsnorm(dt, sv.xl, m->lnf, sv.hf, nullptr, nullptr, R, d, kEps, st));
