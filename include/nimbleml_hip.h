@@ -54,12 +54,12 @@ int nml_event_destroy(void* ev);
 
 /* RMSNorm forward; same arguments as rmsnorm_forward_device (module.cpp:259-270,
  * kernel sdpa_cuda.cu:135-165) plus dtype. ms/rms (float32, rows) may be NULL.
- * Semantics: kernels/fused_rmsnorm.py:360-369 (fp16 branch :360-365). */
+ * Semantics: kernels/fused_rmsnorm.py:153-162 (fp16 branch :153-158). */
 int nml_rmsnorm_forward_device(const void* x, const void* gamma, void* out, float* ms,
                                float* rms, size_t rows, size_t dim, float eps, int dtype);
 
 /* tanh-GELU forward; replaces gelu_forward (module.cpp:19-31, native/src/gelu.cpp:12-21)
- * and the fp16 NumPy branch (kernels/fused_gelu.py:114-116). tanh_u may be NULL. */
+ * and the fp16 NumPy branch (kernels/fused_gelu.py:67-69). tanh_u may be NULL. */
 int nml_gelu_forward_device(const void* x, void* out, float* tanh_u, size_t n, int dtype);
 
 /* x[b,s] = weights[ids[b,s]] + pos_weights[pos_offsets[b] + s] (pos_offsets NULL → 0).
@@ -79,11 +79,36 @@ int nml_linear_device(const void* x, size_t ld_x, const void* w_t, const void* b
                       const void* resid, void* out, size_t rows, size_t in_f, size_t out_f,
                       int epilogue, int dtype);
 
-/* Causal attention; same arguments as flash_sdpa_forward_device (module.cpp:231-242)
- * except that m/l are not produced and `scale` is the reference's divisor sqrt(dk)
- * (attention.py:135, fused_sdpa.py:71-78). q, k, v: (bh, seq, dk); out: (bh, seq, dk). */
-int nml_flash_sdpa_forward_device(const void* q, const void* k, const void* v, void* out,
-                                  size_t bh, size_t seq, size_t dk, float scale, int dtype);
+/* Causal flash attention in float32 with the reference's device-pointer arguments:
+ * flash_sdpa_forward_device (module.cpp:231-242 → flash_sdpa_forward_cuda,
+ * sdpa_cuda.cu:40-77, 235-243), as kernels/fused_sdpa.py:91-115 calls it. q, k, v, out:
+ * (bh, seq, dk); scores s_ij = (q_i·k_j)·scale for keys j ≤ i — `scale` multiplies (the
+ * caller passes 1/sqrt(dk)); m, l: (bh, seq), each query row's max score and
+ * Σ_j exp(s_ij − m). Head dims 8, 16, 32, 64, 128. */
+int nml_flash_sdpa_forward_device(const float* q, const float* k, const float* v, float* out,
+                                  float* m, float* l, size_t bh, size_t seq, size_t dk,
+                                  float scale);
+/* Its backward: flash_sdpa_backward_device (module.cpp:243-257 → flash_sdpa_backward_cuda,
+ * sdpa_cuda.cu:79-133, 245-256). grad_out, q, k, v, grad_q/k/v: (bh, seq, dk); m, l from the
+ * forward; grad_q, grad_k, grad_v are overwritten. */
+int nml_flash_sdpa_backward_device(const float* grad_out, const float* q, const float* k,
+                                   const float* v, const float* m, const float* l, float* grad_q,
+                                   float* grad_k, float* grad_v, size_t bh, size_t seq, size_t dk,
+                                   float scale);
+/* RMSNorm backward in float32: rmsnorm_backward_device (module.cpp:271-284 →
+ * rmsnorm_backward_cuda, sdpa_cuda.cu:167-201, 225-233). grad, x, grad_x: (rows, dim);
+ * grad_x and grad_gamma (dim) are overwritten. ms/rms (the forward's statistics) may be
+ * NULL: they are recomputed from x. */
+int nml_rmsnorm_backward_device(const float* grad, const float* x, const float* gamma,
+                                const float* ms, const float* rms, float* grad_x,
+                                float* grad_gamma, size_t rows, size_t dim, float eps);
+
+/* Causal attention in the compute dtype as the reference's CPU path computes it for GPT
+ * (kernels/fused_sdpa.py:71-78, reached from fused_sdpa_forward :256-289 with the causal
+ * mask): scores (q·k) / scale_div with scale_div = sqrt(dk) (attention.py:135), softmax,
+ * then P·v. q, k, v, out: (bh, seq, dk). */
+int nml_causal_attention_device(const void* q, const void* k, const void* v, void* out, size_t bh,
+                                size_t seq, size_t dk, float scale_div, int dtype);
 
 /* Mean tied-head cross-entropy (kernels/fused_tied_crossentropy.py:8-24 →
  * fused_crossentropy.py:14-30) without materialising all (rows, vocab) logits at once.
@@ -185,6 +210,13 @@ int nml_model_loss_train(nml_model* m, const int64_t* ids, const int64_t* labels
  * d(loss)/d(parameter) to every gradient (losses/cross_entropy.py:166-191, grad_scale =
  * output.grad). Returns after the device finishes. */
 int nml_model_backward(nml_model* m, double grad_scale);
+
+/* Which forward the saved activations belong to: a counter that every
+ * nml_model_loss_train advances (0: nothing saved). A caller holding the loss of an
+ * earlier nml_model_loss_train compares it before nml_model_backward, since backward
+ * always differentiates the latest saved forward (the reference keeps one graph per loss,
+ * utils/tensor.py:286-332; here the device keeps one). */
+int nml_model_saved_generation(nml_model* m, unsigned long long* generation);
 
 /* AdamW.step() over every parameter of the model (optimizers/adam.py:85-128 with the
  * native float32 update of adamw_step, native/src/adamw.cpp:6-20, in its operation order):

@@ -55,7 +55,10 @@ _SIGS = {
     "nml_gelu_forward_device": [vp, vp, vp, sz, i32],
     "nml_embedding_gather_device": [vp, vp, vp, vp, sz, sz, sz, sz, sz, vp, vp, i32],
     "nml_linear_device": [vp, sz, vp, vp, vp, vp, sz, sz, sz, i32, i32],
-    "nml_flash_sdpa_forward_device": [vp, vp, vp, vp, sz, sz, sz, f32, i32],
+    "nml_flash_sdpa_forward_device": [vp, vp, vp, vp, vp, vp, sz, sz, sz, f32],
+    "nml_flash_sdpa_backward_device": [vp, vp, vp, vp, vp, vp, vp, vp, vp, sz, sz, sz, f32],
+    "nml_rmsnorm_backward_device": [vp, vp, vp, vp, vp, vp, vp, sz, sz, f32],
+    "nml_causal_attention_device": [vp, vp, vp, vp, sz, sz, sz, f32, i32],
     "nml_tied_ce_forward_device": [vp, vp, vp, sz, sz, sz, i64, i32, C.POINTER(C.c_double), i32],
     "nml_sample_device": [vp, sz, sz, f32, i32, f32, f32, vp, vp, sz, vp, vp, i32],
     "nml_adamw_step_device": [vp, vp, vp, vp, sz, f32, f32, f32, f32, f32, f32, f32],
@@ -70,6 +73,7 @@ _SIGS = {
     "nml_model_grad_ptr": [vp, i32, i32, C.POINTER(C.c_void_p)],
     "nml_model_loss_train": [vp, vp, vp, sz, sz, i64, i32, C.POINTER(C.c_double)],
     "nml_model_backward": [vp, C.c_double],
+    "nml_model_saved_generation": [vp, C.POINTER(C.c_ulonglong)],
     "nml_model_adamw_step": [vp, f32, f32, f32, f32, f32, f32, f32],
     "nml_model_adam_moments": [vp, i32, i32, C.POINTER(C.c_void_p), C.POINTER(C.c_void_p)],
     "nml_cache_create": [vp, sz, C.POINTER(vp)],

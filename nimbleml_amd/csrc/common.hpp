@@ -122,7 +122,7 @@ __device__ __forceinline__ float block_sum(float v, float* red) {
 // GELU, tanh form: 0.5·x·(1 + tanh(√(2/π)·(x + 0.044715·x³))).
 // fp32: the operation order of the reference's native kernel
 // (native/src/gelu.cpp:15-19). fp16: the reference evaluates the same formula
-// as NumPy fp16 ufuncs (kernels/fused_gelu.py:114-116), Python constants taken
+// as NumPy fp16 ufuncs (kernels/fused_gelu.py:67-69), Python constants taken
 // as fp16, left to right, one rounding per op — reproduced op by op here.
 __device__ __forceinline__ float gelu_f32(float x) {
 #pragma clang fp contract(off)

@@ -294,7 +294,7 @@ __device__ __forceinline__ float block_max4(float v, float* red) {
   return fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
 }
 
-// RMSNorm of the D values in x (LDS) into y (LDS), kernels/fused_rmsnorm.py:360-369
+// RMSNorm of the D values in x (LDS) into y (LDS), kernels/fused_rmsnorm.py:153-162
 // (same arithmetic as rmsnorm_kernel). g_reg holds this thread's gamma entries.
 template <typename T, int D>
 __device__ __forceinline__ void rmsnorm_lds(const T* x, const float (&g_reg)[D / kT], T* y,

@@ -109,6 +109,10 @@ struct AttnArgs {
   // Training: per (sequence, head, query) log Σ exp(score − max) + max of the softmax,
   // (B, H, S) floats (float32 models only). Null: not written.
   float* lse;
+  // The same row's max score and Σ exp(score − max) separately, (B, H, S) floats (the
+  // m and l of the reference's flash kernel, sdpa_cuda.cu:40-77). Null: not written.
+  float* m_out;
+  float* l_out;
 };
 int launch_attention_prefill(int dt, const AttnArgs& a, hipStream_t st);
 

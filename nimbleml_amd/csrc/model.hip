@@ -24,6 +24,10 @@ struct nml_cache {
   void* v = nullptr;
   int32_t* len_dev = nullptr;  // B
   std::vector<int32_t> len;    // host mirror
+  // Single-token steps at batch 1 through the persistent kernel: the fed ids at their
+  // positions (P int64) and the kernel's error word. Allocated on first such step.
+  int64_t* tok = nullptr;
+  int* err = nullptr;
 };
 
 namespace nml {
@@ -430,6 +434,31 @@ int persist_prepare(nml_model* m, PersistArgs* pa, hipStream_t st) {
   return 0;
 }
 
+// Arguments of a persistent decode step over cache c (batch 1): feeds tokens[pos[0]]
+// at position pos[0], writes the logits; fuse_argmax also writes the greedy choice to
+// tokens[pos[0] + 1] and advances pos[0].
+int persist_args(nml_model* m, nml_cache* c, int64_t* tokens, int32_t* pos, void* logits, int* err,
+                 int fuse_argmax, PersistArgs* pa, hipStream_t st) {
+  NML_TRY(persist_prepare(m, pa, st));
+  pa->emb = m->emb;
+  pa->posw = m->pos;
+  pa->lnf = m->lnf;
+  pa->kc = c->k;
+  pa->vc = c->v;
+  pa->kv_layer = (long long)c->B * m->H * m->P * m->dk;
+  pa->kv_head = (long long)m->P * m->dk;
+  pa->tokens = tokens;
+  pa->pos = pos;
+  pa->logits = logits;
+  pa->err = err;
+  pa->V = m->V;
+  pa->L = m->L;
+  pa->P = m->P;
+  pa->fuse_argmax = fuse_argmax;
+  pa->scale = sqrtf((float)m->dk);
+  return 0;
+}
+
 __global__ void add_scalar_kernel(int32_t* p, int n, int v) {
   const int i = blockIdx.x * blockDim.x + threadIdx.x;
   if (i < n) p[i] += v;
@@ -666,6 +695,7 @@ int nml_cache_destroy(nml_cache* c) {
   if (c->k) (void)hipFree(c->k);
   if (c->v) (void)hipFree(c->v);
   if (c->len_dev) (void)hipFree(c->len_dev);
+  if (c->tok) (void)hipFree(c->tok);
   delete c;
   return 0;
 }
@@ -687,6 +717,32 @@ int nml_model_forward_cached(nml_model* m, nml_cache* c, const int64_t* ids, siz
   NML_REQUIRE((size_t)start + seq <= (size_t)m->P,
               "Sequence length %zu exceeds maximum sequence length %d", start + seq, m->P);
   hipStream_t st = nml::stream();
+  if (B == 1 && S == 1 && persist_wanted() && !rope_on(m) &&
+      persist_supported(m->dt, m->d, m->H, m->F, B, m->P)) {
+    // One token of one sequence: the persistent decode kernel (logits out, no choice).
+    if (!c->tok) {
+      void* p = nullptr;
+      NML_HIP(hipMalloc(&p, align256((size_t)m->P * 8) + 256));
+      c->tok = static_cast<int64_t*>(p);
+      c->err = reinterpret_cast<int*>(static_cast<char*>(p) + align256((size_t)m->P * 8));
+    }
+    NML_HIP(hipMemcpyAsync(c->tok + start, ids, sizeof(int64_t), hipMemcpyDeviceToDevice, st));
+    NML_HIP(hipMemsetAsync(c->err, 0, sizeof(int), st));
+    PersistArgs pa{};
+    NML_TRY(persist_args(m, c, c->tok, c->len_dev, logits, c->err, 0, &pa, st));
+    NML_TRY(launch_decode_persist(m->dt, m->d, m->H, pa, st));
+    add_scalar_kernel<<<1, 64, 0, st>>>(c->len_dev, 1, 1);
+    NML_LAUNCHED();
+    c->len[0] += 1;
+    int herr = 0;
+    NML_HIP(hipMemcpyAsync(&herr, c->err, sizeof(int), hipMemcpyDeviceToHost, st));
+    NML_HIP(hipStreamSynchronize(st));
+    m->last_decode_persistent = 1;
+    NML_REQUIRE((herr & 4) == 0, "persistent decode: a data exchange timed out");
+    NML_REQUIRE(herr == 0, "Token ID out of range [0, %d)", m->V);
+    return 0;
+  }
+  if (S == 1) m->last_decode_persistent = 0;
   Acts a;
   NML_TRY(acts_for(m, B * S, 0, &a));
   NML_TRY(launch_embed(m->dt, ids, m->emb, posw(m), c->len_dev, a.x, B, S, m->d, m->V, m->P,
@@ -845,25 +901,9 @@ int nml_model_generate(nml_model* m, const int64_t* prompts, size_t prompt_strid
   const bool persistent = persist_wanted() && !rope_on(m) &&
                           persist_supported(m->dt, m->d, m->H, m->F, B, m->P);
   PersistArgs pa{};
-  if (persistent) {
-    NML_TRY(persist_prepare(m, &pa, st));
-    pa.emb = m->emb;
-    pa.posw = m->pos;
-    pa.lnf = m->lnf;
-    pa.kc = c->k;
-    pa.vc = c->v;
-    pa.kv_layer = (long long)B * m->H * m->P * m->dk;
-    pa.kv_head = (long long)m->P * m->dk;
-    pa.tokens = tokens_out;
-    pa.pos = sm.pos;
-    pa.logits = logits;
-    pa.err = sm.err;
-    pa.V = m->V;
-    pa.L = m->L;
-    pa.P = m->P;
-    pa.fuse_argmax = (temperature <= 0.f && repetition_penalty == 1.0f) ? 1 : 0;
-    pa.scale = sqrtf((float)m->dk);
-  }
+  if (persistent)
+    NML_TRY(persist_args(m, c, tokens_out, sm.pos, logits, sm.err,
+                         (temperature <= 0.f && repetition_penalty == 1.0f) ? 1 : 0, &pa, st));
   // NIMBLEML_PERSIST_TRACE=<file>: phase timestamps of the last persistent step.
   const char* trace_path = persistent ? std::getenv("NIMBLEML_PERSIST_TRACE") : nullptr;
   const size_t trace_n = (size_t)kPersistGroups * persist_trace_stride(m->L);

@@ -1,5 +1,6 @@
 // Single-op entry points of the C-ABI (the `*_device` family). Each validates its
 // shapes on the host, then launches on the library stream.
+#include <cmath>
 #include <vector>
 
 #include "kernels.hpp"
@@ -30,6 +31,35 @@ Scratch g_scratch;
 
 int check_dtype(int dt) {
   NML_REQUIRE(dt == F32 || dt == F16, "dtype must be 0 (float32) or 1 (float16), got %d", dt);
+  return 0;
+}
+
+// lse = m + log(max(l, 1e-20)): the softmax statistics of the reference's flash kernel
+// (sdpa_cuda.cu:84-86) as the log-sum-exp the attention backward kernels take.
+__global__ void lse_from_ml_kernel(const float* __restrict__ m, const float* __restrict__ l,
+                                   float* __restrict__ lse, long long n) {
+  const long long i = static_cast<long long>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i < n) lse[i] = m[i] + logf(fmaxf(l[i], 1e-20f));
+}
+
+// Rows of [dq | dk | dv] (rows, 3·dk) → three (rows, dk) arrays.
+__global__ void split3_kernel(const float* __restrict__ src, float* __restrict__ a,
+                              float* __restrict__ b, float* __restrict__ c, long long rows,
+                              int dk) {
+  const long long i = static_cast<long long>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i >= rows * dk) return;
+  const long long r = i / dk, j = i % dk;
+  const float* s = src + r * 3 * dk;
+  a[i] = s[j];
+  b[i] = s[dk + j];
+  c[i] = s[2 * dk + j];
+}
+
+int attn_shape_ok(size_t bh, size_t seq, size_t dk) {
+  NML_REQUIRE(dk == 8 || dk == 16 || dk == 32 || dk == 64 || dk == 128,
+              "attention: head_dim %zu unsupported (8, 16, 32, 64, 128)", dk);
+  NML_REQUIRE(bh <= 65535 && bh * seq <= 0x7fffffff, "attention: %zu × %zu rows too many", bh,
+              seq);
   return 0;
 }
 
@@ -82,23 +112,113 @@ int nml_linear_device(const void* x, size_t ld_x, const void* w_t, const void* b
   return launch_linear(dtype, a, nml::stream());
 }
 
-int nml_flash_sdpa_forward_device(const void* q, const void* k, const void* v, void* out,
-                                  size_t bh, size_t seq, size_t dk, float scale, int dtype) {
+int nml_causal_attention_device(const void* q, const void* k, const void* v, void* out, size_t bh,
+                                size_t seq, size_t dk, float scale_div, int dtype) {
   NML_TRY(check_dtype(dtype));
+  NML_TRY(attn_shape_ok(bh, seq, dk));
   AttnArgs a{};
   a.q = q;
   a.k = k;
   a.v = v;
   a.out = out;
-  a.pos_base = nullptr;
   a.kv_stride_b = (long long)(seq * dk);
-  a.kv_stride_h = 0;
   a.B = (int)bh;
   a.H = 1;
   a.S = (int)seq;
   a.dk = (int)dk;
-  a.scale = scale;
+  a.scale = scale_div;
   return launch_attention_prefill(dtype, a, nml::stream());
+}
+
+int nml_flash_sdpa_forward_device(const float* q, const float* k, const float* v, float* out,
+                                  float* m, float* l, size_t bh, size_t seq, size_t dk,
+                                  float scale) {
+  NML_TRY(attn_shape_ok(bh, seq, dk));
+  NML_REQUIRE(scale > 0.f && std::isfinite(scale), "flash_sdpa_forward: scale must be positive");
+  NML_REQUIRE(m != nullptr && l != nullptr, "flash_sdpa_forward: m and l are required");
+  AttnArgs a{};
+  a.q = q;
+  a.k = k;
+  a.v = v;
+  a.out = out;
+  a.kv_stride_b = (long long)(seq * dk);
+  a.B = (int)bh;
+  a.H = 1;
+  a.S = (int)seq;
+  a.dk = (int)dk;
+  a.scale = 1.0f / scale;  // the kernels divide the scores; the reference multiplies
+  a.m_out = m;
+  a.l_out = l;
+  return launch_attention_prefill(F32, a, nml::stream());
+}
+
+int nml_flash_sdpa_backward_device(const float* grad_out, const float* q, const float* k,
+                                   const float* v, const float* m, const float* l, float* grad_q,
+                                   float* grad_k, float* grad_v, size_t bh, size_t seq, size_t dk,
+                                   float scale) {
+  NML_TRY(attn_shape_ok(bh, seq, dk));
+  NML_REQUIRE(scale > 0.f && std::isfinite(scale), "flash_sdpa_backward: scale must be positive");
+  const size_t rows = bh * seq;
+  if (rows == 0) return 0;
+  // scratch: the forward output (rows·dk), lse and the per-row dot (rows each), and the
+  // three gradients side by side (rows·3dk)
+  const size_t o_b = ((rows * dk * 4 + 255) / 256) * 256, r_b = ((rows * 4 + 255) / 256) * 256;
+  NML_TRY(g_scratch.ensure(o_b + 2 * r_b + 3 * o_b));
+  char* base = static_cast<char*>(g_scratch.p);
+  float* o = reinterpret_cast<float*>(base);
+  float* lse = reinterpret_cast<float*>(base + o_b);
+  float* dvec = reinterpret_cast<float*>(base + o_b + r_b);
+  float* dqkv = reinterpret_cast<float*>(base + o_b + 2 * r_b);
+  hipStream_t st = nml::stream();
+  AttnArgs fa{};
+  fa.q = q;
+  fa.k = k;
+  fa.v = v;
+  fa.out = o;
+  fa.kv_stride_b = (long long)(seq * dk);
+  fa.B = (int)bh;
+  fa.H = 1;
+  fa.S = (int)seq;
+  fa.dk = (int)dk;
+  fa.scale = 1.0f / scale;
+  NML_TRY(launch_attention_prefill(F32, fa, st));
+  lse_from_ml_kernel<<<(unsigned)((rows + 255) / 256), 256, 0, st>>>(m, l, lse, (long long)rows);
+  NML_LAUNCHED();
+  AttnBwdArgs ba{};
+  ba.q = q;
+  ba.k = k;
+  ba.v = v;
+  ba.o = o;
+  ba.dout = grad_out;
+  ba.lse = lse;
+  ba.dvec = dvec;
+  ba.dqkv = dqkv;
+  ba.B = (int)bh;
+  ba.H = 1;
+  ba.S = (int)seq;
+  ba.dk = (int)dk;
+  ba.scale = 1.0f / scale;
+  NML_TRY(launch_attention_backward(F32, ba, st));
+  split3_kernel<<<(unsigned)((rows * dk + 255) / 256), 256, 0, st>>>(dqkv, grad_q, grad_k, grad_v,
+                                                                   (long long)rows, (int)dk);
+  NML_LAUNCHED();
+  return 0;
+}
+
+int nml_rmsnorm_backward_device(const float* grad, const float* x, const float* gamma,
+                                const float* ms, const float* rms, float* grad_x,
+                                float* grad_gamma, size_t rows, size_t dim, float eps) {
+  (void)ms;
+  (void)rms;  // recomputed from x with the forward's own arithmetic
+  NML_REQUIRE(dim > 0 && dim <= 8192, "rmsnorm backward: dim %zu outside (0, 8192]", dim);
+  NML_REQUIRE(rows <= 0x7fffffff, "rmsnorm backward: too many rows");
+  hipStream_t st = nml::stream();
+  NML_HIP(hipMemsetAsync(grad_gamma, 0, dim * sizeof(float), st));
+  if (rows == 0) return 0;
+  const size_t parts = (size_t)rmsnorm_bwd_parts((int)rows) + 1;
+  NML_TRY(g_scratch.ensure(parts * dim * sizeof(float)));
+  return launch_rmsnorm_bwd(F32, grad, x, gamma, grad_x, 0, grad_gamma,
+                            static_cast<float*>(g_scratch.p), (int)rows, (int)dim, eps, st);
 }
 
 int nml_tied_ce_forward_device(const void* hidden, const void* weights, const int64_t* labels,

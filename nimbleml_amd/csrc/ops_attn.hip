@@ -110,6 +110,10 @@ __global__ __launch_bounds__(64) void attn_prefill_kernel(AttnArgs a) {
 #pragma unroll
     for (int d = 0; d < DK; ++d) out[d] = static_cast<T>(o[d] * inv);
     if (a.lse) a.lse[static_cast<size_t>(bh) * a.S + s] = m + logf(l);
+    if (a.m_out) {
+      a.m_out[static_cast<size_t>(bh) * a.S + s] = m;
+      a.l_out[static_cast<size_t>(bh) * a.S + s] = l;
+    }
   }
 }
 
@@ -591,6 +595,10 @@ __global__ __launch_bounds__(256, 2) void attn_prefill_mfma_kernel(AttnArgs a) {
   }
   l += __shfl_xor(l, 32, 64);
   if (myq < S && a.lse && hi == 0) a.lse[static_cast<size_t>(bh) * a.S + myq] = m + logf(l);
+  if (myq < S && a.m_out && hi == 0) {
+    a.m_out[static_cast<size_t>(bh) * a.S + myq] = m;
+    a.l_out[static_cast<size_t>(bh) * a.S + myq] = l;
+  }
   if (myq < S) {
     const float inv = 1.f / l;
     const int hd = a.H * DK;
@@ -737,6 +745,10 @@ __global__ __launch_bounds__(256) void attn_prefill_f32_mfma(AttnArgs a) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) out[32 * j + 8 * (r >> 2) + 4 * hi + (r & 3)] = o[j][r] * inv;
     if (a.lse && hi == 0) a.lse[static_cast<size_t>(bh) * a.S + s] = m + logf(l);
+    if (a.m_out && hi == 0) {
+      a.m_out[static_cast<size_t>(bh) * a.S + s] = m;
+      a.l_out[static_cast<size_t>(bh) * a.S + s] = l;
+    }
   }
 }
 

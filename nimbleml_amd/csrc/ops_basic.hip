@@ -94,7 +94,7 @@ __global__ __launch_bounds__(256) void rope_kernel(T* __restrict__ q, T* __restr
   rot(k + b * sb + h * sh + static_cast<long long>(p) * dk);
 }
 
-// RMSNorm (kernels/fused_rmsnorm.py:360-369).
+// RMSNorm (kernels/fused_rmsnorm.py:153-162).
 //   fp32: ms = mean(x²); rms = sqrt(ms + eps); y = (x / rms) · γ
 //   fp16: x² rounded to fp16, mean accumulated in fp32; inv = fp16(1 / rms);
 //         y = fp16(fp16(x · inv) · γ)

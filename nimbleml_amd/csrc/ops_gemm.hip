@@ -526,7 +526,7 @@ int gemv_dispatch_rpw(const LinearArgs& a, hipStream_t st) {
 // B[(l/16)·8 + 0..7][l%16]; the result D[(l/16)·4 + e][l%16], e < 4.
 //
 // NORM (decode RMSNorm fused into the GEMM that consumes it, kernels/fused_rmsnorm.py:
-// 360-369): the producer of x (an EPI_BIAS_RESID GEMM) also wrote the sums of
+// 153-162): the producer of x (an EPI_BIAS_RESID GEMM) also wrote the sums of
 // squares rnd(v·v) of its rounded outputs per 16-column piece (ssq_out); this kernel
 // sums a row's pieces in a fixed order, takes inv = rnd(1 / sqrt(mean + eps)) and
 // normalises each loaded x piece as rnd(rnd(x·inv)·g) with two fp16 multiplies — the

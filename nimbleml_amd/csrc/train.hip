@@ -36,6 +36,7 @@ struct TrainState {
   Buf io;       // ids and labels of the last loss_train, loss accumulators
   int B = 0, S = 0;
   bool saved = false;
+  unsigned long long generation = 0;  // advanced by every loss_train: which forward is saved
   long long ignore_index = 0;
   int has_ignore = 0;
   double n_valid = 0.0;
@@ -295,6 +296,7 @@ int nml_model_loss_train(nml_model* m, const int64_t* ids, const int64_t* labels
   t->has_ignore = has_ignore;
   t->n_valid = host[1];
   t->saved = true;
+  t->generation += 1;
   return 0;
 }
 
@@ -441,6 +443,12 @@ int nml_model_adam_moments(nml_model* m, int kind, int layer, void** first, void
   const size_t off = f32_off(m, *slot);
   *first = static_cast<char*>(m->train->moments.p) + off;
   *second = static_cast<char*>(m->train->moments.p) + f32_bytes(m) + off;
+  return 0;
+}
+
+int nml_model_saved_generation(nml_model* m, unsigned long long* generation) {
+  NML_REQUIRE(m != nullptr && generation != nullptr, "saved_generation: null argument");
+  *generation = (m->train && m->train->saved) ? m->train->generation : 0;
   return 0;
 }
 

@@ -255,17 +255,26 @@ class GPT(Module):
         out.data = np.asarray([loss.value], dtype=self._dtype)
         if train:
             dev = self._dev
+            gen = self._saved_generation()
 
             def _backward():
                 if self._dev is not dev:
                     raise RuntimeError("parameters were re-uploaded since this loss was "
                                        "computed; compute the loss again")
+                if self._saved_generation() != gen:
+                    raise RuntimeError("activations were overwritten by a later compute_loss; "
+                                       "compute this loss again before its backward()")
                 N.check(N.lib.nml_model_zero_grad(h))
                 N.check(N.lib.nml_model_backward(h, float(out.grad[0])))
                 self._pull_grads()
 
             out._backward = _backward
         return out
+
+    def _saved_generation(self) -> int:
+        g = C.c_ulonglong()
+        N.check(N.lib.nml_model_saved_generation(self._dev.handle, C.byref(g)))
+        return int(g.value)
 
     def _grad_array(self, kind, layer, shape):
         """Device gradient of parameter (kind, layer) as a host float32 array."""

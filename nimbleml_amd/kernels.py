@@ -71,9 +71,48 @@ def fused_sdpa_forward(q, k, v, scale, mask_arr=None, *, batch=None, num_heads=N
     qd, kd, vd = _dev(q, dt), _dev(k, dt), _dev(v, dt)
     bh, seq, dk = qd.shape
     out = N.DeviceArray((bh, seq, dk), dt)
-    N.check(N.lib.nml_flash_sdpa_forward_device(qd.ptr, kd.ptr, vd.ptr, out.ptr, bh, seq, dk,
-                                                float(scale), N.np_dtype_code(dt)))
+    N.check(N.lib.nml_causal_attention_device(qd.ptr, kd.ptr, vd.ptr, out.ptr, bh, seq, dk,
+                                              float(scale), N.np_dtype_code(dt)))
     return out, None
+
+
+def flash_sdpa_forward(q, k, v, scale):
+    """The reference's native flash path (kernels/fused_sdpa.py:91-115): float32 causal
+    attention over (bh, seq, dk) with ``scale`` the sqrt(dk) divisor, returning
+    ``(out, m, l)`` — m, l the per-row softmax max and sum from
+    ``flash_sdpa_forward_device`` called with the multiplier ``1/scale``."""
+    qd, kd, vd = _dev(q, np.float32), _dev(k, np.float32), _dev(v, np.float32)
+    bh, seq, dk = qd.shape
+    out = N.DeviceArray((bh, seq, dk), np.float32)
+    m = N.DeviceArray((bh, seq), np.float32)
+    lsum = N.DeviceArray((bh, seq), np.float32)
+    N.check(N.lib.nml_flash_sdpa_forward_device(qd.ptr, kd.ptr, vd.ptr, out.ptr, m.ptr, lsum.ptr,
+                                                bh, seq, dk, float(1.0 / scale)))
+    return out, m, lsum
+
+
+def flash_sdpa_backward(grad_out, q, k, v, m, lsum, scale):
+    """``flash_sdpa_backward_device`` (kernels/fused_sdpa.py:118-140): float32 gradients
+    (grad_q, grad_k, grad_v) of the causal flash forward, ``scale`` the sqrt(dk) divisor."""
+    arrs = [_dev(a, np.float32) for a in (grad_out, q, k, v, m, lsum)]
+    bh, seq, dk = arrs[1].shape
+    gq, gk, gv = (N.DeviceArray((bh, seq, dk), np.float32) for _ in range(3))
+    N.check(N.lib.nml_flash_sdpa_backward_device(*[a.ptr for a in arrs], gq.ptr, gk.ptr, gv.ptr,
+                                                 bh, seq, dk, float(1.0 / scale)))
+    return gq, gk, gv
+
+
+def fused_rmsnorm_backward(grad, x, gamma, epsilon=1e-5):
+    """``rmsnorm_backward_device`` (kernels/fused_rmsnorm.py:104-128 device branch, float32):
+    returns (grad_x, grad_gamma)."""
+    gd, xd, gmd = _dev(grad, np.float32), _dev(x, np.float32), _dev(gamma, np.float32)
+    d = xd.shape[-1]
+    rows = xd.size // d
+    gx = N.DeviceArray(xd.shape, np.float32)
+    gg = N.DeviceArray((d,), np.float32)
+    N.check(N.lib.nml_rmsnorm_backward_device(gd.ptr, xd.ptr, gmd.ptr, None, None, gx.ptr, gg.ptr,
+                                              rows, d, float(epsilon)))
+    return gx, gg
 
 
 def embedding_lookup(weights, ids, pos_weights=None):

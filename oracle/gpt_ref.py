@@ -13,12 +13,22 @@ from __future__ import annotations
 
 import numpy as np
 
+from oracle import halfmm
+
 GELU_K = 0.7978845608028654  # sqrt(2/pi), native/src/gelu.cpp:7
 GELU_COEF = 0.044715  # native/src/gelu.cpp:8
 RMS_EPS = 1e-5  # layers/rms_norm.py:16
 
 
 # --------------------------------------------------------------------------- ops
+def _mm(a, b):
+    """``a @ b`` with NumPy's semantics; float16 products go through the exact C
+    restatement of NumPy's float16 loop (oracle/halfmm.c), which is much faster."""
+    if a.dtype == np.float16 and b.dtype == np.float16:
+        return halfmm.matmul16(a, b)
+    return np.matmul(a, b)
+
+
 def embed(tok_w, pos_w, ids):
     """``token_emb(ids) + pos_emb.forward_prefix(S)``.
 
@@ -64,7 +74,7 @@ def apply_rope(x, cos, sin, offset=0):
 
 
 def rmsnorm(x, gamma, eps=RMS_EPS):
-    """kernels/fused_rmsnorm.py:360-369 (CPU branches: fp16 at :360-365, else :366-369)."""
+    """kernels/fused_rmsnorm.py:153-162 (CPU branches: fp16 at :153-158, else :159-162)."""
     if x.dtype == np.float16:
         ms = np.mean(x * x, axis=-1, keepdims=True, dtype=np.float32)
         rms = np.sqrt(ms + np.float32(eps))
@@ -77,7 +87,7 @@ def rmsnorm(x, gamma, eps=RMS_EPS):
 
 def gelu(x):
     """tanh-GELU. fp32: native gelu_forward_cpu (native/src/gelu.cpp:12-21, reached
-    via kernels/fused_gelu.py:107-111); other dtypes: NumPy at fused_gelu.py:114-116."""
+    via kernels/fused_gelu.py:61-64); other dtypes: NumPy at fused_gelu.py:67-69."""
     if x.dtype == np.float32:
         x3 = x * x * x
         tu = np.tanh(np.float32(GELU_K) * (x + np.float32(GELU_COEF) * x3))
@@ -101,12 +111,12 @@ def softmax(a, axis=-1):
 
 def sdpa(q, k, v, scale, mask):
     """kernels/fused_sdpa.py:71-78 (the CPU ``auto`` path, :284-288)."""
-    scores = np.matmul(q, np.swapaxes(k, -2, -1))
+    scores = _mm(q, np.swapaxes(k, -2, -1))
     np.divide(scores, scale, out=scores)
     if mask is not None:
         np.add(scores, mask, out=scores)
     probs = softmax(scores, axis=-1)
-    return np.matmul(probs, v)
+    return _mm(probs, v)
 
 
 def _split_heads(a, b, s, h, dk):
@@ -128,7 +138,7 @@ def mha(x, w, prefix, num_heads, mask, rope=None):
     x2d = x.reshape(b * s, d)
     w_qkv = np.concatenate([w[prefix + "W_q.weights"], w[prefix + "W_k.weights"],
                             w[prefix + "W_v.weights"]], axis=1)
-    qkv = x2d @ w_qkv
+    qkv = _mm(x2d, w_qkv)
     qkv = qkv + np.concatenate([w[prefix + "W_q.biases"], w[prefix + "W_k.biases"],
                                 w[prefix + "W_v.biases"]])
     q = _split_heads(qkv[:, :d].reshape(b, s, d), b, s, num_heads, dk)
@@ -139,7 +149,7 @@ def mha(x, w, prefix, num_heads, mask, rope=None):
         k = apply_rope(k, rope[0], rope[1])
     att = sdpa(q, k, v, scale, mask)
     merged = _merge_heads(att, b, s, num_heads, dk).reshape(b * s, d)
-    out = merged @ w[prefix + "W_o.weights"]
+    out = _mm(merged, w[prefix + "W_o.weights"])
     out = out + w[prefix + "W_o.biases"]
     return out.reshape(b, s, d)
 
@@ -148,10 +158,10 @@ def ffn(x, w, prefix):
     """neural_network/_fused_arrays.py:187-222."""
     shape = x.shape
     x2d = x.reshape(-1, shape[-1])
-    pre = x2d @ w[prefix + "dense1.weights"]
+    pre = _mm(x2d, w[prefix + "dense1.weights"])
     pre = pre + w[prefix + "dense1.biases"]
     hidden = gelu(pre)
-    out = hidden @ w[prefix + "dense2.weights"]
+    out = _mm(hidden, w[prefix + "dense2.weights"])
     out = out + w[prefix + "dense2.biases"]
     return out.reshape(shape)
 
@@ -182,7 +192,7 @@ def hidden_states(w, ids, num_heads, num_layers, rope=None):
 def tied_logits(h, emb):
     """models/gpt.py:139-153: ``h2d @ swapaxes(E)`` → (B, S, V)."""
     b, s, d = h.shape
-    return np.matmul(h.reshape(b * s, d), np.swapaxes(emb, -2, -1)).reshape(b, s, emb.shape[0])
+    return _mm(h.reshape(b * s, d), np.swapaxes(emb, -2, -1)).reshape(b, s, emb.shape[0])
 
 
 def forward(w, ids, num_heads, num_layers, rope=None):
@@ -222,7 +232,7 @@ def compute_loss(w, ids, labels, num_heads, num_layers, ignore_index=None, rope=
             return 0.0
         h2d, labels = h2d[valid], labels[valid]
     emb = w["token_emb.weights"]
-    logits = np.matmul(h2d, np.swapaxes(emb, -2, -1))
+    logits = _mm(h2d, np.swapaxes(emb, -2, -1))
     return crossentropy(logits, labels)
 
 
@@ -320,6 +330,17 @@ class KVOracle:
         self.k = [None] * num_layers  # (B*H, t, dk)
         self.v = [None] * num_layers
         self.t = 0
+        self._qkv = {}  # layer → (stacked W, stacked b); the same values every step
+
+    def _stacked(self, i):
+        if i not in self._qkv:
+            w, p = self.w, f"blocks.layers.{i}."
+            self._qkv[i] = (
+                np.concatenate([w[p + "mha.W_q.weights"], w[p + "mha.W_k.weights"],
+                                w[p + "mha.W_v.weights"]], axis=1),
+                np.concatenate([w[p + "mha.W_q.biases"], w[p + "mha.W_k.biases"],
+                                w[p + "mha.W_v.biases"]]))
+        return self._qkv[i]
 
     def step(self, ids):
         """Feed ``ids`` (B, s) at positions t..t+s-1; return logits (B, s, V)."""
@@ -337,10 +358,8 @@ class KVOracle:
         for i in range(self.n_layers):
             p = f"blocks.layers.{i}."
             n1 = rmsnorm(x.reshape(b * s, d), w[p + "ln1.gamma"])
-            w_qkv = np.concatenate([w[p + "mha.W_q.weights"], w[p + "mha.W_k.weights"],
-                                    w[p + "mha.W_v.weights"]], axis=1)
-            qkv = n1 @ w_qkv + np.concatenate([w[p + "mha.W_q.biases"], w[p + "mha.W_k.biases"],
-                                              w[p + "mha.W_v.biases"]])
+            w_qkv, b_qkv = self._stacked(i)
+            qkv = _mm(n1, w_qkv) + b_qkv
             q = _split_heads(qkv[:, :d], b, s, self.h, dk)
             k = _split_heads(qkv[:, d:2 * d], b, s, self.h, dk)
             v = _split_heads(qkv[:, 2 * d:], b, s, self.h, dk)
@@ -351,9 +370,121 @@ class KVOracle:
             self.v[i] = v if self.v[i] is None else np.concatenate([self.v[i], v], axis=1)
             att = sdpa(q, self.k[i], self.v[i], scale, mask)
             merged = _merge_heads(att, b, s, self.h, dk).reshape(b * s, d)
-            x = x + (merged @ w[p + "mha.W_o.weights"] + w[p + "mha.W_o.biases"]).reshape(b, s, d)
+            x = x + (_mm(merged, w[p + "mha.W_o.weights"]) + w[p + "mha.W_o.biases"]).reshape(b, s, d)
             n2 = rmsnorm(x.reshape(b * s, d), w[p + "ln2.gamma"]).reshape(b, s, d)
             x = x + ffn(n2, w, p + "ffn.")
         self.t = total
         h = rmsnorm(x.reshape(b * s, d), w["ln.gamma"]).reshape(b, s, d)
         return tied_logits(h, w["token_emb.weights"])
+
+
+class RaggedKVOracle:
+    """Rows of different lengths decoded in lockstep, one :class:`KVOracle` per row.
+
+    Each row is prefilled on its own, as the reference runs one sequence at a time. A
+    decode step then feeds one token per row and runs the row-independent ops (GEMMs,
+    RMSNorm, GELU, the tied head) on all rows at once; attention runs per row over its
+    own cache. NumPy computes every row of those ops as it would at batch 1, so each
+    row's logits equal its own batch-1 :class:`KVOracle` (pinned by a test)."""
+
+    def __init__(self, w, num_heads, num_layers):
+        self.w = w
+        self.h = num_heads
+        self.n_layers = num_layers
+        self.rows = []
+
+    def prefill(self, rows):
+        """``rows``: list of 1-D id arrays. Returns the last-position logits (B, V)."""
+        out = []
+        self.rows = []
+        for r in rows:
+            kv = KVOracle(self.w, self.h, self.n_layers)
+            out.append(kv.step(np.asarray(r, dtype=np.int64).reshape(1, -1))[0, -1])
+            self.rows.append(kv)
+        return np.stack(out)
+
+    def step(self, tokens):
+        """Feed one token per row (B,); return the logits (B, V)."""
+        w = self.w
+        tokens = np.asarray(tokens, dtype=np.int64).reshape(-1)
+        B = tokens.size
+        pos = np.asarray([kv.t for kv in self.rows])
+        x = w["token_emb.weights"][tokens] + w["pos_emb.weights"][pos]
+        d = x.shape[-1]
+        dk = d // self.h
+        scale = float(dk) ** 0.5
+        for i in range(self.n_layers):
+            p = f"blocks.layers.{i}."
+            n1 = rmsnorm(x, w[p + "ln1.gamma"])
+            w_qkv, b_qkv = self.rows[0]._stacked(i)
+            qkv = _mm(n1, w_qkv) + b_qkv
+            merged = np.empty_like(x)
+            for b, kv in enumerate(self.rows):
+                q = _split_heads(qkv[b:b + 1, :d], 1, 1, self.h, dk)
+                k = _split_heads(qkv[b:b + 1, d:2 * d], 1, 1, self.h, dk)
+                v = _split_heads(qkv[b:b + 1, 2 * d:], 1, 1, self.h, dk)
+                kv.k[i] = np.concatenate([kv.k[i], k], axis=1)
+                kv.v[i] = np.concatenate([kv.v[i], v], axis=1)
+                total = kv.t + 1
+                mask = np.triu(np.full((total, total), -np.inf, dtype=x.dtype), k=1)[kv.t:total]
+                att = sdpa(q, kv.k[i], kv.v[i], scale, mask)
+                merged[b] = _merge_heads(att, 1, 1, self.h, dk).reshape(d)
+            x = x + (_mm(merged, w[p + "mha.W_o.weights"]) + w[p + "mha.W_o.biases"])
+            n2 = rmsnorm(x, w[p + "ln2.gamma"])
+            x = x + ffn(n2, w, p + "ffn.")
+        for kv in self.rows:
+            kv.t += 1
+        h = rmsnorm(x, w["ln.gamma"])
+        return tied_logits(h.reshape(B, 1, d), w["token_emb.weights"])[:, 0]
+
+
+# ------------------------------------------------------------ decision robustness
+def sample_flip_tol(logits, u, token, *, temperature, top_k):
+    """Largest ε such that changing every logit by at most ε provably cannot change
+    ``token``, the pick of ``sample_logits(logits, temperature, top_k, top_p=1, u)`` (no
+    repetition penalty). Conservative: tokens within 2ε/T of the top-k threshold may leave or join
+    the kept set (their probability mass then shifts the CDF), and a CDF value c moves by
+    at most c(1 − c)(e^{2ε/T} − 1) when every logit/T moves by at most ε/T; the pick must
+    stay strictly inside its CDF interval under both. Greedy (temperature ≤ 0): half the top-2 gap."""
+    x = np.asarray(logits, dtype=np.float32).reshape(-1).astype(np.float64)
+    if temperature <= 0:
+        top2 = np.sort(x)[-2:]
+        return float(top2[1] - top2[0]) / 2.0
+    xt = np.asarray(logits, dtype=np.float32).reshape(-1) / np.float32(temperature)
+    k = min(top_k, xt.size) if top_k and top_k > 0 else xt.size
+    th = float(np.partition(xt, -k)[-k])
+    keep = xt >= th
+    p = np.exp((xt - xt[keep].max()).astype(np.float64)) * keep
+    p /= p.sum()
+    cdf = np.cumsum(p)
+    j = int(token)
+    lo = cdf[j - 1] if j > 0 else 0.0
+    hi = cdf[j]
+    if not (lo <= u < hi):
+        return 0.0
+    xt64 = xt.astype(np.float64)
+
+    def robust(eps):
+        e = 2.0 * eps / float(temperature)
+        amb = np.abs(xt64 - th) <= e
+        if k < xt.size and amb[j]:
+            return False
+        mass = p[amb].sum() * np.exp(e) if k < xt.size else 0.0
+
+        def shift(c):  # |Δc| for a CDF value c when every logit/T moves by ≤ e/2
+            return c * (1.0 - c) * (np.exp(e) - 1.0) + mass
+
+        return (u - lo) > shift(lo) and (hi - u) > shift(hi)
+
+    if not robust(0.0):
+        return 0.0
+    a, b = 0.0, 1.0
+    if robust(b):
+        return b
+    for _ in range(40):
+        mid = 0.5 * (a + b)
+        if robust(mid):
+            a = mid
+        else:
+            b = mid
+    return a

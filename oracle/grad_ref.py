@@ -196,3 +196,45 @@ def loss_and_grads(w, ids, labels, num_heads, num_layers, ignore_index=None, rop
     if rope is None:
         grads["pos_emb.weights"][:s] += g.reshape(b, s, d).sum(axis=0)
     return loss, grads
+
+
+# ------------------------------------------------ single ops of the native extension
+def flash_forward(q, k, v, scale):
+    """The reference's native flash attention forward (native/src/sdpa_cuda.cu:40-77) in the
+    dtype of ``q``: causal over (bh, seq, dk), scores ``(q_i·k_j)·scale`` (``scale``
+    multiplies), returning ``out`` and each query row's max score ``m`` and
+    ``l = Σ_j exp(s_ij − m)``."""
+    s = np.matmul(q, np.swapaxes(k, -2, -1)) * scale
+    seq = q.shape[-2]
+    s = np.where(np.tril(np.ones((seq, seq), dtype=bool)), s, -np.inf)
+    m = s.max(axis=-1)
+    e = np.exp(s - m[..., None])
+    lsum = e.sum(axis=-1)
+    return np.matmul(e, v) / lsum[..., None], m, lsum
+
+
+def flash_backward(grad_out, q, k, v, scale):
+    """Its backward (sdpa_cuda.cu:79-133): P = softmax of the causal scores,
+    dV = Pᵀ·dO, dP = dO·Vᵀ, D_i = Σ_j P_ij dP_ij, dS = P∘(dP − D), dQ = dS·K·scale,
+    dK = dSᵀ·Q·scale."""
+    out, m, lsum = flash_forward(q, k, v, scale)
+    s = np.matmul(q, np.swapaxes(k, -2, -1)) * scale
+    seq = q.shape[-2]
+    s = np.where(np.tril(np.ones((seq, seq), dtype=bool)), s, -np.inf)
+    p = np.exp(s - m[..., None]) / lsum[..., None]
+    dv = np.matmul(np.swapaxes(p, -2, -1), grad_out)
+    dp = np.matmul(grad_out, np.swapaxes(v, -2, -1))
+    dvec = (p * dp).sum(axis=-1, keepdims=True)
+    ds = p * (dp - dvec)
+    return np.matmul(ds, k) * scale, np.matmul(np.swapaxes(ds, -2, -1), q) * scale, dv
+
+
+def rmsnorm_backward(grad, x, gamma, eps=RMS_EPS):
+    """RMSNorm backward of the native extension (sdpa_cuda.cu:167-201; the fp32 CPU branch
+    kernels/fused_rmsnorm.py:208-217 is the same mathematics): ``(grad_x, grad_gamma)``."""
+    x2 = x.reshape(-1, x.shape[-1])
+    g2 = grad.reshape(-1, x.shape[-1])
+    ms = np.mean(x2 * x2, axis=-1, keepdims=True)
+    rms = np.sqrt(ms + eps)
+    gx, gg = _rms_bwd(g2, x2, gamma, ms, rms, eps)
+    return gx.reshape(x.shape), gg

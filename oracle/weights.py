@@ -107,6 +107,22 @@ def make_weights(cfg: GPTConfig, seed: int = 0, dtype=np.float32, rich: bool = F
     return out
 
 
+def c4_rows(vocab: int, seed: int = 5, batch: int = 32):
+    """The C4 prompts: lengths uniform in [128, 1024], ids
+    uniform in [0, vocab), from one seeded generator."""
+    rng = np.random.default_rng(seed)
+    lens = rng.integers(128, 1025, batch)
+    return [rng.integers(0, vocab, int(n)).astype(np.int64) for n in lens]
+
+
+def row_uniforms(steps: int, batch: int, seed0: int = 1000) -> np.ndarray:
+    """u[t, b]: the t-th draw of ``RandomState(seed0 + b)``, which is what the reference
+    consumes when it generates row b alone after ``np.random.seed(seed0 + b)``
+    (models/generate.py:57,59: one draw per row per step)."""
+    return np.stack([np.random.RandomState(seed0 + b).random_sample(steps)
+                     for b in range(batch)], axis=1)
+
+
 def random_ids(shape, vocab: int, seed: int) -> np.ndarray:
     """Uniform token ids in [0, vocab) as int64."""
     return np.random.default_rng([seed, 7919]).integers(0, vocab, size=shape, dtype=np.int64)

@@ -1,0 +1,203 @@
+"""GPU parity at the benchmark-sized configs.
+
+The expected values come from the oracle at full size (tests/golden/make_configs.py):
+the reference's float16 path restated op by op, with float16 products computed by a
+bit-exact restatement of NumPy's float16 matmul. Bars:
+fp16 logits within 3e-2, loss within 1e-4 relative, token ids identical wherever the
+reference decision is farther than the logit tolerance from flipping (greedy: top-2
+gap; sampling: the largest logit change that cannot move the draw across a CDF
+boundary or the top-k threshold, tests/golden/make_configs.py). Where a decision is
+closer than that, the two runs may part ways; the comparison of that row ends there.
+
+  C3  d1024 / L24 / V32000, batch 1, prompt 512: 64 greedy tokens from generate() (one
+      persistent kernel launch per token), and the same kernel's logits at every step
+      teacher-forced through forward_with_cache.
+  C4  the same model, 32 prompts of lengths U[128, 1024], 256 sampled tokens each
+      (T 0.8, top-k 50) through the batched decode step.
+  C5  d2048 / H16 (head dim 128) / V50304 widths: a 2-layer slice at S 4096 against the
+      oracle (loss, logits), and the full 24-layer 4 × 4096 model through properties
+      that hold at any size (the training loss equals the inference loss; the loss of
+      the batch equals the mean of its sequences' losses).
+"""
+import ctypes
+
+import numpy as np
+import pytest
+
+from conftest import golden
+from oracle.weights import C3, C5, GPTConfig, c4_rows, make_weights, random_ids, row_uniforms
+
+pytestmark = pytest.mark.gpu
+
+TOL16 = 3e-2
+
+
+def _build(cfg, w):
+    import nimbleml_amd as nm
+
+    return nm.GPT.from_arrays(w, cfg.vocab_size, cfg.d_model, cfg.num_heads, cfg.num_layers,
+                              cfg.max_seq_len, dtype=np.float16)
+
+
+@pytest.fixture(scope="module")
+def c3_model(gpu):
+    f = golden("c3_fp16")
+    assert tuple(int(x) for x in f["config"][:5]) == (C3.vocab_size, C3.d_model, C3.num_heads,
+                                                       C3.num_layers, C3.max_seq_len)
+    w = make_weights(C3, seed=int(f["seed"]), dtype=np.float16)
+    m = _build(C3, w)
+    del w
+    return f, m
+
+
+def _c3_prompt(f):
+    return random_ids((1, int(f["prompt_len"])), C3.vocab_size, int(f["prompt_seed"]))
+
+
+def test_c3_full_depth_persistent_greedy(c3_model):
+    import nimbleml_amd as nm
+
+    f, m = c3_model
+    prompt = _c3_prompt(f)
+    ref, margins = f["greedy"], f["margins"]
+    n = ref.size
+    out = nm.generate(m, prompt, max_new_tokens=n, temperature=0.0)
+    assert m.last_decode_persistent()
+    s0 = prompt.shape[1]
+    agreed = decidable = 0
+    for t in range(n):
+        if out[0, s0 + t] != ref[t]:
+            assert margins[t] <= TOL16, f"step {t}: token {out[0, s0 + t]} != {ref[t]}, margin {margins[t]}"
+            break
+        agreed += 1
+        decidable += int(margins[t] > TOL16)
+    print(f"C3 greedy: {agreed}/{n} tokens equal, {decidable} of them decidable")
+    assert decidable >= 40, (agreed, decidable)
+
+
+@pytest.mark.parametrize("persistent", [True, False])
+def test_c3_full_depth_logits_teacher_forced(c3_model, monkeypatch, persistent):
+    """Feed the oracle's own tokens one at a time: every step's logits from the decode
+    kernel (persistent, or the multi-kernel step) against the oracle's."""
+    f, m = c3_model
+    if not persistent:
+        monkeypatch.setenv("NIMBLEML_PERSISTENT", "0")
+    prompt = _c3_prompt(f)
+    ref, margins = f["greedy"], f["margins"]
+    keep = set(int(k) for k in f["keep_steps"])
+    lg, cache = m.forward_with_cache(prompt)
+    cur = lg.numpy()[0, -1].astype(np.float64)
+    worst = 0.0
+    decided = 0
+    for t in range(ref.size):
+        if t in keep:
+            dev = float(np.abs(cur - f[f"logits_step{t}"].astype(np.float64)).max())
+            worst = max(worst, dev)
+            assert dev <= TOL16, (t, dev)
+        if margins[t] > TOL16:
+            assert int(np.argmax(cur)) == ref[t], f"step {t}"
+            decided += 1
+        if t + 1 < ref.size:
+            lg, cache = m.forward_with_cache(np.asarray([[ref[t]]]), cache)
+            assert m.last_decode_persistent() == persistent
+            cur = lg.numpy()[0, -1].astype(np.float64)
+    print(f"C3 teacher-forced ({'persistent' if persistent else 'multi-kernel'}): "
+          f"max |dlogit| {worst:.3e} at the kept steps, {decided}/{ref.size} argmax decided")
+    assert decided >= 48
+
+
+def test_c4_full_config_sampled(c3_model):
+    """32 ragged prompts, 256 sampled tokens each, against the oracle's per-row runs."""
+    from nimbleml_amd.generate import _generate_device
+
+    _, m = c3_model
+    f = golden("c4_fp16")
+    assert int(f["seed"]) == int(golden("c3_fp16")["seed"])  # the same model
+    rows = c4_rows(C3.vocab_size)
+    ref, flip = f["tokens"], f["flip_tol"]
+    new, batch = ref.shape
+    u = row_uniforms(new, batch)
+    # deviation of our logits from the oracle's (prefill of the first rows)
+    dev = 0.0
+    for b in range(f["prefill_logits"].shape[0]):
+        lg = m.forward_last(rows[b][None]).numpy()[0].astype(np.float64)
+        dev = max(dev, float(np.abs(lg - f["prefill_logits"][b].astype(np.float64)).max()))
+    tol = 1e-2
+    assert dev <= tol / 2, dev
+    plen = np.asarray([len(r) for r in rows], dtype=np.int32)
+    toks = _generate_device(m, rows, plen, new, float(f["temperature"]), int(f["top_k"]), 1.0,
+                            1.0, u, True)
+    compared = ended = 0
+    for b in range(batch):
+        s0 = plen[b]
+        assert np.array_equal(toks[b, :s0], rows[b])
+        for t in range(new):
+            if toks[b, s0 + t] != ref[t, b]:
+                assert flip[t, b] <= tol, f"row {b} step {t}: {toks[b, s0 + t]} != {ref[t, b]}"
+                ended += 1
+                break
+            compared += int(flip[t, b] > tol)
+    print(f"C4: prefill max |dlogit| {dev:.2e}; {compared} decidable tokens equal, "
+          f"{ended} rows parted at an undecidable step")
+    assert compared >= 1000, compared
+
+
+C5SLICE = GPTConfig(50304, 2048, 16, 2, 4096)
+
+
+def _raw_loss(m, ids, labels):
+    from nimbleml_amd import _native as N
+
+    b, s = ids.shape
+    raw = ctypes.c_double()
+    dids = N.DeviceArray.from_host(ids)
+    dlab = N.DeviceArray.from_host(labels.reshape(-1))
+    N.check(N.lib.nml_model_loss(m._device_model(), dids.ptr, dlab.ptr, b, s, 0, 0,
+                                 ctypes.byref(raw)))
+    return raw.value
+
+
+def test_c5_slice_loss_and_logits(gpu):
+    f = golden("c5slice_fp16")
+    cfg = C5SLICE
+    w = make_weights(cfg, seed=int(f["seed"]), dtype=np.float16, rich=True)
+    m = _build(cfg, w)
+    del w
+    s = cfg.max_seq_len
+    ids = random_ids((1, s), cfg.vocab_size, int(f["ids_seed"]))
+    labels = random_ids((1, s), cfg.vocab_size, int(f["ids_seed"]) + 1)
+    raw = _raw_loss(m, ids, labels)
+    want = float(f["loss"])
+    print(f"C5 slice: loss {raw:.7f} vs oracle {want:.7f} (rel {abs(raw - want) / want:.2e})")
+    assert abs(raw - want) <= 1e-4 * abs(want)
+    api = m.compute_loss(ids, labels).item()
+    assert api == float(np.float16(raw))
+    lg = m.forward(ids).numpy()[0]
+    for p in f["keep_pos"]:
+        dev = float(np.abs(lg[int(p)].astype(np.float64) - f[f"logits_pos{int(p)}"]).max())
+        assert dev <= TOL16, (int(p), dev)
+
+
+def test_c5_full_size_properties(gpu):
+    """d2048 / L24 / V50304, 4 × 4096: properties that need no oracle at this size."""
+    from nimbleml_amd import _native as N
+
+    cfg = C5
+    w = make_weights(cfg, seed=43, dtype=np.float16)
+    m = _build(cfg, w)
+    del w
+    ids = random_ids((4, 4096), cfg.vocab_size, 51)
+    labels = random_ids((4, 4096), cfg.vocab_size, 52)
+    full = _raw_loss(m, ids, labels)
+    per_seq = [_raw_loss(m, ids[b:b + 1], labels[b:b + 1]) for b in range(4)]
+    assert np.isfinite(full) and abs(full - np.log(cfg.vocab_size)) < 1.0
+    # The batch's loss is the mean over its rows: the mean of the four sequences' losses
+    # (rows are independent; only the float64 summation order differs).
+    assert abs(full - np.mean(per_seq)) <= 1e-6 * full, (full, per_seq)
+    raw = ctypes.c_double()
+    dids = N.DeviceArray.from_host(ids)
+    dlab = N.DeviceArray.from_host(labels.reshape(-1))
+    N.check(N.lib.nml_model_loss_train(m._device_model(), dids.ptr, dlab.ptr, 4, 4096, 0, 0,
+                                       ctypes.byref(raw)))
+    print(f"C5 full: loss {full:.7f}, per sequence {per_seq}, training forward {raw.value:.7f}")
+    assert abs(raw.value - full) <= 1e-5 * full

@@ -95,7 +95,20 @@ def test_tiny_greedy_generate(gpu, name):
         assert out.shape == f["greedy"].shape
         assert_tokens_agree(out, f["greedy"], s0, margins, tol_for(dt))
     out = nm.generate(m, f["prompt"], max_new_tokens=n, temperature=0.0, repetition_penalty=1.5)
-    assert np.array_equal(out[:, :s0 + 4], f["greedy_reppen"][:, :s0 + 4])
+    ref = f["greedy_reppen"]
+    compared = 0
+    for b in range(ref.shape[0]):
+        for t in range(n):
+            prefix = ref[b:b + 1, :s0 + t]
+            lg = R.forward(w, prefix, cfg.num_heads, cfg.num_layers)[0, -1]
+            pen = R.apply_repetition_penalty(lg.astype(np.float32), list(prefix[0]), 1.5)
+            if out[b, s0 + t] != ref[b, s0 + t]:
+                # only where the penalised decision is within tolerance of a tie
+                assert greedy_margin(pen) <= tol_for(dt), f"row {b} step {t}"
+                break
+            compared += int(greedy_margin(pen) > tol_for(dt))
+    print(f"{name}: repetition-penalty greedy, {compared} decidable tokens equal")
+    assert compared >= (ref.shape[0] * n // 2 if dt == np.float32 else 4), compared
 
 
 @pytest.mark.parametrize("name", TINY)
@@ -119,7 +132,7 @@ def test_tiny_loss(gpu, name):
         lab = N.DeviceArray.from_host(f["loss_labels"].reshape(-1))
         N.check(N.lib.nml_model_loss(m._device_model(), ids.ptr, lab.ptr, 2, 32, 0, 0,
                                      ctypes.byref(raw)))
-        assert abs(raw.value - unrounded) <= 1e-3 * abs(unrounded)
+        assert abs(raw.value - unrounded) <= 1e-4 * abs(unrounded)
     else:
         assert abs(got - ref) <= 1e-4 * abs(ref)
     gi = m.compute_loss(f["loss_ids"], f["loss_ignore_labels"], ignore_index=-100).item()
@@ -153,7 +166,7 @@ def test_tiny_sampled_generate(gpu, name, mode):
     out = nm.generate(m, f["prompt"], max_new_tokens=ref.shape[1] - s0, **kw)
     u = f[mode + "_u"]
     live = np.ones(ref.shape[0], dtype=bool)  # rows still compared
-    compared = 0
+    compared = undecided = 0
     for t in range(ref.shape[1] - s0):
         prefix = ref[:, :s0 + t]
         want = R.forward(w, prefix, cfg.num_heads, cfg.num_layers)[:, -1].astype(np.float64)
@@ -164,15 +177,20 @@ def test_tiny_sampled_generate(gpu, name, mode):
             # KV-cache decode and full forward differ in summation order: allow 2x.
             eff = 2.0 * float(dev[b]) + 1e-6
             if _u_near_boundary(want[b], u[t, b], ref[b, :s0 + t], kw, eff):
-                live[b] = False  # a logit change of the observed size could flip this draw
+                # a logit change of the observed size could flip this draw: the runs may
+                # part here; while they agree the row stays comparable
+                if out[b, s0 + t] != ref[b, s0 + t]:
+                    live[b] = False
+                undecided += 1
                 continue
             assert out[b, s0 + t] == ref[b, s0 + t], f"row {b} step {t}"
             compared += 1
         if not live.any():
             break
-    # fp32: every row is decidable for several steps. fp16: the tiny model's logits
-    # sit a few fp16 ulps apart, so a row may be undecidable from its first step.
-    assert compared >= (ref.shape[0] if dt == np.float32 else 0), compared
+    print(f"{name} {mode}: {compared} decidable tokens equal, {undecided} undecidable steps")
+    # fp32: every row is decidable for several steps. fp16: the tiny model's logits sit a
+    # few fp16 ulps apart, so fewer draws are decidable (measured 1-26 of 48).
+    assert compared >= (2 * ref.shape[0] if dt == np.float32 else 1), compared
 
 
 def _u_near_boundary(logits, u, hist, kw, tol):
@@ -309,5 +327,18 @@ def test_c3slice_fp16_steps(gpu):
         assert np.abs(got - ref).max() <= 3e-2, t
         if t + 1 < n:
             lg, cache = m.forward_with_cache(f["greedy"][:, s0 + t:s0 + t + 1], cache)
-    loss = m.compute_loss(f["loss_ids"], f["loss_labels"]).item()
-    assert abs(loss - float(f["loss"])) <= 2 ** -7 * abs(float(f["loss"]))
+    # The fixture holds the reference's loss rounded to fp16 (its loss Tensor); the raw
+    # float64 loss must round to it, up to 1e-4 relative at a rounding boundary.
+    import ctypes
+
+    from nimbleml_amd import _native as N
+
+    raw = ctypes.c_double()
+    ids = N.DeviceArray.from_host(f["loss_ids"])
+    lab = N.DeviceArray.from_host(f["loss_labels"].reshape(-1))
+    N.check(N.lib.nml_model_loss(m._device_model(), ids.ptr, lab.ptr, f["loss_ids"].shape[0],
+                                 f["loss_ids"].shape[1], 0, 0, ctypes.byref(raw)))
+    ref = float(f["loss"])
+    half_ulp = float(np.spacing(np.float16(ref))) / 2
+    assert abs(raw.value - ref) <= half_ulp + 1e-4 * abs(ref), (raw.value, ref)
+    assert m.compute_loss(f["loss_ids"], f["loss_labels"]).item() == float(np.float16(raw.value))

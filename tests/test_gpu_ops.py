@@ -319,3 +319,55 @@ def test_sdpa_mfma_long_fp16(gpu, dk):
     want = R.sdpa(q.astype(np.float64), k.astype(np.float64), v.astype(np.float64),
                   float(dk) ** 0.5, R.causal_mask(s, np.float64))
     assert np.abs(out - want).max() < 6e-3
+
+
+@pytest.mark.parametrize("dk", [16, 64, 128])
+@pytest.mark.parametrize("seq", [1, 37, 200])
+def test_flash_sdpa_forward_device_reference_arguments(gpu, dk, seq):
+    """flash_sdpa_forward_device with the reference's arguments (module.cpp:231-242):
+    `scale` = 1/sqrt(dk) multiplies the scores; out, m and l against the float64
+    restatement of sdpa_cuda.cu:40-77."""
+    from oracle import grad_ref as G
+
+    rng = np.random.default_rng(dk + seq)
+    q, k, v = (rng.standard_normal((3, seq, dk)).astype(np.float32) for _ in range(3))
+    out, m, lsum = _k().flash_sdpa_forward(q, k, v, np.sqrt(dk))
+    want, wm, wl = G.flash_forward(q.astype(np.float64), k.astype(np.float64),
+                                   v.astype(np.float64), 1.0 / np.sqrt(dk))
+    assert np.abs(np.asarray(out) - want).max() < 1e-5
+    assert np.abs(np.asarray(m) - wm).max() < 1e-5 * max(1.0, np.abs(wm).max())
+    assert (np.abs(np.asarray(lsum) - wl) / wl).max() < 1e-5
+
+
+@pytest.mark.parametrize("dk", [16, 64, 128])
+def test_flash_sdpa_backward_device(gpu, dk):
+    """flash_sdpa_backward_device (module.cpp:243-257): gradients against the float64
+    restatement of sdpa_cuda.cu:79-133, with the forward's m and l."""
+    from oracle import grad_ref as G
+
+    rng = np.random.default_rng(dk)
+    seq = 150
+    q, k, v, go = (rng.standard_normal((2, seq, dk)).astype(np.float32) for _ in range(4))
+    _, m, lsum = _k().flash_sdpa_forward(q, k, v, np.sqrt(dk))
+    grads = _k().flash_sdpa_backward(go, q, k, v, m, lsum, np.sqrt(dk))
+    want = G.flash_backward(*(a.astype(np.float64) for a in (go, q, k, v)), 1.0 / np.sqrt(dk))
+    for got, w in zip(grads, want):
+        assert np.abs(np.asarray(got) - w).max() <= 2e-5 * np.abs(w).max()
+
+
+@pytest.mark.parametrize("rows,dim", [(1, 64), (37, 96), (300, 1024)])
+def test_rmsnorm_backward_device(gpu, rows, dim):
+    """rmsnorm_backward_device (module.cpp:271-284): grad_x and grad_gamma (overwritten)
+    against the float64 restatement."""
+    from oracle import grad_ref as G
+
+    rng = np.random.default_rng(rows)
+    x = rng.standard_normal((rows, dim)).astype(np.float32)
+    g = (1.0 + 0.1 * rng.standard_normal(dim)).astype(np.float32)
+    go = rng.standard_normal((rows, dim)).astype(np.float32)
+    gx, gg = _k().fused_rmsnorm_backward(go, x, g)
+    wx, wg = G.rmsnorm_backward(go.astype(np.float64), x.astype(np.float64), g.astype(np.float64))
+    assert np.abs(np.asarray(gx) - wx).max() <= 1e-5 * np.abs(wx).max()
+    assert np.abs(np.asarray(gg) - wg).max() <= 1e-5 * np.abs(wg).max()
+    gx2, gg2 = _k().fused_rmsnorm_backward(go, x, g)  # grad_gamma overwritten, not added
+    assert np.array_equal(np.asarray(gg2), np.asarray(gg))

@@ -475,3 +475,32 @@ def test_no_grad_loss_equals_training_loss(gpu, dtype):
     trained = m.compute_loss(ids, labels)
     assert trained.requires_grad
     assert plain.item() == trained.item()
+
+
+def test_interleaved_losses_and_inference_before_backward(gpu):
+    """Two losses before one backward: the device keeps one saved forward, so the older
+    loss refuses its backward (instead of returning the later batch's gradients); the
+    latest one back-propagates correctly. Inference between a loss and its backward
+    (forward, no_grad loss, generate) leaves the saved forward intact."""
+    import nimbleml_amd as nm
+
+    cfg = GPTConfig(256, 64, 4, 2, 64)
+    m, w = _model(cfg, seed=31)
+    ids_a = random_ids((2, 20), cfg.vocab_size, seed=1)
+    ids_b = random_ids((2, 20), cfg.vocab_size, seed=2)
+    lab_a = random_ids((40,), cfg.vocab_size, seed=3)
+    lab_b = random_ids((40,), cfg.vocab_size, seed=4)
+    loss_a = m.compute_loss(ids_a, lab_a)
+    loss_b = m.compute_loss(ids_b, lab_b)
+    with pytest.raises(RuntimeError, match="overwritten by a later compute_loss"):
+        loss_a.backward()
+    # inference in between does not disturb loss_b's saved forward
+    m.forward(ids_a)
+    with nm.no_grad():
+        m.compute_loss(ids_a, lab_a)
+    nm.generate(m, ids_a, max_new_tokens=3, temperature=0.0)
+    for p in m.parameters():
+        p.zero_grad()
+    loss_b.backward()
+    _, want = _oracle(w, cfg, ids_b, lab_b)
+    _compare(_named_grads(m), want)
