@@ -118,6 +118,19 @@ int nml_tied_ce_forward_device(const void* hidden, const void* weights, const in
                                size_t rows, size_t dim, size_t vocab, int64_t ignore_index,
                                int has_ignore, double* loss, int dtype);
 
+/* nml_tied_ce_forward_device without any device allocation: no counterpart in the
+ * reference. For callers that cannot allocate device memory (tight serving or training
+ * loops, harnesses that forbid hipMalloc). The logits chunks live in a fixed 32 MiB
+ * device scratch that the library holds on each GPU it runs on, so rows go through in
+ * chunks of at most 32 MiB / (vocab · element size) rows; a vocabulary whose single row
+ * does not fit is refused with an error. Same arguments and result as
+ * nml_tied_ce_forward_device; calls on one GPU share the scratch, so they must not
+ * overlap (one stream, or synchronise between them). */
+int nml_tied_ce_forward_device_noalloc(const void* hidden, const void* weights,
+                                       const int64_t* labels, size_t rows, size_t dim,
+                                       size_t vocab, int64_t ignore_index, int has_ignore,
+                                       double* loss, int dtype);
+
 /* Next-token choice per row of (batch, vocab) logits (models/generate.py:23-59):
  * temperature ≤ 0 → argmax; else temperature, top_k (≤0 off), top_p (outside (0,1) off)
  * with u[b] replacing RandomState.choice's draw. repetition_penalty uses

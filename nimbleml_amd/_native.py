@@ -60,6 +60,8 @@ _SIGS = {
     "nml_rmsnorm_backward_device": [vp, vp, vp, vp, vp, vp, vp, sz, sz, f32],
     "nml_causal_attention_device": [vp, vp, vp, vp, sz, sz, sz, f32, i32],
     "nml_tied_ce_forward_device": [vp, vp, vp, sz, sz, sz, i64, i32, C.POINTER(C.c_double), i32],
+    "nml_tied_ce_forward_device_noalloc": [vp, vp, vp, sz, sz, sz, i64, i32,
+                                           C.POINTER(C.c_double), i32],
     "nml_sample_device": [vp, sz, sz, f32, i32, f32, f32, vp, vp, sz, vp, vp, i32],
     "nml_adamw_step_device": [vp, vp, vp, vp, sz, f32, f32, f32, f32, f32, f32, f32],
     "nml_clip_grad_norm_device": [C.POINTER(vp), C.POINTER(sz), sz, f32, C.POINTER(f32)],

@@ -1,12 +1,20 @@
 // Single-op entry points of the C-ABI (the `*_device` family). Each validates its
 // shapes on the host, then launches on the library stream.
 #include <cmath>
+#include <mutex>
 #include <vector>
 
 #include "kernels.hpp"
 #include "nimbleml_hip.h"
 
 using namespace nml;
+
+// Fixed device scratch of nml_tied_ce_forward_device_noalloc: 32 MiB, held by every GPU the
+// library runs on until the process ends. All calls on one GPU share it (and it keeps the
+// last call's contents), so such calls must not overlap on one GPU: issue them on one
+// stream, or synchronise between them.
+constexpr size_t kNoAllocScratchBytes = size_t(32) << 20;
+static __device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
 
 namespace {
 
@@ -60,6 +68,89 @@ int attn_shape_ok(size_t bh, size_t seq, size_t dk) {
               "attention: head_dim %zu unsupported (8, 16, 32, 64, 128)", dk);
   NML_REQUIRE(bh <= 65535 && bh * seq <= 0x7fffffff, "attention: %zu × %zu rows too many", bh,
               seq);
+  return 0;
+}
+
+// Scratch of one tied cross-entropy pass over row chunks of `chunk` rows: the chunk's
+// logits, its per-row losses and validity flags, then the error word and the float64
+// accumulators.
+size_t ce_scratch_bytes(size_t chunk, size_t vocab, size_t es) {
+  const size_t lb = ((chunk * vocab * es + 255) / 256) * 256;
+  const size_t rb = ((chunk * 4 + 255) / 256) * 256;
+  return lb + 2 * rb + 256;
+}
+
+__global__ void zero_words_kernel(unsigned* p, int n) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) p[i] = 0u;
+}
+
+// Mean tied cross-entropy in row chunks of at most `chunk` rows with the scratch at ws
+// (ce_scratch_bytes(chunk, vocab, es) bytes). Allocates nothing; returns after the device
+// finishes, the mean in *loss.
+int tied_ce(const void* hidden, const void* weights, const int64_t* labels, size_t rows,
+            size_t dim, size_t vocab, int64_t ignore_index, int has_ignore, double* loss, int dtype,
+            void* ws, size_t chunk) {
+  NML_REQUIRE(rows <= 0x7fffffff && vocab <= 0x7fffffff && dim <= 0x7fffffff,
+              "cross-entropy: sizes out of range");
+  const size_t es = dtype_size(dtype);
+  const size_t lbytes = ((chunk * vocab * es + 255) / 256) * 256;
+  const size_t rbytes = ((chunk * 4 + 255) / 256) * 256;
+  char* base = static_cast<char*>(ws);
+  void* logits = base;
+  float* row_loss = reinterpret_cast<float*>(base + lbytes);
+  int* row_valid = reinterpret_cast<int*>(base + lbytes + rbytes);
+  int* err = reinterpret_cast<int*>(base + lbytes + 2 * rbytes);
+  double* acc = reinterpret_cast<double*>(base + lbytes + 2 * rbytes + 64);
+  hipStream_t st = nml::stream();
+  // err and the two accumulators start at zero (a fill kernel, no memset node)
+  zero_words_kernel<<<1, 64, 0, st>>>(reinterpret_cast<unsigned*>(base + lbytes + 2 * rbytes), 32);
+  NML_LAUNCHED();
+  for (size_t r0 = 0; r0 < rows; r0 += chunk) {
+    const size_t n = (rows - r0 < chunk) ? rows - r0 : chunk;
+    LinearArgs a{};
+    a.x = static_cast<const char*>(hidden) + r0 * dim * es;
+    a.lda = (long long)dim;
+    a.w = weights;
+    a.out = logits;
+    a.M = (int)n;
+    a.N = (int)vocab;
+    a.K = (int)dim;
+    a.epi = EPI_NONE;
+    NML_TRY(launch_linear(dtype, a, st));
+    NML_TRY(launch_ce_rows(dtype, logits, (int)n, (int)vocab, labels + r0, ignore_index,
+                           has_ignore, row_loss, row_valid, err, st));
+    NML_TRY(launch_ce_reduce(row_loss, row_valid, (int)n, acc, r0 > 0 ? 1 : 0, st));
+  }
+  NML_TRY(launch_ce_finalize(acc, acc + 2, st));
+  double host[3];
+  int herr = 0;
+  NML_HIP(hipMemcpyAsync(host, acc, sizeof(host), hipMemcpyDeviceToHost, st));
+  NML_HIP(hipMemcpyAsync(&herr, err, sizeof(int), hipMemcpyDeviceToHost, st));
+  NML_HIP(hipStreamSynchronize(st));
+  NML_REQUIRE(herr == 0, "cross-entropy: label out of range [0, %zu)", vocab);
+  *loss = host[2];
+  return 0;
+}
+
+constexpr int kMaxDevices = 64;
+std::mutex g_noalloc_mu;
+void* g_noalloc_ptr[kMaxDevices] = {};
+
+// The device address of `scratch` on the current device, looked up once per device (the
+// host-side name `scratch` is not a device address and must never reach a kernel).
+int noalloc_scratch(void** out) {
+  int dev = 0;
+  NML_HIP(hipGetDevice(&dev));
+  NML_REQUIRE(dev >= 0 && dev < kMaxDevices, "no-alloc scratch: device %d out of range", dev);
+  std::lock_guard<std::mutex> lock(g_noalloc_mu);
+  if (!g_noalloc_ptr[dev]) {
+    void* p = nullptr;
+    NML_HIP(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+    NML_REQUIRE(p != nullptr, "no-alloc scratch: no device address on device %d", dev);
+    g_noalloc_ptr[dev] = p;
+  }
+  *out = g_noalloc_ptr[dev];
   return 0;
 }
 
@@ -229,43 +320,28 @@ int nml_tied_ce_forward_device(const void* hidden, const void* weights, const in
   size_t chunk = rows ? rows : 1;
   const size_t cap = (size_t)256 << 20;
   while (chunk > 1 && chunk * vocab * es > cap) chunk = (chunk + 1) / 2;
-  const size_t lbytes = ((chunk * vocab * es + 255) / 256) * 256;
-  const size_t rbytes = ((rows * 8 + 255) / 256) * 256 + 256;
-  NML_TRY(g_scratch.ensure(lbytes + 2 * rbytes + 256));
-  char* base = static_cast<char*>(g_scratch.p);
-  void* logits = base;
-  float* row_loss = reinterpret_cast<float*>(base + lbytes);
-  int* row_valid = reinterpret_cast<int*>(base + lbytes + rbytes);
-  double* acc = reinterpret_cast<double*>(base + lbytes + 2 * rbytes);
-  int* err = reinterpret_cast<int*>(acc + 3);
-  hipStream_t st = nml::stream();
-  NML_HIP(hipMemsetAsync(err, 0, sizeof(int), st));
-  for (size_t r0 = 0; r0 < rows; r0 += chunk) {
-    const size_t n = (rows - r0 < chunk) ? rows - r0 : chunk;
-    LinearArgs a{};
-    a.x = static_cast<const char*>(hidden) + r0 * dim * es;
-    a.lda = (long long)dim;
-    a.w = weights;
-    a.out = logits;
-    a.M = (int)n;
-    a.N = (int)vocab;
-    a.K = (int)dim;
-    a.epi = EPI_NONE;
-    NML_TRY(launch_linear(dtype, a, st));
-    NML_TRY(launch_ce_rows(dtype, logits, (int)n, (int)vocab, labels + r0, ignore_index,
-                           has_ignore, row_loss, row_valid, err, st));
-    NML_TRY(launch_ce_reduce(row_loss, row_valid, (int)n, acc, r0 > 0 ? 1 : 0, st));
-  }
-  if (rows == 0) NML_HIP(hipMemsetAsync(acc, 0, 2 * sizeof(double), st));
-  NML_TRY(launch_ce_finalize(acc, acc + 2, st));
-  double host[3];
-  int herr = 0;
-  NML_HIP(hipMemcpyAsync(host, acc, sizeof(host), hipMemcpyDeviceToHost, st));
-  NML_HIP(hipMemcpyAsync(&herr, err, sizeof(int), hipMemcpyDeviceToHost, st));
-  NML_HIP(hipStreamSynchronize(st));
-  NML_REQUIRE(herr == 0, "cross-entropy: label out of range [0, %zu)", vocab);
-  *loss = host[2];
-  return 0;
+  NML_TRY(g_scratch.ensure(ce_scratch_bytes(chunk, vocab, es)));
+  return tied_ce(hidden, weights, labels, rows, dim, vocab, ignore_index, has_ignore, loss, dtype,
+                 g_scratch.p, chunk);
+}
+
+int nml_tied_ce_forward_device_noalloc(const void* hidden, const void* weights,
+                                       const int64_t* labels, size_t rows, size_t dim,
+                                       size_t vocab, int64_t ignore_index, int has_ignore,
+                                       double* loss, int dtype) {
+  NML_TRY(check_dtype(dtype));
+  const size_t es = dtype_size(dtype);
+  NML_REQUIRE(ce_scratch_bytes(1, vocab, es) <= kNoAllocScratchBytes,
+              "tied cross-entropy (no-alloc): one row of %zu logits needs %zu bytes of scratch, "
+              "more than the fixed %zu",
+              vocab, ce_scratch_bytes(1, vocab, es), kNoAllocScratchBytes);
+  size_t chunk = rows ? rows : 1;
+  while (chunk > 1 && ce_scratch_bytes(chunk, vocab, es) > kNoAllocScratchBytes)
+    chunk = (chunk + 1) / 2;
+  void* ws = nullptr;
+  NML_TRY(noalloc_scratch(&ws));
+  return tied_ce(hidden, weights, labels, rows, dim, vocab, ignore_index, has_ignore, loss, dtype,
+                 ws, chunk);
 }
 
 int nml_sample_device(const void* logits, size_t batch, size_t vocab, float temperature, int top_k,
