@@ -110,6 +110,15 @@ int nml_rmsnorm_backward_device(const float* grad, const float* x, const float* 
 int nml_causal_attention_device(const void* q, const void* k, const void* v, void* out, size_t bh,
                                 size_t seq, size_t dk, float scale_div, int dtype);
 
+/* fused_sdpa_forward for any mask (kernels/fused_sdpa.py:256-289 → _matmul_sdpa_forward
+ * :71-78): causal != 0 is the causal case above (mask must be NULL); causal == 0 attends
+ * every query to all seq keys, adding mask[i·seq + j] (an additive (seq, seq) matrix in
+ * the compute dtype, e.g. 0 / −inf) to each scaled score when mask is non-NULL, and to
+ * nothing when it is NULL (the reference's mask_arr=None). */
+int nml_sdpa_forward_device(const void* q, const void* k, const void* v, const void* mask,
+                            void* out, size_t bh, size_t seq, size_t dk, float scale_div,
+                            int causal, int dtype);
+
 /* Mean tied-head cross-entropy (kernels/fused_tied_crossentropy.py:8-24 →
  * fused_crossentropy.py:14-30) without materialising all (rows, vocab) logits at once.
  * has_ignore: drop rows with label == ignore_index (losses/_ce_prepare.py:46-69).
@@ -195,6 +204,26 @@ int nml_model_param_ptr(nml_model* m, int kind, int layer, void** ptr);
  * for the last position. ids: device int64 (batch, seq). */
 int nml_model_forward(nml_model* m, const int64_t* ids, size_t batch, size_t seq, void* logits,
                       int last_only);
+
+/* The model's blocks over an already-embedded input: FusedTransformerBlock.forward
+ * (neural_network/transformer_fused.py:44-95 → fused_block_forward_arrays,
+ * _fused_arrays.py:251-284) for each layer in order, then, when final_norm != 0, the
+ * final RMSNorm — FusedGPTTrunk.forward (transformer_fused.py:103-144 →
+ * fused_trunk_forward_arrays). x, out: device (batch, seq, d_model) in the compute dtype
+ * (they may be the same buffer); positions start at 0 (RoPE when its tables are set).
+ * causal != 0 masks causally (the modules' mask=None); causal == 0 attends to every key,
+ * adding mask (an additive (seq, seq) matrix, or NULL for none) to the scaled scores.
+ * The token and position tables are not used. */
+int nml_model_blocks_forward(nml_model* m, const void* x, void* out, size_t batch, size_t seq,
+                             int final_norm, int causal, const void* mask);
+
+/* MultiHeadAttention.forward (neural_network/attention.py:139-168) with layer `layer`'s
+ * projections: out = merge(softmax(q·kᵀ / sqrt(dk) [+ mask]) · v) · W_o + b_o with
+ * q, k, v = x·W_{q,k,v} + b. No rotary embedding (the module applies none). causal and
+ * mask as for nml_model_blocks_forward; the module's own mask=None is causal == 0 with
+ * a NULL mask. x, out: device (batch, seq, d_model), distinct buffers. */
+int nml_model_mha_forward(nml_model* m, int layer, const void* x, void* out, size_t batch,
+                          size_t seq, int causal, const void* mask);
 
 /* GPT.compute_loss (models/gpt.py:123-137): mean tied-head CE over batch·seq rows,
  * labels device int64. Returns after the device finishes; *loss is float64. */

@@ -59,6 +59,7 @@ _SIGS = {
     "nml_flash_sdpa_backward_device": [vp, vp, vp, vp, vp, vp, vp, vp, vp, sz, sz, sz, f32],
     "nml_rmsnorm_backward_device": [vp, vp, vp, vp, vp, vp, vp, sz, sz, f32],
     "nml_causal_attention_device": [vp, vp, vp, vp, sz, sz, sz, f32, i32],
+    "nml_sdpa_forward_device": [vp, vp, vp, vp, vp, sz, sz, sz, f32, i32, i32],
     "nml_tied_ce_forward_device": [vp, vp, vp, sz, sz, sz, i64, i32, C.POINTER(C.c_double), i32],
     "nml_tied_ce_forward_device_noalloc": [vp, vp, vp, sz, sz, sz, i64, i32,
                                            C.POINTER(C.c_double), i32],
@@ -70,6 +71,8 @@ _SIGS = {
     "nml_model_set_param": [vp, i32, i32, vp, sz],
     "nml_model_param_ptr": [vp, i32, i32, C.POINTER(vp)],
     "nml_model_forward": [vp, vp, sz, sz, vp, i32],
+    "nml_model_blocks_forward": [vp, vp, vp, sz, sz, i32, i32, vp],
+    "nml_model_mha_forward": [vp, i32, vp, vp, sz, sz, i32, vp],
     "nml_model_loss": [vp, vp, vp, sz, sz, i64, i32, C.POINTER(C.c_double)],
     "nml_model_zero_grad": [vp],
     "nml_model_grad_ptr": [vp, i32, i32, C.POINTER(C.c_void_p)],

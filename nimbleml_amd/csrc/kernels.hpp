@@ -113,6 +113,12 @@ struct AttnArgs {
   // m and l of the reference's flash kernel, sdpa_cuda.cu:40-77). Null: not written.
   float* m_out;
   float* l_out;
+  // Non-causal attention (full != 0): every query sees all S keys, with mask[s·S + key]
+  // (an additive (S, S) matrix in the compute dtype) added to each scaled score when
+  // mask is non-null — the dense path of kernels/fused_sdpa.py:71-78. Dense rows only
+  // (no pos_base, no ragged rows). Zero: causal.
+  int full;
+  const void* mask;
 };
 int launch_attention_prefill(int dt, const AttnArgs& a, hipStream_t st);
 

@@ -159,63 +159,85 @@ struct Ragged {
   int R;
 };
 
+// How a forward masks its attention: causal (the GPT path), or every key of a dense
+// sequence plus an optional additive (S, S) mask (full != 0).
+struct AttnMode {
+  int full = 0;
+  const void* mask = nullptr;
+};
+
+// One attention sublayer over R rows of xin: [q | k | v] = xin·W_qkvᵀ + b (q head-major
+// into acts.q, k and v through c), RoPE when `rope`, attention into acts.att, then
+// out = acts.att·W_oᵀ + b_o (+ resid when non-null; out may equal resid).
+int attention_sublayer(nml_model* m, const Layer& w, const void* xin, const Acts& a, int B, int S,
+                       const int32_t* pos_base, const KVView& c, bool rope, const AttnMode& am,
+                       const void* resid, void* out, hipStream_t st, const Ragged* rg) {
+  const int R = rg ? rg->R : B * S, d = m->d;
+  LinearArgs qkv{};
+  qkv.x = xin;
+  qkv.lda = d;
+  qkv.w = w.wqkv;
+  qkv.bias = w.bqkv;
+  qkv.M = R;
+  qkv.N = 3 * d;
+  qkv.K = d;
+  qkv.epi = EPI_QKV;
+  qkv.qkv = QKVDst{a.q, c.k, c.v, pos_base, c.sb, c.sh, S, m->H, m->dk, d,
+                   rg ? rg->row_seg : nullptr};
+  NML_TRY(launch_linear(m->dt, qkv, st));
+  if (rope)  // models/gpt.py:62-64 → _fused_arrays.py:95-98
+    NML_TRY(launch_rope(m->dt, a.q, c.k, c.sb, c.sh, B, m->H, S, m->dk, pos_base,
+                        rg ? rg->seq_len : nullptr, m->rope_cos, m->rope_sin, m->P, st));
+  AttnArgs at{};
+  at.q = a.q;
+  at.k = c.k;
+  at.v = c.v;
+  at.out = a.att;
+  at.pos_base = pos_base;
+  at.kv_stride_b = c.sb;
+  at.kv_stride_h = c.sh;
+  at.B = B;
+  at.H = m->H;
+  at.S = S;
+  at.dk = m->dk;
+  at.scale = sqrtf((float)m->dk);
+  at.full = am.full;
+  at.mask = am.mask;
+  if (rg) {
+    at.seq_len = rg->seq_len;
+    at.row_start = rg->row_start;
+  }
+  NML_TRY(launch_attention_prefill(m->dt, at, st));
+  LinearArgs wo{};
+  wo.x = a.att;
+  wo.lda = d;
+  wo.w = w.wo;
+  wo.bias = w.bo;
+  wo.resid = resid;
+  wo.out = out;
+  wo.M = R;
+  wo.N = d;
+  wo.K = d;
+  wo.epi = resid ? EPI_BIAS_RESID : EPI_BIAS;
+  return launch_linear(m->dt, wo, st);
+}
+
 // The transformer trunk over R = B·S rows already embedded in acts.x (or rg->R packed
 // ragged rows, S then being the longest length). Leaves the final-normed hidden states
-// in acts.xn. pos_base (device, B) gives each row's first position (null → 0); kv(l)
-// gives layer l's K/V destination.
+// in acts.xn (final_norm) or the residual stream in acts.x (!final_norm: a stack of
+// blocks without the trunk's last RMSNorm). pos_base (device, B) gives each row's first
+// position (null → 0); kv(l) gives layer l's K/V destination.
 template <typename KVF>
 int trunk(nml_model* m, const Acts& a, int B, int S, const int32_t* pos_base, KVF kv,
-          hipStream_t st, const Ragged* rg = nullptr) {
+          hipStream_t st, const Ragged* rg = nullptr, bool final_norm = true,
+          const AttnMode& am = AttnMode{}) {
   const int R = rg ? rg->R : B * S, d = m->d;
   for (int l = 0; l < m->L; ++l) {
     const Layer& w = m->layers[l];
     const KVView c = kv(l);
     NML_TRY(launch_rmsnorm(m->dt, a.x, w.ln1, a.xn, nullptr, nullptr, R, d, kEps, st));
-    LinearArgs qkv{};
-    qkv.x = a.xn;
-    qkv.lda = d;
-    qkv.w = w.wqkv;
-    qkv.bias = w.bqkv;
-    qkv.M = R;
-    qkv.N = 3 * d;
-    qkv.K = d;
-    qkv.epi = EPI_QKV;
-    qkv.qkv = QKVDst{a.q, c.k, c.v, pos_base, c.sb, c.sh, S, m->H, m->dk, d,
-                     rg ? rg->row_seg : nullptr};
-    NML_TRY(launch_linear(m->dt, qkv, st));
-    if (rope_on(m))  // models/gpt.py:62-64 → _fused_arrays.py:95-98
-      NML_TRY(launch_rope(m->dt, a.q, c.k, c.sb, c.sh, B, m->H, S, m->dk, pos_base,
-                          rg ? rg->seq_len : nullptr, m->rope_cos, m->rope_sin, m->P, st));
-    AttnArgs at{};
-    at.q = a.q;
-    at.k = c.k;
-    at.v = c.v;
-    at.out = a.att;
-    at.pos_base = pos_base;
-    at.kv_stride_b = c.sb;
-    at.kv_stride_h = c.sh;
-    at.B = B;
-    at.H = m->H;
-    at.S = S;
-    at.dk = m->dk;
-    at.scale = sqrtf((float)m->dk);
-    if (rg) {
-      at.seq_len = rg->seq_len;
-      at.row_start = rg->row_start;
-    }
-    NML_TRY(launch_attention_prefill(m->dt, at, st));
-    LinearArgs wo{};
-    wo.x = a.att;
-    wo.lda = d;
-    wo.w = w.wo;
-    wo.bias = w.bo;
-    wo.resid = a.x;
-    wo.out = a.x;
-    wo.M = R;
-    wo.N = d;
-    wo.K = d;
-    wo.epi = EPI_BIAS_RESID;
-    NML_TRY(launch_linear(m->dt, wo, st));
+    NML_TRY(attention_sublayer(m, w, a.xn, a, B, S, pos_base, c, rope_on(m), am, a.x, a.x, st,
+                               rg));
     NML_TRY(launch_rmsnorm(m->dt, a.x, w.ln2, a.xn, nullptr, nullptr, R, d, kEps, st));
     LinearArgs f1{};
     f1.x = a.xn;
@@ -241,7 +263,7 @@ int trunk(nml_model* m, const Acts& a, int B, int S, const int32_t* pos_base, KV
     f2.epi = EPI_BIAS_RESID;
     NML_TRY(launch_linear(m->dt, f2, st));
   }
-  NML_TRY(launch_rmsnorm(m->dt, a.x, m->lnf, a.xn, nullptr, nullptr, R, d, kEps, st));
+  if (final_norm) NML_TRY(launch_rmsnorm(m->dt, a.x, m->lnf, a.xn, nullptr, nullptr, R, d, kEps, st));
   return 0;
 }
 
@@ -602,6 +624,57 @@ int nml_model_forward(nml_model* m, const int64_t* ids, size_t batch, size_t seq
   const long long sb = (long long)m->H * S * m->dk, sh = (long long)S * m->dk;
   NML_TRY(trunk(m, a, B, S, nullptr, [&](int) { return KVView{kbuf, vbuf, sb, sh}; }, st));
   return head(m, a, B, S, logits, last_only, st);
+}
+
+int nml_model_blocks_forward(nml_model* m, const void* x, void* out, size_t batch, size_t seq,
+                             int final_norm, int causal, const void* mask) {
+  NML_REQUIRE(m != nullptr, "model is null");
+  NML_REQUIRE(seq <= (size_t)m->P, "Sequence length %zu exceeds maximum sequence length %d", seq,
+              m->P);
+  NML_REQUIRE(!causal || mask == nullptr, "blocks_forward: a causal call takes no mask");
+  if (batch == 0 || seq == 0) return 0;
+  const int B = (int)batch, S = (int)seq;
+  hipStream_t st = nml::stream();
+  Acts a;
+  NML_TRY(acts_for(m, B * S, 0, &a));
+  const size_t bytes = (size_t)B * S * m->d * m->es;
+  const size_t kvb = align256(bytes);
+  NML_TRY(m->kvs.ensure(2 * kvb));
+  void* kbuf = m->kvs.p;
+  void* vbuf = static_cast<char*>(m->kvs.p) + kvb;
+  NML_HIP(hipMemcpyAsync(a.x, x, bytes, hipMemcpyDeviceToDevice, st));
+  AttnMode am;
+  am.full = causal ? 0 : 1;
+  am.mask = mask;
+  const long long sb = (long long)m->H * S * m->dk, sh = (long long)S * m->dk;
+  NML_TRY(trunk(m, a, B, S, nullptr, [&](int) { return KVView{kbuf, vbuf, sb, sh}; }, st,
+                nullptr, final_norm != 0, am));
+  NML_HIP(hipMemcpyAsync(out, final_norm ? a.xn : a.x, bytes, hipMemcpyDeviceToDevice, st));
+  return 0;
+}
+
+int nml_model_mha_forward(nml_model* m, int layer, const void* x, void* out, size_t batch,
+                          size_t seq, int causal, const void* mask) {
+  NML_REQUIRE(m != nullptr, "model is null");
+  NML_REQUIRE(layer >= 0 && layer < m->L, "layer %d outside [0, %d)", layer, m->L);
+  NML_REQUIRE(seq <= (size_t)m->P, "Sequence length %zu exceeds maximum sequence length %d", seq,
+              m->P);
+  NML_REQUIRE(!causal || mask == nullptr, "mha_forward: a causal call takes no mask");
+  if (batch == 0 || seq == 0) return 0;
+  const int B = (int)batch, S = (int)seq;
+  hipStream_t st = nml::stream();
+  Acts a;
+  NML_TRY(acts_for(m, B * S, 0, &a));
+  const size_t kvb = align256((size_t)B * S * m->d * m->es);
+  NML_TRY(m->kvs.ensure(2 * kvb));
+  AttnMode am;
+  am.full = causal ? 0 : 1;
+  am.mask = mask;
+  const long long sb = (long long)m->H * S * m->dk, sh = (long long)S * m->dk;
+  const KVView c{m->kvs.p, static_cast<char*>(m->kvs.p) + kvb, sb, sh};
+  // neural_network/attention.py:139-168 applies no rotary embedding
+  return attention_sublayer(m, m->layers[layer], x, a, B, S, nullptr, c, false, am, nullptr, out,
+                            st, nullptr);
 }
 
 int nml_model_loss(nml_model* m, const int64_t* ids, const int64_t* labels, size_t batch,

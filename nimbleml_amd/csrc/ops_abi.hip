@@ -221,6 +221,28 @@ int nml_causal_attention_device(const void* q, const void* k, const void* v, voi
   return launch_attention_prefill(dtype, a, nml::stream());
 }
 
+int nml_sdpa_forward_device(const void* q, const void* k, const void* v, const void* mask,
+                            void* out, size_t bh, size_t seq, size_t dk, float scale_div,
+                            int causal, int dtype) {
+  NML_TRY(check_dtype(dtype));
+  NML_TRY(attn_shape_ok(bh, seq, dk));
+  NML_REQUIRE(!causal || mask == nullptr, "sdpa_forward: a causal call takes no mask");
+  AttnArgs a{};
+  a.q = q;
+  a.k = k;
+  a.v = v;
+  a.out = out;
+  a.kv_stride_b = (long long)(seq * dk);
+  a.B = (int)bh;
+  a.H = 1;
+  a.S = (int)seq;
+  a.dk = (int)dk;
+  a.scale = scale_div;
+  a.full = causal ? 0 : 1;
+  a.mask = mask;
+  return launch_attention_prefill(dtype, a, nml::stream());
+}
+
 int nml_flash_sdpa_forward_device(const float* q, const float* k, const float* v, float* out,
                                   float* m, float* l, size_t bh, size_t seq, size_t dk,
                                   float scale) {

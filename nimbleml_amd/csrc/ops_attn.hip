@@ -38,13 +38,16 @@ __global__ __launch_bounds__(64) void attn_prefill_kernel(AttnArgs a) {
   const int base = a.pos_base ? a.pos_base[b] : 0;
   const int qpos = base + s;
   const int last_s = min(S, (blockIdx.x + 1) * kTile) - 1;
-  const int kv_end = base + last_s + 1;
+  const int kv_end = a.full ? S : base + last_s + 1;
   const float scale_t = static_cast<float>(static_cast<T>(a.scale));
   const T* __restrict__ K = static_cast<const T*>(a.k) + b * a.kv_stride_b + h * a.kv_stride_h;
   const T* __restrict__ Vp = static_cast<const T*>(a.v) + b * a.kv_stride_b + h * a.kv_stride_h;
 
   float q[DK];
   const bool valid = s < S;
+  // row s of the additive mask (row 0 for the idle lanes past S)
+  const T* __restrict__ mrow =
+      a.mask ? static_cast<const T*>(a.mask) + static_cast<size_t>(valid ? s : 0) * S : nullptr;
   {
     const T* qp = static_cast<const T*>(a.q) + ((static_cast<size_t>(bh) * a.S) + (valid ? s : 0)) * DK;
 #pragma unroll
@@ -74,11 +77,12 @@ __global__ __launch_bounds__(64) void attn_prefill_kernel(AttnArgs a) {
       for (int jj = 0; jj < 16; ++jj) {
         const int kj = j0 + jj;
         float v = -INFINITY;
-        if (kj < nkeys && k0 + kj <= qpos) {
+        if (kj < nkeys && (a.full || k0 + kj <= qpos)) {
           float dot = 0.f;
 #pragma unroll
           for (int d = 0; d < DK; ++d) dot += q[d] * static_cast<float>(Ks[kj][d]);
           v = rnd<T>(rnd<T>(dot) / scale_t);
+          if (mrow) v = rnd<T>(v + static_cast<float>(mrow[k0 + kj]));
         }
         sc[jj] = v;
         mloc = fmaxf(mloc, v);
@@ -135,6 +139,26 @@ __device__ __forceinline__ void ld8(const T* p, float (&o)[8]) {
   }
 }
 
+// 8 consecutive elements kept in their storage type (half: one 16-byte register
+// quad), widened where they are used.
+template <typename T>
+struct Raw8;
+template <>
+struct Raw8<half_t> {
+  half8 v;
+  __device__ __forceinline__ void load(const half_t* p) { v = *reinterpret_cast<const half8*>(p); }
+  __device__ __forceinline__ float at(int e) const { return static_cast<float>(v[e]); }
+};
+template <>
+struct Raw8<float> {
+  floatx4 x, y;
+  __device__ __forceinline__ void load(const float* p) {
+    x = *reinterpret_cast<const floatx4*>(p);
+    y = *reinterpret_cast<const floatx4*>(p + 4);
+  }
+  __device__ __forceinline__ float at(int e) const { return e < 4 ? x[e] : y[e - 4]; }
+};
+
 // Decode attention for head dims ≥ 32, one launch: a 256-lane workgroup takes a group
 // of G 64-key chunks of one (row, head) — all their K/V rows are loaded up front
 // (clamped into [0, len), the clamped ones never used) — scores every key with 4
@@ -176,23 +200,20 @@ __global__ __launch_bounds__(256) void attn_decode_group_kernel(AttnArgs a, cons
   const T* __restrict__ Vp = static_cast<const T*>(a.v) + b * a.kv_stride_b + h * a.kv_stride_h;
   const float scale_t = static_cast<float>(static_cast<T>(a.scale));
   const int qq = tid & 3, dg = tid % DG, ks = tid / DG;
-  float kr[G][DPT];
-  float vr[G][KPT][8];
+  // K/V stay in their storage type in registers (half the registers of widened copies,
+  // so more workgroups per CU keep loads in flight)
+  Raw8<T> kr[G][DPT / 8];
+  Raw8<T> vr[G][KPT];
 #pragma unroll
   for (int j = 0; j < G; ++j) {
     const int key = k0 + j * CH + (tid >> 2);
     const int keyc = key < len ? key : len - 1;
 #pragma unroll
-    for (int e = 0; e < DPT; e += 8) {
-      float t8[8];
-      ld8<T>(K + static_cast<long long>(keyc) * DK + qq * DPT + e, t8);
-#pragma unroll
-      for (int u = 0; u < 8; ++u) kr[j][e + u] = t8[u];
-    }
+    for (int e = 0; e < DPT / 8; ++e) kr[j][e].load(K + static_cast<long long>(keyc) * DK + qq * DPT + e * 8);
 #pragma unroll
     for (int i = 0; i < KPT; ++i) {
       const int vk = k0 + j * CH + ks + i * NKS;
-      ld8<T>(Vp + static_cast<long long>(vk < len ? vk : len - 1) * DK + dg * 8, vr[j][i]);
+      vr[j][i].load(Vp + static_cast<long long>(vk < len ? vk : len - 1) * DK + dg * 8);
     }
   }
   if (tid < DK) s_q[tid] = static_cast<float>(static_cast<const T*>(a.q)[static_cast<size_t>(bh) * DK + tid]);
@@ -203,7 +224,7 @@ __global__ __launch_bounds__(256) void attn_decode_group_kernel(AttnArgs a, cons
   for (int j = 0; j < G; ++j) {
     float dot = 0.f;
 #pragma unroll
-    for (int e = 0; e < DPT; ++e) dot += s_q[qq * DPT + e] * kr[j][e];
+    for (int e = 0; e < DPT; ++e) dot += s_q[qq * DPT + e] * kr[j][e / 8].at(e % 8);
     dot = quad_sum_dpp(dot);
     const bool valid = k0 + j * CH + (tid >> 2) < len;
     sc[j] = valid ? rnd<T>(rnd<T>(dot) / scale_t) : -INFINITY;
@@ -237,7 +258,7 @@ __global__ __launch_bounds__(256) void attn_decode_group_kernel(AttnArgs a, cons
       if (k0 + jj < len) {
         const float pj = s_p[jj];
 #pragma unroll
-        for (int e = 0; e < 8; ++e) o[e] += pj * vr[j][i][e];
+        for (int e = 0; e < 8; ++e) o[e] += pj * vr[j][i].at(e);
       }
     }
 #pragma unroll
@@ -769,6 +790,14 @@ int prefill_f32_mfma(const AttnArgs& a, hipStream_t st) {
 
 template <typename T, int DK>
 int prefill_typed(const AttnArgs& a, hipStream_t st) {
+  if (a.full) {  // non-causal / masked: the scalar kernel only
+    NML_REQUIRE(!a.pos_base && !a.seq_len && !a.row_start,
+                "attention: non-causal attention takes dense rows from position 0");
+    dim3 grid((a.S + kTile - 1) / kTile, a.B * a.H);
+    attn_prefill_kernel<T, DK><<<grid, 64, 0, st>>>(a);
+    NML_LAUNCHED();
+    return 0;
+  }
   if constexpr (sizeof(T) == 4 && (DK == 64 || DK == 128)) {
     if (!std::getenv("NIMBLEML_ATTN_F32_SCALAR")) return prefill_f32_mfma<DK>(a, st);
   }

@@ -17,7 +17,7 @@ from nimbleml_amd import _native as N
 from nimbleml_amd import np_backend
 from nimbleml_amd.grad_mode import is_grad_enabled
 from nimbleml_amd.layers import (Embedding, FusedGPTTrunk, FusedTransformerBlock, Module,
-                                 RMSNorm, Sequential)
+                                 RMSNorm, Sequential, block_device_arrays, rope_device_arrays)
 from nimbleml_amd.tensor import Tensor
 
 
@@ -124,27 +124,12 @@ class GPT(Module):
 
         out = [(N.P_TOKEN_EMB, 0, a(self.token_emb.weights)), (N.P_LN_F, 0, a(self.ln.gamma))]
         if self.use_rope:
-            # the first half of each row, cast to the compute dtype as apply_rope_flat
-            # casts it (utils/rope.py:36-38)
-            half = (self.d_model // self.num_heads) // 2
-            out += [(N.P_ROPE_COS, 0, np.ascontiguousarray(self._rope_cos[:, :half].astype(dt))),
-                    (N.P_ROPE_SIN, 0, np.ascontiguousarray(self._rope_sin[:, :half].astype(dt)))]
+            out += rope_device_arrays((self._rope_cos, self._rope_sin),
+                                      self.d_model // self.num_heads, dt)
         else:
             out.append((N.P_POS_EMB, 0, a(self.pos_emb.weights)))
         for i, blk in enumerate(self._block_list):
-            m = blk.mha
-            wqkv = np.concatenate([a(m.W_q.weights), a(m.W_k.weights), a(m.W_v.weights)], axis=1)
-            bqkv = np.concatenate([a(m.W_q.biases), a(m.W_k.biases), a(m.W_v.biases)])
-            out += [(N.P_LN1, i, a(blk.ln1.gamma)),
-                    (N.P_WQKV, i, np.ascontiguousarray(wqkv.T)),
-                    (N.P_BQKV, i, bqkv),
-                    (N.P_WO, i, np.ascontiguousarray(a(m.W_o.weights).T)),
-                    (N.P_BO, i, a(m.W_o.biases)),
-                    (N.P_LN2, i, a(blk.ln2.gamma)),
-                    (N.P_W1, i, np.ascontiguousarray(a(blk.ffn.dense1.weights).T)),
-                    (N.P_B1, i, a(blk.ffn.dense1.biases)),
-                    (N.P_W2, i, np.ascontiguousarray(a(blk.ffn.dense2.weights).T)),
-                    (N.P_B2, i, a(blk.ffn.dense2.biases))]
+            out += block_device_arrays(blk, i, dt)
         return out
 
     def _device_model(self):

@@ -4,7 +4,7 @@ Each takes host arrays or ``DeviceArray``s in the compute dtype and returns
 ``DeviceArray`` results computed by the HIP kernels:
   fused_rmsnorm_forward       kernels/fused_rmsnorm.py:130-162
   fused_gelu_forward          kernels/fused_gelu.py:57-83
-  fused_sdpa_forward          kernels/fused_sdpa.py:256-289 (causal mask only)
+  fused_sdpa_forward          kernels/fused_sdpa.py:256-289 (any additive mask, or none)
   embedding_lookup            kernels/embedding_scatter.py:25-36
   fused_tied_crossentropy_forward  kernels/fused_tied_crossentropy.py:8-24 (loss only)
   linear                      the `x @ W + b` of neural_network/_fused_arrays.py:25-30
@@ -63,16 +63,26 @@ def fused_gelu_forward(x):
 
 
 def fused_sdpa_forward(q, k, v, scale, mask_arr=None, *, batch=None, num_heads=None):
-    """Causal attention over (bh, seq, dk); ``scale`` is the sqrt(dk) divisor. The
-    reference's GPT always passes the causal mask; other masks are not supported."""
-    if mask_arr is None:
-        raise NotImplementedError("only causal attention (the GPT path) runs on the HIP device")
+    """Attention over (bh, seq, dk) (kernels/fused_sdpa.py:256-289); ``scale`` is the
+    sqrt(dk) divisor. ``mask_arr``: None attends to every key (the reference's
+    ``_matmul_sdpa_forward`` without a mask); the causal mask (−inf above the diagonal)
+    runs the causal kernels; any other additive (seq, seq) mask is added to the scaled
+    scores. Returns ``(out, None)``: no probability matrix is formed."""
     dt = _float_dtype(q)
     qd, kd, vd = _dev(q, dt), _dev(k, dt), _dev(v, dt)
     bh, seq, dk = qd.shape
+    causal, md = 0, None
+    if mask_arr is not None:
+        m = np.ascontiguousarray(np.asarray(mask_arr).astype(dt, copy=False))
+        if m.shape != (seq, seq):
+            raise ValueError(f"mask must be ({seq}, {seq}), got {m.shape}")
+        if np.array_equal(m, np.triu(np.full((seq, seq), -np.inf, dtype=dt), k=1)):
+            causal = 1
+        else:
+            md = N.DeviceArray.from_host(m)
     out = N.DeviceArray((bh, seq, dk), dt)
-    N.check(N.lib.nml_causal_attention_device(qd.ptr, kd.ptr, vd.ptr, out.ptr, bh, seq, dk,
-                                              float(scale), N.np_dtype_code(dt)))
+    N.check(N.lib.nml_sdpa_forward_device(qd.ptr, kd.ptr, vd.ptr, N.ptr(md), out.ptr, bh, seq, dk,
+                                          float(scale), causal, N.np_dtype_code(dt)))
     return out, None
 
 

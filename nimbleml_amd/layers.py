@@ -10,16 +10,34 @@ its modules (NimbleML/utils/saveload.py:16-41), so checkpoints interchange.
   FusedTransformerBlock ln1, mha, ln2, ffn              neural_network/transformer_fused.py:35-42
 Initial values follow the same distributions (embedding N(0, 0.02), dense
 U(−1, 1)/sqrt(in), zero biases, unit gammas) from NumPy's global generator.
-The forward passes run in the GPT driver on the GPU (gpt.py).
+
+Every module's ``forward`` runs on the GPU and returns a Tensor over a ``DeviceArray``:
+  Dense.forward               layers/dense.py:27-70        x·W + b (nml_linear_device)
+  Embedding.forward / _prefix layers/embedding.py:23-118   gather (nml_embedding_gather_device)
+  RMSNorm.forward             layers/rms_norm.py:25-95     (nml_rmsnorm_forward_device)
+  FeedForward.forward         neural_network/feed_forward.py   two GEMMs, GELU fused
+  MultiHeadAttention.forward  neural_network/attention.py:139-168  (nml_model_mha_forward)
+  FusedTransformerBlock.forward  neural_network/transformer_fused.py:44-95
+  FusedGPTTrunk.forward          transformer_fused.py:103-144 (nml_model_blocks_forward)
+  Sequential.forward          neural_network/module.py:54-65
+The block, trunk and attention modules upload their current host parameters into a
+device model for the call (the GPT keeps its own resident copy instead). Masks follow
+the reference: an additive (seq, seq) array or Tensor; ``None`` is causal for the
+fused block and trunk and no mask for MultiHeadAttention. Gradients of these
+module-level outputs are not computed on the device (``GPT.compute_loss`` is the
+training path); calling ``backward`` through one raises.
 """
 from __future__ import annotations
 
 import contextlib
-from math import sqrt
+import ctypes as C
+from math import prod, sqrt
 
 import numpy as np
 
+from nimbleml_amd import _native as N
 from nimbleml_amd import np_backend
+from nimbleml_amd.grad_mode import is_grad_enabled
 from nimbleml_amd.tensor import Tensor
 
 _SKIP_INIT = [False]
@@ -71,8 +89,168 @@ class Module:
         for child in self._child_modules():
             child.eval()
 
-    def __call__(self, x):
-        return self.forward(x)
+    def __call__(self, *args, **kwargs):
+        return self.forward(*args, **kwargs)
+
+
+# ------------------------------------------------------------------ device plumbing
+def _compute_dtype():
+    return np.dtype(np_backend.dtype)
+
+
+def _device_input(x, dt):
+    """``x`` (Tensor, DeviceArray or array) as a DeviceArray of its own shape in ``dt``."""
+    data, shape = (x.data, x.shape) if isinstance(x, Tensor) else (x, np.shape(x))
+    if isinstance(data, N.DeviceArray):
+        if data.dtype != dt:
+            raise TypeError(f"expected a {dt} input, got {data.dtype}")
+        return data.reshape(shape)
+    return N.DeviceArray.from_host(np.asarray(data, dtype=dt).reshape(shape))
+
+
+def _host(t, shape, dt):
+    return np.ascontiguousarray(np.asarray(t.data, dtype=dt).reshape(shape))
+
+
+def _output(arr, shape, x, params, op):
+    """The module's result Tensor. With gradients wanted, its backward raises: module-level
+    gradients are not computed on the device."""
+    needs = is_grad_enabled() and (getattr(x, "requires_grad", False)
+                                   or any(p.requires_grad for p in params))
+    out = Tensor(arr, shape, requires_grad=needs, _op=op)
+    if needs:
+        def _backward():
+            raise NotImplementedError(
+                f"{op}: gradients of module-level forwards are not computed on the device; "
+                "train through GPT.compute_loss")
+
+        out._backward = _backward
+    return out
+
+
+def _mask_mode(mask, seq, dt, *, none_is_causal):
+    """``(causal, DeviceArray | None)`` for a mask argument: a mask equal to the causal
+    mask (utils/mask.py:8-13: −inf above the diagonal, 0 elsewhere) takes the causal
+    kernels; any other (seq, seq) mask is added to the scores as given."""
+    if mask is None:
+        return (1, None) if none_is_causal else (0, None)
+    arr = np.asarray(mask.data if isinstance(mask, Tensor) else mask)
+    if isinstance(mask, Tensor):
+        arr = arr.reshape(mask.shape)
+    if arr.shape != (seq, seq):
+        raise ValueError(f"mask must be ({seq}, {seq}), got {arr.shape}")
+    arr = np.ascontiguousarray(arr.astype(dt, copy=False))
+    if np.array_equal(arr, np.triu(np.full((seq, seq), -np.inf, dtype=dt), k=1)):
+        return 1, None
+    return 0, N.DeviceArray.from_host(arr)
+
+
+def _dense_bias(dense, dt):
+    if dense.biases is None:
+        return np.zeros(dense.out_features, dtype=dt)
+    return _host(dense.biases, (dense.out_features,), dt)
+
+
+def mha_device_arrays(mha, layer, dt):
+    """(kind, layer, array) of one attention module in the device layout: W_q | W_k | W_v
+    stacked and transposed to (3d, d), W_o transposed to (d, d)."""
+    d = mha.d_model
+    w = [_host(x.weights, (d, d), dt) for x in (mha.W_q, mha.W_k, mha.W_v)]
+    b = [_dense_bias(x, dt) for x in (mha.W_q, mha.W_k, mha.W_v)]
+    return [(N.P_WQKV, layer, np.ascontiguousarray(np.concatenate(w, axis=1).T)),
+            (N.P_BQKV, layer, np.concatenate(b)),
+            (N.P_WO, layer, np.ascontiguousarray(_host(mha.W_o.weights, (d, d), dt).T)),
+            (N.P_BO, layer, _dense_bias(mha.W_o, dt))]
+
+
+def block_device_arrays(blk, layer, dt):
+    """(kind, layer, array) of one FusedTransformerBlock in the device layout."""
+    d = blk.d_model
+    f1, f2 = blk.ffn.dense1, blk.ffn.dense2
+    return ([(N.P_LN1, layer, _host(blk.ln1.gamma, (d,), dt))]
+            + mha_device_arrays(blk.mha, layer, dt)
+            + [(N.P_LN2, layer, _host(blk.ln2.gamma, (d,), dt)),
+               (N.P_W1, layer, np.ascontiguousarray(_host(f1.weights, (d, f1.out_features),
+                                                          dt).T)),
+               (N.P_B1, layer, _dense_bias(f1, dt)),
+               (N.P_W2, layer, np.ascontiguousarray(_host(f2.weights, (f2.in_features, d),
+                                                          dt).T)),
+               (N.P_B2, layer, _dense_bias(f2, dt))])
+
+
+def rope_device_arrays(rope_cache, head_dim, dt):
+    """The first half of each RoPE table row in the compute dtype, as apply_rope_flat casts
+    it (utils/rope.py:36-38)."""
+    cos, sin = rope_cache
+    half = head_dim // 2
+    return [(N.P_ROPE_COS, 0, np.ascontiguousarray(np.asarray(cos)[:, :half].astype(dt))),
+            (N.P_ROPE_SIN, 0, np.ascontiguousarray(np.asarray(sin)[:, :half].astype(dt)))]
+
+
+class _CallModel:
+    """A device model built for one module-level call: only the arrays given are uploaded
+    (the token and position tables stay unused); freed with the object."""
+
+    def __init__(self, d_model, num_heads, num_layers, max_seq_len, d_ff, dt, arrays):
+        N.ensure_init()
+        h = C.c_void_p()
+        N.check(N.lib.nml_model_create(1, d_model, num_heads, num_layers, max_seq_len, d_ff,
+                                       N.np_dtype_code(dt), C.byref(h)))
+        self.handle = h
+        try:
+            for kind, layer, arr in arrays:
+                N.check(N.lib.nml_model_set_param(h, kind, layer, arr.ctypes.data, arr.nbytes))
+        except Exception:
+            self.close()
+            raise
+
+    def close(self):
+        if self.handle:
+            N.lib.nml_model_destroy(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+def _blocks_forward(blocks, ln, x, mask, op, params):
+    """FusedTransformerBlock / FusedGPTTrunk forward over a (batch, seq, d) input."""
+    blocks = list(blocks)
+    if len(x.shape) != 3:
+        raise ValueError(f"expected (batch, seq, d_model), got {x.shape}")
+    b, s, d = x.shape
+    blk0 = blocks[0]
+    if d != blk0.d_model:
+        raise ValueError(f"Expected d_model {blk0.d_model}, got {d}")
+    dt = _compute_dtype()
+    causal, mdev = _mask_mode(mask, s, dt, none_is_causal=True)
+    dk = d // blk0.num_heads
+    arrays = []
+    for i, blk in enumerate(blocks):
+        arrays += block_device_arrays(blk, i, dt)
+    arrays.append((N.P_LN_F, 0, _host(ln.gamma, (d,), dt) if ln is not None
+                   else np.ones(d, dtype=dt)))
+    rope = blk0.mha._rope_cache
+    p = max(s, 1)
+    if rope is not None:  # _fused_arrays.py:95-98: positions 0..seq-1 of the block's table
+        arrays += rope_device_arrays(rope, dk, dt)
+        p = int(np.asarray(rope[0]).shape[0])
+        if s > p:
+            raise ValueError(f"Sequence length {s} exceeds the RoPE table ({p} positions)")
+    model = _CallModel(d, blk0.num_heads, len(blocks), p, blk0.ffn.dense1.out_features, dt,
+                       arrays)
+    xd = _device_input(x, dt)
+    out = N.DeviceArray((b, s, d), dt)
+    try:
+        N.check(N.lib.nml_model_blocks_forward(model.handle, xd.ptr, out.ptr, b, s,
+                                               int(ln is not None), causal, N.ptr(mdev)))
+        N.check(N.lib.nml_synchronize())
+    finally:
+        model.close()
+    return _output(out, (b, s, d), x, params, op)
 
 
 class Sequential(Module):
@@ -81,6 +259,12 @@ class Sequential(Module):
 
     def __iter__(self):
         return iter(self.layers)
+
+    def forward(self, data):
+        """neural_network/module.py:54-65: each layer in order."""
+        for layer in self.layers:
+            data = layer(data)
+        return data
 
     def parameters(self):
         params = []
@@ -104,6 +288,19 @@ class Dense(Module):
                               (in_features, out_features))
         self.biases = _param(np.zeros(out_features), (out_features,)) if bias else None
 
+    def forward(self, inputs):
+        """layers/dense.py:27-70: ``x·W + b`` over the last dimension."""
+        if inputs.shape[-1] != self.in_features:
+            raise ValueError(f"Expected last dim {self.in_features}, got {inputs.shape[-1]}")
+        from nimbleml_amd import kernels as K
+
+        dt = _compute_dtype()
+        shape = (*inputs.shape[:-1], self.out_features)
+        x = _device_input(inputs, dt)
+        b = None if self.biases is None else _host(self.biases, (self.out_features,), dt)
+        out = K.linear(x, _host(self.weights, (self.in_features, self.out_features), dt), b)
+        return _output(out.reshape(shape), shape, inputs, self.parameters(), "dense")
+
     def parameters(self):
         return [self.weights] + ([self.biases] if self.biases is not None else [])
 
@@ -116,6 +313,32 @@ class Embedding(Module):
                                     * init_std, (vocab_size, embed_dim)),
                               (vocab_size, embed_dim))
 
+    def forward(self, inputs):
+        """layers/embedding.py:23-70: rows of the table for integer ids of any shape."""
+        from nimbleml_amd import kernels as K
+
+        if isinstance(inputs, Tensor):
+            ids = np.asarray(inputs.data, dtype=np.int64).reshape(inputs.shape)
+        else:
+            ids = np.asarray(inputs, dtype=np.int64)
+        dt = _compute_dtype()
+        w = N.DeviceArray.from_host(_host(self.weights, (self.vocab_size, self.embed_dim), dt))
+        shape = (*ids.shape, self.embed_dim)
+        if ids.size == 0:
+            return _output(N.DeviceArray(shape, dt), shape, None, self.parameters(), "embedding")
+        out = K.embedding_lookup(w, ids)
+        return _output(out.reshape(shape), shape, None, self.parameters(), "embedding")
+
+    def forward_prefix(self, seq_len: int):
+        """layers/embedding.py:72-118: rows ``[0, seq_len)`` of the table, (seq_len, dim)."""
+        if seq_len < 0 or seq_len > self.vocab_size:
+            raise ValueError(f"seq_len must be in [0, {self.vocab_size}), got {seq_len}.")
+        dt = _compute_dtype()
+        rows = _host(self.weights, (self.vocab_size, self.embed_dim), dt)[:seq_len]
+        shape = (seq_len, self.embed_dim)
+        return _output(N.DeviceArray.from_host(rows), shape, None, self.parameters(),
+                       "embedding_prefix")
+
     def parameters(self):
         return [self.weights]
 
@@ -125,6 +348,20 @@ class RMSNorm(Module):
         self.normalized_shape = normalized_shape
         self.epsilon = epsilon
         self.gamma = _param(np.ones(normalized_shape), (normalized_shape,))
+
+    def forward(self, inputs):
+        """layers/rms_norm.py:25-95: ``gamma · x / sqrt(mean(x²) + eps)`` over the last dim."""
+        if inputs.shape[-1] != self.normalized_shape:
+            raise ValueError(f"Expected last dim {self.normalized_shape}, got {inputs.shape[-1]}")
+        from nimbleml_amd import kernels as K
+
+        dt = _compute_dtype()
+        d = self.normalized_shape
+        rows = prod(inputs.shape[:-1]) if len(inputs.shape) > 1 else 1
+        x = _device_input(inputs, dt).reshape(rows, d)
+        out = K.fused_rmsnorm_forward(x, _host(self.gamma, (d,), dt), self.epsilon)[0]
+        return _output(out.reshape(inputs.shape), inputs.shape, inputs, self.parameters(),
+                       "rms_norm")
 
     def parameters(self):
         return [self.gamma]
@@ -144,6 +381,30 @@ class MultiHeadAttention(Module):
         self.scale = float(self.d_k) ** 0.5
         self._rope_cache = None
 
+    def forward(self, x, mask=None):
+        """neural_network/attention.py:139-168: per-head softmax(q·kᵀ / sqrt(d_k) + mask)·v
+        of x's projections, heads merged, then W_o. ``mask=None`` attends to every key;
+        the RoPE cache is not applied here (the reference applies it in the fused block)."""
+        if len(x.shape) != 3:
+            raise ValueError(f"expected (batch, seq, d_model), got {x.shape}")
+        b, s, d = x.shape
+        if d != self.d_model:
+            raise ValueError(f"Expected d_model {self.d_model}, got {d}")
+        dt = _compute_dtype()
+        causal, mdev = _mask_mode(mask, s, dt, none_is_causal=False)
+        vec = 8 if dt == np.float16 else 4
+        model = _CallModel(d, self.num_heads, 1, max(s, 1), vec, dt,
+                           mha_device_arrays(self, 0, dt))
+        xd = _device_input(x, dt)
+        out = N.DeviceArray((b, s, d), dt)
+        try:
+            N.check(N.lib.nml_model_mha_forward(model.handle, 0, xd.ptr, out.ptr, b, s, causal,
+                                                N.ptr(mdev)))
+            N.check(N.lib.nml_synchronize())
+        finally:
+            model.close()
+        return _output(out, (b, s, d), x, self.parameters(), "multi_head_attention")
+
     def parameters(self):
         params = []
         for layer in (self.W_q, self.W_k, self.W_v, self.W_o):
@@ -157,13 +418,33 @@ class FeedForward(Module):
         self.dense1 = Dense(d_model, hidden)
         self.dense2 = Dense(hidden, d_model)
 
+    def forward(self, x):
+        """neural_network/feed_forward.py: ``GELU(x·W₁ + b₁)·W₂ + b₂`` per token, the GELU
+        fused into the first GEMM's epilogue."""
+        from nimbleml_amd import kernels as K
+
+        w1, w2 = self.dense1, self.dense2
+        if x.shape[-1] != w1.in_features:
+            raise ValueError(f"Expected last dim {w1.in_features}, got {x.shape[-1]}")
+        if w1.out_features != w2.in_features:
+            raise ValueError(f"Dense1 out ({w1.out_features}) must match Dense2 in "
+                             f"({w2.in_features})")
+        if w2.out_features != x.shape[-1]:
+            raise ValueError(f"Expected output last dim {x.shape[-1]}, got {w2.out_features}")
+        dt = _compute_dtype()
+        xd = _device_input(x, dt)
+        h = K.linear(xd, _host(w1.weights, (w1.in_features, w1.out_features), dt),
+                     _dense_bias(w1, dt), epilogue=K.EPI_BIAS_GELU)
+        out = K.linear(h, _host(w2.weights, (w2.in_features, w2.out_features), dt),
+                       _dense_bias(w2, dt))
+        return _output(out.reshape(x.shape), x.shape, x, self.parameters(), "feed_forward")
+
     def parameters(self):
         return self.dense1.parameters() + self.dense2.parameters()
 
 
 class FusedTransformerBlock(Module):
-    """Pre-norm block (x + MHA(LN1(x)); x + FFN(LN2(x))). Its forward runs inside
-    the GPT driver on the GPU, one launch sequence per block."""
+    """Pre-norm block (x + MHA(LN1(x)); x + FFN(LN2(x)))."""
 
     def __init__(self, d_model, num_heads, ff_mult=4, *, gradient_checkpointing: bool = False):
         self.d_model = d_model
@@ -173,6 +454,12 @@ class FusedTransformerBlock(Module):
         self.mha = MultiHeadAttention(d_model, num_heads)
         self.ln2 = RMSNorm(d_model)
         self.ffn = FeedForward(d_model, ff_mult=ff_mult)
+
+    def forward(self, x, mask=None):
+        """neural_network/transformer_fused.py:44-95 → fused_block_forward_arrays
+        (_fused_arrays.py:251-284); ``mask=None`` is causal."""
+        return _blocks_forward([self], None, x, mask, "fused_transformer_block",
+                               self.parameters())
 
     def parameters(self):
         params = []
@@ -187,6 +474,11 @@ class FusedGPTTrunk(Module):
     def __init__(self, blocks, ln: RMSNorm):
         self.blocks = list(blocks)
         self.ln = ln
+
+    def forward(self, x, mask=None):
+        """transformer_fused.py:103-144: every block, then the final RMSNorm."""
+        return _blocks_forward(self.blocks, self.ln, x, mask, "fused_gpt_trunk",
+                               self.parameters())
 
     def parameters(self):
         params = []
