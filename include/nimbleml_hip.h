@@ -272,6 +272,28 @@ int nml_model_adamw_step(nml_model* m, float lr, float beta1, float beta2, float
  * v[i], adam.py:64-83), for checkpoints and tests. */
 int nml_model_adam_moments(nml_model* m, int kind, int layer, void** first, void** second);
 
+/* Allocate the AdamW state if absent (Adam.__init__, adam.py:64-83): zero moments and,
+ * for float16 models, float32 masters copied from the current parameters. Lets a
+ * checkpoint's state (load_checkpoint, utils/saveload.py:334-358 → _load_optimizer_state
+ * :130-175) be written through nml_model_adam_moments / nml_model_adam_master before the
+ * first step. Idempotent. Parameters uploaded later with nml_model_set_param refresh their
+ * masters. */
+int nml_model_adam_state_init(nml_model* m);
+
+/* Device pointer of the float32 master copy of parameter (kind, layer) of a float16 model
+ * (Adam.masters[i], adam.py:75-81; saved as optimizer/master/i, saveload.py:108-110). */
+int nml_model_adam_master(nml_model* m, int kind, int layer, void** master);
+
+/* The per-parameter AdamW update of Adam._adam_update (adam.py:210-290) over elements
+ * [offset, offset + count) of parameter (kind, layer) in the device layout (a contiguous
+ * range: one of Q/K/V's row blocks of the stacked weight, a whole weight, a bias),
+ * with that parameter group's lr and weight_decay — for optimizers whose parameter groups
+ * or missing gradients (adam.py:97-104 skips parameters without one) rule out the whole-model
+ * nml_model_adamw_step. offset is a multiple of 4. */
+int nml_model_adamw_update(nml_model* m, int kind, int layer, size_t offset, size_t count,
+                           float lr, float beta1, float beta2, float bias_corr1, float bias_corr2,
+                           float eps, float weight_decay);
+
 /* KV cache for batch rows: K and V per layer, (batch, heads, max_seq, head_dim) each.
  * The seam generate() probes for (models/generate.py:93-100). */
 int nml_cache_create(nml_model* m, size_t batch, nml_cache** out);

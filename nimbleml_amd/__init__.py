@@ -15,12 +15,15 @@ from nimbleml_amd.layers import (Dense, Embedding, FeedForward, FusedGPTTrunk,
                                  FusedTransformerBlock, Module, MultiHeadAttention, RMSNorm,
                                  Sequential)
 from nimbleml_amd.np_backend import device, set_device, set_dtype, using_gpu
-from nimbleml_amd.saveload import load, load_arrays, named_parameters, save
+from nimbleml_amd.optim import Adam, AdamW
+from nimbleml_amd.saveload import (load, load_arrays, load_checkpoint, named_parameters, save,
+                                   save_checkpoint)
 from nimbleml_amd.tensor import Tensor
 
 __all__ = [
     "GPT", "KVCache", "generate", "Tensor", "DeviceArray", "Dense", "Embedding", "RMSNorm",
     "MultiHeadAttention", "FeedForward", "FusedTransformerBlock", "FusedGPTTrunk", "Module",
-    "Sequential", "save", "load", "load_arrays", "named_parameters", "device", "using_gpu",
+    "Sequential", "save", "load", "load_arrays", "named_parameters", "save_checkpoint",
+    "load_checkpoint", "Adam", "AdamW", "device", "using_gpu",
     "set_device", "set_dtype", "np_backend", "no_grad", "enable_grad", "is_grad_enabled",
 ]

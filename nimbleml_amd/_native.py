@@ -81,6 +81,9 @@ _SIGS = {
     "nml_model_saved_generation": [vp, C.POINTER(C.c_ulonglong)],
     "nml_model_adamw_step": [vp, f32, f32, f32, f32, f32, f32, f32],
     "nml_model_adam_moments": [vp, i32, i32, C.POINTER(C.c_void_p), C.POINTER(C.c_void_p)],
+    "nml_model_adam_state_init": [vp],
+    "nml_model_adam_master": [vp, i32, i32, C.POINTER(C.c_void_p)],
+    "nml_model_adamw_update": [vp, i32, i32, sz, sz, f32, f32, f32, f32, f32, f32, f32],
     "nml_cache_create": [vp, sz, C.POINTER(vp)],
     "nml_cache_destroy": [vp],
     "nml_cache_length": [vp, C.POINTER(sz)],

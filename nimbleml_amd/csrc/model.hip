@@ -591,6 +591,7 @@ int nml_model_set_param(nml_model* m, int kind, int layer, const void* host, siz
   const size_t want = param_elems(m, kind) * m->es;
   NML_REQUIRE(bytes == want, "parameter kind %d: expected %zu bytes, got %zu", kind, want, bytes);
   NML_HIP(hipMemcpyAsync(*slot, host, bytes, hipMemcpyHostToDevice, nml::stream()));
+  NML_TRY(train_param_uploaded(m, *slot, param_elems(m, kind)));
   NML_HIP(hipStreamSynchronize(nml::stream()));
   if (kind == NML_P_ROPE_COS) m->rope_cos_set = true;
   if (kind == NML_P_ROPE_SIN) m->rope_sin_set = true;

@@ -84,5 +84,8 @@ int check_ready(nml_model* m);
 
 // Training state teardown (train.hip), called by nml_model_destroy.
 void train_release(nml_model* m);
+// After a parameter upload: an fp16 model's AdamW master copy of that parameter (when the
+// optimizer state exists) is taken again from the uploaded values.
+int train_param_uploaded(nml_model* m, const void* param, size_t elems);
 
 }  // namespace nml

@@ -168,7 +168,36 @@ void param_ranges(const nml_model* m, size_t (&r)[2][2]) {
   r[1][1] = total;
 }
 
+// The AdamW state: zero first and second moments and, for fp16 models, float32 masters
+// taken from the parameters (optimizers/adam.py:64-81), allocated once.
+int ensure_adam(nml_model* m) {
+  NML_TRY(ensure_train(m));
+  TrainState* t = m->train;
+  hipStream_t st = nml::stream();
+  const size_t fb = f32_bytes(m);
+  if (!t->moments.p) {
+    NML_TRY(t->moments.ensure(2 * fb));
+    NML_HIP(hipMemsetAsync(t->moments.p, 0, 2 * fb, st));
+  }
+  if (m->dt == F16 && !t->masters.p) {
+    NML_TRY(t->masters.ensure(fb));
+    NML_TRY(launch_convert(F16, m->arena, F32, t->masters.p, m->arena_bytes / m->es, st));
+  }
+  return 0;
+}
+
+// What AdamW updates: the float32 parameters themselves, or the fp16 models' masters.
+float* master_base(nml_model* m) {
+  return static_cast<float*>(m->dt == F16 ? m->train->masters.p : m->arena);
+}
+
 }  // namespace
+
+int train_param_uploaded(nml_model* m, const void* param, size_t elems) {
+  if (m->dt != F16 || !m->train || !m->train->masters.p) return 0;
+  return launch_convert(F16, param, F32, static_cast<char*>(m->train->masters.p) + f32_off(m, param),
+                        elems, nml::stream());
+}
 
 }  // namespace nml
 
@@ -397,39 +426,67 @@ int nml_model_backward(nml_model* m, double grad_scale) {
   return 0;
 }
 
+int nml_model_adam_state_init(nml_model* m) {
+  NML_TRY(check_ready(m));
+  return ensure_adam(m);
+}
+
 int nml_model_adamw_step(nml_model* m, float lr, float beta1, float beta2, float bias_corr1,
                          float bias_corr2, float eps, float weight_decay) {
   NML_TRY(check_ready(m));
-  NML_TRY(ensure_train(m));
+  NML_TRY(ensure_adam(m));
   TrainState* t = m->train;
   hipStream_t st = nml::stream();
-  const size_t fb = f32_bytes(m), n_all = m->arena_bytes / m->es;
-  if (!t->moments.p) {
-    NML_TRY(t->moments.ensure(2 * fb));
-    NML_HIP(hipMemsetAsync(t->moments.p, 0, 2 * fb, st));
-  }
-  // float32 parameters are updated in place; fp16 ones through float32 masters, taken from
-  // the parameters on the first step and rounded back after every step (adam.py:75-81,
-  // :238-245)
-  float* master = static_cast<float*>(m->arena);
-  if (m->dt == F16) {
-    if (!t->masters.p) {
-      NML_TRY(t->masters.ensure(fb));
-      NML_TRY(launch_convert(F16, m->arena, F32, t->masters.p, n_all, st));
-    }
-    master = static_cast<float*>(t->masters.p);
-  }
+  const size_t n_all = m->arena_bytes / m->es;
+  // float32 parameters are updated in place; fp16 ones through their float32 masters,
+  // the parameters rounded from the updated masters in the same pass (adam.py:238-245)
+  float* master = master_base(m);
   size_t ranges[2][2];
   param_ranges(m, ranges);
   float* g = static_cast<float*>(t->grads.p);
   float* mm = static_cast<float*>(t->moments.p);
   for (const auto& r : ranges) {
     if (r[1] <= r[0]) continue;
-    // (fp16 models: the parameters rounded from the updated masters in the same pass)
     NML_TRY(launch_adamw(master + r[0], g + r[0], mm + r[0], mm + n_all + r[0], r[1] - r[0], lr,
                          beta1, beta2, bias_corr1, bias_corr2, eps, weight_decay, st,
                          m->dt == F16 ? static_cast<char*>(m->arena) + r[0] * m->es : nullptr));
   }
+  return 0;
+}
+
+int nml_model_adamw_update(nml_model* m, int kind, int layer, size_t offset, size_t count,
+                           float lr, float beta1, float beta2, float bias_corr1, float bias_corr2,
+                           float eps, float weight_decay) {
+  NML_TRY(check_ready(m));
+  NML_REQUIRE(kind != NML_P_ROPE_COS && kind != NML_P_ROPE_SIN,
+              "rotary tables are buffers, not parameters: no optimizer step");
+  void** slot = param_slot(m, kind, layer);
+  NML_REQUIRE(slot != nullptr, "unknown parameter kind %d / layer %d", kind, layer);
+  NML_REQUIRE(offset <= param_elems(m, kind) && count <= param_elems(m, kind) - offset,
+              "adamw_update: elements [%zu, %zu) outside parameter kind %d (%zu elements)", offset,
+              offset + count, kind, param_elems(m, kind));
+  NML_REQUIRE(offset % 4 == 0, "adamw_update: offset %zu must be a multiple of 4", offset);
+  NML_TRY(ensure_adam(m));
+  TrainState* t = m->train;
+  const size_t n_all = m->arena_bytes / m->es;
+  const size_t e0 = f32_off(m, *slot) / 4 + offset;  // element index in the arena
+  float* mm = static_cast<float*>(t->moments.p);
+  return launch_adamw(master_base(m) + e0, static_cast<float*>(t->grads.p) + e0, mm + e0,
+                      mm + n_all + e0, count, lr, beta1, beta2, bias_corr1, bias_corr2, eps,
+                      weight_decay, nml::stream(),
+                      m->dt == F16 ? static_cast<char*>(m->arena) + e0 * m->es : nullptr);
+}
+
+int nml_model_adam_master(nml_model* m, int kind, int layer, void** master) {
+  NML_TRY(check_ready(m));
+  NML_REQUIRE(m->dt == F16, "float32 models keep no master copies (the parameters are updated)");
+  NML_REQUIRE(kind != NML_P_ROPE_COS && kind != NML_P_ROPE_SIN,
+              "rotary tables are buffers, not parameters: no master copy");
+  void** slot = param_slot(m, kind, layer);
+  NML_REQUIRE(slot != nullptr, "unknown parameter kind %d / layer %d", kind, layer);
+  NML_REQUIRE(m->train && m->train->masters.p,
+              "no optimizer state yet (call nml_model_adam_state_init)");
+  *master = static_cast<char*>(m->train->masters.p) + f32_off(m, *slot);
   return 0;
 }
 
@@ -439,7 +496,8 @@ int nml_model_adam_moments(nml_model* m, int kind, int layer, void** first, void
               "rotary tables are buffers, not parameters: no optimizer state");
   void** slot = param_slot(m, kind, layer);
   NML_REQUIRE(slot != nullptr, "unknown parameter kind %d / layer %d", kind, layer);
-  NML_REQUIRE(m->train && m->train->moments.p, "no optimizer state yet (call nml_model_adamw_step)");
+  NML_REQUIRE(m->train && m->train->moments.p,
+              "no optimizer state yet (call nml_model_adam_state_init or nml_model_adamw_step)");
   const size_t off = f32_off(m, *slot);
   *first = static_cast<char*>(m->train->moments.p) + off;
   *second = static_cast<char*>(m->train->moments.p) + f32_bytes(m) + off;

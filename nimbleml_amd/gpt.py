@@ -10,6 +10,7 @@ Q/K/V stacked — into one device allocation, re-uploaded after ``load``.
 from __future__ import annotations
 
 import ctypes as C
+import weakref
 
 import numpy as np
 
@@ -19,6 +20,9 @@ from nimbleml_amd.grad_mode import is_grad_enabled
 from nimbleml_amd.layers import (Embedding, FusedGPTTrunk, FusedTransformerBlock, Module,
                                  RMSNorm, Sequential, block_device_arrays, rope_device_arrays)
 from nimbleml_amd.tensor import Tensor
+
+# Every live GPT, so that an optimizer given ``model.parameters()`` finds its model.
+_MODELS = weakref.WeakSet()
 
 
 def _ids_array(input_ids) -> np.ndarray:
@@ -96,6 +100,10 @@ class GPT(Module):
                        else Sequential(*block_modules))
         self._dtype = np.dtype(np_backend.dtype)
         self._dev = None
+        self._host_stale = False   # device parameters changed since the host Tensors
+        self._arena_grads = None   # (device model, {id(param): grad}) when they agree
+        self._adam_stash = None    # optimizer state kept across a device re-upload
+        _MODELS.add(self)
 
     # ------------------------------------------------------------------ params
     @property
@@ -113,7 +121,166 @@ class GPT(Module):
         return params
 
     def _invalidate_device(self):
-        self._dev = None  # re-upload on next use (the old handle is freed by __del__ below)
+        """The host parameters changed (``load``): re-upload them on next use. The AdamW state
+        of the old device copy (moments, fp16 masters) moves to the new one, as the
+        reference's optimizer keeps its state across a ``load``."""
+        self._stash_adam()
+        self._dev = None  # the old handle is freed by _DeviceModel.__del__
+        self._host_stale = False
+        self._arena_grads = None
+
+    # ---------------------------------------------------------- device layout
+    def _device_shape(self, kind):
+        d, f = self.d_model, self.ff_mult * self.d_model
+        return {N.P_TOKEN_EMB: (self.vocab_size, d), N.P_POS_EMB: (self.max_seq_len, d),
+                N.P_LN_F: (d,), N.P_LN1: (d,), N.P_LN2: (d,), N.P_WQKV: (3 * d, d),
+                N.P_BQKV: (3 * d,), N.P_WO: (d, d), N.P_BO: (d,), N.P_W1: (f, d), N.P_B1: (f,),
+                N.P_W2: (d, f), N.P_B2: (d,)}[kind]
+
+    def _param_layout(self):
+        """Where each parameter lives in the device layout: (Tensor, kind, layer, first row,
+        rows, transposed). Weights are stored (out, in), the reference's transpose; W_q,
+        W_k, W_v are the row blocks of the stacked (3d, d) weight, their biases the thirds
+        of the stacked bias."""
+        d = self.d_model
+        out = [(self.token_emb.weights, N.P_TOKEN_EMB, 0, 0, None, False)]
+        if self.pos_emb is not None:
+            out.append((self.pos_emb.weights, N.P_POS_EMB, 0, 0, None, False))
+        out.append((self.ln.gamma, N.P_LN_F, 0, 0, None, False))
+        for i, blk in enumerate(self._block_list):
+            m = blk.mha
+            out.append((blk.ln1.gamma, N.P_LN1, i, 0, None, False))
+            for j, dense in enumerate((m.W_q, m.W_k, m.W_v)):
+                out.append((dense.weights, N.P_WQKV, i, j * d, d, True))
+                out.append((dense.biases, N.P_BQKV, i, j * d, d, False))
+            out += [(m.W_o.weights, N.P_WO, i, 0, None, True),
+                    (m.W_o.biases, N.P_BO, i, 0, None, False),
+                    (blk.ln2.gamma, N.P_LN2, i, 0, None, False),
+                    (blk.ffn.dense1.weights, N.P_W1, i, 0, None, True),
+                    (blk.ffn.dense1.biases, N.P_B1, i, 0, None, False),
+                    (blk.ffn.dense2.weights, N.P_W2, i, 0, None, True),
+                    (blk.ffn.dense2.biases, N.P_B2, i, 0, None, False)]
+        return out
+
+    def _param_ranges(self):
+        """{id(param): (kind, layer, first element, elements)} in the device layout."""
+        out = {}
+        for t, kind, layer, r0, rows, _tr in self._param_layout():
+            shape = self._device_shape(kind)
+            row = int(np.prod(shape[1:], dtype=np.int64)) if len(shape) > 1 else 1
+            n = (rows if rows is not None else shape[0]) * row
+            out[id(t)] = (kind, layer, r0 * row, n)
+        return out
+
+    def _read_device(self, ptr_of, dtype, params=None):
+        """{id(param): array in the reference's layout} read from the device arrays that
+        ``ptr_of(kind, layer)`` points to (parameters, gradients, moments, masters)."""
+        want = None if params is None else {id(p) for p in params}
+        blocks, out = {}, {}
+        for t, kind, layer, r0, rows, tr in self._param_layout():
+            if want is not None and id(t) not in want:
+                continue
+            if (kind, layer) not in blocks:
+                a = np.empty(self._device_shape(kind), dtype=dtype)
+                N.check(N.lib.nml_memcpy_d2h(a.ctypes.data, ptr_of(kind, layer), a.nbytes))
+                blocks[(kind, layer)] = a
+            a = blocks[(kind, layer)]
+            v = a if rows is None else a[r0:r0 + rows]
+            out[id(t)] = np.ascontiguousarray(v.T if tr else v).reshape(t.shape)
+        return out
+
+    def _write_device(self, ptr_of, dtype, values):
+        """Write {id(param): array in the reference's layout} into the device arrays that
+        ``ptr_of(kind, layer)`` points to; rows of a stacked block without a value keep
+        theirs."""
+        groups = {}
+        for t, kind, layer, r0, rows, tr in self._param_layout():
+            if id(t) in values:
+                groups.setdefault((kind, layer), []).append((t, r0, rows, tr))
+        for (kind, layer), items in groups.items():
+            shape = self._device_shape(kind)
+            whole = len(items) == 1 and items[0][2] is None
+            a = np.empty(shape, dtype=dtype)
+            if not whole and sum(it[2] for it in items) != shape[0]:
+                N.check(N.lib.nml_memcpy_d2h(a.ctypes.data, ptr_of(kind, layer), a.nbytes))
+            for t, r0, rows, tr in items:
+                v = np.asarray(values[id(t)], dtype=dtype)
+                if tr:
+                    v = v.reshape(t.shape).T
+                tgt = a if rows is None else a[r0:r0 + rows]
+                tgt[...] = v.reshape(tgt.shape)
+            N.check(N.lib.nml_memcpy_h2d(ptr_of(kind, layer), a.ctypes.data, a.nbytes))
+
+    def _ptr(self, fn, kind, layer, which=0):
+        if fn is N.lib.nml_model_adam_moments:
+            a, b = C.c_void_p(), C.c_void_p()
+            N.check(fn(self._dev.handle, kind, layer, C.byref(a), C.byref(b)))
+            return (a, b)[which]
+        p = C.c_void_p()
+        N.check(fn(self._dev.handle, kind, layer, C.byref(p)))
+        return p
+
+    # ------------------------------------------------------------ host sync
+    def sync_to_host(self):
+        """Copy the device parameters into the host Tensors (after optimizer steps on the
+        device), in the reference's layouts, so ``save``, ``named_parameters`` and reads of
+        ``param.data`` see the trained values. A no-op when the host is current."""
+        if self._dev is None or not self._host_stale:
+            return self
+        vals = self._read_device(lambda k, l: self._ptr(N.lib.nml_model_param_ptr, k, l),
+                                 self._dtype)
+        for t, *_ in self._param_layout():
+            t.data[...] = vals[id(t)].ravel()
+        self._host_stale = False
+        return self
+
+    def _push_grads(self, params):
+        """Put the host ``grad`` of ``params`` (zeros where it is None) into the device
+        gradient arena, unless the arena already holds exactly those arrays (one backward
+        since the gradients were cleared)."""
+        rec = self._arena_grads
+        if rec is not None and rec[0] is self._dev and all(
+                p.grad is rec[1].get(id(p)) for p in params):
+            return
+        vals = {id(p): (p.grad if p.grad is not None else np.zeros(p.size, np.float32))
+                for p in params}
+        self._write_device(lambda k, l: self._ptr(N.lib.nml_model_grad_ptr, k, l), np.float32,
+                           vals)
+        self._arena_grads = None
+
+    # ------------------------------------------------------ optimizer state
+    def _adam_pointers(self, which):
+        if which == "master":
+            return lambda k, l: self._ptr(N.lib.nml_model_adam_master, k, l)
+        i = 0 if which == "m" else 1
+        return lambda k, l: self._ptr(N.lib.nml_model_adam_moments, k, l, i)
+
+    def _adam_read(self, which, params=None):
+        return self._read_device(self._adam_pointers(which), np.float32, params)
+
+    def _adam_write(self, which, values):
+        self._write_device(self._adam_pointers(which), np.float32, values)
+
+    def _stash_adam(self):
+        if self._dev is None or not getattr(self._dev, "adam", False):
+            return
+        st = {w: self._adam_read(w) for w in ("m", "v")}
+        if self._dtype == np.float16:
+            st["master"] = self._adam_read("master")
+        self._adam_stash = st
+
+    def _adam_state_ready(self):
+        """Allocate the device AdamW state (restoring one carried over a re-upload)."""
+        h = self._device_model()
+        if getattr(self._dev, "adam", False):
+            return h
+        N.check(N.lib.nml_model_adam_state_init(h))
+        self._dev.adam = True
+        if self._adam_stash is not None:
+            for which, vals in self._adam_stash.items():
+                self._adam_write(which, vals)
+            self._adam_stash = None
+        return h
 
     def _device_arrays(self):
         """(kind, layer, host array in device layout) for every device parameter."""
@@ -145,8 +312,10 @@ class GPT(Module):
         return self._dev.handle
 
     def to_device(self):
-        """Upload (again) the current host parameters."""
-        self._dev = None
+        """Upload (again) the current host parameters (after changing them in place). The
+        device optimizer state carries over. Parameters trained on the device and not yet
+        copied back (``sync_to_host``) are replaced by the host values."""
+        self._invalidate_device()
         self._device_model()
         return self
 
@@ -263,36 +432,22 @@ class GPT(Module):
 
     def _grad_array(self, kind, layer, shape):
         """Device gradient of parameter (kind, layer) as a host float32 array."""
-        ptr = C.c_void_p()
-        N.check(N.lib.nml_model_grad_ptr(self._dev.handle, kind, layer, C.byref(ptr)))
         out = np.empty(shape, dtype=np.float32)
-        N.check(N.lib.nml_memcpy_d2h(out.ctypes.data, ptr, out.nbytes))
+        N.check(N.lib.nml_memcpy_d2h(out.ctypes.data, self._ptr(N.lib.nml_model_grad_ptr, kind,
+                                                                 layer), out.nbytes))
         return out
 
     def _pull_grads(self):
         """Add the device gradients of one backward to the parameters' ``grad``, in the
         reference layouts ((in, out) weights, Q/K/V split)."""
-        d, f = self.d_model, self.ff_mult * self.d_model
-        g = self._grad_array
-        self.token_emb.weights._accumulate_grad(g(N.P_TOKEN_EMB, 0, (self.vocab_size, d)))
-        if self.pos_emb is not None:
-            self.pos_emb.weights._accumulate_grad(g(N.P_POS_EMB, 0, (self.max_seq_len, d)))
-        self.ln.gamma._accumulate_grad(g(N.P_LN_F, 0, (d,)))
-        for i, blk in enumerate(self._block_list):
-            m = blk.mha
-            wqkv = g(N.P_WQKV, i, (3 * d, d))
-            bqkv = g(N.P_BQKV, i, (3 * d,))
-            for j, dense in enumerate((m.W_q, m.W_k, m.W_v)):
-                dense.weights._accumulate_grad(wqkv[j * d:(j + 1) * d].T)
-                dense.biases._accumulate_grad(bqkv[j * d:(j + 1) * d])
-            m.W_o.weights._accumulate_grad(g(N.P_WO, i, (d, d)).T)
-            m.W_o.biases._accumulate_grad(g(N.P_BO, i, (d,)))
-            blk.ln1.gamma._accumulate_grad(g(N.P_LN1, i, (d,)))
-            blk.ln2.gamma._accumulate_grad(g(N.P_LN2, i, (d,)))
-            blk.ffn.dense1.weights._accumulate_grad(g(N.P_W1, i, (f, d)).T)
-            blk.ffn.dense1.biases._accumulate_grad(g(N.P_B1, i, (f,)))
-            blk.ffn.dense2.weights._accumulate_grad(g(N.P_W2, i, (d, f)).T)
-            blk.ffn.dense2.biases._accumulate_grad(g(N.P_B2, i, (d,)))
+        params = [t for t, *_ in self._param_layout()]
+        fresh = all(p.grad is None for p in params)
+        g = self._read_device(lambda k, l: self._ptr(N.lib.nml_model_grad_ptr, k, l), np.float32)
+        for p in params:
+            p._accumulate_grad(g[id(p)])
+        # the arena equals the host gradients when each was empty before and is float32
+        self._arena_grads = (self._dev, {id(p): p.grad for p in params}) if fresh and all(
+            p.grad.dtype == np.float32 for p in params) else None
 
     @classmethod
     def from_arrays(cls, arrays, vocab_size, d_model, num_heads, num_layers, max_seq_len,
@@ -344,6 +499,7 @@ class _DeviceModel:
                                        model.ff_mult * model.d_model,
                                        N.np_dtype_code(model._dtype), C.byref(h)))
         self.handle = h
+        self.adam = False  # AdamW state allocated on the device
         try:
             for kind, layer, arr in model._device_arrays():
                 N.check(N.lib.nml_model_set_param(h, kind, layer, arr.ctypes.data, arr.nbytes))
