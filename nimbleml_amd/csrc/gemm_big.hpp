@@ -77,11 +77,14 @@ struct Lgkm<2, 1> {
   }
 };
 
-// acc[i][j] += Σ_k A[row a_i][k] · B[row b_j][k] over k in [k0, k0 + S·kK), for this
-// wave's 32×32 tiles at rows m0 + (wave / 4)·TM/2 + 32i and columns n0 + (wave % 4)·TN/4
-// + 32j. Rows past M or N read row M-1 / N-1 (the caller stores none of them); the k
-// range must lie inside both operands. S ≥ 1.
-template <int TM, int TN>
+// acc[i][j] += Σ_k A[row a_i][k] · B[row b_j][k] over k in [k0, k0 + S·kK) (transposed
+// when TR), for this wave's 32×32 tiles at rows m0 + (wave / 4)·TM/2 + 32i and columns
+// n0 + (wave % 4)·TN/4 + 32j. Rows past M or N read row M-1 / N-1 (the caller stores
+// none of them); the k range must lie inside both operands. S ≥ 1.
+// TR: the accumulators hold the transposed tiles, D[n][m] (the operands of each MFMA
+// swapped), so that in the D layout a lane holds one output row and runs of consecutive
+// columns.
+template <int TM, int TN, bool TR = false>
 __device__ __forceinline__ void mainloop(const half_t* __restrict__ A, long long lda,
                                          const half_t* __restrict__ B, long long ldb, int M, int N,
                                          int k0, int S, int m0, int n0, char* lds_raw,
@@ -152,7 +155,8 @@ __device__ __forceinline__ void mainloop(const half_t* __restrict__ A, long long
     for (int i = 0; i < IA; ++i)
 #pragma unroll
       for (int j = 0; j < JB; ++j)
-        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(fa[i], fb[j], acc[i][j], 0, 0, 0);
+        acc[i][j] = TR ? __builtin_amdgcn_mfma_f32_32x32x16_f16(fb[j], fa[i], acc[i][j], 0, 0, 0)
+                       : __builtin_amdgcn_mfma_f32_32x32x16_f16(fa[i], fb[j], acc[i][j], 0, 0, 0);
   };
   typedef Lgkm<IA, JB> W;
   issue(0);

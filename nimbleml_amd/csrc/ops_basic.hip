@@ -209,7 +209,7 @@ __global__ __launch_bounds__(256) void gelu_kernel(const T* __restrict__ x, T* _
         t = rnd<T>(t * v);
         t = rnd<T>(v + t);
         t = rnd<T>(k * t);
-        tanh_u[i] = rnd<T>(tanhf(t));
+        tanh_u[i] = rnd<T>(tanh_h(t));
       } else {
         const float x3 = v * v * v;
         tanh_u[i] = tanhf(0.7978845608028654f * (v + 0.044715f * x3));

@@ -160,6 +160,141 @@ __device__ __forceinline__ float bias_at(const LinearArgs& a, int n) {
   return static_cast<float>(static_cast<const half_t*>(a.bias)[n < a.N ? n : a.N - 1]);
 }
 
+typedef _Float16 half4v __attribute__((ext_vector_type(4)));
+
+// Epilogue of the big GEMM's block tile, fp16, from transposed accumulators
+// (big::mainloop with TR: lane l holds row 32i + l%32 of its wave's block and, in
+// accumulator r = 4g + q of tile (i, j), column 32j + 8g + 4(l/32) + q). Each wave rounds
+// its (TM/2) × (TN/4) block to fp16 — the first rounding of every epilogue, so nothing is
+// lost — into its own region of the LDS the main loop no longer needs, as 8-byte runs,
+// then reads the region back as runs of 8 consecutive columns of one row and finishes
+// each run with epilogue_with's arithmetic: the residual and bias loads and the output
+// stores are 16-byte vectors, 8 rows × 128 bytes per wave instruction, instead of 2-byte
+// elements. Widths that are not a multiple of 8 (or operands not 16-byte aligned) take
+// the same path element by element.
+template <int TM, int TN>
+struct Staged {
+  static constexpr int R = TM / 2, C = TN / 4, P = C + 8;  // region rows, columns, pitch
+  static constexpr size_t Lds = static_cast<size_t>(8) * R * P * sizeof(half_t);
+};
+
+template <int EPI>
+__device__ __forceinline__ void epilogue_run8(const LinearArgs& a, int m, int n, half8 h, bool vec) {
+  const int N = a.N;
+  if constexpr (EPI == EPI_QKV) {
+    const QKVDst& q = a.qkv;
+    int b, s;
+    if (q.row_seg) {
+      const int rs = q.row_seg[m];
+      b = rs >> 16;
+      s = rs & 0xffff;
+    } else {
+      b = m / q.S;
+      s = m - b * q.S;
+    }
+    const int which = n / q.d, within = n - which * q.d;
+    const int hd = within / q.dk, j = within - hd * q.dk;
+    half_t* dst = which == 0
+        ? static_cast<half_t*>(q.q) + ((static_cast<size_t>(b) * q.H + hd) * q.S + s) * q.dk + j
+        : static_cast<half_t*>(which == 1 ? q.k : q.v) + b * q.kv_stride_b + hd * q.kv_stride_h +
+              static_cast<long long>((q.pos_base ? q.pos_base[b] : 0) + s) * q.dk + j;
+    const half_t* bias = static_cast<const half_t*>(a.bias) + n;
+    half8 bv;
+    if (vec) {
+      bv = *reinterpret_cast<const half8*>(bias);
+    } else {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) bv[e] = bias[e];  // a run of 8 stays inside one head
+    }
+    const half8 o = h + bv;  // fp16 adds round as rnd(float + float) does
+    if (vec) {
+      *reinterpret_cast<half8*>(dst) = o;
+    } else {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) dst[e] = o[e];
+    }
+    return;
+  }
+  const size_t row = static_cast<size_t>(m) * N;
+  half_t* out = static_cast<half_t*>(a.out) + row;
+  half8 bv = {0, 0, 0, 0, 0, 0, 0, 0}, rv = bv;
+  if (vec) {
+    if constexpr (EPI != EPI_NONE) bv = *reinterpret_cast<const half8*>(static_cast<const half_t*>(a.bias) + n);
+    if constexpr (EPI == EPI_BIAS_RESID)
+      rv = *reinterpret_cast<const half8*>(static_cast<const half_t*>(a.resid) + row + n);
+  } else {
+#pragma unroll
+    for (int e = 0; e < 8; ++e)
+      if (n + e < N) {
+        if constexpr (EPI != EPI_NONE) bv[e] = static_cast<const half_t*>(a.bias)[n + e];
+        if constexpr (EPI == EPI_BIAS_RESID) rv[e] = static_cast<const half_t*>(a.resid)[row + n + e];
+      }
+  }
+  // fp16 arithmetic on the 8 values at once (an fp16 sum rounds as rnd(float + float)
+  // does): lin = rnd(rnd(acc) + b), then the epilogue's own op
+  half8 o = h, p = h;
+  if constexpr (EPI != EPI_NONE) {
+    p = h + bv;
+    if constexpr (EPI == EPI_BIAS) o = p;
+    else if constexpr (EPI == EPI_BIAS_GELU) o = gelu8_f16(p);
+    else o = rv + p;  // EPI_BIAS_RESID
+  }
+  half_t* pre = EPI == EPI_BIAS_GELU && a.pre_out ? static_cast<half_t*>(a.pre_out) + row : nullptr;
+  if (vec) {
+    *reinterpret_cast<half8*>(out + n) = o;
+    if (pre) *reinterpret_cast<half8*>(pre + n) = p;
+  } else {
+#pragma unroll
+    for (int e = 0; e < 8; ++e)
+      if (n + e < N) {
+        out[n + e] = o[e];
+        if (pre) pre[n + e] = p[e];
+      }
+  }
+}
+
+template <int EPI, int TM, int TN>
+__device__ __forceinline__ void epilogue_staged(const LinearArgs& a, int m0, int n0,
+                                                const floatx16 (&acc)[TM / 64][TN / 128],
+                                                char* lds_raw) {
+  typedef Staged<TM, TN> St;
+  constexpr int IA = TM / 64, JB = TN / 128, R = St::R, C = St::C, P = St::P;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) >> 6);
+  const int wm = wave >> 2, wn = wave & 3;
+  half_t* reg = reinterpret_cast<half_t*>(lds_raw) + wave * R * P;
+  __syncthreads();  // every wave is done with the main loop's stages
+#pragma unroll
+  for (int i = 0; i < IA; ++i)
+#pragma unroll
+    for (int j = 0; j < JB; ++j)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        half4v v;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) v[q] = static_cast<half_t>(acc[i][j][4 * g + q]);
+        *reinterpret_cast<half4v*>(reg + (32 * i + (lane & 31)) * P + 32 * j + 8 * g + 4 * (lane >> 5)) = v;
+      }
+  // (the wave reads back only its own region: its LDS operations complete in order)
+  const int M = a.M, N = a.N;
+  uintptr_t ptrs = reinterpret_cast<uintptr_t>(a.out) | reinterpret_cast<uintptr_t>(a.bias) |
+                   reinterpret_cast<uintptr_t>(a.resid) | reinterpret_cast<uintptr_t>(a.pre_out);
+  if constexpr (EPI == EPI_QKV)
+    ptrs |= reinterpret_cast<uintptr_t>(a.qkv.q) | reinterpret_cast<uintptr_t>(a.qkv.k) |
+            reinterpret_cast<uintptr_t>(a.qkv.v);
+  const bool aligned = (ptrs & 15) == 0;
+  const bool vec8 = (N & 7) == 0 && aligned;
+  constexpr int CH = C / 8;              // 16-byte runs per region row
+  constexpr int IT = R * CH / 64;        // runs per lane
+#pragma unroll
+  for (int it = 0; it < IT; ++it) {
+    const int id = it * 64 + lane, row = id / CH, c8 = id - row * CH;
+    const int m = m0 + wm * R + row, n = n0 + wn * C + c8 * 8;
+    const half8 h = *reinterpret_cast<const half8*>(reg + row * P + c8 * 8);
+    if (m < M && n < N) epilogue_run8<EPI>(a, m, n, h, vec8 && n + 7 < N);
+  }
+}
+
 constexpr int kBM = 128, kBN = 128;
 
 // ---------------------------------------------------------------- fp16 MFMA GEMM
@@ -281,36 +416,18 @@ __global__ __launch_bounds__(kHT, TM == 256 ? 1 : 4) void gemm_f16_big_kernel(Li
     for (int j = 0; j < JB; ++j)
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
-  big::mainloop<TM, TN>(static_cast<const half_t*>(a.x), a.lda, static_cast<const half_t*>(a.w), a.K, a.M,
-                        a.N, 0, a.K / kHK, m0, n0, lds_raw, acc);
+  big::mainloop<TM, TN, true>(static_cast<const half_t*>(a.x), a.lda, static_cast<const half_t*>(a.w), a.K,
+                              a.M, a.N, 0, a.K / kHK, m0, n0, lds_raw, acc);
 
-  // D layout of a 32×32 MFMA tile: lane l, register r → row 8(r/4) + 4(l/32) + r%4, col l%32.
-  // Written out: a loop here is not always unrolled, and acc must stay in registers.
-  const int na = n0 + wn * (TN / 4) + (lane & 31);
-  const float ba = bias_at<EPI>(a, na);
-  const int mb = m0 + wm * (TM / 2) + 4 * (lane >> 5);
-  if constexpr (TM == 256 && TN == 256) {
-    const int nb = na + 32;
-    const float bb = bias_at<EPI>(a, nb);
-    epilogue_tile32<EPI>(a, mb, na, acc[0][0], ba);
-    epilogue_tile32<EPI>(a, mb, nb, acc[0][1], bb);
-    epilogue_tile32<EPI>(a, mb + 32, na, acc[1][0], ba);
-    epilogue_tile32<EPI>(a, mb + 32, nb, acc[1][1], bb);
-    epilogue_tile32<EPI>(a, mb + 64, na, acc[2][0], ba);
-    epilogue_tile32<EPI>(a, mb + 64, nb, acc[2][1], bb);
-    epilogue_tile32<EPI>(a, mb + 96, na, acc[3][0], ba);
-    epilogue_tile32<EPI>(a, mb + 96, nb, acc[3][1], bb);
-  } else {
-    static_assert(TM == 128 && TN == 128, "tile");
-    epilogue_tile32<EPI>(a, mb, na, acc[0][0], ba);
-    epilogue_tile32<EPI>(a, mb + 32, na, acc[1][0], ba);
-  }
+  epilogue_staged<EPI, TM, TN>(a, m0, n0, acc, lds_raw);
 }
 
 template <int EPI, int GM, int TM, int TN>
 int gemm_big_launch_gm(const LinearArgs& a, hipStream_t st) {
   static bool attr = false;
-  constexpr size_t lds = big::Shape<TM, TN>::Lds;  // 128 KiB (256 × 256) or 64 KiB (128 × 128)
+  // main loop: 128 KiB (256 × 256) or 64 KiB (128 × 128); epilogue: 144 KiB or 36 KiB
+  constexpr size_t lds = big::Shape<TM, TN>::Lds > Staged<TM, TN>::Lds ? big::Shape<TM, TN>::Lds
+                                                                       : Staged<TM, TN>::Lds;
   if (!attr) {
     NML_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(&gemm_f16_big_kernel<EPI, GM, TM, TN>),
                                 hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds)));

@@ -76,7 +76,7 @@ __device__ __forceinline__ float gelu_grad_f16_factor(float x) {
   t = rnd<half_t>(t * x);
   t = rnd<half_t>(x + t);
   t = rnd<half_t>(k * t);
-  const float tu = rnd<half_t>(tanhf(t));
+  const float tu = rnd<half_t>(tanh_h(t));
   float du = rnd<half_t>(dc * x);
   du = rnd<half_t>(du * x);
   du = rnd<half_t>(1.0f + du);

@@ -50,6 +50,33 @@ def test_gelu_matches_reference_fixture(gpu, name):
     assert np.abs(np.asarray(tu) - want_tu).max() < (2e-3 if out.dtype == np.float16 else 1e-6)
 
 
+def test_gelu_fp16_every_input_bit_exact(gpu):
+    """The fp16 GELU on every finite fp16 input equals the reference's NumPy float16
+    evaluation (oracle gelu: each op rounded to fp16, kernels/fused_gelu.py:67-69) bit for
+    bit — the standalone kernel (and its tanh output) and the GEMM epilogue (x·I + 0 with
+    epilogue GELU, so the accumulator is the input exactly)."""
+    bits = np.arange(65536, dtype=np.uint32).astype(np.uint16)
+    x = bits.view(np.float16)
+    x = x[np.isfinite(x)]
+    with np.errstate(over="ignore", invalid="ignore"):
+        want = R.gelu(x)
+        t = R.GELU_K * (x + R.GELU_COEF * x * x * x)
+        want_tu = np.tanh(t)
+    out, tu = _k().fused_gelu_forward(x)
+    out, tu = np.asarray(out), np.asarray(tu)
+    same = lambda a, b: (a == b) | (np.isnan(a) & np.isnan(b))
+    bad = ~same(out, want)
+    print(f"standalone: {int(bad.sum())} of {x.size} differ")
+    assert not bad.any(), (x[bad][:8], out[bad][:8], want[bad][:8])
+    assert np.all(same(tu, want_tu.astype(np.float32)))
+    grid = x[: (x.size // 64) * 64].reshape(-1, 64)  # 992 × 64
+    eye = np.eye(64, dtype=np.float16)
+    got = np.asarray(_k().linear(grid, eye, np.zeros(64, np.float16), epilogue=2))
+    bad = ~same(got, want[: grid.size].reshape(grid.shape))
+    print(f"GEMM epilogue: {int(bad.sum())} of {grid.size} differ")
+    assert not bad.any()
+
+
 @pytest.mark.parametrize("name", ["ops_fp32", "ops_fp16"])
 def test_embedding_gather_bit_exact(gpu, name):
     f = golden(name)
@@ -279,12 +306,16 @@ def test_linear_skinny_fp16(gpu, rows, k, epi):
 
 @pytest.mark.parametrize("rows,k,n,epi", [(4096, 256, 4096, 0), (4096, 192, 4224, 1),
                                           (4096, 128, 4224, 2), (3000, 256, 4224, 3),
+                                          (4096, 128, 4099, 3), (4096, 64, 4097, 2),
                                           (1024, 192, 3072, 1), (700, 256, 1000, 3),
-                                          (300, 128, 520, 2), (515, 64, 136, 0)])
+                                          (300, 128, 520, 2), (515, 64, 136, 0),
+                                          (700, 64, 1001, 3), (600, 128, 1030, 1)])
 def test_linear_big_tile_fp16(gpu, rows, k, n, epi):
     """Prefill-sized shapes on the direct-to-LDS MFMA GEMM: 256×256 tiles where there are
-    ≥ 256 of them, 128×128 tiles below that (the last four shapes), with ragged last column
-    tiles (n = 4224, 1000, 520, 136) and ragged last row tiles (rows = 3000, 700, 300, 515)."""
+    ≥ 256 of them, 128×128 tiles below that (rows ≤ 1024), with ragged last column tiles
+    (n = 4224, 1000, 520, 136), ragged last row tiles (rows = 3000, 700, 300, 515), and
+    widths that are not multiples of 4 (4099, 4097, 1001, 1030: the epilogue's
+    element-by-element path instead of 8-byte runs)."""
     rng = np.random.default_rng(rows + k + n + epi)
     x = rng.standard_normal((rows, k)).astype(np.float16)
     w = (rng.standard_normal((k, n)) * (1.0 / np.sqrt(k))).astype(np.float16)
