@@ -442,10 +442,16 @@ class RaggedKVOracle:
 def sample_flip_tol(logits, u, token, *, temperature, top_k):
     """Largest ε such that changing every logit by at most ε provably cannot change
     ``token``, the pick of ``sample_logits(logits, temperature, top_k, top_p=1, u)`` (no
-    repetition penalty). Conservative: tokens within 2ε/T of the top-k threshold may leave or join
-    the kept set (their probability mass then shifts the CDF), and a CDF value c moves by
-    at most c(1 − c)(e^{2ε/T} − 1) when every logit/T moves by at most ε/T; the pick must
-    stay strictly inside its CDF interval under both. Greedy (temperature ≤ 0): half the top-2 gap."""
+    repetition penalty). With η = ε/T the bound on each scaled logit's move: a kept token
+    and a dropped one can trade places only if their scaled logits are within 2η, so the
+    top-k set can change only among tokens whose scaled logit lies in
+    [v_k − 2η, v_{k+1} + 2η] (v_k the k-th largest, v_{k+1} the next; no change at all
+    when v_k − v_{k+1} > 2η),
+    and their probability mass — kept or joining, each at most e^{2η} times its present
+    share — may then shift the CDF; every CDF value c also moves by at most
+    c(1 − c)(e^{2η} − 1) from the common rescaling. The pick must stay strictly inside its
+    CDF interval under both, and may not itself be one of the tokens that can leave.
+    Greedy (temperature ≤ 0): half the top-2 gap."""
     x = np.asarray(logits, dtype=np.float32).reshape(-1).astype(np.float64)
     if temperature <= 0:
         top2 = np.sort(x)[-2:]
@@ -455,7 +461,8 @@ def sample_flip_tol(logits, u, token, *, temperature, top_k):
     th = float(np.partition(xt, -k)[-k])
     keep = xt >= th
     p = np.exp((xt - xt[keep].max()).astype(np.float64)) * keep
-    p /= p.sum()
+    z = p.sum()
+    p /= z
     cdf = np.cumsum(p)
     j = int(token)
     lo = cdf[j - 1] if j > 0 else 0.0
@@ -463,16 +470,25 @@ def sample_flip_tol(logits, u, token, *, temperature, top_k):
     if not (lo <= u < hi):
         return 0.0
     xt64 = xt.astype(np.float64)
+    share = np.exp(xt64 - float(xt[keep].max())) / z  # present share of every token
+    srt = np.sort(xt64)[::-1]
+    vk = srt[k - 1]
+    vk1 = srt[k] if k < xt.size else -np.inf
 
     def robust(eps):
-        e = 2.0 * eps / float(temperature)
-        amb = np.abs(xt64 - th) <= e
-        if k < xt.size and amb[j]:
-            return False
-        mass = p[amb].sum() * np.exp(e) if k < xt.size else 0.0
+        e = 2.0 * eps / float(temperature)  # 2η
+        # the window, widened by the float32 roundings of the perturbed logits and of the
+        # division by T in the reference's sampler (a few ulps of the scaled logits)
+        w = e + 1e-6 * max(1.0, abs(vk))
+        mass = 0.0
+        if k < xt.size and vk - vk1 <= w:
+            amb = (xt64 >= vk - w) & (xt64 <= vk1 + w)
+            if amb[j]:
+                return False
+            mass = share[amb].sum() * np.exp(e)
 
-        def shift(c):  # |Δc| for a CDF value c when every logit/T moves by ≤ e/2
-            return c * (1.0 - c) * (np.exp(e) - 1.0) + mass
+        def shift(c):  # |Δc| for a CDF value c (+ float32 rounding of the probabilities)
+            return c * (1.0 - c) * (np.exp(e) - 1.0) + mass + 1e-6
 
         return (u - lo) > shift(lo) and (hi - u) > shift(hi)
 
