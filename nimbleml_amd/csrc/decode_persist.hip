@@ -278,53 +278,6 @@ __device__ __forceinline__ void gather_partials(const u64* src, int nch, uint32_
   }
 }
 
-__device__ __forceinline__ float block_sum4(float v, float* red) {
-  v = wave_sum_dpp(v);
-  __syncthreads();
-  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
-  __syncthreads();
-  return red[0] + red[1] + red[2] + red[3];
-}
-
-__device__ __forceinline__ float block_max4(float v, float* red) {
-  v = wave_max_dpp(v);
-  __syncthreads();
-  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
-  __syncthreads();
-  return fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
-}
-
-// RMSNorm of the D values in x (LDS) into y (LDS), kernels/fused_rmsnorm.py:153-162
-// (same arithmetic as rmsnorm_kernel). g_reg holds this thread's gamma entries.
-template <typename T, int D>
-__device__ __forceinline__ void rmsnorm_lds(const T* x, const float (&g_reg)[D / kT], T* y,
-                                            float* red) {
-#pragma clang fp contract(off)
-  float acc = 0.f;
-#pragma unroll
-  for (int j = 0; j < D / kT; ++j) {
-    const float v = static_cast<float>(x[threadIdx.x + j * kT]);
-    acc += rnd<T>(v * v);
-  }
-  const float m = block_sum4(acc, red) / static_cast<float>(D);
-  const float r = sqrtf(m + 1e-5f);
-  if constexpr (sizeof(T) == 2) {
-    const float inv = rnd<T>(1.0f / r);
-#pragma unroll
-    for (int j = 0; j < D / kT; ++j) {
-      const int i = threadIdx.x + j * kT;
-      y[i] = static_cast<T>(rnd<T>(static_cast<float>(x[i]) * inv) * g_reg[j]);
-    }
-  } else {
-#pragma unroll
-    for (int j = 0; j < D / kT; ++j) {
-      const int i = threadIdx.x + j * kT;
-      y[i] = static_cast<T>((static_cast<float>(x[i]) / r) * g_reg[j]);
-    }
-  }
-  __syncthreads();
-}
-
 // This lane's slice of a K-long row: 16-byte pieces (j·64 + lane)·VEC, j < K/(64·VEC).
 template <typename T, int K>
 struct RowSlice {
@@ -355,6 +308,58 @@ __device__ __forceinline__ float dot_slice(const RowSlice<T, K>& s, const T* x) 
 #pragma unroll
     for (int e = 0; e < VEC; ++e) acc += static_cast<float>(s.v[j][e]) * static_cast<float>(xv[e]);
   }
+  return acc;
+}
+
+// RMSNorm of the D values in x (LDS), as this lane's slice of the result: lane l of
+// every wave holds elements (j·64 + l)·VEC + e, the slice dot_slice multiplies. Each
+// wave covers all D elements, so it sums the squares itself (no barrier, no LDS round
+// trip) and normalises only what its rows need; g is the same slice of the gain.
+// Element arithmetic of kernels/fused_rmsnorm.py:153-162 (fp16: `inv` rounded to fp16)
+// and :159-161 (fp32).
+template <typename T, int D>
+__device__ __forceinline__ void rmsnorm_slice(const T* x, const RowSlice<T, D>& g, RowSlice<T, D>& y) {
+#pragma clang fp contract(off)
+  const int lane = threadIdx.x & 63;
+  constexpr int VEC = RowSlice<T, D>::VEC, J = RowSlice<T, D>::J;
+  typename V16<T>::type xv[J];
+  float acc = 0.f;
+#pragma unroll
+  for (int j = 0; j < J; ++j) {
+    xv[j] = *reinterpret_cast<const typename V16<T>::type*>(x + (j * 64 + lane) * VEC);
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) {
+      const float v = static_cast<float>(xv[j][e]);
+      acc += rnd<T>(v * v);
+    }
+  }
+  const float m = wave_sum_dpp(acc) / static_cast<float>(D);
+  const float r = sqrtf(m + 1e-5f);
+  if constexpr (sizeof(T) == 2) {
+    const float inv = rnd<T>(1.0f / r);
+#pragma unroll
+    for (int j = 0; j < J; ++j)
+#pragma unroll
+      for (int e = 0; e < VEC; ++e)
+        y.v[j][e] = static_cast<T>(rnd<T>(static_cast<float>(xv[j][e]) * inv) * static_cast<float>(g.v[j][e]));
+  } else {
+#pragma unroll
+    for (int j = 0; j < J; ++j)
+#pragma unroll
+      for (int e = 0; e < VEC; ++e)
+        y.v[j][e] = static_cast<T>((static_cast<float>(xv[j][e]) / r) * static_cast<float>(g.v[j][e]));
+  }
+}
+
+// Lane-partial dot product of two row slices (the order of dot_slice); not reduced.
+template <typename T, int K>
+__device__ __forceinline__ float dot_regs(const RowSlice<T, K>& w, const RowSlice<T, K>& y) {
+  float acc = 0.f;
+#pragma unroll
+  for (int j = 0; j < RowSlice<T, K>::J; ++j)
+#pragma unroll
+    for (int e = 0; e < RowSlice<T, K>::VEC; ++e)
+      acc += static_cast<float>(w.v[j][e]) * static_cast<float>(y.v[j][e]);
   return acc;
 }
 
@@ -419,7 +424,7 @@ __global__ __launch_bounds__(kT) void decode_persist_kernel(PersistArgs a) {
   __shared__ __attribute__((aligned(16))) T s_xn[D];  // normalised x, or attention output
   __shared__ __attribute__((aligned(16))) T s_xm[D];  // x_mid
   __shared__ __attribute__((aligned(16))) T s_h[F];   // FFN hidden
-  __shared__ float s_q[DK], s_kn[DK], s_vn[DK], s_p[kChunk];
+  __shared__ float s_q[DK], s_kn[DK], s_vn[DK];
   __shared__ float s_o[NKS][DK + 1];
   __shared__ float s_part[NPART * kT];
   __shared__ float s_red[8];
@@ -473,7 +478,7 @@ __global__ __launch_bounds__(kT) void decode_persist_kernel(PersistArgs a) {
 
   for (int l = 0; l < a.L; ++l) {
     const uint32_t tg = base + 8u * l;
-    const int mk = 4 + 10 * l;
+    const int mk = 4 + kMarks * l;
     // ------------------------------------------------------------------ P1
     {
       const T* W = layer_ptr<T>(a.wqkv, l, LB);
@@ -491,22 +496,19 @@ __global__ __launch_bounds__(kT) void decode_persist_kernel(PersistArgs a) {
         load_row<T, D>(W, rs.row[i], w[i]);
         braw[i] = Bq[rs.row[i]];
       }
-      T graw[D / kT];
-#pragma unroll
-      for (int j = 0; j < D / kT; ++j) graw[j] = G1[tid + j * kT];
+      RowSlice<T, D> gsl;
+      load_row<T, D>(G1, 0, gsl);
       NML_MARK(mk + 0);
       if (l > 0) {
         gather_lines<T, kG, R_W2, 1, SL::SX>(X, tg, s_x, err, bad);
         __syncthreads();
       }
       NML_MARK(mk + 1);
-      float gam[D / kT];
-#pragma unroll
-      for (int j = 0; j < D / kT; ++j) gam[j] = static_cast<float>(graw[j]);
-      rmsnorm_lds<T, D>(s_x, gam, s_xn, s_red);
+      RowSlice<T, D> y;
+      rmsnorm_slice<T, D>(s_x, gsl, y);
 #pragma unroll
       for (int i = 0; i < RW_QKV; ++i) {
-        const float acc = wave_sum_dpp(dot_slice<T, D>(w[i], s_xn));
+        const float acc = wave_sum_dpp(dot_regs<T, D>(w[i], y));
         if (lane == 0 && rs.live[i]) {
           const float lin = rnd<T>(rnd<T>(acc) + static_cast<float>(braw[i]));
           const int r = rs.row[i];
@@ -540,10 +542,11 @@ __global__ __launch_bounds__(kT) void decode_persist_kernel(PersistArgs a) {
         Raw8<T> vr[KPT];
 #pragma unroll
         for (int i = 0; i < KPT; ++i) {
-          const int vk = k0 + ks + i * NKS;
+          const int vk = k0 + 16 * wave + (lane >> 3) + 8 * i;
           load8<T>(Vc + static_cast<long long>(vk < len ? vk : len - 1) * DK + dg * 8, vr[i]);
         }
         if (first) {  // q, and k/v of the new position for the workgroup that owns it
+          NML_MARK(mk + 14);
           int idx[1];
           uint32_t pv[1];
           const int part = tid / DK, j = tid % DK;  // tid = row within the head's 3·DK
@@ -566,19 +569,19 @@ __global__ __launch_bounds__(kT) void decode_persist_kernel(PersistArgs a) {
           for (int e = 0; e < DPT; ++e) dot += s_q[qq * DPT + e] * at8<T>(kr[e / 8], e % 8);
         }
         dot = quad_sum_dpp(dot);
+        // Each wave takes the softmax of its own 16 keys against its own maximum; the
+        // waves' (max, sum, P·V) are combined after one barrier below.
         const float sc = kvalid ? rnd<T>(rnd<T>(dot) / scale_t) : -INFINITY;
-        const float mc = block_max4(sc, s_red);
-        const float p = kvalid ? expf(sc - mc) : 0.f;
-        if (qq == 0) s_p[tid >> 2] = p;
-        const float lc = block_sum4(qq == 0 ? p : 0.f, s_red + 4);
-        // (block_sum4's barriers also publish s_p)
+        const float mw = wave_max_dpp(sc);
+        const float p = kvalid ? expf(sc - mw) : 0.f;
+        const float lw = wave_sum_dpp(qq == 0 ? p : 0.f);
         float o[8];
 #pragma unroll
         for (int e = 0; e < 8; ++e) o[e] = 0.f;
 #pragma unroll
         for (int i = 0; i < KPT; ++i) {
-          const int jj = ks + i * NKS, vk = k0 + jj;
-          const float pj = s_p[jj];
+          const int jj = (lane >> 3) + 8 * i, vk = k0 + 16 * wave + jj;  // key jj of the wave's 16
+          const float pj = __shfl(p, 4 * jj, 64);
           // Row `pos` of the cache may not be written yet in this step (and clamped
           // keys past len read it): those keys never touch the loaded values.
           if (vk == pos) {
@@ -591,15 +594,32 @@ __global__ __launch_bounds__(kT) void decode_persist_kernel(PersistArgs a) {
         }
 #pragma unroll
         for (int e = 0; e < 8; ++e) s_o[ks][dg * 8 + e] = o[e];
+        if (lane == 0) {
+          s_red[wave] = mw;
+          s_red[4 + wave] = lw;
+        }
         __syncthreads();
         u64* dst = PART + (static_cast<long long>(head) * kMaxCh + c) * SL::PCH;
-        if (tid < DK) {
-          float s = 0.f;
-          for (int k2 = 0; k2 < NKS; ++k2) s += s_o[k2][tid];
-          put(dst + 2 + tid, tg + 2, __float_as_uint(s));
-        } else if (tid == DK) {
-          put(dst, tg + 2, __float_as_uint(mc));
-          put(dst + 1, tg + 2, __float_as_uint(lc));
+        if (tid <= DK) {
+          const float M = fmaxf(fmaxf(s_red[0], s_red[1]), fmaxf(s_red[2], s_red[3]));
+          float f[4];
+#pragma unroll
+          for (int w2 = 0; w2 < 4; ++w2) f[w2] = s_red[w2] == -INFINITY ? 0.f : expf(s_red[w2] - M);
+          if (tid < DK) {
+            float s = 0.f;
+#pragma unroll
+            for (int w2 = 0; w2 < 4; ++w2) {
+              float sw = 0.f;
+#pragma unroll
+              for (int k2 = 0; k2 < NKS / 4; ++k2) sw += s_o[w2 * (NKS / 4) + k2][tid];
+              s += f[w2] * sw;
+            }
+            put(dst + 2 + tid, tg + 2, __float_as_uint(s));
+          } else {
+            const float L = (f[0] * s_red[4] + f[1] * s_red[5]) + (f[2] * s_red[6] + f[3] * s_red[7]);
+            put(dst, tg + 2, __float_as_uint(M));
+            put(dst + 1, tg + 2, __float_as_uint(L));
+          }
         }
         __syncthreads();
       }
@@ -610,15 +630,15 @@ __global__ __launch_bounds__(kT) void decode_persist_kernel(PersistArgs a) {
       gather_partials<DK, SL::PCH>(PART + static_cast<long long>(head) * kMaxCh * SL::PCH, nch,
                                    tg + 2, s_part, err, bad);
       __syncthreads();
-      if (tid < DK) {
-        float M = -INFINITY;
-        for (int c = 0; c < nch; ++c) M = fmaxf(M, s_part[c * (DK + 2)]);
-        float den = 0.f, num = 0.f;
-        for (int c = 0; c < nch; ++c) {
-          const float e = expf(s_part[c * (DK + 2)] - M);
-          den += e * s_part[c * (DK + 2) + 1];
-          num += e * s_part[c * (DK + 2) + 2 + tid];
-        }
+      if (tid < DK) {  // wave 0: lane c holds chunk c's (max, sum), lane d sums dim d
+        static_assert(kMaxCh <= 64, "one lane per chunk");
+        const bool has = lane < nch;
+        const float mcl = has ? s_part[lane * (DK + 2)] : -INFINITY;
+        const float M = wave_max_dpp(mcl);
+        const float ec = has ? expf(mcl - M) : 0.f;
+        const float den = wave_sum_dpp(has ? ec * s_part[lane * (DK + 2) + 1] : 0.f);
+        float num = 0.f;
+        for (int c = 0; c < nch; ++c) num += lane_f(ec, c) * s_part[c * (DK + 2) + 2 + tid];
         const float o = num * (1.f / den);
         const float o1 = __shfl_xor(o, 1, 64);  // dims 2k, 2k+1 share a slot
         if ((tid & 1) == 0) put_pair<T>(ATT + head * (DK / kPack<T>), tid, tg + 3, o, o1);
@@ -640,7 +660,7 @@ __global__ __launch_bounds__(kT) void decode_persist_kernel(PersistArgs a) {
         load_row<T, D>(W, rs.row[i], w[i]);
         braw[i] = Bo[rs.row[i]];
       }
-      __syncthreads();  // s_xn is reused for the attention output
+      NML_MARK(mk + 15);
       gather<T, D, kPack<T>>(ATT, tg + 3, s_xn, err, bad);
       __syncthreads();
       NML_MARK(mk + 6);
@@ -653,6 +673,7 @@ __global__ __launch_bounds__(kT) void decode_persist_kernel(PersistArgs a) {
               enc<T>(static_cast<float>(s_x[rs.row[i]]) + lin));
         }
       }
+      NML_MARK(mk + 10);
     }
     // ------------------------------------------------------------------ P4
     {
@@ -670,26 +691,25 @@ __global__ __launch_bounds__(kT) void decode_persist_kernel(PersistArgs a) {
         load_row<T, D>(W, rs.row[i], w[i]);
         braw[i] = B1[rs.row[i]];
       }
-      T graw[D / kT];
-#pragma unroll
-      for (int j = 0; j < D / kT; ++j) graw[j] = G2[tid + j * kT];
+      RowSlice<T, D> gsl;
+      load_row<T, D>(G2, 0, gsl);
+      NML_MARK(mk + 11);
       gather_lines<T, kG, R_WO, 1, SL::SX>(XM, tg + 4, s_xm, err, bad);
       __syncthreads();
       NML_MARK(mk + 7);
-      float gam[D / kT];
-#pragma unroll
-      for (int j = 0; j < D / kT; ++j) gam[j] = static_cast<float>(graw[j]);
-      rmsnorm_lds<T, D>(s_xm, gam, s_xn, s_red);
+      RowSlice<T, D> y;
+      rmsnorm_slice<T, D>(s_xm, gsl, y);
 #pragma unroll
       for (int i = 0; i < RW_W1; i += 2) {
         float v[2];
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
-          const float acc = wave_sum_dpp(dot_slice<T, D>(w[i + h], s_xn));
+          const float acc = wave_sum_dpp(dot_regs<T, D>(w[i + h], y));
           v[h] = gelu_t<T>(rnd<T>(rnd<T>(acc) + static_cast<float>(braw[i + h])));
         }
         if (lane == 0) put_pair<T>(HID + g * SL::SH, rs.row[i] - g * R_W1, tg + 5, v[0], v[1]);
       }
+      NML_MARK(mk + 12);
     }
     // ------------------------------------------------------------------ P5
     {
@@ -706,6 +726,7 @@ __global__ __launch_bounds__(kT) void decode_persist_kernel(PersistArgs a) {
         load_row<T, F>(W, rs.row[i], w[i]);
         braw[i] = B2[rs.row[i]];
       }
+      NML_MARK(mk + 13);
       gather_lines<T, kG, R_W1, kPack<T>, SL::SH>(HID, tg + 5, s_h, err, bad);
       __syncthreads();
       NML_MARK(mk + 8);
@@ -721,7 +742,7 @@ __global__ __launch_bounds__(kT) void decode_persist_kernel(PersistArgs a) {
       NML_MARK(mk + 9);
     }
   }
-  const int mh = 4 + 10 * a.L;
+  const int mh = 4 + kMarks * a.L;
 
   // ---------------------------------------------------------------- head
   const uint32_t tgh = base + 8u * a.L;
@@ -733,17 +754,14 @@ __global__ __launch_bounds__(kT) void decode_persist_kernel(PersistArgs a) {
   int rb = r0 + wave * HR;
 #pragma unroll
   for (int i = 0; i < HR; ++i) load_row<T, D>(E, rb + i < r1 ? rb + i : r0, cur[i]);
+  RowSlice<T, D> y;
   {
-    T graw[D / kT];
-#pragma unroll
-    for (int j = 0; j < D / kT; ++j) graw[j] = static_cast<const T*>(a.lnf)[tid + j * kT];
+    RowSlice<T, D> gsl;
+    load_row<T, D>(static_cast<const T*>(a.lnf), 0, gsl);
     gather_lines<T, kG, R_W2, 1, SL::SX>(X, tgh, s_x, err, bad);
     __syncthreads();
     NML_MARK(mh + 0);
-    float gam[D / kT];
-#pragma unroll
-    for (int j = 0; j < D / kT; ++j) gam[j] = static_cast<float>(graw[j]);
-    rmsnorm_lds<T, D>(s_x, gam, s_xn, s_red);
+    rmsnorm_slice<T, D>(s_x, gsl, y);
   }
   T* logits = static_cast<T*>(a.logits);
   float best = -INFINITY;
@@ -755,7 +773,7 @@ __global__ __launch_bounds__(kT) void decode_persist_kernel(PersistArgs a) {
     for (int i = 0; i < HR; ++i) load_row<T, D>(E, rn + i < r1 ? rn + i : r0, nxt[i]);
 #pragma unroll
     for (int i = 0; i < HR; ++i) {
-      const float acc = wave_sum_dpp(dot_slice<T, D>(cur[i], s_xn));
+      const float acc = wave_sum_dpp(dot_regs<T, D>(cur[i], y));
       const float v = rnd<T>(acc);
       if (rb + i < r1) {
         if (lane == 0) logits[rb + i] = static_cast<T>(v);

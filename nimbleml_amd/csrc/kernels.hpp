@@ -267,10 +267,13 @@ struct PersistArgs {
   unsigned long long* trace;
 };
 
-// Marks: 0 start, 1 embedded; layer l at 4 + 10·l + {0 P1 loads issued, 1 x in,
+// Marks: 0 start, 1 embedded; layer l at 4 + kMarks·l + {0 P1 loads issued, 1 x in,
 // 2 QKV out, 3 q in, 4 chunks out, 5 merged, 6 attention in, 7 x_mid in, 8 h in,
-// 9 x out}; head at 4 + 10·L + {0 x in, 1 logits out, 2 choice}.
-__host__ __device__ inline int persist_trace_stride(int L) { return 4 + 10 * L + 4; }
+// 9 x out, 10 x_mid out, 11 W1 loads issued, 12 h out, 13 W2 loads issued, 14 K/V
+// loads issued, 15 W_o loads issued}; head at 4 + kMarks·L + {0 x in, 1 logits out,
+// 2 choice}.
+constexpr int kMarks = 16;
+__host__ __device__ inline int persist_trace_stride(int L) { return 4 + kMarks * L + 4; }
 
 bool persist_supported(int dt, int d, int H, int F, int B, int P);
 size_t persist_slot_count(int d, int H);
