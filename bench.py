@@ -20,7 +20,10 @@ Two more lines of the same metric ride along (BASELINE.json "batch 1 & 32"):
   c5: d2048/L24/V50304 fp16, 4×4096 causal prefill + tied cross-entropy over all
       16384 positions (compute_loss), MFMA roofline (49.56 TFLOP algorithmic).
 `cpu_baseline` times the oracle (the reference algorithm restated: full re-forward per
-token, host sampling; fp32 because NumPy fp16 has no BLAS path) on a bounded sample.
+token, host sampling; fp32 because NumPy fp16 has no BLAS path) on a bounded sample:
+C3 tokens spread over the run's contexts; c4 and c5 carry their own (c4: a few rows at
+batch 1, as the reference runs ragged prompts; c5: one block and the head on one
+sequence, extrapolated).
 """
 from __future__ import annotations
 
@@ -71,17 +74,28 @@ def cpu_threads():
         return os.cpu_count() or 1
 
 
-def cpu_baseline(cfg, w16, prompt, tokens):
-    """Reference algorithm on the host (oracle): fp32, full re-forward per token."""
+def cpu_baseline(cfg, w16, prompt, n_new, samples):
+    """Reference algorithm on the host (oracle): fp32, full re-forward per token.
+
+    The reference's cost per generated token grows with the context, so the sample
+    spreads `samples` tokens evenly over the run's contexts prompt … prompt + n_new - 1
+    (each one generate step: a full forward over the context and the greedy choice) and
+    reports their mean rate, the rate of the whole run to within the sampling."""
     from oracle import gpt_ref as R
 
     w = {k: v.astype(np.float32) for k, v in w16.items()}
+    s0 = prompt.shape[1]
+    ctxs = np.linspace(s0, s0 + n_new - 1, samples).round().astype(int)
+    rng = np.random.default_rng(4)
+    ids = np.concatenate([prompt, rng.integers(0, cfg.vocab_size, (1, n_new), dtype=np.int64)], axis=1)
     t0 = time.perf_counter()
-    R.generate(w, prompt, cfg.num_heads, cfg.num_layers, max_new_tokens=tokens, temperature=0.0)
+    for c in ctxs:
+        R.generate(w, ids[:, :c], cfg.num_heads, cfg.num_layers, max_new_tokens=1, temperature=0.0)
     dt = time.perf_counter() - t0
-    return {"value": round(tokens / dt, 4), "unit": "tokens/s", "cores": int(cpu_threads()),
+    return {"value": round(len(ctxs) / dt, 4), "unit": "tokens/s", "cores": int(cpu_threads()),
             "kind": "port",
-            "sample": f"C3 shapes at fp32, batch 1, prompt {prompt.shape[1]}, {tokens} greedy tokens, "
+            "sample": f"C3 shapes at fp32, batch 1: {len(ctxs)} greedy tokens at contexts "
+                      f"{ctxs[0]}..{ctxs[-1]} evenly spread over the run's {s0}..{s0 + n_new - 1}, "
                       f"each a full re-forward as the reference does ({dt:.1f} s)"}
 
 
@@ -104,7 +118,32 @@ def bench_c3(nm, cfg, model, prompt, n, steps, warmup, use_graph):
     return elapsed, step_ms, bytes_avg, model.last_decode_persistent()
 
 
-def bench_c4(nm, cfg, model, use_graph, reps=2):
+def cpu_baseline_c4(cfg, w16, rows, new, samples=4):
+    """Reference algorithm on the host for a bounded sample of C4: the reference cannot
+    batch ragged prompts, so each row generates at batch 1 (full re-forward per token,
+    temperature 0.8, top-k 50); `samples` rows take one sampled token each at a context
+    spread over their own run, and the rate is that of one row after another."""
+    from oracle import gpt_ref as R
+
+    w = {k: v.astype(np.float32) for k, v in w16.items()}
+    rng = np.random.default_rng(6)
+    t0 = time.perf_counter()
+    for i in range(samples):
+        row = np.asarray(rows[i], dtype=np.int64)
+        extra = int(round(i * (new - 1) / max(1, samples - 1)))
+        ids = np.concatenate([row, rng.integers(0, cfg.vocab_size, extra)])[None, :]
+        u = np.random.RandomState(i).random_sample()  # the reference's legacy-RNG draw
+        R.generate(w, ids, cfg.num_heads, cfg.num_layers, max_new_tokens=1, temperature=0.8,
+                   top_k=50, top_p=1.0, uniforms=[[u]])
+    dt = time.perf_counter() - t0
+    return {"value": round(samples / dt, 4), "unit": "tokens/s", "cores": int(cpu_threads()),
+            "kind": "port",
+            "sample": f"C4 rows 0..{samples - 1} at fp32, batch 1 each (the reference cannot batch "
+                      f"ragged prompts), one sampled token per row at contexts spread over its "
+                      f"{new} steps, full re-forward per token ({dt:.1f} s)"}
+
+
+def bench_c4(nm, cfg, model, use_graph, reps=2, w16=None):
     rng = np.random.default_rng(5)
     lens = rng.integers(128, 1025, 32)
     rows = [rng.integers(0, cfg.vocab_size, int(n)) for n in lens]
@@ -126,7 +165,9 @@ def bench_c4(nm, cfg, model, use_graph, reps=2):
                    for s in range(1, new)]
     step_ms = float(np.mean(decode_ms))
     achieved = float(np.mean(bytes_steps)) / (step_ms * 1e-3) / 1e9
-    return {"workload": "C4: same model, batch 32, prompts U[128,1024], 256 sampled tokens each "
+    base = cpu_baseline_c4(cfg, w16, rows, new) if w16 is not None else None
+    return {**({"cpu_baseline": base} if base else {}),
+            "workload": "C4: same model, batch 32, prompts U[128,1024], 256 sampled tokens each "
                         "(T=0.8, top-k 50, top_p 1.0)",
             "value": round(32 * new / elapsed, 1), "unit": "tokens/s",
             "ms_per_generate": round(elapsed * 1e3, 2), "decode_ms_per_step": round(step_ms, 4),
@@ -217,17 +258,46 @@ def bench_train(nm, batch=4, seq=1024, steps=3, dtype=np.float32):
                          "unit": "TFLOP/s", "frac": round(tf / peak, 4), "flops": 3 * fwd}}
 
 
-def bench_c5(nm, reps=2):
+def cpu_baseline_c5(cfg, w16, ids, lab):
+    """Reference algorithm on the host (oracle, fp32: NumPy fp16 has no BLAS path) for a
+    bounded sample of C5: layer 0 of the first sequence (the reference's full (S, S)
+    scores), then the tied logits and cross-entropy of that sequence's 4096 positions;
+    the whole compute_loss is extrapolated as B·(L·block + head)."""
+    from oracle import gpt_ref as R
+
+    B, S = ids.shape
+    w = {k: w16[k].astype(np.float32) for k in w16 if k.startswith("blocks.layers.0.")}
+    w["token_emb.weights"] = w16["token_emb.weights"].astype(np.float32)
+    w["pos_emb.weights"] = w16["pos_emb.weights"].astype(np.float32)
+    w["ln.gamma"] = w16["ln.gamma"].astype(np.float32)
+    x = R.embed(w["token_emb.weights"], w["pos_emb.weights"], ids[:1])
+    mask = R.causal_mask(S, x.dtype)
+    t0 = time.perf_counter()
+    x = R.block(x, w, 0, cfg.num_heads, mask)
+    t1 = time.perf_counter()
+    h = R.rmsnorm(x.reshape(S, -1), w["ln.gamma"])
+    R.crossentropy(R._mm(h, np.swapaxes(w["token_emb.weights"], -2, -1)), lab[:1])
+    t2 = time.perf_counter()
+    total = B * (cfg.num_layers * (t1 - t0) + (t2 - t1))
+    return {"value": round(B * S / total, 2), "unit": "positions/s", "cores": int(cpu_threads()),
+            "kind": "port", "extrapolated": True,
+            "sample": f"C5 shapes at fp32: one block over one 4096-token sequence ({t1 - t0:.1f} s) "
+                      f"and its tied head + cross-entropy ({t2 - t1:.1f} s), extrapolated to "
+                      f"{B} sequences x {cfg.num_layers} layers ({total:.0f} s per compute_loss)"}
+
+
+def bench_c5(nm, reps=2, cpu=False):
     from oracle.weights import C5, make_weights, random_ids
 
     cfg = C5
     w = make_weights(cfg, seed=7, dtype=np.float16)
     model = nm.GPT.from_arrays(w, cfg.vocab_size, cfg.d_model, cfg.num_heads, cfg.num_layers,
                                cfg.max_seq_len, dtype=np.float16)
-    del w
-    model.to_device()
     ids = random_ids((4, 4096), cfg.vocab_size, seed=1)
     lab = random_ids((4, 4096), cfg.vocab_size, seed=2)
+    base = cpu_baseline_c5(cfg, w, ids, lab) if cpu else None
+    del w
+    model.to_device()
     from nimbleml_amd.grad_mode import no_grad
 
     with no_grad():  # the loss alone: no activations kept for a backward
@@ -245,7 +315,8 @@ def bench_c5(nm, reps=2):
             "loss": round(float(loss), 5),
             "roofline": {"bound": "mfma", "achieved": round(tf, 1), "peak": MFMA_F16_PEAK_TFLOPS,
                          "unit": "TFLOP/s", "frac": round(tf / MFMA_F16_PEAK_TFLOPS, 4),
-                         "flops": flops}}
+                         "flops": flops},
+            **({"cpu_baseline": base} if base else {})}
 
 
 def main():
@@ -260,7 +331,8 @@ def main():
     ap.add_argument("--only-c3", action="store_true", help="skip the batch-32 and prefill lines")
     ap.add_argument("--only", choices=["c3", "c4", "c5", "adamw", "train", "train16"], default=None,
                     help="run one workload only (for profiling); c4/c5 print their own line")
-    ap.add_argument("--cpu-tokens", type=int, default=12)
+    ap.add_argument("--cpu-samples", type=int, default=8,
+                    help="tokens of the CPU baseline, spread over the run's contexts")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only copy 256 MiB device to device three times (the known-size "
                          "reference for scaling the FETCH_SIZE / WRITE_SIZE counters)")
@@ -287,7 +359,7 @@ def main():
         print(json.dumps({"copy_calibration_bytes": nbytes, "copies": 3}), flush=True)
         return
     if args.only == "c5":
-        print(json.dumps({"c5": bench_c5(nm)}), flush=True)
+        print(json.dumps({"c5": bench_c5(nm, cpu=not args.no_cpu_baseline)}), flush=True)
         return
     if args.only == "adamw":
         print(json.dumps({"adamw": bench_adamw(nm)}), flush=True)
@@ -306,7 +378,8 @@ def main():
     n = args.new_tokens
     use_graph = not args.no_graph
     if args.only == "c4":
-        print(json.dumps({"c4": bench_c4(nm, cfg, model, use_graph)}), flush=True)
+        print(json.dumps({"c4": bench_c4(nm, cfg, model, use_graph,
+                                         w16=None if args.no_cpu_baseline else w16)}), flush=True)
         return
 
     elapsed, step_ms, bytes_avg, persistent = bench_c3(nm, cfg, model, prompt, n, args.steps,
@@ -339,13 +412,13 @@ def main():
                      "bytes_per_launch": round(bytes_avg)},
     }
     if not (args.only_c3 or args.only == "c3"):
-        result["c4"] = bench_c4(nm, cfg, model, use_graph)
+        result["c4"] = bench_c4(nm, cfg, model, use_graph, w16=None if args.no_cpu_baseline else w16)
         del model
-        result["c5"] = bench_c5(nm)
+        result["c5"] = bench_c5(nm, cpu=not args.no_cpu_baseline)
         result["train"] = bench_train(nm)
         result["train16"] = bench_train(nm, dtype=np.float16)
     if not args.no_cpu_baseline:
-        result["cpu_baseline"] = cpu_baseline(cfg, w16, prompt, args.cpu_tokens)
+        result["cpu_baseline"] = cpu_baseline(cfg, w16, prompt, args.new_tokens, args.cpu_samples)
     print(json.dumps(result), flush=True)
 
 
