@@ -18,6 +18,10 @@
 // come in descending index order, which is what reversing a stable ascending sort
 // gives (NumPy's default argsort is not stable, so the order of exact ties is
 // whatever its sort produced; descending index is the stable reading).
+// The sampled-decode case (fp16 rows, top-k ≤ 256 without top-p) first tries
+// sample_topk_regs: the row stays in registers, and the k-th largest is counted among
+// the few elements above a per-wave lower bound; the general path below runs when it
+// declines.
 #include "kernels.hpp"
 
 namespace nml {
@@ -46,6 +50,7 @@ struct Shared {
   int sel_bin_cnt;
   double sel_bin_mass;
   int found_index;
+  float reg_thr, reg_max;  // sample_topk_regs: the k-th largest s and the largest
 };
 
 __device__ float block_max_f(float v, Shared& sh) {
@@ -119,12 +124,12 @@ struct Row {
   bool use_pen;
   const uint32_t* bitmap;
 
-  // Penalised float32 logit (generate.py:34-37 then :9-20).
-  __device__ float base(int i) const {
-    float x = static_cast<float>(lg[i]);
+  // Penalised float32 logit (generate.py:34-37 then :9-20) of the value x at index i.
+  __device__ float penalised(float x, int i) const {
     if (use_pen && ((bitmap[i >> 5] >> (i & 31)) & 1u)) x = x < 0.f ? x * pen : x / pen;
     return x;
   }
+  __device__ float base(int i) const { return penalised(static_cast<float>(lg[i]), i); }
   // After temperature (generate.py:42): float32 division by float32(T).
   __device__ float scaled(int i) const { return base(i) / temperature; }
 };
@@ -248,6 +253,202 @@ __device__ int gather_candidates(const Row<T>& row, float lo, Shared& sh, int* c
   }
   __syncthreads();
   return n;
+}
+
+// Top-k sampling without top-p on fp16 logits held in registers (no LDS copy of the
+// row) — the sampled-decode case: 1 ≤ k ≤ kRegK, V a multiple of 8 up to 32·1024,
+// 16-byte aligned rows. Thread t holds elements 32t … 32t+31 as penalised float32
+// values y; the temperature-scaled value is s = y / T (float32 division), a
+// non-decreasing function of y, so every order question is answered on y and s is
+// formed only for the elements that can be kept. Every element below the k-th largest
+// s becomes -1e9, whose exp(x − max) is exactly 0, so only the elements ≥ it carry mass.
+//   1. A lower bound without a block-wide select: each of the nw waves whose lanes all
+//      hold elements takes the q-th largest of its 64 lane maxima of y (q = ⌈k / nw⌉)
+//      by repeated wave maxima; the smallest of those, L, has ≥ nw·q ≥ k elements
+//      at or above it, so the k-th largest s is ≥ L / T.
+//   2. y* = the smallest float with y* / T ≥ L / T (a few steps down from L): the
+//      elements with y ≥ y* are exactly those with s ≥ L / T, a superset of the kept
+//      ones. They are gathered into LDS with s, in index order (threads own
+//      consecutive elements).
+//   3. Among them, the k-th largest s (#(> s) < k ≤ #(≥ s)) and the maximum by counting.
+//   4. draw_kept: the index-order float64 CDF over the kept ones (s ≥ the k-th largest).
+// Returns the chosen index, or -1 (the general path then runs) when more than kRegCand
+// elements reach y*, or when fewer than k/64 waves are full. All threads must call it.
+constexpr int kRegElems = 32;   // elements per thread: V ≤ 32768
+constexpr int kRegK = 256;
+constexpr int kRegCand = 1024;  // gathered candidates (≤ kCandMax)
+
+__device__ bool sample_regs_applies(const Row<half_t>& row, int k) {
+  const int V = row.V;
+  return k >= 1 && k <= kRegK && (V & 7) == 0 && V <= kRegElems * kThreads &&
+         (reinterpret_cast<uintptr_t>(row.lg) & 15) == 0;
+}
+
+__device__ __forceinline__ float prev_float(float y) {
+  if (y == 0.f) return -__int_as_float(1);
+  const int b = __float_as_int(y);
+  return __int_as_float(y > 0.f ? b - 1 : b + 1);
+}
+
+// Wave 0 draws over the n candidates (index order; candx = scaled values) keeping those
+// ≥ thr, with max mx: p = exp(x − mx) / Σ exp (float32), then the first kept index whose
+// float64 running sum / total exceeds u (V − 1 if rounding leaves none). n ≤ 64·R.
+template <int R>
+__device__ __forceinline__ int draw_kept(int V, int n, float thr, float mx, double u, Shared& sh, const int* cand,
+                         const float* candx) {
+  if (threadIdx.x < 64) {
+    const int l = threadIdx.x;
+    float e[R];
+    float se = 0.f;
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const int j = l + 64 * r;
+      const float x = j < n ? candx[j] : -INFINITY;
+      e[r] = x >= thr ? expf(x - mx) : 0.f;
+      se += e[r];
+    }
+    se = wave_sum(se);
+    double p[R], total = 0.0;
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      p[r] = static_cast<double>(e[r] / se);
+      total += p[r];
+    }
+    total = wave_sum_d(total);
+    double carry = 0.0;
+    int found = 0x7fffffff;
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      if (found != 0x7fffffff || 64 * r >= n) break;
+      const int j = l + 64 * r;
+      const bool keep = j < n && candx[j] >= thr;
+      double inc = p[r];
+#pragma unroll
+      for (int o = 1; o < 64; o <<= 1) {
+        const double t = __shfl_up(inc, o, 64);
+        if (l >= o) inc += t;
+      }
+      const unsigned long long hits = __ballot(keep && (carry + inc) / total > u);
+      if (hits) found = cand[64 * r + __ffsll(static_cast<long long>(hits)) - 1];
+      carry += __shfl(inc, 63, 64);
+    }
+    if (l == 0) sh.found_index = found == 0x7fffffff ? V - 1 : found;
+  }
+  __syncthreads();
+  return sh.found_index;
+}
+
+__device__ __forceinline__ int sample_topk_regs(const Row<half_t> row, int k, double u, Shared& sh,
+                                                int* cand, float* candx) {
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int V = row.V;
+  // waves 0 … nw-1 have every lane holding elements (lane 63 of wave w starts at
+  // 32·(64w + 63))
+  const int last = (V - 1) / kRegElems;  // the last thread holding elements
+  const int nw = last < 63 ? 0 : ((last - 63) / 64 + 1 < kWaves ? (last - 63) / 64 + 1 : kWaves);
+  if (nw == 0 || (k + nw - 1) / nw > 64) return -1;
+  const int q = (k + nw - 1) / nw;
+  const int i0 = kRegElems * tid;
+  float y[kRegElems];
+  float tmax = -INFINITY;
+#pragma unroll
+  for (int c = 0; c < kRegElems / 8; ++c) {
+    if (i0 + 8 * c < V) {
+      const half8 h = *reinterpret_cast<const half8*>(row.lg + i0 + 8 * c);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        y[8 * c + e] = row.penalised(static_cast<float>(h[e]), i0 + 8 * c + e);
+        tmax = fmaxf(tmax, y[8 * c + e]);
+      }
+    } else {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) y[8 * c + e] = -INFINITY;
+    }
+  }
+  if (wave < nw) {
+    // q-th largest lane maximum: each round takes the wave maximum and retires the lanes
+    // holding it; the round where the retired count reaches q has it (≤ q rounds)
+    float cur = tmax, qv = -INFINITY;
+    int rem = q;
+    for (int r = 0; r < q; ++r) {
+      const float mw = wave_max_dpp(cur);
+      const int cnt = __popcll(__ballot(cur == mw));
+      if (cnt >= rem) {
+        qv = mw;
+        break;
+      }
+      rem -= cnt;
+      if (cur == mw) cur = -INFINITY;
+    }
+    if (lane == 0) sh.redf[wave] = qv;
+  }
+  __syncthreads();
+  // every thread forms the same y* (no broadcast round); INFINITY: give up (n = 0 → -1)
+  float lo = INFINITY;
+  for (int w = 0; w < nw; ++w) lo = fminf(lo, sh.redf[w]);
+  {
+    const float ls = lo / row.temperature;
+    int steps = 0;
+    for (; steps < 64; ++steps) {
+      const float yd = prev_float(lo);
+      if (!(yd / row.temperature >= ls)) break;
+      lo = yd;
+    }
+    if (steps == 64) lo = INFINITY;
+  }
+  int c = 0;
+#pragma unroll
+  for (int j = 0; j < kRegElems; ++j) c += y[j] >= lo ? 1 : 0;
+  int inc = c;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const int t = __shfl_up(inc, o, 64);
+    if (lane >= o) inc += t;
+  }
+  if (lane == 63) sh.redi[wave] = inc;
+  __syncthreads();
+  int off = inc - c, n = 0;
+  for (int w = 0; w < kWaves; ++w) {
+    const int cw = sh.redi[w];
+    if (w < wave) off += cw;
+    n += cw;
+  }
+  if (n > kRegCand || n < k) return -1;  // the same n in every thread
+#pragma unroll
+  for (int j = 0; j < kRegElems; ++j)
+    if (y[j] >= lo) {
+      cand[off] = i0 + j;
+      candx[off] = y[j] / row.temperature;
+      ++off;
+    }
+  const int n4 = (n + 3) & ~3;  // padded to whole float4 reads: -inf never counts
+  if (tid >= n && tid < n4) candx[tid] = -INFINITY;
+  __syncthreads();
+  const float4* cx4 = reinterpret_cast<const float4*>(candx);
+  if (tid < n) {  // every thread whose value is the k-th largest writes the same
+    const float xt = candx[tid];
+    int gt = 0, ge = 0;
+    int r = 0;
+    for (; r + 4 <= n4 / 4; r += 4) {
+      float4 v[4];
+#pragma unroll
+      for (int h = 0; h < 4; ++h) v[h] = cx4[r + h];
+#pragma unroll
+      for (int h = 0; h < 4; ++h) {
+        gt += (v[h].x > xt) + (v[h].y > xt) + (v[h].z > xt) + (v[h].w > xt);
+        ge += (v[h].x >= xt) + (v[h].y >= xt) + (v[h].z >= xt) + (v[h].w >= xt);
+      }
+    }
+    for (; r < n4 / 4; ++r) {
+      const float4 v = cx4[r];
+      gt += (v.x > xt) + (v.y > xt) + (v.z > xt) + (v.w > xt);
+      ge += (v.x >= xt) + (v.y >= xt) + (v.z >= xt) + (v.w >= xt);
+    }
+    if (gt < k && ge >= k) sh.reg_thr = xt;
+    if (gt == 0) sh.reg_max = xt;
+  }
+  __syncthreads();
+  return draw_kept<kRegCand / 64>(row.V, n, sh.reg_thr, sh.reg_max, u, sh, cand, candx);
 }
 
 // Top-k sampling without top-p (generate.py:43-47, then RandomState.choice): every
@@ -381,7 +582,7 @@ __global__ __launch_bounds__(kThreads) void sample_kernel(SampleArgs a) {
   __shared__ Shared sh;
   __shared__ __attribute__((aligned(16))) char s_row[kRowCacheBytes];
   __shared__ int s_cand[kCandMax];
-  __shared__ float s_candx[kCandMax];
+  __shared__ __attribute__((aligned(16))) float s_candx[kCandMax];
   __shared__ uint32_t s_tkeys[kThreads];
   const int b = blockIdx.x;
   const int V = a.V;
@@ -389,24 +590,6 @@ __global__ __launch_bounds__(kThreads) void sample_kernel(SampleArgs a) {
   const int p_cur = gen ? a.pos[b] : (a.hist_len ? a.hist_len[b] - 1 : -1);
   Row<T> row;
   row.lg = static_cast<const T*>(a.logits) + b * a.logits_stride;
-  // The selection passes re-read the row many times: with room for it, stage it in LDS
-  // once (all 16-byte loads of the row in flight together) and let every pass read LDS.
-  if (a.V * static_cast<int>(sizeof(T)) <= kRowCacheBytes) {
-    T* cache = reinterpret_cast<T*>(s_row);
-    constexpr int E = 16 / sizeof(T);
-    const int nv = a.V / E;
-    const bool aligned = (reinterpret_cast<uintptr_t>(row.lg) & 15) == 0;
-    if (aligned) {
-      typedef int iv4 __attribute__((ext_vector_type(4)));
-      for (int i = threadIdx.x; i < nv; i += kThreads)
-        reinterpret_cast<iv4*>(cache)[i] = reinterpret_cast<const iv4*>(row.lg)[i];
-      for (int i = nv * E + threadIdx.x; i < a.V; i += kThreads) cache[i] = row.lg[i];
-    } else {
-      for (int i = threadIdx.x; i < a.V; i += kThreads) cache[i] = row.lg[i];
-    }
-    __syncthreads();
-    row.lg = cache;
-  }
   row.V = V;
   row.pen = a.rep_penalty;
   row.temperature = a.temperature;
@@ -424,142 +607,174 @@ __global__ __launch_bounds__(kThreads) void sample_kernel(SampleArgs a) {
     __syncthreads();
   }
 
-  int chosen = 0;
-  if (a.temperature <= 0.f) {
-    // argmax, first index among equal maxima
-    float best = -INFINITY;
-    int bi = 0x7fffffff;
-    for (int i = threadIdx.x; i < V; i += kThreads) {
-      const float x = row.base(i);
-      if (x > best || (x == best && i < bi)) {
-        best = x;
-        bi = i;
-      }
-    }
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) {
-      const float ob = __shfl_xor(best, o, 64);
-      const int oi = __shfl_xor(bi, o, 64);
-      if (ob > best || (ob == best && oi < bi)) {
-        best = ob;
-        bi = oi;
-      }
-    }
-    __syncthreads();
-    if ((threadIdx.x & 63) == 0) {
-      sh.redf[threadIdx.x >> 6] = best;
-      sh.redi[threadIdx.x >> 6] = bi;
-    }
-    __syncthreads();
-    if (threadIdx.x == 0) {
-      float bb = sh.redf[0];
-      int ii = sh.redi[0];
-      for (int w = 1; w < kWaves; ++w) {
-        if (sh.redf[w] > bb || (sh.redf[w] == bb && sh.redi[w] < ii)) {
-          bb = sh.redf[w];
-          ii = sh.redi[w];
-        }
-      }
-      sh.found_index = ii;
-    }
-    __syncthreads();
-    chosen = sh.found_index;
-  } else {
+  const bool sampled = a.temperature > 0.f;
+  const bool use_p = a.top_p > 0.f && a.top_p < 1.f;
+  const bool use_k = a.top_k > 0;
+  const int k_eff = a.top_k < V ? a.top_k : V;
+  double u = 0.0;
+  if (sampled) {
     const long long ui = gen ? static_cast<long long>(p_cur + 1 - a.plen[b]) * a.B + b : b;
-    const double u = a.uniforms[ui];
-    const bool use_p = a.top_p > 0.f && a.top_p < 1.f;
-    bool use_k = a.top_k > 0;
-    chosen = -1;
-    if (use_k && !use_p)
-      chosen = sample_topk_fast(row, a.top_k < V ? a.top_k : V, u, sh, s_cand, s_candx, s_tkeys);
-    // top-k threshold on the temperature-scaled logits
-    float thresh = -INFINITY;
-    if (use_k && chosen < 0) {
-      const int k = a.top_k < V ? a.top_k : V;
-      const uint32_t tk = select_kth_key(V, k, [&](int i) { return fkey(row.scaled(i)); }, sh);
-      const uint32_t bits = (tk & 0x80000000u) ? (tk & 0x7fffffffu) : ~tk;
-      thresh = __uint_as_float(bits);
-    }
-    auto xm = [&](int i) {
-      const float x = row.scaled(i);
-      return (use_k && x < thresh) ? -1e9f : x;
-    };
-    float mx = -INFINITY;
-    for (int i = threadIdx.x; i < V; i += kThreads) mx = fmaxf(mx, xm(i));
-    mx = block_max_f(mx, sh);
-    float se = 0.f;
-    for (int i = threadIdx.x; i < V; i += kThreads) se += expf(xm(i) - mx);
-    se = block_sum_f(se, sh);
-    auto prob = [&](int i) { return expf(xm(i) - mx) / se; };
-    auto keyp = [&](int i) { return fkey(prob(i)); };
-
-    if (use_k && !use_p && chosen < 0) chosen = sample_topk_candidates(row, thresh, u, sh, s_cand, s_candx);
-    if (chosen >= 0) {
-      // sampled among the top-k candidates
-    } else if (use_p) {
-      // Cut: first descending position whose running mass exceeds top_p.
-      uint32_t tau1;
-      int j1;
-      select_by_mass(V, static_cast<double>(a.top_p), keyp, prob, [](int) { return true; }, &tau1,
-                     &j1, sh);
-      // Index of that element; kept = the elements before it in walk order:
-      // key > τ1, or key == τ1 and index > cut index.
-      const int cut = find_nth(V, j1, [&](int i) { return keyp(i) == tau1; }, sh);
-      int ties1 = 0;
-      for (int i = threadIdx.x; i < V; i += kThreads) ties1 += keyp(i) == tau1 ? 1 : 0;
-      {
-        int tot = 0;
-        block_excl_scan_i(ties1, &tot, sh);
-        ties1 = tot;
+    u = a.uniforms[ui];
+  }
+  int chosen = -1;
+  if constexpr (sizeof(T) == 2) {
+    if (sampled && use_k && !use_p && sample_regs_applies(row, k_eff))
+      chosen = sample_topk_regs(row, k_eff, u, sh, s_cand, s_candx);
+  }
+  if (chosen < 0) {
+    // The selection passes re-read the row many times: with room for it, stage it in LDS
+    // once (all 16-byte loads of the row in flight together) and let every pass read LDS.
+    if (a.V * static_cast<int>(sizeof(T)) <= kRowCacheBytes) {
+      T* cache = reinterpret_cast<T*>(s_row);
+      constexpr int E = 16 / sizeof(T);
+      const int nv = a.V / E;
+      const bool aligned = (reinterpret_cast<uintptr_t>(row.lg) & 15) == 0;
+      if (aligned) {
+        typedef int iv4 __attribute__((ext_vector_type(4)));
+        for (int i = threadIdx.x; i < nv; i += kThreads)
+          reinterpret_cast<iv4*>(cache)[i] = reinterpret_cast<const iv4*>(row.lg)[i];
+        for (int i = nv * E + threadIdx.x; i < a.V; i += kThreads) cache[i] = row.lg[i];
+      } else {
+        for (int i = threadIdx.x; i < a.V; i += kThreads) cache[i] = row.lg[i];
       }
-      // Empty prefix (the crossing element is the top one) keeps that element alone.
-      int above = 0;
-      for (int i = threadIdx.x; i < V; i += kThreads) above += keyp(i) > tau1 ? 1 : 0;
-      {
-        int tot = 0;
-        block_excl_scan_i(above, &tot, sh);
-        above = tot;
-      }
-      const bool single = (above == 0 && j1 == ties1);  // cut is the largest tied index
-      auto kept = [&](int i) {
-        const uint32_t k = keyp(i);
-        if (single) return i == cut;
-        return k > tau1 || (k == tau1 && i > cut);
-      };
-      float ks = 0.f;
-      for (int i = threadIdx.x; i < V; i += kThreads) ks += kept(i) ? prob(i) : 0.f;
-      ks = block_sum_f(ks, sh);
-      auto q = [&](int i) { return prob(i) / ks; };
-      double tq = 0.0;
-      for (int i = threadIdx.x; i < V; i += kThreads) tq += kept(i) ? static_cast<double>(q(i)) : 0.0;
-      double total = 0.0;
-      block_excl_scan_d(tq, &total, sh);
-      uint32_t tau2;
-      int j2;
-      // The renormalised list keeps the order of p (generate.py:50-58).
-      select_by_mass(V, u * total, keyp, q, kept, &tau2, &j2, sh);
-      chosen = find_nth(V, j2, [&](int i) { return kept(i) && keyp(i) == tau2; }, sh);
-    } else {
-      // Index-order float64 CDF; first i with cdf[i] / cdf[-1] > u.
-      const int seg = (V + kThreads - 1) / kThreads;
-      const int lo = threadIdx.x * seg, hi = min(V, lo + seg);
-      double part = 0.0;
-      for (int i = lo; i < hi; ++i) part += static_cast<double>(prob(i));
-      double total = 0.0;
-      double run = block_excl_scan_d(part, &total, sh);
-      if (threadIdx.x == 0) sh.found_index = 0x7fffffff;
       __syncthreads();
-      for (int i = lo; i < hi; ++i) {
-        run += static_cast<double>(prob(i));
-        if (run / total > u) {
-          atomicMin(&sh.found_index, i);
-          break;
+      row.lg = cache;
+    }
+
+    if (!sampled) {
+      // argmax, first index among equal maxima
+      float best = -INFINITY;
+      int bi = 0x7fffffff;
+      for (int i = threadIdx.x; i < V; i += kThreads) {
+        const float x = row.base(i);
+        if (x > best || (x == best && i < bi)) {
+          best = x;
+          bi = i;
+        }
+      }
+  #pragma unroll
+      for (int o = 32; o > 0; o >>= 1) {
+        const float ob = __shfl_xor(best, o, 64);
+        const int oi = __shfl_xor(bi, o, 64);
+        if (ob > best || (ob == best && oi < bi)) {
+          best = ob;
+          bi = oi;
         }
       }
       __syncthreads();
-      chosen = sh.found_index == 0x7fffffff ? V - 1 : sh.found_index;
+      if ((threadIdx.x & 63) == 0) {
+        sh.redf[threadIdx.x >> 6] = best;
+        sh.redi[threadIdx.x >> 6] = bi;
+      }
+      __syncthreads();
+      if (threadIdx.x == 0) {
+        float bb = sh.redf[0];
+        int ii = sh.redi[0];
+        for (int w = 1; w < kWaves; ++w) {
+          if (sh.redf[w] > bb || (sh.redf[w] == bb && sh.redi[w] < ii)) {
+            bb = sh.redf[w];
+            ii = sh.redi[w];
+          }
+        }
+        sh.found_index = ii;
+      }
+      __syncthreads();
+      chosen = sh.found_index;
+    } else {
+      if (use_k && !use_p) chosen = sample_topk_fast(row, k_eff, u, sh, s_cand, s_candx, s_tkeys);
+      // top-k threshold on the temperature-scaled logits
+      float thresh = -INFINITY;
+      if (use_k && chosen < 0) {
+        const uint32_t tk =
+            select_kth_key(V, k_eff, [&](int i) { return fkey(row.scaled(i)); }, sh);
+        const uint32_t bits = (tk & 0x80000000u) ? (tk & 0x7fffffffu) : ~tk;
+        thresh = __uint_as_float(bits);
+      }
+      auto xm = [&](int i) {
+        const float x = row.scaled(i);
+        return (use_k && x < thresh) ? -1e9f : x;
+      };
+      if (use_k && !use_p && chosen < 0)
+        chosen = sample_topk_candidates(row, thresh, u, sh, s_cand, s_candx);
+      // max and Σ exp over the whole row, for the top-p and full-CDF draws
+      float mx = -INFINITY, se = 0.f;
+      if (chosen < 0) {
+        for (int i = threadIdx.x; i < V; i += kThreads) mx = fmaxf(mx, xm(i));
+        mx = block_max_f(mx, sh);
+        for (int i = threadIdx.x; i < V; i += kThreads) se += expf(xm(i) - mx);
+        se = block_sum_f(se, sh);
+      }
+      auto prob = [&](int i) { return expf(xm(i) - mx) / se; };
+      auto keyp = [&](int i) { return fkey(prob(i)); };
+
+      if (chosen >= 0) {
+        // sampled among the top-k candidates
+      } else if (use_p) {
+        // Cut: first descending position whose running mass exceeds top_p.
+        uint32_t tau1;
+        int j1;
+        select_by_mass(V, static_cast<double>(a.top_p), keyp, prob, [](int) { return true; }, &tau1,
+                       &j1, sh);
+        // Index of that element; kept = the elements before it in walk order:
+        // key > τ1, or key == τ1 and index > cut index.
+        const int cut = find_nth(V, j1, [&](int i) { return keyp(i) == tau1; }, sh);
+        int ties1 = 0;
+        for (int i = threadIdx.x; i < V; i += kThreads) ties1 += keyp(i) == tau1 ? 1 : 0;
+        {
+          int tot = 0;
+          block_excl_scan_i(ties1, &tot, sh);
+          ties1 = tot;
+        }
+        // Empty prefix (the crossing element is the top one) keeps that element alone.
+        int above = 0;
+        for (int i = threadIdx.x; i < V; i += kThreads) above += keyp(i) > tau1 ? 1 : 0;
+        {
+          int tot = 0;
+          block_excl_scan_i(above, &tot, sh);
+          above = tot;
+        }
+        const bool single = (above == 0 && j1 == ties1);  // cut is the largest tied index
+        auto kept = [&](int i) {
+          const uint32_t k = keyp(i);
+          if (single) return i == cut;
+          return k > tau1 || (k == tau1 && i > cut);
+        };
+        float ks = 0.f;
+        for (int i = threadIdx.x; i < V; i += kThreads) ks += kept(i) ? prob(i) : 0.f;
+        ks = block_sum_f(ks, sh);
+        auto q = [&](int i) { return prob(i) / ks; };
+        double tq = 0.0;
+        for (int i = threadIdx.x; i < V; i += kThreads)
+          tq += kept(i) ? static_cast<double>(q(i)) : 0.0;
+        double total = 0.0;
+        block_excl_scan_d(tq, &total, sh);
+        uint32_t tau2;
+        int j2;
+        // The renormalised list keeps the order of p (generate.py:50-58).
+        select_by_mass(V, u * total, keyp, q, kept, &tau2, &j2, sh);
+        chosen = find_nth(V, j2, [&](int i) { return kept(i) && keyp(i) == tau2; }, sh);
+      } else {
+        // Index-order float64 CDF; first i with cdf[i] / cdf[-1] > u.
+        const int seg = (V + kThreads - 1) / kThreads;
+        const int lo = threadIdx.x * seg, hi = min(V, lo + seg);
+        double part = 0.0;
+        for (int i = lo; i < hi; ++i) part += static_cast<double>(prob(i));
+        double total = 0.0;
+        double run = block_excl_scan_d(part, &total, sh);
+        if (threadIdx.x == 0) sh.found_index = 0x7fffffff;
+        __syncthreads();
+        for (int i = lo; i < hi; ++i) {
+          run += static_cast<double>(prob(i));
+          if (run / total > u) {
+            atomicMin(&sh.found_index, i);
+            break;
+          }
+        }
+        __syncthreads();
+        chosen = sh.found_index == 0x7fffffff ? V - 1 : sh.found_index;
+      }
     }
-  }
+  }  // general path
 
   if (threadIdx.x == 0) {
     if (gen) {

@@ -229,6 +229,40 @@ def test_top_k_sampling_ties_and_large_k(gpu, top_k, grid):
     assert list(got) == want
 
 
+@pytest.mark.parametrize("v", [32000, 32768, 4096, 520, 32776])
+@pytest.mark.parametrize("top_k", [1, 50, 256, 257])
+def test_top_k_sampling_fp16_rows(gpu, v, top_k):
+    """fp16 logits, top-k without top-p: the register-resident draw (1 <= k <= 256, V a
+    multiple of 8 up to 32768) and, past those bounds or when more than 512 elements
+    reach its lower bound, the general path give the oracle's token, for random rows,
+    rows with exact ties at the k-th largest value, an ascending row and a constant row."""
+    rng = np.random.default_rng(v + top_k)
+    b = 8
+    lg = (rng.standard_normal((b, v)) * 2).astype(np.float16)
+    lg[1] = (rng.integers(-8, 8, v) * 0.5).astype(np.float16)
+    lg[2] = np.linspace(-4, 4, v).astype(np.float16)
+    lg[3] = np.float16(0.0)
+    u = rng.random(b)
+    got = _k().sample_tokens(lg, temperature=0.8, top_k=top_k, top_p=1.0, uniforms=u)
+    want = [R.sample_logits(lg[i], temperature=0.8, top_k=top_k, top_p=1.0, u=u[i])
+            for i in range(b)]
+    assert list(got) == want
+
+
+def test_top_k_sampling_fp16_with_repetition_penalty(gpu):
+    rng = np.random.default_rng(13)
+    b, v = 6, 32000
+    lg = (rng.standard_normal((b, v)) * 2).astype(np.float16)
+    top = np.argsort(-lg.astype(np.float32), axis=1)
+    hist = [list(top[i, :40:3]) + [int(t) for t in rng.integers(0, v, 50)] for i in range(b)]
+    u = rng.random(b)
+    got = _k().sample_tokens(lg, temperature=0.7, top_k=50, uniforms=u, history=hist,
+                             repetition_penalty=1.3)
+    want = [R.sample_logits(lg[i], temperature=0.7, top_k=50, top_p=1.0, u=u[i],
+                            token_ids=hist[i], repetition_penalty=1.3) for i in range(b)]
+    assert list(got) == want
+
+
 def test_sampling_with_repetition_penalty(gpu):
     rng = np.random.default_rng(11)
     lg = _distinct_logits(rng, 3, 1000)
