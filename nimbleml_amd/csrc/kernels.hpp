@@ -17,6 +17,7 @@ enum Epilogue : int {
   EPI_BIAS_GELU = 2,   // out = gelu_T(T(T(acc) + b))
   EPI_BIAS_RESID = 3,  // out = T(r + T(T(acc) + b))
   EPI_QKV = 4,         // T(T(acc) + b) scattered to head-major Q and the K/V cache
+  EPI_CE = 5,          // fp16 tied head fused with cross-entropy: softmax partials, no output
 };
 
 // Destination of the QKV epilogue. Output row r = b·S + s of the projection is
@@ -36,6 +37,18 @@ struct QKVDst {
   // Packed ragged rows: row m is position s of sequence b, row_seg[m] = (b << 16) | s
   // (s < 65536); q keeps the padded (B, H, S, dk) layout. Null: b = m / S, s = m % S.
   const int32_t* row_seg;
+};
+
+// Destination of the EPI_CE epilogue (fp16, 256 × 256 tiles): for row m and column tile
+// t (256 columns), part[m·tiles_n + t] = (mx, Σ rnd(exp(rnd(x − mx)))) over the tile's
+// fp16 logits x (mx their maximum; the terms rounded where ce_rows rounds them), and
+// label_logit[m] = the fp16 logit of column labels[m], written by the tile holding it.
+// The logits themselves are never stored.
+struct CEDst {
+  const int64_t* labels;
+  float2* part;
+  float* label_logit;
+  int tiles_n;
 };
 
 struct LinearArgs {
@@ -59,10 +72,15 @@ struct LinearArgs {
   // EPI_BIAS_GELU with more than 64 rows: also writes the pre-activation x·Wᵀ + b, (M, N),
   // the value the GELU was taken of (the training forward keeps it). Null: not written.
   void* pre_out;
+  CEDst ce;  // EPI_CE only
 };
 
 // Whether launch_linear can fuse RMSNorm into this GEMM (ssq_in / ssq_out above).
 bool linear_norm_fusable(int dt, int M, int K, int N);
+// Whether launch_linear takes EPI_CE for this shape (x 16-byte aligned, lda = K); the
+// column tile width of its partials is kLinearCETile.
+bool linear_ce_fusable(int dt, int M, int K, int N);
+constexpr int kLinearCETile = 256;
 
 int launch_linear(int dt, const LinearArgs& a, hipStream_t st);
 // Workspace of the split-K skinny GEMM (8 < M ≤ 64) for outputs up to max_n wide.
@@ -135,6 +153,11 @@ size_t attention_decode_workspace(int B, int H, int dk, int max_len);
 int launch_ce_rows(int dt, const void* logits, int rows, int V, const int64_t* labels,
                    long long ignore_index, int has_ignore, float* row_loss, int* row_valid,
                    int* err, hipStream_t st);
+// Per-row loss from the EPI_CE partials (tiles_n per row): lse = M + log(Σ_t s_t·
+// exp(mx_t − M)), M = max_t mx_t, loss = lse − label_logit; row flags as launch_ce_rows.
+int launch_ce_combine(const float2* part, int tiles_n, const float* label_logit, int rows, int V,
+                      const int64_t* labels, long long ignore_index, int has_ignore,
+                      float* row_loss, int* row_valid, int* err, hipStream_t st);
 // Sum of valid row losses / count → out[0] (double); 0 when no row is valid.
 int launch_ce_reduce(const float* row_loss, const int* row_valid, int rows, double* sum_count,
                      int accumulate, hipStream_t st);

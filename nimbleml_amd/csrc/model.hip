@@ -678,6 +678,20 @@ int nml_model_mha_forward(nml_model* m, int layer, const void* x, void* out, siz
                             st, nullptr);
 }
 
+// Mean of the accumulated row losses → *loss, with the embedding and label range checks.
+static int finish_loss(nml_model* m, const Small& sm, hipStream_t st, double* loss) {
+  NML_TRY(launch_ce_finalize(sm.acc, sm.acc + 2, st));
+  double host[3];
+  int herr = 0;
+  NML_HIP(hipMemcpyAsync(host, sm.acc, sizeof(host), hipMemcpyDeviceToHost, st));
+  NML_HIP(hipMemcpyAsync(&herr, sm.err, sizeof(int), hipMemcpyDeviceToHost, st));
+  NML_HIP(hipStreamSynchronize(st));
+  NML_REQUIRE((herr & 1) == 0, "Token ID out of range [0, %d)", m->V);
+  NML_REQUIRE((herr & 2) == 0, "label out of range [0, %d)", m->V);
+  *loss = host[2];
+  return 0;
+}
+
 int nml_model_loss(nml_model* m, const int64_t* ids, const int64_t* labels, size_t batch,
                    size_t seq, int64_t ignore_index, int has_ignore, double* loss) {
   NML_TRY(check_ready(m));
@@ -702,6 +716,33 @@ int nml_model_loss(nml_model* m, const int64_t* ids, const int64_t* labels, size
                        st));
   const long long sb = (long long)m->H * S * m->dk, sh = (long long)S * m->dk;
   NML_TRY(trunk(m, a, B, S, nullptr, [&](int) { return KVView{kbuf, vbuf, sb, sh}; }, st));
+  if (linear_ce_fusable(m->dt, R, m->d, m->V)) {
+    // fp16 at prefill sizes: the head GEMM's epilogue forms each row's softmax partials
+    // per 256-column tile and the label's logit; no logits are stored.
+    const int tn = (m->V + kLinearCETile - 1) / kLinearCETile;
+    const size_t pb = align256((size_t)R * tn * sizeof(float2));
+    const size_t rb = align256((size_t)R * 4);
+    NML_TRY(m->logits_ws.ensure(pb + 3 * rb));
+    char* w = static_cast<char*>(m->logits_ws.p);
+    float2* part = reinterpret_cast<float2*>(w);
+    float* label_logit = reinterpret_cast<float*>(w + pb);
+    float* row_loss = reinterpret_cast<float*>(w + pb + rb);
+    int* row_valid = reinterpret_cast<int*>(w + pb + 2 * rb);
+    LinearArgs lm{};
+    lm.x = a.xn;
+    lm.lda = m->d;
+    lm.w = m->emb;
+    lm.M = R;
+    lm.N = m->V;
+    lm.K = m->d;
+    lm.epi = EPI_CE;
+    lm.ce = CEDst{labels, part, label_logit, tn};
+    NML_TRY(launch_linear(m->dt, lm, st));
+    NML_TRY(launch_ce_combine(part, tn, label_logit, R, m->V, labels, ignore_index, has_ignore,
+                              row_loss, row_valid, sm.err, st));
+    NML_TRY(launch_ce_reduce(row_loss, row_valid, R, sm.acc, 0, st));
+    return finish_loss(m, sm, st, loss);
+  }
   // Logits in row chunks of ≤ 512 MiB, never all (R, V) at once.
   size_t chunk = R;
   while (chunk > 1 && chunk * m->V * m->es > ((size_t)512 << 20)) chunk = (chunk + 1) / 2;
@@ -727,16 +768,7 @@ int nml_model_loss(nml_model* m, const int64_t* ids, const int64_t* labels, size
                            row_valid, sm.err, st));
     NML_TRY(launch_ce_reduce(row_loss, row_valid, n, sm.acc, r0 > 0, st));
   }
-  NML_TRY(launch_ce_finalize(sm.acc, sm.acc + 2, st));
-  double host[3];
-  int herr = 0;
-  NML_HIP(hipMemcpyAsync(host, sm.acc, sizeof(host), hipMemcpyDeviceToHost, st));
-  NML_HIP(hipMemcpyAsync(&herr, sm.err, sizeof(int), hipMemcpyDeviceToHost, st));
-  NML_HIP(hipStreamSynchronize(st));
-  NML_REQUIRE((herr & 1) == 0, "Token ID out of range [0, %d)", m->V);
-  NML_REQUIRE((herr & 2) == 0, "label out of range [0, %d)", m->V);
-  *loss = host[2];
-  return 0;
+  return finish_loss(m, sm, st, loss);
 }
 
 int nml_cache_create(nml_model* m, size_t batch, nml_cache** out) {

@@ -295,6 +295,90 @@ __device__ __forceinline__ void epilogue_staged(const LinearArgs& a, int m0, int
   }
 }
 
+// EPI_CE epilogue (tied head fused with cross-entropy): the tile's fp16 logits stay in
+// the accumulators. From the transposed layout (lane l: row 32i + l%32 of its wave's
+// TM/2 × TN/4 block, columns 32j + 8g + 4(l/32) + q), each row's maximum over the
+// tile's TN columns is formed from the 2 lanes holding it and the 4 waves along N (LDS),
+// then Σ rnd(exp(rnd(x − max))) — ce_rows_kernel's terms, shifted by the tile maximum —
+// likewise; the label's logit is written by the lane holding it. Columns past N count
+// as −∞ (each tile holds at least one column below N, so the maximum is finite).
+template <int TM, int TN>
+__device__ __forceinline__ void epilogue_ce(const LinearArgs& a, int m0, int n0,
+                                            const floatx16 (&acc)[TM / 64][TN / 128],
+                                            char* lds_raw) {
+#pragma clang fp contract(off)
+  constexpr int IA = TM / 64, JB = TN / 128, R = TM / 2, C = TN / 4;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) >> 6);
+  const int wm = wave >> 2, wn = wave & 3, h = lane >> 5, rl = lane & 31;
+  const int N = a.N, cb = n0 + wn * C;  // first column of this wave's block
+  float* s_max = reinterpret_cast<float*>(lds_raw);  // [2][4][R]
+  float* s_sum = s_max + 8 * R;                      // [2][4][R]
+  auto logit = [&](int i, int j, int g, int q) {
+    const int col = cb + 32 * j + 8 * g + 4 * h + q;
+    return col < N ? rnd<half_t>(acc[i][j][4 * g + q]) : -INFINITY;
+  };
+  __syncthreads();  // every wave is done with the main loop's stages
+#pragma unroll
+  for (int i = 0; i < IA; ++i) {
+    float m = -INFINITY;
+#pragma unroll
+    for (int j = 0; j < JB; ++j)
+#pragma unroll
+      for (int g = 0; g < 4; ++g)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) m = fmaxf(m, logit(i, j, g, q));
+    m = fmaxf(m, __shfl_xor(m, 32, 64));
+    if (h == 0) s_max[(wm * 4 + wn) * R + 32 * i + rl] = m;
+  }
+  __syncthreads();
+  float mt[IA];
+#pragma unroll
+  for (int i = 0; i < IA; ++i) {
+    const float* sm = s_max + wm * 4 * R + 32 * i + rl;
+    mt[i] = fmaxf(fmaxf(sm[0], sm[R]), fmaxf(sm[2 * R], sm[3 * R]));
+  }
+#pragma unroll
+  for (int i = 0; i < IA; ++i) {
+    float sum = 0.f;
+#pragma unroll
+    for (int j = 0; j < JB; ++j)
+#pragma unroll
+      for (int g = 0; g < 4; ++g)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) sum += rnd<half_t>(expf(rnd<half_t>(logit(i, j, g, q) - mt[i])));
+    sum += __shfl_xor(sum, 32, 64);
+    if (h == 0) s_sum[(wm * 4 + wn) * R + 32 * i + rl] = sum;
+    const int m = m0 + wm * R + 32 * i + rl;
+    if (m < a.M) {  // the label's logit, from the one lane of the one tile holding it
+      const long long c = a.ce.labels[m] - cb;
+      if (c >= 0 && c < C && ((c >> 2) & 1) == h) {
+        float v = 0.f;
+#pragma unroll
+        for (int j = 0; j < JB; ++j)
+#pragma unroll
+          for (int g = 0; g < 4; ++g)
+#pragma unroll
+            for (int q = 0; q < 4; ++q)
+              if (c == 32 * j + 8 * g + 4 * h + q) v = logit(i, j, g, q);
+        a.ce.label_logit[m] = v;
+      }
+    }
+  }
+  __syncthreads();
+  if (wn == 0 && h == 0) {
+    const int t = n0 / TN;
+#pragma unroll
+    for (int i = 0; i < IA; ++i) {
+      const int m = m0 + wm * R + 32 * i + rl;
+      const float* ss = s_sum + wm * 4 * R + 32 * i + rl;
+      if (m < a.M)
+        a.ce.part[static_cast<size_t>(m) * a.ce.tiles_n + t] =
+            make_float2(mt[i], ((ss[0] + ss[R]) + ss[2 * R]) + ss[3 * R]);
+    }
+  }
+}
+
 constexpr int kBM = 128, kBN = 128;
 
 // ---------------------------------------------------------------- fp16 MFMA GEMM
@@ -392,6 +476,7 @@ __global__ __launch_bounds__(256) void gemm_f16_kernel(LinearArgs a) {
 // on XCD b % 8 and takes a contiguous range of tiles), grouped GM m-bands at a time so
 // the workgroups resident on one XCD share A bands and B tiles in its L2.
 constexpr int kHM = 256, kHN = 256, kHK = big::kK;
+static_assert(kHN == kLinearCETile, "EPI_CE partials are per 256-column tile");
 constexpr int kHT = big::kThreads;
 
 template <int EPI, int GM, int TM, int TN>
@@ -419,7 +504,10 @@ __global__ __launch_bounds__(kHT, TM == 256 ? 1 : 4) void gemm_f16_big_kernel(Li
   big::mainloop<TM, TN, true>(static_cast<const half_t*>(a.x), a.lda, static_cast<const half_t*>(a.w), a.K,
                               a.M, a.N, 0, a.K / kHK, m0, n0, lds_raw, acc);
 
-  epilogue_staged<EPI, TM, TN>(a, m0, n0, acc, lds_raw);
+  if constexpr (EPI == EPI_CE)
+    epilogue_ce<TM, TN>(a, m0, n0, acc, lds_raw);
+  else
+    epilogue_staged<EPI, TM, TN>(a, m0, n0, acc, lds_raw);
 }
 
 template <int EPI, int GM, int TM, int TN>
@@ -926,6 +1014,9 @@ int linear_epi(const LinearArgs& a, hipStream_t st) {
     case EPI_BIAS_GELU: return linear_typed<T, EPI_BIAS_GELU>(a, st);
     case EPI_BIAS_RESID: return linear_typed<T, EPI_BIAS_RESID>(a, st);
     case EPI_QKV: return linear_typed<T, EPI_QKV>(a, st);
+    case EPI_CE:
+      if constexpr (sizeof(T) == 2) return gemm_big_launch_gm<EPI_CE, 4, kHM, kHN>(a, st);
+      break;
   }
   set_error("unknown epilogue %d", a.epi);
   return -1;
@@ -959,7 +1050,12 @@ int launch_linear(int dt, const LinearArgs& a, hipStream_t st) {
   NML_REQUIRE((reinterpret_cast<uintptr_t>(a.x) & 15) == 0 &&
                   (reinterpret_cast<uintptr_t>(a.w) & 15) == 0,
               "linear: x and w must be 16-byte aligned");
-  NML_REQUIRE(a.epi == EPI_NONE || a.bias != nullptr, "linear: epilogue %d needs a bias", a.epi);
+  NML_REQUIRE(a.epi == EPI_NONE || a.epi == EPI_CE || a.bias != nullptr,
+              "linear: epilogue %d needs a bias", a.epi);
+  NML_REQUIRE(a.epi != EPI_CE ||
+                  (linear_ce_fusable(dt, a.M, a.K, a.N) && a.lda == a.K && a.ce.labels &&
+                   a.ce.part && a.ce.label_logit && a.ce.tiles_n == (a.N + kHN - 1) / kHN),
+              "linear: the fused cross-entropy epilogue needs fp16, 256 x 256 tiles and its outputs");
   NML_REQUIRE(a.epi != EPI_BIAS_RESID || a.resid != nullptr, "linear: residual pointer missing");
   NML_REQUIRE(a.epi != EPI_QKV || (a.qkv.d > 0 && a.qkv.dk > 0 && a.N == 3 * a.qkv.d &&
                                    (a.qkv.row_seg || a.M == a.qkv.S * (a.M / a.qkv.S))),
@@ -971,6 +1067,13 @@ int launch_linear(int dt, const LinearArgs& a, hipStream_t st) {
   NML_REQUIRE(!a.ssq_out || (a.epi == EPI_BIAS_RESID && linear_norm_fusable(dt, a.M, a.K, a.N)),
               "linear: sums of squares are written by an fp16 skinny residual GEMM only");
   return dt == F16 ? linear_epi<half_t>(a, st) : linear_epi<float>(a, st);
+}
+
+bool linear_ce_fusable(int dt, int M, int K, int N) {
+  LinearArgs t{};
+  t.M = M;
+  t.N = N;
+  return dt == F16 && K % kHK == 0 && big_gemm_wide(t);
 }
 
 bool linear_norm_fusable(int dt, int M, int K, int N) {

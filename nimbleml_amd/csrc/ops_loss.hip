@@ -55,6 +55,47 @@ __global__ __launch_bounds__(256) void ce_rows_kernel(const T* __restrict__ logi
   }
 }
 
+// Rows of the fused head (EPI_CE partials), one wave per row: M = max of the tile maxima,
+// S = Σ_t s_t·exp(mx_t − M) (tiles in lane-strided order, then the wave sum), and the
+// row's loss lse − logit[label] with lse = M + log S, as ce_rows_kernel forms it.
+__global__ __launch_bounds__(256) void ce_combine_kernel(const float2* __restrict__ part, int tiles_n,
+                                                         const float* __restrict__ label_logit,
+                                                         int rows, int V,
+                                                         const int64_t* __restrict__ labels,
+                                                         long long ignore_index, int has_ignore,
+                                                         float* __restrict__ row_loss,
+                                                         int* __restrict__ row_valid,
+                                                         int* __restrict__ err) {
+#pragma clang fp contract(off)
+  const int r = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
+  if (r >= rows) return;
+  const int64_t y = labels[r];
+  const bool ignored = has_ignore && y == ignore_index;
+  if (ignored || y < 0 || y >= V) {
+    if (lane == 0) {
+      if (!ignored) atomicOr(err, 2);
+      row_loss[r] = 0.f;
+      row_valid[r] = 0;
+    }
+    return;
+  }
+  const float2* p = part + static_cast<size_t>(r) * tiles_n;
+  float mx = -INFINITY;
+  for (int t = lane; t < tiles_n; t += 64) mx = fmaxf(mx, p[t].x);
+  mx = wave_max(mx);
+  float s = 0.f;
+  for (int t = lane; t < tiles_n; t += 64) {
+    const float2 v = p[t];
+    s += v.y * expf(v.x - mx);
+  }
+  s = wave_sum(s);
+  if (lane == 0) {
+    const float lse = mx + logf(s);
+    row_loss[r] = lse - label_logit[r];
+    row_valid[r] = 1;
+  }
+}
+
 // Single block: accumulate Σ valid row losses and the count into sum_count[0..1].
 __global__ __launch_bounds__(1024) void ce_reduce_kernel(const float* __restrict__ row_loss,
                                                          const int* __restrict__ row_valid,
@@ -108,6 +149,17 @@ int launch_ce_rows(int dt, const void* logits, int rows, int V, const int64_t* l
   else
     ce_rows_kernel<float><<<rows, 256, 0, st>>>((const float*)logits, V, labels, ignore_index,
                                                 has_ignore, row_loss, row_valid, err);
+  NML_LAUNCHED();
+  return 0;
+}
+
+int launch_ce_combine(const float2* part, int tiles_n, const float* label_logit, int rows, int V,
+                      const int64_t* labels, long long ignore_index, int has_ignore,
+                      float* row_loss, int* row_valid, int* err, hipStream_t st) {
+  if (rows == 0) return 0;
+  ce_combine_kernel<<<(rows + 3) / 4, 256, 0, st>>>(part, tiles_n, label_logit, rows, V, labels,
+                                                    ignore_index, has_ignore, row_loss, row_valid,
+                                                    err);
   NML_LAUNCHED();
   return 0;
 }

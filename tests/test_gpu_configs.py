@@ -239,3 +239,37 @@ def test_c5_full_size_properties(gpu):
                                        ctypes.byref(raw)))
     print(f"C5 full: loss {full:.7f}, per sequence {per_seq}, training forward {raw.value:.7f}")
     assert abs(raw.value - full) <= 1e-5 * full
+
+
+def test_fused_head_cross_entropy_matches_stored_logits(gpu):
+    """float16 losses at prefill sizes run the tied head with the cross-entropy in its GEMM
+    epilogue (per-tile softmax partials; no logits stored). V = 8000 leaves a 64-column
+    last tile, and every fifth label is ignore_index: the loss equals the training
+    forward's, which stores the logits and reduces them row by row (pinned to the oracle
+    by the model tests), and a label outside the vocabulary is reported."""
+    from nimbleml_amd import _native as N
+
+    cfg = GPTConfig(vocab_size=8000, d_model=256, num_heads=8, num_layers=2, max_seq_len=256)
+    w = make_weights(cfg, seed=5, dtype=np.float16)
+    m = _build(cfg, w)
+    ids = random_ids((8, 256), cfg.vocab_size, 61)
+    labels = random_ids((8, 256), cfg.vocab_size, 62)
+    labels[:, ::5] = -100
+    labels[3, 7] = cfg.vocab_size - 1  # a label in the partial last tile
+    dids = N.DeviceArray.from_host(ids)
+    dlab = N.DeviceArray.from_host(labels.reshape(-1))
+    fused, stored = ctypes.c_double(), ctypes.c_double()
+    N.check(N.lib.nml_model_loss(m._device_model(), dids.ptr, dlab.ptr, 8, 256, -100, 1,
+                                 ctypes.byref(fused)))
+    N.check(N.lib.nml_model_loss_train(m._device_model(), dids.ptr, dlab.ptr, 8, 256, -100, 1,
+                                       ctypes.byref(stored)))
+    print(f"fused {fused.value:.8f} stored {stored.value:.8f}")
+    assert np.isfinite(fused.value) and abs(fused.value - np.log(cfg.vocab_size)) < 1.0
+    assert abs(fused.value - stored.value) <= 1e-5 * stored.value
+    bad = labels.copy()
+    bad[5, 11] = cfg.vocab_size
+    dbad = N.DeviceArray.from_host(bad.reshape(-1))
+    with pytest.raises(ValueError, match="label out of range"):
+        N.check(N.lib.nml_model_loss(m._device_model(), dids.ptr, dbad.ptr, 8, 256, -100, 1,
+                                     ctypes.byref(fused)))
+
