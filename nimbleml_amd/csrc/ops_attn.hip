@@ -502,12 +502,13 @@ __global__ __launch_bounds__(256, 2) void attn_prefill_mfma_kernel(AttnArgs a) {
   constexpr int CH = kFK * DK / 8 / 256;
   constexpr int VG = DK / 8;                  // 8-dim groups of a key
   half8 kn[CH], vn[CH];
-  auto fetch = [&](int k0) {
+  // (keys past kend only in the last tile: the bounds test is made there alone)
+  auto fetch_tile = [&](int k0, bool full) {
 #pragma unroll
     for (int i = 0; i < CH; ++i) {
       const int c = tid + 256 * i;
       const int key = c / VG, d8 = (c % VG) * 8;
-      const bool ok = k0 + key < kend;
+      const bool ok = full || k0 + key < kend;
       kn[i] = ok ? *reinterpret_cast<const half8*>(Kg + static_cast<long long>(k0 + key) * DK + d8) : z8;
     }
 #pragma unroll
@@ -516,11 +517,17 @@ __global__ __launch_bounds__(256, 2) void attn_prefill_mfma_kernel(AttnArgs a) {
       const int key = 2 * (tid & 31);
 #pragma unroll
       for (int u = 0; u < 2; ++u) {
-        const bool ok = k0 + key + u < kend;
+        const bool ok = full || k0 + key + u < kend;
         vn[2 * i + u] = ok ? *reinterpret_cast<const half8*>(Vg + static_cast<long long>(k0 + key + u) * DK + grp * 8)
                            : z8;
       }
     }
+  };
+  auto fetch = [&](int k0) {
+    if (k0 + kFK <= kend)
+      fetch_tile(k0, true);
+    else
+      fetch_tile(k0, false);
   };
   fetch(0);
   for (int k0 = 0; k0 < kend; k0 += kFK) {
@@ -555,28 +562,41 @@ __global__ __launch_bounds__(256, 2) void attn_prefill_mfma_kernel(AttnArgs a) {
         st[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ka, qb[ks], st[t], 0, 0, 0);
       }
     }
-    float mx = m;
+    // Scores as fp16 pairs (registers r = 2c, 2c + 1): rnd(rnd(q·k)·rscale) is one mixed
+    // fma with an fp16 result (the exact product rounds as its fp32 rounding does, see
+    // rscale), the running maximum a packed fp16 max.
+    typedef _Float16 half2v __attribute__((ext_vector_type(2)));
+    half2v sp[2][8];
+    half2v mp = {static_cast<_Float16>(-INFINITY), static_cast<_Float16>(-INFINITY)};
+    auto score = [&](float acc) {
+      return static_cast<_Float16>(__builtin_fmaf(static_cast<float>(static_cast<_Float16>(acc)), rscale, 0.f));
+    };
     if (k0 + kFK - 1 > base + qw) {  // the tile reaches past some query of this wave: mask
 #pragma unroll
       for (int t = 0; t < 2; ++t)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int key = k0 + t * 32 + 8 * (r >> 2) + 4 * hi + (r & 3);
-          const float sv = rnd<half_t>(rnd<half_t>(st[t][r]) * rscale);
-          const float s = (key <= qpos && key < kend) ? sv : -INFINITY;
-          st[t][r] = s;
-          mx = fmaxf(mx, s);
+        for (int c = 0; c < 8; ++c) {
+          half2v v;
+#pragma unroll
+          for (int u = 0; u < 2; ++u) {
+            const int r = 2 * c + u;
+            const int key = k0 + t * 32 + 8 * (r >> 2) + 4 * hi + (r & 3);
+            v[u] = (key <= qpos && key < kend) ? score(st[t][r]) : static_cast<_Float16>(-INFINITY);
+          }
+          sp[t][c] = v;
+          mp = __builtin_elementwise_max(mp, v);
         }
     } else {  // every key of the tile precedes every query of the wave
 #pragma unroll
       for (int t = 0; t < 2; ++t)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const float s = rnd<half_t>(rnd<half_t>(st[t][r]) * rscale);
-          st[t][r] = s;
-          mx = fmaxf(mx, s);
+        for (int c = 0; c < 8; ++c) {
+          const half2v v = {score(st[t][2 * c]), score(st[t][2 * c + 1])};
+          sp[t][c] = v;
+          mp = __builtin_elementwise_max(mp, v);
         }
     }
+    float mx = fmaxf(m, fmaxf(static_cast<float>(mp[0]), static_cast<float>(mp[1])));
     mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
     constexpr float kLog2e = 1.4426950408889634f;
     const float alpha = (mx == -INFINITY) ? 1.f : __builtin_amdgcn_exp2f((m - mx) * kLog2e);
@@ -599,7 +619,8 @@ __global__ __launch_bounds__(256, 2) void attn_prefill_mfma_kernel(AttnArgs a) {
         for (int j = 0; j < 8; ++j) {
           // mx is finite (key 0 precedes every query, and tiles run from key 0), so a
           // masked score gives exp2(-inf) = 0
-          const float p = __builtin_amdgcn_exp2f(__builtin_fmaf(st[t][8 * kb + j], kLog2e, nmx));
+          const float sv = static_cast<float>(sp[t][(8 * kb + j) >> 1][j & 1]);
+          const float p = __builtin_amdgcn_exp2f(__builtin_fmaf(sv, kLog2e, nmx));
           l += p;
           pb[j] = static_cast<half_t>(p);
         }
