@@ -286,7 +286,7 @@ def cpu_baseline_c5(cfg, w16, ids, lab):
                       f"{B} sequences x {cfg.num_layers} layers ({total:.0f} s per compute_loss)"}
 
 
-def bench_c5(nm, reps=2, cpu=False):
+def bench_c5(nm, reps=5, cpu=False):
     from oracle.weights import C5, make_weights, random_ids
 
     cfg = C5
