@@ -160,10 +160,13 @@ struct Raw8<float> {
 };
 
 // Decode attention for head dims ≥ 32, one launch: a 256-lane workgroup takes a group
-// of G 64-key chunks of one (row, head) — all their K/V rows are loaded up front
-// (clamped into [0, len), the clamped ones never used) — scores every key with 4
-// lanes per key (DK/4 dims each), takes the group's max and Σp with one block
-// reduction each, and P·V with each lane owning 8 dims of a key subset. Every group
+// of G 64-key chunks of one (row, head) — their K rows are loaded up front and their V
+// rows once the scores are formed (clamped into [0, len), the clamped ones never used;
+// K and V are never held together, which keeps the kernel at ≤ 72 registers: seven
+// workgroups per CU, so a batched step's groups are all resident at once) — scores
+// every key with 4 lanes per key (DK/4 dims each), takes the group's max and Σp with
+// one block reduction each, and P·V with each lane owning 8 dims of a key subset
+// (C4, hd 64: 21.9 → 21.0 µs a layer against the K and V both loaded up front). Every group
 // but the last of its (row, head) publishes (max, Σp, Σp·v) as flagged 64-bit slots
 // (1 << 32 | value, relaxed device-scope stores, no fences) and exits. The last group
 // — later in dispatch order than its siblings (x is the fastest grid index), so its
@@ -210,11 +213,6 @@ __global__ __launch_bounds__(256) void attn_decode_group_kernel(AttnArgs a, cons
     const int keyc = key < len ? key : len - 1;
 #pragma unroll
     for (int e = 0; e < DPT / 8; ++e) kr[j][e].load(K + static_cast<long long>(keyc) * DK + qq * DPT + e * 8);
-#pragma unroll
-    for (int i = 0; i < KPT; ++i) {
-      const int vk = k0 + j * CH + ks + i * NKS;
-      vr[j][i].load(Vp + static_cast<long long>(vk < len ? vk : len - 1) * DK + dg * 8);
-    }
   }
   if (tid < DK) s_q[tid] = static_cast<float>(static_cast<const T*>(a.q)[static_cast<size_t>(bh) * DK + tid]);
   __syncthreads();
@@ -233,6 +231,13 @@ __global__ __launch_bounds__(256) void attn_decode_group_kernel(AttnArgs a, cons
   mx = wave_max_dpp(mx);
   if (lane == 0) s_red[wave] = mx;
   __syncthreads();
+#pragma unroll
+  for (int j = 0; j < G; ++j)
+#pragma unroll
+    for (int i = 0; i < KPT; ++i) {
+      const int vk = k0 + j * CH + ks + i * NKS;
+      vr[j][i].load(Vp + static_cast<long long>(vk < len ? vk : len - 1) * DK + dg * 8);
+    }
   mx = fmaxf(fmaxf(s_red[0], s_red[1]), fmaxf(s_red[2], s_red[3]));
   float lsum = 0.f;
 #pragma unroll
