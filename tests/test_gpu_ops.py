@@ -338,6 +338,24 @@ def test_linear_skinny_fp16(gpu, rows, k, epi):
     assert np.all(np.abs(out - want) <= tol), float(np.max(np.abs(out - want) / tol))
 
 
+@pytest.mark.parametrize("rows,k,n", [(9, 2048, 8200), (32, 1024, 32000), (64, 512, 8198),
+                                      (33, 1024, 8192), (17, 1536, 12345)])
+def test_linear_skinny_wide_fp16(gpu, rows, k, n):
+    """Head-like shapes (8 < rows <= 64, N >= 8192, no epilogue, K a multiple of 512):
+    x staged once per workgroup, each wave streaming 16 W rows over the whole K; ragged
+    N against the 64-row workgroup and the 4-column stores. K = 1536 (not a multiple of
+    512) and 33 rows at K = 1024 (x too large for two workgroups' LDS) take the skinny
+    kernel: both give x·Wᵀ within the fp16 bound."""
+    rng = np.random.default_rng(rows * 1000 + n)
+    x = rng.standard_normal((rows, k)).astype(np.float16)
+    w = (rng.standard_normal((k, n)) * (1.0 / np.sqrt(k))).astype(np.float16)
+    out = np.asarray(_k().linear(x, w, None, epilogue=0)).astype(np.float64)
+    acc = (x.astype(np.float64) @ w.astype(np.float64))
+    want = acc.astype(np.float16).astype(np.float64)
+    tol = 2.0 * 2.0 ** -10 * (np.abs(acc) + np.abs(want)) + 1e-4
+    assert np.all(np.abs(out - want) <= tol), float(np.max(np.abs(out - want) / tol))
+
+
 @pytest.mark.parametrize("rows,k,n,epi", [(4096, 256, 4096, 0), (4096, 192, 4224, 1),
                                           (4096, 128, 4224, 2), (3000, 256, 4224, 3),
                                           (4096, 128, 4099, 3), (4096, 64, 4097, 2),
