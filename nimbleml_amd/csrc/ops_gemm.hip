@@ -788,8 +788,8 @@ __global__ __launch_bounds__(256) void skinny_f16_kernel(LinearArgs a, unsigned 
       pre_r[t] = static_cast<float>(static_cast<const half_t*>(a.resid)[static_cast<size_t>(m) * N + ec]);
     }
   }
-  // Operands of one step of U 32-wide k blocks (and the RMSNorm gains with NORM). The
-  // first step is issued before the RMSNorm statistics so both share a round trip.
+  // Operands of one step of U 32-wide k blocks (and the RMSNorm gains with NORM); the
+  // first step shares its round trip with the RMSNorm statistics.
   half8 av[U], bv[U][MT], gv[U];
   const half_t* gp = NORM ? static_cast<const half_t*>(a.norm_g) + kbeg + kk : nullptr;
   auto load = [&](int k) {
@@ -805,27 +805,33 @@ __global__ __launch_bounds__(256) void skinny_f16_kernel(LinearArgs a, unsigned 
       if constexpr (NORM) gv[u] = *reinterpret_cast<const half8*>(gp + k + u * 32);
     }
   };
-  load(0);
-  half8 inv8[MT];
+  // RMSNorm statistics (NORM): lane group g = lane / 16 sums the g-th quarter of the
+  // K/16 pieces of rows t·16 + r in order; the quarters are added as (q0 + q1) + (q2 + q3)
+  // by lane exchanges (the same value in all four groups). With K = 1024 the loads are
+  // issued before the operands': they return first, and the statistics are formed while
+  // the operands are in flight. No barrier.
+  const int np = K / 16, nq4 = np / 4, g = lane >> 4;
+  float sqs[MT];
+  const float* sps[MT];
+  floatx4 v4[MT][4];
   if constexpr (NORM) {
-    // Lane group g = lane / 16 sums the g-th quarter of the K/16 pieces of rows t·16 + r
-    // in order; the quarters are added as (q0 + q1) + (q2 + q3) by lane exchanges (the
-    // same value in all four groups). No barrier: these loads overlap the operands'.
-    const int np = K / 16, nq4 = np / 4, g = lane >> 4;
-    float sqs[MT];
-    const float* sps[MT];
 #pragma unroll
     for (int t = 0; t < MT; ++t) {  // rows clamped to 0 past M (their result is discarded)
       const int row = t * 16 + r;
       sps[t] = a.ssq_in + static_cast<size_t>(row < M ? row : 0) * np + g * nq4;
       sqs[t] = 0.f;
     }
-    if (nq4 == 16) {  // K = 1024: every tile's quarter in one batch of 16-byte loads
-      floatx4 v4[MT][4];
+    if (nq4 == 16) {
 #pragma unroll
       for (int t = 0; t < MT; ++t)
 #pragma unroll
         for (int e = 0; e < 4; ++e) v4[t][e] = *reinterpret_cast<const floatx4*>(sps[t] + 4 * e);
+    }
+  }
+  load(0);
+  half8 inv8[MT];
+  if constexpr (NORM) {
+    if (nq4 == 16) {  // K = 1024: every tile's quarter in one batch of 16-byte loads
 #pragma unroll
       for (int t = 0; t < MT; ++t)
 #pragma unroll
