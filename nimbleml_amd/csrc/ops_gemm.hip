@@ -780,12 +780,23 @@ __global__ __launch_bounds__(256) void skinny_f16_kernel(LinearArgs a, unsigned 
   const int ec = n0 + ei < N ? n0 + ei : N - 1;
   float pre_b = 0.f, pre_r[MT];
   if constexpr (EPI != EPI_NONE) pre_b = static_cast<float>(static_cast<const half_t*>(a.bias)[ec]);
+  // EPI_QKV: the row's cache position (pos_base) is loaded here too, and the destination
+  // of each output (q, or the K/V cache row) is formed below while the operands are in
+  // flight, not after them.
+  int pre_pos[MT];
 #pragma unroll
   for (int t = 0; t < MT; ++t) {
     pre_r[t] = 0.f;
-    if constexpr (EPI == EPI_BIAS_RESID) {
-      const int m = t * 16 + ej < M ? t * 16 + ej : M - 1;
+    pre_pos[t] = 0;
+    const int m = t * 16 + ej < M ? t * 16 + ej : M - 1;
+    if constexpr (EPI == EPI_BIAS_RESID)
       pre_r[t] = static_cast<float>(static_cast<const half_t*>(a.resid)[static_cast<size_t>(m) * N + ec]);
+    if constexpr (EPI == EPI_QKV) {
+      const QKVDst& q = a.qkv;
+      int b = m;  // row segments: (b << 16) | s; else b = m / S
+      if (q.row_seg) b = q.row_seg[m] >> 16;
+      else if (q.S != 1) b = m / q.S;
+      pre_pos[t] = q.pos_base ? q.pos_base[b] : 0;
     }
   }
   // Operands of one step of U 32-wide k blocks (and the RMSNorm gains with NORM); the
@@ -859,6 +870,30 @@ __global__ __launch_bounds__(256) void skinny_f16_kernel(LinearArgs a, unsigned 
       inv8[t] = half8{hv, hv, hv, hv, hv, hv, hv, hv};
     }
   }
+  half_t* qdst[MT];
+  if constexpr (EPI == EPI_QKV) {
+    const QKVDst& q = a.qkv;
+    const int which = ec / q.d, within = ec - which * q.d;
+    const int hd = within / q.dk, j = within - hd * q.dk;
+#pragma unroll
+    for (int t = 0; t < MT; ++t) {
+      const int m = t * 16 + ej < M ? t * 16 + ej : M - 1;
+      int b = m, sp = 0;
+      if (q.row_seg) {
+        const int rs = q.row_seg[m];
+        b = rs >> 16;
+        sp = rs & 0xffff;
+      } else if (q.S != 1) {
+        b = m / q.S;
+        sp = m - b * q.S;
+      }
+      qdst[t] = which == 0
+          ? static_cast<half_t*>(q.q) + ((static_cast<size_t>(b) * q.H + hd) * q.S + sp) * q.dk + j
+          : static_cast<half_t*>(which == 1 ? q.k : q.v) + b * q.kv_stride_b + hd * q.kv_stride_h +
+                static_cast<long long>(pre_pos[t] + sp) * q.dk + j;
+      asm volatile("" ::"v"(qdst[t]));  // formed here, before the operands are waited for
+    }
+  }
   for (int k = 0; k < kq; k += 32 * U) {
     if constexpr (NORM) {
 #pragma unroll
@@ -921,7 +956,14 @@ __global__ __launch_bounds__(256) void skinny_f16_kernel(LinearArgs a, unsigned 
     const int j = ej, i = ei;
     const int m = t * 16 + j, n = n0 + i;
     float v = 0.f;
-    if (m < M && n < N) v = epilogue_with<half_t, EPI>(a, m, n, sum[t], pre_b, pre_r[t]);
+    if constexpr (EPI == EPI_QKV) {
+      if (m < M && n < N) {
+        v = rnd<half_t>(rnd<half_t>(sum[t]) + pre_b);
+        *qdst[t] = static_cast<half_t>(v);
+      }
+    } else if (m < M && n < N) {
+      v = epilogue_with<half_t, EPI>(a, m, n, sum[t], pre_b, pre_r[t]);
+    }
     if constexpr (EPI == EPI_BIAS_RESID) {
       if (a.ssq_out) {  // this tile's piece of the row's sum of squares (16 lanes = 1 row)
         const float sq = row16_sum_dpp(rnd<half_t>(v * v));
