@@ -295,6 +295,23 @@ __device__ __forceinline__ void load_row(const T* W, long long row, RowSlice<T, 
     s.v[j] = *reinterpret_cast<const typename V16<T>::type*>(p + j * 64 * RowSlice<T, K>::VEC);
 }
 
+// acc + Σ_e a[e]·b[e] over one 16-byte piece: fp16 pairs on v_dot2_f32_f16 (the two
+// products exact in fp32), fp32 by fused multiply-adds.
+template <typename T>
+__device__ __forceinline__ float dot16(const typename V16<T>::type& a, const typename V16<T>::type& b,
+                                       float acc) {
+  if constexpr (sizeof(T) == 2) {
+    typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+#pragma unroll
+    for (int e = 0; e < 8; e += 2)
+      acc = __builtin_amdgcn_fdot2(h2{a[e], a[e + 1]}, h2{b[e], b[e + 1]}, acc, false);
+  } else {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) acc += a[e] * b[e];
+  }
+  return acc;
+}
+
 // Lane-partial dot product of a row slice with x (LDS, same slicing); not reduced.
 template <typename T, int K>
 __device__ __forceinline__ float dot_slice(const RowSlice<T, K>& s, const T* x) {
@@ -305,8 +322,7 @@ __device__ __forceinline__ float dot_slice(const RowSlice<T, K>& s, const T* x) 
   for (int j = 0; j < RowSlice<T, K>::J; ++j) {
     const typename V16<T>::type xv =
         *reinterpret_cast<const typename V16<T>::type*>(x + (j * 64 + lane) * VEC);
-#pragma unroll
-    for (int e = 0; e < VEC; ++e) acc += static_cast<float>(s.v[j][e]) * static_cast<float>(xv[e]);
+    acc = dot16<T>(s.v[j], xv, acc);
   }
   return acc;
 }
@@ -356,10 +372,7 @@ template <typename T, int K>
 __device__ __forceinline__ float dot_regs(const RowSlice<T, K>& w, const RowSlice<T, K>& y) {
   float acc = 0.f;
 #pragma unroll
-  for (int j = 0; j < RowSlice<T, K>::J; ++j)
-#pragma unroll
-    for (int e = 0; e < RowSlice<T, K>::VEC; ++e)
-      acc += static_cast<float>(w.v[j][e]) * static_cast<float>(y.v[j][e]);
+  for (int j = 0; j < RowSlice<T, K>::J; ++j) acc = dot16<T>(w.v[j], y.v[j], acc);
   return acc;
 }
 
