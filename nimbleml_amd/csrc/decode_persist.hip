@@ -298,8 +298,8 @@ __device__ __forceinline__ void load_row(const T* W, long long row, RowSlice<T, 
 // acc + Σ_e a[e]·b[e] over one 16-byte piece: fp16 pairs on v_dot2_f32_f16 (the two
 // products exact in fp32), fp32 by fused multiply-adds.
 template <typename T>
-__device__ __forceinline__ float dot16(const typename V16<T>::type& a, const typename V16<T>::type& b,
-                                       float acc) {
+__device__ __forceinline__ float dot16(const typename V16<T>::type& a,
+                                       const typename V16<T>::type& b, float acc) {
   if constexpr (sizeof(T) == 2) {
     typedef _Float16 h2 __attribute__((ext_vector_type(2)));
 #pragma unroll
@@ -343,21 +343,31 @@ __device__ __forceinline__ void rmsnorm_slice(const T* x, const RowSlice<T, D>& 
 #pragma unroll
   for (int j = 0; j < J; ++j) {
     xv[j] = *reinterpret_cast<const typename V16<T>::type*>(x + (j * 64 + lane) * VEC);
+    if constexpr (sizeof(T) == 2) {
+      // rnd(v·v) is the fp16 product (packed, two per instruction); pairs of squares are
+      // added to the fp32 sum by v_dot2_f32_f16 against (1, 1)
+      typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+      const typename V16<T>::type sq = xv[j] * xv[j];
+      const h2 one2 = {static_cast<_Float16>(1.0f), static_cast<_Float16>(1.0f)};
 #pragma unroll
-    for (int e = 0; e < VEC; ++e) {
-      const float v = static_cast<float>(xv[j][e]);
-      acc += rnd<T>(v * v);
+      for (int e = 0; e < VEC; e += 2)
+        acc = __builtin_amdgcn_fdot2(h2{sq[e], sq[e + 1]}, one2, acc, false);
+    } else {
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) {
+        const float v = static_cast<float>(xv[j][e]);
+        acc += rnd<T>(v * v);
+      }
     }
   }
   const float m = wave_sum_dpp(acc) / static_cast<float>(D);
   const float r = sqrtf(m + 1e-5f);
   if constexpr (sizeof(T) == 2) {
-    const float inv = rnd<T>(1.0f / r);
+    // rnd(rnd(x·inv)·g) with inv rounded to fp16: two fp16 products (packed)
+    const T hv = static_cast<T>(rnd<T>(1.0f / r));
+    const typename V16<T>::type inv8 = {hv, hv, hv, hv, hv, hv, hv, hv};
 #pragma unroll
-    for (int j = 0; j < J; ++j)
-#pragma unroll
-      for (int e = 0; e < VEC; ++e)
-        y.v[j][e] = static_cast<T>(rnd<T>(static_cast<float>(xv[j][e]) * inv) * static_cast<float>(g.v[j][e]));
+    for (int j = 0; j < J; ++j) y.v[j] = (xv[j] * inv8) * g.v[j];
   } else {
 #pragma unroll
     for (int j = 0; j < J; ++j)
