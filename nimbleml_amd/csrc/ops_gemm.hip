@@ -183,6 +183,14 @@ __device__ __forceinline__ void epilogue_run8(const LinearArgs& a, int m, int n,
   const int N = a.N;
   if constexpr (EPI == EPI_QKV) {
     const QKVDst& q = a.qkv;
+    if (q.dk & 7) {  // a run of 8 may cross a head: element by element
+#pragma unroll
+      for (int e = 0; e < 8; ++e)
+        if (n + e < N)
+          epilogue_with<half_t, EPI_QKV>(a, m, n + e, static_cast<float>(h[e]),
+                                         static_cast<float>(static_cast<const half_t*>(a.bias)[n + e]), 0.f);
+      return;
+    }
     int b, s;
     if (q.row_seg) {
       const int rs = q.row_seg[m];
@@ -204,7 +212,7 @@ __device__ __forceinline__ void epilogue_run8(const LinearArgs& a, int m, int n,
       bv = *reinterpret_cast<const half8*>(bias);
     } else {
 #pragma unroll
-      for (int e = 0; e < 8; ++e) bv[e] = bias[e];  // a run of 8 stays inside one head
+      for (int e = 0; e < 8; ++e) bv[e] = bias[e];  // dk % 8 == 0: a run stays inside one head
     }
     const half8 o = h + bv;  // fp16 adds round as rnd(float + float) does
     if (vec) {
@@ -286,6 +294,67 @@ __device__ __forceinline__ void epilogue_staged(const LinearArgs& a, int m0, int
   const bool vec8 = (N & 7) == 0 && aligned;
   constexpr int CH = C / 8;              // 16-byte runs per region row
   constexpr int IT = R * CH / 64;        // runs per lane
+  if constexpr (EPI == EPI_QKV) if ((a.qkv.dk & 7) == 0) {
+    // A lane's runs all sit in one column (the 64 lanes cover whole region rows), so the
+    // column's destination (q / k / v, head, lane within the head) is resolved once, and
+    // the row's (sequence, position) is stepped from run to run instead of divided. With
+    // dk a multiple of 8 (so is d = H·dk) a run of 8 columns stays inside one head.
+    static_assert(64 % CH == 0, "runs of a lane share a column");
+    constexpr int RS = 64 / CH;  // region rows between a lane's runs
+    const QKVDst& q = a.qkv;
+    const int c8 = lane % CH, n = n0 + wn * C + c8 * 8;
+    const int which = n / q.d, within = n - which * q.d;
+    const int hd = within / q.dk, j = within - hd * q.dk;
+    half_t* dst0 = static_cast<half_t*>(which == 0 ? q.q : which == 1 ? q.k : q.v);
+    half8 bv = {0, 0, 0, 0, 0, 0, 0, 0};
+    const bool vec = vec8 && n + 7 < N;
+    if (n < N) {
+      if (vec) {
+        bv = *reinterpret_cast<const half8*>(static_cast<const half_t*>(a.bias) + n);
+      } else {
+#pragma unroll
+        for (int e = 0; e < 8; ++e)
+          if (n + e < N) bv[e] = static_cast<const half_t*>(a.bias)[n + e];
+      }
+    }
+    const int mfirst = m0 + wm * R + lane / CH;
+    int b = 0, sq = 0;
+    if (!q.row_seg) {
+      b = mfirst / q.S;
+      sq = mfirst - b * q.S;
+    }
+#pragma unroll
+    for (int it = 0; it < IT; ++it) {
+      const int row = lane / CH + it * RS, m = mfirst + it * RS;
+      if (it > 0 && !q.row_seg) {
+        sq += RS;
+        while (sq >= q.S) {
+          sq -= q.S;
+          ++b;
+        }
+      }
+      if (m >= M || n >= N) continue;
+      int bb = b, ss = sq;
+      if (q.row_seg) {
+        const int rs = q.row_seg[m];
+        bb = rs >> 16;
+        ss = rs & 0xffff;
+      }
+      half_t* dst = which == 0
+          ? dst0 + ((static_cast<size_t>(bb) * q.H + hd) * q.S + ss) * q.dk + j
+          : dst0 + bb * q.kv_stride_b + hd * q.kv_stride_h +
+                static_cast<long long>((q.pos_base ? q.pos_base[bb] : 0) + ss) * q.dk + j;
+      const half8 o = *reinterpret_cast<const half8*>(reg + row * P + c8 * 8) + bv;
+      if (vec) {
+        *reinterpret_cast<half8*>(dst) = o;
+      } else {
+#pragma unroll
+        for (int e = 0; e < 8; ++e)
+          if (n + e < N) dst[e] = o[e];
+      }
+    }
+    return;
+  }
 #pragma unroll
   for (int it = 0; it < IT; ++it) {
     const int id = it * 64 + lane, row = id / CH, c8 = id - row * CH;
