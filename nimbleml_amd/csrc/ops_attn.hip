@@ -436,7 +436,10 @@ __global__ __launch_bounds__(64) void attn_combine_kernel(AttnArgs a, const int3
 //                (registers for the whole walk); lane l then holds query l%32 and
 //                keys 8(r/4) + 4(l/32) + r%4 of each 32-key tile in register r;
 //   online softmax per query: lane-local over its 16 keys, one xor-32 shuffle with
-//                the lane holding the other 16 (scores rounded as in the scalar path);
+//                the lane holding the other 16. R16 (calls that store the softmax
+//                statistics for the backward, which recomputes the scores from them):
+//                scores rounded to fp16 as in the scalar path; otherwise the scores
+//                stay fp32 accumulators (one FMA and one exp2 per score);
 //   Oᵀ += Vᵀ·Pᵀ  A = Vᵀ (32 dims × 16 keys) from LDS, B = Pᵀ in fp16 straight from the
 //                Sᵀ registers: B's k-slot j of lane l is key 8(j/4) + 4(l/32) + j%4 of
 //                the 16-key block, and A is read with the same key order;
@@ -446,7 +449,7 @@ __global__ __launch_bounds__(64) void attn_combine_kernel(AttnArgs a, const int3
 // tiles are dispatched last-first (the causal walk is longest for them).
 constexpr int kFQ = 128, kFK = 64;
 
-template <int DK>
+template <int DK, bool R16>
 __global__ __launch_bounds__(256, 2) void attn_prefill_mfma_kernel(AttnArgs a) {
 #pragma clang fp contract(off)
   constexpr int KS = DK / 16;  // 16-dim steps of q·k
@@ -481,6 +484,7 @@ __global__ __launch_bounds__(256, 2) void attn_prefill_mfma_kernel(AttnArgs a) {
   // the exact quotient of an fp16 by s is never within 2^-19 (relative) of an fp16
   // rounding midpoint, far beyond the product's 2^-23 error.
   const float rscale = 1.0f / scale_t;
+  const float cscale = 1.4426950408889634f / scale_t;  // log2(e) / scale (fp32 scores)
   const int qw = q0 + wave * 32;           // first query of this wave
   const int myq = qw + (lane & 31);        // this lane's query
   const int hi = lane >> 5;                // which half of the wave
@@ -567,82 +571,146 @@ __global__ __launch_bounds__(256, 2) void attn_prefill_mfma_kernel(AttnArgs a) {
         st[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ka, qb[ks], st[t], 0, 0, 0);
       }
     }
-    // Scores as fp16 pairs (registers r = 2c, 2c + 1): rnd(rnd(q·k)·rscale) is one mixed
-    // fma with an fp16 result (the exact product rounds as its fp32 rounding does, see
-    // rscale), the running maximum a packed fp16 max.
-    typedef _Float16 half2v __attribute__((ext_vector_type(2)));
-    half2v sp[2][8];
-    half2v mp = {static_cast<_Float16>(-INFINITY), static_cast<_Float16>(-INFINITY)};
-    auto score = [&](float acc) {
-      return static_cast<_Float16>(__builtin_fmaf(static_cast<float>(static_cast<_Float16>(acc)), rscale, 0.f));
-    };
-    if (k0 + kFK - 1 > base + qw) {  // the tile reaches past some query of this wave: mask
+    if constexpr (R16) {
+      // Scores as fp16 pairs (registers r = 2c, 2c + 1): rnd(rnd(q·k)·rscale) is one mixed
+      // fma with an fp16 result (the exact product rounds as its fp32 rounding does, see
+      // rscale), the running maximum a packed fp16 max.
+      typedef _Float16 half2v __attribute__((ext_vector_type(2)));
+      half2v sp[2][8];
+      half2v mp = {static_cast<_Float16>(-INFINITY), static_cast<_Float16>(-INFINITY)};
+      auto score = [&](float acc) {
+        return static_cast<_Float16>(__builtin_fmaf(static_cast<float>(static_cast<_Float16>(acc)), rscale, 0.f));
+      };
+      if (k0 + kFK - 1 > base + qw) {  // the tile reaches past some query of this wave: mask
 #pragma unroll
-      for (int t = 0; t < 2; ++t)
+        for (int t = 0; t < 2; ++t)
 #pragma unroll
-        for (int c = 0; c < 8; ++c) {
-          half2v v;
+          for (int c = 0; c < 8; ++c) {
+            half2v v;
 #pragma unroll
-          for (int u = 0; u < 2; ++u) {
-            const int r = 2 * c + u;
-            const int key = k0 + t * 32 + 8 * (r >> 2) + 4 * hi + (r & 3);
-            v[u] = (key <= qpos && key < kend) ? score(st[t][r]) : static_cast<_Float16>(-INFINITY);
+            for (int u = 0; u < 2; ++u) {
+              const int r = 2 * c + u;
+              const int key = k0 + t * 32 + 8 * (r >> 2) + 4 * hi + (r & 3);
+              v[u] = (key <= qpos && key < kend) ? score(st[t][r]) : static_cast<_Float16>(-INFINITY);
+            }
+            sp[t][c] = v;
+            mp = __builtin_elementwise_max(mp, v);
           }
-          sp[t][c] = v;
-          mp = __builtin_elementwise_max(mp, v);
-        }
-    } else {  // every key of the tile precedes every query of the wave
+      } else {  // every key of the tile precedes every query of the wave
 #pragma unroll
-      for (int t = 0; t < 2; ++t)
+        for (int t = 0; t < 2; ++t)
 #pragma unroll
-        for (int c = 0; c < 8; ++c) {
-          const half2v v = {score(st[t][2 * c]), score(st[t][2 * c + 1])};
-          sp[t][c] = v;
-          mp = __builtin_elementwise_max(mp, v);
-        }
-    }
-    float mx = fmaxf(m, fmaxf(static_cast<float>(mp[0]), static_cast<float>(mp[1])));
-    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-    constexpr float kLog2e = 1.4426950408889634f;
-    const float alpha = (mx == -INFINITY) ? 1.f : __builtin_amdgcn_exp2f((m - mx) * kLog2e);
-    const float nmx = -mx * kLog2e;  // exp(s - mx) as exp2(s·log2 e − mx·log2 e), one FMA a score
-    l *= alpha;
-    // alpha is exactly 1 where the running max did not grow; the accumulators are
-    // rescaled only when some lane's max grew (rare after the first tiles)
-    if (__any(mx > m)) {
-#pragma unroll
-      for (int t = 0; t < OT; ++t)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) o[t][r] *= alpha;
-    }
-#pragma unroll
-    for (int t = 0; t < 2; ++t)
-#pragma unroll
-      for (int kb = 0; kb < 2; ++kb) {
-        half8 pb;
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-          // mx is finite (key 0 precedes every query, and tiles run from key 0), so a
-          // masked score gives exp2(-inf) = 0
-          const float sv = static_cast<float>(sp[t][(8 * kb + j) >> 1][j & 1]);
-          const float p = __builtin_amdgcn_exp2f(__builtin_fmaf(sv, kLog2e, nmx));
-          l += p;
-          pb[j] = static_cast<half_t>(p);
-        }
-        const int kblk = t * 32 + kb * 16 + 4 * hi;
-#pragma unroll
-        for (int ot = 0; ot < OT; ++ot) {
-          const half_t* vrow = &Vt[ot * 32 + (lane & 31)][kblk];
-          half8 va;
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            va[e] = vrow[e];
-            va[4 + e] = vrow[8 + e];
+          for (int c = 0; c < 8; ++c) {
+            const half2v v = {score(st[t][2 * c]), score(st[t][2 * c + 1])};
+            sp[t][c] = v;
+            mp = __builtin_elementwise_max(mp, v);
           }
-          o[ot] = __builtin_amdgcn_mfma_f32_32x32x16_f16(va, pb, o[ot], 0, 0, 0);
-        }
       }
-    m = mx;
+      float mx = fmaxf(m, fmaxf(static_cast<float>(mp[0]), static_cast<float>(mp[1])));
+      mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+      constexpr float kLog2e = 1.4426950408889634f;
+      const float alpha = (mx == -INFINITY) ? 1.f : __builtin_amdgcn_exp2f((m - mx) * kLog2e);
+      const float nmx = -mx * kLog2e;  // exp(s - mx) as exp2(s·log2 e − mx·log2 e), one FMA a score
+      l *= alpha;
+      // alpha is exactly 1 where the running max did not grow; the accumulators are
+      // rescaled only when some lane's max grew (rare after the first tiles)
+      if (__any(mx > m)) {
+#pragma unroll
+        for (int t = 0; t < OT; ++t)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) o[t][r] *= alpha;
+      }
+#pragma unroll
+      for (int t = 0; t < 2; ++t)
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb) {
+          half8 pb;
+#pragma unroll
+          for (int j = 0; j < 8; ++j) {
+            // mx is finite (key 0 precedes every query, and tiles run from key 0), so a
+            // masked score gives exp2(-inf) = 0
+            const float sv = static_cast<float>(sp[t][(8 * kb + j) >> 1][j & 1]);
+            const float p = __builtin_amdgcn_exp2f(__builtin_fmaf(sv, kLog2e, nmx));
+            l += p;
+            pb[j] = static_cast<half_t>(p);
+          }
+          const int kblk = t * 32 + kb * 16 + 4 * hi;
+#pragma unroll
+          for (int ot = 0; ot < OT; ++ot) {
+            const half_t* vrow = &Vt[ot * 32 + (lane & 31)][kblk];
+            half8 va;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              va[e] = vrow[e];
+              va[4 + e] = vrow[8 + e];
+            }
+            o[ot] = __builtin_amdgcn_mfma_f32_32x32x16_f16(va, pb, o[ot], 0, 0, 0);
+          }
+        }
+      m = mx;
+    } else {
+      // Scores kept in fp32, in units of q·k (m is the running maximum of q·k): the
+      // maximum over the raw accumulators (the scale is positive), then
+      // p = exp2(q·k·c − m·c) with c = log2(e) / scale, one FMA and one exp2 a score, and
+      // the row sum over the fp16 probabilities the PV product uses, two per v_dot2.
+      if (k0 + kFK - 1 > base + qw) {
+#pragma unroll
+        for (int t = 0; t < 2; ++t)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            const int key = k0 + t * 32 + 8 * (r >> 2) + 4 * hi + (r & 3);
+            if (!(key <= qpos && key < kend)) st[t][r] = -INFINITY;
+          }
+      }
+      float mloc = st[0][0];
+#pragma unroll
+      for (int t = 0; t < 2; ++t)
+#pragma unroll
+        for (int r = 0; r < 16; ++r)
+          if (t + r > 0) mloc = fmaxf(mloc, st[t][r]);
+      float mx = fmaxf(m, mloc);
+      mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+      const float alpha = (mx == -INFINITY) ? 1.f : __builtin_amdgcn_exp2f((m - mx) * cscale);
+      const float nmx = -mx * cscale;
+      l *= alpha;
+      if (__any(mx > m)) {
+#pragma unroll
+        for (int t = 0; t < OT; ++t)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) o[t][r] *= alpha;
+      }
+      typedef _Float16 half2v __attribute__((ext_vector_type(2)));
+      const half2v ones = {static_cast<_Float16>(1.0f), static_cast<_Float16>(1.0f)};
+#pragma unroll
+      for (int t = 0; t < 2; ++t)
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb) {
+          half8 pb;
+#pragma unroll
+          for (int j = 0; j < 8; j += 2) {
+            // mx is finite (key 0 precedes every query), so a masked score gives 0
+            const float p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(st[t][8 * kb + j], cscale, nmx));
+            const float p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(st[t][8 * kb + j + 1], cscale, nmx));
+            const half2v pp = {static_cast<_Float16>(p0), static_cast<_Float16>(p1)};
+            l = __builtin_amdgcn_fdot2(pp, ones, l, false);
+            pb[j] = pp[0];
+            pb[j + 1] = pp[1];
+          }
+          const int kblk = t * 32 + kb * 16 + 4 * hi;
+#pragma unroll
+          for (int ot = 0; ot < OT; ++ot) {
+            const half_t* vrow = &Vt[ot * 32 + (lane & 31)][kblk];
+            half8 va;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              va[e] = vrow[e];
+              va[4 + e] = vrow[8 + e];
+            }
+            o[ot] = __builtin_amdgcn_mfma_f32_32x32x16_f16(va, pb, o[ot], 0, 0, 0);
+          }
+        }
+      m = mx;
+    }
   }
   l += __shfl_xor(l, 32, 64);
   if (myq < S && a.lse && hi == 0) a.lse[static_cast<size_t>(bh) * a.S + myq] = m + logf(l);
@@ -833,7 +901,11 @@ int prefill_typed(const AttnArgs& a, hipStream_t st) {
   }
   if constexpr (sizeof(T) == 2 && (DK == 64 || DK == 128)) {
     dim3 grid((a.S + kFQ - 1) / kFQ, a.B * a.H);
-    attn_prefill_mfma_kernel<DK><<<grid, 256, 0, st>>>(a);
+    // fp16-rounded scores where the backward recomputes them from the statistics
+    if (a.lse || a.m_out)
+      attn_prefill_mfma_kernel<DK, true><<<grid, 256, 0, st>>>(a);
+    else
+      attn_prefill_mfma_kernel<DK, false><<<grid, 256, 0, st>>>(a);
     NML_LAUNCHED();
     return 0;
   }
