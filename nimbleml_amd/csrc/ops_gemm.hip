@@ -13,6 +13,7 @@
 //  * skinny_f16: 8 < M ≤ 64 rows (batched decode), MFMA 16×16×32 with optional split-K
 //    and a fused RMSNorm of x (see its comment).
 #include <cstdlib>
+#include <mutex>
 
 #include "gemm_big.hpp"
 #include "kernels.hpp"
@@ -172,14 +173,85 @@ typedef _Float16 half4v __attribute__((ext_vector_type(4)));
 // stores are 16-byte vectors, 8 rows × 128 bytes per wave instruction, instead of 2-byte
 // elements. Widths that are not a multiple of 8 (or operands not 16-byte aligned) take
 // the same path element by element.
+// fp16 tanh by table for the 256 × 256 GELU epilogue: entry i is rnd(tanh_h(t)) for the
+// fp16 t of magnitude code kTanhLo + i, so a lookup equals the computed form bit for bit.
+// Below the range rnd(tanh t) = t (tanh t = t·(1 − t²/3 + …) and t²/3 < 2^-12, less than
+// half an fp16 ulp below t); from code 0x4500 (|t| = 5) on, rnd(tanh t) = 1, the last
+// entry's value (1 − tanh t < 2^-12), so indices clamp there (inf included; a NaN t comes
+// only from a NaN x, whose GELU is NaN whatever tanh returns). 16 KiB, copied into LDS
+// past the epilogue's staging region.
+constexpr int kTanhLo = 0x2500, kTanhN = 0x2000;
+constexpr size_t kTanhBytes = kTanhN * sizeof(half_t);
+__device__ half_t g_tanh_tab[kTanhN];
+
+__global__ __launch_bounds__(256) void tanh_tab_kernel() {
+  const int i = blockIdx.x * 256 + threadIdx.x;
+  if (i >= kTanhN) return;
+  const unsigned short code = static_cast<unsigned short>(kTanhLo + i);
+  const float t = static_cast<float>(__builtin_bit_cast(half_t, code));
+  g_tanh_tab[i] = static_cast<half_t>(tanh_h(t));
+}
+
+// Fills g_tanh_tab on the current device before its first use (once per device; the
+// first call waits for the fill on `st`, so it cannot be made under stream capture).
+int ensure_tanh_tab(hipStream_t st) {
+  static std::mutex mu;
+  static bool ready[64] = {};
+  int dev = 0;
+  NML_HIP(hipGetDevice(&dev));
+  NML_REQUIRE(dev >= 0 && dev < 64, "device ordinal %d out of range", dev);
+  std::lock_guard<std::mutex> lock(mu);
+  if (!ready[dev]) {
+    tanh_tab_kernel<<<kTanhN / 256, 256, 0, st>>>();
+    NML_LAUNCHED();
+    NML_HIP(hipStreamSynchronize(st));
+    ready[dev] = true;
+  }
+  return 0;
+}
+
+// gelu8_f16 with its tanh looked up in the LDS copy of g_tanh_tab (byte address tab).
+__device__ __forceinline__ half8 gelu8_f16_tab(half8 x, const half_t* tab) {
+#pragma clang fp contract(off)
+  const half_t k = static_cast<half_t>(0.7978845608028654f);
+  const half_t c = static_cast<half_t>(0.044715f);
+  half8 t = x * c;
+  t = t * x;
+  t = t * x;
+  t = x + t;
+  t = t * k;
+  typedef unsigned short u16x8 __attribute__((ext_vector_type(8)));
+  const u16x8 tb = __builtin_bit_cast(u16x8, t);
+  const u16x8 ab = tb & static_cast<unsigned short>(0x7fff);
+  const u16x8 sg = tb & static_cast<unsigned short>(0x8000);
+  const unsigned short* tabu = reinterpret_cast<const unsigned short*>(tab);
+  unsigned int v[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) v[e] = tabu[min(max(static_cast<int>(ab[e]) - kTanhLo, 0), kTanhN - 1)];
+  // all eight reads issued, and complete here, on every lane (in range by the clamp): the
+  // selects below stay selects instead of branches around single reads
+  asm volatile("" : "+v"(v[0]), "+v"(v[1]), "+v"(v[2]), "+v"(v[3]), "+v"(v[4]), "+v"(v[5]),
+               "+v"(v[6]), "+v"(v[7]));
+  u16x8 r;
+#pragma unroll
+  for (int e = 0; e < 8; ++e)
+    r[e] = ab[e] < kTanhLo ? tb[e] : static_cast<unsigned short>(v[e] | sg[e]);
+  const half8 tu = __builtin_bit_cast(half8, r);
+  const half8 a = x * static_cast<half_t>(0.5f);
+  const half8 bb = tu + static_cast<half_t>(1.0f);
+  return a * bb;
+}
+
 template <int TM, int TN>
 struct Staged {
   static constexpr int R = TM / 2, C = TN / 4, P = C + 8;  // region rows, columns, pitch
   static constexpr size_t Lds = static_cast<size_t>(8) * R * P * sizeof(half_t);
 };
 
-template <int EPI>
-__device__ __forceinline__ void epilogue_run8(const LinearArgs& a, int m, int n, half8 h, bool vec) {
+// TAB: the GELU's tanh from the LDS table at tanh_tab.
+template <int EPI, bool TAB = false>
+__device__ __forceinline__ void epilogue_run8(const LinearArgs& a, int m, int n, half8 h, bool vec,
+                                              const half_t* tanh_tab = nullptr) {
   const int N = a.N;
   if constexpr (EPI == EPI_QKV) {
     const QKVDst& q = a.qkv;
@@ -244,7 +316,12 @@ __device__ __forceinline__ void epilogue_run8(const LinearArgs& a, int m, int n,
   if constexpr (EPI != EPI_NONE) {
     p = h + bv;
     if constexpr (EPI == EPI_BIAS) o = p;
-    else if constexpr (EPI == EPI_BIAS_GELU) o = gelu8_f16(p);
+    else if constexpr (EPI == EPI_BIAS_GELU) {
+      if constexpr (TAB)
+        o = gelu8_f16_tab(p, tanh_tab);
+      else
+        o = gelu8_f16(p);
+    }
     else o = rv + p;  // EPI_BIAS_RESID
   }
   half_t* pre = EPI == EPI_BIAS_GELU && a.pre_out ? static_cast<half_t*>(a.pre_out) + row : nullptr;
@@ -294,6 +371,9 @@ __device__ __forceinline__ void epilogue_staged(const LinearArgs& a, int m0, int
   const bool vec8 = (N & 7) == 0 && aligned;
   constexpr int CH = C / 8;              // 16-byte runs per region row
   constexpr int IT = R * CH / 64;        // runs per lane
+  // 256 × 256 GELU tiles: the tanh table sits right past the staging region
+  constexpr bool kGeluTab = EPI == EPI_BIAS_GELU && TM == 256;
+  const half_t* tab = reinterpret_cast<const half_t*>(lds_raw + Staged<TM, TN>::Lds);
   if constexpr (EPI == EPI_QKV) if ((a.qkv.dk & 7) == 0) {
     // A lane's runs all sit in one column (the 64 lanes cover whole region rows), so the
     // column's destination (q / k / v, head, lane within the head) is resolved once, and
@@ -360,7 +440,7 @@ __device__ __forceinline__ void epilogue_staged(const LinearArgs& a, int m0, int
     const int id = it * 64 + lane, row = id / CH, c8 = id - row * CH;
     const int m = m0 + wm * R + row, n = n0 + wn * C + c8 * 8;
     const half8 h = *reinterpret_cast<const half8*>(reg + row * P + c8 * 8);
-    if (m < M && n < N) epilogue_run8<EPI>(a, m, n, h, vec8 && n + 7 < N);
+    if (m < M && n < N) epilogue_run8<EPI, kGeluTab>(a, m, n, h, vec8 && n + 7 < N, tab);
   }
 }
 
@@ -570,6 +650,18 @@ __global__ __launch_bounds__(kHT, TM == 256 ? 1 : 4) void gemm_f16_big_kernel(Li
     for (int j = 0; j < JB; ++j)
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
+  if constexpr (EPI == EPI_BIAS_GELU && TM == 256) {
+    // the tanh table into LDS past the staging region, 1 KiB per direct-to-LDS load (two
+    // per wave); the main loop's first stage wait (vmcnt(0), then a barrier) publishes it
+    static_assert(kTanhBytes == 16 * 1024, "two 1 KiB blocks per wave");
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int blk = 2 * wave + j;
+      __builtin_amdgcn_global_load_lds(
+          (const __attribute__((address_space(1))) void*)(g_tanh_tab + blk * 512 + lane * 8),
+          (__attribute__((address_space(3))) void*)(lds_raw + Staged<TM, TN>::Lds + blk * 1024), 16, 0, 0);
+    }
+  }
   big::mainloop<TM, TN, true>(static_cast<const half_t*>(a.x), a.lda, static_cast<const half_t*>(a.w), a.K,
                               a.M, a.N, 0, a.K / kHK, m0, n0, lds_raw, acc);
 
@@ -582,9 +674,12 @@ __global__ __launch_bounds__(kHT, TM == 256 ? 1 : 4) void gemm_f16_big_kernel(Li
 template <int EPI, int GM, int TM, int TN>
 int gemm_big_launch_gm(const LinearArgs& a, hipStream_t st) {
   static bool attr = false;
-  // main loop: 128 KiB (256 × 256) or 64 KiB (128 × 128); epilogue: 144 KiB or 36 KiB
-  constexpr size_t lds = big::Shape<TM, TN>::Lds > Staged<TM, TN>::Lds ? big::Shape<TM, TN>::Lds
-                                                                       : Staged<TM, TN>::Lds;
+  // main loop: 128 KiB (256 × 256) or 64 KiB (128 × 128); epilogue: 144 KiB or 36 KiB;
+  // 256 × 256 GELU: 16 KiB more for the tanh table (160 KiB, all of a CU's LDS)
+  constexpr size_t lds = (big::Shape<TM, TN>::Lds > Staged<TM, TN>::Lds ? big::Shape<TM, TN>::Lds
+                                                                        : Staged<TM, TN>::Lds) +
+                         (EPI == EPI_BIAS_GELU && TM == 256 ? kTanhBytes : 0);
+  if constexpr (EPI == EPI_BIAS_GELU && TM == 256) NML_TRY(ensure_tanh_tab(st));
   if (!attr) {
     NML_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(&gemm_f16_big_kernel<EPI, GM, TM, TN>),
                                 hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds)));

@@ -75,6 +75,18 @@ def test_gelu_fp16_every_input_bit_exact(gpu):
     bad = ~same(got, want[: grid.size].reshape(grid.shape))
     print(f"GEMM epilogue: {int(bad.sum())} of {grid.size} differ")
     assert not bad.any()
+    # 4096 × 4096 outputs take the 256 × 256 tiles, whose GELU looks tanh up in a table:
+    # every finite input (repeated to fill 4096 × 64) through x·[I | 0] + 0
+    reps = -(-4096 * 64 // x.size)
+    big = np.tile(x, reps)[: 4096 * 64].reshape(4096, 64)
+    wbig = np.zeros((64, 4096), np.float16)
+    wbig[:, :64] = eye
+    got = np.asarray(_k().linear(big, wbig, np.zeros(4096, np.float16), epilogue=2))
+    wbig_want = np.tile(want, reps)[: 4096 * 64].reshape(4096, 64)
+    bad = ~same(got[:, :64], wbig_want)
+    print(f"GEMM epilogue, 256 x 256 tiles: {int(bad.sum())} of {big.size} differ")
+    assert not bad.any(), (big[bad][:8], got[:, :64][bad][:8], wbig_want[bad][:8])
+    assert not got[:, 64:].any()
 
 
 @pytest.mark.parametrize("name", ["ops_fp32", "ops_fp16"])
