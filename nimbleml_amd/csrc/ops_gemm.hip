@@ -248,8 +248,10 @@ struct Staged {
   static constexpr size_t Lds = static_cast<size_t>(8) * R * P * sizeof(half_t);
 };
 
-// TAB: the GELU's tanh from the LDS table at tanh_tab.
-template <int EPI, bool TAB = false>
+// TAB: the GELU's tanh from the LDS table at tanh_tab. NT: 16-byte stores non-temporal
+// (outputs of the 256 × 256 tiles, too large to stay in the caches for their consumer,
+// are streamed past L2 instead of evicting the operand lines the other tiles still read).
+template <int EPI, bool TAB = false, bool NT = false>
 __device__ __forceinline__ void epilogue_run8(const LinearArgs& a, int m, int n, half8 h, bool vec,
                                               const half_t* tanh_tab = nullptr) {
   const int N = a.N;
@@ -288,7 +290,10 @@ __device__ __forceinline__ void epilogue_run8(const LinearArgs& a, int m, int n,
     }
     const half8 o = h + bv;  // fp16 adds round as rnd(float + float) does
     if (vec) {
-      *reinterpret_cast<half8*>(dst) = o;
+      if constexpr (NT)
+        __builtin_nontemporal_store(o, reinterpret_cast<half8*>(dst));
+      else
+        *reinterpret_cast<half8*>(dst) = o;
     } else {
 #pragma unroll
       for (int e = 0; e < 8; ++e) dst[e] = o[e];
@@ -326,7 +331,10 @@ __device__ __forceinline__ void epilogue_run8(const LinearArgs& a, int m, int n,
   }
   half_t* pre = EPI == EPI_BIAS_GELU && a.pre_out ? static_cast<half_t*>(a.pre_out) + row : nullptr;
   if (vec) {
-    *reinterpret_cast<half8*>(out + n) = o;
+    if constexpr (NT)
+      __builtin_nontemporal_store(o, reinterpret_cast<half8*>(out + n));
+    else
+      *reinterpret_cast<half8*>(out + n) = o;
     if (pre) *reinterpret_cast<half8*>(pre + n) = p;
   } else {
 #pragma unroll
@@ -426,7 +434,10 @@ __device__ __forceinline__ void epilogue_staged(const LinearArgs& a, int m0, int
                 static_cast<long long>((q.pos_base ? q.pos_base[bb] : 0) + ss) * q.dk + j;
       const half8 o = *reinterpret_cast<const half8*>(reg + row * P + c8 * 8) + bv;
       if (vec) {
-        *reinterpret_cast<half8*>(dst) = o;
+        if constexpr (TM == 256)  // non-temporal, as epilogue_run8's NT
+          __builtin_nontemporal_store(o, reinterpret_cast<half8*>(dst));
+        else
+          *reinterpret_cast<half8*>(dst) = o;
       } else {
 #pragma unroll
         for (int e = 0; e < 8; ++e)
@@ -440,7 +451,7 @@ __device__ __forceinline__ void epilogue_staged(const LinearArgs& a, int m0, int
     const int id = it * 64 + lane, row = id / CH, c8 = id - row * CH;
     const int m = m0 + wm * R + row, n = n0 + wn * C + c8 * 8;
     const half8 h = *reinterpret_cast<const half8*>(reg + row * P + c8 * 8);
-    if (m < M && n < N) epilogue_run8<EPI, kGeluTab>(a, m, n, h, vec8 && n + 7 < N, tab);
+    if (m < M && n < N) epilogue_run8<EPI, kGeluTab, TM == 256>(a, m, n, h, vec8 && n + 7 < N, tab);
   }
 }
 
