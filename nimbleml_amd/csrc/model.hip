@@ -8,6 +8,7 @@
 //   x  = x + (a·W_oᵀ + b_o);  xn = RMSNorm₂(x)
 //   h  = GELU(xn·W₁ᵀ + b₁);   x = x + (h·W₂ᵀ + b₂)
 // then xn = RMSNorm_f(x) and logits = xn·Eᵀ (tied head).
+#include <algorithm>
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
@@ -1042,8 +1043,15 @@ int nml_model_generate(nml_model* m, const int64_t* prompts, size_t prompt_strid
     if (use_graph) {
       hipGraph_t graph = nullptr;
       hipGraphExec_t exec = nullptr;
+      // G steps per graph (fewer launches; each step reads the position the previous one
+      // advanced on the device), the remainder one step per launch of a second graph
+      const char* ge = std::getenv("NIMBLEML_GRAPH_STEPS");
+      const int G = std::max(1, std::min(steps, ge ? atoi(ge) : 8));
+      hipGraph_t graph1 = nullptr;
+      hipGraphExec_t exec1 = nullptr;
+      int r1 = 0;
       NML_HIP(hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal));
-      const int r1 = step();
+      for (int i = 0; i < G && r1 == 0; ++i) r1 = step();
       hipError_t ec = hipStreamEndCapture(st, &graph);
       if (r1 != 0) {
         if (graph) (void)hipGraphDestroy(graph);
@@ -1051,13 +1059,30 @@ int nml_model_generate(nml_model* m, const int64_t* prompts, size_t prompt_strid
       }
       NML_HIP(ec);
       NML_HIP(hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0));
+      if (steps % G) {
+        NML_HIP(hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal));
+        r1 = step();
+        ec = hipStreamEndCapture(st, &graph1);
+        if (r1 != 0) {
+          if (graph1) (void)hipGraphDestroy(graph1);
+          (void)hipGraphExecDestroy(exec);
+          (void)hipGraphDestroy(graph);
+          return -1;
+        }
+        NML_HIP(ec);
+        NML_HIP(hipGraphInstantiate(&exec1, graph1, nullptr, nullptr, 0));
+      }
       NML_HIP(hipEventRecord(e0, st));
-      for (int t = 0; t < steps && rc == 0; ++t)
+      for (int t = 0; t + G <= steps && rc == 0; t += G)
         if (hipGraphLaunch(exec, st) != hipSuccess) rc = -1;
+      for (int t = 0; t < steps % G && rc == 0; ++t)
+        if (hipGraphLaunch(exec1, st) != hipSuccess) rc = -1;
       NML_HIP(hipEventRecord(e1, st));
       (void)hipStreamSynchronize(st);
       (void)hipGraphExecDestroy(exec);
       (void)hipGraphDestroy(graph);
+      if (exec1) (void)hipGraphExecDestroy(exec1);
+      if (graph1) (void)hipGraphDestroy(graph1);
       NML_REQUIRE(rc == 0, "hipGraphLaunch failed");
     } else {
       NML_HIP(hipEventRecord(e0, st));
