@@ -346,6 +346,34 @@ __device__ __forceinline__ void epilogue_run8(const LinearArgs& a, int m, int n,
   }
 }
 
+// epilogue_run8's 16-byte case with its bias and residual runs already in registers.
+template <int EPI, bool TAB, bool NT>
+__device__ __forceinline__ void epilogue_vec8(const LinearArgs& a, int m, int n, half8 h, half8 bv, half8 rv,
+                                              const half_t* tanh_tab) {
+  const size_t row = static_cast<size_t>(m) * a.N;
+  half8 o = h, p = h;
+  if constexpr (EPI != EPI_NONE) {
+    p = h + bv;
+    if constexpr (EPI == EPI_BIAS) {
+      o = p;
+    } else if constexpr (EPI == EPI_BIAS_GELU) {
+      if constexpr (TAB)
+        o = gelu8_f16_tab(p, tanh_tab);
+      else
+        o = gelu8_f16(p);
+    } else {
+      o = rv + p;  // EPI_BIAS_RESID
+    }
+  }
+  half_t* out = static_cast<half_t*>(a.out) + row + n;
+  if constexpr (NT)
+    __builtin_nontemporal_store(o, reinterpret_cast<half8*>(out));
+  else
+    *reinterpret_cast<half8*>(out) = o;
+  if constexpr (EPI == EPI_BIAS_GELU)
+    if (a.pre_out) *reinterpret_cast<half8*>(static_cast<half_t*>(a.pre_out) + row + n) = p;
+}
+
 template <int EPI, int TM, int TN>
 __device__ __forceinline__ void epilogue_staged(const LinearArgs& a, int m0, int n0,
                                                 const floatx16 (&acc)[TM / 64][TN / 128],
@@ -445,6 +473,38 @@ __device__ __forceinline__ void epilogue_staged(const LinearArgs& a, int m0, int
       }
     }
     return;
+  }
+  if constexpr (EPI != EPI_QKV) {
+    // A lane's runs share one column (lane % CH): its bias is loaded once and its rows'
+    // residual runs all before the first store, so the loads' latencies overlap instead of
+    // each run waiting for its own (the residual may be the output itself: every run reads
+    // its elements before any is written). Rows past M read row M − 1 and store nothing.
+    static_assert(64 % CH == 0, "runs of a lane share a column");
+    constexpr int RS = 64 / CH;
+    const int c8 = lane % CH, n = n0 + wn * C + c8 * 8;
+    if (vec8 && n + 7 < N) {
+      const half8 z = {0, 0, 0, 0, 0, 0, 0, 0};
+      half8 bv = z, rv[IT];
+      if constexpr (EPI != EPI_NONE) bv = *reinterpret_cast<const half8*>(static_cast<const half_t*>(a.bias) + n);
+      const int mfirst = m0 + wm * R + lane / CH;
+#pragma unroll
+      for (int it = 0; it < IT; ++it) {
+        rv[it] = z;
+        if constexpr (EPI == EPI_BIAS_RESID) {
+          const int mc = min(mfirst + it * RS, M - 1);
+          rv[it] = *reinterpret_cast<const half8*>(static_cast<const half_t*>(a.resid) +
+                                                   static_cast<size_t>(mc) * N + n);
+        }
+      }
+#pragma unroll
+      for (int it = 0; it < IT; ++it) {
+        const int m = mfirst + it * RS;
+        if (m >= M) continue;
+        const half8 h = *reinterpret_cast<const half8*>(reg + (lane / CH + it * RS) * P + c8 * 8);
+        epilogue_vec8<EPI, kGeluTab, TM == 256>(a, m, n, h, bv, rv[it], tab);
+      }
+      return;
+    }
   }
 #pragma unroll
   for (int it = 0; it < IT; ++it) {
