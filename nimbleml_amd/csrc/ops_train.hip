@@ -1770,12 +1770,40 @@ __global__ __launch_bounds__(256) void rope_bwd_kernel(T* __restrict__ dqkv, int
 template <typename T>
 __global__ __launch_bounds__(256) void embed_bwd_tok_kernel(const T* __restrict__ g,
                                                             const int64_t* __restrict__ ids,
-                                                            float* __restrict__ demb, int d, int V) {
-  const int r = blockIdx.x;
+                                                            float* __restrict__ demb, int d, int V,
+                                                            int n) {
+  // demb[id] += the rows of g whose token is id, in ascending row order — the order of
+  // the reference's scatter (kernels/embedding_scatter.py:39-80, np.add.at or the native
+  // loop, called from layers/embedding.py:138-142) — so the sum does not
+  // depend on scheduling. Block r does the work when row r is its id's first row: the
+  // other blocks of that id find an earlier match and leave.
+  const int r = blockIdx.x, t = threadIdx.x, w = t >> 6, lane = t & 63;
   const long long id = ids[r];
-  if (id < 0 || id >= V) return;
-  for (int c = threadIdx.x; c < d; c += 256)
-    atomicAdd(demb + id * d + c, static_cast<float>(g[static_cast<long long>(r) * d + c]));
+  if (id < 0 || id >= V) return;  // uniform over the block
+  __shared__ int s_cnt[4];
+  __shared__ int s_idx[256];
+  for (int j0 = 0; j0 < r; j0 += 256) {
+    const int j = j0 + t;
+    if (__syncthreads_or(j < r && ids[j] == id)) return;
+  }
+  float* dst = demb + id * d;
+  for (int j0 = r; j0 < n; j0 += 256) {
+    const int j = j0 + t;
+    const bool hit = j < n && ids[j] == id;
+    const unsigned long long m = __ballot(hit);
+    if (lane == 0) s_cnt[w] = __popcll(m);
+    __syncthreads();
+    int off = 0;
+    for (int q = 0; q < w; ++q) off += s_cnt[q];
+    const int tot = s_cnt[0] + s_cnt[1] + s_cnt[2] + s_cnt[3];
+    if (hit) s_idx[off + __popcll(m & ((1ull << lane) - 1ull))] = j;
+    __syncthreads();
+    for (int q = 0; q < tot; ++q) {
+      const T* src = g + static_cast<long long>(s_idx[q]) * d;
+      for (int c = t; c < d; c += 256) dst[c] += static_cast<float>(src[c]);
+    }
+    __syncthreads();
+  }
 }
 
 template <typename T>
@@ -1988,9 +2016,9 @@ int launch_embed_backward(int dt, const void* g, const int64_t* ids, float* demb
                           int S, int d, int V, hipStream_t st) {
   if (B * S == 0) return 0;
   if (dt == F16)
-    embed_bwd_tok_kernel<half_t><<<B * S, 256, 0, st>>>(static_cast<const half_t*>(g), ids, demb, d, V);
+    embed_bwd_tok_kernel<half_t><<<B * S, 256, 0, st>>>(static_cast<const half_t*>(g), ids, demb, d, V, B * S);
   else
-    embed_bwd_tok_kernel<float><<<B * S, 256, 0, st>>>(static_cast<const float*>(g), ids, demb, d, V);
+    embed_bwd_tok_kernel<float><<<B * S, 256, 0, st>>>(static_cast<const float*>(g), ids, demb, d, V, B * S);
   NML_LAUNCHED();
   if (dpos) {
     const dim3 grid((d + 255) / 256, S);

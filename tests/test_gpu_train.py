@@ -504,3 +504,24 @@ def test_interleaved_losses_and_inference_before_backward(gpu):
     loss_b.backward()
     _, want = _oracle(w, cfg, ids_b, lab_b)
     _compare(_named_grads(m), want)
+
+
+def test_token_embedding_gradient_is_deterministic_with_repeated_ids(gpu):
+    """A 12-token vocabulary over 2 x 300 positions: every id repeats ~50 times, on both
+    sides of the 256-row chunk boundaries of the scatter. The token-embedding gradient sums
+    an id's rows in ascending row order, as the reference's scatter does, so two backward
+    passes give the same bits, and both are within RTOL of the oracle."""
+    cfg = GPTConfig(12, 64, 4, 1, 320)
+    m, w = _model(cfg, seed=31)
+    ids = random_ids((2, 300), cfg.vocab_size, seed=7)
+    labels = random_ids((600,), cfg.vocab_size, seed=8)
+    assert np.bincount(ids.ravel(), minlength=12).min() >= 20
+    grads = []
+    for _ in range(2):
+        for p in m.parameters():
+            p.zero_grad()
+        m.compute_loss(ids, labels).backward()
+        grads.append(_named_grads(m))
+    _, want = _oracle(w, cfg, ids, labels)
+    _compare(grads[0], want)
+    assert np.array_equal(grads[0]["token_emb.weights"], grads[1]["token_emb.weights"])
