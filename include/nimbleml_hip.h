@@ -84,7 +84,7 @@ int nml_linear_device(const void* x, size_t ld_x, const void* w_t, const void* b
  * sdpa_cuda.cu:40-77, 235-243), as kernels/fused_sdpa.py:91-115 calls it. q, k, v, out:
  * (bh, seq, dk); scores s_ij = (q_i·k_j)·scale for keys j ≤ i — `scale` multiplies (the
  * caller passes 1/sqrt(dk)); m, l: (bh, seq), each query row's max score and
- * Σ_j exp(s_ij − m). Head dims 8, 16, 32, 64, 128. */
+ * Σ_j exp(s_ij − m). Any head dim 1 ≤ dk ≤ 256 (sdpa_cuda.cu:237 takes dk ≤ 256). */
 int nml_flash_sdpa_forward_device(const float* q, const float* k, const float* v, float* out,
                                   float* m, float* l, size_t bh, size_t seq, size_t dk,
                                   float scale);
@@ -118,6 +118,25 @@ int nml_causal_attention_device(const void* q, const void* k, const void* v, voi
 int nml_sdpa_forward_device(const void* q, const void* k, const void* v, const void* mask,
                             void* out, size_t bh, size_t seq, size_t dk, float scale_div,
                             int causal, int dtype);
+
+/* One new query per (row, head) against a KV cache: the attention of a decode step behind
+ * the forward_with_cache(ids, cache) seam that generate() probes for
+ * (models/generate.py:93-100), with the scores of kernels/fused_sdpa.py:71-78:
+ * s_j = (q·k_j) / scale_div (scale_div = sqrt(dk), attention.py:135), softmax over keys
+ * 0 ≤ j < lens[b], then Σ_j p_j·v_j. The reference has no KV cache and no such kernel; it
+ * re-forwards the whole sequence per token (generate.py:101-103).
+ *   q:      (batch, heads, dk) — the new token's query of each row
+ *   kcache, vcache: (batch, heads, max_seq, dk) — one head's keys are contiguous
+ *   lens:   device int32 (batch): keys attended per row, 1 ≤ lens[b] ≤ max_seq; a length
+ *           outside that range is clamped into it and sets bit 0 of *err (err: device int,
+ *           may be NULL; the caller clears it)
+ *   out:    (batch, heads·dk) — merged heads, as the W_o projection reads them
+ * Any head dim 1 ≤ dk ≤ 256; float32 or float16 (dtype). Asynchronous on the library
+ * stream; the library keeps a grow-only workspace (allocated and cleared on the first call
+ * at a larger shape, so do not capture that call into a graph). */
+int nml_decode_attention_device(const void* q, const void* kcache, const void* vcache,
+                                const int32_t* lens, void* out, size_t batch, size_t heads,
+                                size_t max_seq, size_t dk, float scale_div, int* err, int dtype);
 
 /* Mean tied-head cross-entropy (kernels/fused_tied_crossentropy.py:8-24 →
  * fused_crossentropy.py:14-30) without materialising all (rows, vocab) logits at once.

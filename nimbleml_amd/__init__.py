@@ -4,7 +4,7 @@ The same user-facing API as the reference for this path — ``GPT`` (forward,
 ``compute_loss``, ``forward_with_cache``, ``generate``), ``generate``, ``Tensor``,
 ``save``/``load`` — executed by hand-written HIP kernels through the C-ABI in
 include/nimbleml_hip.h. Importing requires the built library
-(``python -m nimbleml_amd.build``); there is no CPU fallback.
+(``python nimbleml_amd/build.py``); there is no CPU fallback.
 """
 from nimbleml_amd import np_backend
 from nimbleml_amd._native import DeviceArray

@@ -21,7 +21,7 @@ LIB_PATH = os.environ.get("NIMBLEML_HIP_LIB", os.path.join(_PKG, "_lib", "libnim
 
 _INSTALL_HINT = (
     "nimbleml_amd requires its HIP library (libnimbleml_hip.so). Build it with\n"
-    "  python -m nimbleml_amd.build\n"
+    "  python nimbleml_amd/build.py\n"
     "(hipcc for gfx950, ROCm 7)."
 )
 
@@ -59,6 +59,7 @@ _SIGS = {
     "nml_flash_sdpa_backward_device": [vp, vp, vp, vp, vp, vp, vp, vp, vp, sz, sz, sz, f32],
     "nml_rmsnorm_backward_device": [vp, vp, vp, vp, vp, vp, vp, sz, sz, f32],
     "nml_causal_attention_device": [vp, vp, vp, vp, sz, sz, sz, f32, i32],
+    "nml_decode_attention_device": [vp, vp, vp, vp, vp, sz, sz, sz, sz, f32, vp, i32],
     "nml_sdpa_forward_device": [vp, vp, vp, vp, vp, sz, sz, sz, f32, i32, i32],
     "nml_tied_ce_forward_device": [vp, vp, vp, sz, sz, sz, i64, i32, C.POINTER(C.c_double), i32],
     "nml_tied_ce_forward_device_noalloc": [vp, vp, vp, sz, sz, sz, i64, i32,

@@ -2,7 +2,7 @@
 
 Each ``csrc/*.hip`` file is compiled with hipcc for ``--offload-arch=gfx950`` (in
 parallel), then linked into one shared library exporting the C-ABI declared in
-``include/nimbleml_hip.h``. Usage: ``python -m nimbleml_amd.build``.
+``include/nimbleml_hip.h``. Usage: ``python nimbleml_amd/build.py``.
 """
 from __future__ import annotations
 

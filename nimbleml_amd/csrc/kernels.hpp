@@ -111,6 +111,10 @@ int launch_gelu(int dt, const void* x, void* out, float* tanh_u, size_t n, hipSt
 // (B, H, S, dk); keys/values at positions [0, pos(b) + S) are read from
 // k/v at b·kv_stride_b + h·kv_stride_h + p·dk; query s sits at pos(b) + s and sees
 // keys p ≤ pos(b) + s. Output is merged-head (B·S, H·dk).
+// Largest head dim the attention kernels take (the reference's device flash kernel
+// accepts dk ≤ 256, native/src/sdpa_cuda.cu:237).
+constexpr int kMaxHeadDim = 256;
+
 struct AttnArgs {
   const void* q;
   const void* k;

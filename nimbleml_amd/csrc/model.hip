@@ -521,6 +521,8 @@ int nml_model_create(int vocab, int d_model, int num_heads, int num_layers, int 
               "model dimensions must be positive");
   NML_REQUIRE(d_model % num_heads == 0, "d_model (%d) must be divisible by num_heads (%d).",
               d_model, num_heads);
+  NML_REQUIRE(d_model / num_heads <= kMaxHeadDim, "head_dim %d above %d (d_model / num_heads)",
+              d_model / num_heads, kMaxHeadDim);
   const int vec = dtype == F16 ? 8 : 4;
   NML_REQUIRE(d_model % vec == 0 && d_ff % vec == 0,
               "d_model and d_ff must be multiples of %d for 16-byte loads", vec);

@@ -64,8 +64,8 @@ __global__ void split3_kernel(const float* __restrict__ src, float* __restrict__
 }
 
 int attn_shape_ok(size_t bh, size_t seq, size_t dk) {
-  NML_REQUIRE(dk == 8 || dk == 16 || dk == 32 || dk == 64 || dk == 128,
-              "attention: head_dim %zu unsupported (8, 16, 32, 64, 128)", dk);
+  NML_REQUIRE(dk >= 1 && dk <= (size_t)kMaxHeadDim, "attention: head_dim %zu outside [1, %d]", dk,
+              kMaxHeadDim);
   NML_REQUIRE(bh <= 65535 && bh * seq <= 0x7fffffff, "attention: %zu × %zu rows too many", bh,
               seq);
   return 0;
@@ -131,6 +131,40 @@ int tied_ce(const void* hidden, const void* weights, const int64_t* labels, size
   NML_REQUIRE(herr == 0, "cross-entropy: label out of range [0, %zu)", vocab);
   *loss = host[2];
   return 0;
+}
+
+// Library-owned workspace of nml_decode_attention_device: the rows' last positions
+// (int32), then the decode kernels' partials. The grouped kernel leaves its partial slots
+// zeroed after every launch, so the buffer is cleared once, when it is (re)allocated.
+struct DecodeWs {
+  void* p = nullptr;
+  size_t bytes = 0;
+  int ensure(size_t want, hipStream_t st) {
+    if (want <= bytes) return 0;
+    if (p) {
+      NML_HIP(hipStreamSynchronize(st));
+      NML_HIP(hipFree(p));
+      p = nullptr;
+      bytes = 0;
+    }
+    NML_HIP(hipMalloc(&p, want));
+    bytes = want;
+    NML_HIP(hipMemsetAsync(p, 0, want, st));
+    return 0;
+  }
+};
+DecodeWs g_decode_ws;
+
+// pos[b] = lens[b] − 1 for the decode kernels, with lens clamped into [1, max_seq] so no
+// key past the cache is read; a clamped length sets bit 0 of *err.
+__global__ void lens_to_pos_kernel(const int32_t* __restrict__ lens, int32_t* __restrict__ pos,
+                                   int n, int max_seq, int* __restrict__ err) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  const int len = lens[i];
+  const int c = len < 1 ? 1 : (len > max_seq ? max_seq : len);
+  if (c != len && err) __hip_atomic_fetch_or(err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  pos[i] = c - 1;
 }
 
 constexpr int kMaxDevices = 64;
@@ -263,6 +297,44 @@ int nml_flash_sdpa_forward_device(const float* q, const float* k, const float* v
   a.m_out = m;
   a.l_out = l;
   return launch_attention_prefill(F32, a, nml::stream());
+}
+
+int nml_decode_attention_device(const void* q, const void* kcache, const void* vcache,
+                                const int32_t* lens, void* out, size_t batch, size_t heads,
+                                size_t max_seq, size_t dk, float scale_div, int* err, int dtype) {
+  NML_TRY(check_dtype(dtype));
+  NML_REQUIRE(dk >= 1 && dk <= (size_t)kMaxHeadDim, "decode attention: head_dim %zu outside [1, %d]",
+              dk, kMaxHeadDim);
+  NML_REQUIRE(batch * heads <= 65535, "decode attention: %zu × %zu (row, head) pairs too many", batch,
+              heads);
+  NML_REQUIRE(max_seq >= 1 && max_seq <= 65536, "decode attention: max_seq %zu outside [1, 65536]",
+              max_seq);
+  NML_REQUIRE(scale_div > 0.f && std::isfinite(scale_div),
+              "decode attention: scale_div must be positive");
+  NML_REQUIRE(lens != nullptr, "decode attention: lens is required");
+  if (batch == 0 || heads == 0) return 0;
+  hipStream_t st = nml::stream();
+  const size_t pos_b = ((batch * 4 + 255) / 256) * 256;
+  NML_TRY(g_decode_ws.ensure(
+      pos_b + attention_decode_workspace((int)batch, (int)heads, (int)dk, (int)max_seq), st));
+  int32_t* pos = static_cast<int32_t*>(g_decode_ws.p);
+  lens_to_pos_kernel<<<(unsigned)((batch + 255) / 256), 256, 0, st>>>(lens, pos, (int)batch,
+                                                                     (int)max_seq, err);
+  NML_LAUNCHED();
+  AttnArgs a{};
+  a.q = q;
+  a.k = kcache;
+  a.v = vcache;
+  a.out = out;
+  a.kv_stride_b = (long long)(heads * max_seq * dk);
+  a.kv_stride_h = (long long)(max_seq * dk);
+  a.B = (int)batch;
+  a.H = (int)heads;
+  a.S = 1;
+  a.dk = (int)dk;
+  a.scale = scale_div;
+  return launch_attention_decode(dtype, a, pos, (int)max_seq, static_cast<char*>(g_decode_ws.p) + pos_b,
+                                 st);
 }
 
 int nml_flash_sdpa_backward_device(const float* grad_out, const float* q, const float* k,

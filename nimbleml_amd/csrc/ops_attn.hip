@@ -8,11 +8,13 @@
 //
 //  * prefill, fp16 head dim 64/128: attn_prefill_mfma_kernel — MFMA flash
 //    attention, 128 queries per workgroup, 64-key K/V tiles in LDS (see its comment);
-//    other types / head dims: attn_prefill_kernel, one wave per 64 queries, scalar.
-//  * decode, head dim ≥ 32: attn_decode_group_kernel — split-K in one launch: each
-//    workgroup scores a group of 64-key chunks of one (sequence, head) and publishes
+//    fp32 head dim 64/128: attn_prefill_f32_mfma; head dims 8/16/32 (and the non-causal
+//    masked form): attn_prefill_kernel, one wave per 64 queries, scalar; any other head
+//    dim ≤ 256: attn_prefill_quad_kernel, four lanes per query.
+//  * decode, head dim 32/64/128/256: attn_decode_group_kernel — split-K in one launch:
+//    each workgroup scores a group of 64-key chunks of one (sequence, head) and publishes
 //    its (max, Σp, Σp·v) as flagged slots; the last workgroup of the (sequence, head)
-//    merges them. Head dims 8/16: attn_decode_small_kernel + attn_combine_kernel.
+//    merges them. Other head dims ≤ 256: attn_decode_small_kernel + attn_combine_kernel.
 #include <cstdlib>
 
 #include "kernels.hpp"
@@ -117,6 +119,112 @@ __global__ __launch_bounds__(64) void attn_prefill_kernel(AttnArgs a) {
     if (a.m_out) {
       a.m_out[static_cast<size_t>(bh) * a.S + s] = m;
       a.l_out[static_cast<size_t>(bh) * a.S + s] = l;
+    }
+  }
+}
+
+// Prefill for any head dim up to 4·DPL (the runtime a.dk: 96, 80, 256, ...), the
+// attn_prefill_kernel semantics (same score roundings, mask, ragged rows and statistics)
+// with four lanes per query: lane `sub` of a query's quad owns dims sub + 4i, so a lane
+// keeps DPL query and output values in registers (at dk 256, 64 + 64 instead of 512). A
+// workgroup takes 64 queries (16 per wave) and walks key tiles of KT rows staged in LDS,
+// zero-padded to 4·DPL columns; a score is the quad's four partial dot products summed
+// by DPP lane moves.
+template <typename T, int DPL>
+__global__ __launch_bounds__(256) void attn_prefill_quad_kernel(AttnArgs a) {
+  constexpr int QW = 64, DKP = 4 * DPL, KT = DPL >= 64 ? 16 : 32;
+  __shared__ T Ks[KT][DKP];
+  __shared__ T Vs[KT][DKP];
+  const int tid = threadIdx.x, sub = tid & 3;
+  const int dk = a.dk;
+  const int bh = blockIdx.y;
+  const int b = bh / a.H, h = bh - (bh / a.H) * a.H;
+  const int s = blockIdx.x * QW + (tid >> 2);
+  const int S = a.seq_len ? a.seq_len[b] : a.S;
+  if (static_cast<int>(blockIdx.x) * QW >= S) return;  // past a ragged sequence's end
+  const int base = a.pos_base ? a.pos_base[b] : 0;
+  const int qpos = base + s;
+  const int last_s = min(S, (blockIdx.x + 1) * QW) - 1;
+  const int kv_end = a.full ? S : base + last_s + 1;
+  const float scale_t = static_cast<float>(static_cast<T>(a.scale));
+  const T* __restrict__ K = static_cast<const T*>(a.k) + b * a.kv_stride_b + h * a.kv_stride_h;
+  const T* __restrict__ Vp = static_cast<const T*>(a.v) + b * a.kv_stride_b + h * a.kv_stride_h;
+  const bool valid = s < S;
+  const T* __restrict__ mrow =
+      a.mask ? static_cast<const T*>(a.mask) + static_cast<size_t>(valid ? s : 0) * S : nullptr;
+  float q[DPL], o[DPL];
+  {
+    const T* qp = static_cast<const T*>(a.q) + ((static_cast<size_t>(bh) * a.S) + (valid ? s : 0)) * dk;
+#pragma unroll
+    for (int i = 0; i < DPL; ++i) {
+      const int d = sub + 4 * i;
+      q[i] = d < dk ? static_cast<float>(qp[d]) : 0.f;
+      o[i] = 0.f;
+    }
+  }
+  float m = -INFINITY, l = 0.f;
+  for (int k0 = 0; k0 < kv_end; k0 += KT) {
+    __syncthreads();  // the previous tile's readers are done
+    for (int e = tid; e < KT * DKP; e += 256) {
+      const int r = e / DKP, c = e - (e / DKP) * DKP, key = k0 + r;
+      const bool in = key < kv_end && c < dk;
+      Ks[r][c] = in ? K[static_cast<long long>(key) * dk + c] : static_cast<T>(0.f);
+      Vs[r][c] = in ? Vp[static_cast<long long>(key) * dk + c] : static_cast<T>(0.f);
+    }
+    __syncthreads();
+    const int nkeys = min(KT, kv_end - k0);
+    for (int j0 = 0; j0 < nkeys; j0 += 16) {
+      float sc[16];
+      float mloc = -INFINITY;
+#pragma unroll
+      for (int jj = 0; jj < 16; ++jj) {
+        const int kj = j0 + jj;  // < KT: rows past nkeys are zero-filled
+        float dot = 0.f;
+#pragma unroll
+        for (int i = 0; i < DPL; ++i) dot += q[i] * static_cast<float>(Ks[kj][sub + 4 * i]);
+        dot = quad_sum_dpp(dot);  // every lane of the quad: no divergence before this
+        float v = -INFINITY;
+        if (kj < nkeys && (a.full || k0 + kj <= qpos)) {
+          v = rnd<T>(rnd<T>(dot) / scale_t);
+          if (mrow) v = rnd<T>(v + static_cast<float>(mrow[k0 + kj]));
+        }
+        sc[jj] = v;
+        mloc = fmaxf(mloc, v);
+      }
+      const float mn = fmaxf(m, mloc);
+      if (mn == -INFINITY) continue;
+      const float alpha = __expf(m - mn);
+      l *= alpha;
+#pragma unroll
+      for (int i = 0; i < DPL; ++i) o[i] *= alpha;
+#pragma unroll
+      for (int jj = 0; jj < 16; ++jj) {
+        const float p = expf(sc[jj] - mn);
+        if (p != 0.f) {
+          l += p;
+          const int kj = j0 + jj;
+#pragma unroll
+          for (int i = 0; i < DPL; ++i) o[i] += p * static_cast<float>(Vs[kj][sub + 4 * i]);
+        }
+      }
+      m = mn;
+    }
+  }
+  if (valid) {
+    const size_t row = (a.row_start ? a.row_start[b] : static_cast<size_t>(b) * a.S) + s;
+    T* out = static_cast<T*>(a.out) + row * a.H * dk + h * dk;
+    const float inv = 1.f / l;
+#pragma unroll
+    for (int i = 0; i < DPL; ++i) {
+      const int d = sub + 4 * i;
+      if (d < dk) out[d] = static_cast<T>(o[i] * inv);
+    }
+    if (sub == 0) {
+      if (a.lse) a.lse[static_cast<size_t>(bh) * a.S + s] = m + logf(l);
+      if (a.m_out) {
+        a.m_out[static_cast<size_t>(bh) * a.S + s] = m;
+        a.l_out[static_cast<size_t>(bh) * a.S + s] = l;
+      }
     }
   }
 }
@@ -275,10 +383,12 @@ __global__ __launch_bounds__(256) void attn_decode_group_kernel(AttnArgs a, cons
   if (tid < DK)
     for (int k2 = 0; k2 < NKS; ++k2) own += s_o[k2][tid];
   if (grp != ng - 1) {  // publish this group's partial and leave
-    if (tid < DK) {
+    // (max, Σp) from the first lane past the head's dims; at DK 256 (no such lane) lane 0
+    constexpr int kStatLane = DK < 256 ? DK : 0;
+    if (tid < DK)
       __hip_atomic_store(pb + grp * PS + 2 + tid, flag | __float_as_uint(own), __ATOMIC_RELAXED,
                          __HIP_MEMORY_SCOPE_AGENT);
-    } else if (tid == DK) {
+    if (tid == kStatLane) {
       __hip_atomic_store(pb + grp * PS, flag | __float_as_uint(mx), __ATOMIC_RELAXED,
                          __HIP_MEMORY_SCOPE_AGENT);
       __hip_atomic_store(pb + grp * PS + 1, flag | __float_as_uint(l), __ATOMIC_RELAXED,
@@ -351,44 +461,48 @@ __global__ __launch_bounds__(256) void attn_decode_group_kernel(AttnArgs a, cons
     __hip_atomic_store(pb + i, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-template <typename T, int DK>
+// Decode attention for head dims outside the group kernel's set (8, 16 and any dk that
+// is not 32, 64, 128 or 256; runtime a.dk ≤ 256): one wave per 64-key chunk, lane j
+// scores key k0 + j, then P·V with each lane owning up to four output dims; the chunk's
+// (max, Σp, Σp·v) go to `part` for attn_combine_kernel.
+template <typename T>
 __global__ __launch_bounds__(64) void attn_decode_small_kernel(AttnArgs a, const int32_t* __restrict__ pos,
                                                          int max_chunks, float* __restrict__ part) {
   const int lane = threadIdx.x;
   const int c = blockIdx.x, bh = blockIdx.y;
   const int b = bh / a.H, h = bh - (bh / a.H) * a.H;
+  const int dk = a.dk;
   const int len = pos[b] + 1;
   const int k0 = c * kTile;
-  float* pp = part + (static_cast<size_t>(bh) * max_chunks + c) * (DK + 2);
+  float* pp = part + (static_cast<size_t>(bh) * max_chunks + c) * (dk + 2);
   if (k0 >= len) return;  // the combine pass only reads chunks below len
   const float scale_t = static_cast<float>(static_cast<T>(a.scale));
   const T* __restrict__ K = static_cast<const T*>(a.k) + b * a.kv_stride_b + h * a.kv_stride_h;
   const T* __restrict__ Vp = static_cast<const T*>(a.v) + b * a.kv_stride_b + h * a.kv_stride_h;
-  const T* __restrict__ qp = static_cast<const T*>(a.q) + static_cast<size_t>(bh) * DK;
+  const T* __restrict__ qp = static_cast<const T*>(a.q) + static_cast<size_t>(bh) * dk;
 
   const int key = k0 + lane;
   float sc = -INFINITY;
   if (key < len) {
-    const T* kr = K + static_cast<long long>(key) * DK;
+    const T* kr = K + static_cast<long long>(key) * dk;
     float dot = 0.f;
-#pragma unroll
-    for (int d = 0; d < DK; ++d) dot += static_cast<float>(qp[d]) * static_cast<float>(kr[d]);
+    for (int d = 0; d < dk; ++d) dot += static_cast<float>(qp[d]) * static_cast<float>(kr[d]);
     sc = rnd<T>(rnd<T>(dot) / scale_t);
   }
   const float mx = wave_max(sc);
   const float p = (key < len) ? expf(sc - mx) : 0.f;
   const float l = wave_sum(p);
   const int nkeys = min(kTile, len - k0);
-  constexpr int DPL = (DK + 63) / 64;  // output dims per lane
+  constexpr int DPL = 4;  // output dims per lane: dk ≤ 256
 #pragma unroll
   for (int t = 0; t < DPL; ++t) {
     const int d = lane + 64 * t;
     float acc = 0.f;
     for (int j = 0; j < nkeys; ++j) {
       const float pj = __shfl(p, j, 64);
-      if (d < DK) acc += pj * static_cast<float>(Vp[static_cast<long long>(k0 + j) * DK + d]);
+      if (d < dk) acc += pj * static_cast<float>(Vp[static_cast<long long>(k0 + j) * dk + d]);
     }
-    if (d < DK) pp[2 + d] = acc;
+    if (d < dk) pp[2 + d] = acc;
   }
   if (lane == 0) {
     pp[0] = mx;
@@ -399,32 +513,33 @@ __global__ __launch_bounds__(64) void attn_decode_small_kernel(AttnArgs a, const
 // Merge of the chunk partials of one (row, head): lane c holds chunk c's (max, Σp) —
 // up to 64 chunks per pass, loaded in parallel — then each lane owns output dims and
 // sums the chunks' Σp·v with weights exp(max_c − M) / Σ_c exp(max_c − M)·Σp_c.
-template <typename T, int DK>
+template <typename T>
 __global__ __launch_bounds__(64) void attn_combine_kernel(AttnArgs a, const int32_t* __restrict__ pos,
                                                           int max_chunks, const float* __restrict__ part) {
   __shared__ float s_w[kCombineMax];
   const int lane = threadIdx.x;
   const int bh = blockIdx.x;
   const int b = bh / a.H, h = bh - (bh / a.H) * a.H;
+  const int dk = a.dk, ps = dk + 2;
   const int len = pos[b] + 1;
   const int nc = (len + kTile - 1) / kTile;
-  const float* pb = part + static_cast<size_t>(bh) * max_chunks * (DK + 2);
+  const float* pb = part + static_cast<size_t>(bh) * max_chunks * ps;
   float M = -INFINITY;
-  for (int c = lane; c < nc; c += 64) M = fmaxf(M, pb[c * (DK + 2)]);
+  for (int c = lane; c < nc; c += 64) M = fmaxf(M, pb[c * ps]);
   M = wave_max(M);
   float den = 0.f;
   for (int c = lane; c < nc; c += 64) {
-    const float w = expf(pb[c * (DK + 2)] - M);
+    const float w = expf(pb[c * ps] - M);
     s_w[c] = w;
-    den += w * pb[c * (DK + 2) + 1];
+    den += w * pb[c * ps + 1];
   }
   den = wave_sum(den);
   __syncthreads();
   const float inv = 1.f / den;
-  T* out = static_cast<T*>(a.out) + static_cast<size_t>(b) * a.H * DK + h * DK;
-  for (int d = lane; d < DK; d += 64) {
+  T* out = static_cast<T*>(a.out) + static_cast<size_t>(b) * a.H * dk + h * dk;
+  for (int d = lane; d < dk; d += 64) {
     float num = 0.f;
-    for (int c = 0; c < nc; ++c) num += s_w[c] * pb[c * (DK + 2) + 2 + d];
+    for (int c = 0; c < nc; ++c) num += s_w[c] * pb[c * ps + 2 + d];
     out[d] = static_cast<T>(num * inv);
   }
 }
@@ -916,45 +1031,66 @@ int prefill_typed(const AttnArgs& a, hipStream_t st) {
 }
 
 template <typename T, int DK>
-int decode_typed(const AttnArgs& a, const int32_t* pos, int max_len, void* ws, hipStream_t st) {
-  if constexpr (DK >= 32) {
-    constexpr int G = dec_groups<T, DK>();
-    const int max_groups = (max_len + kTile * G - 1) / (kTile * G);
-    unsigned long long* part = static_cast<unsigned long long*>(ws);
-    attn_decode_group_kernel<T, DK, G><<<dim3(max_groups, a.B * a.H), 256, 0, st>>>(
-        a, pos, max_groups, part);
-    NML_LAUNCHED();
-  } else {
-    const int max_chunks = (max_len + kTile - 1) / kTile;
-    float* part = static_cast<float*>(ws);
-    attn_decode_small_kernel<T, DK><<<dim3(max_chunks, a.B * a.H), 64, 0, st>>>(a, pos, max_chunks,
-                                                                               part);
-    NML_LAUNCHED();
-    attn_combine_kernel<T, DK><<<a.B * a.H, 64, 0, st>>>(a, pos, max_chunks, part);
-    NML_LAUNCHED();
-  }
+int decode_group(const AttnArgs& a, const int32_t* pos, int max_len, void* ws, hipStream_t st) {
+  constexpr int G = dec_groups<T, DK>();
+  const int max_groups = (max_len + kTile * G - 1) / (kTile * G);
+  unsigned long long* part = static_cast<unsigned long long*>(ws);
+  attn_decode_group_kernel<T, DK, G><<<dim3(max_groups, a.B * a.H), 256, 0, st>>>(
+      a, pos, max_groups, part);
+  NML_LAUNCHED();
   return 0;
 }
 
-#define NML_DK_SWITCH(dk, FN, ...)                                  \
-  switch (dk) {                                                     \
-    case 8: return FN<T, 8>(__VA_ARGS__);                           \
-    case 16: return FN<T, 16>(__VA_ARGS__);                         \
-    case 32: return FN<T, 32>(__VA_ARGS__);                         \
-    case 64: return FN<T, 64>(__VA_ARGS__);                         \
-    case 128: return FN<T, 128>(__VA_ARGS__);                       \
-    default: set_error("attention: head_dim %d unsupported (8, 16, 32, 64, 128)", dk); \
-      return -1;                                                    \
-  }
+template <typename T>
+int decode_chunks(const AttnArgs& a, const int32_t* pos, int max_len, void* ws, hipStream_t st) {
+  const int max_chunks = (max_len + kTile - 1) / kTile;
+  float* part = static_cast<float*>(ws);
+  attn_decode_small_kernel<T><<<dim3(max_chunks, a.B * a.H), 64, 0, st>>>(a, pos, max_chunks, part);
+  NML_LAUNCHED();
+  attn_combine_kernel<T><<<a.B * a.H, 64, 0, st>>>(a, pos, max_chunks, part);
+  NML_LAUNCHED();
+  return 0;
+}
+
+template <typename T, int DPL>
+int prefill_quad(const AttnArgs& a, hipStream_t st) {
+  dim3 grid((a.S + 63) / 64, a.B * a.H);
+  attn_prefill_quad_kernel<T, DPL><<<grid, 256, 0, st>>>(a);
+  NML_LAUNCHED();
+  return 0;
+}
 
 template <typename T>
 int prefill_dk(const AttnArgs& a, hipStream_t st) {
-  NML_DK_SWITCH(a.dk, prefill_typed, a, st);
+  switch (a.dk) {
+    case 8: return prefill_typed<T, 8>(a, st);
+    case 16: return prefill_typed<T, 16>(a, st);
+    case 32: return prefill_typed<T, 32>(a, st);
+    case 64: return prefill_typed<T, 64>(a, st);
+    case 128: return prefill_typed<T, 128>(a, st);
+  }
+  // other head dims: four lanes per query, dims padded to 32, 64, 128 or 256
+  if (a.dk <= 32) return prefill_quad<T, 8>(a, st);
+  if (a.dk <= 64) return prefill_quad<T, 16>(a, st);
+  if (a.dk <= 128) return prefill_quad<T, 32>(a, st);
+  if (a.dk <= kMaxHeadDim) return prefill_quad<T, 64>(a, st);
+  set_error("attention: head_dim %d above %d", a.dk, kMaxHeadDim);
+  return -1;
 }
 
 template <typename T>
 int decode_dk(const AttnArgs& a, const int32_t* pos, int max_len, void* ws, hipStream_t st) {
-  NML_DK_SWITCH(a.dk, decode_typed, a, pos, max_len, ws, st);
+  switch (a.dk) {
+    case 32: return decode_group<T, 32>(a, pos, max_len, ws, st);
+    case 64: return decode_group<T, 64>(a, pos, max_len, ws, st);
+    case 128: return decode_group<T, 128>(a, pos, max_len, ws, st);
+    case 256: return decode_group<T, 256>(a, pos, max_len, ws, st);
+  }
+  if (a.dk < 1 || a.dk > kMaxHeadDim) {
+    set_error("attention: head_dim %d outside [1, %d]", a.dk, kMaxHeadDim);
+    return -1;
+  }
+  return decode_chunks<T>(a, pos, max_len, ws, st);
 }
 
 }  // namespace

@@ -188,8 +188,8 @@ constexpr int kCandMax = 2048;
 
 // Wave 0 draws over n candidates (index order, candx = scaled logits) keeping those
 // ≥ thresh: max, Σ exp, probabilities and the float64 index-order CDF; returns the first
-// kept index whose cdf / total exceeds u (V − 1 if rounding leaves none, as the full
-// scan does). All threads must call it (barriers).
+// kept index whose cdf / total exceeds u (the last kept index if rounding leaves none,
+// where the reference's cdf / cdf[-1] is exactly 1). All threads must call it (barriers).
 template <typename T>
 __device__ int draw_candidates(int V, int n, float thresh, double u, Shared& sh, const int* cand,
                                const float* candx) {
@@ -209,7 +209,7 @@ __device__ int draw_candidates(int V, int n, float thresh, double u, Shared& sh,
     total = wave_sum_d(total);
     // index-order running sums, 64 candidates per round
     double carry = 0.0;
-    int found = 0x7fffffff;
+    int found = 0x7fffffff, last_kept = V - 1;
     for (int j0 = 0; j0 < n && found == 0x7fffffff; j0 += 64) {
       const int j = j0 + l;
       const bool keep = j < n && candx[j] >= thresh;
@@ -222,10 +222,14 @@ __device__ int draw_candidates(int V, int n, float thresh, double u, Shared& sh,
       }
       const bool hit = keep && (carry + inc) / total > u;
       const unsigned long long hits = __ballot(hit);
+      const unsigned long long kept = __ballot(keep);
       if (hits) found = cand[j0 + __ffsll(static_cast<long long>(hits)) - 1];
+      if (kept) last_kept = cand[j0 + 63 - __clzll(static_cast<long long>(kept))];
       carry += __shfl(inc, 63, 64);
     }
-    if (l == 0) sh.found_index = found == 0x7fffffff ? V - 1 : found;
+    // none hit (the scan's running sum ends an ulp below `total`): the reference's
+    // searchsorted over cdf / cdf[-1] lands on the last kept index, where that ratio is 1
+    if (l == 0) sh.found_index = found == 0x7fffffff ? last_kept : found;
   }
   __syncthreads();
   return sh.found_index;
@@ -292,7 +296,8 @@ __device__ __forceinline__ float prev_float(float y) {
 
 // Wave 0 draws over the n candidates (index order; candx = scaled values) keeping those
 // ≥ thr, with max mx: p = exp(x − mx) / Σ exp (float32), then the first kept index whose
-// float64 running sum / total exceeds u (V − 1 if rounding leaves none). n ≤ 64·R.
+// float64 running sum / total exceeds u (the last kept index if rounding leaves none).
+// n ≤ 64·R.
 template <int R>
 __device__ __forceinline__ int draw_kept(int V, int n, float thr, float mx, double u, Shared& sh, const int* cand,
                          const float* candx) {
@@ -316,7 +321,7 @@ __device__ __forceinline__ int draw_kept(int V, int n, float thr, float mx, doub
     }
     total = wave_sum_d(total);
     double carry = 0.0;
-    int found = 0x7fffffff;
+    int found = 0x7fffffff, last_kept = V - 1;
 #pragma unroll
     for (int r = 0; r < R; ++r) {
       if (found != 0x7fffffff || 64 * r >= n) break;
@@ -329,10 +334,13 @@ __device__ __forceinline__ int draw_kept(int V, int n, float thr, float mx, doub
         if (l >= o) inc += t;
       }
       const unsigned long long hits = __ballot(keep && (carry + inc) / total > u);
+      const unsigned long long kept = __ballot(keep);
       if (hits) found = cand[64 * r + __ffsll(static_cast<long long>(hits)) - 1];
+      if (kept) last_kept = cand[64 * r + 63 - __clzll(static_cast<long long>(kept))];
       carry += __shfl(inc, 63, 64);
     }
-    if (l == 0) sh.found_index = found == 0x7fffffff ? V - 1 : found;
+    // none hit: the last kept index, as the reference's searchsorted over cdf / cdf[-1]
+    if (l == 0) sh.found_index = found == 0x7fffffff ? last_kept : found;
   }
   __syncthreads();
   return sh.found_index;
@@ -771,7 +779,20 @@ __global__ __launch_bounds__(kThreads) void sample_kernel(SampleArgs a) {
           }
         }
         __syncthreads();
-        chosen = sh.found_index == 0x7fffffff ? V - 1 : sh.found_index;
+        if (sh.found_index == 0x7fffffff) {
+          // none hit (the running sums end an ulp below `total`): the reference's
+          // searchsorted over cdf / cdf[-1] lands on the last index of nonzero mass
+          __syncthreads();
+          if (threadIdx.x == 0) sh.found_index = -1;
+          __syncthreads();
+          for (int i = hi - 1; i >= lo; --i)
+            if (prob(i) > 0.f) {
+              atomicMax(&sh.found_index, i);
+              break;
+            }
+          __syncthreads();
+        }
+        chosen = sh.found_index < 0 ? V - 1 : sh.found_index;
       }
     }
   }  // general path

@@ -1032,31 +1032,38 @@ struct AttnTile {
   }
 };
 
-// rows [lo, lo + BT) of a head-major (B·H, S, DK) tensor into dst (0 past S)
+// rows [lo, lo + BT) of a head-major (B·H, S, dk) tensor into dst (0 past S and in the
+// padding columns dk ≤ c < DK)
 template <int DK, int BT, typename T>
 __device__ __forceinline__ void load_rows(float (*dst)[DK + 1], const T* __restrict__ src,
-                                          int lo, int S) {
+                                          int lo, int S, int dk) {
   for (int e = threadIdx.x; e < BT * DK; e += 256) {
     const int r = e / DK, c = e - (e / DK) * DK;
-    dst[r][c] = lo + r < S ? static_cast<float>(src[static_cast<long long>(lo + r) * DK + c]) : 0.f;
+    dst[r][c] = lo + r < S && c < dk ? static_cast<float>(src[static_cast<long long>(lo + r) * dk + c]) : 0.f;
   }
 }
 
-// rows [lo, lo + BT) of head h of a merged (B·S, H·DK) tensor
+// rows [lo, lo + BT) of head h of a merged (B·S, H·dk) tensor
 template <int DK, int BT, typename T>
 __device__ __forceinline__ void load_merged(float (*dst)[DK + 1], const T* __restrict__ src,
-                                            int b, int h, int H, int lo, int S) {
+                                            int b, int h, int H, int lo, int S, int dk) {
   for (int e = threadIdx.x; e < BT * DK; e += 256) {
     const int r = e / DK, c = e - (e / DK) * DK;
-    dst[r][c] = lo + r < S ? static_cast<float>(src[(static_cast<long long>(b) * S + lo + r) * H * DK + h * DK + c])
-                           : 0.f;
+    dst[r][c] = lo + r < S && c < dk
+                    ? static_cast<float>(src[(static_cast<long long>(b) * S + lo + r) * H * dk + h * dk + c])
+                    : 0.f;
   }
 }
+
+// The scalar kernels keep their tiles in dynamic LDS (at DK 256 they exceed the 64 KiB
+// of static shared memory). DK is the padded tile width; the runtime a.dk ≤ DK is the
+// head dim (columns dk ≤ c < DK hold zeros and are never written back).
+extern __shared__ __align__(16) unsigned char attn_bwd_smem[];
 
 // dK, dV of BT keys: walk the query tiles from the key tile on (causal).
 template <int DK, int BT, typename T>
 __global__ __launch_bounds__(256) void attn_bwd_dkdv_kernel(AttnBwdArgs a) {
-  __shared__ AttnTile<DK, BT, T> sh;
+  AttnTile<DK, BT, T>& sh = *reinterpret_cast<AttnTile<DK, BT, T>*>(attn_bwd_smem);
   const T* qg = static_cast<const T*>(a.q);
   const T* kg = static_cast<const T*>(a.k);
   const T* vg = static_cast<const T*>(a.v);
@@ -1064,18 +1071,18 @@ __global__ __launch_bounds__(256) void attn_bwd_dkdv_kernel(AttnBwdArgs a) {
   constexpr int TPK = 256 / BT;       // threads per key row of the output
   constexpr int NCOL = (DK + TPK - 1) / TPK;
   const int bh = blockIdx.y, b = bh / a.H, h = bh - (bh / a.H) * a.H;
-  const int S = a.S, k_lo = blockIdx.x * BT;
-  const long long hoff = static_cast<long long>(bh) * S * DK;
-  load_rows<DK, BT>(sh.Ks, kg + hoff, k_lo, S);
-  load_rows<DK, BT>(sh.Vs, vg + hoff, k_lo, S);
+  const int S = a.S, k_lo = blockIdx.x * BT, hd = a.dk;
+  const long long hoff = static_cast<long long>(bh) * S * hd;
+  load_rows<DK, BT>(sh.Ks, kg + hoff, k_lo, S, hd);
+  load_rows<DK, BT>(sh.Vs, vg + hoff, k_lo, S, hd);
   const int jo = threadIdx.x / TPK, co = threadIdx.x % TPK;
   float dk[NCOL], dv[NCOL];
 #pragma unroll
   for (int u = 0; u < NCOL; ++u) dk[u] = dv[u] = 0.f;
   for (int q_lo = k_lo; q_lo < S; q_lo += BT) {
     __syncthreads();  // the previous tile's readers are done
-    load_rows<DK, BT>(sh.Qs, qg + hoff, q_lo, S);
-    load_merged<DK, BT>(sh.dOs, og, b, h, a.H, q_lo, S);
+    load_rows<DK, BT>(sh.Qs, qg + hoff, q_lo, S, hd);
+    load_merged<DK, BT>(sh.dOs, og, b, h, a.H, q_lo, S, hd);
     for (int i = threadIdx.x; i < BT; i += 256) {
       const bool ok = q_lo + i < S;
       sh.lse[i] = ok ? a.lse[static_cast<long long>(bh) * S + q_lo + i] : 0.f;
@@ -1101,12 +1108,12 @@ __global__ __launch_bounds__(256) void attn_bwd_dkdv_kernel(AttnBwdArgs a) {
   }
   const int key = k_lo + jo;
   if (key < S) {
-    const int d = a.H * DK;
-    T* row = static_cast<T*>(a.dqkv) + (static_cast<long long>(b) * S + key) * 3 * d + h * DK;
+    const int d = a.H * hd;
+    T* row = static_cast<T*>(a.dqkv) + (static_cast<long long>(b) * S + key) * 3 * d + h * hd;
 #pragma unroll
     for (int u = 0; u < NCOL; ++u) {
       const int c = co + TPK * u;
-      if (c < DK) {
+      if (c < hd) {
         row[d + c] = static_cast<T>(dk[u]);
         row[2 * d + c] = static_cast<T>(dv[u]);
       }
@@ -1117,7 +1124,7 @@ __global__ __launch_bounds__(256) void attn_bwd_dkdv_kernel(AttnBwdArgs a) {
 // dQ of BT queries: walk the key tiles up to the query tile (causal).
 template <int DK, int BT, typename T>
 __global__ __launch_bounds__(256) void attn_bwd_dq_kernel(AttnBwdArgs a) {
-  __shared__ AttnTile<DK, BT, T> sh;
+  AttnTile<DK, BT, T>& sh = *reinterpret_cast<AttnTile<DK, BT, T>*>(attn_bwd_smem);
   const T* qg = static_cast<const T*>(a.q);
   const T* kg = static_cast<const T*>(a.k);
   const T* vg = static_cast<const T*>(a.v);
@@ -1125,10 +1132,10 @@ __global__ __launch_bounds__(256) void attn_bwd_dq_kernel(AttnBwdArgs a) {
   constexpr int TPK = 256 / BT;
   constexpr int NCOL = (DK + TPK - 1) / TPK;
   const int bh = blockIdx.y, b = bh / a.H, h = bh - (bh / a.H) * a.H;
-  const int S = a.S, q_lo = blockIdx.x * BT;
-  const long long hoff = static_cast<long long>(bh) * S * DK;
-  load_rows<DK, BT>(sh.Qs, qg + hoff, q_lo, S);
-  load_merged<DK, BT>(sh.dOs, og, b, h, a.H, q_lo, S);
+  const int S = a.S, q_lo = blockIdx.x * BT, hd = a.dk;
+  const long long hoff = static_cast<long long>(bh) * S * hd;
+  load_rows<DK, BT>(sh.Qs, qg + hoff, q_lo, S, hd);
+  load_merged<DK, BT>(sh.dOs, og, b, h, a.H, q_lo, S, hd);
   for (int i = threadIdx.x; i < BT; i += 256) {
     const bool ok = q_lo + i < S;
     sh.lse[i] = ok ? a.lse[static_cast<long long>(bh) * S + q_lo + i] : 0.f;
@@ -1141,8 +1148,8 @@ __global__ __launch_bounds__(256) void attn_bwd_dq_kernel(AttnBwdArgs a) {
   const int k_end = min(S, q_lo + BT);
   for (int k_lo = 0; k_lo < k_end; k_lo += BT) {
     __syncthreads();
-    load_rows<DK, BT>(sh.Ks, kg + hoff, k_lo, S);
-    load_rows<DK, BT>(sh.Vs, vg + hoff, k_lo, S);
+    load_rows<DK, BT>(sh.Ks, kg + hoff, k_lo, S, hd);
+    load_rows<DK, BT>(sh.Vs, vg + hoff, k_lo, S, hd);
     __syncthreads();
     sh.scores(q_lo, k_lo, S, a.scale);
     __syncthreads();
@@ -1159,12 +1166,12 @@ __global__ __launch_bounds__(256) void attn_bwd_dq_kernel(AttnBwdArgs a) {
   }
   const int q = q_lo + io;
   if (q < S) {
-    const int d = a.H * DK;
-    T* row = static_cast<T*>(a.dqkv) + (static_cast<long long>(b) * S + q) * 3 * d + h * DK;
+    const int d = a.H * hd;
+    T* row = static_cast<T*>(a.dqkv) + (static_cast<long long>(b) * S + q) * 3 * d + h * hd;
 #pragma unroll
     for (int u = 0; u < NCOL; ++u) {
       const int c = co + TPK * u;
-      if (c < DK) row[c] = static_cast<T>(dq[u]);
+      if (c < hd) row[c] = static_cast<T>(dq[u]);
     }
   }
 }
@@ -1682,6 +1689,27 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dq_f16(AttnBwdArgs a) {
   }
 }
 
+// The scalar pair (any head dim ≤ DK, tiles padded to DK columns).
+template <int DK, typename T>
+int attn_bwd_scalar(const AttnBwdArgs& a, hipStream_t st) {
+  constexpr int BT = DK >= 128 ? 16 : 32;
+  constexpr size_t lds = sizeof(AttnTile<DK, BT, T>);
+  static bool attr = false;
+  if (!attr) {
+    NML_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(&attn_bwd_dkdv_kernel<DK, BT, T>),
+                                hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds)));
+    NML_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(&attn_bwd_dq_kernel<DK, BT, T>),
+                                hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds)));
+    attr = true;
+  }
+  const dim3 grid((a.S + BT - 1) / BT, a.B * a.H);
+  attn_bwd_dkdv_kernel<DK, BT, T><<<grid, 256, lds, st>>>(a);
+  NML_LAUNCHED();
+  attn_bwd_dq_kernel<DK, BT, T><<<grid, 256, lds, st>>>(a);
+  NML_LAUNCHED();
+  return 0;
+}
+
 template <int DK>
 int attn_bwd_f16(const AttnBwdArgs& a, hipStream_t st) {
   constexpr size_t lds = attn_f16_lds<DK>();
@@ -1730,13 +1758,7 @@ int attn_bwd_dk(const AttnBwdArgs& a, hipStream_t st) {
       return attn_bwd_mfma<DK, T>(a, st);
     }
   }
-  constexpr int BT = DK >= 128 ? 16 : 32;
-  const dim3 grid((a.S + BT - 1) / BT, a.B * a.H);
-  attn_bwd_dkdv_kernel<DK, BT, T><<<grid, 256, 0, st>>>(a);
-  NML_LAUNCHED();
-  attn_bwd_dq_kernel<DK, BT, T><<<grid, 256, 0, st>>>(a);
-  NML_LAUNCHED();
-  return 0;
+  return attn_bwd_scalar<DK, T>(a, st);
 }
 
 // --------------------------------------------------------------- RoPE backward
@@ -1798,9 +1820,14 @@ __global__ __launch_bounds__(256) void embed_bwd_tok_kernel(const T* __restrict_
     const int tot = s_cnt[0] + s_cnt[1] + s_cnt[2] + s_cnt[3];
     if (hit) s_idx[off + __popcll(m & ((1ull << lane) - 1ull))] = j;
     __syncthreads();
-    for (int q = 0; q < tot; ++q) {
-      const T* src = g + static_cast<long long>(s_idx[q]) * d;
-      for (int c = t; c < d; c += 256) dst[c] += static_cast<float>(src[c]);
+    // each column read once, its rows added in ascending order in a register, stored
+    // once: the loads of a column's rows are independent, so a frequent id (a pad token)
+    // costs a stream of loads rather than a chain of read-modify-writes per row
+    for (int c = t; c < d; c += 256) {
+      float acc = dst[c];
+#pragma unroll 4
+      for (int q = 0; q < tot; ++q) acc += static_cast<float>(g[static_cast<long long>(s_idx[q]) * d + c]);
+      dst[c] = acc;
     }
     __syncthreads();
   }
@@ -1986,8 +2013,15 @@ int attention_backward_t(const AttnBwdArgs& a, hipStream_t st) {
     case 64: return attn_bwd_dk<64, T>(a, st);
     case 128: return attn_bwd_dk<128, T>(a, st);
   }
-  set_error("attention backward: head_dim %d unsupported (8, 16, 32, 64, 128)", a.dk);
-  return -1;
+  // other head dims: the scalar kernels on tiles padded to 32, 64, 128 or 256 columns
+  if (a.dk < 1 || a.dk > kMaxHeadDim) {
+    set_error("attention backward: head_dim %d outside [1, %d]", a.dk, kMaxHeadDim);
+    return -1;
+  }
+  if (a.dk <= 32) return attn_bwd_scalar<32, T>(a, st);
+  if (a.dk <= 64) return attn_bwd_scalar<64, T>(a, st);
+  if (a.dk <= 128) return attn_bwd_scalar<128, T>(a, st);
+  return attn_bwd_scalar<256, T>(a, st);
 }
 
 int launch_attention_backward(int dt, const AttnBwdArgs& a, hipStream_t st) {

@@ -5,6 +5,8 @@ Each takes host arrays or ``DeviceArray``s in the compute dtype and returns
   fused_rmsnorm_forward       kernels/fused_rmsnorm.py:130-162
   fused_gelu_forward          kernels/fused_gelu.py:57-83
   fused_sdpa_forward          kernels/fused_sdpa.py:256-289 (any additive mask, or none)
+  decode_attention            one cached decode step of that attention (the KV-cache seam of
+                              models/generate.py:93-100; no reference kernel)
   embedding_lookup            kernels/embedding_scatter.py:25-36
   fused_tied_crossentropy_forward  kernels/fused_tied_crossentropy.py:8-24 (loss only)
   linear                      the `x @ W + b` of neural_network/_fused_arrays.py:25-30
@@ -99,6 +101,31 @@ def flash_sdpa_forward(q, k, v, scale):
     N.check(N.lib.nml_flash_sdpa_forward_device(qd.ptr, kd.ptr, vd.ptr, out.ptr, m.ptr, lsum.ptr,
                                                 bh, seq, dk, float(1.0 / scale)))
     return out, m, lsum
+
+
+def decode_attention(q, kcache, vcache, lens, scale):
+    """Attention of one new query per (row, head) over a KV cache: ``q`` (batch, heads, dk),
+    ``kcache``/``vcache`` (batch, heads, max_seq, dk), ``lens`` (batch,) keys attended per
+    row, ``scale`` the sqrt(dk) divisor (kernels/fused_sdpa.py:71-78 on the cached keys).
+    Returns the merged-head output (batch, heads·dk). Raises ValueError for a length
+    outside [1, max_seq]."""
+    dt = _float_dtype(q)
+    qd, kd, vd = _dev(q, dt), _dev(kcache, dt), _dev(vcache, dt)
+    batch, heads, max_seq, dk = kd.shape
+    if qd.shape != (batch, heads, dk) or vd.shape != kd.shape:
+        raise ValueError(f"decode_attention: q {qd.shape}, kcache {kd.shape}, vcache {vd.shape}")
+    ln = _dev(np.ascontiguousarray(lens, dtype=np.int32) if not isinstance(lens, N.DeviceArray)
+              else lens, np.int32)
+    if ln.shape != (batch,):
+        raise ValueError(f"decode_attention: lens must be ({batch},), got {ln.shape}")
+    err = N.DeviceArray.from_host(np.zeros(1, np.int32))
+    out = N.DeviceArray((batch, heads * dk), dt)
+    N.check(N.lib.nml_decode_attention_device(qd.ptr, kd.ptr, vd.ptr, ln.ptr, out.ptr, batch,
+                                              heads, max_seq, dk, float(scale), err.ptr,
+                                              N.np_dtype_code(dt)))
+    if int(err.numpy()[0]):
+        raise ValueError(f"decode_attention: a length is outside [1, {max_seq}]")
+    return out
 
 
 def flash_sdpa_backward(grad_out, q, k, v, m, lsum, scale):

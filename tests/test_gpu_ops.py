@@ -416,7 +416,7 @@ def test_sdpa_mfma_long_fp16(gpu, dk):
     assert np.abs(out - want).max() < 6e-3
 
 
-@pytest.mark.parametrize("dk", [16, 64, 128])
+@pytest.mark.parametrize("dk", [16, 40, 64, 96, 128, 256])
 @pytest.mark.parametrize("seq", [1, 37, 200])
 def test_flash_sdpa_forward_device_reference_arguments(gpu, dk, seq):
     """flash_sdpa_forward_device with the reference's arguments (module.cpp:231-242):
@@ -434,7 +434,7 @@ def test_flash_sdpa_forward_device_reference_arguments(gpu, dk, seq):
     assert (np.abs(np.asarray(lsum) - wl) / wl).max() < 1e-5
 
 
-@pytest.mark.parametrize("dk", [16, 64, 128])
+@pytest.mark.parametrize("dk", [16, 40, 64, 96, 128, 256])
 def test_flash_sdpa_backward_device(gpu, dk):
     """flash_sdpa_backward_device (module.cpp:243-257): gradients against the float64
     restatement of sdpa_cuda.cu:79-133, with the forward's m and l."""

@@ -5,8 +5,9 @@ pinned by finite differences in test_grad_oracle.py).
 Tolerance: for each parameter tensor, max |device − oracle| ≤ 2e-5 · max |oracle| + 1e-7
 (float32 products and sums in another order; the mistakes this test is for — a wrong
 index, transposed operand or dropped term — move a gradient by O(1) of its size).
-Head dims 8, 16, 32, 64 and 128 cover every attention-backward tile shape; sequence
-lengths that are not tile multiples cover the partial tiles."""
+Head dims 8, 16, 32, 64 and 128 cover every attention-backward tile shape, and 40, 96
+and 256 the scalar kernels on padded tiles; sequence lengths that are not tile multiples
+cover the partial tiles."""
 import ctypes as C
 
 import numpy as np
@@ -86,6 +87,9 @@ CASES = [
     ((512, 128, 2, 2, 128), 2, 70),    # dk 64
     ((1024, 256, 2, 1, 64), 2, 45),    # dk 128 (16-row tiles)
     ((256, 128, 2, 1, 512), 2, 512),   # 1024 rows: weight gradients split over K
+    ((256, 80, 2, 1, 64), 2, 50),      # dk 40: tiles padded to 64 columns
+    ((256, 192, 2, 1, 64), 2, 45),     # dk 96: padded to 128
+    ((256, 512, 2, 1, 48), 2, 20),     # dk 256 (16-row tiles in dynamic LDS)
 ]
 
 
@@ -188,7 +192,8 @@ def test_c_abi_backward_accumulates_and_matches_loss(gpu):
 
 
 @pytest.mark.parametrize("dims,b,s", [((256, 64, 4, 2, 64), 2, 40), ((512, 128, 2, 2, 96), 2, 70),
-                                      ((512, 256, 2, 1, 64), 2, 33), ((256, 128, 2, 1, 128), 2, 128)])
+                                      ((512, 256, 2, 1, 64), 2, 33), ((256, 128, 2, 1, 128), 2, 128),
+                                      ((256, 192, 2, 1, 64), 2, 45)])
 def test_backward_fp16(gpu, dims, b, s):
     """float16 models: the loss equals the fp16 oracle's (the reference's fp16 rounding),
     and the gradients (kept float32, as under an optimizer's _grad_dtype) match the float64
@@ -475,6 +480,38 @@ def test_no_grad_loss_equals_training_loss(gpu, dtype):
     trained = m.compute_loss(ids, labels)
     assert trained.requires_grad
     assert plain.item() == trained.item()
+
+
+@pytest.mark.parametrize("dims", [(1024, 128, 2, 2, 512), (1024, 256, 2, 2, 512)],
+                         ids=["dk64", "dk128"])
+def test_fp16_no_grad_loss_stays_near_training_loss(gpu, dims):
+    """float16 models at head dims 64/128: without grad the prefill attention keeps its
+    scores as fp32 accumulators, while the training forward (whose backward recomputes the
+    scores from the saved statistics) rounds them to fp16 as the reference's fp16 path
+    does. The two losses (float64 from the C-ABI, before the fp16 Tensor rounding) must
+    stay within 1e-5 relative (measured ~1e-6), and each within the fp16 loss rounding of
+    the fp16 oracle."""
+    import nimbleml_amd as nm
+    from nimbleml_amd import _native as N
+
+    cfg = GPTConfig(*dims)
+    w = {k: v.astype(np.float16) for k, v in make_weights(cfg, seed=33, rich=True).items()}
+    m = nm.GPT.from_arrays(w, cfg.vocab_size, cfg.d_model, cfg.num_heads, cfg.num_layers,
+                           cfg.max_seq_len, dtype=np.float16)
+    b, s = 2, 400
+    ids = random_ids((b, s), cfg.vocab_size, seed=28)
+    labels = random_ids((b * s,), cfg.vocab_size, seed=29)
+    h = m._device_model()
+    dids, dlab = N.DeviceArray.from_host(ids), N.DeviceArray.from_host(labels)
+    plain, trained = C.c_double(), C.c_double()
+    N.check(N.lib.nml_model_loss(h, dids.ptr, dlab.ptr, b, s, 0, 0, C.byref(plain)))
+    N.check(N.lib.nml_model_loss_train(h, dids.ptr, dlab.ptr, b, s, 0, 0, C.byref(trained)))
+    gap = abs(plain.value - trained.value) / abs(trained.value)
+    print(f"no_grad vs training loss: relative gap {gap:.2e}")
+    assert gap <= 1e-5, gap
+    want = R.compute_loss(w, ids, labels, cfg.num_heads, cfg.num_layers)
+    for got in (plain.value, trained.value):
+        assert abs(got - want) <= 2 ** -10 * abs(want), (got, want)
 
 
 def test_interleaved_losses_and_inference_before_backward(gpu):
