@@ -317,11 +317,24 @@ int nml_model_adamw_update(nml_model* m, int kind, int layer, size_t offset, siz
  * The seam generate() probes for (models/generate.py:93-100). */
 int nml_cache_create(nml_model* m, size_t batch, nml_cache** out);
 int nml_cache_destroy(nml_cache* c);
+/* The length of row 0 (rows prefilled with nml_model_prefill_ragged may differ). */
 int nml_cache_length(nml_cache* c, size_t* len);
-/* Append seq tokens (same count per row) and return their logits (batch, seq, vocab),
- * or (batch, vocab) for the last position when last_only. */
+/* Append seq tokens (same count per row, each row at its own position) and return their
+ * logits (batch, seq, vocab), or (batch, vocab) for the last position when last_only.
+ * seq == 1 is one step of generate()'s decode loop (the same kernels as
+ * nml_model_generate: the whole-step decode of the graph-launched loop); it returns
+ * after the device finishes. */
 int nml_model_forward_cached(nml_model* m, nml_cache* c, const int64_t* ids, size_t batch,
                              size_t seq, void* logits, int last_only);
+/* Prefill an empty cache with prompts of different lengths — row b is prompts[b ·
+ * prompt_stride …] of prompt_len[b] tokens (device int64; prompt_len on the host) — as
+ * generate() does for a ragged batch (one packed pass); logits (batch, vocab) receive each
+ * row's last-position logits. Each row then continues at its own position through
+ * nml_model_forward_cached. The reference runs such rows one at a time
+ * (models/generate.py:80-89); each row here gives what it gives alone. */
+int nml_model_prefill_ragged(nml_model* m, nml_cache* c, const int64_t* prompts,
+                             size_t prompt_stride, const int32_t* prompt_len, size_t batch,
+                             void* logits);
 
 /* Whole generate() (models/generate.py:62-119) on device, no host sync per token:
  * prompts (batch, prompt_stride) device int64, row b valid for prompt_len[b] (host array;

@@ -89,6 +89,7 @@ _SIGS = {
     "nml_cache_destroy": [vp],
     "nml_cache_length": [vp, C.POINTER(sz)],
     "nml_model_forward_cached": [vp, vp, vp, sz, sz, vp, i32],
+    "nml_model_prefill_ragged": [vp, vp, vp, sz, PI32, sz, vp],
     "nml_model_generate": [vp, vp, sz, PI32, sz, sz, f32, i32, f32, f32, vp, vp, sz, i32],
     "nml_model_last_decode_ms": [vp, C.POINTER(f32)],
     "nml_model_last_decode_path": [vp, C.POINTER(C.c_int)],

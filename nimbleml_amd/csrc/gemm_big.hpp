@@ -162,7 +162,11 @@ __device__ __forceinline__ void mainloop(const half_t* __restrict__ A, long long
   issue(0);
   wait_stage(0);
   read(fa0, fb0, 0, 0);
-  for (int s = 0; s < S; ++s) {
+  // Stages with a successor, then the last stage without the next stage's first read:
+  // on every path (the loop's back edge and its exit alike) the reads issued at the bottom
+  // meet the wait at the top of the next body before any use, and no path leaves the
+  // main loop with reads still in flight (the caller's epilogue reuses their registers).
+  auto body = [&](int s) {
     read(fa1, fb1, s, 1);
     W::prev(fa0, fb0);
     mma(fa0, fb0);
@@ -173,12 +177,16 @@ __device__ __forceinline__ void mainloop(const half_t* __restrict__ A, long long
     W::prev(fa0, fb0);
     mma(fa0, fb0);
     W::all(fa1, fb1);
-    if (s + 1 < S) {
-      wait_stage(s + 1);
-      read(fa0, fb0, s + 1, 0);
-    }
+  };
+  int s = 0;
+  for (; s + 1 < S; ++s) {
+    body(s);
+    wait_stage(s + 1);
+    read(fa0, fb0, s + 1, 0);
     mma(fa1, fb1);
   }
+  body(s);
+  mma(fa1, fb1);
 }
 
 }  // namespace big

@@ -25,8 +25,9 @@ struct nml_cache {
   void* v = nullptr;
   int32_t* len_dev = nullptr;  // B
   std::vector<int32_t> len;    // host mirror
-  // Single-token steps at batch 1 through the persistent kernel: the fed ids at their
-  // positions (P int64) and the kernel's error word. Allocated on first such step.
+  // Single-token steps (forward_with_cache with one token per row): the fed ids at their
+  // positions (B × P int64, row b at b·P) and the step's error word. Allocated on the
+  // first such step.
   int64_t* tok = nullptr;
   int* err = nullptr;
 };
@@ -500,12 +501,138 @@ __global__ void gather_last_rows_kernel(const char* __restrict__ src, const int3
   for (int i = threadIdx.x; i < bytes / 16; i += blockDim.x) o[i] = s[i];
 }
 
+// tok[b·P + pos[b]] = ids[b]: one fed token per row at the row's own position.
+__global__ void scatter_step_tokens_kernel(const int64_t* __restrict__ ids, const int32_t* __restrict__ pos,
+                                           int64_t* __restrict__ tok, int B, int P) {
+  const int b = blockIdx.x * blockDim.x + threadIdx.x;
+  if (b < B) tok[static_cast<long long>(b) * P + pos[b]] = ids[b];
+}
+
 __global__ void copy_rows_kernel(const int64_t* __restrict__ src, long long sstride,
                                  int64_t* __restrict__ dst, long long dstride,
                                  const int32_t* __restrict__ lens) {
   const int b = blockIdx.x;
   const int n = lens[b];
   for (int i = threadIdx.x; i < n; i += blockDim.x) dst[b * dstride + i] = src[b * sstride + i];
+}
+
+// The fed-token buffer (B × P int64) and error word of single-token steps on cache c.
+int cache_step_buffers(nml_model* m, nml_cache* c) {
+  if (c->tok) return 0;
+  void* p = nullptr;
+  const size_t tb = align256((size_t)c->B * m->P * 8);
+  NML_HIP(hipMalloc(&p, tb + 256));
+  c->tok = static_cast<int64_t*>(p);
+  c->err = reinterpret_cast<int*>(static_cast<char*>(p) + tb);
+  return 0;
+}
+
+// Prefill of B prompts (device int64 rows at prompt_stride, host lengths plen) into
+// cache c from position 0: one batched pass, prompts of different lengths packed row
+// after row (the GEMMs see Σ plen rows, attention runs per sequence over its own length).
+// Leaves each row's last-position logits (B, V) in `logits`; out-of-range ids set sm.err.
+int prefill_rows(nml_model* m, nml_cache* c, const int64_t* prompts, size_t prompt_stride,
+                 const std::vector<int32_t>& plen, const Small& sm, void* logits, hipStream_t st) {
+  const int B = (int)plen.size();
+  int maxp = 0;
+  bool same = true;
+  for (int b = 0; b < B; ++b) {
+    maxp = plen[b] > maxp ? plen[b] : maxp;
+    same = same && plen[b] == plen[0];
+  }
+  const size_t layer_kv = (size_t)B * m->H * m->P * m->dk * m->es;
+  const long long sb = (long long)m->H * m->P * m->dk, sh = (long long)m->P * m->dk;
+  NML_HIP(hipMemsetAsync(sm.zeros, 0, B * 4, st));
+  if (same) {
+    const int S = plen[0];
+    Acts a;
+    NML_TRY(acts_for(m, B * S, B, &a));
+    if ((int)prompt_stride != S) {
+      for (int b = 0; b < B; ++b)
+        NML_TRY(launch_embed(m->dt, prompts + (size_t)b * prompt_stride, m->emb, posw(m), nullptr,
+                             static_cast<char*>(a.x) + (size_t)b * S * m->d * m->es, 1, S, m->d,
+                             m->V, m->P, sm.err, st));
+    } else {
+      NML_TRY(launch_embed(m->dt, prompts, m->emb, posw(m), nullptr, a.x, B, S, m->d, m->V, m->P,
+                           sm.err, st));
+    }
+    NML_TRY(trunk(m, a, B, S, sm.zeros,
+                  [&](int l) {
+                    return KVView{static_cast<char*>(c->k) + l * layer_kv,
+                                  static_cast<char*>(c->v) + l * layer_kv, sb, sh};
+                  },
+                  st));
+    NML_TRY(head(m, a, B, S, logits, 1, st));
+  } else {
+    // Packed rows: (b << 16) | s per row, then the lengths and row starts.
+    std::vector<int32_t> tab;
+    int R = 0;
+    for (int b = 0; b < B; ++b) R += plen[b];
+    NML_REQUIRE(maxp < 65536 && B < 32768, "ragged prefill: %d prompts up to %d long", B, maxp);
+    NML_REQUIRE(((size_t)m->d * m->es) % 16 == 0, "ragged prefill: row of %d not 16-byte sized", m->d);
+    tab.reserve((size_t)R + 2 * B + 1);
+    for (int b = 0; b < B; ++b)
+      for (int s = 0; s < plen[b]; ++s) tab.push_back((b << 16) | s);
+    tab.insert(tab.end(), plen.begin(), plen.end());
+    std::vector<int32_t> starts(B);
+    for (int b = 0, r = 0; b < B; r += plen[b], ++b) starts[b] = r;
+    tab.insert(tab.end(), starts.begin(), starts.end());
+    NML_TRY(m->ragged.ensure(tab.size() * 4));
+    const int32_t* dtab = static_cast<const int32_t*>(m->ragged.p);
+    NML_HIP(hipMemcpyAsync(m->ragged.p, tab.data(), tab.size() * 4, hipMemcpyHostToDevice, st));
+    const Ragged rg{dtab, dtab + R, dtab + R + B, R};
+    // activations sized for the padded (B, maxp) query layout
+    Acts a;
+    NML_TRY(acts_for(m, B * maxp, B, &a));
+    for (int b = 0; b < B; ++b)
+      NML_TRY(launch_embed(m->dt, prompts + (size_t)b * prompt_stride, m->emb, posw(m), nullptr,
+                           static_cast<char*>(a.x) + (size_t)starts[b] * m->d * m->es, 1, plen[b],
+                           m->d, m->V, m->P, sm.err, st));
+    NML_TRY(trunk(m, a, B, maxp, sm.zeros,
+                  [&](int l) {
+                    return KVView{static_cast<char*>(c->k) + l * layer_kv,
+                                  static_cast<char*>(c->v) + l * layer_kv, sb, sh};
+                  },
+                  st, &rg));
+    gather_last_rows_kernel<<<B, 128, 0, st>>>(static_cast<const char*>(a.xn), rg.row_start,
+                                               rg.seq_len, static_cast<char*>(a.att),
+                                               m->d * (int)m->es);
+    NML_LAUNCHED();
+    Acts last = a;
+    last.xn = a.att;
+    NML_TRY(head(m, last, B, 1, logits, 1, st));
+  }
+  return 0;
+}
+
+// One token per row (device int64 ids, (B)) at each row's own position c->len[b],
+// through generate()'s decode step (decode_step: the skinny projections with the fused
+// norms, split-K attention over the cache, the tied head); logits (B, V). Advances every
+// row by one position; reports an out-of-range id.
+int decode_rows(nml_model* m, nml_cache* c, const int64_t* ids, void* logits, hipStream_t st) {
+  const int B = c->B;
+  int maxlen = 0;
+  for (int v : c->len) maxlen = v > maxlen ? v : maxlen;
+  NML_REQUIRE(maxlen + 1 <= m->P, "Sequence length %d exceeds maximum sequence length %d",
+              maxlen + 1, m->P);
+  NML_TRY(cache_step_buffers(m, c));
+  scatter_step_tokens_kernel<<<(B + 255) / 256, 256, 0, st>>>(ids, c->len_dev, c->tok, B, m->P);
+  NML_LAUNCHED();
+  NML_HIP(hipMemsetAsync(c->err, 0, sizeof(int), st));
+  Acts a;
+  NML_TRY(acts_for(m, B, B, &a));
+  // the workspace is shared with other forwards: clear the attention partials each call
+  NML_HIP(hipMemsetAsync(a.part, 0, attention_decode_workspace(B, m->H, m->dk, m->P), st));
+  NML_TRY(decode_step(m, c, a, c->tok, m->P, c->len_dev, c->err, logits, maxlen + 1, st));
+  add_scalar_kernel<<<(B + 255) / 256, 256, 0, st>>>(c->len_dev, B, 1);
+  NML_LAUNCHED();
+  for (auto& v : c->len) v += 1;
+  int herr = 0;
+  NML_HIP(hipMemcpyAsync(&herr, c->err, sizeof(int), hipMemcpyDeviceToHost, st));
+  NML_HIP(hipStreamSynchronize(st));
+  m->last_decode_persistent = 0;
+  NML_REQUIRE(herr == 0, "Token ID out of range [0, %d)", m->V);
+  return 0;
 }
 
 }  // namespace
@@ -822,19 +949,15 @@ int nml_model_forward_cached(nml_model* m, nml_cache* c, const int64_t* ids, siz
   NML_REQUIRE((int)batch == c->B, "batch %zu does not match the cache batch %d", batch, c->B);
   const int B = (int)batch, S = (int)seq;
   if (S == 0) return 0;
-  const int start = c->len[0];
+  int start = 0;  // the longest row (rows prefilled ragged sit at different positions)
+  for (int v : c->len) start = v > start ? v : start;
   NML_REQUIRE((size_t)start + seq <= (size_t)m->P,
               "Sequence length %zu exceeds maximum sequence length %d", start + seq, m->P);
   hipStream_t st = nml::stream();
   if (B == 1 && S == 1 && persist_wanted() && !rope_on(m) &&
       persist_supported(m->dt, m->d, m->H, m->F, B, m->P)) {
     // One token of one sequence: the persistent decode kernel (logits out, no choice).
-    if (!c->tok) {
-      void* p = nullptr;
-      NML_HIP(hipMalloc(&p, align256((size_t)m->P * 8) + 256));
-      c->tok = static_cast<int64_t*>(p);
-      c->err = reinterpret_cast<int*>(static_cast<char*>(p) + align256((size_t)m->P * 8));
-    }
+    NML_TRY(cache_step_buffers(m, c));
     NML_HIP(hipMemcpyAsync(c->tok + start, ids, sizeof(int64_t), hipMemcpyDeviceToDevice, st));
     NML_HIP(hipMemsetAsync(c->err, 0, sizeof(int), st));
     PersistArgs pa{};
@@ -851,7 +974,8 @@ int nml_model_forward_cached(nml_model* m, nml_cache* c, const int64_t* ids, siz
     NML_REQUIRE(herr == 0, "Token ID out of range [0, %d)", m->V);
     return 0;
   }
-  if (S == 1) m->last_decode_persistent = 0;
+  // one token per row: generate()'s decode step (rows may sit at different positions)
+  if (S == 1) return decode_rows(m, c, ids, logits, st);
   Acts a;
   NML_TRY(acts_for(m, B * S, 0, &a));
   NML_TRY(launch_embed(m->dt, ids, m->emb, posw(m), c->len_dev, a.x, B, S, m->d, m->V, m->P,
@@ -868,6 +992,35 @@ int nml_model_forward_cached(nml_model* m, nml_cache* c, const int64_t* ids, siz
   add_scalar_kernel<<<(B + 255) / 256, 256, 0, st>>>(c->len_dev, B, S);
   NML_LAUNCHED();
   for (auto& v : c->len) v += S;
+  return 0;
+}
+
+int nml_model_prefill_ragged(nml_model* m, nml_cache* c, const int64_t* prompts,
+                             size_t prompt_stride, const int32_t* prompt_len, size_t batch,
+                             void* logits) {
+  NML_TRY(check_ready(m));
+  NML_REQUIRE(c != nullptr && c->m == m, "cache does not belong to this model");
+  NML_REQUIRE((int)batch == c->B, "batch %zu does not match the cache batch %d", batch, c->B);
+  for (int v : c->len) NML_REQUIRE(v == 0, "prefill_ragged: the cache is not empty");
+  const int B = (int)batch;
+  std::vector<int32_t> plen(prompt_len, prompt_len + B);
+  for (int b = 0; b < B; ++b) {
+    NML_REQUIRE(plen[b] > 0, "prompt %d is empty", b);
+    NML_REQUIRE((size_t)plen[b] <= prompt_stride, "prompt %d longer than its stride", b);
+    NML_REQUIRE(plen[b] <= m->P, "Sequence length %d exceeds maximum sequence length %d", plen[b],
+                m->P);
+  }
+  hipStream_t st = nml::stream();
+  Small sm;
+  NML_TRY(small_for(m, B, &sm));
+  NML_HIP(hipMemsetAsync(sm.err, 0, sizeof(int), st));
+  NML_TRY(prefill_rows(m, c, prompts, prompt_stride, plen, sm, logits, st));
+  NML_HIP(hipMemcpyAsync(c->len_dev, plen.data(), B * 4, hipMemcpyHostToDevice, st));
+  int herr = 0;
+  NML_HIP(hipMemcpyAsync(&herr, sm.err, sizeof(int), hipMemcpyDeviceToHost, st));
+  NML_HIP(hipStreamSynchronize(st));  // plen (host) is read by the copy above
+  c->len = plen;
+  NML_REQUIRE(herr == 0, "Token ID out of range [0, %d)", m->V);
   return 0;
 }
 
@@ -916,70 +1069,7 @@ int nml_model_generate(nml_model* m, const int64_t* prompts, size_t prompt_strid
   NML_TRY(m->logits_ws.ensure(lb));
   void* logits = m->logits_ws.p;
 
-  // Prefill: one batched pass; prompts of different lengths are packed row after row
-  // (the GEMMs see Σ prompt_len rows, attention runs per sequence over its own length).
-  const size_t layer_kv = (size_t)B * m->H * m->P * m->dk * m->es;
-  const long long sb = (long long)m->H * m->P * m->dk, sh = (long long)m->P * m->dk;
-  NML_HIP(hipMemsetAsync(sm.zeros, 0, B * 4, st));
-  if (same) {
-    const int S = plen[0];
-    Acts a;
-    NML_TRY(acts_for(m, B * S, B, &a));
-    if ((int)prompt_stride != S) {
-      for (int b = 0; b < B; ++b)
-        NML_TRY(launch_embed(m->dt, prompts + (size_t)b * prompt_stride, m->emb, posw(m), nullptr,
-                             static_cast<char*>(a.x) + (size_t)b * S * m->d * m->es, 1, S, m->d,
-                             m->V, m->P, sm.err, st));
-    } else {
-      NML_TRY(launch_embed(m->dt, prompts, m->emb, posw(m), nullptr, a.x, B, S, m->d, m->V, m->P,
-                           sm.err, st));
-    }
-    NML_TRY(trunk(m, a, B, S, sm.zeros,
-                  [&](int l) {
-                    return KVView{static_cast<char*>(c->k) + l * layer_kv,
-                                  static_cast<char*>(c->v) + l * layer_kv, sb, sh};
-                  },
-                  st));
-    NML_TRY(head(m, a, B, S, logits, 1, st));
-  } else {
-    // Packed rows: (b << 16) | s per row, then the lengths and row starts.
-    std::vector<int32_t> tab;
-    int R = 0;
-    for (int b = 0; b < B; ++b) R += plen[b];
-    NML_REQUIRE(maxp < 65536 && B < 32768, "ragged prefill: %d prompts up to %d long", B, maxp);
-    NML_REQUIRE(((size_t)m->d * m->es) % 16 == 0, "ragged prefill: row of %d not 16-byte sized", m->d);
-    tab.reserve((size_t)R + 2 * B + 1);
-    for (int b = 0; b < B; ++b)
-      for (int s = 0; s < plen[b]; ++s) tab.push_back((b << 16) | s);
-    tab.insert(tab.end(), plen.begin(), plen.end());
-    std::vector<int32_t> starts(B);
-    for (int b = 0, r = 0; b < B; r += plen[b], ++b) starts[b] = r;
-    tab.insert(tab.end(), starts.begin(), starts.end());
-    NML_TRY(m->ragged.ensure(tab.size() * 4));
-    const int32_t* dtab = static_cast<const int32_t*>(m->ragged.p);
-    NML_HIP(hipMemcpyAsync(m->ragged.p, tab.data(), tab.size() * 4, hipMemcpyHostToDevice, st));
-    const Ragged rg{dtab, dtab + R, dtab + R + B, R};
-    // activations sized for the padded (B, maxp) query layout
-    Acts a;
-    NML_TRY(acts_for(m, B * maxp, B, &a));
-    for (int b = 0; b < B; ++b)
-      NML_TRY(launch_embed(m->dt, prompts + (size_t)b * prompt_stride, m->emb, posw(m), nullptr,
-                           static_cast<char*>(a.x) + (size_t)starts[b] * m->d * m->es, 1, plen[b],
-                           m->d, m->V, m->P, sm.err, st));
-    NML_TRY(trunk(m, a, B, maxp, sm.zeros,
-                  [&](int l) {
-                    return KVView{static_cast<char*>(c->k) + l * layer_kv,
-                                  static_cast<char*>(c->v) + l * layer_kv, sb, sh};
-                  },
-                  st, &rg));
-    gather_last_rows_kernel<<<B, 128, 0, st>>>(static_cast<const char*>(a.xn), rg.row_start,
-                                               rg.seq_len, static_cast<char*>(a.att),
-                                               m->d * (int)m->es);
-    NML_LAUNCHED();
-    Acts last = a;
-    last.xn = a.att;
-    NML_TRY(head(m, last, B, 1, logits, 1, st));
-  }
+  NML_TRY(prefill_rows(m, c, prompts, prompt_stride, plen, sm, logits, st));
   // pos[b] = prompt_len[b] − 1, then the first choice advances it to prompt_len[b].
   std::vector<int32_t> pos0(B);
   for (int b = 0; b < B; ++b) pos0[b] = plen[b] - 1;

@@ -10,8 +10,9 @@ Randomness: the reference draws one uniform per row per step from NumPy's
 global legacy generator (``np.random.choice``, generate.py:57,59), rows in
 order within a step. Here the same ``max_new_tokens × batch`` draws are taken
 up front from that generator (``np.random.random_sample``) and consumed in that
-order on the device, so a seeded run gives the reference's tokens. (With
-``eos_id`` the reference may stop early and draw fewer; the tokens still agree.)
+order on the device, so a seeded run gives the reference's tokens. With ``eos_id``
+the reference stops drawing at the eos step; the global generator is then rewound
+to the state those fewer draws leave, so later draws of the caller agree too.
 
 Ragged batches: ``input_ids`` may be a list of rows of different lengths; each
 row then generates as if run alone (the result is a list of arrays).
@@ -65,6 +66,7 @@ def generate(model, input_ids, *, max_new_tokens: int = 64, temperature: float =
                          f"{model.max_seq_len}")
 
     sampling = temperature > 0
+    rng_state = np.random.get_state() if sampling else None
     u = np.random.random_sample((n, batch)) if sampling else None
 
     if use_kv_cache:
@@ -81,6 +83,11 @@ def generate(model, input_ids, *, max_new_tokens: int = 64, temperature: float =
             if all(int(tokens[b, plen[b] + t]) == eos_id for b in range(batch)):
                 steps = t + 1
                 break
+    if sampling and steps < n:
+        # the reference drew one uniform per row per step only up to the eos step
+        # (generate.py:116-117): leave the global generator where its draws end
+        np.random.set_state(rng_state)
+        np.random.random_sample((steps, batch))
     out = [tokens[b, :plen[b] + steps].copy() for b in range(batch)]
     return out if ragged else np.asarray(out, dtype=np.int64)
 

@@ -42,6 +42,7 @@ class KVCache:
         N.check(N.lib.nml_cache_create(self._model_handle, self.batch, C.byref(h)))
         self._h = h
         self._owner = model._dev  # keeps the device model alive while the cache exists
+        self.lengths = None  # per-row lengths of a ragged prefill (None: all rows alike)
 
     @property
     def length(self) -> int:
@@ -372,13 +373,47 @@ class GPT(Module):
         if cache._model_handle is not h:
             raise ValueError("parameters were reloaded since this cache was created; start a "
                              "new cache")
-        if cache.length + s > self.max_seq_len:
-            raise ValueError(f"Sequence length {cache.length + s} exceeds maximum sequence "
+        longest = int(cache.lengths.max()) if cache.lengths is not None else cache.length
+        if longest + s > self.max_seq_len:
+            raise ValueError(f"Sequence length {longest + s} exceeds maximum sequence "
                              f"length {self.max_seq_len}")
         out = self._logits_array((b, s, self.vocab_size))
         dids = N.DeviceArray.from_host(ids)
         N.check(N.lib.nml_model_forward_cached(h, cache._h, dids.ptr, b, s, out.ptr, 0))
+        if cache.lengths is not None:
+            cache.lengths = cache.lengths + s
         return Tensor(out, (b, s, self.vocab_size)), cache
+
+    def prefill_ragged(self, rows):
+        """Prefill a new KV cache with rows of different lengths (a list of 1-D id arrays)
+        in one packed pass, as ``generate`` does for a ragged batch; returns each row's
+        last-position logits (batch, vocab) and the cache. Each row continues at its own
+        position: ``forward_with_cache(ids (batch, 1), cache)`` then runs one step of the
+        batched decode loop. (The reference runs such rows one at a time,
+        models/generate.py:80-89.)"""
+        rows = [np.asarray(r, dtype=np.int64).reshape(-1) for r in rows]
+        if not rows or any(r.size == 0 for r in rows):
+            raise ValueError("prompts must not be empty")
+        for r in rows:
+            if int(r.min()) < 0 or int(r.max()) >= self.vocab_size:
+                raise ValueError(f"Token ID out of range [0, {self.vocab_size})")
+            if r.size > self.max_seq_len:
+                raise ValueError(f"Sequence length {r.size} exceeds maximum sequence length "
+                                 f"{self.max_seq_len}")
+        b = len(rows)
+        plen = np.asarray([r.size for r in rows], dtype=np.int32)
+        stride = int(plen.max())
+        prompts = np.zeros((b, stride), dtype=np.int64)
+        for i, r in enumerate(rows):
+            prompts[i, :r.size] = r
+        h = self._device_model()
+        cache = KVCache(self, b)
+        out = self._logits_array((b, self.vocab_size))
+        dp = N.DeviceArray.from_host(prompts)
+        N.check(N.lib.nml_model_prefill_ragged(h, cache._h, dp.ptr, stride,
+                                               plen.ctypes.data_as(N.PI32), b, out.ptr))
+        cache.lengths = plen.astype(np.int64)
+        return Tensor(out, (b, self.vocab_size)), cache
 
     def compute_loss(self, input_ids, labels, ignore_index=None):
         """Mean tied-head cross-entropy (models/gpt.py:123-137); logits are formed in

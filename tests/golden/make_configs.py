@@ -14,7 +14,8 @@ the tests; the files hold only the decisions and the values the GPU is compared 
   c4_fp16      C4: the same model, 32 prompts of lengths U[128, 1024], 256 sampled
                tokens each (T 0.8, top-k 50, top-p off), row b's draws from
                RandomState(1000 + b) — per row and step the pick and the largest logit
-               change that cannot alter it; prefill logits of four rows.
+               change that cannot alter it; prefill logits of four rows; every row's
+               logits at steps 0, 1, 63 and 255 (teacher-forced on the oracle's tokens).
   c5slice_fp16 C5 widths at two layers: V50304 d2048 H16 (head dim 128), one 4096-token
                sequence, rich weights — compute_loss, and the logits of four positions.
 
@@ -39,6 +40,7 @@ C3_SEED, C3_PROMPT_SEED, C3_PROMPT, C3_STEPS = 41, 42, 512, 64
 C3_KEEP = (0, 1, 2, 31, 63)
 C4_SEED, C4_ROWS_SEED, C4_ROWS, C4_NEW = 41, 5, 32, 256
 C4_T, C4_K, C4_U_SEED = 0.8, 50, 1000
+C4_KEEP = (0, 1, 63, 255)
 C5SLICE = GPTConfig(50304, 2048, 16, 2, 4096)
 C5_SEED, C5_IDS_SEED, C5_S = 43, 44, 4096
 C5_KEEP = (0, 1, 2047, 4095)
@@ -75,9 +77,12 @@ def make_c4():
     orc = R.RaggedKVOracle(w, cfg.num_heads, cfg.num_layers)
     lg = orc.prefill(rows)
     pre = lg[:4].copy()
+    keep = {}
     toks = np.zeros((C4_NEW, C4_ROWS), dtype=np.int32)
     flip = np.zeros((C4_NEW, C4_ROWS), dtype=np.float32)
     for t in range(C4_NEW):
+        if t in C4_KEEP:  # every row's logits, teacher-forced on the oracle's own tokens
+            keep[f"logits_step{t}"] = lg.copy()
         for b in range(C4_ROWS):
             tok = R.sample_logits(lg[b], temperature=C4_T, top_k=C4_K, top_p=1.0, u=u[t, b])
             toks[t, b] = tok
@@ -87,7 +92,8 @@ def make_c4():
         if t % 32 == 0:
             print(f"  c4 step {t}", flush=True)
     return dict(seed=np.array(C4_SEED), tokens=toks, flip_tol=flip, prefill_logits=pre,
-                temperature=np.array(C4_T), top_k=np.array(C4_K))
+                temperature=np.array(C4_T), top_k=np.array(C4_K),
+                keep_steps=np.asarray(C4_KEEP), **keep)
 
 
 def make_c5():

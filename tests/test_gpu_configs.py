@@ -13,7 +13,8 @@ closer than that, the two runs may part ways; the comparison of that row ends th
       persistent kernel launch per token), and the same kernel's logits at every step
       teacher-forced through forward_with_cache.
   C4  the same model, 32 prompts of lengths U[128, 1024], 256 sampled tokens each
-      (T 0.8, top-k 50) through the batched decode step.
+      (T 0.8, top-k 50) through the batched decode step; and every row's logits at four
+      decode steps, teacher-forced on the oracle's tokens through that step.
   C5  d2048 / H16 (head dim 128) / V50304 widths: a 2-layer slice at S 4096 against the
       oracle (loss, logits), and the full 24-layer 4 × 4096 model through properties
       that hold at any size (the training loss equals the inference loss; the loss of
@@ -178,6 +179,39 @@ def test_c4_full_config_sampled(c3_model):
     # row would part every row within a step or two
     assert rate <= 0.25, rate
     assert agree >= 200, agree
+
+
+def test_c4_teacher_forced_decode_logits(c3_model):
+    """C4's decode path pinned by logits (its sampled tokens are undecidable by
+    construction, see above): the 32 ragged prompts go through the same packed prefill as
+    generate() (nml_model_prefill_ragged), then 255 batched decode steps feed the oracle's
+    own sampled tokens (teacher forcing, one token per row at each row's own position:
+    the skinny MFMA projections with the fused norms, the split-K decode attention over
+    contexts up to 1279, the tied head). Every row's logits at steps 0, 1, 63 and 255 are
+    within 3e-2 (the north star's fp16 bound) of the oracle's (tests/golden/make_configs.py,
+    RaggedKVOracle: each row as the reference would run it alone)."""
+    _, m = c3_model
+    f = golden("c4_fp16")
+    assert int(f["seed"]) == int(golden("c3_fp16")["seed"])  # the same model
+    rows = c4_rows(C3.vocab_size)
+    ref = f["tokens"]  # (256, 32): the oracle's sampled token of each step and row
+    keep = [int(t) for t in f["keep_steps"]]
+    lg, cache = m.prefill_ragged(rows)
+    assert not m.last_decode_persistent() or len(rows) == 1
+    worst = {}
+    cur = lg.numpy().astype(np.float64)
+    for t in range(max(keep) + 1):
+        if t in keep:
+            want = f[f"logits_step{t}"].astype(np.float64)
+            dev = np.abs(cur - want).max(axis=1)  # per row
+            worst[t] = float(dev.max())
+            assert dev.max() <= TOL16, (t, int(np.argmax(dev)), float(dev.max()))
+        if t < max(keep):
+            out, cache = m.forward_with_cache(ref[t].astype(np.int64).reshape(-1, 1), cache)
+            cur = out.numpy()[:, 0].astype(np.float64)
+    assert np.array_equal(cache.lengths, np.asarray([len(r) for r in rows]) + max(keep))
+    print("C4 teacher-forced max |dlogit| per kept step (all 32 rows): " +
+          ", ".join(f"step {t}: {v:.3e}" for t, v in worst.items()))
 
 
 C5SLICE = GPTConfig(50304, 2048, 16, 2, 4096)

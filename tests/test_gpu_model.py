@@ -271,6 +271,7 @@ def test_small_generate_and_logits(gpu, name):
     out = nm.generate(m, f["prompt"], max_new_tokens=n, temperature=0.0)
     margins = oracle_greedy_margins(w, cfg, f["greedy"], s0)
     compared = assert_tokens_agree(out, f["greedy"], s0, margins, 1e-3)
+    print(f"{name}: {compared} greedy tokens compared")
     assert compared >= f["greedy"].shape[0]
     for t in f["logit_steps"]:
         lg = m.forward_last(f["greedy"][:, :s0 + int(t)]).numpy()
@@ -342,3 +343,29 @@ def test_c3slice_fp16_steps(gpu):
     half_ulp = float(np.spacing(np.float16(ref))) / 2
     assert abs(raw.value - ref) <= half_ulp + 1e-4 * abs(ref), (raw.value, ref)
     assert m.compute_loss(f["loss_ids"], f["loss_labels"]).item() == float(np.float16(raw.value))
+
+
+def test_eos_stop_leaves_the_global_rng_as_the_reference_does(gpu):
+    """The reference draws one uniform per row per step from NumPy's global generator and
+    stops at the step where every row emitted eos (models/generate.py:57,59,116-117). After
+    an early stop, the generator must be where those draws leave it, not past all
+    max_new_tokens × batch draws."""
+    import nimbleml_amd as nm
+
+    f = golden("tiny_fp32")
+    cfg, w = fixture_weights(f)
+    m = build(cfg, w, np.float32)
+    prompt = f["prompt"][:1]
+    kw = dict(temperature=0.8, top_k=1, top_p=1.0)  # top-k 1: the draw cannot move the pick
+    np.random.seed(77)
+    full = nm.generate(m, prompt, max_new_tokens=12, **kw)
+    s0 = prompt.shape[1]
+    eos = int(full[0, s0 + 3])
+    first = s0 + int(np.argmax(full[0, s0:] == eos))  # the first step that emits it
+    np.random.seed(77)
+    out = nm.generate(m, prompt, max_new_tokens=12, eos_id=eos, **kw)
+    assert out.shape[1] == first + 1 and out[0, -1] == eos
+    after = np.random.random_sample()
+    np.random.seed(77)
+    np.random.random_sample(first + 1 - s0)  # one draw per step taken
+    assert after == np.random.random_sample()
