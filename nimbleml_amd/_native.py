@@ -189,6 +189,16 @@ def np_dtype_code(dt) -> int:
     raise ValueError(f"unsupported dtype {dt} (float32 or float16)")
 
 
+# Host-to-device copies made by this binding (calls, bytes): DeviceArray.from_host and the
+# parameter uploads of device models. Tests read it to check what a call re-uploads.
+h2d_stats = {"calls": 0, "bytes": 0}
+
+
+def count_h2d(nbytes: int) -> None:
+    h2d_stats["calls"] += 1
+    h2d_stats["bytes"] += int(nbytes)
+
+
 class DeviceArray:
     """A contiguous device buffer with a NumPy dtype and shape.
 
@@ -218,6 +228,7 @@ class DeviceArray:
         d = cls(a.shape, a.dtype)
         if a.nbytes:
             check(lib.nml_memcpy_h2d(d.ptr, a.ctypes.data, a.nbytes))
+            count_h2d(a.nbytes)
         return d
 
     @property

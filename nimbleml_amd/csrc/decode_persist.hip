@@ -25,8 +25,10 @@
 // once another thread has given up) it sets bit 2 of *err and goes on, so the
 // grid always drains and the host reports the failure.
 //
-// Work placement is XCD-aware (workgroup g runs on XCD g % 8): the QKV rows of a
-// head, its attention chunks and its merge all sit on the XCD of that head.
+// Work placement is XCD-aware: the dispatcher deals workgroups to the 8 XCDs round
+// robin (workgroup g on XCD (g + c) % 8 for a per-launch offset c; measured c = 7), so the
+// workgroups g ≡ x (mod 8) share one XCD, and a head's team — its QKV rows, attention
+// chunks and merge — is made of such workgroups.
 #include "kernels.hpp"
 
 namespace nml {
@@ -485,6 +487,11 @@ __global__ __launch_bounds__(kT) void decode_persist_kernel(PersistArgs a) {
   const T* posw = static_cast<const T*>(a.posw);
   u64* const trace = a.trace ? a.trace + static_cast<long long>(g) * persist_trace_stride(a.L) : nullptr;
   NML_MARK(0);
+  if (trace && tid == 0) {  // mark 2: the XCD this workgroup runs on (placement check)
+    unsigned xcc;
+    asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(xcc));
+    trace[2] = xcc & 0xfu;
+  }
 
   // ---- embedding, computed by every workgroup (no exchange needed)
   {

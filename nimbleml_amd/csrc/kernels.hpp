@@ -290,7 +290,7 @@ struct PersistArgs {
   int fuse_argmax;             // greedy: write tokens[pos+1] and advance pos in-kernel
   float scale;                 // sqrt(dk)
   // Optional phase timestamps (wall_clock64) of each workgroup: trace[g·stride + mark],
-  // stride = persist_trace_stride(L). Null: no tracing.
+  // stride = persist_trace_stride(L), and at mark 2 the workgroup's XCD. Null: no tracing.
   unsigned long long* trace;
 };
 

@@ -232,6 +232,7 @@ class GPT(Module):
                                  self._dtype)
         for t, *_ in self._param_layout():
             t.data[...] = vals[id(t)].ravel()
+            t._bump_version()
         self._host_stale = False
         return self
 

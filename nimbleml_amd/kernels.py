@@ -193,6 +193,21 @@ def linear(x, weights, bias=None, *, epilogue=None, resid=None):
     return out
 
 
+def linear_t(x, w_t, bias=None, *, epilogue=None):
+    """``epi(x @ w_tᵀ + bias)`` with ``w_t`` a DeviceArray already in the device layout
+    (out, in) and ``bias`` a DeviceArray or None: no host copy of the weights."""
+    dt = _float_dtype(x)
+    xd = _dev(x, dt)
+    n_out, k = w_t.shape
+    rows = xd.size // k
+    if epilogue is None:
+        epilogue = EPI_BIAS if bias is not None else EPI_NONE
+    out = N.DeviceArray((rows, n_out), dt)
+    N.check(N.lib.nml_linear_device(xd.ptr, k, w_t.ptr, N.ptr(bias), None, out.ptr, rows, k,
+                                    n_out, int(epilogue), N.np_dtype_code(dt)))
+    return out
+
+
 def fused_tied_crossentropy_forward(hidden, weights, label_indices, ignore_index=None):
     """Mean CE of ``hidden @ weights.T`` against labels (float)."""
     dt = _float_dtype(hidden)

@@ -20,8 +20,12 @@ Every module's ``forward`` runs on the GPU and returns a Tensor over a ``DeviceA
   FusedTransformerBlock.forward  neural_network/transformer_fused.py:44-95
   FusedGPTTrunk.forward          transformer_fused.py:103-144 (nml_model_blocks_forward)
   Sequential.forward          neural_network/module.py:54-65
-The block, trunk and attention modules upload their current host parameters into a
-device model for the call (the GPT keeps its own resident copy instead). Masks follow
+Each module keeps a device copy of its parameters (a device model for the block, trunk
+and attention modules; transposed weights for Dense and FeedForward), keyed on the
+parameters' versions: ``load``/``load_arrays`` and ``GPT.sync_to_host`` bump them, and
+code that edits ``param.data`` in place by other means calls
+``module.mark_parameters_changed()``. A second call with unchanged parameters uploads
+nothing. Masks follow
 the reference: an additive (seq, seq) array or Tensor; ``None`` is causal for the
 fused block and trunk and no mask for MultiHeadAttention. Gradients of these
 module-level outputs are not computed on the device (``GPT.compute_loss`` is the
@@ -91,6 +95,43 @@ class Module:
 
     def __call__(self, *args, **kwargs):
         return self.forward(*args, **kwargs)
+
+    def mark_parameters_changed(self):
+        """Declare that parameter values were edited in place: the device copies are
+        rebuilt at the next call (load/load_arrays do this themselves)."""
+        for p in self.parameters():
+            p._bump_version()
+
+
+# ------------------------------------------------------------------ resident copies
+def _params_key(params, dt, *extra):
+    """What a device copy depends on: each parameter's identity, version and buffer."""
+    def buf(p):
+        return p.data.ctypes.data if isinstance(p.data, np.ndarray) else id(p.data)
+
+    return (np.dtype(dt).str, extra, tuple((id(p), p._version, buf(p)) for p in params))
+
+
+def _resident(module, name, key, build):
+    """The device copy ``name`` of ``module`` for ``key``, built (and the previous one
+    released) when the key changed."""
+    cache = module.__dict__.setdefault("_device_copies", {})
+    hit = cache.get(name)
+    if hit is not None and hit[0] == key:
+        return hit[1]
+    if hit is not None and hasattr(hit[1], "close"):
+        hit[1].close()
+    value = build()
+    cache[name] = (key, value)
+    return value
+
+
+def _seq_capacity(s):
+    """Positions a cached device model is built for: at least 64, a power of two ≥ s."""
+    p = 64
+    while p < s:
+        p *= 2
+    return p
 
 
 # ------------------------------------------------------------------ device plumbing
@@ -188,8 +229,9 @@ def rope_device_arrays(rope_cache, head_dim, dt):
 
 
 class _CallModel:
-    """A device model built for one module-level call: only the arrays given are uploaded
-    (the token and position tables stay unused); freed with the object."""
+    """A device model of a module's parameters: only the arrays given are uploaded (the
+    token and position tables stay unused); kept by the module while its parameters are
+    unchanged, freed with the object."""
 
     def __init__(self, d_model, num_heads, num_layers, max_seq_len, d_ff, dt, arrays):
         N.ensure_init()
@@ -197,9 +239,11 @@ class _CallModel:
         N.check(N.lib.nml_model_create(1, d_model, num_heads, num_layers, max_seq_len, d_ff,
                                        N.np_dtype_code(dt), C.byref(h)))
         self.handle = h
+        self.max_seq_len = max_seq_len
         try:
             for kind, layer, arr in arrays:
                 N.check(N.lib.nml_model_set_param(h, kind, layer, arr.ctypes.data, arr.nbytes))
+                N.count_h2d(arr.nbytes)
         except Exception:
             self.close()
             raise
@@ -216,8 +260,9 @@ class _CallModel:
             pass
 
 
-def _blocks_forward(blocks, ln, x, mask, op, params):
-    """FusedTransformerBlock / FusedGPTTrunk forward over a (batch, seq, d) input."""
+def _blocks_forward(owner, blocks, ln, x, mask, op, params):
+    """FusedTransformerBlock / FusedGPTTrunk forward over a (batch, seq, d) input, on the
+    device model ``owner`` keeps of its parameters."""
     blocks = list(blocks)
     if len(x.shape) != 3:
         raise ValueError(f"expected (batch, seq, d_model), got {x.shape}")
@@ -228,28 +273,35 @@ def _blocks_forward(blocks, ln, x, mask, op, params):
     dt = _compute_dtype()
     causal, mdev = _mask_mode(mask, s, dt, none_is_causal=True)
     dk = d // blk0.num_heads
-    arrays = []
-    for i, blk in enumerate(blocks):
-        arrays += block_device_arrays(blk, i, dt)
-    arrays.append((N.P_LN_F, 0, _host(ln.gamma, (d,), dt) if ln is not None
-                   else np.ones(d, dtype=dt)))
     rope = blk0.mha._rope_cache
-    p = max(s, 1)
     if rope is not None:  # _fused_arrays.py:95-98: positions 0..seq-1 of the block's table
-        arrays += rope_device_arrays(rope, dk, dt)
         p = int(np.asarray(rope[0]).shape[0])
         if s > p:
             raise ValueError(f"Sequence length {s} exceeds the RoPE table ({p} positions)")
-    model = _CallModel(d, blk0.num_heads, len(blocks), p, blk0.ffn.dense1.out_features, dt,
-                       arrays)
+    else:
+        p = _seq_capacity(s)
+        hit = owner.__dict__.get("_device_copies", {}).get("blocks")
+        if hit is not None and hit[1].max_seq_len >= s:
+            p = hit[1].max_seq_len  # the cached model covers this length
+    rope_key = (id(rope[0]), id(rope[1])) if rope is not None else None
+
+    def build():
+        arrays = []
+        for i, blk in enumerate(blocks):
+            arrays += block_device_arrays(blk, i, dt)
+        arrays.append((N.P_LN_F, 0, _host(ln.gamma, (d,), dt) if ln is not None
+                       else np.ones(d, dtype=dt)))
+        if rope is not None:
+            arrays += rope_device_arrays(rope, dk, dt)
+        return _CallModel(d, blk0.num_heads, len(blocks), p, blk0.ffn.dense1.out_features, dt,
+                          arrays)
+
+    model = _resident(owner, "blocks", _params_key(params, dt, p, rope_key), build)
     xd = _device_input(x, dt)
     out = N.DeviceArray((b, s, d), dt)
-    try:
-        N.check(N.lib.nml_model_blocks_forward(model.handle, xd.ptr, out.ptr, b, s,
-                                               int(ln is not None), causal, N.ptr(mdev)))
-        N.check(N.lib.nml_synchronize())
-    finally:
-        model.close()
+    N.check(N.lib.nml_model_blocks_forward(model.handle, xd.ptr, out.ptr, b, s,
+                                           int(ln is not None), causal, N.ptr(mdev)))
+    N.check(N.lib.nml_synchronize())
     return _output(out, (b, s, d), x, params, op)
 
 
@@ -297,9 +349,20 @@ class Dense(Module):
         dt = _compute_dtype()
         shape = (*inputs.shape[:-1], self.out_features)
         x = _device_input(inputs, dt)
-        b = None if self.biases is None else _host(self.biases, (self.out_features,), dt)
-        out = K.linear(x, _host(self.weights, (self.in_features, self.out_features), dt), b)
+        w_t, b = self._device_weights(dt)
+        out = K.linear_t(x, w_t, b)
         return _output(out.reshape(shape), shape, inputs, self.parameters(), "dense")
+
+    def _device_weights(self, dt):
+        """(W transposed to (out, in), bias or None) on the device, kept while unchanged."""
+        def build():
+            w = np.ascontiguousarray(_host(self.weights, (self.in_features, self.out_features),
+                                           dt).T)
+            b = None if self.biases is None else _host(self.biases, (self.out_features,), dt)
+            return (N.DeviceArray.from_host(w),
+                    None if b is None else N.DeviceArray.from_host(b))
+
+        return _resident(self, "linear", _params_key(self.parameters(), dt), build)
 
     def parameters(self):
         return [self.weights] + ([self.biases] if self.biases is not None else [])
@@ -322,7 +385,7 @@ class Embedding(Module):
         else:
             ids = np.asarray(inputs, dtype=np.int64)
         dt = _compute_dtype()
-        w = N.DeviceArray.from_host(_host(self.weights, (self.vocab_size, self.embed_dim), dt))
+        w = self._device_table(dt)
         shape = (*ids.shape, self.embed_dim)
         if ids.size == 0:
             return _output(N.DeviceArray(shape, dt), shape, None, self.parameters(), "embedding")
@@ -334,10 +397,17 @@ class Embedding(Module):
         if seq_len < 0 or seq_len > self.vocab_size:
             raise ValueError(f"seq_len must be in [0, {self.vocab_size}), got {seq_len}.")
         dt = _compute_dtype()
-        rows = _host(self.weights, (self.vocab_size, self.embed_dim), dt)[:seq_len]
+        table = self._device_table(dt)
         shape = (seq_len, self.embed_dim)
-        return _output(N.DeviceArray.from_host(rows), shape, None, self.parameters(),
-                       "embedding_prefix")
+        rows = N.DeviceArray(shape, dt)
+        if rows.nbytes:
+            N.check(N.lib.nml_memcpy_d2d(rows.ptr, table.ptr, rows.nbytes))
+        return _output(rows, shape, None, self.parameters(), "embedding_prefix")
+
+    def _device_table(self, dt):
+        return _resident(self, "table", _params_key(self.parameters(), dt),
+                         lambda: N.DeviceArray.from_host(
+                             _host(self.weights, (self.vocab_size, self.embed_dim), dt)))
 
     def parameters(self):
         return [self.weights]
@@ -359,7 +429,9 @@ class RMSNorm(Module):
         d = self.normalized_shape
         rows = prod(inputs.shape[:-1]) if len(inputs.shape) > 1 else 1
         x = _device_input(inputs, dt).reshape(rows, d)
-        out = K.fused_rmsnorm_forward(x, _host(self.gamma, (d,), dt), self.epsilon)[0]
+        g = _resident(self, "gamma", _params_key(self.parameters(), dt),
+                      lambda: N.DeviceArray.from_host(_host(self.gamma, (d,), dt)))
+        out = K.fused_rmsnorm_forward(x, g, self.epsilon)[0]
         return _output(out.reshape(inputs.shape), inputs.shape, inputs, self.parameters(),
                        "rms_norm")
 
@@ -393,16 +465,18 @@ class MultiHeadAttention(Module):
         dt = _compute_dtype()
         causal, mdev = _mask_mode(mask, s, dt, none_is_causal=False)
         vec = 8 if dt == np.float16 else 4
-        model = _CallModel(d, self.num_heads, 1, max(s, 1), vec, dt,
-                           mha_device_arrays(self, 0, dt))
+        p = _seq_capacity(s)
+        hit = self.__dict__.get("_device_copies", {}).get("mha")
+        if hit is not None and hit[1].max_seq_len >= s:
+            p = hit[1].max_seq_len
+        model = _resident(self, "mha", _params_key(self.parameters(), dt, p),
+                          lambda: _CallModel(d, self.num_heads, 1, p, vec, dt,
+                                             mha_device_arrays(self, 0, dt)))
         xd = _device_input(x, dt)
         out = N.DeviceArray((b, s, d), dt)
-        try:
-            N.check(N.lib.nml_model_mha_forward(model.handle, 0, xd.ptr, out.ptr, b, s, causal,
-                                                N.ptr(mdev)))
-            N.check(N.lib.nml_synchronize())
-        finally:
-            model.close()
+        N.check(N.lib.nml_model_mha_forward(model.handle, 0, xd.ptr, out.ptr, b, s, causal,
+                                            N.ptr(mdev)))
+        N.check(N.lib.nml_synchronize())
         return _output(out, (b, s, d), x, self.parameters(), "multi_head_attention")
 
     def parameters(self):
@@ -433,10 +507,15 @@ class FeedForward(Module):
             raise ValueError(f"Expected output last dim {x.shape[-1]}, got {w2.out_features}")
         dt = _compute_dtype()
         xd = _device_input(x, dt)
-        h = K.linear(xd, _host(w1.weights, (w1.in_features, w1.out_features), dt),
-                     _dense_bias(w1, dt), epilogue=K.EPI_BIAS_GELU)
-        out = K.linear(h, _host(w2.weights, (w2.in_features, w2.out_features), dt),
-                       _dense_bias(w2, dt))
+        w1_t, b1 = w1._device_weights(dt)
+        w2_t, b2 = w2._device_weights(dt)
+        zero = None
+        if b1 is None or b2 is None:  # the GELU epilogue takes a bias: zeros for none
+            n = max(w1.out_features, w2.out_features)
+            zero = _resident(self, "zero_bias", (np.dtype(dt).str, n),
+                             lambda: N.DeviceArray.from_host(np.zeros(n, dtype=dt)))
+        h = K.linear_t(xd, w1_t, b1 if b1 is not None else zero, epilogue=K.EPI_BIAS_GELU)
+        out = K.linear_t(h, w2_t, b2 if b2 is not None else zero, epilogue=K.EPI_BIAS)
         return _output(out.reshape(x.shape), x.shape, x, self.parameters(), "feed_forward")
 
     def parameters(self):
@@ -458,7 +537,7 @@ class FusedTransformerBlock(Module):
     def forward(self, x, mask=None):
         """neural_network/transformer_fused.py:44-95 → fused_block_forward_arrays
         (_fused_arrays.py:251-284); ``mask=None`` is causal."""
-        return _blocks_forward([self], None, x, mask, "fused_transformer_block",
+        return _blocks_forward(self, [self], None, x, mask, "fused_transformer_block",
                                self.parameters())
 
     def parameters(self):
@@ -477,7 +556,7 @@ class FusedGPTTrunk(Module):
 
     def forward(self, x, mask=None):
         """transformer_fused.py:103-144: every block, then the final RMSNorm."""
-        return _blocks_forward(self.blocks, self.ln, x, mask, "fused_gpt_trunk",
+        return _blocks_forward(self, self.blocks, self.ln, x, mask, "fused_gpt_trunk",
                                self.parameters())
 
     def parameters(self):

@@ -86,7 +86,26 @@ def summary(t, layers):
     h = 4 + MARKS * layers
     lines.append(f"head: x in {np.nanmax(us[:, h]):.2f} us, logits out {np.nanmax(us[:, h + 1]):.2f} us, "
                  f"choice {np.nanmax(us[:, h + 2]):.2f} us (from the first mark)")
+    lines.extend(placement(t))
     return "\n".join(lines)
+
+
+def placement(t, xcds=8, heads=16):
+    """Mark 2 holds each workgroup's XCD (HW_REG_XCC_ID): the offset c with workgroup g on
+    XCD (g + c) % 8 (and how many follow it), and whether every head team (workgroups
+    x + 8·k, k in the head's range) shares one XCD."""
+    g = t.shape[0]
+    xcc = t[:, 2]
+    c = int((xcc[0] - 0) % xcds)
+    same = int(np.sum(xcc == (np.arange(g) + c) % xcds))
+    team = g // heads
+    split = 0
+    for h in range(heads):
+        x, k0 = h % xcds, (h // xcds) * team
+        members = [x + xcds * (k0 + k) for k in range(team)]
+        split += len(set(int(v) for v in xcc[members])) > 1
+    return [f"placement: {same}/{g} workgroups on XCD (g + {c}) % {xcds}; "
+            f"{split}/{heads} head teams spread over more than one XCD"]
 
 
 def main(argv):

@@ -76,6 +76,7 @@ def load_arrays(model, arrays):
         if loaded.size != param.size:
             raise ValueError(f"Shape mismatch for {name}: expected {param.shape}, got {loaded.shape}")
         param.data[...] = loaded.ravel()
+        param._bump_version()
     _mark_stale(model)
     return model
 

@@ -35,6 +35,7 @@ class Tensor:
         self._op = _op
         self._prev = set(_children)
         self._backward = None
+        self._version = 0  # bumped when the values change (device copies key on it)
 
     @classmethod
     def from_int64(cls, data, shape):
@@ -49,7 +50,12 @@ class Tensor:
         obj._op = ""
         obj._prev = set()
         obj._backward = None
+        obj._version = 0
         return obj
+
+    def _bump_version(self):
+        """Mark the values changed: device copies made from the old values are rebuilt."""
+        self._version += 1
 
     @property
     def ndim(self):

@@ -188,9 +188,17 @@ def test_tiny_sampled_generate(gpu, name, mode):
         if not live.any():
             break
     print(f"{name} {mode}: {compared} decidable tokens equal, {undecided} undecidable steps")
-    # fp32: every row is decidable for several steps. fp16: the tiny model's logits sit a
-    # few fp16 ulps apart, so fewer draws are decidable (measured 1-26 of 48).
-    assert compared >= (2 * ref.shape[0] if dt == np.float32 else 1), compared
+    # fp32: every draw is decidable (measured 48 of 48). fp16: the tiny model's logits sit
+    # a few fp16 ulps apart, so fewer draws are decidable; the bars are about 3/4 of the
+    # counts measured on green runs (topk 1 / 15, topp 4 / 3, reppen 26 / 21 for the plain
+    # / rich weights), so a path that loses tokens fails.
+    if dt == np.float32:
+        assert compared == ref.shape[0] * (ref.shape[1] - s0), compared
+    else:
+        want = {("tiny_fp16", "topk"): 1, ("tiny_rich_fp16", "topk"): 11,
+                ("tiny_fp16", "topp"): 3, ("tiny_rich_fp16", "topp"): 2,
+                ("tiny_fp16", "reppen"): 19, ("tiny_rich_fp16", "reppen"): 15}[(name, mode)]
+        assert compared >= want, compared
 
 
 def _u_near_boundary(logits, u, hist, kw, tol):
@@ -272,7 +280,8 @@ def test_small_generate_and_logits(gpu, name):
     margins = oracle_greedy_margins(w, cfg, f["greedy"], s0)
     compared = assert_tokens_agree(out, f["greedy"], s0, margins, 1e-3)
     print(f"{name}: {compared} greedy tokens compared")
-    assert compared >= f["greedy"].shape[0]
+    # every row up to its first near-tie; measured 575 (plain) and 181 (rich) of 8 × 192
+    assert compared >= {"small_fp32": 430, "small_rich_fp32": 135}[name], compared
     for t in f["logit_steps"]:
         lg = m.forward_last(f["greedy"][:, :s0 + int(t)]).numpy()
         assert np.abs(lg - f[f"logits_step{int(t)}"]).max() <= 1e-3

@@ -261,3 +261,49 @@ def test_module_outputs_refuse_backward(gpu):
         out.backward(np.ones(out.size, np.float32))
     with nm.no_grad():
         assert not blk(x).requires_grad
+
+
+@pytest.mark.parametrize("dtype_ctx", DTYPES, indirect=True)
+def test_module_forwards_keep_parameters_resident(dtype_ctx):
+    """Each module keeps a device copy of its parameters: a second call with unchanged
+    parameters (input already on the device) copies nothing host-to-device and gives the
+    same result; load_arrays, and mark_parameters_changed after an in-place edit, make
+    the next call upload again, and its result follows the new values."""
+    import nimbleml_amd as nm
+    from nimbleml_amd import _native as N
+
+    dt = dtype_ctx
+    w = weights(dt)
+    m = gpt_with(w, dt)
+    blk = m._block_list[0]
+    xh = xin(dt, seed=16)
+    x = nm.Tensor(N.DeviceArray.from_host(xh), xh.shape)
+    calls = [lambda: blk(x), lambda: m.blocks(x), lambda: blk.mha(x), lambda: blk.ffn(x),
+             lambda: blk.ln1(x), lambda: blk.mha.W_q(x)]
+    for call in calls:
+        first = np.asarray(call().data)
+        before = dict(N.h2d_stats)
+        again = np.asarray(call().data)
+        assert N.h2d_stats == before, (before, N.h2d_stats)
+        assert np.array_equal(first, again)
+    ids = np.arange(30, dtype=np.int64).reshape(2, 15)
+    m.token_emb(ids)
+    before = dict(N.h2d_stats)
+    m.token_emb(ids)
+    assert N.h2d_stats["bytes"] - before["bytes"] == ids.nbytes  # the ids only
+    # new values through load_arrays: uploaded again, and the result is the new block's
+    w2 = weights(dt, seed=12)
+    before = dict(N.h2d_stats)
+    nm.load_arrays(m, w2)
+    out = blk(x)
+    assert N.h2d_stats["calls"] > before["calls"]
+    ref = R.block(xh, w2, 0, CFG.num_heads, R.causal_mask(40, dt))
+    assert worst(out, ref) <= bound(dt, ref, 1e-5, 4)
+    # an in-place edit declared with mark_parameters_changed
+    blk.ln1.gamma.data[...] = (np.asarray(blk.ln1.gamma.data) * 2).astype(dt)
+    blk.mark_parameters_changed()
+    w3 = dict(w2)
+    w3["blocks.layers.0.ln1.gamma"] = (w2["blocks.layers.0.ln1.gamma"] * 2).astype(dt)
+    out = blk(x)
+    ref = R.block(xh, w3, 0, CFG.num_heads, R.causal_mask(40, dt))
+    assert worst(out, ref) <= bound(dt, ref, 1e-5, 4)
