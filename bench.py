@@ -23,7 +23,9 @@ Two more lines of the same metric ride along (BASELINE.json "batch 1 & 32"):
 token, host sampling; fp32 because NumPy fp16 has no BLAS path) on a bounded sample:
 C3 tokens spread over the run's contexts; c4 and c5 carry their own (c4: a few rows at
 batch 1, as the reference runs ragged prompts; c5: one block and the head on one
-sequence, extrapolated).
+sequence, extrapolated). `cpu_baseline_fp16` is the same algorithm in the reference's
+fp16 arithmetic, truncated to one layer at the run's first and last contexts plus the
+head and extrapolated (labelled so).
 """
 from __future__ import annotations
 
@@ -99,6 +101,39 @@ def cpu_baseline(cfg, w16, prompt, n_new, samples):
                       f"each a full re-forward as the reference does ({dt:.1f} s)"}
 
 
+def cpu_baseline_fp16(cfg, w16, prompt, n_new):
+    """The reference algorithm in its own fp16 arithmetic (oracle, every op rounded to fp16
+    as NumPy does), truncated: one re-forward token costs L blocks over the context plus
+    the last row's tied head. Timed here: layer 0 over the run's first and last contexts
+    (prompt and prompt + n_new − 1 tokens) and the head; the per-token cost of the run is
+    extrapolated as L × the mean block time + the head. The fp16 products go through the
+    oracle's C restatement of NumPy's fp16 matmul loop (bit-exact; NumPy's own loop, the
+    reference's, is about two orders of magnitude slower still)."""
+    from oracle import gpt_ref as R
+
+    s0 = prompt.shape[1]
+    rng = np.random.default_rng(4)
+    ids = np.concatenate([prompt, rng.integers(0, cfg.vocab_size, (1, n_new), dtype=np.int64)],
+                         axis=1)
+    blocks = []
+    for c in (s0, s0 + n_new - 1):
+        x = R.embed(w16["token_emb.weights"], w16["pos_emb.weights"], ids[:, :c])
+        t0 = time.perf_counter()
+        y = R.block(x, w16, 0, cfg.num_heads, R.causal_mask(c, x.dtype))
+        blocks.append(time.perf_counter() - t0)
+    t0 = time.perf_counter()
+    h = R.rmsnorm(y[0, -1:], w16["ln.gamma"])
+    R._mm(h, np.swapaxes(w16["token_emb.weights"], -2, -1))
+    head = time.perf_counter() - t0
+    per_token = cfg.num_layers * float(np.mean(blocks)) + head
+    return {"value": round(1.0 / per_token, 5), "unit": "tokens/s", "cores": int(cpu_threads()),
+            "kind": "port", "extrapolated": True,
+            "sample": f"C3 at fp16 (the reference's fp16 rounding): layer 0 re-forwarded over "
+                      f"{s0} and {s0 + n_new - 1} tokens ({blocks[0]:.1f} s, {blocks[1]:.1f} s) and "
+                      f"the last row's tied head ({head:.2f} s), extrapolated to {cfg.num_layers} "
+                      f"layers per generated token ({per_token:.1f} s per token)"}
+
+
 def bench_c3(nm, cfg, model, prompt, n, steps, warmup, use_graph):
     kw = dict(max_new_tokens=n, temperature=0.0, use_graph=use_graph)
     for _ in range(warmup):
@@ -143,15 +178,23 @@ def cpu_baseline_c4(cfg, w16, rows, new, samples=4):
                       f"{new} steps, full re-forward per token ({dt:.1f} s)"}
 
 
-def bench_c4(nm, cfg, model, use_graph, reps=2, w16=None):
+def bench_c4(nm, cfg, model, use_graph, reps=2, w16=None, uniform=False):
+    """C4 line: one warm-up generate() and `reps` timed ones (reps 0: the warm-up only,
+    for counter passes). uniform: every prompt at the ragged prompts' mean length (the
+    same decode kernels and per-step bytes, through the uniform prefill path)."""
     rng = np.random.default_rng(5)
     lens = rng.integers(128, 1025, 32)
+    if uniform:
+        lens = np.full(32, int(round(lens.mean())))
     rows = [rng.integers(0, cfg.vocab_size, int(n)) for n in lens]
     new = 256
     kw = dict(max_new_tokens=new, temperature=0.8, top_k=50, top_p=1.0, use_graph=use_graph)
     np.random.seed(0)
     nm.generate(model, rows, **kw)  # warm-up
     nm._native.synchronize()
+    if reps == 0:
+        return {"workload": "C4 warm-up generate() only (counter pass)",
+                "decode_ms_per_step": round(model.last_decode_ms(), 4)}
     t0 = time.perf_counter()
     decode_ms = []
     for _ in range(reps):
@@ -331,6 +374,10 @@ def main():
     ap.add_argument("--only-c3", action="store_true", help="skip the batch-32 and prefill lines")
     ap.add_argument("--only", choices=["c3", "c4", "c5", "adamw", "train", "train16"], default=None,
                     help="run one workload only (for profiling); c4/c5 print their own line")
+    ap.add_argument("--c4-uniform", action="store_true",
+                    help="C4 with every prompt at the ragged lengths' mean (counter passes)")
+    ap.add_argument("--c4-reps", type=int, default=2,
+                    help="timed generate() calls of the C4 line (0: the warm-up only)")
     ap.add_argument("--cpu-samples", type=int, default=8,
                     help="tokens of the CPU baseline, spread over the run's contexts")
     ap.add_argument("--copy-calibration", action="store_true",
@@ -378,8 +425,9 @@ def main():
     n = args.new_tokens
     use_graph = not args.no_graph
     if args.only == "c4":
-        print(json.dumps({"c4": bench_c4(nm, cfg, model, use_graph,
-                                         w16=None if args.no_cpu_baseline else w16)}), flush=True)
+        print(json.dumps({"c4": bench_c4(nm, cfg, model, use_graph, reps=args.c4_reps,
+                                         w16=None if args.no_cpu_baseline else w16,
+                                         uniform=args.c4_uniform)}), flush=True)
         return
 
     elapsed, step_ms, bytes_avg, persistent = bench_c3(nm, cfg, model, prompt, n, args.steps,
@@ -419,6 +467,7 @@ def main():
         result["train16"] = bench_train(nm, dtype=np.float16)
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline(cfg, w16, prompt, args.new_tokens, args.cpu_samples)
+        result["cpu_baseline_fp16"] = cpu_baseline_fp16(cfg, w16, prompt, args.new_tokens)
     print(json.dumps(result), flush=True)
 
 
