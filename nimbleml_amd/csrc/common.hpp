@@ -25,6 +25,8 @@ inline size_t dtype_size(int dt) { return dt == F16 ? 2 : 4; }
 // Per-thread error text (host side).
 void set_error(const char* fmt, ...) __attribute__((format(printf, 1, 2)));
 hipStream_t stream();
+hipStream_t stream2();  // a second stream for forked work, joined back by events
+bool is_stream2(hipStream_t s);
 
 constexpr int kWave = 64;
 

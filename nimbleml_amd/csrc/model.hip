@@ -105,13 +105,13 @@ struct Acts {
   float* ssq;   // decode: (Bdec, d/16) sums of squares of x in 16-column pieces
 };
 
-int acts_for(nml_model* m, int R, int Bdec, Acts* a) {
+int acts_in(nml_model* m, Buf& buf, int R, int Bdec, Acts* a) {
   const size_t rd = align256((size_t)R * m->d * m->es);
   const size_t rf = align256((size_t)R * m->F * m->es);
   const size_t part = Bdec ? align256(attention_decode_workspace(Bdec, m->H, m->dk, m->P)) : 0;
   const size_t ssq = Bdec ? align256((size_t)Bdec * (m->d / 16 + 1) * sizeof(float)) : 0;
-  NML_TRY(m->ws.ensure(4 * rd + rf + part + ssq));
-  char* b = static_cast<char*>(m->ws.p);
+  NML_TRY(buf.ensure(4 * rd + rf + part + ssq));
+  char* b = static_cast<char*>(buf.p);
   a->x = b;
   a->xn = b + rd;
   a->q = b + 2 * rd;
@@ -121,6 +121,8 @@ int acts_for(nml_model* m, int R, int Bdec, Acts* a) {
   a->ssq = ssq ? reinterpret_cast<float*>(b + 4 * rd + rf + part) : nullptr;
   return 0;
 }
+
+int acts_for(nml_model* m, int R, int Bdec, Acts* a) { return acts_in(m, m->ws, R, Bdec, a); }
 
 // Small device scratch: [0] int err, then B int32 positions etc.
 struct Small {
@@ -290,15 +292,21 @@ int head(nml_model* m, const Acts& a, int B, int S, void* logits, int last_only,
 }
 
 
-// One decode step for B rows of a cache: feeds tokens[b][pos[b]] at position
-// pos[b], leaves logits (B, V) in `logits`.
-int decode_step(nml_model* m, nml_cache* c, const Acts& a, const int64_t* tokens,
+// One decode step for rows [b0, b0 + Bn) of a cache: feeds tokens[b][pos[b]] at position
+// pos[b], leaves those rows' logits (B, V; row b at b·V) in `logits`. tokens, pos and
+// logits are the whole batch's arrays.
+int decode_step(nml_model* m, nml_cache* c, const Acts& a, int b0, int Bn, const int64_t* tokens,
                 long long tok_stride, int32_t* pos, int* err, void* logits, int max_len,
                 hipStream_t st) {
-  const int B = c->B, d = m->d;
+  const int B = Bn, d = m->d;
+  tokens += (long long)b0 * tok_stride;
+  pos += b0;
+  logits = static_cast<char*>(logits) + (size_t)b0 * m->V * m->es;
   NML_TRY(launch_embed_decode(m->dt, tokens, tok_stride, pos, m->emb, posw(m), a.x, B, d, m->V,
                               m->P, err, st));
-  const size_t layer_kv = (size_t)B * m->H * m->P * m->dk * m->es;
+  // the cache holds all c->B rows per layer; this step's rows start at row b0
+  const size_t layer_kv = (size_t)c->B * m->H * m->P * m->dk * m->es;
+  const size_t row0 = (size_t)b0 * m->H * m->P * m->dk * m->es;
   // RMSNorm fused into the GEMMs that consume it (fp16, 8 < B ≤ 64): the residual GEMMs
   // (W_o, W2) leave per-piece sums of squares of x in a.ssq, and QKV, W1 and the head
   // normalise x on load; layer 0's input (the embedding) still takes the RMSNorm kernel.
@@ -309,8 +317,8 @@ int decode_step(nml_model* m, nml_cache* c, const Acts& a, const int64_t* tokens
                     linear_norm_fusable(m->dt, B, d, m->V);
   for (int l = 0; l < m->L; ++l) {
     const Layer& w = m->layers[l];
-    void* kl = static_cast<char*>(c->k) + l * layer_kv;
-    void* vl = static_cast<char*>(c->v) + l * layer_kv;
+    void* kl = static_cast<char*>(c->k) + l * layer_kv + row0;
+    void* vl = static_cast<char*>(c->v) + l * layer_kv + row0;
     const long long sb = (long long)m->H * m->P * m->dk, sh = (long long)m->P * m->dk;
     const bool fuse_in = fuse && l > 0;
     if (!fuse_in) NML_TRY(launch_rmsnorm(m->dt, a.x, w.ln1, a.xn, nullptr, nullptr, B, d, kEps, st));
@@ -623,7 +631,7 @@ int decode_rows(nml_model* m, nml_cache* c, const int64_t* ids, void* logits, hi
   NML_TRY(acts_for(m, B, B, &a));
   // the workspace is shared with other forwards: clear the attention partials each call
   NML_HIP(hipMemsetAsync(a.part, 0, attention_decode_workspace(B, m->H, m->dk, m->P), st));
-  NML_TRY(decode_step(m, c, a, c->tok, m->P, c->len_dev, c->err, logits, maxlen + 1, st));
+  NML_TRY(decode_step(m, c, a, 0, B, c->tok, m->P, c->len_dev, c->err, logits, maxlen + 1, st));
   add_scalar_kernel<<<(B + 255) / 256, 256, 0, st>>>(c->len_dev, B, 1);
   NML_LAUNCHED();
   for (auto& v : c->len) v += 1;
@@ -703,6 +711,7 @@ int nml_model_destroy(nml_model* m) {
   if (!m) return 0;
   (void)hipStreamSynchronize(nml::stream());
   m->ws.release();
+  m->ws2.release();
   m->kvs.release();
   m->logits_ws.release();
   m->small.release();
@@ -1091,9 +1100,32 @@ int nml_model_generate(nml_model* m, const int64_t* prompts, size_t prompt_strid
   sa.plen = sm.plen;
   NML_TRY(launch_sample(m->dt, sa, st));
 
-  Acts a;
-  NML_TRY(acts_for(m, B, B, &a));
-  NML_HIP(hipMemsetAsync(a.part, 0, attention_decode_workspace(B, m->H, m->dk, m->P), st));
+  // Batched decode in two halves on two streams (NIMBLEML_DECODE_SPLIT=0: one): one
+  // half's latency-bound projections run beside the other half's bandwidth-bound
+  // attention. Each half has its own activations and attention workspace.
+  const char* se = std::getenv("NIMBLEML_DECODE_SPLIT");
+  const bool split = !(se && se[0] == '0') && B >= 16 && B % 2 == 0;
+  const int BA = split ? B / 2 : B;
+  Acts a, a2;
+  NML_TRY(acts_for(m, BA, BA, &a));
+  NML_HIP(hipMemsetAsync(a.part, 0, attention_decode_workspace(BA, m->H, m->dk, m->P), st));
+  hipStream_t st2 = nullptr;
+  hipEvent_t ev_fork = nullptr, ev_join = nullptr;
+  struct EvGuard {
+    hipEvent_t* e[2];
+    ~EvGuard() {
+      for (hipEvent_t* p : e)
+        if (*p) (void)hipEventDestroy(*p);
+    }
+  } ev_guard{{&ev_fork, &ev_join}};
+  if (split) {
+    NML_TRY(acts_in(m, m->ws2, BA, BA, &a2));
+    NML_HIP(hipMemsetAsync(a2.part, 0, attention_decode_workspace(BA, m->H, m->dk, m->P), st));
+    st2 = nml::stream2();
+    NML_REQUIRE(st2 != nullptr, "decode: second stream unavailable");
+    NML_HIP(hipEventCreateWithFlags(&ev_fork, hipEventDisableTiming));
+    NML_HIP(hipEventCreateWithFlags(&ev_join, hipEventDisableTiming));
+  }
   // Attention length bound of the decode steps: the last step feeds position
   // maxp + max_new - 2 and attends to every key up to it.
   const int decode_len = maxp + (int)max_new - 1;
@@ -1122,7 +1154,18 @@ int nml_model_generate(nml_model* m, const int64_t* prompts, size_t prompt_strid
       NML_TRY(launch_decode_persist(m->dt, m->d, m->H, pa, st));
       return pa.fuse_argmax ? 0 : launch_sample(m->dt, sa, st);
     }
-    NML_TRY(decode_step(m, c, a, tokens_out, (long long)out_stride, sm.pos, sm.err, logits,
+    if (split) {  // fork: rows [BA, B) on the second stream, then join before sampling
+      NML_HIP(hipEventRecord(ev_fork, st));
+      NML_HIP(hipStreamWaitEvent(st2, ev_fork, 0));
+      NML_TRY(decode_step(m, c, a2, BA, B - BA, tokens_out, (long long)out_stride, sm.pos, sm.err,
+                          logits, decode_len, st2));
+      NML_TRY(decode_step(m, c, a, 0, BA, tokens_out, (long long)out_stride, sm.pos, sm.err,
+                          logits, decode_len, st));
+      NML_HIP(hipEventRecord(ev_join, st2));
+      NML_HIP(hipStreamWaitEvent(st, ev_join, 0));
+      return launch_sample(m->dt, sa, st);
+    }
+    NML_TRY(decode_step(m, c, a, 0, B, tokens_out, (long long)out_stride, sm.pos, sm.err, logits,
                         decode_len, st));
     return launch_sample(m->dt, sa, st);
   };

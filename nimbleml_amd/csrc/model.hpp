@@ -56,6 +56,7 @@ struct nml_model {
   bool rope_cos_set = false, rope_sin_set = false;
   std::vector<nml::Layer> layers;
   nml::Buf ws;         // activations
+  nml::Buf ws2;        // activations of the second half of a split batched decode
   nml::Buf kvs;        // K/V scratch for forward() without a cache
   nml::Buf logits_ws;  // logits chunk for compute_loss / generate
   nml::Buf small;      // device counters, positions, loss accumulators

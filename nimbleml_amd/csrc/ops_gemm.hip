@@ -978,7 +978,10 @@ struct SkinnyWs {
   size_t part_slots = 0;
   int tiles = 0;
 };
-SkinnyWs g_skinny;
+// One workspace per library stream (the second serves work forked onto stream2), so
+// split-K launches on the two streams never share partial slots.
+SkinnyWs g_skinny_ws[2];
+inline SkinnyWs& skinny_ws(hipStream_t st) { return g_skinny_ws[is_stream2(st) ? 1 : 0]; }
 
 template <int EPI, int MT, int U, bool NORM>
 __global__ __launch_bounds__(256) void skinny_f16_kernel(LinearArgs a, unsigned long long* ws) {
@@ -1211,22 +1214,22 @@ __global__ __launch_bounds__(256) void skinny_f16_kernel(LinearArgs a, unsigned 
 // Slices of K: about 1024 columns of K per workgroup (measured on MI355X with weights
 // streamed from HBM: unsplit is fastest for K = 1024 at N = 1024…4096, four slices for
 // K = 4096), each wave's part of K a multiple of 32, and a workspace large enough.
-int skinny_slices(const LinearArgs& a, int MT) {
+int skinny_slices(const LinearArgs& a, int MT, const SkinnyWs& w) {
   const int tiles = (a.N + kSkN - 1) / kSkN;
   int S = 1;
   while (S < 8 && a.K / S > 1024 && a.K % (128 * S * 2) == 0) S *= 2;
-  while (S > 1 && (tiles > g_skinny.tiles ||
-                   static_cast<size_t>(tiles) * (S - 1) * MT * 256 > g_skinny.part_slots))
+  while (S > 1 && (tiles > w.tiles || static_cast<size_t>(tiles) * (S - 1) * MT * 256 > w.part_slots))
     S /= 2;
   return S;
 }
 
 template <int EPI, int MT, bool NORM>
 int skinny_launch(const LinearArgs& a, hipStream_t st) {
-  const int S = skinny_slices(a, MT);
+  const SkinnyWs& w = skinny_ws(st);
+  const int S = skinny_slices(a, MT, w);
   dim3 grid((a.N + kSkN - 1) / kSkN, S);
   const int kq = a.K / (4 * S);
-  unsigned long long* ws = g_skinny.part;
+  unsigned long long* ws = w.part;
   if (kq == 256)  // every operand of the wave in one round trip
     skinny_f16_kernel<EPI, MT, 8, NORM><<<grid, 256, 0, st>>>(a, ws);
   else if (kq % 128 == 0)
@@ -1448,16 +1451,18 @@ int linear_reserve_workspace(int max_n) {
   // tiles), zeroed. Grow-only; call outside stream capture.
   const int tiles = (max_n + kSkN - 1) / kSkN;
   const size_t slots = static_cast<size_t>(tiles) * 7 * 4 * 256;
-  if (tiles <= g_skinny.tiles && slots <= g_skinny.part_slots) return 0;
-  NML_HIP(hipStreamSynchronize(stream()));
-  if (g_skinny.part) NML_HIP(hipFree(g_skinny.part));
-  g_skinny = SkinnyWs{};
-  unsigned long long* p = nullptr;
-  NML_HIP(hipMalloc(&p, slots * 8));
-  NML_HIP(hipMemset(p, 0, slots * 8));
-  g_skinny.part = p;
-  g_skinny.part_slots = slots;
-  g_skinny.tiles = tiles;
+  for (SkinnyWs& w : g_skinny_ws) {
+    if (tiles <= w.tiles && slots <= w.part_slots) continue;
+    NML_HIP(hipDeviceSynchronize());  // both streams may hold launches that use it
+    if (w.part) NML_HIP(hipFree(w.part));
+    w = SkinnyWs{};
+    unsigned long long* p = nullptr;
+    NML_HIP(hipMalloc(&p, slots * 8));
+    NML_HIP(hipMemset(p, 0, slots * 8));
+    w.part = p;
+    w.part_slots = slots;
+    w.tiles = tiles;
+  }
   return 0;
 }
 

@@ -30,6 +30,21 @@ void set_error(const char* fmt, ...) {
 
 hipStream_t stream() { return g_stream; }
 
+// A second library stream (default priority, like the first) for work the library forks
+// off the library stream and joins back with events; created on first use.
+namespace {
+hipStream_t g_stream2 = nullptr;
+}
+
+hipStream_t stream2() {
+  std::lock_guard<std::mutex> lock(g_init_mu);
+  if (g_stream2 == nullptr && hipStreamCreateWithFlags(&g_stream2, hipStreamNonBlocking) != hipSuccess)
+    g_stream2 = nullptr;
+  return g_stream2;
+}
+
+bool is_stream2(hipStream_t s) { return s != nullptr && s == g_stream2; }
+
 }  // namespace nml
 
 using nml::set_error;
