@@ -248,7 +248,7 @@ def bench_adamw(nm, n=337_100_000, steps=20):
 MFMA_F32_PEAK_TFLOPS = 157.3
 
 
-def bench_train(nm, batch=4, seq=1024, steps=3, dtype=np.float32):
+def bench_train(nm, batch=4, seq=1024, steps=3, dtype=np.float32, skew=False):
     """One training step of the C3 architecture in float32: zero_grad, compute_loss keeping
     the activations (nml_model_loss_train), loss.backward() into the device gradients
     (nml_model_backward) and AdamW over every parameter (nml_model_adamw_step), batch × seq
@@ -266,7 +266,10 @@ def bench_train(nm, batch=4, seq=1024, steps=3, dtype=np.float32):
                                cfg.max_seq_len, dtype=dtype)
     del w
     h = model._device_model()
-    ids = N.DeviceArray.from_host(random_ids((batch, seq), cfg.vocab_size, seed=3))
+    ids_h = random_ids((batch, seq), cfg.vocab_size, seed=3)
+    if skew:  # half of the positions hold one id (a pad token): the embedding scatter's worst case
+        ids_h.reshape(-1)[::2] = 7
+    ids = N.DeviceArray.from_host(ids_h)
     lab = N.DeviceArray.from_host(random_ids((batch * seq,), cfg.vocab_size, seed=4))
     loss = C.c_double()
     t_step = [0]
@@ -294,7 +297,8 @@ def bench_train(nm, batch=4, seq=1024, steps=3, dtype=np.float32):
     # attention backward still runs on the fp32 MFMA, from fp16 operands)
     peak = MFMA_F32_PEAK_TFLOPS if dtype == np.float32 else MFMA_F16_PEAK_TFLOPS
     return {"workload": f"train step: GPT V32000 d1024 H16 L24 {name}, batch {batch} x {seq}, "
-                        "zero_grad + compute_loss + backward + AdamW on the device",
+                        "zero_grad + compute_loss + backward + AdamW on the device"
+                        + (" (half of the ids one token)" if skew else ""),
             "value": round(R / (ms * 1e-3), 1), "unit": "tokens/s", "ms_per_step": round(ms, 3),
             "loss": round(loss.value, 5),
             "roofline": {"bound": "mfma", "achieved": round(tf, 1), "peak": peak,
@@ -374,6 +378,8 @@ def main():
     ap.add_argument("--only-c3", action="store_true", help="skip the batch-32 and prefill lines")
     ap.add_argument("--only", choices=["c3", "c4", "c5", "adamw", "train", "train16"], default=None,
                     help="run one workload only (for profiling); c4/c5 print their own line")
+    ap.add_argument("--train-skew", action="store_true",
+                    help="train lines with half of the input ids one token (embedding scatter)")
     ap.add_argument("--c4-uniform", action="store_true",
                     help="C4 with every prompt at the ragged lengths' mean (counter passes)")
     ap.add_argument("--c4-reps", type=int, default=2,
@@ -415,7 +421,8 @@ def main():
         print(json.dumps({"train": bench_train(nm)}), flush=True)
         return
     if args.only == "train16":
-        print(json.dumps({"train16": bench_train(nm, dtype=np.float16)}), flush=True)
+        print(json.dumps({"train16": bench_train(nm, dtype=np.float16, skew=args.train_skew)}),
+              flush=True)
         return
     w16 = make_weights(cfg, seed=1234, dtype=np.float16)
     model = nm.GPT.from_arrays(w16, cfg.vocab_size, cfg.d_model, cfg.num_heads, cfg.num_layers,

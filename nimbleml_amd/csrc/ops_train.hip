@@ -1820,14 +1820,31 @@ __global__ __launch_bounds__(256) void embed_bwd_tok_kernel(const T* __restrict_
     const int tot = s_cnt[0] + s_cnt[1] + s_cnt[2] + s_cnt[3];
     if (hit) s_idx[off + __popcll(m & ((1ull << lane) - 1ull))] = j;
     __syncthreads();
-    // each column read once, its rows added in ascending order in a register, stored
-    // once: the loads of a column's rows are independent, so a frequent id (a pad token)
-    // costs a stream of loads rather than a chain of read-modify-writes per row
-    for (int c = t; c < d; c += 256) {
-      float acc = dst[c];
-#pragma unroll 4
-      for (int q = 0; q < tot; ++q) acc += static_cast<float>(g[static_cast<long long>(s_idx[q]) * d + c]);
-      dst[c] = acc;
+    // each column read once, its rows added in ascending order in registers, stored
+    // once: thread t owns 4 adjacent columns (one 8- or 16-byte load per row) and keeps 8
+    // rows' loads in flight, so a frequent id (a pad token) costs a stream of loads rather
+    // than a chain of read-modify-writes per row (d is a multiple of 4)
+    for (int c = 4 * t; c < d; c += 1024) {
+      float acc[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) acc[e] = dst[c + e];
+      for (int q0 = 0; q0 < tot; q0 += 8) {
+        T v[8][4];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+          const int q = q0 + u < tot ? q0 + u : q0;  // past tot: a valid row, never added
+          const T* src = g + static_cast<long long>(s_idx[q]) * d + c;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) v[u][e] = src[e];
+        }
+#pragma unroll
+        for (int u = 0; u < 8; ++u)
+          if (q0 + u < tot)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) acc[e] += static_cast<float>(v[u][e]);
+      }
+#pragma unroll
+      for (int e = 0; e < 4; ++e) dst[c + e] = acc[e];
     }
     __syncthreads();
   }
