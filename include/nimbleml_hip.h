@@ -103,6 +103,30 @@ int nml_rmsnorm_backward_device(const float* grad, const float* x, const float* 
                                 const float* ms, const float* rms, float* grad_x,
                                 float* grad_gamma, size_t rows, size_t dim, float eps);
 
+/* Backward helpers of the module-level autograd closures, in the compute dtype (dtype 0
+ * float32, 1 float16); parameter gradients are float32 and ADDED to, as
+ * Tensor._accumulate_grad does (utils/tensor.py:334-352). Each returns after the device
+ * finishes. */
+/* Dense.forward's closure (layers/dense.py:81-94): dy (rows, out), x (rows, in), w_t the
+ * weight transposed to (out, in), as the device keeps it. dx (rows, in) = dy·W is
+ * overwritten; with gelu_pre (rows, in) non-NULL — the pre-activation whose GELU gave x —
+ * dx = (dy·W)·gelu'(gelu_pre) instead, the GELU backward of FeedForward's closure
+ * (neural_network/feed_forward.py:105-129, kernels/fused_gelu.py:86-111). dw_t
+ * (out, in) += dyᵀ·x; db (out) += Σ_rows dy. dx, dw_t, db may each be NULL. */
+int nml_linear_backward_device(const void* dy, const void* x, const void* w_t, void* dx,
+                               float* dw_t, float* db, size_t rows, size_t in_features,
+                               size_t out_features, const void* gelu_pre, int dtype);
+/* RMSNorm's closure (layers/rms_norm.py:76-94 → kernels/fused_rmsnorm.py:195-217) in the
+ * compute dtype: grad_x (rows, dim) overwritten, grad_gamma (dim, float32) added to. */
+int nml_rmsnorm_backward_typed_device(const void* grad, const void* x, const void* gamma,
+                                      void* grad_x, float* grad_gamma, size_t rows, size_t dim,
+                                      float eps, int dtype);
+/* Embedding's closure (layers/embedding.py:63-69 → kernels/embedding_scatter.py:39-60):
+ * grad_weights[ids[r]] += grad[r] for each of the rows, in ascending row order per id;
+ * ids outside [0, vocab) add nothing. */
+int nml_embedding_backward_device(const void* grad, const int64_t* ids, float* grad_weights,
+                                  size_t rows, size_t dim, size_t vocab, int dtype);
+
 /* Causal attention in the compute dtype as the reference's CPU path computes it for GPT
  * (kernels/fused_sdpa.py:71-78, reached from fused_sdpa_forward :256-289 with the causal
  * mask): scores (q·k) / scale_div with scale_div = sqrt(dk) (attention.py:135), softmax,
@@ -243,6 +267,27 @@ int nml_model_blocks_forward(nml_model* m, const void* x, void* out, size_t batc
  * a NULL mask. x, out: device (batch, seq, d_model), distinct buffers. */
 int nml_model_mha_forward(nml_model* m, int layer, const void* x, void* out, size_t batch,
                           size_t seq, int causal, const void* mask);
+
+/* Module-level autograd: the autograd closures that FusedTransformerBlock.forward,
+ * FusedGPTTrunk.forward (neural_network/transformer_fused.py:65-78, :123-131) and the
+ * attention of MultiHeadAttention.forward (neural_network/attention.py:103-119) attach.
+ * A *_forward_train call computes the same output as its forward above and keeps the
+ * activations its backward needs in the model's training state (one saved forward per
+ * model: each saving forward, nml_model_loss_train included, replaces the last and
+ * advances nml_model_saved_generation; a mask is copied). Its *_backward takes
+ * dout = d(loss)/d(out) (device, the compute dtype, out's shape), ADDS d(loss)/d(param)
+ * of every parameter the forward used to the float32 gradients (nml_model_grad_ptr), and
+ * writes dx = d(loss)/d(x) (same shape as x; NULL skips it). Backward returns after the
+ * device finishes. Non-causal and masked attention backward runs on the scalar kernels. */
+int nml_model_blocks_forward_train(nml_model* m, const void* x, void* out, size_t batch,
+                                   size_t seq, int final_norm, int causal, const void* mask);
+/* fused_block_backward_arrays / fused_trunk_backward_arrays (_fused_arrays.py:311-377). */
+int nml_model_blocks_backward(nml_model* m, const void* dout, void* dx);
+int nml_model_mha_forward_train(nml_model* m, int layer, const void* x, void* out, size_t batch,
+                                size_t seq, int causal, const void* mask);
+/* mha_backward_arrays (_fused_arrays.py:129-184) without RoPE, the SDPA backward of
+ * kernels/fused_sdpa.py:26-29, :81-88 for the forward's mask. */
+int nml_model_mha_backward(nml_model* m, const void* dout, void* dx);
 
 /* GPT.compute_loss (models/gpt.py:123-137): mean tied-head CE over batch·seq rows,
  * labels device int64. Returns after the device finishes; *loss is float64. */

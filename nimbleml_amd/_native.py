@@ -58,6 +58,9 @@ _SIGS = {
     "nml_flash_sdpa_forward_device": [vp, vp, vp, vp, vp, vp, sz, sz, sz, f32],
     "nml_flash_sdpa_backward_device": [vp, vp, vp, vp, vp, vp, vp, vp, vp, sz, sz, sz, f32],
     "nml_rmsnorm_backward_device": [vp, vp, vp, vp, vp, vp, vp, sz, sz, f32],
+    "nml_linear_backward_device": [vp, vp, vp, vp, vp, vp, sz, sz, sz, vp, i32],
+    "nml_rmsnorm_backward_typed_device": [vp, vp, vp, vp, vp, sz, sz, f32, i32],
+    "nml_embedding_backward_device": [vp, vp, vp, sz, sz, sz, i32],
     "nml_causal_attention_device": [vp, vp, vp, vp, sz, sz, sz, f32, i32],
     "nml_decode_attention_device": [vp, vp, vp, vp, vp, sz, sz, sz, sz, f32, vp, i32],
     "nml_sdpa_forward_device": [vp, vp, vp, vp, vp, sz, sz, sz, f32, i32, i32],
@@ -74,6 +77,10 @@ _SIGS = {
     "nml_model_forward": [vp, vp, sz, sz, vp, i32],
     "nml_model_blocks_forward": [vp, vp, vp, sz, sz, i32, i32, vp],
     "nml_model_mha_forward": [vp, i32, vp, vp, sz, sz, i32, vp],
+    "nml_model_blocks_forward_train": [vp, vp, vp, sz, sz, i32, i32, vp],
+    "nml_model_blocks_backward": [vp, vp, vp],
+    "nml_model_mha_forward_train": [vp, i32, vp, vp, sz, sz, i32, vp],
+    "nml_model_mha_backward": [vp, vp, vp],
     "nml_model_loss": [vp, vp, vp, sz, sz, i64, i32, C.POINTER(C.c_double)],
     "nml_model_zero_grad": [vp],
     "nml_model_grad_ptr": [vp, i32, i32, C.POINTER(C.c_void_p)],

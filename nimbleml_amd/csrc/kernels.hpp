@@ -229,10 +229,12 @@ int launch_colsum(int dt, const void* a, long long lda, int rows, int n, float* 
 int launch_ce_grad(int dt, void* logits, int rows, int V, const int64_t* labels,
                    long long ignore_index, int has_ignore, float scale, hipStream_t st);
 
-// Causal attention backward for one layer (kernels/fused_sdpa.py:26-29, :81-88). q, k, v
+// Attention backward for one layer (kernels/fused_sdpa.py:26-29, :81-88). q, k, v
 // head-major (B, H, S, dk) as the forward saw them (after RoPE); o and dout merged-head
 // (B·S, H·dk); lse from the forward; dvec scratch (B, H, S) floats. Writes dq, dk, dv
-// into dqkv (B·S, 3·H·dk) at column offsets 0, H·dk, 2·H·dk (all of type dt).
+// into dqkv (B·S, 3·H·dk) at column offsets 0, H·dk, 2·H·dk (all of type dt). Causal
+// unless `full`; a full call may add an (S, S) mask of type dt to the scores, as the
+// forward's non-causal path did (the scalar kernels take it).
 struct AttnBwdArgs {
   const void* q;
   const void* k;
@@ -244,6 +246,8 @@ struct AttnBwdArgs {
   void* dqkv;
   int B, H, S, dk;
   float scale;  // sqrt(dk), the divisor of the scores
+  int full = 0;
+  const void* mask = nullptr;
 };
 int launch_attention_backward(int dt, const AttnBwdArgs& a, hipStream_t st);
 // RoPE backward on dqkv rows (the dq and dk parts): pair (i, i + dk/2) of row b·S + s

@@ -406,6 +406,75 @@ int nml_rmsnorm_backward_device(const float* grad, const float* x, const float* 
                             static_cast<float*>(g_scratch.p), (int)rows, (int)dim, eps, st);
 }
 
+int nml_linear_backward_device(const void* dy, const void* x, const void* w_t, void* dx,
+                               float* dw_t, float* db, size_t rows, size_t in_features,
+                               size_t out_features, const void* gelu_pre, int dtype) {
+  NML_TRY(check_dtype(dtype));
+  NML_REQUIRE(rows <= 0x7fffffff && in_features <= 0x7fffffff && out_features <= 0x7fffffff,
+              "linear backward: shape too large");
+  NML_REQUIRE(!gelu_pre || dx, "linear backward: gelu_pre given without dx");
+  if (rows == 0 || in_features == 0 || out_features == 0) return 0;
+  const int M = (int)rows, K = (int)in_features, N = (int)out_features;
+  hipStream_t st = nml::stream();
+  auto gbw = [](const void* a, long long lda, const void* b, long long ldb, void* c,
+                long long ldc, int m, int n, int k, const void* aux, long long ldaux) {
+    GemmBwdArgs g{};
+    g.a = a;
+    g.lda = lda;
+    g.b = b;
+    g.ldb = ldb;
+    g.c = c;
+    g.ldc = ldc;
+    g.aux = aux;
+    g.ldaux = ldaux;
+    g.M = m;
+    g.N = n;
+    g.K = k;
+    return g;
+  };
+  if (dx)  // dx(r, i) = Σ_o dy(r, o)·W(o, i) [· gelu'(pre(r, i))]
+    NML_TRY(launch_gemm_bwd(dtype, gbw(dy, N, w_t, K, dx, K, M, K, N, gelu_pre, K), true, false,
+                            gelu_pre ? GB_GELU : GB_SET, st));
+  if (dw_t)  // dW(o, i) += Σ_r dy(r, o)·x(r, i)
+    NML_TRY(launch_gemm_bwd(dtype, gbw(dy, N, x, K, dw_t, K, N, K, M, nullptr, 0), false, false,
+                            GB_ADD, st));
+  if (db) {  // db(o) += Σ_r dy(r, o)
+    NML_TRY(g_scratch.ensure((size_t)colsum_parts(M) * N * sizeof(float)));
+    NML_TRY(launch_colsum(dtype, dy, N, M, N, db, static_cast<float*>(g_scratch.p), st));
+  }
+  NML_HIP(hipStreamSynchronize(st));
+  return 0;
+}
+
+int nml_rmsnorm_backward_typed_device(const void* grad, const void* x, const void* gamma,
+                                      void* grad_x, float* grad_gamma, size_t rows, size_t dim,
+                                      float eps, int dtype) {
+  NML_TRY(check_dtype(dtype));
+  NML_REQUIRE(dim > 0 && dim <= 8192, "rmsnorm backward: dim %zu outside (0, 8192]", dim);
+  NML_REQUIRE(rows <= 0x7fffffff, "rmsnorm backward: too many rows");
+  if (rows == 0) return 0;
+  hipStream_t st = nml::stream();
+  const size_t parts = (size_t)rmsnorm_bwd_parts((int)rows) + 1;
+  NML_TRY(g_scratch.ensure(parts * dim * sizeof(float)));
+  NML_TRY(launch_rmsnorm_bwd(dtype, grad, x, gamma, grad_x, 0, grad_gamma,
+                             static_cast<float*>(g_scratch.p), (int)rows, (int)dim, eps, st));
+  NML_HIP(hipStreamSynchronize(st));
+  return 0;
+}
+
+int nml_embedding_backward_device(const void* grad, const int64_t* ids, float* grad_weights,
+                                  size_t rows, size_t dim, size_t vocab, int dtype) {
+  NML_TRY(check_dtype(dtype));
+  NML_REQUIRE(rows <= 0x7fffffff && dim <= 0x7fffffff && vocab <= 0x7fffffff,
+              "embedding backward: shape too large");
+  if (rows == 0 || dim == 0) return 0;
+  hipStream_t st = nml::stream();
+  NML_TRY(launch_embed_backward(dtype, grad, ids, grad_weights, nullptr, 1, (int)rows, (int)dim,
+                                (int)vocab, st));
+  NML_HIP(hipStreamSynchronize(st));
+  return 0;
+}
+
 int nml_tied_ce_forward_device(const void* hidden, const void* weights, const int64_t* labels,
                                size_t rows, size_t dim, size_t vocab, int64_t ignore_index,
                                int has_ignore, double* loss, int dtype) {

@@ -993,7 +993,9 @@ __device__ __forceinline__ float score_mul(float scale) {
 
 // Shared per-tile step: thread t scores EPT (query i, key j) pairs of a BT × BT tile,
 // i = t / TPR, j = (t % TPR)·EPT + e: p = exp(q·k/scale − lse_i) where key ≤ query (both
-// inside the sequence), else 0; ds = p·(dO_i·v_j − D_i)/scale.
+// inside the sequence), else 0; ds = p·(dO_i·v_j − D_i)/scale. A full (non-causal) call
+// scores every key inside the sequence with the non-causal forward's roundings
+// (rnd(rnd(q·k) / scale), then + mask[query][key] rounded) — a masked −inf gives p = 0.
 template <int DK, int BT, typename T>
 struct AttnTile {
   static constexpr int EPT = BT * BT / 256;
@@ -1007,8 +1009,9 @@ struct AttnTile {
   float lse[BT];
   float D[BT];
 
-  __device__ void scores(int q_lo, int k_lo, int S, float scale) {
+  __device__ void scores(int q_lo, int k_lo, int S, float scale, int full, const T* mask) {
     const float mul = score_mul<T>(scale), inv_scale = 1.0f / scale;
+    const float scale_t = static_cast<float>(static_cast<T>(scale));
     const int t = threadIdx.x;
     const int i = t / TPR, j0 = (t % TPR) * EPT;
     const int qi = q_lo + i;
@@ -1016,14 +1019,21 @@ struct AttnTile {
     for (int e = 0; e < EPT; ++e) {
       const int j = j0 + e, kj = k_lo + j;
       float p = 0.f, ds = 0.f;
-      if (kj <= qi && qi < S) {
+      if (qi < S && (full ? kj < S : kj <= qi)) {
         float dot = 0.f, dp = 0.f;
 #pragma unroll 8
         for (int c = 0; c < DK; ++c) {
           dot += Qs[i][c] * Ks[j][c];
           dp += dOs[i][c] * Vs[j][c];
         }
-        p = expf(attn_score<T>(dot, mul) - lse[i]);
+        float sc;
+        if (full) {
+          sc = rnd<T>(rnd<T>(dot) / scale_t);
+          if (mask) sc = rnd<T>(sc + static_cast<float>(mask[static_cast<long long>(qi) * S + kj]));
+        } else {
+          sc = attn_score<T>(dot, mul);
+        }
+        p = sc == -INFINITY ? 0.f : expf(sc - lse[i]);
         ds = p * (dp - D[i]) * inv_scale;
       }
       Ps[i][j] = p;
@@ -1060,7 +1070,8 @@ __device__ __forceinline__ void load_merged(float (*dst)[DK + 1], const T* __res
 // head dim (columns dk ≤ c < DK hold zeros and are never written back).
 extern __shared__ __align__(16) unsigned char attn_bwd_smem[];
 
-// dK, dV of BT keys: walk the query tiles from the key tile on (causal).
+// dK, dV of BT keys: walk the query tiles from the key tile on (causal; every query tile
+// when full).
 template <int DK, int BT, typename T>
 __global__ __launch_bounds__(256) void attn_bwd_dkdv_kernel(AttnBwdArgs a) {
   AttnTile<DK, BT, T>& sh = *reinterpret_cast<AttnTile<DK, BT, T>*>(attn_bwd_smem);
@@ -1079,7 +1090,8 @@ __global__ __launch_bounds__(256) void attn_bwd_dkdv_kernel(AttnBwdArgs a) {
   float dk[NCOL], dv[NCOL];
 #pragma unroll
   for (int u = 0; u < NCOL; ++u) dk[u] = dv[u] = 0.f;
-  for (int q_lo = k_lo; q_lo < S; q_lo += BT) {
+  const T* mask = static_cast<const T*>(a.mask);
+  for (int q_lo = a.full ? 0 : k_lo; q_lo < S; q_lo += BT) {
     __syncthreads();  // the previous tile's readers are done
     load_rows<DK, BT>(sh.Qs, qg + hoff, q_lo, S, hd);
     load_merged<DK, BT>(sh.dOs, og, b, h, a.H, q_lo, S, hd);
@@ -1089,7 +1101,7 @@ __global__ __launch_bounds__(256) void attn_bwd_dkdv_kernel(AttnBwdArgs a) {
       sh.D[i] = ok ? a.dvec[static_cast<long long>(bh) * S + q_lo + i] : 0.f;
     }
     __syncthreads();
-    sh.scores(q_lo, k_lo, S, a.scale);
+    sh.scores(q_lo, k_lo, S, a.scale, a.full, mask);
     __syncthreads();
 #pragma unroll
     for (int u = 0; u < NCOL; ++u) {
@@ -1121,7 +1133,8 @@ __global__ __launch_bounds__(256) void attn_bwd_dkdv_kernel(AttnBwdArgs a) {
   }
 }
 
-// dQ of BT queries: walk the key tiles up to the query tile (causal).
+// dQ of BT queries: walk the key tiles up to the query tile (causal; every key tile when
+// full).
 template <int DK, int BT, typename T>
 __global__ __launch_bounds__(256) void attn_bwd_dq_kernel(AttnBwdArgs a) {
   AttnTile<DK, BT, T>& sh = *reinterpret_cast<AttnTile<DK, BT, T>*>(attn_bwd_smem);
@@ -1145,13 +1158,14 @@ __global__ __launch_bounds__(256) void attn_bwd_dq_kernel(AttnBwdArgs a) {
   float dq[NCOL];
 #pragma unroll
   for (int u = 0; u < NCOL; ++u) dq[u] = 0.f;
-  const int k_end = min(S, q_lo + BT);
+  const int k_end = a.full ? S : min(S, q_lo + BT);
+  const T* mask = static_cast<const T*>(a.mask);
   for (int k_lo = 0; k_lo < k_end; k_lo += BT) {
     __syncthreads();
     load_rows<DK, BT>(sh.Ks, kg + hoff, k_lo, S, hd);
     load_rows<DK, BT>(sh.Vs, vg + hoff, k_lo, S, hd);
     __syncthreads();
-    sh.scores(q_lo, k_lo, S, a.scale);
+    sh.scores(q_lo, k_lo, S, a.scale, a.full, mask);
     __syncthreads();
 #pragma unroll
     for (int u = 0; u < NCOL; ++u) {
@@ -1751,7 +1765,7 @@ int attn_bwd_mfma(const AttnBwdArgs& a, hipStream_t st) {
 template <int DK, typename T>
 int attn_bwd_dk(const AttnBwdArgs& a, hipStream_t st) {
   if constexpr (DK == 64 || DK == 128) {
-    if (!std::getenv("NIMBLEML_ATTN_BWD_VALU")) {
+    if (!a.full && !std::getenv("NIMBLEML_ATTN_BWD_VALU")) {  // MFMA kernels: causal only
       if constexpr (sizeof(T) == 2) {
         if (!std::getenv("NIMBLEML_TRAIN_F16_WIDEN")) return attn_bwd_f16<DK>(a, st);
       }
@@ -2043,6 +2057,7 @@ int attention_backward_t(const AttnBwdArgs& a, hipStream_t st) {
 
 int launch_attention_backward(int dt, const AttnBwdArgs& a, hipStream_t st) {
   if (a.B * a.S == 0) return 0;
+  NML_REQUIRE(a.full || !a.mask, "attention backward: a causal call takes no mask");
   return dt == F16 ? attention_backward_t<half_t>(a, st) : attention_backward_t<float>(a, st);
 }
 

@@ -34,16 +34,25 @@ struct TrainState {
   Buf acts;     // saved activations of the last loss_train
   Buf scratch;  // backward scratch
   Buf io;       // ids and labels of the last loss_train, loss accumulators
+  Buf mask;     // the (S, S) additive mask of a saved module forward, when it took one
   int B = 0, S = 0;
   bool saved = false;
-  unsigned long long generation = 0;  // advanced by every loss_train: which forward is saved
+  int what = 0;        // the saved forward: kSavedLoss, kSavedBlocks or kSavedMha
+  int final_norm = 0;  // kSavedBlocks: the final RMSNorm ran after the blocks
+  int full = 0;        // module forwards: non-causal attention
+  int masked = 0;      // ... with the additive mask kept in `mask`
+  int mha_layer = 0;   // kSavedMha: the layer whose attention ran
+  unsigned long long generation = 0;  // advanced by every saving forward: which one is saved
   long long ignore_index = 0;
   int has_ignore = 0;
   double n_valid = 0.0;
 };
 
+constexpr int kSavedLoss = 1, kSavedBlocks = 2, kSavedMha = 3;
+
 void train_release(nml_model* m) {
   if (!m->train) return;
+  m->train->mask.release();
   m->train->grads.release();
   m->train->moments.release();
   m->train->masters.release();
@@ -191,6 +200,191 @@ float* master_base(nml_model* m) {
   return static_cast<float*>(m->dt == F16 ? m->train->masters.p : m->arena);
 }
 
+
+// Attention of a saved forward: causal, or full (non-causal) with an optional (S, S)
+// additive mask of the model's type.
+struct MaskMode {
+  int full = 0;
+  const void* mask = nullptr;
+};
+
+// The attention half of a block over R = B·S rows of n1 (its normalised input):
+// [q | k | v] = n1·W_qkvᵀ + b into head-major q, k, v, RoPE when `rope`, attention into att
+// (merged heads) with each row's log-sum-exp in lse (_fused_arrays.py:52-104).
+int attn_forward_saving(nml_model* m, const Layer& w, int B, int S, const char* n1, char* q,
+                        char* k, char* v, char* att, float* lse, MaskMode mm, bool rope,
+                        hipStream_t st) {
+  const int R = B * S, d = m->d, dt = m->dt;
+  const long long sb = (long long)m->H * S * m->dk, sh = (long long)S * m->dk;
+  LinearArgs qkv = lin(n1, d, w.wqkv, w.bqkv, nullptr, R, 3 * d, d, EPI_QKV);
+  qkv.qkv = QKVDst{q, k, v, nullptr, sb, sh, S, m->H, m->dk, d, nullptr};
+  NML_TRY(launch_linear(dt, qkv, st));
+  if (rope)
+    NML_TRY(launch_rope(dt, q, k, sb, sh, B, m->H, S, m->dk, nullptr, nullptr, m->rope_cos,
+                        m->rope_sin, m->P, st));
+  AttnArgs a{};
+  a.q = q;
+  a.k = k;
+  a.v = v;
+  a.out = att;
+  a.kv_stride_b = sb;
+  a.kv_stride_h = sh;
+  a.B = B;
+  a.H = m->H;
+  a.S = S;
+  a.dk = m->dk;
+  a.scale = sqrtf((float)m->dk);
+  a.lse = lse;
+  a.full = mm.full;
+  a.mask = mm.mask;
+  return launch_attention_prefill(dt, a, st);
+}
+
+// Every block over R = B·S rows of sv.x (layer 0's input), keeping what the backward
+// reads; the last block's output lands in sv.xl (_fused_arrays.py:251-296).
+int blocks_forward_saving(nml_model* m, const Saved& sv, int B, int S, MaskMode mm,
+                          hipStream_t st) {
+  const int R = B * S, d = m->d, F = m->F, dt = m->dt;
+  for (int l = 0; l < m->L; ++l) {
+    const Layer& w = m->layers[l];
+    char *x = at(sv.x, sv, l), *n1 = at(sv.n1, sv, l), *q = at(sv.q, sv, l), *k = at(sv.k, sv, l),
+         *v = at(sv.v, sv, l), *att = at(sv.att, sv, l), *xm = at(sv.xm, sv, l),
+         *n2 = at(sv.n2, sv, l), *pre = at(sv.pre, sv, l), *hid = at(sv.hid, sv, l);
+    float* lse = at(sv.lse, sv, l);
+    char* xnext = l + 1 < m->L ? at(sv.x, sv, l + 1) : sv.xl;
+    NML_TRY(launch_rmsnorm(dt, x, w.ln1, n1, nullptr, nullptr, R, d, kEps, st));
+    NML_TRY(attn_forward_saving(m, w, B, S, n1, q, k, v, att, lse, mm, rope_on(m), st));
+    NML_TRY(launch_linear(dt, lin(att, d, w.wo, w.bo, xm, R, d, d, EPI_BIAS_RESID, x), st));
+    NML_TRY(launch_rmsnorm(dt, xm, w.ln2, n2, nullptr, nullptr, R, d, kEps, st));
+    if (R > 64) {  // GELU in the GEMM's epilogue, which also keeps the pre-activation
+      LinearArgs f1 = lin(n2, d, w.w1, w.b1, hid, R, F, d, EPI_BIAS_GELU);
+      f1.pre_out = pre;
+      NML_TRY(launch_linear(dt, f1, st));
+    } else {
+      NML_TRY(launch_linear(dt, lin(n2, d, w.w1, w.b1, pre, R, F, d, EPI_BIAS), st));
+      NML_TRY(launch_gelu(dt, pre, hid, nullptr, (size_t)R * F, st));
+    }
+    NML_TRY(launch_linear(dt, lin(hid, F, w.w2, w.b2, xnext, R, d, F, EPI_BIAS_RESID, xm), st));
+  }
+  return 0;
+}
+
+// Backward scratch (storage type): G, DX (R, d); DQKV (R, 3d); DPRE (R, F); then float32
+// DVEC (B, H, S) and the row- and column-sum partials.
+struct BwdScratch {
+  char *G, *DX, *DQKV, *DPRE;
+  float *DVEC, *PART;
+};
+
+int bwd_scratch(nml_model* m, int B, int S, BwdScratch* w) {
+  const int R = B * S, d = m->d, F = m->F;
+  const size_t es = m->es;
+  const size_t rd = align256((size_t)R * d * es), r3 = align256((size_t)R * 3 * d * es),
+               rf = align256((size_t)R * F * es), rv = align256((size_t)B * m->H * S * 4);
+  const int widest = F > 3 * d ? F : 3 * d;
+  const size_t pn = (size_t)(rmsnorm_bwd_parts(R) > colsum_parts(R) ? rmsnorm_bwd_parts(R)
+                                                                     : colsum_parts(R)) *
+                    widest;
+  NML_TRY(m->train->scratch.ensure(2 * rd + r3 + rf + rv + align256(pn * 4)));
+  char* sp = static_cast<char*>(m->train->scratch.p);
+  w->G = sp;
+  w->DX = sp + rd;
+  w->DQKV = sp + 2 * rd;
+  w->DPRE = sp + 2 * rd + r3;
+  w->DVEC = reinterpret_cast<float*>(sp + 2 * rd + r3 + rf);
+  w->PART = reinterpret_cast<float*>(sp + 2 * rd + r3 + rf + rv);
+  return 0;
+}
+
+// Backward of attn_forward_saving followed by its W_o projection, from ws.G = d/d(the
+// projection's output): the W_o and W_qkv gradients are added to, ws.DX = d/d(n1)
+// (_fused_arrays.py:129-184).
+int attn_backward_saved(nml_model* m, const Layer& w, int B, int S, const char* n1,
+                        const char* q, const char* k, const char* v, const char* att,
+                        const float* lse, MaskMode mm, bool rope, const BwdScratch& ws,
+                        hipStream_t st) {
+  const int R = B * S, d = m->d, dt = m->dt;
+  NML_TRY(launch_gemm_bwd(dt, gb(ws.G, d, att, d, grad_of(m, w.wo), d, d, d, R), false, false, GB_ADD, st));
+  NML_TRY(launch_colsum(dt, ws.G, d, R, d, grad_of(m, w.bo), ws.PART, st));
+  NML_TRY(launch_gemm_bwd(dt, gb(ws.G, d, w.wo, d, ws.DX, d, R, d, d), true, false, GB_SET, st));
+  AttnBwdArgs ab{};
+  ab.q = q;
+  ab.k = k;
+  ab.v = v;
+  ab.o = att;
+  ab.dout = ws.DX;
+  ab.lse = lse;
+  ab.dvec = ws.DVEC;
+  ab.dqkv = ws.DQKV;
+  ab.B = B;
+  ab.H = m->H;
+  ab.S = S;
+  ab.dk = m->dk;
+  ab.scale = sqrtf((float)m->dk);
+  ab.full = mm.full;
+  ab.mask = mm.mask;
+  NML_TRY(launch_attention_backward(dt, ab, st));
+  if (rope)
+    NML_TRY(launch_rope_backward(dt, ws.DQKV, R, S, m->H, m->dk, m->rope_cos, m->rope_sin, st));
+  NML_TRY(launch_gemm_bwd(dt, gb(ws.DQKV, 3 * d, n1, d, grad_of(m, w.wqkv), d, 3 * d, d, R), false,
+                          false, GB_ADD, st));
+  NML_TRY(launch_colsum(dt, ws.DQKV, 3 * d, R, 3 * d, grad_of(m, w.bqkv), ws.PART, st));
+  return launch_gemm_bwd(dt, gb(ws.DQKV, 3 * d, w.wqkv, d, ws.DX, d, R, d, 3 * d), true, false,
+                         GB_SET, st);
+}
+
+// Backward of blocks_forward_saving: ws.G holds d/d(sv.xl) on entry and d/d(layer 0's
+// input) on return; every block parameter's gradient is added to
+// (_fused_arrays.py:335-377, in reverse block order as :311-332 runs them).
+int blocks_backward_saved(nml_model* m, const Saved& sv, int B, int S, MaskMode mm,
+                          const BwdScratch& ws, hipStream_t st) {
+  const int R = B * S, d = m->d, F = m->F, dt = m->dt;
+  for (int l = m->L - 1; l >= 0; --l) {
+    const Layer& w = m->layers[l];
+    const char *x = at(sv.x, sv, l), *n1 = at(sv.n1, sv, l), *q = at(sv.q, sv, l),
+               *k = at(sv.k, sv, l), *v = at(sv.v, sv, l), *att = at(sv.att, sv, l),
+               *xm = at(sv.xm, sv, l), *n2 = at(sv.n2, sv, l), *pre = at(sv.pre, sv, l),
+               *hid = at(sv.hid, sv, l);
+    const float* lse = at(sv.lse, sv, l);
+    // FFN (_fused_arrays.py:225-248)
+    NML_TRY(launch_gemm_bwd(dt, gb(ws.G, d, hid, F, grad_of(m, w.w2), F, d, F, R), false, false, GB_ADD, st));
+    NML_TRY(launch_colsum(dt, ws.G, d, R, d, grad_of(m, w.b2), ws.PART, st));
+    NML_TRY(launch_gemm_bwd(dt, gb(ws.G, d, w.w2, F, ws.DPRE, F, R, F, d, pre, F), true, false, GB_GELU, st));
+    NML_TRY(launch_gemm_bwd(dt, gb(ws.DPRE, F, n2, d, grad_of(m, w.w1), d, F, d, R), false, false, GB_ADD, st));
+    NML_TRY(launch_colsum(dt, ws.DPRE, F, R, F, grad_of(m, w.b1), ws.PART, st));
+    NML_TRY(launch_gemm_bwd(dt, gb(ws.DPRE, F, w.w1, d, ws.DX, d, R, d, F), true, false, GB_SET, st));
+    NML_TRY(launch_rmsnorm_bwd(dt, ws.DX, xm, w.ln2, ws.G, 1, grad_of(m, w.ln2), ws.PART, R, d, kEps, st));
+    // MHA (_fused_arrays.py:129-184), then RMSNorm₁ into the residual gradient
+    NML_TRY(attn_backward_saved(m, w, B, S, n1, q, k, v, att, lse, mm, rope_on(m), ws, st));
+    NML_TRY(launch_rmsnorm_bwd(dt, ws.DX, x, w.ln1, ws.G, 1, grad_of(m, w.ln1), ws.PART, R, d, kEps, st));
+  }
+  return 0;
+}
+
+// A module forward's mask mode; a mask is copied into the training state, since the
+// backward reads it after the caller's buffer may be gone.
+int module_mask(nml_model* m, int S, int causal, const void* mask, hipStream_t st, MaskMode* mm) {
+  TrainState* t = m->train;
+  mm->full = causal ? 0 : 1;
+  mm->mask = nullptr;
+  t->full = mm->full;
+  t->masked = mask != nullptr;
+  if (mask && S > 0) {
+    const size_t bytes = (size_t)S * S * m->es;
+    NML_TRY(t->mask.ensure(bytes));
+    NML_HIP(hipMemcpyAsync(t->mask.p, mask, bytes, hipMemcpyDeviceToDevice, st));
+    mm->mask = t->mask.p;
+  }
+  return 0;
+}
+
+MaskMode saved_mask(const TrainState* t) {
+  MaskMode mm;
+  mm.full = t->full;
+  mm.mask = t->masked ? t->mask.p : nullptr;
+  return mm;
+}
+
 }  // namespace
 
 int train_param_uploaded(nml_model* m, const void* param, size_t elems) {
@@ -232,7 +426,7 @@ int nml_model_loss_train(nml_model* m, const int64_t* ids, const int64_t* labels
   NML_TRY(ensure_train(m));
   TrainState* t = m->train;
   t->saved = false;
-  const int B = (int)batch, S = (int)seq, R = B * S, d = m->d, F = m->F, dt = m->dt;
+  const int B = (int)batch, S = (int)seq, R = B * S, d = m->d, dt = m->dt;
   const size_t es = m->es;
   if (R == 0) {
     *loss = 0.0;
@@ -257,47 +451,7 @@ int nml_model_loss_train(nml_model* m, const int64_t* ids, const int64_t* labels
   NML_HIP(hipMemsetAsync(err, 0, sizeof(int), st));
 
   NML_TRY(launch_embed(dt, dids, m->emb, posw(m), nullptr, sv.x, B, S, d, m->V, m->P, err, st));
-  const long long sb = (long long)m->H * S * m->dk, sh = (long long)S * m->dk;
-  for (int l = 0; l < m->L; ++l) {
-    const Layer& w = m->layers[l];
-    char *x = at(sv.x, sv, l), *n1 = at(sv.n1, sv, l), *q = at(sv.q, sv, l), *k = at(sv.k, sv, l),
-         *v = at(sv.v, sv, l), *att = at(sv.att, sv, l), *xm = at(sv.xm, sv, l),
-         *n2 = at(sv.n2, sv, l), *pre = at(sv.pre, sv, l), *hid = at(sv.hid, sv, l);
-    float* lse = at(sv.lse, sv, l);
-    char* xnext = l + 1 < m->L ? at(sv.x, sv, l + 1) : sv.xl;
-    NML_TRY(launch_rmsnorm(dt, x, w.ln1, n1, nullptr, nullptr, R, d, kEps, st));
-    LinearArgs qkv = lin(n1, d, w.wqkv, w.bqkv, nullptr, R, 3 * d, d, EPI_QKV);
-    qkv.qkv = QKVDst{q, k, v, nullptr, sb, sh, S, m->H, m->dk, d, nullptr};
-    NML_TRY(launch_linear(dt, qkv, st));
-    if (rope_on(m))
-      NML_TRY(launch_rope(dt, q, k, sb, sh, B, m->H, S, m->dk, nullptr, nullptr, m->rope_cos,
-                          m->rope_sin, m->P, st));
-    AttnArgs a{};
-    a.q = q;
-    a.k = k;
-    a.v = v;
-    a.out = att;
-    a.kv_stride_b = sb;
-    a.kv_stride_h = sh;
-    a.B = B;
-    a.H = m->H;
-    a.S = S;
-    a.dk = m->dk;
-    a.scale = sqrtf((float)m->dk);
-    a.lse = lse;
-    NML_TRY(launch_attention_prefill(dt, a, st));
-    NML_TRY(launch_linear(dt, lin(att, d, w.wo, w.bo, xm, R, d, d, EPI_BIAS_RESID, x), st));
-    NML_TRY(launch_rmsnorm(dt, xm, w.ln2, n2, nullptr, nullptr, R, d, kEps, st));
-    if (R > 64) {  // GELU in the GEMM's epilogue, which also keeps the pre-activation
-      LinearArgs f1 = lin(n2, d, w.w1, w.b1, hid, R, F, d, EPI_BIAS_GELU);
-      f1.pre_out = pre;
-      NML_TRY(launch_linear(dt, f1, st));
-    } else {
-      NML_TRY(launch_linear(dt, lin(n2, d, w.w1, w.b1, pre, R, F, d, EPI_BIAS), st));
-      NML_TRY(launch_gelu(dt, pre, hid, nullptr, (size_t)R * F, st));
-    }
-    NML_TRY(launch_linear(dt, lin(hid, F, w.w2, w.b2, xnext, R, d, F, EPI_BIAS_RESID, xm), st));
-  }
+  NML_TRY(blocks_forward_saving(m, sv, B, S, MaskMode{}, st));
   NML_TRY(launch_rmsnorm(dt, sv.xl, m->lnf, sv.hf, nullptr, nullptr, R, d, kEps, st));
 
   const size_t chunk = logits_chunk(m, R);
@@ -324,6 +478,7 @@ int nml_model_loss_train(nml_model* m, const int64_t* ids, const int64_t* labels
   t->ignore_index = ignore_index;
   t->has_ignore = has_ignore;
   t->n_valid = host[1];
+  t->what = kSavedLoss;
   t->saved = true;
   t->generation += 1;
   return 0;
@@ -331,10 +486,10 @@ int nml_model_loss_train(nml_model* m, const int64_t* ids, const int64_t* labels
 
 int nml_model_backward(nml_model* m, double grad_scale) {
   NML_TRY(check_ready(m));
-  NML_REQUIRE(m->train && m->train->saved,
-              "backward: no saved forward (call nml_model_loss_train first)");
+  NML_REQUIRE(m->train && m->train->saved && m->train->what == kSavedLoss,
+              "backward: no saved loss forward (call nml_model_loss_train first)");
   TrainState* t = m->train;
-  const int B = t->B, S = t->S, R = B * S, d = m->d, F = m->F, V = m->V, dt = m->dt;
+  const int B = t->B, S = t->S, R = B * S, d = m->d, V = m->V, dt = m->dt;
   const size_t es = m->es;
   if (t->n_valid <= 0.0) return 0;  // every label ignored: the loss is a constant 0
   hipStream_t st = nml::stream();
@@ -344,22 +499,11 @@ int nml_model_backward(nml_model* m, double grad_scale) {
   const int64_t* dids = reinterpret_cast<const int64_t*>(t->io.p);
   const int64_t* dlab = reinterpret_cast<const int64_t*>(static_cast<char*>(t->io.p) + ib);
 
-  // scratch (storage type): G, DX (R, d); DQKV (R, 3d); DPRE (R, F); then float32 dvec
-  // (B, H, S) and row-sum partials
-  const size_t rd = align256((size_t)R * d * es), r3 = align256((size_t)R * 3 * d * es),
-               rf = align256((size_t)R * F * es), rv = align256((size_t)B * m->H * S * 4);
-  const int widest = F > 3 * d ? F : 3 * d;
-  const size_t pn = (size_t)(rmsnorm_bwd_parts(R) > colsum_parts(R) ? rmsnorm_bwd_parts(R)
-                                                                     : colsum_parts(R)) *
-                    widest;
-  NML_TRY(t->scratch.ensure(2 * rd + r3 + rf + rv + align256(pn * 4)));
-  char* sp = static_cast<char*>(t->scratch.p);
-  char* G = sp;
-  char* DX = sp + rd;
-  char* DQKV = sp + 2 * rd;
-  char* DPRE = sp + 2 * rd + r3;
-  float* DVEC = reinterpret_cast<float*>(sp + 2 * rd + r3 + rf);
-  float* PART = reinterpret_cast<float*>(sp + 2 * rd + r3 + rf + rv);
+  BwdScratch ws;
+  NML_TRY(bwd_scratch(m, B, S, &ws));
+  char* G = ws.G;
+  char* DX = ws.DX;
+  float* PART = ws.PART;
   const void* E = m->emb;
   float* dE = grad_of(m, m->emb);
 
@@ -378,50 +522,126 @@ int nml_model_backward(nml_model* m, double grad_scale) {
   }
   NML_TRY(launch_rmsnorm_bwd(dt, DX, sv.xl, m->lnf, G, 0, grad_of(m, m->lnf), PART, R, d, kEps, st));
 
-  for (int l = m->L - 1; l >= 0; --l) {
-    const Layer& w = m->layers[l];
-    const char *x = at(sv.x, sv, l), *n1 = at(sv.n1, sv, l), *q = at(sv.q, sv, l),
-               *k = at(sv.k, sv, l), *v = at(sv.v, sv, l), *att = at(sv.att, sv, l),
-               *xm = at(sv.xm, sv, l), *n2 = at(sv.n2, sv, l), *pre = at(sv.pre, sv, l),
-               *hid = at(sv.hid, sv, l);
-    const float* lse = at(sv.lse, sv, l);
-    // FFN (_fused_arrays.py:225-248)
-    NML_TRY(launch_gemm_bwd(dt, gb(G, d, hid, F, grad_of(m, w.w2), F, d, F, R), false, false, GB_ADD, st));
-    NML_TRY(launch_colsum(dt, G, d, R, d, grad_of(m, w.b2), PART, st));
-    NML_TRY(launch_gemm_bwd(dt, gb(G, d, w.w2, F, DPRE, F, R, F, d, pre, F), true, false, GB_GELU, st));
-    NML_TRY(launch_gemm_bwd(dt, gb(DPRE, F, n2, d, grad_of(m, w.w1), d, F, d, R), false, false, GB_ADD, st));
-    NML_TRY(launch_colsum(dt, DPRE, F, R, F, grad_of(m, w.b1), PART, st));
-    NML_TRY(launch_gemm_bwd(dt, gb(DPRE, F, w.w1, d, DX, d, R, d, F), true, false, GB_SET, st));
-    NML_TRY(launch_rmsnorm_bwd(dt, DX, xm, w.ln2, G, 1, grad_of(m, w.ln2), PART, R, d, kEps, st));
-    // MHA (_fused_arrays.py:129-184)
-    NML_TRY(launch_gemm_bwd(dt, gb(G, d, att, d, grad_of(m, w.wo), d, d, d, R), false, false, GB_ADD, st));
-    NML_TRY(launch_colsum(dt, G, d, R, d, grad_of(m, w.bo), PART, st));
-    NML_TRY(launch_gemm_bwd(dt, gb(G, d, w.wo, d, DX, d, R, d, d), true, false, GB_SET, st));
-    AttnBwdArgs ab{};
-    ab.q = q;
-    ab.k = k;
-    ab.v = v;
-    ab.o = att;
-    ab.dout = DX;
-    ab.lse = lse;
-    ab.dvec = DVEC;
-    ab.dqkv = DQKV;
-    ab.B = B;
-    ab.H = m->H;
-    ab.S = S;
-    ab.dk = m->dk;
-    ab.scale = sqrtf((float)m->dk);
-    NML_TRY(launch_attention_backward(dt, ab, st));
-    if (rope_on(m))
-      NML_TRY(launch_rope_backward(dt, DQKV, R, S, m->H, m->dk, m->rope_cos, m->rope_sin, st));
-    NML_TRY(launch_gemm_bwd(dt, gb(DQKV, 3 * d, n1, d, grad_of(m, w.wqkv), d, 3 * d, d, R), false,
-                            false, GB_ADD, st));
-    NML_TRY(launch_colsum(dt, DQKV, 3 * d, R, 3 * d, grad_of(m, w.bqkv), PART, st));
-    NML_TRY(launch_gemm_bwd(dt, gb(DQKV, 3 * d, w.wqkv, d, DX, d, R, d, 3 * d), true, false, GB_SET, st));
-    NML_TRY(launch_rmsnorm_bwd(dt, DX, x, w.ln1, G, 1, grad_of(m, w.ln1), PART, R, d, kEps, st));
-  }
+  NML_TRY(blocks_backward_saved(m, sv, B, S, MaskMode{}, ws, st));
   NML_TRY(launch_embed_backward(dt, G, dids, dE, rope_on(m) ? nullptr : grad_of(m, m->pos), B, S, d,
                                 V, st));
+  NML_HIP(hipStreamSynchronize(st));
+  return 0;
+}
+
+// ------------------------------------------------------------ module-level autograd
+// A saving forward of a module: shape checks, the activation buffer carved, the mask kept.
+static int module_forward_begin(nml_model* m, size_t batch, size_t seq, int causal,
+                                const void* mask, const char* what, Saved* sv, MaskMode* mm) {
+  NML_REQUIRE(m != nullptr, "model is null");
+  NML_REQUIRE(seq <= (size_t)m->P, "Sequence length %zu exceeds maximum sequence length %d", seq,
+              m->P);
+  NML_REQUIRE(!causal || mask == nullptr, "%s: a causal call takes no mask", what);
+  NML_TRY(ensure_train(m));
+  TrainState* t = m->train;
+  t->saved = false;
+  const int B = (int)batch, S = (int)seq;
+  NML_TRY(t->acts.ensure(saved_bytes(m, B, S, nullptr, nullptr)));
+  saved_bytes(m, B, S, sv, static_cast<char*>(t->acts.p));
+  NML_TRY(module_mask(m, S, causal, mask, nml::stream(), mm));
+  t->B = B;
+  t->S = S;
+  return 0;
+}
+
+static void module_forward_end(nml_model* m, int what) {
+  m->train->what = what;
+  m->train->saved = true;
+  m->train->generation += 1;
+}
+
+static int module_backward_begin(nml_model* m, int what, const char* name, Saved* sv,
+                                 BwdScratch* ws) {
+  NML_REQUIRE(m != nullptr, "model is null");
+  NML_REQUIRE(m->train && m->train->saved && m->train->what == what,
+              "%s: no saved forward of this kind (run its saving forward first)", name);
+  TrainState* t = m->train;
+  saved_bytes(m, t->B, t->S, sv, static_cast<char*>(t->acts.p));
+  if (t->B * t->S == 0) return 0;
+  return bwd_scratch(m, t->B, t->S, ws);
+}
+
+int nml_model_blocks_forward_train(nml_model* m, const void* x, void* out, size_t batch,
+                                   size_t seq, int final_norm, int causal, const void* mask) {
+  Saved sv;
+  MaskMode mm;
+  NML_TRY(module_forward_begin(m, batch, seq, causal, mask, "blocks_forward_train", &sv, &mm));
+  const int B = (int)batch, S = (int)seq, R = B * S;
+  m->train->final_norm = final_norm != 0;
+  if (R > 0) {
+    hipStream_t st = nml::stream();
+    const size_t bytes = (size_t)R * m->d * m->es;
+    NML_HIP(hipMemcpyAsync(sv.x, x, bytes, hipMemcpyDeviceToDevice, st));
+    NML_TRY(blocks_forward_saving(m, sv, B, S, mm, st));
+    if (final_norm)
+      NML_TRY(launch_rmsnorm(m->dt, sv.xl, m->lnf, sv.hf, nullptr, nullptr, R, m->d, kEps, st));
+    NML_HIP(hipMemcpyAsync(out, final_norm ? sv.hf : sv.xl, bytes, hipMemcpyDeviceToDevice, st));
+  }
+  module_forward_end(m, kSavedBlocks);
+  return 0;
+}
+
+int nml_model_blocks_backward(nml_model* m, const void* dout, void* dx) {
+  Saved sv;
+  BwdScratch ws;
+  NML_TRY(module_backward_begin(m, kSavedBlocks, "blocks_backward", &sv, &ws));
+  TrainState* t = m->train;
+  const int B = t->B, S = t->S, R = B * S, d = m->d;
+  if (R == 0) return 0;
+  hipStream_t st = nml::stream();
+  const size_t bytes = (size_t)R * d * m->es;
+  if (t->final_norm)  // fused_trunk_backward_arrays (_fused_arrays.py:311-332): final norm first
+    NML_TRY(launch_rmsnorm_bwd(m->dt, dout, sv.xl, m->lnf, ws.G, 0, grad_of(m, m->lnf), ws.PART,
+                               R, d, kEps, st));
+  else
+    NML_HIP(hipMemcpyAsync(ws.G, dout, bytes, hipMemcpyDeviceToDevice, st));
+  NML_TRY(blocks_backward_saved(m, sv, B, S, saved_mask(t), ws, st));
+  if (dx) NML_HIP(hipMemcpyAsync(dx, ws.G, bytes, hipMemcpyDeviceToDevice, st));
+  NML_HIP(hipStreamSynchronize(st));
+  return 0;
+}
+
+int nml_model_mha_forward_train(nml_model* m, int layer, const void* x, void* out, size_t batch,
+                                size_t seq, int causal, const void* mask) {
+  NML_REQUIRE(m != nullptr, "model is null");
+  NML_REQUIRE(layer >= 0 && layer < m->L, "layer %d outside [0, %d)", layer, m->L);
+  Saved sv;
+  MaskMode mm;
+  NML_TRY(module_forward_begin(m, batch, seq, causal, mask, "mha_forward_train", &sv, &mm));
+  const int B = (int)batch, S = (int)seq, R = B * S, d = m->d;
+  m->train->mha_layer = layer;
+  if (R > 0) {
+    // the layer-0 slots of the saved buffer: n1 holds the input, then q, k, v, att, lse
+    hipStream_t st = nml::stream();
+    const Layer& w = m->layers[layer];
+    NML_HIP(hipMemcpyAsync(sv.n1, x, (size_t)R * d * m->es, hipMemcpyDeviceToDevice, st));
+    // neural_network/attention.py:139-168 applies no rotary embedding
+    NML_TRY(attn_forward_saving(m, w, B, S, sv.n1, sv.q, sv.k, sv.v, sv.att, sv.lse, mm, false,
+                                st));
+    NML_TRY(launch_linear(m->dt, lin(sv.att, d, w.wo, w.bo, out, R, d, d, EPI_BIAS), st));
+  }
+  module_forward_end(m, kSavedMha);
+  return 0;
+}
+
+int nml_model_mha_backward(nml_model* m, const void* dout, void* dx) {
+  Saved sv;
+  BwdScratch ws;
+  NML_TRY(module_backward_begin(m, kSavedMha, "mha_backward", &sv, &ws));
+  TrainState* t = m->train;
+  const int B = t->B, S = t->S, R = B * S;
+  if (R == 0) return 0;
+  hipStream_t st = nml::stream();
+  const size_t bytes = (size_t)R * m->d * m->es;
+  NML_HIP(hipMemcpyAsync(ws.G, dout, bytes, hipMemcpyDeviceToDevice, st));
+  NML_TRY(attn_backward_saved(m, m->layers[t->mha_layer], B, S, sv.n1, sv.q, sv.k, sv.v, sv.att,
+                              sv.lse, saved_mask(t), false, ws, st));
+  if (dx) NML_HIP(hipMemcpyAsync(dx, ws.DX, bytes, hipMemcpyDeviceToDevice, st));
   NML_HIP(hipStreamSynchronize(st));
   return 0;
 }

@@ -27,9 +27,26 @@ code that edits ``param.data`` in place by other means calls
 ``module.mark_parameters_changed()``. A second call with unchanged parameters uploads
 nothing. Masks follow
 the reference: an additive (seq, seq) array or Tensor; ``None`` is causal for the
-fused block and trunk and no mask for MultiHeadAttention. Gradients of these
-module-level outputs are not computed on the device (``GPT.compute_loss`` is the
-training path); calling ``backward`` through one raises.
+fused block and trunk and no mask for MultiHeadAttention.
+
+Autograd: with gradients wanted (``is_grad_enabled()`` and the input or a parameter
+requiring them), each output carries the closure its reference module attaches, run on
+the device by ``Tensor.backward`` in reverse topological order:
+  Dense                 layers/dense.py:81-94          nml_linear_backward_device
+  Embedding / _prefix   layers/embedding.py:63-69, :111-117  nml_embedding_backward_device
+  RMSNorm               layers/rms_norm.py:76-94       nml_rmsnorm_backward_typed_device
+  FeedForward           neural_network/feed_forward.py:105-129  two linear backwards, the
+                        GELU derivative fused into the second
+  MultiHeadAttention    neural_network/attention.py:103-119 (its SDPA) with the projections
+                        nml_model_mha_forward_train / nml_model_mha_backward
+  FusedTransformerBlock transformer_fused.py:65-78     nml_model_blocks_forward_train /
+  FusedGPTTrunk         transformer_fused.py:128-136   nml_model_blocks_backward
+Parameter gradients are added to each parameter's ``grad`` (Tensor._accumulate_grad) in the
+reference layouts; the input's gradient goes to the input Tensor. The device models keep
+one saved forward each: a backward whose forward was replaced by a later saving forward
+of the same module recomputes it from the kept input first (the reference's
+``gradient_checkpointing`` recompute, transformer_fused.py:69-73), so any number of
+outstanding graphs give the same gradients.
 """
 from __future__ import annotations
 
@@ -153,20 +170,102 @@ def _host(t, shape, dt):
     return np.ascontiguousarray(np.asarray(t.data, dtype=dt).reshape(shape))
 
 
-def _output(arr, shape, x, params, op):
-    """The module's result Tensor. With gradients wanted, its backward raises: module-level
-    gradients are not computed on the device."""
-    needs = is_grad_enabled() and (getattr(x, "requires_grad", False)
-                                   or any(p.requires_grad for p in params))
-    out = Tensor(arr, shape, requires_grad=needs, _op=op)
-    if needs:
-        def _backward():
-            raise NotImplementedError(
-                f"{op}: gradients of module-level forwards are not computed on the device; "
-                "train through GPT.compute_loss")
+def _needs_grad(x, params):
+    return is_grad_enabled() and (getattr(x, "requires_grad", False)
+                                  or any(p.requires_grad for p in params))
 
-        out._backward = _backward
+
+def _output(arr, shape, x, params, op, backward=None):
+    """The module's result Tensor. With gradients wanted, ``backward(out)`` becomes its
+    autograd closure and the input Tensor ``x`` its child (the edge Tensor.backward
+    walks)."""
+    needs = _needs_grad(x, params)
+    kids = (x,) if needs and isinstance(x, Tensor) else ()
+    out = Tensor(arr, shape, requires_grad=needs, _children=kids, _op=op)
+    if needs and backward is not None:
+        out._backward = lambda: backward(out)
     return out
+
+
+# ------------------------------------------------------------------ backward helpers
+def _dy(out, dt):
+    """``out.grad`` on the device in the compute dtype and out's shape (None when unset)."""
+    if out.grad is None:
+        return None
+    g = np.asarray(out.grad).reshape(out.shape)
+    return N.DeviceArray.from_host(np.ascontiguousarray(g, dtype=dt))
+
+
+def _f32_zeros(shape, wanted):
+    """A zeroed float32 device gradient buffer, or None when not wanted."""
+    return N.DeviceArray.from_host(np.zeros(shape, np.float32)) if wanted else None
+
+
+def _wants(t):
+    return isinstance(t, Tensor) and t.requires_grad
+
+
+def _to_input(x, dx):
+    """Hand the input gradient (a DeviceArray) to the input Tensor."""
+    if dx is not None and _wants(x):
+        x._accumulate_grad(dx.numpy().reshape(-1))
+
+
+def _model_grad(model, kind, layer, shape):
+    """The float32 gradient of a device model's parameter (kind, layer) on the host."""
+    p = C.c_void_p()
+    N.check(N.lib.nml_model_grad_ptr(model.handle, kind, layer, C.byref(p)))
+    out = np.empty(shape, np.float32)
+    N.check(N.lib.nml_memcpy_d2h(out.ctypes.data, p.value, out.nbytes))
+    return out
+
+
+def _saved_generation(model):
+    g = C.c_ulonglong()
+    N.check(N.lib.nml_model_saved_generation(model.handle, C.byref(g)))
+    return int(g.value)
+
+
+def _saved_forward(model, state, rerun):
+    """Make the device model's saved activations those of this output's forward:
+    ``state[0]`` is the generation it saved; a later saving forward replaced it, so run
+    ``rerun`` (the same forward on the kept input) again."""
+    if model.handle is None:
+        raise RuntimeError("the module's parameters changed since this output was computed; "
+                           "run the forward again before backward()")
+    if _saved_generation(model) != state[0]:
+        rerun()
+        state[0] = _saved_generation(model)
+
+
+def _add_dense_grads(dense, w_t_grad, b_grad):
+    """Device-layout (out, in) weight gradient and bias gradient into a Dense's ``grad``."""
+    if w_t_grad is not None:
+        dense.weights._accumulate_grad(np.ascontiguousarray(w_t_grad.T))
+    if b_grad is not None and dense.biases is not None:
+        dense.biases._accumulate_grad(b_grad)
+
+
+def _mha_grads(model, mha, layer):
+    d = mha.d_model
+    wqkv = _model_grad(model, N.P_WQKV, layer, (3 * d, d))
+    bqkv = _model_grad(model, N.P_BQKV, layer, (3 * d,))
+    for j, dense in enumerate((mha.W_q, mha.W_k, mha.W_v)):
+        _add_dense_grads(dense, wqkv[j * d:(j + 1) * d], bqkv[j * d:(j + 1) * d])
+    _add_dense_grads(mha.W_o, _model_grad(model, N.P_WO, layer, (d, d)),
+                     _model_grad(model, N.P_BO, layer, (d,)))
+
+
+def _block_grads(model, blk, layer):
+    d = blk.d_model
+    f1, f2 = blk.ffn.dense1, blk.ffn.dense2
+    blk.ln1.gamma._accumulate_grad(_model_grad(model, N.P_LN1, layer, (d,)))
+    _mha_grads(model, blk.mha, layer)
+    blk.ln2.gamma._accumulate_grad(_model_grad(model, N.P_LN2, layer, (d,)))
+    _add_dense_grads(f1, _model_grad(model, N.P_W1, layer, (f1.out_features, d)),
+                     _model_grad(model, N.P_B1, layer, (f1.out_features,)))
+    _add_dense_grads(f2, _model_grad(model, N.P_W2, layer, (d, f2.in_features)),
+                     _model_grad(model, N.P_B2, layer, (d,)))
 
 
 def _mask_mode(mask, seq, dt, *, none_is_causal):
@@ -299,10 +398,34 @@ def _blocks_forward(owner, blocks, ln, x, mask, op, params):
     model = _resident(owner, "blocks", _params_key(params, dt, p, rope_key), build)
     xd = _device_input(x, dt)
     out = N.DeviceArray((b, s, d), dt)
-    N.check(N.lib.nml_model_blocks_forward(model.handle, xd.ptr, out.ptr, b, s,
-                                           int(ln is not None), causal, N.ptr(mdev)))
+    args = (b, s, int(ln is not None), causal, N.ptr(mdev))
+    if not _needs_grad(x, params):
+        N.check(N.lib.nml_model_blocks_forward(model.handle, xd.ptr, out.ptr, *args))
+        N.check(N.lib.nml_synchronize())
+        return _output(out, (b, s, d), x, params, op)
+    N.check(N.lib.nml_model_blocks_forward_train(model.handle, xd.ptr, out.ptr, *args))
     N.check(N.lib.nml_synchronize())
-    return _output(out, (b, s, d), x, params, op)
+    state = [_saved_generation(model)]
+
+    def rerun():
+        tmp = N.DeviceArray((b, s, d), dt)
+        N.check(N.lib.nml_model_blocks_forward_train(model.handle, xd.ptr, tmp.ptr, *args))
+
+    def backward(o):
+        dy = _dy(o, dt)
+        if dy is None:
+            return
+        _saved_forward(model, state, rerun)
+        N.check(N.lib.nml_model_zero_grad(model.handle))
+        dx = N.DeviceArray((b, s, d), dt) if _wants(x) else None
+        N.check(N.lib.nml_model_blocks_backward(model.handle, dy.ptr, N.ptr(dx)))
+        for i, blk in enumerate(blocks):
+            _block_grads(model, blk, i)
+        if ln is not None:
+            ln.gamma._accumulate_grad(_model_grad(model, N.P_LN_F, 0, (d,)))
+        _to_input(x, dx)
+
+    return _output(out, (b, s, d), x, params, op, backward)
 
 
 class Sequential(Module):
@@ -351,7 +474,23 @@ class Dense(Module):
         x = _device_input(inputs, dt)
         w_t, b = self._device_weights(dt)
         out = K.linear_t(x, w_t, b)
-        return _output(out.reshape(shape), shape, inputs, self.parameters(), "dense")
+        rows = prod(shape[:-1])
+
+        def backward(o):  # layers/dense.py:81-94
+            dy = _dy(o, dt)
+            if dy is None:
+                return
+            dx = N.DeviceArray((rows, self.in_features), dt) if _wants(inputs) else None
+            dw = _f32_zeros((self.out_features, self.in_features), self.weights.requires_grad)
+            db = _f32_zeros((self.out_features,), _wants(self.biases))
+            N.check(N.lib.nml_linear_backward_device(
+                dy.ptr, x.ptr, w_t.ptr, N.ptr(dx), N.ptr(dw), N.ptr(db), rows, self.in_features,
+                self.out_features, None, N.np_dtype_code(dt)))
+            _add_dense_grads(self, None if dw is None else dw.numpy(),
+                             None if db is None else db.numpy())
+            _to_input(inputs, dx)
+
+        return _output(out.reshape(shape), shape, inputs, self.parameters(), "dense", backward)
 
     def _device_weights(self, dt):
         """(W transposed to (out, in), bias or None) on the device, kept while unchanged."""
@@ -390,7 +529,19 @@ class Embedding(Module):
         if ids.size == 0:
             return _output(N.DeviceArray(shape, dt), shape, None, self.parameters(), "embedding")
         out = K.embedding_lookup(w, ids)
-        return _output(out.reshape(shape), shape, None, self.parameters(), "embedding")
+
+        def backward(o):  # layers/embedding.py:63-69: scatter-add into the rows used
+            dy = _dy(o, dt)
+            if dy is None or not self.weights.requires_grad:
+                return
+            gw = _f32_zeros((self.vocab_size, self.embed_dim), True)
+            idd = N.DeviceArray.from_host(ids.reshape(-1))
+            N.check(N.lib.nml_embedding_backward_device(dy.ptr, idd.ptr, gw.ptr, ids.size,
+                                                        self.embed_dim, self.vocab_size,
+                                                        N.np_dtype_code(dt)))
+            self.weights._accumulate_grad(gw.numpy())
+
+        return _output(out.reshape(shape), shape, None, self.parameters(), "embedding", backward)
 
     def forward_prefix(self, seq_len: int):
         """layers/embedding.py:72-118: rows ``[0, seq_len)`` of the table, (seq_len, dim)."""
@@ -402,7 +553,15 @@ class Embedding(Module):
         rows = N.DeviceArray(shape, dt)
         if rows.nbytes:
             N.check(N.lib.nml_memcpy_d2d(rows.ptr, table.ptr, rows.nbytes))
-        return _output(rows, shape, None, self.parameters(), "embedding_prefix")
+
+        def backward(o):  # layers/embedding.py:111-117: rows [0, seq_len) take the gradient
+            if o.grad is None or not self.weights.requires_grad:
+                return
+            g = np.zeros((self.vocab_size, self.embed_dim), np.float32)
+            g[:seq_len] = np.asarray(o.grad, dtype=np.float32).reshape(shape)
+            self.weights._accumulate_grad(g)
+
+        return _output(rows, shape, None, self.parameters(), "embedding_prefix", backward)
 
     def _device_table(self, dt):
         return _resident(self, "table", _params_key(self.parameters(), dt),
@@ -432,8 +591,21 @@ class RMSNorm(Module):
         g = _resident(self, "gamma", _params_key(self.parameters(), dt),
                       lambda: N.DeviceArray.from_host(_host(self.gamma, (d,), dt)))
         out = K.fused_rmsnorm_forward(x, g, self.epsilon)[0]
+
+        def backward(o):  # layers/rms_norm.py:76-94
+            dy = _dy(o, dt)
+            if dy is None:
+                return
+            dx = N.DeviceArray((rows, d), dt)
+            dg = _f32_zeros((d,), True)
+            N.check(N.lib.nml_rmsnorm_backward_typed_device(dy.ptr, x.ptr, g.ptr, dx.ptr, dg.ptr,
+                                                            rows, d, float(self.epsilon),
+                                                            N.np_dtype_code(dt)))
+            self.gamma._accumulate_grad(dg.numpy())
+            _to_input(inputs, dx)
+
         return _output(out.reshape(inputs.shape), inputs.shape, inputs, self.parameters(),
-                       "rms_norm")
+                       "rms_norm", backward)
 
     def parameters(self):
         return [self.gamma]
@@ -474,10 +646,34 @@ class MultiHeadAttention(Module):
                                              mha_device_arrays(self, 0, dt)))
         xd = _device_input(x, dt)
         out = N.DeviceArray((b, s, d), dt)
-        N.check(N.lib.nml_model_mha_forward(model.handle, 0, xd.ptr, out.ptr, b, s, causal,
-                                            N.ptr(mdev)))
+        params = self.parameters()
+        if not _needs_grad(x, params):
+            N.check(N.lib.nml_model_mha_forward(model.handle, 0, xd.ptr, out.ptr, b, s, causal,
+                                                N.ptr(mdev)))
+            N.check(N.lib.nml_synchronize())
+            return _output(out, (b, s, d), x, params, "multi_head_attention")
+        N.check(N.lib.nml_model_mha_forward_train(model.handle, 0, xd.ptr, out.ptr, b, s, causal,
+                                                  N.ptr(mdev)))
         N.check(N.lib.nml_synchronize())
-        return _output(out, (b, s, d), x, self.parameters(), "multi_head_attention")
+        state = [_saved_generation(model)]
+
+        def rerun():
+            tmp = N.DeviceArray((b, s, d), dt)
+            N.check(N.lib.nml_model_mha_forward_train(model.handle, 0, xd.ptr, tmp.ptr, b, s,
+                                                      causal, N.ptr(mdev)))
+
+        def backward(o):  # the projections' closures around attention.py:103-119
+            dy = _dy(o, dt)
+            if dy is None:
+                return
+            _saved_forward(model, state, rerun)
+            N.check(N.lib.nml_model_zero_grad(model.handle))
+            dx = N.DeviceArray((b, s, d), dt) if _wants(x) else None
+            N.check(N.lib.nml_model_mha_backward(model.handle, dy.ptr, N.ptr(dx)))
+            _mha_grads(model, self, 0)
+            _to_input(x, dx)
+
+        return _output(out, (b, s, d), x, params, "multi_head_attention", backward)
 
     def parameters(self):
         params = []
@@ -514,9 +710,44 @@ class FeedForward(Module):
             n = max(w1.out_features, w2.out_features)
             zero = _resident(self, "zero_bias", (np.dtype(dt).str, n),
                              lambda: N.DeviceArray.from_host(np.zeros(n, dtype=dt)))
-        h = K.linear_t(xd, w1_t, b1 if b1 is not None else zero, epilogue=K.EPI_BIAS_GELU)
-        out = K.linear_t(h, w2_t, b2 if b2 is not None else zero, epilogue=K.EPI_BIAS)
-        return _output(out.reshape(x.shape), x.shape, x, self.parameters(), "feed_forward")
+        b1d = b1 if b1 is not None else zero
+        b2d = b2 if b2 is not None else zero
+        params = self.parameters()
+        if not _needs_grad(x, params):
+            h = K.linear_t(xd, w1_t, b1d, epilogue=K.EPI_BIAS_GELU)
+            out = K.linear_t(h, w2_t, b2d, epilogue=K.EPI_BIAS)
+            return _output(out.reshape(x.shape), x.shape, x, params, "feed_forward")
+        # the backward reads the pre-activation: the GELU runs as its own kernel
+        pre = K.linear_t(xd, w1_t, b1d, epilogue=K.EPI_BIAS)
+        h = K.fused_gelu_forward(pre)[0]
+        out = K.linear_t(h, w2_t, b2d, epilogue=K.EPI_BIAS)
+        rows, hid = pre.shape
+        d = w1.in_features
+
+        def backward(o):  # neural_network/feed_forward.py:105-129
+            dy = _dy(o, dt)
+            if dy is None:
+                return
+            code = N.np_dtype_code(dt)
+            dpre = N.DeviceArray((rows, hid), dt)
+            dw2 = _f32_zeros((d, hid), w2.weights.requires_grad)
+            db2 = _f32_zeros((d,), _wants(w2.biases))
+            N.check(N.lib.nml_linear_backward_device(dy.ptr, h.ptr, w2_t.ptr, dpre.ptr,
+                                                     N.ptr(dw2), N.ptr(db2), rows, hid, d,
+                                                     pre.ptr, code))
+            dx = N.DeviceArray((rows, d), dt) if _wants(x) else None
+            dw1 = _f32_zeros((hid, d), w1.weights.requires_grad)
+            db1 = _f32_zeros((hid,), _wants(w1.biases))
+            N.check(N.lib.nml_linear_backward_device(dpre.ptr, xd.ptr, w1_t.ptr, N.ptr(dx),
+                                                     N.ptr(dw1), N.ptr(db1), rows, d, hid, None,
+                                                     code))
+            _add_dense_grads(w2, None if dw2 is None else dw2.numpy(),
+                             None if db2 is None else db2.numpy())
+            _add_dense_grads(w1, None if dw1 is None else dw1.numpy(),
+                             None if db1 is None else db1.numpy())
+            _to_input(x, dx)
+
+        return _output(out.reshape(x.shape), x.shape, x, params, "feed_forward", backward)
 
     def parameters(self):
         return self.dense1.parameters() + self.dense2.parameters()

@@ -6,10 +6,13 @@ A flat buffer plus a shape. Float data is coerced to the compute dtype
 ``DeviceArray`` for results left on the GPU (logits); ``np.asarray(t.data)``
 works for both.
 
-Autograd covers the one graph this path builds: the loss of ``GPT.compute_loss``
-on a float32 model, whose ``backward()`` runs the whole backward on the device and
-accumulates each parameter's ``grad`` (tensor.py:271-352 for ``zero_grad``,
-``backward`` and ``_accumulate_grad``).
+Autograd (tensor.py:271-352 for ``zero_grad``, ``backward`` and ``_accumulate_grad``):
+each result that needs gradients holds a ``_backward`` closure and its input Tensors in
+``_prev``; ``backward`` seeds this tensor's ``grad`` and runs the closures of the graph
+below it in reverse topological order (tensor.py:286-332 with the post-order walk of
+tensor.py:88-121). The closures are the GPT loss's (``GPT.compute_loss``) and the
+modules' (``nimbleml_amd.layers``); each runs its backward on the device and adds the
+gradients to its parameters' and inputs' ``grad``.
 """
 from __future__ import annotations
 
@@ -102,19 +105,49 @@ class Tensor:
             self.grad = self.grad + grad
 
     def backward(self, grad=None, retain_graph=False):
-        """tensor.py:286-332 for a scalar loss: seed ``grad`` (default 1) and run the
-        recorded backward once (the graph is released unless ``retain_graph``)."""
+        """tensor.py:286-332: add ``grad`` (default 1 for a scalar) to this tensor's ``grad``,
+        then run every ``_backward`` closure of the graph below it, each after all the
+        closures of the tensors computed from it. Unless ``retain_graph``, the closures and
+        edges are released afterwards."""
         if grad is None:
             if self.size != 1:
                 raise ValueError("grad must be specified for non-scalar tensors.")
             grad = np.array([1.0], dtype=np_backend.dtype)
-        self.grad = np.asarray(grad, dtype=np_backend.dtype).reshape(-1)
-        fn = self._backward
-        if fn is None:
-            return
+        elif isinstance(grad, (int, float)):
+            grad = np.array([float(grad)], dtype=np_backend.dtype)
+        elif isinstance(grad, Tensor):
+            grad = np.asarray(grad.data)
+        else:
+            grad = np.asarray(grad, dtype=np_backend.dtype)
+        self._accumulate_grad(grad)
+        topo = _backward_order(self)
+        for node in reversed(topo):
+            fn = node._backward
+            if fn is not None:
+                fn()
         if not retain_graph:
-            self._backward = None
-        fn()
+            for node in topo:
+                node._backward = None
+                node._prev = set()
 
     def __repr__(self):
         return f"Tensor(shape={self.shape}, data={self.data})"
+
+
+def _backward_order(root):
+    """The tensors reachable from ``root`` through ``_prev``, each after all of its inputs
+    (an iterative post-order walk, tensor.py:88-121)."""
+    order, visited, stack = [], set(), [(root, False)]
+    while stack:
+        node, expanded = stack.pop()
+        if expanded:
+            order.append(node)
+            continue
+        if id(node) in visited:
+            continue
+        visited.add(id(node))
+        stack.append((node, True))
+        for child in node._prev:
+            if id(child) not in visited:
+                stack.append((child, False))
+    return order

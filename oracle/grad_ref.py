@@ -72,6 +72,111 @@ def _layer_names(i):
     return p, p + "mha.", p + "ffn."
 
 
+def _mha_fwd(x2d, w, pm, b, s, num_heads, mask, rope):
+    """mha_forward_arrays (_fused_arrays.py:52-126) on (b·s, d) rows: ``(out, saved)``.
+    ``mask``: an additive (s, s) array, or None for none."""
+    n, d = x2d.shape
+    dk = d // num_heads
+    scale = float(dk) ** 0.5
+    w_qkv = np.concatenate([w[pm + "W_q.weights"], w[pm + "W_k.weights"],
+                            w[pm + "W_v.weights"]], axis=1)
+    b_qkv = np.concatenate([w[pm + "W_q.biases"], w[pm + "W_k.biases"],
+                            w[pm + "W_v.biases"]])
+    qkv = x2d @ w_qkv + b_qkv
+    q = _split_heads(qkv[:, :d], b, s, num_heads, dk)
+    k = _split_heads(qkv[:, d:2 * d], b, s, num_heads, dk)
+    v = _split_heads(qkv[:, 2 * d:], b, s, num_heads, dk)
+    if rope is not None:
+        q = apply_rope(q, rope[0], rope[1])
+        k = apply_rope(k, rope[0], rope[1])
+    sc = np.matmul(q, np.swapaxes(k, -2, -1)) / scale
+    if mask is not None:
+        sc = sc + mask
+    sc = sc - np.max(sc, axis=-1, keepdims=True)
+    e = np.exp(sc)
+    probs = e / np.sum(e, axis=-1, keepdims=True)
+    att = np.matmul(probs, v)
+    merged = _merge_heads(att, b, s, num_heads, dk).reshape(n, d)
+    out = merged @ w[pm + "W_o.weights"] + w[pm + "W_o.biases"]
+    return out, (x2d, w_qkv, q, k, v, probs, merged)
+
+
+def _mha_bwd(g, saved, w, pm, b, s, num_heads, grads, rope):
+    """mha_backward_arrays (_fused_arrays.py:129-184): adds the projection gradients to
+    ``grads`` and returns d/d(input rows). SDPA: kernels/fused_sdpa.py:26-29, :81-88 (the
+    scores gradient divided by ``scale = sqrt(dk)``); RoPE inverse rotation at :151-154."""
+    x2d, w_qkv, q, k, v, probs, merged = saved
+    n, d = x2d.shape
+    dk = d // num_heads
+    scale = float(dk) ** 0.5
+    grads[pm + "W_o.weights"] += merged.T @ g
+    grads[pm + "W_o.biases"] += g.sum(axis=0)
+    dmerged = g @ w[pm + "W_o.weights"].T
+    datt = _split_heads(dmerged, b, s, num_heads, dk)
+    dprobs = np.matmul(datt, np.swapaxes(v, -2, -1))
+    dsc = probs * (dprobs - np.sum(dprobs * probs, axis=-1, keepdims=True))
+    dsc = dsc / scale
+    dq = np.matmul(dsc, k)
+    dk_ = np.matmul(np.swapaxes(dsc, -2, -1), q)
+    dv = np.matmul(np.swapaxes(probs, -2, -1), datt)
+    if rope is not None:
+        dq = _rope_inv(dq, rope[0], rope[1])
+        dk_ = _rope_inv(dk_, rope[0], rope[1])
+    dqkv = np.concatenate([_merge_heads(t, b, s, num_heads, dk).reshape(n, d)
+                           for t in (dq, dk_, dv)], axis=1)
+    dw_qkv = x2d.T @ dqkv
+    db_qkv = dqkv.sum(axis=0)
+    for j, nm in enumerate(("W_q", "W_k", "W_v")):
+        grads[pm + nm + ".weights"] += dw_qkv[:, j * d:(j + 1) * d]
+        grads[pm + nm + ".biases"] += db_qkv[j * d:(j + 1) * d]
+    return dqkv @ w_qkv.T
+
+
+def _ffn_fwd(x2d, w, pf):
+    """ffn_forward_arrays (_fused_arrays.py:187-222)."""
+    pre = x2d @ w[pf + "dense1.weights"] + w[pf + "dense1.biases"]
+    hid, tu = _gelu_fwd(pre)
+    return hid @ w[pf + "dense2.weights"] + w[pf + "dense2.biases"], (x2d, pre, hid, tu)
+
+
+def _ffn_bwd(g, saved, w, pf, grads):
+    """ffn_backward_arrays (_fused_arrays.py:225-248); GELU: kernels/fused_gelu.py:86-111
+    (native/src/gelu.cpp:23-33)."""
+    x2d, pre, hid, tu = saved
+    grads[pf + "dense2.weights"] += hid.T @ g
+    grads[pf + "dense2.biases"] += g.sum(axis=0)
+    dpre = _gelu_bwd(g @ w[pf + "dense2.weights"].T, pre, tu)
+    grads[pf + "dense1.weights"] += x2d.T @ dpre
+    grads[pf + "dense1.biases"] += dpre.sum(axis=0)
+    return dpre @ w[pf + "dense1.weights"].T
+
+
+def _block_fwd(x, w, i, b, s, num_heads, mask, rope):
+    """fused_block_forward_arrays (_fused_arrays.py:251-284) on (b·s, d) rows."""
+    p, pm, pf = _layer_names(i)
+    n1, ms1, rms1 = _rms_fwd(x, w[p + "ln1.gamma"])
+    a_out, msave = _mha_fwd(n1, w, pm, b, s, num_heads, mask, rope)
+    x_mid = x + a_out
+    n2, ms2, rms2 = _rms_fwd(x_mid, w[p + "ln2.gamma"])
+    f_out, fsave = _ffn_fwd(n2, w, pf)
+    return x_mid + f_out, (x, ms1, rms1, msave, x_mid, ms2, rms2, fsave)
+
+
+def _block_bwd(g, saved, w, i, b, s, num_heads, grads, rope):
+    """fused_block_backward_arrays (_fused_arrays.py:335-377):
+    ``grad_mid = g + RMSNorm₂ᵀ(FFNᵀ(g))``, ``grad_x0 = grad_mid + RMSNorm₁ᵀ(MHAᵀ(grad_mid))``."""
+    p, pm, pf = _layer_names(i)
+    x0, ms1, rms1, msave, x_mid, ms2, rms2, fsave = saved
+    dn2 = _ffn_bwd(g, fsave, w, pf, grads)
+    gx, dg2 = _rms_bwd(dn2, x_mid, w[p + "ln2.gamma"], ms2, rms2)
+    grads[p + "ln2.gamma"] += dg2
+    g = g + gx
+    dn1 = _mha_bwd(g, msave, w, pm, b, s, num_heads, grads, rope)
+    gx, dg1 = _rms_bwd(dn1, x0, w[p + "ln1.gamma"], ms1, rms1)
+    grads[p + "ln1.gamma"] += dg1
+    return g + gx
+
+
 def loss_and_grads(w, ids, labels, num_heads, num_layers, ignore_index=None, rope=None,
                    grad_scale=1.0):
     """``(loss, {name: grad})`` of ``compute_loss(ids, labels)`` and one ``backward()``.
@@ -84,9 +189,6 @@ def loss_and_grads(w, ids, labels, num_heads, num_layers, ignore_index=None, rop
     b, s = ids.shape
     emb = w["token_emb.weights"]
     d = emb.shape[1]
-    h_ = num_heads
-    dk = d // h_
-    scale = float(dk) ** 0.5
     n = b * s
     if rope is not None:
         rope = (rope[0].astype(dt), rope[1].astype(dt))
@@ -98,33 +200,8 @@ def loss_and_grads(w, ids, labels, num_heads, num_layers, ignore_index=None, rop
     mask = np.triu(np.full((s, s), -np.inf, dtype=dt), k=1)
     saves = []
     for i in range(num_layers):
-        p, pm, pf = _layer_names(i)
-        n1, ms1, rms1 = _rms_fwd(x, w[p + "ln1.gamma"])
-        w_qkv = np.concatenate([w[pm + "W_q.weights"], w[pm + "W_k.weights"],
-                                w[pm + "W_v.weights"]], axis=1)
-        b_qkv = np.concatenate([w[pm + "W_q.biases"], w[pm + "W_k.biases"],
-                                w[pm + "W_v.biases"]])
-        qkv = n1 @ w_qkv + b_qkv
-        q = _split_heads(qkv[:, :d], b, s, h_, dk)
-        k = _split_heads(qkv[:, d:2 * d], b, s, h_, dk)
-        v = _split_heads(qkv[:, 2 * d:], b, s, h_, dk)
-        if rope is not None:
-            q = apply_rope(q, rope[0], rope[1])
-            k = apply_rope(k, rope[0], rope[1])
-        sc = np.matmul(q, np.swapaxes(k, -2, -1)) / scale + mask
-        sc = sc - np.max(sc, axis=-1, keepdims=True)
-        e = np.exp(sc)
-        probs = e / np.sum(e, axis=-1, keepdims=True)
-        att = np.matmul(probs, v)
-        merged = _merge_heads(att, b, s, h_, dk).reshape(n, d)
-        x_mid = x + merged @ w[pm + "W_o.weights"] + w[pm + "W_o.biases"]
-        n2, ms2, rms2 = _rms_fwd(x_mid, w[p + "ln2.gamma"])
-        pre = n2 @ w[pf + "dense1.weights"] + w[pf + "dense1.biases"]
-        hid, tu = _gelu_fwd(pre)
-        x_out = x_mid + hid @ w[pf + "dense2.weights"] + w[pf + "dense2.biases"]
-        saves.append((x, n1, ms1, rms1, w_qkv, q, k, v, probs, merged, x_mid, n2, ms2, rms2,
-                      pre, hid, tu))
-        x = x_out
+        x, sv = _block_fwd(x, w, i, b, s, num_heads, mask, rope)
+        saves.append(sv)
     hf, msf, rmsf = _rms_fwd(x, w["ln.gamma"])
 
     labels = np.asarray(labels, dtype=np.int64).reshape(-1)
@@ -154,48 +231,77 @@ def loss_and_grads(w, ids, labels, num_heads, num_layers, ignore_index=None, rop
     g, dgf = _rms_bwd(dh, x, w["ln.gamma"], msf, rmsf)
     grads["ln.gamma"] += dgf
     for i in reversed(range(num_layers)):
-        p, pm, pf = _layer_names(i)
-        (x0, n1, ms1, rms1, w_qkv, q, k, v, probs, merged, x_mid, n2, ms2, rms2, pre, hid,
-         tu) = saves[i]
-        # FFN (_fused_arrays.py:225-248)
-        grads[pf + "dense2.weights"] += hid.T @ g
-        grads[pf + "dense2.biases"] += g.sum(axis=0)
-        dpre = _gelu_bwd(g @ w[pf + "dense2.weights"].T, pre, tu)
-        grads[pf + "dense1.weights"] += n2.T @ dpre
-        grads[pf + "dense1.biases"] += dpre.sum(axis=0)
-        dn2 = dpre @ w[pf + "dense1.weights"].T
-        gx, dg2 = _rms_bwd(dn2, x_mid, w[p + "ln2.gamma"], ms2, rms2)
-        grads[p + "ln2.gamma"] += dg2
-        g = g + gx
-        # MHA (_fused_arrays.py:129-184)
-        grads[pm + "W_o.weights"] += merged.T @ g
-        grads[pm + "W_o.biases"] += g.sum(axis=0)
-        dmerged = g @ w[pm + "W_o.weights"].T
-        datt = _split_heads(dmerged, b, s, h_, dk)
-        dprobs = np.matmul(datt, np.swapaxes(v, -2, -1))
-        dsc = probs * (dprobs - np.sum(dprobs * probs, axis=-1, keepdims=True))
-        dsc = dsc / scale
-        dq = np.matmul(dsc, k)
-        dk_ = np.matmul(np.swapaxes(dsc, -2, -1), q)
-        dv = np.matmul(np.swapaxes(probs, -2, -1), datt)
-        if rope is not None:
-            dq = _rope_inv(dq, rope[0], rope[1])
-            dk_ = _rope_inv(dk_, rope[0], rope[1])
-        dqkv = np.concatenate([_merge_heads(t, b, s, h_, dk).reshape(n, d) for t in (dq, dk_, dv)],
-                              axis=1)
-        dw_qkv = n1.T @ dqkv
-        db_qkv = dqkv.sum(axis=0)
-        for j, nm in enumerate(("W_q", "W_k", "W_v")):
-            grads[pm + nm + ".weights"] += dw_qkv[:, j * d:(j + 1) * d]
-            grads[pm + nm + ".biases"] += db_qkv[j * d:(j + 1) * d]
-        dn1 = dqkv @ w_qkv.T
-        gx, dg1 = _rms_bwd(dn1, x0, w[p + "ln1.gamma"], ms1, rms1)
-        grads[p + "ln1.gamma"] += dg1
-        g = g + gx
+        g = _block_bwd(g, saves[i], w, i, b, s, num_heads, grads, rope)
     np.add.at(grads["token_emb.weights"], ids.reshape(-1), g)
     if rope is None:
         grads["pos_emb.weights"][:s] += g.reshape(b, s, d).sum(axis=0)
     return loss, grads
+
+
+# ------------------------------------------------------ module-level vector-Jacobian products
+# Each returns the module's output, d(<dout, out>)/d(input) and {name: gradient} for the
+# parameters it reads (reference names and (in, out) layouts): the closures the reference's
+# modules attach (utils/tensor.py:286-332 runs them).
+
+def blocks_vjp(w, layers, x, dout, num_heads, mask=None, rope=None, final_gamma=None):
+    """FusedTransformerBlock (``layers = [i]``, transformer_fused.py:65-78) or
+    FusedGPTTrunk (every layer then the final RMSNorm of ``final_gamma``,
+    transformer_fused.py:128-136 → _fused_arrays.py:311-332) over x (b, s, d). ``mask``:
+    additive (s, s) or None for none (the modules' own None is the causal mask). The
+    final norm's gradient comes back under ``"final.gamma"``."""
+    b, s, d = x.shape
+    cur = x.reshape(b * s, d)
+    saves = []
+    for i in layers:
+        cur, sv = _block_fwd(cur, w, i, b, s, num_heads, mask, rope)
+        saves.append(sv)
+    grads = {name: np.zeros_like(a) for name, a in w.items()}
+    g = dout.reshape(b * s, d)
+    out = cur
+    if final_gamma is not None:
+        out, msf, rmsf = _rms_fwd(cur, final_gamma)
+        g, dgf = _rms_bwd(g, cur, final_gamma, msf, rmsf)
+        grads["final.gamma"] = dgf
+    for i, sv in reversed(list(zip(layers, saves))):
+        g = _block_bwd(g, sv, w, i, b, s, num_heads, grads, rope)
+    return out.reshape(b, s, d), g.reshape(b, s, d), grads
+
+
+def mha_vjp(w, prefix, x, dout, num_heads, mask=None):
+    """MultiHeadAttention.forward (attention.py:139-168; its SDPA closure :103-119) with the
+    parameters under ``prefix`` (e.g. ``"blocks.layers.0.mha."``)."""
+    b, s, d = x.shape
+    out, saved = _mha_fwd(x.reshape(b * s, d), w, prefix, b, s, num_heads, mask, None)
+    grads = {name: np.zeros_like(a) for name, a in w.items()}
+    dx = _mha_bwd(dout.reshape(b * s, d), saved, w, prefix, b, s, num_heads, grads, None)
+    return out.reshape(b, s, d), dx.reshape(b, s, d), grads
+
+
+def ffn_vjp(w, prefix, x, dout):
+    """FeedForward.forward and its closure (neural_network/feed_forward.py:105-129)."""
+    d = x.shape[-1]
+    out, saved = _ffn_fwd(x.reshape(-1, d), w, prefix)
+    grads = {name: np.zeros_like(a) for name, a in w.items()}
+    dx = _ffn_bwd(dout.reshape(-1, d), saved, w, prefix, grads)
+    return out.reshape(x.shape), dx.reshape(x.shape), grads
+
+
+def dense_vjp(weights, biases, x, dout):
+    """Dense.forward's closure (layers/dense.py:81-94): ``(out, dx, dW, db)``."""
+    x2 = x.reshape(-1, weights.shape[0])
+    g2 = dout.reshape(-1, weights.shape[1])
+    out = x2 @ weights + (biases if biases is not None else 0)
+    return (out.reshape(*x.shape[:-1], weights.shape[1]), (g2 @ weights.T).reshape(x.shape),
+            x2.T @ g2, g2.sum(axis=0))
+
+
+def embedding_vjp(vocab, ids, dout):
+    """Embedding.forward's closure (layers/embedding.py:63-69 → embedding_scatter.py:39-60):
+    the (vocab, dim) gradient with each id's rows of dout added in."""
+    dim = dout.shape[-1]
+    g = np.zeros((vocab, dim), dout.dtype)
+    np.add.at(g, np.asarray(ids, np.int64).reshape(-1), dout.reshape(-1, dim))
+    return g
 
 
 # ------------------------------------------------ single ops of the native extension

@@ -249,20 +249,6 @@ def test_sdpa_without_and_with_general_mask(dtype_ctx):
             assert err <= bound(dt, ref, 1e-6, 2)
 
 
-def test_module_outputs_refuse_backward(gpu):
-    import nimbleml_amd as nm
-
-    w = weights(np.float32)
-    blk = gpt_with(w, np.float32)._block_list[0]
-    x = nm.Tensor(xin(np.float32), (2, 40, CFG.d_model), requires_grad=True)
-    out = blk(x)
-    assert out.requires_grad
-    with pytest.raises(NotImplementedError):
-        out.backward(np.ones(out.size, np.float32))
-    with nm.no_grad():
-        assert not blk(x).requires_grad
-
-
 @pytest.mark.parametrize("dtype_ctx", DTYPES, indirect=True)
 def test_module_forwards_keep_parameters_resident(dtype_ctx):
     """Each module keeps a device copy of its parameters: a second call with unchanged

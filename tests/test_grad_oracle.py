@@ -161,3 +161,144 @@ def test_planted_slips_fail_the_check(monkeypatch, slip):
         monkeypatch.setattr(G, "_rope_inv", lambda x, c, s: R.apply_rope(x, c, s))
     with pytest.raises(AssertionError):
         _fd_check(w, ids, labels, rope=rope, per_kind=4, grad_fn=G.loss_and_grads)
+
+
+# ------------------------------------------------------- module-level vector-Jacobian products
+# Each VJP oracle is pinned by central differences of the forward oracle (oracle/gpt_ref.py:
+# R.block / R.mha / R.ffn / R.rmsnorm): d<dout, f(θ)>/dθ at random coordinates of the input
+# and of every parameter the module reads.
+
+def _module_case(seed, b=2, s=6):
+    rng = np.random.default_rng(seed)
+    x = rng.standard_normal((b, s, CFG.d_model))
+    dout = rng.standard_normal((b, s, CFG.d_model))
+    return x, dout
+
+
+def _mixed_mask(s, seed):
+    m = np.where(np.random.default_rng(seed).random((s, s)) < 0.3, -np.inf, 0.0)
+    np.fill_diagonal(m, 0.0)  # every query keeps one key
+    return m + np.random.default_rng(seed + 1).standard_normal((s, s)) * 0.5 * (m == 0)
+
+
+def _fd_vjp(f, w, x, dout, dx, grads, names, per_kind=3, seed=0):
+    """Central differences of <dout, f(w, x)> against dx and grads[name]."""
+    rng = np.random.default_rng(seed)
+
+    def obj():
+        return float(np.sum(dout * f(w, x)))
+
+    worst = 0.0
+    for name in ["x"] + list(names):
+        a = x if name == "x" else w[name]
+        got_all = dx if name == "x" else grads[name]
+        for _ in range(per_kind):
+            idx = tuple(int(rng.integers(0, n)) for n in a.shape)
+            h = 1e-5
+            old = a[idx]
+            a[idx] = old + h
+            lp = obj()
+            a[idx] = old - h
+            lm = obj()
+            a[idx] = old
+            fd = (lp - lm) / (2 * h)
+            # the objective is O(100): differences carry ~1e-9 of rounding noise
+            err = abs(got_all[idx] - fd) / max(1e-2, abs(fd))
+            worst = max(worst, err)
+            assert err < 1e-5, (name, idx, got_all[idx], fd)
+    return worst
+
+
+def _block_names(i):
+    return [n for n in KINDS if n.startswith(f"blocks.layers.{i}.")]
+
+
+@pytest.mark.parametrize("mask_kind", ["causal", "none", "mixed"])
+def test_fd_block_vjp(mask_kind):
+    w = _weights()
+    x, dout = _module_case(20)
+    s = x.shape[1]
+    mask = {"causal": R.causal_mask(s, np.float64), "none": None,
+            "mixed": _mixed_mask(s, 3)}[mask_kind]
+    out, dx, grads = G.blocks_vjp(w, [1], x, dout, CFG.num_heads, mask)
+    assert np.allclose(out, R.block(x, w, 1, CFG.num_heads, mask), rtol=1e-12, atol=1e-12)
+    _fd_vjp(lambda w_, x_: R.block(x_, w_, 1, CFG.num_heads, mask), w, x, dout, dx, grads,
+            _block_names(1))
+    assert not any(np.any(grads[n]) for n in _block_names(0))  # other layers untouched
+
+
+def test_fd_block_vjp_rope():
+    w = _weights(rope=True)
+    x, dout = _module_case(21, s=7)
+    cos, sin = R.rope_cache(CFG.max_seq_len, CFG.head_dim)
+    rc = (cos.astype(np.float64), sin.astype(np.float64))
+    mask = R.causal_mask(7, np.float64)
+    out, dx, grads = G.blocks_vjp(w, [0], x, dout, CFG.num_heads, mask, rope=rc)
+    _fd_vjp(lambda w_, x_: R.block(x_, w_, 0, CFG.num_heads, mask, rc), w, x, dout, dx, grads,
+            _block_names(0))
+
+
+def test_fd_trunk_vjp():
+    w = _weights()
+    x, dout = _module_case(22)
+    mask = R.causal_mask(6, np.float64)
+    w["final.gamma"] = 1.0 + 0.3 * np.random.default_rng(9).standard_normal(CFG.d_model)
+
+    def trunk(w_, x_):
+        h = x_
+        for i in range(CFG.num_layers):
+            h = R.block(h, w_, i, CFG.num_heads, mask)
+        return R.rmsnorm(h, w_["final.gamma"])
+
+    out, dx, grads = G.blocks_vjp(w, list(range(CFG.num_layers)), x, dout, CFG.num_heads, mask,
+                                  final_gamma=w["final.gamma"])
+    assert np.allclose(out, trunk(w, x), rtol=1e-12, atol=1e-12)
+    _fd_vjp(trunk, w, x, dout, dx, grads,
+            _block_names(0) + _block_names(1) + ["final.gamma"])
+
+
+@pytest.mark.parametrize("mask_kind", ["none", "mixed"])
+def test_fd_mha_vjp(mask_kind):
+    w = _weights()
+    x, dout = _module_case(23, s=5)
+    mask = None if mask_kind == "none" else _mixed_mask(5, 4)
+    pm = "blocks.layers.0.mha."
+    out, dx, grads = G.mha_vjp(w, pm, x, dout, CFG.num_heads, mask)
+    assert np.allclose(out, R.mha(x, w, pm, CFG.num_heads, mask), rtol=1e-12, atol=1e-12)
+    _fd_vjp(lambda w_, x_: R.mha(x_, w_, pm, CFG.num_heads, mask), w, x, dout, dx, grads,
+            [n for n in _block_names(0) if ".mha." in n])
+
+
+def test_fd_ffn_dense_embedding_vjp():
+    w = _weights()
+    x, dout = _module_case(24, s=3)
+    pf = "blocks.layers.1.ffn."
+    out, dx, grads = G.ffn_vjp(w, pf, x, dout)
+    assert np.allclose(out, R.ffn(x, w, pf), rtol=1e-12, atol=1e-12)
+    _fd_vjp(lambda w_, x_: R.ffn(x_, w_, pf), w, x, dout, dx, grads,
+            [n for n in _block_names(1) if ".ffn." in n])
+    # Dense: a linear map, so its VJP is fixed by the transposes; checked against
+    # differences all the same
+    W, bvec = w[pf + "dense1.weights"], w[pf + "dense1.biases"]
+    dy = np.random.default_rng(25).standard_normal((2, 3, W.shape[1]))
+    out, dx, dW, db = G.dense_vjp(W, bvec, x, dy)
+    _fd_vjp(lambda w_, x_: x_ @ w_["W"] + w_["b"], {"W": W, "b": bvec}, x, dy, dx,
+            {"W": dW, "b": db}, ["W", "b"])
+    # Embedding: each id's rows of dout summed; a repeated id gets both
+    ids = np.array([[3, 7, 3], [0, 3, 47]])
+    g = G.embedding_vjp(CFG.vocab_size, ids, dout)
+    assert np.allclose(g[3], dout[0, 0] + dout[0, 2] + dout[1, 1])
+    assert np.allclose(g[47], dout[1, 2]) and not np.any(g[[1, 2, 4]])
+
+
+def test_planted_mask_slip_fails_the_module_check():
+    """A backward that forgets the additive mask (the gradient of the unmasked attention)
+    must fail the differences of the masked forward."""
+    w = _weights()
+    x, dout = _module_case(26, s=5)
+    mask = _mixed_mask(5, 8)
+    pm = "blocks.layers.0.mha."
+    _, dx, grads = G.mha_vjp(w, pm, x, dout, CFG.num_heads, None)
+    with pytest.raises(AssertionError):
+        _fd_vjp(lambda w_, x_: R.mha(x_, w_, pm, CFG.num_heads, mask), w, x, dout, dx, grads,
+                [n for n in _block_names(0) if ".mha." in n])
