@@ -341,3 +341,49 @@ def test_no_grad_and_frozen_parameters(gpu):
     _, dx, _ = G.blocks_vjp(_w64(w), [0], x.astype(np.float64), np.ones(x.shape),
                             CFG.num_heads, R.causal_mask(9, np.float64))
     _check(xt.grad, dx, np.float32, "x")
+
+
+@pytest.mark.parametrize("dt", [np.float32, np.float16])
+@pytest.mark.parametrize("dims", [(128, 192, 2, 1, 64), (128, 512, 2, 1, 64)],
+                         ids=lambda d: f"dk{d[1] // d[2]}")
+def test_padded_head_dims_with_masks(gpu, dims, dt):
+    """Head dims 96 and 256 (the scalar backward on tiles padded to 128 / 256 columns):
+    MultiHeadAttention with an arbitrary mask (non-causal) and the block with its causal
+    default, every gradient against the oracle."""
+    import nimbleml_amd as nm
+
+    cfg = GPTConfig(*dims)
+    old = nm.np_backend.dtype
+    nm.set_dtype(np.dtype(dt).name)
+    try:
+        w = make_weights(cfg, seed=27, dtype=np.float32, rich=True)
+        w = {k: v.astype(dt) for k, v in w.items()}
+        m = nm.GPT.from_arrays(w, cfg.vocab_size, cfg.d_model, cfg.num_heads, cfg.num_layers,
+                               cfg.max_seq_len, dtype=dt)
+        blk = m._block_list[0]
+        s = 21
+        x = _x((2, s, cfg.d_model), 28, dt)
+        dout = _x((2, s, cfg.d_model), 29, dt)
+        mask = _mixed_mask(s, dt, 7)
+        xt = nm.Tensor(x, x.shape, requires_grad=True)
+        out = blk.mha(xt, nm.Tensor(mask, mask.shape))
+        out.backward(dout)
+        pm = "blocks.layers.0.mha."
+        _, want_dx, want = G.mha_vjp(_w64(w), pm, x.astype(np.float64), dout.astype(np.float64),
+                                     cfg.num_heads, mask.astype(np.float64))
+        _check(xt.grad, want_dx, dt, "mha x")
+        for n in ("W_q", "W_v", "W_o"):
+            _check(getattr(blk.mha, n).weights.grad, want[pm + n + ".weights"], dt, n)
+        _zero(blk.parameters())
+        xt = nm.Tensor(x, x.shape, requires_grad=True)
+        out = blk(xt)
+        out.backward(dout)
+        _, want_dx, want = G.blocks_vjp(_w64(w), [0], x.astype(np.float64),
+                                        dout.astype(np.float64), cfg.num_heads,
+                                        R.causal_mask(s, np.float64))
+        _check(xt.grad, want_dx, dt, "block x")
+        for name, t in _block_params(blk, 0).items():
+            if not name.endswith("W_k.biases"):
+                _check(t.grad, want[name], dt, name)
+    finally:
+        nm.set_dtype(np.dtype(old).name)
