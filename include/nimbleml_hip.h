@@ -317,6 +317,15 @@ int nml_model_loss_train(nml_model* m, const int64_t* ids, const int64_t* labels
  * output.grad). Returns after the device finishes. */
 int nml_model_backward(nml_model* m, double grad_scale);
 
+/* The backward of GPT.forward (models/gpt.py:92-121; its closures are the blocks' and the
+ * tied head's, gpt.py:139-181, run by utils/tensor.py:286-332): recomputes the forward at
+ * ids (device int64, batch × seq) keeping its activations, then ADDS d(loss)/d(parameter)
+ * for dlogits = d(loss)/d(logits) (device, the compute dtype, batch × seq × vocab) to every
+ * gradient. Replaces any saved forward (advances nml_model_saved_generation). Returns after
+ * the device finishes. */
+int nml_model_logits_backward(nml_model* m, const int64_t* ids, size_t batch, size_t seq,
+                              const void* dlogits);
+
 /* Which forward the saved activations belong to: a counter that every
  * nml_model_loss_train advances (0: nothing saved). A caller holding the loss of an
  * earlier nml_model_loss_train compares it before nml_model_backward, since backward

@@ -86,6 +86,7 @@ _SIGS = {
     "nml_model_grad_ptr": [vp, i32, i32, C.POINTER(C.c_void_p)],
     "nml_model_loss_train": [vp, vp, vp, sz, sz, i64, i32, C.POINTER(C.c_double)],
     "nml_model_backward": [vp, C.c_double],
+    "nml_model_logits_backward": [vp, vp, sz, sz, vp],
     "nml_model_saved_generation": [vp, C.POINTER(C.c_ulonglong)],
     "nml_model_adamw_step": [vp, f32, f32, f32, f32, f32, f32, f32],
     "nml_model_adam_moments": [vp, i32, i32, C.POINTER(C.c_void_p), C.POINTER(C.c_void_p)],

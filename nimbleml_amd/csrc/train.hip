@@ -529,6 +529,50 @@ int nml_model_backward(nml_model* m, double grad_scale) {
   return 0;
 }
 
+int nml_model_logits_backward(nml_model* m, const int64_t* ids, size_t batch, size_t seq,
+                              const void* dlogits) {
+  NML_TRY(check_ready(m));
+  NML_REQUIRE(seq <= (size_t)m->P, "Sequence length %zu exceeds maximum sequence length %d", seq,
+              m->P);
+  NML_TRY(ensure_train(m));
+  TrainState* t = m->train;
+  // the recompute below overwrites the saved activations of any earlier saving forward
+  t->saved = false;
+  t->generation += 1;
+  const int B = (int)batch, S = (int)seq, R = B * S, d = m->d, V = m->V, dt = m->dt;
+  if (R == 0) return 0;
+  hipStream_t st = nml::stream();
+  Saved sv;
+  NML_TRY(t->acts.ensure(saved_bytes(m, B, S, nullptr, nullptr)));
+  saved_bytes(m, B, S, &sv, static_cast<char*>(t->acts.p));
+  const size_t ib = align256((size_t)R * 8);
+  NML_TRY(t->io.ensure(ib + 256));
+  int64_t* dids = reinterpret_cast<int64_t*>(t->io.p);
+  int* err = reinterpret_cast<int*>(static_cast<char*>(t->io.p) + ib);
+  NML_HIP(hipMemcpyAsync(dids, ids, (size_t)R * 8, hipMemcpyDeviceToDevice, st));
+  NML_HIP(hipMemsetAsync(err, 0, sizeof(int), st));
+  // the forward of GPT.forward, keeping what the backward reads
+  NML_TRY(launch_embed(dt, dids, m->emb, posw(m), nullptr, sv.x, B, S, d, V, m->P, err, st));
+  NML_TRY(blocks_forward_saving(m, sv, B, S, MaskMode{}, st));
+  NML_TRY(launch_rmsnorm(dt, sv.xl, m->lnf, sv.hf, nullptr, nullptr, R, d, kEps, st));
+  BwdScratch ws;
+  NML_TRY(bwd_scratch(m, B, S, &ws));
+  // tied head (gpt.py:150-153): dH = dlogits·E, dE += dlogitsᵀ·H
+  float* dE = grad_of(m, m->emb);
+  NML_TRY(launch_gemm_bwd(dt, gb(dlogits, V, m->emb, d, ws.DX, d, R, d, V), true, false, GB_SET, st));
+  NML_TRY(launch_gemm_bwd(dt, gb(dlogits, V, sv.hf, d, dE, d, V, d, R), false, false, GB_ADD, st));
+  NML_TRY(launch_rmsnorm_bwd(dt, ws.DX, sv.xl, m->lnf, ws.G, 0, grad_of(m, m->lnf), ws.PART, R, d,
+                             kEps, st));
+  NML_TRY(blocks_backward_saved(m, sv, B, S, MaskMode{}, ws, st));
+  NML_TRY(launch_embed_backward(dt, ws.G, dids, dE, rope_on(m) ? nullptr : grad_of(m, m->pos), B,
+                                S, d, V, st));
+  int herr = 0;
+  NML_HIP(hipMemcpyAsync(&herr, err, sizeof(int), hipMemcpyDeviceToHost, st));
+  NML_HIP(hipStreamSynchronize(st));
+  NML_REQUIRE((herr & 1) == 0, "Token ID out of range [0, %d)", V);
+  return 0;
+}
+
 // ------------------------------------------------------------ module-level autograd
 // A saving forward of a module: shape checks, the activation buffer carved, the mask kept.
 static int module_forward_begin(nml_model* m, size_t batch, size_t seq, int causal,

@@ -336,7 +336,13 @@ class GPT(Module):
 
     # ---------------------------------------------------------------- forward
     def forward(self, input_ids):
-        """All-position logits (batch, seq, vocab) on the device (models/gpt.py:92-121)."""
+        """All-position logits (batch, seq, vocab) on the device (models/gpt.py:92-121).
+
+        With gradients wanted (grad mode on and a parameter requiring them) the logits carry
+        the backward of the whole forward: ``logits.backward(dlogits)`` recomputes the
+        forward keeping its activations (the recompute of gradient checkpointing,
+        transformer_fused.py:69-73) and adds every parameter's gradient
+        (``nml_model_logits_backward``)."""
         ids = _ids_array(input_ids)
         self._check_ids(ids)
         h = self._device_model()
@@ -344,7 +350,27 @@ class GPT(Module):
         out = self._logits_array((b, s, self.vocab_size))
         dids = N.DeviceArray.from_host(ids)
         N.check(N.lib.nml_model_forward(h, dids.ptr, b, s, out.ptr, 0))
-        return Tensor(out, (b, s, self.vocab_size))
+        params = self.parameters()
+        needs = is_grad_enabled() and any(p.requires_grad for p in params)
+        logits = Tensor(out, (b, s, self.vocab_size), requires_grad=needs)
+        if needs:
+            dev = self._dev
+
+            def _backward():
+                if logits.grad is None:
+                    return
+                if self._dev is not dev:
+                    raise RuntimeError("parameters were re-uploaded since these logits were "
+                                       "computed; run the forward again")
+                g = np.ascontiguousarray(np.asarray(logits.grad).reshape(logits.shape),
+                                         dtype=self._dtype)
+                dg = N.DeviceArray.from_host(g)
+                N.check(N.lib.nml_model_zero_grad(h))
+                N.check(N.lib.nml_model_logits_backward(h, dids.ptr, b, s, dg.ptr))
+                self._pull_grads()
+
+            logits._backward = _backward
+        return logits
 
     def forward_last(self, input_ids):
         """Logits of the last position only, (batch, vocab)."""

@@ -243,6 +243,41 @@ def loss_and_grads(w, ids, labels, num_heads, num_layers, ignore_index=None, rop
 # parameters it reads (reference names and (in, out) layouts): the closures the reference's
 # modules attach (utils/tensor.py:286-332 runs them).
 
+def logits_vjp(w, ids, dlogits, num_heads, num_layers, rope=None):
+    """GPT.forward (models/gpt.py:92-121) and the backward its graph runs for a given
+    d(loss)/d(logits) (batch, seq, vocab): ``(logits, {name: grad})`` — the tied head
+    (gpt.py:150-153), the final RMSNorm, every block in reverse, the embeddings."""
+    dt = w["token_emb.weights"].dtype
+    ids = np.asarray(ids, dtype=np.int64)
+    b, s = ids.shape
+    emb = w["token_emb.weights"]
+    d = emb.shape[1]
+    n = b * s
+    if rope is not None:
+        rope = (rope[0].astype(dt), rope[1].astype(dt))
+    x = emb[ids.reshape(-1)].reshape(n, d).astype(dt)
+    if rope is None:
+        x = x + np.tile(w["pos_emb.weights"][:s], (b, 1))
+    mask = np.triu(np.full((s, s), -np.inf, dtype=dt), k=1)
+    saves = []
+    for i in range(num_layers):
+        x, sv = _block_fwd(x, w, i, b, s, num_heads, mask, rope)
+        saves.append(sv)
+    hf, msf, rmsf = _rms_fwd(x, w["ln.gamma"])
+    logits = hf @ emb.T
+    grads = {name: np.zeros_like(a) for name, a in w.items()}
+    dl = np.asarray(dlogits, dtype=dt).reshape(n, -1)
+    grads["token_emb.weights"] += dl.T @ hf
+    g, dgf = _rms_bwd(dl @ emb, x, w["ln.gamma"], msf, rmsf)
+    grads["ln.gamma"] += dgf
+    for i in reversed(range(num_layers)):
+        g = _block_bwd(g, saves[i], w, i, b, s, num_heads, grads, rope)
+    np.add.at(grads["token_emb.weights"], ids.reshape(-1), g)
+    if rope is None:
+        grads["pos_emb.weights"][:s] += g.reshape(b, s, d).sum(axis=0)
+    return logits.reshape(b, s, -1), grads
+
+
 def blocks_vjp(w, layers, x, dout, num_heads, mask=None, rope=None, final_gamma=None):
     """FusedTransformerBlock (``layers = [i]``, transformer_fused.py:65-78) or
     FusedGPTTrunk (every layer then the final RMSNorm of ``final_gamma``,

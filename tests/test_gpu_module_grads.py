@@ -387,3 +387,39 @@ def test_padded_head_dims_with_masks(gpu, dims, dt):
                 _check(t.grad, want[name], dt, name)
     finally:
         nm.set_dtype(np.dtype(old).name)
+
+
+@pytest.mark.parametrize("dt", [np.float32, np.float16])
+@pytest.mark.parametrize("rope", [False, True])
+def test_gpt_forward_logits_backward(gpu, dt, rope):
+    """GPT.forward's logits carry the whole model's backward: logits.backward(dlogits)
+    gives every parameter's gradient (the tied embedding gets both the head's and the
+    scatter's), against the oracle's logits_vjp; under no_grad the logits carry none."""
+    import nimbleml_amd as nm
+
+    w = _weights(dt, seed=30)
+    if rope:  # no position table (W_q and W_k at the test's common scale)
+        w.pop("pos_emb.weights")
+    m = _gpt(w, dt, use_rope=rope)
+    ids = np.random.default_rng(31).integers(0, CFG.vocab_size, (2, 33))
+    dl = (np.random.default_rng(32).standard_normal((2, 33, CFG.vocab_size)) * 0.1).astype(dt)
+    logits = m.forward(ids)
+    assert logits.requires_grad
+    logits.backward(dl)
+    rc = None
+    if rope:
+        cos, sin = R.rope_cache(CFG.max_seq_len, CFG.d_model // CFG.num_heads)
+        rc = (cos.astype(np.float64), sin.astype(np.float64))
+    want_logits, want = G.logits_vjp(_w64(w), ids, dl.astype(np.float64), CFG.num_heads,
+                                     CFG.num_layers, rope=rc)
+    _check(logits.numpy(), want_logits, dt, "logits")
+    named = {"token_emb.weights": m.token_emb.weights, "ln.gamma": m.ln.gamma}
+    if not rope:
+        named["pos_emb.weights"] = m.pos_emb.weights
+    for i, blk in enumerate(m._block_list):
+        named.update(_block_params(blk, i))
+    for name, t in named.items():
+        if not name.endswith("W_k.biases"):
+            _check(t.grad, want[name], dt, name)
+    with nm.no_grad():
+        assert not m.forward(ids).requires_grad

@@ -302,3 +302,30 @@ def test_planted_mask_slip_fails_the_module_check():
     with pytest.raises(AssertionError):
         _fd_vjp(lambda w_, x_: R.mha(x_, w_, pm, CFG.num_heads, mask), w, x, dout, dx, grads,
                 [n for n in _block_names(0) if ".mha." in n])
+
+
+def test_fd_logits_vjp():
+    """GPT.forward's backward for a given d(loss)/d(logits), against differences of the
+    forward oracle's <dlogits, logits>."""
+    w = _weights()
+    ids, _ = _case(27, b=2, s=6)
+    dl = np.random.default_rng(28).standard_normal((2, 6, CFG.vocab_size))
+    logits, grads = G.logits_vjp(w, ids, dl, CFG.num_heads, CFG.num_layers)
+    want = R.forward(w, ids, CFG.num_heads, CFG.num_layers)
+    assert np.allclose(logits, want, rtol=1e-12, atol=1e-12)
+    rng = np.random.default_rng(29)
+    for name in KINDS:
+        a = w[name]
+        for _ in range(2):
+            idx = tuple(int(rng.integers(0, n)) for n in a.shape)
+            if name == "pos_emb.weights":
+                idx = (int(rng.integers(0, 6)), idx[1])
+            h = 1e-5
+            old = a[idx]
+            a[idx] = old + h
+            lp = float(np.sum(dl * R.forward(w, ids, CFG.num_heads, CFG.num_layers)))
+            a[idx] = old - h
+            lm = float(np.sum(dl * R.forward(w, ids, CFG.num_heads, CFG.num_layers)))
+            a[idx] = old
+            fd = (lp - lm) / (2 * h)
+            assert abs(grads[name][idx] - fd) <= 1e-5 * max(1e-2, abs(fd)), (name, idx)
