@@ -231,8 +231,9 @@ def _saved_forward(model, state, rerun):
     ``state[0]`` is the generation it saved; a later saving forward replaced it, so run
     ``rerun`` (the same forward on the kept input) again."""
     if model.handle is None:
-        raise RuntimeError("the module's parameters changed since this output was computed; "
-                           "run the forward again before backward()")
+        raise RuntimeError("the module's device copy was rebuilt since this output was "
+                           "computed (its parameters changed, or a longer sequence needed a "
+                           "larger one); run the forward again before backward()")
     if _saved_generation(model) != state[0]:
         rerun()
         state[0] = _saved_generation(model)
