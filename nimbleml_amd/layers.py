@@ -130,14 +130,14 @@ def _params_key(params, dt, *extra):
 
 
 def _resident(module, name, key, build):
-    """The device copy ``name`` of ``module`` for ``key``, built (and the previous one
-    released) when the key changed."""
+    """The device copy ``name`` of ``module`` for ``key``, built when the key changed. The
+    previous copy is dropped from the module; it is freed when nothing else holds it (an
+    output's autograd closure keeps the copy its forward ran on until its backward)."""
     cache = module.__dict__.setdefault("_device_copies", {})
     hit = cache.get(name)
     if hit is not None and hit[0] == key:
         return hit[1]
-    if hit is not None and hasattr(hit[1], "close"):
-        hit[1].close()
+    cache.pop(name, None)
     value = build()
     cache[name] = (key, value)
     return value
@@ -231,9 +231,8 @@ def _saved_forward(model, state, rerun):
     ``state[0]`` is the generation it saved; a later saving forward replaced it, so run
     ``rerun`` (the same forward on the kept input) again."""
     if model.handle is None:
-        raise RuntimeError("the module's device copy was rebuilt since this output was "
-                           "computed (its parameters changed, or a longer sequence needed a "
-                           "larger one); run the forward again before backward()")
+        raise RuntimeError("the device model of this output's forward was closed; run the "
+                           "forward again before backward()")
     if _saved_generation(model) != state[0]:
         rerun()
         state[0] = _saved_generation(model)

@@ -423,3 +423,32 @@ def test_gpt_forward_logits_backward(gpu, dt, rope):
             _check(t.grad, want[name], dt, name)
     with nm.no_grad():
         assert not m.forward(ids).requires_grad
+
+
+def test_backward_after_the_device_copy_was_rebuilt(gpu):
+    """A longer sequence rebuilds the block's device model (a larger position capacity)
+    between a forward and its backward: the closure keeps the model its forward ran on, so
+    the first output's gradients are still right."""
+    import nimbleml_amd as nm
+
+    w = _weights(np.float32, seed=33)
+    blk = _gpt(w, np.float32)._block_list[1]
+    x1 = _x((1, 20, CFG.d_model), 34, np.float32)
+    d1 = _x((1, 20, CFG.d_model), 35, np.float32)
+    t1 = nm.Tensor(x1, x1.shape, requires_grad=True)
+    o1 = blk(t1)
+    before = blk.__dict__["_device_copies"]["blocks"][1]
+    x2 = _x((1, 64, CFG.d_model), 36, np.float32)  # capacity 64 → this fits; 65 would not
+    blk(nm.Tensor(x2, x2.shape))
+    assert blk.__dict__["_device_copies"]["blocks"][1] is before
+    blk.mha.W_o.weights.data = blk.mha.W_o.weights.data.copy()  # a new buffer: a new key
+    blk.mha.W_o.weights._bump_version()
+    blk(nm.Tensor(x2, x2.shape))
+    assert blk.__dict__["_device_copies"]["blocks"][1] is not before
+    o1.backward(d1)
+    _, dx1, g1 = G.blocks_vjp(_w64(w), [1], x1.astype(np.float64), d1.astype(np.float64),
+                              CFG.num_heads, R.causal_mask(20, np.float64))
+    _check(t1.grad, dx1, np.float32, "x1")
+    for name, t in _block_params(blk, 1).items():
+        if not name.endswith("W_k.biases"):
+            _check(t.grad, g1[name], np.float32, name)
