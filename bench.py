@@ -30,6 +30,7 @@ head and extrapolated (labelled so).
 from __future__ import annotations
 
 import argparse
+import ctypes
 import json
 import os
 import re
@@ -366,6 +367,46 @@ def bench_c5(nm, reps=5, cpu=False):
             **({"cpu_baseline": base} if base else {})}
 
 
+def bench_c4_attention(nm, reps=20):
+    """The C4 step's decode attention alone — the kernel the step launches once per layer
+    and half — as one launch over all 32 rows and 16 heads, through the C-ABI export
+    nml_decode_attention_device: K/V caches of the C4 shape (max 1280 positions, head dim
+    64, fp16), every row 128 steps into its 256 (contexts len_b + 128 over the C4
+    prompts). HIP events over `reps` launches; bytes are each row's K and V rows read once
+    (the query and output rows are 4 KB a row)."""
+    N = nm._native
+    rng = np.random.default_rng(5)
+    lens = (rng.integers(128, 1025, 32) + 128).astype(np.int32)
+    B, H, P, dk = 32, 16, 1280, 64
+    q = rng.standard_normal((B, H, dk)).astype(np.float16)
+    kc = rng.standard_normal((B, H, P, dk), dtype=np.float32).astype(np.float16)
+    vc = rng.standard_normal((B, H, P, dk), dtype=np.float32).astype(np.float16)
+    dq, dkc, dvc, dl = (N.DeviceArray.from_host(a) for a in (q, kc, vc, lens))
+    del kc, vc
+    err = N.DeviceArray.from_host(np.zeros(1, np.int32))
+    out = N.DeviceArray((B, H * dk), np.float16)
+    call = lambda: N.check(N.lib.nml_decode_attention_device(
+        dq.ptr, dkc.ptr, dvc.ptr, dl.ptr, out.ptr, B, H, P, dk, ctypes.c_float(8.0), err.ptr,
+        N.np_dtype_code(np.float16)))
+    call()
+    N.synchronize()
+    t = N.Timer()
+    t.start()
+    for _ in range(reps):
+        call()
+    ms = t.stop() / reps
+    N.synchronize()
+    if int(err.numpy()[0]) != 0:
+        raise RuntimeError("decode attention flagged a length")
+    nbytes = int(lens.sum()) * H * dk * 2 * 2
+    gbs = nbytes / (ms * 1e-3) / 1e9
+    return {"workload": "C4 decode attention, one launch: 32 rows x 16 heads, dk 64, fp16, "
+                        f"contexts {int(lens.min())}..{int(lens.max())}",
+            "us_per_launch": round(ms * 1e3, 2), "bytes_per_launch": nbytes,
+            "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS,
+                         "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4)}}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -376,7 +417,8 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-graph", action="store_true")
     ap.add_argument("--only-c3", action="store_true", help="skip the batch-32 and prefill lines")
-    ap.add_argument("--only", choices=["c3", "c4", "c5", "adamw", "train", "train16"], default=None,
+    ap.add_argument("--only", choices=["c3", "c4", "c4attn", "c5", "adamw", "train", "train16"],
+                    default=None,
                     help="run one workload only (for profiling); c4/c5 print their own line")
     ap.add_argument("--train-skew", action="store_true",
                     help="train lines with half of the input ids one token (embedding scatter)")
@@ -413,6 +455,9 @@ def main():
         return
     if args.only == "c5":
         print(json.dumps({"c5": bench_c5(nm, cpu=not args.no_cpu_baseline)}), flush=True)
+        return
+    if args.only == "c4attn":
+        print(json.dumps({"c4attn": bench_c4_attention(nm)}), flush=True)
         return
     if args.only == "adamw":
         print(json.dumps({"adamw": bench_adamw(nm)}), flush=True)
