@@ -1478,18 +1478,27 @@ constexpr size_t attn_f16_lds() {
 // and, when XT is given, the transposed [dim][64 + 8] copy, in blocks of 4 rows × 8 dims
 // (block b of 16·DK/8: rows 4·(b / (DK/8)) …, dims 8·(b % (DK/8)) …) taken by threads
 // first … first + 16·DK/8 − 1.
+// fetch16 loads the block into registers, put16 writes it (and its transpose) to LDS;
+// stage16 does both.
 template <int DK>
-__device__ __forceinline__ void stage16(half_t* X, half_t* XT, const half_t* __restrict__ src, long long ld,
+__device__ __forceinline__ void fetch16(half8 (&v)[4], const half_t* __restrict__ src, long long ld,
                                         int lo, int S, int first) {
-  constexpr int PA = DK + 8, PT = kAT + 8, NB = 16 * DK / 8;
+  constexpr int NB = 16 * DK / 8;
   const int b = static_cast<int>(threadIdx.x) - first;
   if (b < 0 || b >= NB) return;
   const int r0 = 4 * (b / (DK / 8)), c = 8 * (b % (DK / 8));
   const half8 z = {0, 0, 0, 0, 0, 0, 0, 0};
-  half8 v[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i)
     v[i] = lo + r0 + i < S ? *reinterpret_cast<const half8*>(src + static_cast<long long>(lo + r0 + i) * ld + c) : z;
+}
+
+template <int DK>
+__device__ __forceinline__ void put16(half_t* X, half_t* XT, const half8 (&v)[4], int first) {
+  constexpr int PA = DK + 8, PT = kAT + 8, NB = 16 * DK / 8;
+  const int b = static_cast<int>(threadIdx.x) - first;
+  if (b < 0 || b >= NB) return;
+  const int r0 = 4 * (b / (DK / 8)), c = 8 * (b % (DK / 8));
 #pragma unroll
   for (int i = 0; i < 4; ++i) *reinterpret_cast<half8*>(X + (r0 + i) * PA + c) = v[i];
   if (XT) {
@@ -1499,6 +1508,14 @@ __device__ __forceinline__ void stage16(half_t* X, half_t* XT, const half_t* __r
       *reinterpret_cast<half4*>(XT + (c + j) * PT + r0) = w;
     }
   }
+}
+
+template <int DK>
+__device__ __forceinline__ void stage16(half_t* X, half_t* XT, const half_t* __restrict__ src, long long ld,
+                                        int lo, int S, int first) {
+  half8 v[4];
+  fetch16<DK>(v, src, ld, lo, S, first);
+  put16<DK>(X, XT, v, first);
 }
 
 // A 16-row fragment of a transposed [dim][64 + 8] tile: dims d0 + l % 32, rows of step s
@@ -1548,16 +1565,48 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dkdv_f16(AttnBwdArgs a) {
     for (int r = 0; r < 16; ++r) dv[j][r] = dk[j][r] = 0.f;
   const int key = k_lo + 32 * wk + l32;
   const float inv_scale = 1.0f / a.scale, mul = score_mul<half_t>(a.scale);
+  // At DK 64 each thread stages one block (threads 0-127 of Q, 128-255 of dO), so the next
+  // query tile's block and statistics are fetched into registers while the current tile
+  // is multiplied; at DK 128 (two blocks a thread) the registers are not there to spare.
+  constexpr bool PF = NB == 128;
+  const bool own_q = static_cast<int>(threadIdx.x) < NB;
+  half8 nx[4];
+  float nl = 0.f, nd = 0.f;
+  auto fetch_next = [&](int lo) {
+    if (own_q)
+      fetch16<DK>(nx, qg, DK, lo, S, 0);
+    else
+      fetch16<DK>(nx, og, static_cast<long long>(a.H) * DK, lo, S, NB);
+    if (threadIdx.x < kAT) {
+      const int q = lo + threadIdx.x;
+      nl = q < S ? a.lse[static_cast<long long>(bh) * S + q] : 0.f;
+      nd = q < S ? a.dvec[static_cast<long long>(bh) * S + q] : 0.f;
+    }
+  };
+  if constexpr (PF) fetch_next(k_lo);
   for (int q_lo = k_lo; q_lo < S; q_lo += kAT) {
     __syncthreads();
-    stage16<DK>(Qs, QT, qg, DK, q_lo, S, 0);
-    stage16<DK>(Os, OT, og, static_cast<long long>(a.H) * DK, q_lo, S, NB % 256);
-    if (threadIdx.x < kAT) {
-      const int q = q_lo + threadIdx.x;
-      Ls[threadIdx.x] = q < S ? a.lse[static_cast<long long>(bh) * S + q] : 0.f;
-      Ds[threadIdx.x] = q < S ? a.dvec[static_cast<long long>(bh) * S + q] : 0.f;
+    if constexpr (PF) {
+      if (own_q)
+        put16<DK>(Qs, QT, nx, 0);
+      else
+        put16<DK>(Os, OT, nx, NB);
+      if (threadIdx.x < kAT) {
+        Ls[threadIdx.x] = nl;
+        Ds[threadIdx.x] = nd;
+      }
+    } else {
+      stage16<DK>(Qs, QT, qg, DK, q_lo, S, 0);
+      stage16<DK>(Os, OT, og, static_cast<long long>(a.H) * DK, q_lo, S, NB % 256);
+      if (threadIdx.x < kAT) {
+        const int q = q_lo + threadIdx.x;
+        Ls[threadIdx.x] = q < S ? a.lse[static_cast<long long>(bh) * S + q] : 0.f;
+        Ds[threadIdx.x] = q < S ? a.dvec[static_cast<long long>(bh) * S + q] : 0.f;
+      }
     }
     __syncthreads();
+    if constexpr (PF)
+      if (q_lo + kAT < S) fetch_next(q_lo + kAT);
     floatx16 sc, dp;
 #pragma unroll
     for (int r = 0; r < 16; ++r) sc[r] = dp[r] = 0.f;
@@ -1647,11 +1696,32 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dq_f16(AttnBwdArgs a) {
 #pragma unroll
     for (int r = 0; r < 16; ++r) dq[j][r] = 0.f;
   const int k_end = min(S, q_lo + kAT);
+  // DK 64: the next key tile's block (threads 0-127 of K, 128-255 of V) in registers while
+  // the current one is multiplied, as in the dK/dV kernel
+  constexpr bool PF = NB == 128;
+  const bool own_k = static_cast<int>(threadIdx.x) < NB;
+  half8 nx[4];
+  auto fetch_next = [&](int lo) {
+    if (own_k)
+      fetch16<DK>(nx, kg, DK, lo, S, 0);
+    else
+      fetch16<DK>(nx, vg, DK, lo, S, NB);
+  };
+  if constexpr (PF) fetch_next(0);
   for (int k_lo = 0; k_lo < k_end; k_lo += kAT) {
     __syncthreads();
-    stage16<DK>(Ks, KT, kg, DK, k_lo, S, 0);
-    stage16<DK>(Vs, nullptr, vg, DK, k_lo, S, NB % 256);
+    if constexpr (PF) {
+      if (own_k)
+        put16<DK>(Ks, KT, nx, 0);
+      else
+        put16<DK>(Vs, nullptr, nx, NB);
+    } else {
+      stage16<DK>(Ks, KT, kg, DK, k_lo, S, 0);
+      stage16<DK>(Vs, nullptr, vg, DK, k_lo, S, NB % 256);
+    }
     __syncthreads();
+    if constexpr (PF)
+      if (k_lo + kAT < k_end) fetch_next(k_lo + kAT);
     floatx16 sc, dp;
 #pragma unroll
     for (int r = 0; r < 16; ++r) sc[r] = dp[r] = 0.f;
