@@ -13,7 +13,7 @@ from nimbleml_amd.grad_mode import enable_grad, is_grad_enabled, no_grad
 from nimbleml_amd.gpt import GPT, KVCache
 from nimbleml_amd.layers import (Dense, Embedding, FeedForward, FusedGPTTrunk,
                                  FusedTransformerBlock, Module, MultiHeadAttention, RMSNorm,
-                                 Sequential)
+                                 Sequential, TransformerBlock)
 from nimbleml_amd.np_backend import device, set_device, set_dtype, using_gpu
 from nimbleml_amd.optim import Adam, AdamW
 from nimbleml_amd.saveload import (load, load_arrays, load_checkpoint, named_parameters, save,
@@ -22,7 +22,8 @@ from nimbleml_amd.tensor import Tensor
 
 __all__ = [
     "GPT", "KVCache", "generate", "Tensor", "DeviceArray", "Dense", "Embedding", "RMSNorm",
-    "MultiHeadAttention", "FeedForward", "FusedTransformerBlock", "FusedGPTTrunk", "Module",
+    "MultiHeadAttention", "FeedForward", "FusedTransformerBlock", "FusedGPTTrunk",
+    "TransformerBlock", "Module",
     "Sequential", "save", "load", "load_arrays", "named_parameters", "save_checkpoint",
     "load_checkpoint", "Adam", "AdamW", "device", "using_gpu",
     "set_device", "set_dtype", "np_backend", "no_grad", "enable_grad", "is_grad_enabled",

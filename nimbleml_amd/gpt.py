@@ -18,7 +18,8 @@ from nimbleml_amd import _native as N
 from nimbleml_amd import np_backend
 from nimbleml_amd.grad_mode import is_grad_enabled
 from nimbleml_amd.layers import (Embedding, FusedGPTTrunk, FusedTransformerBlock, Module,
-                                 RMSNorm, Sequential, block_device_arrays, rope_device_arrays)
+                                 RMSNorm, Sequential, TransformerBlock, block_device_arrays,
+                                 rope_device_arrays)
 from nimbleml_amd.tensor import Tensor
 
 # Every live GPT, so that an optimizer given ``model.parameters()`` finds its model.
@@ -69,8 +70,9 @@ class GPT(Module):
             raise ValueError(f"d_model ({d_model}) must be divisible by num_heads ({num_heads}).")
         if fused_trunk and not fused_blocks:
             raise ValueError("fused_trunk requires fused_blocks=True.")
-        if not fused_blocks:
-            raise ValueError("nimbleml_amd implements the fused_blocks=True path of GPT.")
+        if use_rope and not fused_blocks:  # models/gpt.py:44-45
+            raise ValueError("use_rope requires fused_blocks=True (RoPE is applied in the "
+                             "fused MHA path).")
         self.vocab_size = vocab_size
         self.d_model = d_model
         self.num_heads = num_heads
@@ -90,9 +92,13 @@ class GPT(Module):
             self._rope_cos, self._rope_sin = build_rope_cache(max_seq_len, d_model // num_heads)
         else:
             self._rope_cos = self._rope_sin = None
-        block_modules = [FusedTransformerBlock(d_model, num_heads, ff_mult,
-                                               gradient_checkpointing=gradient_checkpointing)
-                         for _ in range(num_layers)]
+        if fused_blocks:
+            block_modules = [FusedTransformerBlock(d_model, num_heads, ff_mult,
+                                                   gradient_checkpointing=gradient_checkpointing)
+                             for _ in range(num_layers)]
+        else:  # models/gpt.py:66-67: the unfused block, the same function and parameters
+            block_modules = [TransformerBlock(d_model, num_heads, ff_mult)
+                             for _ in range(num_layers)]
         if self.use_rope:
             for block in block_modules:
                 block.mha._rope_cache = (self._rope_cos, self._rope_sin)

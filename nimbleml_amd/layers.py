@@ -778,6 +778,22 @@ class FusedTransformerBlock(Module):
         return params
 
 
+class TransformerBlock(FusedTransformerBlock):
+    """The unfused pre-norm block of ``GPT(fused_blocks=False)``
+    (neural_network/transformer.py:9-55): the same parameters (ln1, mha, ln2, ffn) and the
+    same function, x + MHA(RMSNorm₁(x)) then + FFN(RMSNorm₂(·)), causal when mask is None.
+    The reference builds it from Tensor-level ops; here it runs the fused block's device
+    path, forward and backward."""
+
+    def __init__(self, d_model, num_heads, ff_mult=4):
+        super().__init__(d_model, num_heads, ff_mult)
+
+    def forward(self, x, mask=None):
+        """transformer.py:19-48."""
+        return _blocks_forward(self, [self], None, x, mask, "transformer_block",
+                               self.parameters())
+
+
 class FusedGPTTrunk(Module):
     """All blocks plus the final RMSNorm as one module (transformer_fused.py:103-144)."""
 

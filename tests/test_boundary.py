@@ -122,6 +122,10 @@ def test_input_validation_matches_reference_errors():
         nm.GPT(20, 10, 3, 1, 6)
     with pytest.raises(ValueError, match="fused_trunk requires"):
         nm.GPT(20, 8, 2, 1, 6, fused_blocks=False, fused_trunk=True)
+    with pytest.raises(ValueError, match="use_rope requires"):
+        nm.GPT(20, 8, 2, 1, 6, fused_blocks=False, use_rope=True)
+    m = nm.GPT(20, 8, 2, 2, 6, fused_blocks=False)  # models/gpt.py:66-67
+    assert [type(b).__name__ for b in m.blocks.layers] == ["TransformerBlock"] * 2
 
 
 def test_backend_device_and_dtype_selection():

@@ -378,3 +378,42 @@ def test_eos_stop_leaves_the_global_rng_as_the_reference_does(gpu):
     np.random.seed(77)
     np.random.random_sample(first + 1 - s0)  # one draw per step taken
     assert after == np.random.random_sample()
+
+
+@pytest.mark.parametrize("name", ["tiny_rich_fp32", "tiny_rich_fp16"])
+def test_unfused_blocks_run_the_same_model(gpu, name):
+    """GPT(fused_blocks=False) (models/gpt.py:66-67: TransformerBlock, the same pre-norm
+    function and parameter names) loads the reference's checkpoint and gives the fused
+    model's logits, loss and greedy tokens exactly, within the reference's tolerance of its
+    logits; its blocks are TransformerBlock modules whose module-level forward equals the
+    fused block's."""
+    import nimbleml_amd as nm
+
+    f = golden(name)
+    cfg, w = fixture_weights(f)
+    dt = w["token_emb.weights"].dtype
+    fused = build(cfg, w, dt)
+    old = nm.np_backend.dtype
+    nm.set_dtype(np.dtype(dt).name)
+    try:
+        unf = nm.GPT(cfg.vocab_size, cfg.d_model, cfg.num_heads, cfg.num_layers,
+                     cfg.max_seq_len, ff_mult=cfg.ff_mult, fused_blocks=False)
+    finally:
+        nm.set_dtype(np.dtype(old).name)
+    nm.load_arrays(unf, w)
+    assert all(type(b) is nm.TransformerBlock for b in unf.blocks.layers)
+    ids = np.asarray(f["greedy"][:, :-1], dtype=np.int64)
+    a = unf.forward(ids).numpy()
+    assert np.array_equal(a, fused.forward(ids).numpy())
+    assert np.abs(a.astype(np.float64) - f["greedy_logits"]).max() <= tol_for(dt)
+    lid, lab = f["loss_ids"], f["loss_labels"]
+    assert unf.compute_loss(lid, lab).item() == fused.compute_loss(lid, lab).item()
+    n = f["greedy"].shape[1] - f["prompt"].shape[1]
+    g1 = nm.generate(unf, f["prompt"], max_new_tokens=n, temperature=0.0)
+    g2 = nm.generate(fused, f["prompt"], max_new_tokens=n, temperature=0.0)
+    assert np.array_equal(np.asarray(g1), np.asarray(g2))
+    x = np.random.default_rng(3).standard_normal((2, 5, cfg.d_model)).astype(dt)
+    with nm.no_grad():
+        o1 = unf.blocks.layers[0](nm.Tensor(x, x.shape)).numpy()
+        o2 = fused.blocks.layers[0](nm.Tensor(x, x.shape)).numpy()
+    assert np.array_equal(o1, o2)
