@@ -14,6 +14,7 @@ from nimbleml_amd.gpt import GPT, KVCache
 from nimbleml_amd.layers import (Dense, Embedding, FeedForward, FusedGPTTrunk,
                                  FusedTransformerBlock, Module, MultiHeadAttention, RMSNorm,
                                  Sequential, TransformerBlock)
+from nimbleml_amd.mask import causal_mask_tensor, make_causal_mask
 from nimbleml_amd.np_backend import device, set_device, set_dtype, using_gpu
 from nimbleml_amd.optim import Adam, AdamW
 from nimbleml_amd.saveload import (load, load_arrays, load_checkpoint, named_parameters, save,
@@ -27,4 +28,5 @@ __all__ = [
     "Sequential", "save", "load", "load_arrays", "named_parameters", "save_checkpoint",
     "load_checkpoint", "Adam", "AdamW", "device", "using_gpu",
     "set_device", "set_dtype", "np_backend", "no_grad", "enable_grad", "is_grad_enabled",
+    "causal_mask_tensor", "make_causal_mask",
 ]

@@ -150,3 +150,23 @@ def test_fused_trunk_names():
     m = nm.GPT(20, 8, 2, 2, 6, fused_trunk=True)
     names = [n for n, _ in nm.named_parameters(m)]
     assert "blocks.blocks.1.ffn.dense2.biases" in names and "blocks.ln.gamma" in names
+
+
+def test_causal_mask_helpers():
+    """utils/mask.py:8-27: triu(−inf, k=1) in the compute dtype, cached per (seq, dtype),
+    no gradient; the modules take it for the causal kernels."""
+    import nimbleml_amd as nm
+    from nimbleml_amd.layers import _mask_mode
+
+    old = nm.np_backend.dtype
+    try:
+        for dt in ("float32", "float16"):
+            nm.set_dtype(dt)
+            t = nm.causal_mask_tensor(5)
+            a = nm.make_causal_mask(5)
+            assert a.dtype == np.dtype(dt) and t.shape == (5, 5) and not t.requires_grad
+            assert np.array_equal(a, np.triu(np.full((5, 5), -np.inf, dtype=dt), k=1))
+            assert nm.causal_mask_tensor(5) is t
+            assert _mask_mode(t, 5, np.dtype(dt), none_is_causal=False) == (1, None)
+    finally:
+        nm.set_dtype(np.dtype(old).name)
