@@ -407,9 +407,10 @@ def _blocks_forward(owner, blocks, ln, x, mask, op, params):
     N.check(N.lib.nml_synchronize())
     state = [_saved_generation(model)]
 
-    def rerun():
+    def rerun():  # the mask's device copy is referenced here, so it outlives the forward
         tmp = N.DeviceArray((b, s, d), dt)
-        N.check(N.lib.nml_model_blocks_forward_train(model.handle, xd.ptr, tmp.ptr, *args))
+        N.check(N.lib.nml_model_blocks_forward_train(model.handle, xd.ptr, tmp.ptr, b, s,
+                                                     int(ln is not None), causal, N.ptr(mdev)))
 
     def backward(o):
         dy = _dy(o, dt)

@@ -452,3 +452,36 @@ def test_backward_after_the_device_copy_was_rebuilt(gpu):
     for name, t in _block_params(blk, 1).items():
         if not name.endswith("W_k.biases"):
             _check(t.grad, g1[name], np.float32, name)
+
+
+def test_recompute_keeps_the_forward_mask(gpu):
+    """A masked output whose saved forward was replaced recomputes with its own mask (the
+    device copy of the mask stays alive with the output's closure): block and attention."""
+    import gc
+
+    import nimbleml_amd as nm
+
+    w = _weights(np.float32, seed=37)
+    blk = _gpt(w, np.float32)._block_list[0]
+    s = 19
+    x1, d1 = _x((2, s, CFG.d_model), 38, np.float32), _x((2, s, CFG.d_model), 39, np.float32)
+    mask = _mixed_mask(s, np.float32, 9)
+    for mod, vjp in ((blk, "block"), (blk.mha, "mha")):
+        _zero(blk.parameters())
+        t1 = nm.Tensor(x1, x1.shape, requires_grad=True)
+        o1 = mod(t1, nm.Tensor(mask, mask.shape))
+        mod(nm.Tensor(x1[:1], (1, s, CFG.d_model)))  # another saving forward, no mask
+        gc.collect()
+        o1.backward(d1)
+        if vjp == "block":
+            _, dx, g = G.blocks_vjp(_w64(w), [0], x1.astype(np.float64), d1.astype(np.float64),
+                                    CFG.num_heads, mask.astype(np.float64))
+            names = _block_params(blk, 0)
+        else:
+            _, dx, g = G.mha_vjp(_w64(w), "blocks.layers.0.mha.", x1.astype(np.float64),
+                                 d1.astype(np.float64), CFG.num_heads, mask.astype(np.float64))
+            names = {k: v for k, v in _block_params(blk, 0).items() if ".mha." in k}
+        _check(t1.grad, dx, np.float32, f"{vjp} x")
+        for name, t in names.items():
+            if not name.endswith("W_k.biases"):
+                _check(t.grad, g[name], np.float32, f"{vjp} {name}")
