@@ -485,3 +485,39 @@ def test_recompute_keeps_the_forward_mask(gpu):
         for name, t in names.items():
             if not name.endswith("W_k.biases"):
                 _check(t.grad, g[name], np.float32, f"{vjp} {name}")
+
+
+@pytest.mark.parametrize("dtype_ctx", [np.float32, np.float16], indirect=True)
+def test_sequential_blocks_and_unbiased_dense(dtype_ctx):
+    """GPT.blocks as a Sequential of blocks (no fused trunk): one closure per block, run by
+    Tensor.backward from the last block to the first; a Dense without bias
+    (layers/dense.py:16-25, bias=False) gets only its weight gradient."""
+    import nimbleml_amd as nm
+
+    dt = dtype_ctx
+    w = _weights(dt, seed=40)
+    m = _gpt(w, dt)
+    x = _x((2, 26, CFG.d_model), 41, dt)
+    dout = _x((2, 26, CFG.d_model), 42, dt)
+    xt = nm.Tensor(x, x.shape, requires_grad=True)
+    out = m.blocks(xt)
+    out.backward(dout)
+    want_out, want_dx, want = G.blocks_vjp(_w64(w), list(range(CFG.num_layers)),
+                                           x.astype(np.float64), dout.astype(np.float64),
+                                           CFG.num_heads, R.causal_mask(26, np.float64))
+    _check(out.numpy(), want_out, dt, "out")
+    _check(xt.grad, want_dx, dt, "x")
+    for i, blk in enumerate(m._block_list):
+        for name, t in _block_params(blk, i).items():
+            if not name.endswith("W_k.biases"):
+                _check(t.grad, want[name], dt, name)
+    dense = nm.Dense(CFG.d_model, 40, bias=False)
+    xt = nm.Tensor(x, x.shape, requires_grad=True)
+    y = dense(xt)
+    dy = _x(y.shape, 43, dt)
+    y.backward(dy)
+    W = np.asarray(dense.weights.data, np.float64).reshape(CFG.d_model, 40)
+    _, dx64, dw64, _ = G.dense_vjp(W, None, x.astype(np.float64), dy.astype(np.float64))
+    _check(xt.grad, dx64, dt, "dense x")
+    _check(dense.weights.grad, dw64, dt, "dense W")
+    assert dense.biases is None
