@@ -600,6 +600,7 @@ __global__ __launch_bounds__(256, 2) void attn_prefill_mfma_kernel(AttnArgs a) {
   // rounding midpoint, far beyond the product's 2^-23 error.
   const float rscale = 1.0f / scale_t;
   const float cscale = 1.4426950408889634f / scale_t;  // log2(e) / scale (fp32 scores)
+  const float lazy = 8.0f / cscale;  // 2^8 in p, in units of q·k
   const int qw = q0 + wave * 32;           // first query of this wave
   const int myq = qw + (lane & 31);        // this lane's query
   const int hi = lane >> 5;                // which half of the wave
@@ -785,15 +786,21 @@ __global__ __launch_bounds__(256, 2) void attn_prefill_mfma_kernel(AttnArgs a) {
           if (t + r > 0) mloc = fmaxf(mloc, st[t][r]);
       float mx = fmaxf(m, mloc);
       mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-      const float alpha = (mx == -INFINITY) ? 1.f : __builtin_amdgcn_exp2f((m - mx) * cscale);
-      const float nmx = -mx * cscale;
-      l *= alpha;
-      if (__any(mx > m)) {
+      // The reference point of the exponents moves only when some query's maximum grew
+      // past it by more than 2^8 in p (the probabilities stay below 256: exact in fp16's
+      // relative precision, far from its range); otherwise the old point stays and no
+      // rescale of O and l is needed.
+      if (__any(mx > m + lazy)) {
+        const float alpha = (mx == -INFINITY) ? 1.f : __builtin_amdgcn_exp2f((m - mx) * cscale);
+        l *= alpha;
 #pragma unroll
         for (int t = 0; t < OT; ++t)
 #pragma unroll
           for (int r = 0; r < 16; ++r) o[t][r] *= alpha;
+      } else {
+        mx = m;
       }
+      const float nmx = -mx * cscale;
       typedef _Float16 half2v __attribute__((ext_vector_type(2)));
       const half2v ones = {static_cast<_Float16>(1.0f), static_cast<_Float16>(1.0f)};
 #pragma unroll
