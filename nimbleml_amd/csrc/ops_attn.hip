@@ -6,8 +6,10 @@
 // fp16 divisor); the softmax itself runs online in fp32 (flash form), so no
 // (S, S) score matrix exists.
 //
-//  * prefill, fp16 head dim 64/128: attn_prefill_mfma_kernel — MFMA flash
-//    attention, 128 queries per workgroup, 64-key K/V tiles in LDS (see its comment);
+//  * prefill, fp16 head dim 64/128: MFMA flash attention, 128 queries per workgroup,
+//    64-key K/V tiles in LDS — attn_prefill_pipe_kernel (fp32 scores, software-pipelined
+//    over the tiles) where no statistics are kept, attn_prefill_mfma_kernel (fp16-rounded
+//    scores, statistics for the backward) otherwise;
 //    fp32 head dim 64/128: attn_prefill_f32_mfma; head dims 8/16/32 (and the non-causal
 //    masked form): attn_prefill_kernel, one wave per 64 queries, scalar; any other head
 //    dim ≤ 256: attn_prefill_quad_kernel, four lanes per query.
@@ -16,6 +18,7 @@
 //    its (max, Σp, Σp·v) as flagged slots; the last workgroup of the (sequence, head)
 //    merges them. Other head dims ≤ 256: attn_decode_small_kernel + attn_combine_kernel.
 #include <cstdlib>
+#include <type_traits>
 
 #include "kernels.hpp"
 
@@ -544,17 +547,16 @@ __global__ __launch_bounds__(64) void attn_combine_kernel(AttnArgs a, const int3
   }
 }
 
-// Causal flash attention on the matrix cores (fp16, head dim 64 or 128). A 256-lane
-// workgroup takes 128 queries of one (row, head), 32 per wave, and walks 64-key tiles
-// of the cache staged in LDS (K row-major, V transposed):
+// Causal flash attention on the matrix cores (fp16, head dim 64 or 128) for the calls
+// that store the softmax statistics (the backward recomputes the scores from them), so
+// the scores are rounded to fp16 as in the scalar path. A 256-lane workgroup takes 128
+// queries of one (row, head), 32 per wave, and walks 64-key tiles of the cache staged
+// in LDS (K row-major, V transposed):
 //   Sᵀ = K·Qᵀ    v_mfma_f32_32x32x16_f16, A = 32 keys × 16 dims from LDS, B = Qᵀ
 //                (registers for the whole walk); lane l then holds query l%32 and
 //                keys 8(r/4) + 4(l/32) + r%4 of each 32-key tile in register r;
 //   online softmax per query: lane-local over its 16 keys, one xor-32 shuffle with
-//                the lane holding the other 16. R16 (calls that store the softmax
-//                statistics for the backward, which recomputes the scores from them):
-//                scores rounded to fp16 as in the scalar path; otherwise the scores
-//                stay fp32 accumulators (one FMA and one exp2 per score);
+//                the lane holding the other 16;
 //   Oᵀ += Vᵀ·Pᵀ  A = Vᵀ (32 dims × 16 keys) from LDS, B = Pᵀ in fp16 straight from the
 //                Sᵀ registers: B's k-slot j of lane l is key 8(j/4) + 4(l/32) + j%4 of
 //                the 16-key block, and A is read with the same key order;
@@ -564,7 +566,7 @@ __global__ __launch_bounds__(64) void attn_combine_kernel(AttnArgs a, const int3
 // tiles are dispatched last-first (the causal walk is longest for them).
 constexpr int kFQ = 128, kFK = 64;
 
-template <int DK, bool R16>
+template <int DK>
 __global__ __launch_bounds__(256, 2) void attn_prefill_mfma_kernel(AttnArgs a) {
 #pragma clang fp contract(off)
   constexpr int KS = DK / 16;  // 16-dim steps of q·k
@@ -599,8 +601,6 @@ __global__ __launch_bounds__(256, 2) void attn_prefill_mfma_kernel(AttnArgs a) {
   // the exact quotient of an fp16 by s is never within 2^-19 (relative) of an fp16
   // rounding midpoint, far beyond the product's 2^-23 error.
   const float rscale = 1.0f / scale_t;
-  const float cscale = 1.4426950408889634f / scale_t;  // log2(e) / scale (fp32 scores)
-  const float lazy = 8.0f / cscale;  // 2^8 in p, in units of q·k
   const int qw = q0 + wave * 32;           // first query of this wave
   const int myq = qw + (lane & 31);        // this lane's query
   const int hi = lane >> 5;                // which half of the wave
@@ -687,7 +687,7 @@ __global__ __launch_bounds__(256, 2) void attn_prefill_mfma_kernel(AttnArgs a) {
         st[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ka, qb[ks], st[t], 0, 0, 0);
       }
     }
-    if constexpr (R16) {
+    {
       // Scores as fp16 pairs (registers r = 2c, 2c + 1): rnd(rnd(q·k)·rscale) is one mixed
       // fma with an fp16 result (the exact product rounds as its fp32 rounding does, see
       // rscale), the running maximum a packed fp16 max.
@@ -764,74 +764,6 @@ __global__ __launch_bounds__(256, 2) void attn_prefill_mfma_kernel(AttnArgs a) {
           }
         }
       m = mx;
-    } else {
-      // Scores kept in fp32, in units of q·k (m is the running maximum of q·k): the
-      // maximum over the raw accumulators (the scale is positive), then
-      // p = exp2(q·k·c − m·c) with c = log2(e) / scale, one FMA and one exp2 a score, and
-      // the row sum over the fp16 probabilities the PV product uses, two per v_dot2.
-      if (k0 + kFK - 1 > base + qw) {
-#pragma unroll
-        for (int t = 0; t < 2; ++t)
-#pragma unroll
-          for (int r = 0; r < 16; ++r) {
-            const int key = k0 + t * 32 + 8 * (r >> 2) + 4 * hi + (r & 3);
-            if (!(key <= qpos && key < kend)) st[t][r] = -INFINITY;
-          }
-      }
-      float mloc = st[0][0];
-#pragma unroll
-      for (int t = 0; t < 2; ++t)
-#pragma unroll
-        for (int r = 0; r < 16; ++r)
-          if (t + r > 0) mloc = fmaxf(mloc, st[t][r]);
-      float mx = fmaxf(m, mloc);
-      mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-      // The reference point of the exponents moves only when some query's maximum grew
-      // past it by more than 2^8 in p (the probabilities stay below 256: exact in fp16's
-      // relative precision, far from its range); otherwise the old point stays and no
-      // rescale of O and l is needed.
-      if (__any(mx > m + lazy)) {
-        const float alpha = (mx == -INFINITY) ? 1.f : __builtin_amdgcn_exp2f((m - mx) * cscale);
-        l *= alpha;
-#pragma unroll
-        for (int t = 0; t < OT; ++t)
-#pragma unroll
-          for (int r = 0; r < 16; ++r) o[t][r] *= alpha;
-      } else {
-        mx = m;
-      }
-      const float nmx = -mx * cscale;
-      typedef _Float16 half2v __attribute__((ext_vector_type(2)));
-      const half2v ones = {static_cast<_Float16>(1.0f), static_cast<_Float16>(1.0f)};
-#pragma unroll
-      for (int t = 0; t < 2; ++t)
-#pragma unroll
-        for (int kb = 0; kb < 2; ++kb) {
-          half8 pb;
-#pragma unroll
-          for (int j = 0; j < 8; j += 2) {
-            // mx is finite (key 0 precedes every query), so a masked score gives 0
-            const float p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(st[t][8 * kb + j], cscale, nmx));
-            const float p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(st[t][8 * kb + j + 1], cscale, nmx));
-            const half2v pp = {static_cast<_Float16>(p0), static_cast<_Float16>(p1)};
-            l = __builtin_amdgcn_fdot2(pp, ones, l, false);
-            pb[j] = pp[0];
-            pb[j + 1] = pp[1];
-          }
-          const int kblk = t * 32 + kb * 16 + 4 * hi;
-#pragma unroll
-          for (int ot = 0; ot < OT; ++ot) {
-            const half_t* vrow = &Vt[ot * 32 + (lane & 31)][kblk];
-            half8 va;
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-              va[e] = vrow[e];
-              va[4 + e] = vrow[8 + e];
-            }
-            o[ot] = __builtin_amdgcn_mfma_f32_32x32x16_f16(va, pb, o[ot], 0, 0, 0);
-          }
-        }
-      m = mx;
     }
   }
   l += __shfl_xor(l, 32, 64);
@@ -840,6 +772,275 @@ __global__ __launch_bounds__(256, 2) void attn_prefill_mfma_kernel(AttnArgs a) {
     a.m_out[static_cast<size_t>(bh) * a.S + myq] = m;
     a.l_out[static_cast<size_t>(bh) * a.S + myq] = l;
   }
+  if (myq < S) {
+    const float inv = 1.f / l;
+    const int hd = a.H * DK;
+    const size_t row = (a.row_start ? a.row_start[b] : static_cast<size_t>(b) * S) + myq;
+    half_t* out = static_cast<half_t*>(a.out) + row * hd + h * DK;
+#pragma unroll
+    for (int ot = 0; ot < OT; ++ot)
+#pragma unroll
+      for (int r = 0; r < 16; ++r)
+        out[ot * 32 + 8 * (r >> 2) + 4 * hi + (r & 3)] = static_cast<half_t>(o[ot][r] * inv);
+  }
+}
+
+// Causal flash attention on the matrix cores with fp32 scores (prefill calls that keep
+// no softmax statistics), software-pipelined over the 64-key tiles. The layout per wave
+// is attn_prefill_mfma_kernel's (32 queries, Sᵀ = K·Qᵀ and Oᵀ += Vᵀ·Pᵀ on
+// v_mfma_f32_32x32x16_f16, each lane owning one query's softmax state and output
+// column); what differs is the order of the work. Iteration j of a wave:
+//   1. one barrier; K of tile j + 2 and V of tile j + 1 go from registers into LDS (two
+//      buffers each: K(j + 2) replaces K(j), read one iteration earlier; V(j + 1)
+//      replaces V(j − 1)), and the loads of K(j + 3) and V(j + 2) are issued;
+//   2. the rescale of O and l when tile j moved a query's reference point (rare: the
+//      point moves only when a maximum grows by more than 2^8 in p);
+//   3. the scores of tile j + 1 (16 MFMAs) beside the probabilities of tile j (exp2,
+//      fp16 packing, row sums) — independent work for the matrix and vector pipes;
+//   4. P·V of tile j (16 MFMAs) beside the masking, maximum and reference point of
+//      tile j + 1.
+// Rows past the last key are read clamped to it (in bounds and finite; the causal
+// mask removes them), so a tile needs no bounds tests. Waves whose queries all lie
+// past the sequence skip the arithmetic but join the barriers.
+template <int DK>
+__global__ __launch_bounds__(256, 2) void attn_prefill_pipe_kernel(AttnArgs a) {
+#pragma clang fp contract(off)
+  constexpr int KS = DK / 16;  // 16-dim steps of q·k
+  constexpr int OT = DK / 32;  // 32-dim tiles of the output
+  constexpr int CH = kFK * DK / 8 / 256;  // 16-byte pieces of a tile's K (and of V) per thread
+  constexpr int VG = DK / 8;              // 8-dim groups of a key
+  __shared__ half_t Ks[2][kFK][DK + 8];
+  __shared__ half_t Vt[2][DK][kFK + 4];  // rows 34 dwords apart, as in attn_prefill_mfma_kernel
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int nq = gridDim.x;
+  int bh = blockIdx.y, qt = blockIdx.x;
+  if (gridDim.y % 8 == 0) {  // all query tiles of one (row, head) on one XCD
+    const int n = blockIdx.x + blockIdx.y * nq;
+    const int slot = n >> 3;
+    bh = (n & 7) + 8 * (slot / nq);
+    qt = slot % nq;
+  }
+  const int b = bh / a.H, h = bh - (bh / a.H) * a.H;
+  const int S = a.seq_len ? a.seq_len[b] : a.S;
+  const int q0 = (nq - 1 - qt) * kFQ;
+  if (q0 >= S) return;  // past a ragged sequence's end (uniform over the workgroup)
+  const int base = a.pos_base ? a.pos_base[b] : 0;
+  const half_t* __restrict__ Kg = static_cast<const half_t*>(a.k) + b * a.kv_stride_b + h * a.kv_stride_h;
+  const half_t* __restrict__ Vg = static_cast<const half_t*>(a.v) + b * a.kv_stride_b + h * a.kv_stride_h;
+  const half_t* __restrict__ Qg = static_cast<const half_t*>(a.q) + static_cast<size_t>(bh) * a.S * DK;
+  const float scale_t = static_cast<float>(static_cast<half_t>(a.scale));
+  const float cscale = 1.4426950408889634f / scale_t;  // log2(e) / scale
+  const float lazy = 8.0f / cscale;                     // 2^8 in p, in units of q·k
+  const int qw = q0 + wave * 32;     // first query of this wave
+  const int myq = qw + (lane & 31);  // this lane's query
+  const int hi = lane >> 5;          // which half of the wave
+  const int qpos = base + myq;
+  const half8 z8 = {0, 0, 0, 0, 0, 0, 0, 0};
+  half8 qb[KS];
+#pragma unroll
+  for (int ks = 0; ks < KS; ++ks)
+    qb[ks] = myq < S ? *reinterpret_cast<const half8*>(Qg + static_cast<size_t>(myq) * DK + ks * 16 + hi * 8)
+                     : z8;
+  const int kend = base + min(q0 + kFQ, S);  // keys of the workgroup's last query
+  const int nt = (kend + kFK - 1) / kFK;     // key tiles of the workgroup
+  const int ntw = qw < S ? (base + min(qw + 31, S - 1)) / kFK + 1 : 0;  // tiles this wave reads
+
+  // K and V through buffer loads: bytes past the last key (kend rows) read as zero, so
+  // a tile needs no bounds tests (the causal mask removes those keys), and a tile's
+  // offset is a scalar added to a fixed per-thread offset.
+  const int kv_bytes = kend * DK * static_cast<int>(sizeof(half_t));
+  const __amdgpu_buffer_rsrc_t kres =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<half_t*>(Kg), static_cast<short>(0), kv_bytes, 0x00020000);
+  const __amdgpu_buffer_rsrc_t vres =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<half_t*>(Vg), static_cast<short>(0), kv_bytes, 0x00020000);
+  constexpr int kTileBytes = kFK * DK * 2;
+  const int koff = (tid / VG) * DK * 2 + (tid % VG) * 16;  // piece i: + i·4096 bytes (256/VG keys)
+  const int voff = 2 * (tid & 31) * DK * 2 + (tid >> 5) * 16;
+  half8 kn[CH], vn[CH];
+  auto fetch_k = [&](int t, half8 (&dst)[CH]) {
+#pragma unroll
+    for (int i = 0; i < CH; ++i)
+      dst[i] = __builtin_bit_cast(half8, __builtin_amdgcn_raw_buffer_load_b128(kres, koff, t * kTileBytes + i * 4096, 0));
+  };
+  // V as key pairs (keys 2p, 2p + 1 of the same 8 dims, p = tid % 32): the transposed
+  // store is one 4-byte word per dim, 32 lanes covering a 128-byte row segment of Vt
+  auto fetch_v = [&](int t) {
+#pragma unroll
+    for (int i = 0; i < CH / 2; ++i)
+#pragma unroll
+      for (int u = 0; u < 2; ++u)
+        vn[2 * i + u] = __builtin_bit_cast(
+            half8, __builtin_amdgcn_raw_buffer_load_b128(vres, voff + u * DK * 2 + i * 128, t * kTileBytes, 0));
+  };
+  auto put_k = [&](auto buf_c, const half8 (&src)[CH]) {
+    constexpr int buf = decltype(buf_c)::value;
+#pragma unroll
+    for (int i = 0; i < CH; ++i) {
+      const int c = tid + 256 * i;
+      *reinterpret_cast<half8*>(&Ks[buf][c / VG][(c % VG) * 8]) = src[i];
+    }
+  };
+  typedef _Float16 half2v __attribute__((ext_vector_type(2)));
+  auto put_v = [&](auto buf_c) {
+    constexpr int buf = decltype(buf_c)::value;
+#pragma unroll
+    for (int i = 0; i < CH / 2; ++i) {
+      const int grp = (tid >> 5) + 8 * i, key = 2 * (tid & 31);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const half2v pr = {vn[2 * i][e], vn[2 * i + 1][e]};
+        *reinterpret_cast<half2v*>(&Vt[buf][grp * 8 + e][key]) = pr;
+      }
+    }
+  };
+  // Sᵀ of one tile: lane l holds query l % 32 and keys 8(r/4) + 4(l/32) + r % 4 of each
+  // 32-key half t in register r of s[t]
+  auto scores = [&](auto buf_c, floatx16 (&s)[2]) {
+    constexpr int buf = decltype(buf_c)::value;
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) s[t][r] = 0.f;
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) {
+        const half8 ka = *reinterpret_cast<const half8*>(&Ks[buf][t * 32 + (lane & 31)][ks * 16 + hi * 8]);
+        s[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ka, qb[ks], s[t], 0, 0, 0);
+      }
+    }
+  };
+
+  float m = -INFINITY, l = 0.f;  // reference point (units of q·k) and Σ p of this lane's query
+  float mnew = -INFINITY;        // the reference point tile j's probabilities use
+  bool grow = false;             // whether it moved (wave-uniform)
+  floatx16 o[OT];
+#pragma unroll
+  for (int t = 0; t < OT; ++t)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) o[t][r] = 0.f;
+
+  // Masking of tile t's scores (keys after the query: −∞), their maximum, and the
+  // reference point the tile's probabilities will use. A key tile past the sequence's
+  // last key never reaches here (kend bounds the tiles), and key 0 precedes every
+  // query, so the reference point is finite from the first tile on.
+  auto prep = [&](auto mask_c, int t, floatx16 (&s)[2]) {
+    if constexpr (decltype(mask_c)::value) {
+#pragma unroll
+      for (int u = 0; u < 2; ++u)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int key = t * kFK + u * 32 + 8 * (r >> 2) + 4 * hi + (r & 3);
+          if (key > qpos) s[u][r] = -INFINITY;
+        }
+    }
+    float mloc = s[0][0];
+#pragma unroll
+    for (int u = 0; u < 2; ++u)
+#pragma unroll
+      for (int r = 0; r < 16; ++r)
+        if (u + r > 0) mloc = fmaxf(mloc, s[u][r]);
+    float mx = fmaxf(m, mloc);
+    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+    grow = __any(mx > m + lazy);
+    mnew = grow ? mx : m;
+  };
+  auto masked = [&](int t) { return (t + 1) * kFK - 1 > base + qw; };
+
+  // One tile's softmax and P·V, with the next tile's scores (NEXT) beside them. PAR is
+  // the tile's parity: its V sits in buffer PAR, the next tile's K in buffer PAR ^ 1
+  // (compile-time, so every LDS address is a constant offset from one register).
+  using I0 = std::integral_constant<int, 0>;
+  using I1 = std::integral_constant<int, 1>;
+  using T_ = std::true_type;
+  using F_ = std::false_type;
+  auto body = [&](auto par_c, auto next_c, auto mask_next_c, int j, floatx16 (&cur)[2], floatx16 (&nxt)[2]) {
+    constexpr int PAR = decltype(par_c)::value;
+    constexpr bool NEXT = decltype(next_c)::value;
+    if (grow) {
+      const float alpha = __builtin_amdgcn_exp2f((m - mnew) * cscale);
+      l *= alpha;
+#pragma unroll
+      for (int t = 0; t < OT; ++t)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) o[t][r] *= alpha;
+    }
+    m = mnew;
+    if constexpr (NEXT) scores(std::integral_constant<int, PAR ^ 1>{}, nxt);
+    const float nmx = -m * cscale;
+    const half2v ones = {static_cast<_Float16>(1.0f), static_cast<_Float16>(1.0f)};
+    half8 pb[4];
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+        for (int jj = 0; jj < 8; jj += 2) {
+          const float p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(cur[t][8 * kb + jj], cscale, nmx));
+          const float p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(cur[t][8 * kb + jj + 1], cscale, nmx));
+          const half2v pp = {static_cast<_Float16>(p0), static_cast<_Float16>(p1)};
+          l = __builtin_amdgcn_fdot2(pp, ones, l, false);
+          pb[2 * t + kb][jj] = pp[0];
+          pb[2 * t + kb][jj + 1] = pp[1];
+        }
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb) {
+        const int kblk = t * 32 + kb * 16 + 4 * hi;
+#pragma unroll
+        for (int ot = 0; ot < OT; ++ot) {
+          const half_t* vrow = &Vt[PAR][ot * 32 + (lane & 31)][kblk];
+          half8 va;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            va[e] = vrow[e];
+            va[4 + e] = vrow[8 + e];
+          }
+          o[ot] = __builtin_amdgcn_mfma_f32_32x32x16_f16(va, pb[2 * t + kb], o[ot], 0, 0, 0);
+        }
+      }
+    if constexpr (NEXT) prep(mask_next_c, j + 1, nxt);
+  };
+  auto iter = [&](auto par_c, int j, floatx16 (&cur)[2], floatx16 (&nxt)[2]) {
+    constexpr int PAR = decltype(par_c)::value;
+    __syncthreads();
+    if (j + 2 < nt) put_k(par_c, kn);
+    if (j + 1 < nt) put_v(std::integral_constant<int, PAR ^ 1>{});
+    if (j + 3 < nt) fetch_k(j + 3, kn);
+    if (j + 2 < nt) fetch_v(j + 2);
+    if (j >= ntw) return;
+    if (j + 1 >= ntw)
+      body(par_c, F_{}, F_{}, j, cur, nxt);
+    else if (masked(j + 1))
+      body(par_c, T_{}, T_{}, j, cur, nxt);
+    else
+      body(par_c, T_{}, F_{}, j, cur, nxt);
+  };
+
+  floatx16 sA[2], sB[2];
+  {  // prologue: K(0), V(0), K(1) into LDS; K(2), V(1) into registers; tile 0's scores
+    half8 k1[CH];
+    fetch_k(0, kn);
+    fetch_v(0);
+    if (nt > 1) fetch_k(1, k1);
+    put_k(I0{}, kn);
+    put_v(I0{});
+    if (nt > 1) put_k(I1{}, k1);
+    if (nt > 2) fetch_k(2, kn);
+    if (nt > 1) fetch_v(1);
+    __syncthreads();
+    if (ntw > 0) {
+      scores(I0{}, sA);
+      if (masked(0))
+        prep(T_{}, 0, sA);
+      else
+        prep(F_{}, 0, sA);
+    }
+  }
+  for (int j = 0; j < nt; j += 2) {
+    iter(I0{}, j, sA, sB);
+    if (j + 1 < nt) iter(I1{}, j + 1, sB, sA);
+  }
+  l += __shfl_xor(l, 32, 64);
   if (myq < S) {
     const float inv = 1.f / l;
     const int hd = a.H * DK;
@@ -1025,9 +1226,9 @@ int prefill_typed(const AttnArgs& a, hipStream_t st) {
     dim3 grid((a.S + kFQ - 1) / kFQ, a.B * a.H);
     // fp16-rounded scores where the backward recomputes them from the statistics
     if (a.lse || a.m_out)
-      attn_prefill_mfma_kernel<DK, true><<<grid, 256, 0, st>>>(a);
+      attn_prefill_mfma_kernel<DK><<<grid, 256, 0, st>>>(a);
     else
-      attn_prefill_mfma_kernel<DK, false><<<grid, 256, 0, st>>>(a);
+      attn_prefill_pipe_kernel<DK><<<grid, 256, 0, st>>>(a);
     NML_LAUNCHED();
     return 0;
   }

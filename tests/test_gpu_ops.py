@@ -416,6 +416,21 @@ def test_sdpa_mfma_long_fp16(gpu, dk):
     assert np.abs(out - want).max() < 6e-3
 
 
+@pytest.mark.parametrize("dk", [64, 128])
+@pytest.mark.parametrize("s", [1, 2, 63, 64, 65, 127, 129, 192, 257])
+def test_sdpa_mfma_tile_edges_fp16(gpu, dk, s):
+    """The fp16 matrix-core kernels at lengths around the 64-key tile and the 128-query
+    workgroup: one, two and three key tiles, partial last tiles, waves past the end."""
+    rng = np.random.default_rng(dk * 1000 + s)
+    bh = 3
+    q, k, v = (rng.standard_normal((bh, s, dk)).astype(np.float16) for _ in range(3))
+    out = np.asarray(_k().fused_sdpa_forward(q, k, v, float(dk) ** 0.5,
+                                             R.causal_mask(s, np.float16))[0]).astype(np.float64)
+    want = R.sdpa(q.astype(np.float64), k.astype(np.float64), v.astype(np.float64),
+                  float(dk) ** 0.5, R.causal_mask(s, np.float64))
+    assert np.abs(out - want).max() < 6e-3
+
+
 @pytest.mark.parametrize("dk", [16, 40, 64, 96, 128, 256])
 @pytest.mark.parametrize("seq", [1, 37, 200])
 def test_flash_sdpa_forward_device_reference_arguments(gpu, dk, seq):
