@@ -136,10 +136,16 @@ __device__ __forceinline__ void mainloop(const half_t* __restrict__ A, long long
   // Stage t's barrier (every wave's loads of t landed, every wave done reading t - 1) is
   // followed by the loads of stage t + 1 into t - 1's buffer; before a stage's last step
   // each wave has its fragments in registers, so the next barrier may release the buffer.
+  // With 256 × 256 tiles the waves sharing a SIMD (w and w + 4) issue at different times:
+  // waves 0-3 after the barrier, waves 4-7 after their first k step's MFMAs (the stage's
+  // loads issued in one burst by all eight waves stalled every SIMD's MFMAs at once:
+  // C5 0.0490 → 0.0479 s and 0.0505 → 0.0497 s per compute_loss in A/Bs on two boxes;
+  // staggering the 128 × 128 tiles too made the fp16 training step 1.6 % slower).
+  constexpr bool kStagger = TM == 256 && TN == 256;
   auto wait_stage = [&](int t) {
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __builtin_amdgcn_s_barrier();
-    if (t + 1 < S) issue(t + 1);
+    if (t + 1 < S && (!kStagger || wave < 4)) issue(t + 1);
   };
   half8 fa0[IA], fb0[JB], fa1[IA], fb1[JB];
   auto read = [&](half8 (&fa)[IA], half8 (&fb)[JB], int t, int kk) {
@@ -170,6 +176,7 @@ __device__ __forceinline__ void mainloop(const half_t* __restrict__ A, long long
     read(fa1, fb1, s, 1);
     W::prev(fa0, fb0);
     mma(fa0, fb0);
+    if (kStagger && s + 1 < S && wave >= 4) issue(s + 1);  // stage s + 1 (see wait_stage)
     read(fa0, fb0, s, 2);
     W::prev(fa1, fb1);
     mma(fa1, fb1);
