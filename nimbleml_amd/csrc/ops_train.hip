@@ -833,8 +833,17 @@ __global__ __launch_bounds__(256) void parts_reduce_kernel(const float* __restri
   const int tx = threadIdx.x & 31, ty = threadIdx.x >> 5;
   const int c = blockIdx.x * 32 + tx;
   float s = 0.f;
-  if (c < n)
-    for (int p = ty; p < nparts; p += 8) s += part[static_cast<long long>(p) * n + c];
+  if (c < n) {  // parts ty, ty + 8, … in order, eight loads in flight at a time
+    int p = ty;
+    for (; p + 56 < nparts; p += 64) {
+      float v[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) v[u] = part[static_cast<long long>(p + 8 * u) * n + c];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) s += v[u];
+    }
+    for (; p < nparts; p += 8) s += part[static_cast<long long>(p) * n + c];
+  }
   red[ty][tx] = s;
   __syncthreads();
   if (ty == 0 && c < n) {
@@ -848,16 +857,54 @@ __global__ __launch_bounds__(256) void parts_reduce_kernel(const float* __restri
 // ---------------------------------------------------------------- column sums
 constexpr int kColRows = 64;
 
-template <typename T>
+// part[p][c] = Σ a[r][c] over the kColRows rows of part p. A workgroup takes 32·VEC columns
+// (VEC per 16-byte load) and 8 row lanes: lane ty sums rows r0 + ty, r0 + ty + 8, … (all
+// its loads in flight at once), and the 8 lane sums are added in order through LDS — a
+// fixed order, so the result is deterministic. Columns are grouped VEC at a time when n
+// and the row stride allow 16-byte loads (colsum_vec), else one at a time.
+template <typename T, int VEC>
 __global__ __launch_bounds__(256) void colsum_part_kernel(const T* __restrict__ a,
                                                           long long lda, int rows, int n,
                                                           float* __restrict__ part) {
-  const int c = blockIdx.x * 256 + threadIdx.x;
-  if (c >= n) return;
-  const int r0 = blockIdx.y * kColRows, r1 = min(rows, r0 + kColRows);
-  float s = 0.f;
-  for (int r = r0; r < r1; ++r) s += static_cast<float>(a[static_cast<long long>(r) * lda + c]);
-  part[static_cast<long long>(blockIdx.y) * n + c] = s;
+  constexpr int RL = 8, PER = kColRows / RL;
+  __shared__ float red[RL][32 * VEC + 1];
+  const int tx = threadIdx.x & 31, ty = threadIdx.x >> 5;
+  const int c0 = blockIdx.x * 32 * VEC + tx * VEC;
+  const int r0 = blockIdx.y * kColRows;
+  float s[VEC];
+#pragma unroll
+  for (int e = 0; e < VEC; ++e) s[e] = 0.f;
+  if (c0 < n) {
+    T v[PER][VEC];
+#pragma unroll
+    for (int j = 0; j < PER; ++j) {
+      const int r = r0 + ty + RL * j;
+      const T* src = a + static_cast<long long>(r < rows ? r : 0) * lda + c0;
+      if constexpr (VEC == 1) {
+        v[j][0] = r < rows ? src[0] : static_cast<T>(0.f);
+      } else {
+        typedef T vec_t __attribute__((ext_vector_type(VEC)));
+        const vec_t w = *reinterpret_cast<const vec_t*>(src);
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) v[j][e] = r < rows ? w[e] : static_cast<T>(0.f);
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < PER; ++j)
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) s[e] += static_cast<float>(v[j][e]);
+  }
+#pragma unroll
+  for (int e = 0; e < VEC; ++e) red[ty][tx * VEC + e] = s[e];
+  __syncthreads();
+  for (int i = threadIdx.x; i < 32 * VEC; i += 256) {
+    const int c = blockIdx.x * 32 * VEC + i;
+    if (c >= n) continue;
+    float t = 0.f;
+#pragma unroll
+    for (int l = 0; l < RL; ++l) t += red[l][i];
+    part[static_cast<long long>(blockIdx.y) * n + c] = t;
+  }
 }
 
 // -------------------------------------------------------- cross-entropy backward
@@ -2060,11 +2107,23 @@ int launch_colsum(int dt, const void* a, long long lda, int rows, int n, float* 
                   hipStream_t st) {
   if (rows == 0 || n == 0) return 0;
   const int parts = colsum_parts(rows);
-  const dim3 grid((n + 255) / 256, parts);
-  if (dt == F16)
-    colsum_part_kernel<half_t><<<grid, 256, 0, st>>>(static_cast<const half_t*>(a), lda, rows, n, part);
-  else
-    colsum_part_kernel<float><<<grid, 256, 0, st>>>(static_cast<const float*>(a), lda, rows, n, part);
+  const int vec = dt == F16 ? 8 : 4;
+  const bool wide = n % vec == 0 && lda % vec == 0 && (reinterpret_cast<uintptr_t>(a) & 15) == 0;
+  const int span = 32 * (wide ? vec : 1);
+  const dim3 grid((n + span - 1) / span, parts);
+  if (dt == F16) {
+    const half_t* h = static_cast<const half_t*>(a);
+    if (wide)
+      colsum_part_kernel<half_t, 8><<<grid, 256, 0, st>>>(h, lda, rows, n, part);
+    else
+      colsum_part_kernel<half_t, 1><<<grid, 256, 0, st>>>(h, lda, rows, n, part);
+  } else {
+    const float* f = static_cast<const float*>(a);
+    if (wide)
+      colsum_part_kernel<float, 4><<<grid, 256, 0, st>>>(f, lda, rows, n, part);
+    else
+      colsum_part_kernel<float, 1><<<grid, 256, 0, st>>>(f, lda, rows, n, part);
+  }
   NML_LAUNCHED();
   parts_reduce_kernel<<<(n + 31) / 32, 256, 0, st>>>(part, parts, n, out);
   NML_LAUNCHED();
