@@ -758,16 +758,36 @@ __global__ __launch_bounds__(256) void rmsnorm_bwd_wave_kernel(const T* __restri
     gv[i] = c < nvec ? ld4(gam + 4 * c) : z;
     ga[i] = z;
   }
-  for (int r = r0; r < r1; ++r) {
+  // A row's operands (x, dy and the dx it adds to when accumulating) are loaded in one
+  // batch, and the next row's before this one is computed. Every load is unconditional —
+  // the column index clamped, columns past the row and dx when not accumulating zeroed by
+  // selects — since a load behind a branch is waited for where the branches join.
+  floatx4 xv[NV], dv[NV], av[NV], xn[NV], dn[NV], an[NV];
+  auto load_row = [&](int r, floatx4 (&xo)[NV], floatx4 (&go)[NV], floatx4 (&ao)[NV]) {
     const T* xr = x + static_cast<long long>(r) * d;
     const T* gr = dy + static_cast<long long>(r) * d;
-    floatx4 xv[NV], dv[NV];
+    const T* orow = dx + static_cast<long long>(r) * d;
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+      const int c = lane + 64 * i, cc = c < nvec ? c : nvec - 1;
+      xo[i] = ld4(xr + 4 * cc);
+      go[i] = ld4(gr + 4 * cc);
+      ao[i] = ld4(orow + 4 * cc);  // dx is the output buffer: always readable
+    }
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+      const bool in = lane + 64 * i < nvec;
+      xo[i] = in ? xo[i] : z;
+      go[i] = in ? go[i] : z;
+      ao[i] = (in && acc) ? ao[i] : z;
+    }
+  };
+  if (r0 < r1) load_row(r0, xv, dv, av);
+  for (int r = r0; r < r1; ++r) {
+    if (r + 1 < r1) load_row(r + 1, xn, dn, an);
     float ssq = 0.f, dot = 0.f;
 #pragma unroll
     for (int i = 0; i < NV; ++i) {
-      const int c = lane + 64 * i;
-      xv[i] = c < nvec ? ld4(xr + 4 * c) : z;
-      dv[i] = c < nvec ? ld4(gr + 4 * c) : z;
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         if constexpr (H) {
@@ -793,21 +813,25 @@ __global__ __launch_bounds__(256) void rmsnorm_bwd_wave_kernel(const T* __restri
 #pragma unroll
     for (int i = 0; i < NV; ++i) {
       const int c = lane + 64 * i;
-      if (c < nvec) {
-        floatx4 v = acc ? ld4(o + 4 * c) : z;
+      floatx4 v = av[i];
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          if constexpr (H) {
-            const float gx = rnd<T>(rnd<T>(rnd<T>(dv[i][e] * gv[i][e]) * inv) + rnd<T>(xv[i][e] * coef));
-            v[e] = acc ? rnd<T>(v[e] + gx) : gx;
-            ga[i][e] += rnd<T>(dv[i][e] * rnd<T>(xv[i][e] * inv));
-          } else {
-            v[e] += (dv[i][e] * gv[i][e]) / rms + xv[i][e] * coef;
-            ga[i][e] += dv[i][e] * (xv[i][e] / rms);
-          }
+      for (int e = 0; e < 4; ++e) {
+        if constexpr (H) {
+          const float gx = rnd<T>(rnd<T>(rnd<T>(dv[i][e] * gv[i][e]) * inv) + rnd<T>(xv[i][e] * coef));
+          v[e] = acc ? rnd<T>(v[e] + gx) : gx;
+          ga[i][e] += rnd<T>(dv[i][e] * rnd<T>(xv[i][e] * inv));
+        } else {
+          v[e] += (dv[i][e] * gv[i][e]) / rms + xv[i][e] * coef;
+          ga[i][e] += dv[i][e] * (xv[i][e] / rms);
         }
-        st4(o + 4 * c, v);
       }
+      if (c < nvec) st4(o + 4 * c, v);
+    }
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+      xv[i] = xn[i];
+      dv[i] = dn[i];
+      av[i] = an[i];
     }
   }
 #pragma unroll
