@@ -1269,6 +1269,7 @@ __global__ __launch_bounds__(256) void attn_bwd_dq_kernel(AttnBwdArgs a) {
 // supplies rows f(r) for k = 0 and f(r) + 4 for k = 1, which only reorders the sum), so
 // P and dS never go through LDS. Tiles in LDS are [row][DK + 1] fp32.
 constexpr int kAT = 64;
+constexpr float kLog2eF = 1.4426950408889634f;
 
 template <int DK>
 constexpr size_t attn_mfma_lds() {
@@ -1690,13 +1691,38 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dkdv_f16(AttnBwdArgs a) {
       sc = __builtin_amdgcn_mfma_f32_32x32x16_f16(qa, kb, sc, 0, 0, 0);
       dp = __builtin_amdgcn_mfma_f32_32x32x16_f16(oa, vb, dp, 0, 0, 0);
     }
+    // The lane's 16 query rows are 32·wq + 8g + 4·hi + {0…3}, g < 4: their statistics as
+    // four broadcast 16-byte reads each (not one conflicting scalar read a score), and
+    // p = exp(s − lse) as exp2(s·log₂e − lse·log₂e). Only a tile that reaches past a
+    // key's queries (the first) or past the sequence (the last) needs the mask.
+    float nl2[16], dd[16];
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const int ql = 32 * wq + d_row(r, lane), q = q_lo + ql;
-      float p = 0.f;
-      if (key <= q && q < S) p = expf(attn_score<half_t>(sc[r], mul) - Ls[ql]);
-      sc[r] = p;
-      dp[r] = p * (dp[r] - Ds[ql]) * inv_scale;
+    for (int g = 0; g < 4; ++g) {
+      const floatx4 l4 = *reinterpret_cast<const floatx4*>(Ls + 32 * wq + 8 * g + 4 * hi);
+      const floatx4 d4 = *reinterpret_cast<const floatx4*>(Ds + 32 * wq + 8 * g + 4 * hi);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        nl2[4 * g + e] = -l4[e] * kLog2eF;
+        dd[4 * g + e] = d4[e];
+      }
+    }
+    if (q_lo < k_lo + kAT || q_lo + kAT > S) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int q = q_lo + 32 * wq + d_row(r, lane);
+        float p = 0.f;
+        if (key <= q && q < S)
+          p = __builtin_amdgcn_exp2f(__builtin_fmaf(attn_score<half_t>(sc[r], mul), kLog2eF, nl2[r]));
+        sc[r] = p;
+        dp[r] = p * (dp[r] - dd[r]) * inv_scale;
+      }
+    } else {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const float p = __builtin_amdgcn_exp2f(__builtin_fmaf(attn_score<half_t>(sc[r], mul), kLog2eF, nl2[r]));
+        sc[r] = p;
+        dp[r] = p * (dp[r] - dd[r]) * inv_scale;
+      }
     }
 #pragma unroll
     for (int st = 0; st < 2; ++st) {
@@ -1760,6 +1786,7 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dq_f16(AttnBwdArgs a) {
   const int q = q_lo + 32 * wq + l32;
   const float lse = q < S ? a.lse[static_cast<long long>(bh) * S + q] : 0.f;
   const float dd = q < S ? a.dvec[static_cast<long long>(bh) * S + q] : 0.f;
+  const float nlse2 = -lse * kLog2eF;
   const float inv_scale = 1.0f / a.scale, mul = score_mul<half_t>(a.scale);
   floatx16 dq[NJ];
 #pragma unroll
@@ -1805,12 +1832,23 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dq_f16(AttnBwdArgs a) {
       sc = __builtin_amdgcn_mfma_f32_32x32x16_f16(ka, qb, sc, 0, 0, 0);
       dp = __builtin_amdgcn_mfma_f32_32x32x16_f16(va, ob, dp, 0, 0, 0);
     }
+    // p = exp(s − lse) as exp2(s·log₂e − lse·log₂e); the mask only on the tile that
+    // reaches past this workgroup's queries (the last) or a tile past the sequence
+    if (k_lo + kAT > q_lo || q_lo + kAT > S) {
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const int kk = k_lo + 32 * wk + d_row(r, lane);
-      float p = 0.f;
-      if (kk <= q && q < S) p = expf(attn_score<half_t>(sc[r], mul) - lse);
-      dp[r] = p * (dp[r] - dd) * inv_scale;
+      for (int r = 0; r < 16; ++r) {
+        const int kk = k_lo + 32 * wk + d_row(r, lane);
+        float p = 0.f;
+        if (kk <= q && q < S)
+          p = __builtin_amdgcn_exp2f(__builtin_fmaf(attn_score<half_t>(sc[r], mul), kLog2eF, nlse2));
+        dp[r] = p * (dp[r] - dd) * inv_scale;
+      }
+    } else {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const float p = __builtin_amdgcn_exp2f(__builtin_fmaf(attn_score<half_t>(sc[r], mul), kLog2eF, nlse2));
+        dp[r] = p * (dp[r] - dd) * inv_scale;
+      }
     }
 #pragma unroll
     for (int st = 0; st < 2; ++st) {

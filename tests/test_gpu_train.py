@@ -193,12 +193,12 @@ def test_c_abi_backward_accumulates_and_matches_loss(gpu):
 
 @pytest.mark.parametrize("dims,b,s", [((256, 64, 4, 2, 64), 2, 40), ((512, 128, 2, 2, 96), 2, 70),
                                       ((512, 256, 2, 1, 64), 2, 33), ((256, 128, 2, 1, 128), 2, 128),
-                                      ((256, 192, 2, 1, 64), 2, 45)])
+                                      ((256, 192, 2, 1, 64), 2, 45), ((512, 256, 2, 1, 192), 2, 150)])
 def test_backward_fp16(gpu, dims, b, s):
     """float16 models: the loss equals the fp16 oracle's (the reference's fp16 rounding),
     and the gradients (kept float32, as under an optimizer's _grad_dtype) match the float64
     gradient at the same fp16 weights within 1.5e-2 of each tensor's largest gradient
-    (measured ≤ 7.4e-3): the fp16 rounding of the activations, activation gradients and the
+    (measured ≤ 9.3e-3): the fp16 rounding of the activations, activation gradients and the
     fp16 P and dS of the attention backward."""
     import nimbleml_amd as nm
 
@@ -226,9 +226,15 @@ def test_backward_fp16(gpu, dims, b, s):
     worst = 0.0
     for k, ref in want.items():
         err = np.abs(got[k].astype(np.float64) - ref).max()
-        assert err <= 1.5e-2 * np.abs(ref).max() + 1e-5, (k, err, np.abs(ref).max())
+        scale = np.abs(ref).max()
+        if k.endswith("W_k.biases"):
+            # exactly zero (a key bias moves every score of a query alike; softmax ignores
+            # it): what the device returns is the fp16 rounding of dS summed over the keys,
+            # bounded against the scale of the same layer's W_q bias gradient
+            scale = np.abs(want[k.replace("W_k", "W_q")]).max()
+        assert err <= 1.5e-2 * scale + 1e-5, (k, err, scale)
         if not k.endswith("W_k.biases"):
-            worst = max(worst, err / np.abs(ref).max())
+            worst = max(worst, err / scale)
     print("worst relative gradient error (fp16)", worst)
 
 
