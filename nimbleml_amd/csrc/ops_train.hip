@@ -1390,13 +1390,36 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dkdv_mfma(AttnBwdArgs a) {
       sc = __builtin_amdgcn_mfma_f32_32x32x2f32(qa[c0], kb[c0], sc, 0, 0, 0);
       dp = __builtin_amdgcn_mfma_f32_32x32x2f32(oa[c0], vb[c0], dp, 0, 0, 0);
     }
+    // the lane's 16 query rows' statistics as broadcast 16-byte reads; p = exp(s − lse) as
+    // exp2(s·log₂e − lse·log₂e); the mask only on the first and a ragged last tile
+    float nl2[16], dd[16];
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const int ql = 32 * wq + d_row(r, lane), q = q_lo + ql;
-      float p = 0.f;
-      if (key <= q && q < S) p = expf(attn_score<T>(sc[r], mul) - Ls[ql]);
-      sc[r] = p;
-      dp[r] = p * (dp[r] - Ds[ql]) * inv_scale;
+    for (int g = 0; g < 4; ++g) {
+      const floatx4 l4 = *reinterpret_cast<const floatx4*>(Ls + 32 * wq + 8 * g + 4 * hi);
+      const floatx4 d4 = *reinterpret_cast<const floatx4*>(Ds + 32 * wq + 8 * g + 4 * hi);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        nl2[4 * g + e] = -l4[e] * kLog2eF;
+        dd[4 * g + e] = d4[e];
+      }
+    }
+    if (q_lo < k_lo + kAT || q_lo + kAT > S) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int q = q_lo + 32 * wq + d_row(r, lane);
+        float p = 0.f;
+        if (key <= q && q < S)
+          p = __builtin_amdgcn_exp2f(__builtin_fmaf(attn_score<T>(sc[r], mul), kLog2eF, nl2[r]));
+        sc[r] = p;
+        dp[r] = p * (dp[r] - dd[r]) * inv_scale;
+      }
+    } else {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const float p = __builtin_amdgcn_exp2f(__builtin_fmaf(attn_score<T>(sc[r], mul), kLog2eF, nl2[r]));
+        sc[r] = p;
+        dp[r] = p * (dp[r] - dd[r]) * inv_scale;
+      }
     }
     // dV[key][c] += Σ_q P[q][key]·dO[q][c];  dK[key][c] += Σ_q dS[q][key]·Q[q][c]
 #pragma unroll
@@ -1496,7 +1519,8 @@ __global__ __launch_bounds__(256) void attn_bwd_dq_mfma(AttnBwdArgs a) {
     for (int r = 0; r < 16; ++r) {
       const int kk = k_lo + 32 * wk + d_row(r, lane);
       float p = 0.f;
-      if (kk <= q && q < S) p = expf(attn_score<T>(sc[r], mul) - lse);
+      if (kk <= q && q < S)
+        p = __builtin_amdgcn_exp2f(__builtin_fmaf(attn_score<T>(sc[r], mul), kLog2eF, -lse * kLog2eF));
       dp[r] = p * (dp[r] - dd) * inv_scale;
     }
     // dQ[q][c] += Σ_key dS[q][key]·K[key][c]
