@@ -1564,9 +1564,13 @@ __global__ __launch_bounds__(256) void attn_bwd_dq_mfma(AttnBwdArgs a) {
 // holds them in fp16). A 16-row step of those products takes rows f(r) (k slots 0–7) and
 // f(r) + 4 (slots 8–15) from registers r = 8s … 8s + 7, i.e. rows 16s + {0–3, 8–11} and
 // 16s + {4–7, 12–15}: two 8-byte reads of the transposed copy per fragment.
+// The transposed copies' rows are 34 dwords apart: the 32 rows an 8-byte fragment read
+// takes (lanes 0-31, and 32-63) then fall on 32 distinct bank pairs (36 dwords put rows l
+// and l + 16 on one pair: half of all LDS cycles of the two kernels were bank conflicts).
+constexpr int kATT = kAT + 4;
 template <int DK>
 constexpr size_t attn_f16_lds() {
-  return (static_cast<size_t>(4) * kAT * (DK + 8) + 2 * DK * (kAT + 8)) * sizeof(half_t) +
+  return (static_cast<size_t>(4) * kAT * (DK + 8) + 2 * DK * kATT) * sizeof(half_t) +
          2 * kAT * sizeof(float);
 }
 
@@ -1591,7 +1595,7 @@ __device__ __forceinline__ void fetch16(half8 (&v)[4], const half_t* __restrict_
 
 template <int DK>
 __device__ __forceinline__ void put16(half_t* X, half_t* XT, const half8 (&v)[4], int first) {
-  constexpr int PA = DK + 8, PT = kAT + 8, NB = 16 * DK / 8;
+  constexpr int PA = DK + 8, PT = kATT, NB = 16 * DK / 8;
   const int b = static_cast<int>(threadIdx.x) - first;
   if (b < 0 || b >= NB) return;
   const int r0 = 4 * (b / (DK / 8)), c = 8 * (b % (DK / 8));
@@ -1617,7 +1621,7 @@ __device__ __forceinline__ void stage16(half_t* X, half_t* XT, const half_t* __r
 // A 16-row fragment of a transposed [dim][64 + 8] tile: dims d0 + l % 32, rows of step s
 // within the 32-row block rb as the register layout pairs them.
 __device__ __forceinline__ half8 frag_t(const half_t* XT, int d0, int rb, int s, int lane) {
-  constexpr int PT = kAT + 8;
+  constexpr int PT = kATT;
   const half_t* p = XT + (d0 + (lane & 31)) * PT + rb + 16 * s + 4 * (lane >> 5);
   const half4 lo = *reinterpret_cast<const half4*>(p);
   const half4 hi = *reinterpret_cast<const half4*>(p + 8);
@@ -1635,7 +1639,7 @@ __device__ __forceinline__ half8 regs16(const floatx16& v, int s) {
 template <int DK>
 __global__ __launch_bounds__(256, 2) void attn_bwd_dkdv_f16(AttnBwdArgs a) {
   extern __shared__ __attribute__((aligned(16))) half_t lds16[];
-  constexpr int PA = DK + 8, PT = kAT + 8, NJ = DK / 32;
+  constexpr int PA = DK + 8, PT = kATT, NJ = DK / 32;
   half_t* Ks = lds16;
   half_t* Vs = Ks + kAT * PA;
   half_t* Qs = Vs + kAT * PA;
