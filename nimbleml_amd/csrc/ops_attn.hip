@@ -1225,7 +1225,10 @@ int prefill_typed(const AttnArgs& a, hipStream_t st) {
   if constexpr (sizeof(T) == 2 && (DK == 64 || DK == 128)) {
     dim3 grid((a.S + kFQ - 1) / kFQ, a.B * a.H);
     // fp16-rounded scores where the backward recomputes them from the statistics
-    if (a.lse || a.m_out)
+    // The pipelined kernel's buffer loads take a 32-bit byte range per (row, head): a
+    // cache row block past 2 GiB (kv_stride_h elements) takes the other kernel.
+    const bool ranged = a.kv_stride_h * static_cast<long long>(sizeof(half_t)) < (1LL << 31);
+    if (a.lse || a.m_out || !ranged)
       attn_prefill_mfma_kernel<DK><<<grid, 256, 0, st>>>(a);
     else
       attn_prefill_pipe_kernel<DK><<<grid, 256, 0, st>>>(a);
