@@ -373,10 +373,13 @@ def test_linear_skinny_wide_fp16(gpu, rows, k, n):
                                           (4096, 128, 4099, 3), (4096, 64, 4097, 2),
                                           (1024, 192, 3072, 1), (700, 256, 1000, 3),
                                           (300, 128, 520, 2), (515, 64, 136, 0),
-                                          (700, 64, 1001, 3), (600, 128, 1030, 1)])
+                                          (700, 64, 1001, 3), (600, 128, 1030, 1),
+                                          (17317, 128, 1024, 3), (17317, 64, 3072, 1)])
 def test_linear_big_tile_fp16(gpu, rows, k, n, epi):
     """Prefill-sized shapes on the direct-to-LDS MFMA GEMM: 256×256 tiles where there are
-    ≥ 256 of them, 128×128 tiles below that (rows ≤ 1024), with ragged last column tiles
+    ≥ 256 of them, 128×128 tiles below that (rows ≤ 1024) and where the last round of big
+    tiles would be short (17317 × 1024: 272 big tiles; 17317 × 3072, 816, stays on the
+    big ones), with ragged last column tiles
     (n = 4224, 1000, 520, 136), ragged last row tiles (rows = 3000, 700, 300, 515), and
     widths that are not multiples of 4 (4099, 4097, 1001, 1030: the epilogue's
     element-by-element path instead of 8-byte runs)."""
