@@ -433,6 +433,8 @@ __global__ __launch_bounds__(256) void transpose16_kernel(const half_t* __restri
 // c (m, n) = out(Σ_k a[m·lda + k] · b[n·ldb + k]) over this split's k range, output modes
 // as gemm_bwd_f16_kernel. Workgroup b → (split, tile) through the XCD-aware order;
 // `tiles_m` m-tiles per column of tiles.
+constexpr int kBwdGM = 8;
+
 template <int TM, int TN, int OUT>
 __global__ __launch_bounds__(big::kThreads, TM == 256 ? 1 : 4) void gemm_bwd_big_kernel(
     GemmBwdArgs g, int tiles_m, int tiles, int splits, int kchunk, long long zstride) {
@@ -440,7 +442,15 @@ __global__ __launch_bounds__(big::kThreads, TM == 256 ? 1 : 4) void gemm_bwd_big
   constexpr int IA = TM / 64, JB = TN / 128;
   const int u = big::xcd_tile(blockIdx.x, tiles * splits);
   const int z = u % splits, tile = u / splits;
-  const int m0 = (tile % tiles_m) * TM, n0 = (tile / tiles_m) * TN;
+  // Tiles in groups of kBwdGM m-tiles (m fastest inside a group, then n), so that an
+  // XCD's contiguous range of tiles is a block of up to kBwdGM rows of tiles by a few
+  // columns rather than whole columns: with whole columns (4096 × 1024 outputs: one
+  // column of 32 tiles per XCD) every XCD streamed all of A through its L2.
+  const int tiles_n = tiles / tiles_m;
+  const int group = tile / (kBwdGM * tiles_n), first_m = group * kBwdGM;
+  const int gm = min(tiles_m - first_m, kBwdGM);
+  const int in_group = tile - group * kBwdGM * tiles_n;
+  const int m0 = (first_m + in_group % gm) * TM, n0 = (in_group / gm) * TN;
   const int kbeg = z * kchunk;
   const int klen = min(kchunk, g.K - kbeg);
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
