@@ -1279,6 +1279,21 @@ __global__ __launch_bounds__(256) void attn_bwd_dq_kernel(AttnBwdArgs a) {
 // supplies rows f(r) for k = 0 and f(r) + 4 for k = 1, which only reorders the sum), so
 // P and dS never go through LDS. Tiles in LDS are [row][DK + 1] fp32.
 constexpr int kAT = 64;
+
+// Grid (tiles, B·H) of the attention backward: when B·H is a multiple of 8, every tile of
+// one (row, head) runs on one XCD (workgroups are dealt to the 8 XCDs round robin in
+// dispatch order), so the Q / dO (or K / V) rows its tiles share come from that XCD's L2
+// instead of being fetched by all eight; tiles of a (row, head) run in index order.
+__device__ __forceinline__ void bwd_tile_order(int& bh, int& t) {
+  bh = blockIdx.y;
+  t = blockIdx.x;
+  if (gridDim.y % 8 == 0) {
+    const int n = blockIdx.x + blockIdx.y * gridDim.x;
+    const int slot = n >> 3;
+    bh = (n & 7) + 8 * (slot / gridDim.x);
+    t = slot % gridDim.x;
+  }
+}
 constexpr float kLog2eF = 1.4426950408889634f;
 
 template <int DK>
@@ -1352,8 +1367,10 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dkdv_mfma(AttnBwdArgs a) {
   float* Ds = Ls + kAT;
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, wq = w >> 1, wk = w & 1;
   const int l32 = lane & 31, hi = lane >> 5;
-  const int bh = blockIdx.y, b = bh / a.H, h = bh - (bh / a.H) * a.H;
-  const int S = a.S, k_lo = blockIdx.x * kAT;
+  int bh, t;
+  bwd_tile_order(bh, t);
+  const int b = bh / a.H, h = bh - (bh / a.H) * a.H;
+  const int S = a.S, k_lo = t * kAT;  // the longest key tiles (most query tiles) first
   const long long hoff = static_cast<long long>(bh) * S * DK;
   tile_rows<DK>(Ks, static_cast<const T*>(a.k) + hoff, k_lo, S);
   tile_rows<DK>(Vs, static_cast<const T*>(a.v) + hoff, k_lo, S);
@@ -1484,8 +1501,10 @@ __global__ __launch_bounds__(256) void attn_bwd_dq_mfma(AttnBwdArgs a) {
   float* Os = Qs + kAT * P;
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, wk = w >> 1, wq = w & 1;
   const int l32 = lane & 31, hi = lane >> 5;
-  const int bh = blockIdx.y, b = bh / a.H, h = bh - (bh / a.H) * a.H;
-  const int S = a.S, q_lo = blockIdx.x * kAT;
+  int bh, t;
+  bwd_tile_order(bh, t);
+  const int b = bh / a.H, h = bh - (bh / a.H) * a.H;
+  const int S = a.S, q_lo = (gridDim.x - 1 - t) * kAT;  // the longest query tiles first
   const long long hoff = static_cast<long long>(bh) * S * DK;
   const T* kg = static_cast<const T*>(a.k);
   const T* vg = static_cast<const T*>(a.v);
@@ -1660,8 +1679,10 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dkdv_f16(AttnBwdArgs a) {
   float* Ds = Ls + kAT;
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, wq = w >> 1, wk = w & 1;
   const int l32 = lane & 31, hi = lane >> 5;
-  const int bh = blockIdx.y, b = bh / a.H, h = bh - (bh / a.H) * a.H;
-  const int S = a.S, k_lo = blockIdx.x * kAT;
+  int bh, t;
+  bwd_tile_order(bh, t);
+  const int b = bh / a.H, h = bh - (bh / a.H) * a.H;
+  const int S = a.S, k_lo = t * kAT;  // the longest key tiles (most query tiles) first
   const long long hoff = static_cast<long long>(bh) * S * DK;
   const half_t* qg = static_cast<const half_t*>(a.q) + hoff;
   const half_t* og = static_cast<const half_t*>(a.dout) + static_cast<long long>(b) * S * a.H * DK + h * DK;
@@ -1812,8 +1833,10 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dq_f16(AttnBwdArgs a) {
   half_t* KT = Os + kAT * PA;
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, wk = w >> 1, wq = w & 1;
   const int l32 = lane & 31, hi = lane >> 5;
-  const int bh = blockIdx.y, b = bh / a.H, h = bh - (bh / a.H) * a.H;
-  const int S = a.S, q_lo = blockIdx.x * kAT;
+  int bh, t;
+  bwd_tile_order(bh, t);
+  const int b = bh / a.H, h = bh - (bh / a.H) * a.H;
+  const int S = a.S, q_lo = (gridDim.x - 1 - t) * kAT;  // the longest query tiles first
   const long long hoff = static_cast<long long>(bh) * S * DK;
   const half_t* kg = static_cast<const half_t*>(a.k) + hoff;
   const half_t* vg = static_cast<const half_t*>(a.v) + hoff;
