@@ -403,11 +403,25 @@ SplitWs g_split;
 
 // dst[c·ldd + r] = src[r·lds + c] for r < rows, c < cols (fp16; rows and cols multiples
 // of 8, strides multiples of 8, both 16-byte aligned); one 64 × 64 tile per workgroup.
-__global__ __launch_bounds__(256) void transpose16_kernel(const half_t* __restrict__ src, long long lds,
-                                                          int rows, int cols, half_t* __restrict__ dst,
-                                                          long long ldd) {
+// Up to two such transposes in one launch (grid z = the job; a workgroup past its job's
+// extent returns), so a product that reads both operands across k pays one launch.
+struct Transpose16Job {
+  const half_t* src;
+  long long lds;
+  int rows, cols;
+  half_t* dst;
+  long long ldd;
+};
+
+__global__ __launch_bounds__(256) void transpose16_kernel(Transpose16Job j0, Transpose16Job j1) {
   __shared__ half_t t[64][66];  // row stride 132 bytes: column reads spread over the banks
+  const Transpose16Job& j = blockIdx.z == 0 ? j0 : j1;
+  const half_t* __restrict__ src = j.src;
+  half_t* __restrict__ dst = j.dst;
+  const long long lds = j.lds, ldd = j.ldd;
+  const int rows = j.rows, cols = j.cols;
   const int r0 = blockIdx.y * 64, c0 = blockIdx.x * 64, tid = threadIdx.x;
+  if (r0 >= rows || c0 >= cols) return;  // (uniform over the workgroup)
 #pragma unroll
   for (int i = 0; i < 2; ++i) {
     const int p = tid + 256 * i, r = p >> 3, c8 = (p & 7) * 8;
@@ -560,20 +574,25 @@ int gemm_bwd_big(const GemmBwdArgs& g0, bool a_kc, bool b_kc, int out, hipStream
   if (at + bt) {
     if (ws_ensure(g_tws, (at + bt) * sizeof(half_t), st) != 0) return -1;
     half_t* ws = static_cast<half_t*>(g_tws.p);
+    Transpose16Job job[2];
+    int jobs = 0, cols = 0;
     if (!a_kc) {  // a: (k, m) at a[k·lda + m]
-      transpose16_kernel<<<dim3((g.M + 63) / 64, (g.K + 63) / 64), 256, 0, st>>>(
-          static_cast<const half_t*>(g.a), g.lda, g.K, g.M, ws, K);
-      NML_LAUNCHED();
+      job[jobs++] = Transpose16Job{static_cast<const half_t*>(g.a), g.lda, static_cast<int>(K),
+                                   static_cast<int>(M), ws, K};
+      cols = static_cast<int>(M);
       g.a = ws;
       g.lda = K;
     }
     if (!b_kc) {  // b: (k, n) at b[k·ldb + n]
-      transpose16_kernel<<<dim3((g.N + 63) / 64, (g.K + 63) / 64), 256, 0, st>>>(
-          static_cast<const half_t*>(g.b), g.ldb, g.K, g.N, ws + at, K);
-      NML_LAUNCHED();
+      job[jobs++] = Transpose16Job{static_cast<const half_t*>(g.b), g.ldb, static_cast<int>(K),
+                                   static_cast<int>(N), ws + at, K};
+      cols = cols > static_cast<int>(N) ? cols : static_cast<int>(N);
       g.b = ws + at;
       g.ldb = K;
     }
+    transpose16_kernel<<<dim3((cols + 63) / 64, static_cast<unsigned>((K + 63) / 64), jobs), 256, 0, st>>>(
+        job[0], jobs > 1 ? job[1] : job[0]);
+    NML_LAUNCHED();
   }
   // 128 × 128 tiles, two workgroups per CU (256 × 256 tiles measured slower here: the
   // backward's products have at most 4096 × 4096 outputs, one round of large tiles, and
