@@ -407,6 +407,43 @@ def bench_c4_attention(nm, reps=20):
                          "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4)}}
 
 
+def bench_c4_projections(nm, reps=50):
+    """The C4 step's four projections alone, as the step launches them for one 16-row half
+    (d1024 fp16: QKV 1024→3072 + bias, W_o 1024→1024 + bias + residual, W1 1024→4096 +
+    bias + GELU, W2 4096→1024 + bias + residual) through the C-ABI export nml_linear_device
+    on the skinny MFMA kernel (without the fused RMSNorm of the step's QKV and W1). HIP events
+    over `reps` back-to-back launches of each; bytes are the weights read once (the 16 input
+    and output rows are 32–128 KB)."""
+    N = nm._native
+    rng = np.random.default_rng(7)
+    rows = 16
+    out = {}
+    for name, k, n, epi in (("qkv", 1024, 3072, 1), ("w_o", 1024, 1024, 3), ("w1", 1024, 4096, 2),
+                            ("w2", 4096, 1024, 3)):
+        x = N.DeviceArray.from_host(rng.standard_normal((rows, k)).astype(np.float16))
+        w = N.DeviceArray.from_host((rng.standard_normal((n, k)) / np.sqrt(k)).astype(np.float16))
+        b = N.DeviceArray.from_host(rng.standard_normal(n).astype(np.float16))
+        r = N.DeviceArray.from_host(rng.standard_normal((rows, n)).astype(np.float16))
+        y = N.DeviceArray((rows, n), np.float16)
+        call = lambda: N.check(N.lib.nml_linear_device(x.ptr, k, w.ptr, b.ptr, r.ptr if epi == 3 else None,
+                                                       y.ptr, rows, k, n, epi, N.np_dtype_code(np.float16)))
+        call()
+        N.synchronize()
+        t = N.Timer()
+        t.start()
+        for _ in range(reps):
+            call()
+        ms = t.stop() / reps
+        N.synchronize()
+        nbytes = n * k * 2
+        gbs = nbytes / (ms * 1e-3) / 1e9
+        out[name] = {"us_per_launch": round(ms * 1e3, 2), "weight_bytes": nbytes,
+                     "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS,
+                                  "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4)}}
+    return {"workload": "C4 projections of one 16-row half, d1024 fp16, nml_linear_device, "
+                        f"{reps} back-to-back launches each", **out}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -417,7 +454,8 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-graph", action="store_true")
     ap.add_argument("--only-c3", action="store_true", help="skip the batch-32 and prefill lines")
-    ap.add_argument("--only", choices=["c3", "c4", "c4attn", "c5", "adamw", "train", "train16"],
+    ap.add_argument("--only", choices=["c3", "c4", "c4attn", "c4proj", "c5", "adamw", "train",
+                                       "train16"],
                     default=None,
                     help="run one workload only (for profiling); c4/c5 print their own line")
     ap.add_argument("--train-skew", action="store_true",
@@ -458,6 +496,9 @@ def main():
         return
     if args.only == "c4attn":
         print(json.dumps({"c4attn": bench_c4_attention(nm)}), flush=True)
+        return
+    if args.only == "c4proj":
+        print(json.dumps({"c4proj": bench_c4_projections(nm)}), flush=True)
         return
     if args.only == "adamw":
         print(json.dumps({"adamw": bench_adamw(nm)}), flush=True)
